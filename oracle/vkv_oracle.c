@@ -1,0 +1,440 @@
+/*
+ * vkv_oracle.c -- CPU restatement of the reference's KV-cache arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY (see vkv_oracle.h).  Built with
+ * -ffp-contract=off so every float expression rounds exactly as written:
+ * the quantizer below must reproduce the reference's fp32 arithmetic bit for
+ * bit, and a fused multiply-add would change its rounding.
+ *
+ * Parity pins for this file (tests/test_oracle_golden.py):
+ *   vkvo_quantize   -- IntegrationTests.swift:3890-3923 aggregates on the
+ *                      reproduced MLX stream (seed 869), plus closed-form
+ *                      invariants and a brute-force tiny-alphabet sweep.
+ *   vkvo_dequantize -- |w - deq| <= |scale|/2 away from the clamp and exact
+ *                      reconstruction of the group's edge element.
+ *   vkvo_sdpa       -- MLXFastKernelTests.swift:101-111 known answer (seed 0),
+ *                      single-key / uniform-score / fully-masked special cases.
+ *   vkvo_quantized_sdpa -- equals vkvo_sdpa on the dequantized cache with the
+ *                      input-dtype query scaling; fully masked row = mean(V).
+ *   vkvo_mla_decode -- equals vkvo_sdpa with Hkv = 1 on dequantized entries.
+ *   conversions     -- exhaustive bf16/f16 round trips and numpy's f16 cast.
+ */
+#include "vkv_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+uint16_t vkvo_f32_to_bf16(float f) {
+  uint32_t u = f2u(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+float vkvo_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+uint16_t vkvo_f32_to_f16(float f) {
+  uint32_t u = f2u(f);
+  uint32_t sign = (u >> 16) & 0x8000u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520: inf */
+  if (a >= 0x38800000u) {                                  /* normal f16 */
+    uint32_t r = a + 0x0fffu + ((a >> 13) & 1u);
+    return (uint16_t)(sign | ((r - 0x38000000u) >> 13));
+  }
+  if (a < 0x33000000u) return (uint16_t)sign; /* < 2^-25: rounds to zero */
+  /* subnormal f16: value = m * 2^-24 with m = round(a_value * 2^24) */
+  {
+    uint32_t e = a >> 23;                 /* 102..112 */
+    uint32_t m = (a & 0x7fffffu) | 0x800000u;
+    uint32_t shift = 126u - e;            /* 14..24: m >> shift = integer part */
+    uint32_t q = m >> shift;
+    uint32_t rem = m & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+  }
+}
+
+float vkvo_f16_to_f32(uint16_t h) {
+  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  uint32_t e = ((uint32_t)h >> 10) & 0x1fu;
+  uint32_t m = (uint32_t)h & 0x3ffu;
+  if (e == 0x1f) return u2f(sign | 0x7f800000u | (m << 13));
+  if (e == 0) {
+    float v = (float)m * (1.0f / 16777216.0f);
+    return sign ? -v : v;
+  }
+  return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+static inline float load_val(const void *p, int dtype, int64_t i) {
+  switch (dtype) {
+    case 1: return vkvo_f16_to_f32(((const uint16_t *)p)[i]);
+    case 2: return vkvo_bf16_to_f32(((const uint16_t *)p)[i]);
+    default: return ((const float *)p)[i];
+  }
+}
+
+static inline void store_val(void *p, int dtype, int64_t i, float v) {
+  switch (dtype) {
+    case 1: ((uint16_t *)p)[i] = vkvo_f32_to_f16(v); break;
+    case 2: ((uint16_t *)p)[i] = vkvo_f32_to_bf16(v); break;
+    default: ((float *)p)[i] = v; break;
+  }
+}
+
+static inline float round_to(float v, int dtype) {
+  switch (dtype) {
+    case 1: return vkvo_f16_to_f32(vkvo_f32_to_f16(v));
+    case 2: return vkvo_bf16_to_f32(vkvo_f32_to_bf16(v));
+    default: return v;
+  }
+}
+
+void vkvo_to_f32(const void *src, int dtype, int64_t n, float *dst) {
+  for (int64_t i = 0; i < n; i++) dst[i] = load_val(src, dtype, i);
+}
+
+void vkvo_from_f32(const float *src, int64_t n, int dtype, void *dst) {
+  for (int64_t i = 0; i < n; i++) store_val(dst, dtype, i, src[i]);
+}
+
+/* Largest finite value of the element type: the Metal kernel starts its
+ * running minimum there (quantized.h:2422, Limits<T>::max). */
+static float type_max(int dtype) {
+  switch (dtype) {
+    case 1: return 65504.0f;
+    case 2: return u2f(0x7f7f0000u);
+    default: return FLT_MAX;
+  }
+}
+
+/* Lowest finite value: the fill of masked scores (KVCache.swift:1950-1975). */
+static double type_lowest(int dtype) {
+  switch (dtype) {
+    case 1: return -65504.0;
+    case 2: return -(double)u2f(0x7f7f0000u);
+    default: return -(double)FLT_MAX;
+  }
+}
+
+static inline int is_tie(float x) { return fabsf(x - truncf(x)) == 0.5f; }
+
+/* quantized.h:2393-2497 (affine_quantize).  Group statistics in fp32 with
+ * the running max starting at 0 and the running min at Limits<T>::max
+ * (:2422-2431); scale = max((max - min) / n_bins, 1e-7) (:2436); the edge
+ * with the larger magnitude is represented exactly: scale is negated when
+ * the max is the edge (:2437-2438), q0 = round(edge / scale), and unless q0
+ * is zero the scale is re-derived as edge / q0 with bias = edge (:2439-2443).
+ * Codes use the unrounded fp32 scale/bias: min(round((w - bias) / scale),
+ * n_bins) (:2458); scale/bias are then stored cast to T (:2447-2450).  Metal
+ * round() is half away from zero, the same as C roundf. */
+int64_t vkvo_quantize(const void *w, int dtype, int64_t rows, int D, int group,
+                      int bits, uint32_t *wq, void *scales, void *biases) {
+  const float n_bins = (float)((1 << bits) - 1);
+  const float eps = 1e-7f;
+  const int per_word = 32 / bits;
+  const int words_per_row = D / per_word;
+  const int groups = D / group;
+  int64_t ties = 0;
+  float *vals = (float *)malloc(sizeof(float) * (size_t)group);
+  for (int64_t r = 0; r < rows; r++) {
+    uint32_t *orow = wq + r * words_per_row;
+    memset(orow, 0, sizeof(uint32_t) * (size_t)words_per_row);
+    for (int g = 0; g < groups; g++) {
+      float w_min = type_max(dtype);
+      float w_max = 0.0f;
+      for (int i = 0; i < group; i++) {
+        float v = load_val(w, dtype, r * D + (int64_t)g * group + i);
+        vals[i] = v;
+        w_min = fminf(w_min, v);
+        w_max = fmaxf(w_max, v);
+      }
+      float scale = fmaxf((w_max - w_min) / n_bins, eps);
+      int side = fabsf(w_min) > fabsf(w_max);
+      scale = side ? scale : -scale;
+      float edge = side ? w_min : w_max;
+      float e_over_s = edge / scale;
+      ties += is_tie(e_over_s);
+      float q0 = roundf(e_over_s);
+      int at_zero = q0 == 0.0f;
+      scale = at_zero ? scale : edge / q0;
+      float bias = at_zero ? 0.0f : edge;
+      store_val(scales, dtype, r * groups + g, scale);
+      store_val(biases, dtype, r * groups + g, bias);
+      for (int i = 0; i < group; i++) {
+        float x = (vals[i] - bias) / scale;
+        ties += is_tie(x);
+        float qv = fminf(roundf(x), n_bins);
+        uint32_t code = qv > 0.0f ? (uint32_t)qv : 0u;
+        int e = g * group + i;
+        orow[e / per_word] |= code << (bits * (e % per_word));
+      }
+    }
+  }
+  free(vals);
+  return ties;
+}
+
+static inline uint32_t code_at(const uint32_t *row, int e, int bits) {
+  const int per_word = 32 / bits;
+  return (row[e / per_word] >> (bits * (e % per_word))) & ((1u << bits) - 1u);
+}
+
+/* quantized.h:2498-2560 (affine_dequantize): scale * q + bias. */
+void vkvo_dequantize(const uint32_t *wq, const void *scales, const void *biases,
+                     int dtype, int64_t rows, int D, int group, int bits, void *out) {
+  const int words_per_row = D * bits / 32;
+  const int groups = D / group;
+  for (int64_t r = 0; r < rows; r++) {
+    for (int e = 0; e < D; e++) {
+      float s = load_val(scales, dtype, r * groups + e / group);
+      float b = load_val(biases, dtype, r * groups + e / group);
+      float q = (float)code_at(wq + r * words_per_row, e, bits);
+      store_val(out, dtype, r * D + e, fmaf(s, q, b));
+    }
+  }
+}
+
+static inline int mask_visible(int mask_mode, const uint8_t *bmask, const float *fmask,
+                               int64_t mo, int l, int L, int t, int T, double *add) {
+  *add = 0.0;
+  if (mask_mode == 1) return t <= T - L + l;
+  if (mask_mode == 2) return bmask[mo] != 0;
+  if (mask_mode == 3) {
+    *add = fmask[mo];
+    return fmask[mo] >= -FLT_MAX;
+  }
+  return 1;
+}
+
+/* MLXFast.swift:173-218 semantics as computed by sdpa_vector.h:15-177:
+ * q scaled in fp32, softmax over visible keys, zero output for an empty row. */
+void vkvo_sdpa(const float *q, const float *k, const float *v, int B, int Hq,
+               int Hkv, int L, int T, int D, int Dv, float scale, int mask_mode,
+               const uint8_t *bmask, const float *fmask, int64_t msb, int64_t msh,
+               int64_t msl, int64_t mst, double *out) {
+  const int rep = Hq / Hkv;
+  double *sc = (double *)malloc(sizeof(double) * (size_t)(T > 0 ? T : 1));
+  unsigned char *vis = (unsigned char *)malloc((size_t)(T > 0 ? T : 1));
+  for (int b = 0; b < B; b++)
+    for (int h = 0; h < Hq; h++)
+      for (int l = 0; l < L; l++) {
+        const float *qr = q + (((int64_t)b * Hq + h) * L + l) * D;
+        const int hk = h / rep;
+        double mx = -INFINITY;
+        for (int t = 0; t < T; t++) {
+          double add;
+          int64_t mo = b * msb + h * msh + l * msl + t * mst;
+          vis[t] = (unsigned char)mask_visible(mask_mode, bmask, fmask, mo, l, L, t, T, &add);
+          if (!vis[t]) continue;
+          const float *kr = k + (((int64_t)b * Hkv + hk) * T + t) * D;
+          double s = 0.0;
+          for (int d = 0; d < D; d++) s += (double)(scale * qr[d]) * (double)kr[d];
+          sc[t] = s + add;
+          if (sc[t] > mx) mx = sc[t];
+        }
+        double den = 0.0;
+        double *o = out + (((int64_t)b * Hq + h) * L + l) * Dv;
+        for (int d = 0; d < Dv; d++) o[d] = 0.0;
+        for (int t = 0; t < T; t++) {
+          if (!vis[t]) continue;
+          double p = exp(sc[t] - mx);
+          den += p;
+          const float *vr = v + (((int64_t)b * Hkv + hk) * T + t) * Dv;
+          for (int d = 0; d < Dv; d++) o[d] += p * (double)vr[d];
+        }
+        if (den > 0.0)
+          for (int d = 0; d < Dv; d++) o[d] /= den;
+      }
+  free(sc);
+  free(vis);
+}
+
+/* One query row against one KV head of a quantized cache (reference layout
+ * rows of length D).  Shared by the batch and the CPU-baseline entry. */
+static void qsdpa_row(const float *qs, const uint32_t *kq, const float *ks,
+                      const float *kb, const uint32_t *vq, const float *vs,
+                      const float *vb, int T, int D, int group, int bits,
+                      const double *add, const unsigned char *vis, double fill,
+                      double *sc, double *o) {
+  const int wpr = D * bits / 32;
+  const int G = D / group;
+  double mx = -INFINITY;
+  for (int t = 0; t < T; t++) {
+    double s = fill;
+    if (!vis || vis[t]) {
+      const uint32_t *kr = kq + (int64_t)t * wpr;
+      s = 0.0;
+      for (int d = 0; d < D; d++) {
+        double kv = (double)ks[(int64_t)t * G + d / group] * (double)code_at(kr, d, bits) +
+                    (double)kb[(int64_t)t * G + d / group];
+        s += (double)qs[d] * kv;
+      }
+      if (add) s += add[t];
+    }
+    sc[t] = s;
+    if (s > mx) mx = s;
+  }
+  double den = 0.0;
+  for (int d = 0; d < D; d++) o[d] = 0.0;
+  for (int t = 0; t < T; t++) {
+    double p = exp(sc[t] - mx);
+    den += p;
+    const uint32_t *vr = vq + (int64_t)t * wpr;
+    for (int d = 0; d < D; d++) {
+      double vv = (double)vs[(int64_t)t * G + d / group] * (double)code_at(vr, d, bits) +
+                  (double)vb[(int64_t)t * G + d / group];
+      o[d] += p * vv;
+    }
+  }
+  if (den > 0.0)
+    for (int d = 0; d < D; d++) o[d] /= den;
+}
+
+/* KVCache.swift:1909-1997 (quantizedScaledDotProductAttention). */
+void vkvo_quantized_sdpa(const float *q, int q_dtype, const uint32_t *kq,
+                         const float *ks, const float *kb, const uint32_t *vq,
+                         const float *vs, const float *vb, int B, int Hq, int Hkv,
+                         int L, int T, int D, int group, int bits, float scale,
+                         int mask_mode, const uint8_t *bmask, const float *fmask,
+                         int64_t msb, int64_t msh, int64_t msl, int64_t mst,
+                         double *out) {
+  const int rep = Hq / Hkv;
+  const int wpr = D * bits / 32;
+  const int G = D / group;
+  const float scale_t = round_to(scale, q_dtype);
+  const double fill = type_lowest(q_dtype);
+  float *qs = (float *)malloc(sizeof(float) * (size_t)D);
+  double *sc = (double *)malloc(sizeof(double) * (size_t)(T > 0 ? T : 1));
+  double *add = (double *)malloc(sizeof(double) * (size_t)(T > 0 ? T : 1));
+  unsigned char *vis = (unsigned char *)malloc((size_t)(T > 0 ? T : 1));
+  for (int b = 0; b < B; b++)
+    for (int h = 0; h < Hq; h++)
+      for (int l = 0; l < L; l++) {
+        const float *qr = q + (((int64_t)b * Hq + h) * L + l) * D;
+        for (int d = 0; d < D; d++) qs[d] = round_to(qr[d] * scale_t, q_dtype);
+        const int hk = h / rep;
+        const int64_t kv_row0 = ((int64_t)b * Hkv + hk) * T;
+        for (int t = 0; t < T; t++) {
+          double a;
+          int64_t mo = b * msb + h * msh + l * msl + t * mst;
+          if (mask_mode == 1) {
+            /* causal: query row l sits at key position l + (T - L) */
+            vis[t] = (unsigned char)(l + (T - L) >= t);
+            add[t] = 0.0;
+          } else {
+            vis[t] = (unsigned char)mask_visible(mask_mode == 3 ? 0 : mask_mode, bmask, fmask,
+                                                 mo, l, L, t, T, &a);
+            add[t] = mask_mode == 3 ? (double)fmask[mo] : 0.0;
+          }
+        }
+        if (T == 0) {
+          double *o = out + (((int64_t)b * Hq + h) * L + l) * D;
+          for (int d = 0; d < D; d++) o[d] = 0.0;
+          continue;
+        }
+        qsdpa_row(qs, kq + kv_row0 * wpr, ks + kv_row0 * G, kb + kv_row0 * G,
+                  vq + kv_row0 * wpr, vs + kv_row0 * G, vb + kv_row0 * G, T, D, group,
+                  bits, add, vis, fill, sc, out + (((int64_t)b * Hq + h) * L + l) * D);
+      }
+  free(qs);
+  free(sc);
+  free(add);
+  free(vis);
+}
+
+void vkvo_quantized_decode_batch(const float *q, int q_dtype, const uint32_t *kq,
+                                 const float *ks, const float *kb, const uint32_t *vq,
+                                 const float *vs, const float *vb, int nseq,
+                                 const int32_t *lens, const int64_t *tok_off, int Hq,
+                                 int Hkv, int D, int group, int bits, float scale,
+                                 int threads, double *out) {
+  const int rep = Hq / Hkv;
+  const int wpr = D * bits / 32;
+  const int G = D / group;
+  const float scale_t = round_to(scale, q_dtype);
+  int maxT = 1;
+  for (int s = 0; s < nseq; s++) maxT = lens[s] > maxT ? lens[s] : maxT;
+#ifdef _OPENMP
+  if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel
+#endif
+  {
+    float *qs = (float *)malloc(sizeof(float) * (size_t)D);
+    double *sc = (double *)malloc(sizeof(double) * (size_t)maxT);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1) collapse(2)
+#endif
+    for (int s = 0; s < nseq; s++)
+      for (int h = 0; h < Hq; h++) {
+        const float *qr = q + ((int64_t)s * Hq + h) * D;
+        for (int d = 0; d < D; d++) qs[d] = round_to(qr[d] * scale_t, q_dtype);
+        const int64_t T = lens[s];
+        /* sequence s is stored [Hkv, T, ...] starting at token row tok_off[s] */
+        const int64_t row0 = tok_off[s] + (int64_t)(h / rep) * T;
+        qsdpa_row(qs, kq + row0 * wpr, ks + row0 * G, kb + row0 * G, vq + row0 * wpr,
+                  vs + row0 * G, vb + row0 * G, (int)T, D, group, bits, NULL, NULL, 0.0, sc,
+                  out + ((int64_t)s * Hq + h) * D);
+      }
+    free(qs);
+    free(sc);
+  }
+}
+
+/* GLM4MOELite.swift:233-290 absorbed MLA decode through
+ * AttentionUtils.swift:43-75 (L == 1 promoted to fp32 SDPA with one KV head):
+ * keys are the cache entries (dequantized to the storage dtype, here given as
+ * f32 values), values are their first Dv dims. */
+void vkvo_mla_decode(const float *q, const uint32_t *cq, const float *cs,
+                     const float *cb, int B, int H, int T, const int32_t *lens,
+                     int Dk, int Dv, int group, int bits, float scale, double *out) {
+  const int wpr = Dk * bits / 32;
+  const int G = Dk / group;
+  double *kv = (double *)malloc(sizeof(double) * (size_t)Dk * (size_t)(T > 0 ? T : 1));
+  double *sc = (double *)malloc(sizeof(double) * (size_t)(T > 0 ? T : 1));
+  for (int b = 0; b < B; b++) {
+    const int n = lens[b];
+    for (int t = 0; t < n; t++) {
+      const int64_t row = (int64_t)b * T + t;
+      for (int d = 0; d < Dk; d++) {
+        /* dequantize to the storage dtype (bf16 for this cache) */
+        float s = cs[row * G + d / group], bb = cb[row * G + d / group];
+        float deq = fmaf(s, (float)code_at(cq + row * wpr, d, bits), bb);
+        kv[(int64_t)t * Dk + d] = (double)vkvo_bf16_to_f32(vkvo_f32_to_bf16(deq));
+      }
+    }
+    for (int h = 0; h < H; h++) {
+      const float *qr = q + ((int64_t)b * H + h) * Dk;
+      double mx = -INFINITY;
+      for (int t = 0; t < n; t++) {
+        double s = 0.0;
+        for (int d = 0; d < Dk; d++) s += (double)(scale * qr[d]) * kv[(int64_t)t * Dk + d];
+        sc[t] = s;
+        if (s > mx) mx = s;
+      }
+      double *o = out + ((int64_t)b * H + h) * Dv;
+      for (int d = 0; d < Dv; d++) o[d] = 0.0;
+      double den = 0.0;
+      for (int t = 0; t < n; t++) {
+        double p = exp(sc[t] - mx);
+        den += p;
+        for (int d = 0; d < Dv; d++) o[d] += p * kv[(int64_t)t * Dk + d];
+      }
+      if (den > 0.0)
+        for (int d = 0; d < Dv; d++) o[d] /= den;
+    }
+  }
+  free(kv);
+  free(sc);
+}
