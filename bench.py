@@ -1,0 +1,240 @@
+"""Benchmark: paged 4-bit KV decode attention + KV append (config 3).
+
+Workload ("Paged continuous batching"): a pool of
+16384 blocks x 32 tokens per layer, bf16 inputs stored affine 4-bit g64,
+8 KV heads x 128 dims; 64 sequences with lengths U[128, 8192] whose block
+tables are random permutations of pool ids; 32 sequences share one
+refcounted 2048-token prefix (64 blocks).  One step = for each of the
+--layers layers: append one token per sequence plus one 512-token
+chunked-prefill chunk, then decode attention (32 query heads) over every
+sequence.  Synthetic data, generated on the GPU; all inputs are resident in
+HBM before timing starts.  The step writes the decode token at the same
+position each step, so every step does identical work.
+
+Prints one JSON line (see DESIGN.md for the field definitions).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "vmlx-swift_amd"))
+
+HBM_PEAK_GBS = 8000.0
+BYTES_PER_TOKEN_HEAD = 144  # 4-bit K+V codes (2 x 64 B) + 2 groups x (scale+bias) x 2 B x 2
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--layers", type=int, default=32)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-threads", type=int, default=0)
+    return p.parse_args()
+
+
+def build_scene(torch, vkv, layers, seed=3):
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    nblocks, bs, H, D, Hq = 16384, 32, 8, 128, 32
+    n_seqs, share_tokens, n_share, prefill = 64, 2048, 32, 512
+    lens = rng.integers(128, 8193, n_seqs)
+    sharers = [i for i in range(n_seqs) if lens[i] > share_tokens][:n_share]
+    perm = rng.permutation(np.arange(1, nblocks))
+    nxt = 0
+
+    def take(n):
+        nonlocal nxt
+        out = perm[nxt:nxt + n]
+        nxt += n
+        return list(out)
+
+    shared = take(share_tokens // bs)
+    tables = []
+    for s in range(n_seqs):
+        L = int(lens[s]) + 1  # + the decode token
+        nb = (L + bs - 1) // bs
+        if s in sharers:
+            t = shared + take(nb - len(shared))
+        else:
+            t = take(nb)
+        tables.append(t)
+    prefill_blocks = take(prefill // bs)
+    width = max(len(t) for t in tables)
+    tab = np.zeros((n_seqs, width), np.int32)
+    for s, t in enumerate(tables):
+        tab[s, :len(t)] = t
+    # slots: initial fill (each shared block written once), decode tokens, prefill chunk
+    fill_slots = []
+    for s in range(n_seqs):
+        start = share_tokens if (s in sharers and s != sharers[0]) else 0
+        fill_slots += [tables[s][p // bs] * bs + p % bs for p in range(start, int(lens[s]))]
+    dec_slots = [tables[s][int(lens[s]) // bs] * bs + int(lens[s]) % bs for s in range(n_seqs)]
+    pre_slots = [prefill_blocks[p // bs] * bs + p % bs for p in range(prefill)]
+    dev = dict(device="cuda")
+    sc = dict(
+        nblocks=nblocks, bs=bs, H=H, D=D, Hq=Hq, n_seqs=n_seqs, lens=lens, sharers=sharers,
+        share_tokens=share_tokens, prefill=prefill,
+        table=torch.from_numpy(tab).to(**dev),
+        seq_lens=torch.from_numpy((lens + 1).astype(np.int32)).to(**dev),
+        max_len=int(lens.max()) + 1,
+        fill_slots=torch.tensor(fill_slots, dtype=torch.int32, **dev),
+        dec_slots=torch.tensor(dec_slots, dtype=torch.int32, **dev),
+        pre_slots=torch.tensor(pre_slots, dtype=torch.int32, **dev),
+    )
+    pool = vkv.PagedPool(nblocks, bs, layers, H, D, dtype=vkv.BF16, bits=4)
+    nfill = len(fill_slots)
+    stage_k = torch.empty((nfill, H, D), dtype=torch.bfloat16, **dev)
+    stage_v = torch.empty_like(stage_k)
+    for l in range(layers):
+        vkv.fill_normal(stage_k, seed=1000 + 2 * l)
+        vkv.fill_normal(stage_v, seed=1001 + 2 * l)
+        pool.append(l, stage_k, stage_v, sc["fill_slots"])
+    del stage_k, stage_v
+    sc["q"] = vkv.fill_normal(torch.empty((layers, n_seqs, Hq, D), dtype=torch.bfloat16, **dev), 7)
+    sc["dk"] = vkv.fill_normal(torch.empty((layers, n_seqs, H, D), dtype=torch.bfloat16, **dev), 8)
+    sc["dv"] = vkv.fill_normal(torch.empty((layers, n_seqs, H, D), dtype=torch.bfloat16, **dev), 9)
+    sc["pk"] = vkv.fill_normal(torch.empty((layers, prefill, H, D), dtype=torch.bfloat16, **dev), 10)
+    sc["pv"] = vkv.fill_normal(torch.empty((layers, prefill, H, D), dtype=torch.bfloat16, **dev), 11)
+    sc["out"] = torch.empty((layers, n_seqs, Hq, D), dtype=torch.bfloat16, **dev)
+    sc["views"] = [pool.view(l, sc["table"], sc["seq_lens"], sc["max_len"]) for l in range(layers)]
+    torch.cuda.synchronize()
+    return pool, sc
+
+
+def cpu_baseline(threads):
+    """The CPU oracle (C restatement of the reference arithmetic) on a bounded
+    sample of the same workload: 8 sequences x 2048 tokens, 32 query heads."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    rng = np.random.default_rng(5)
+    n, T, H, Hq, D = 8, 2048, 8, 32, 128
+    x = O.from_f32(rng.standard_normal((n, H, T, D)).astype(np.float32), O.BF16)
+    kq, ks, kb, _ = O.quantize(x, O.BF16, 64, 4)
+    vq, vs, vb, _ = O.quantize(x[:, :, ::-1].copy(), O.BF16, 64, 4)
+    f = lambda a: O.to_f32(a, O.BF16)
+    ks, kb, vs, vb = f(ks), f(kb), f(vs), f(vb)
+    q = f(O.from_f32(rng.standard_normal((n, Hq, D)).astype(np.float32), O.BF16))
+    lens = np.full(n, T, np.int32)
+    off = np.arange(n, dtype=np.int64) * H * T
+    t0 = time.perf_counter()
+    O.quantized_decode_batch(q, O.BF16, kq, ks, kb, vq, vs, vb, lens, off, H, D ** -0.5, 64, 4,
+                             threads=threads)
+    dt = time.perf_counter() - t0
+    byts = n * T * H * BYTES_PER_TOKEN_HEAD
+    return {"value": round(byts / dt / 1e9, 4), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{n} sequences x {T} tokens, 8 KV / 32 query heads, 4-bit g64, one layer, "
+                      f"{dt:.2f} s, C oracle (fp64 restatement of the reference arithmetic)"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: every GPU box in this build has one, "
+              "so --gpus must be 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import vkv
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    torch.cuda.set_device(0)
+    layers = args.layers
+    pool, sc = build_scene(torch, vkv, layers)
+    stream = torch.cuda.current_stream()
+    scale = sc["D"] ** -0.5
+
+    def step(ev=None):
+        for l in range(layers):
+            if ev is not None:
+                ev[0][l].record(stream)
+            pool.append(l, sc["dk"][l], sc["dv"][l], sc["dec_slots"])
+            pool.append(l, sc["pk"][l], sc["pv"][l], sc["pre_slots"])
+            if ev is not None:
+                ev[1][l].record(stream)
+            o = sc["out"][l]
+            vkv._chk(vkv.lib().vkv_paged_sdpa(
+                vkv.C.byref(vkv.arr(sc["q"][l])), vkv.C.byref(sc["views"][l]), vkv.C.c_float(scale),
+                vkv.C.byref(vkv.arr(o)), vkv.stream_ptr()))
+            if ev is not None:
+                ev[2][l].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # whole-step timing
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(args.steps):
+        step()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / args.steps
+    # per-kernel timing inside the same kind of steps
+    app_ms = att_ms = 0.0
+    for _ in range(args.steps):
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(layers)] for _ in range(3)]
+        step(ev)
+        torch.cuda.synchronize()
+        for l in range(layers):
+            app_ms += ev[0][l].elapsed_time(ev[1][l])
+            att_ms += ev[1][l].elapsed_time(ev[2][l])
+    n_att = args.steps * layers
+    att_avg_ms = att_ms / n_att
+    app_avg_ms = app_ms / n_att
+
+    lens = sc["lens"] + 1
+    logical = int(lens.sum()) * sc["H"] * BYTES_PER_TOKEN_HEAD
+    unique = logical - (len(sc["sharers"]) - 1) * sc["share_tokens"] * sc["H"] * BYTES_PER_TOKEN_HEAD
+    gbs_step = logical * layers / (ms_per_step * 1e-3) / 1e9
+    att_gbs = logical / (att_avg_ms * 1e-3) / 1e9
+    append_tokens = sc["n_seqs"] + sc["prefill"]
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        cpu = cpu_baseline(threads)
+    rec = {
+        "metric": "KV-read GB/s (% HBM peak) in paged quant decode attn; KV append tokens/s",
+        "value": round(gbs_step, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 KV stored affine u4 g64 (fp32 accumulate)",
+        "data": "synthetic (GPU counter-based normal samples)",
+        "config": {
+            "workload": "paged continuous batching: 64 seqs U[128,8192] + 1 decode token, "
+                        "pool 16384 x 32-token blocks per layer, 32/8 heads x 128, 4-bit g64, "
+                        "32 seqs share a 2048-token prefix, +512-token chunked prefill append",
+            "layers": layers, "n_seqs": sc["n_seqs"], "sum_len": int(lens.sum()),
+            "kv_bytes_logical_per_layer": logical, "kv_bytes_unique_per_layer": unique,
+        },
+        "attention": {"ms_per_layer": round(att_avg_ms, 5), "gbs_logical": round(att_gbs, 1),
+                      "gbs_unique": round(unique / (att_avg_ms * 1e-3) / 1e9, 1),
+                      "pct_hbm_peak": round(100 * att_gbs / HBM_PEAK_GBS, 2)},
+        "append": {"tokens_per_layer_step": append_tokens,
+                   "ms_per_layer": round(app_avg_ms, 5),
+                   "tokens_per_s": round(append_tokens / (app_avg_ms * 1e-3), 1)},
+        "roofline": {"bound": "hbm", "achieved": round(att_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(att_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

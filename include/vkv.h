@@ -1,0 +1,385 @@
+/*
+ * vkv.h -- C ABI of the MI355X KV-cache engine (libvkv.so).
+ *
+ * This is the drop-in boundary for the KV-cache hot path of vmlx-swift.  The
+ * reference reaches its tensor arithmetic through mlx-c (the headers under
+ * `Source/Cmlx/include/mlx/c/`, exposed to Swift by `Source/Cmlx/include/module.modulemap:1-3`)
+ * and its cache state machines through the Swift `KVCache` protocol
+ * (`Libraries/MLXLMCommon/KVCache.swift:38-77`).  Each entry point below
+ * names the reference interface it replaces.  Paths are relative to the
+ * osaurus-ai/vmlx-swift checkout.
+ *
+ * Conventions (mirroring mlx-c, `Libraries/CmlxDistributedShim/
+ * MlxCDistributed.cpp:11-28`):
+ *   - every call returns int: 0 = success, non-zero = failure; nothing throws
+ *     across the ABI.  vkv_last_error() gives the message of the calling
+ *     thread's last failure.
+ *   - device memory behind a cache / pool handle is owned by the handle.
+ *     Arrays and views returned by a call stay valid until the next mutating
+ *     call on the same handle (the reference returns MLX views with the same
+ *     lifetime, KVCache.swift:465-508).
+ *   - every call that launches work takes a hipStream_t passed as void*
+ *     (NULL = the default stream); work is stream-ordered, calls do not
+ *     synchronize unless they say so.
+ *   - cache handles are single-writer (the reference's caches take no
+ *     locks); the prefix-cache manager is internally locked like
+ *     PagedCacheManager (PagedCacheManager.swift:51-52).
+ */
+#ifndef VKV_H
+#define VKV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VKV_ABI_VERSION 1
+
+/* ------------------------------------------------------------------ types */
+
+/* element types (the subset of mlx_dtype the cache path uses) */
+enum {
+  VKV_F32 = 0,
+  VKV_F16 = 1,
+  VKV_BF16 = 2,
+  VKV_U32 = 3,
+  VKV_I32 = 4,
+  VKV_U8 = 5,
+  VKV_BOOL = 6
+};
+
+/* A strided device array of up to 4 dims (strides in elements).  Replaces
+ * mlx_array at this boundary (`Source/Cmlx/include/mlx/c/array.h`). */
+typedef struct vkv_array {
+  void *data;
+  int32_t dtype;
+  int32_t ndim;
+  int64_t shape[4];
+  int64_t strides[4];
+} vkv_array;
+
+/* Paged KV storage as the attention kernels read it.  Produced by
+ * vkv_pool_view() and vkv_cache_update_quantized(); it has no reference
+ * counterpart (the reference concatenates blocks back into one array,
+ * Cache/CacheHelpers.swift:431-552).
+ *
+ * Block format of one (layer, block, kv head) chunk, head_bytes long:
+ *   float blocks (bits == 0):  K [block_size][head_dim] dtype,
+ *                              V [block_size][head_dim] dtype
+ *   affine blocks (bits 4/8):  K codes [block_size][head_dim*bits/8] bytes,
+ *                              V codes [head_dim][block_size*bits/8] bytes
+ *                                (dim-major: the tokens of one dim are
+ *                                contiguous, which is the operand order the
+ *                                P.V contraction needs),
+ *                              K scales, K biases, V scales, V biases
+ *                                [block_size][head_dim/group] dtype each.
+ *   keys-only (flags & VKV_VIEW_KEYS_ONLY, MLA latent): K codes, K scales,
+ *                                K biases only; values are the first
+ *                                v_head_dim dims of the key entry.
+ * Codes pack element i of a 32-bit little-endian word at bit bits*i, the
+ * reference's packing (quantized.h:2455-2497). */
+enum { VKV_VIEW_KEYS_ONLY = 1 };
+
+typedef struct vkv_paged_view {
+  const void *base;            /* device address of block 0 of this layer */
+  int32_t dtype;               /* element dtype (float) / scale-bias dtype */
+  int32_t bits;                /* 0, 4 or 8 */
+  int32_t group_size;          /* affine group size (64) */
+  int32_t n_kv_heads;
+  int32_t head_dim;            /* key dims */
+  int32_t v_head_dim;          /* value dims (== head_dim unless keys-only) */
+  int32_t block_size;          /* tokens per block */
+  int32_t flags;
+  int64_t block_bytes;         /* bytes of one block (all kv heads) */
+  int64_t head_bytes;          /* bytes of one (block, kv head) chunk */
+  const int32_t *block_table;  /* device [n_seqs, table_stride] block ids */
+  int32_t table_stride;
+  const int32_t *seq_lens;     /* device [n_seqs] valid tokens per sequence;
+                                  NULL = every sequence holds max_len */
+  int32_t n_seqs;
+  int32_t max_len;             /* host-side upper bound of seq_lens */
+} vkv_paged_view;
+
+typedef struct vkv_cache_s *vkv_cache;
+typedef struct vkv_pool_s *vkv_pool;
+typedef struct vkv_prefix_s *vkv_prefix;
+
+/* ------------------------------------------------------------------ errors */
+
+/* Last error message of the calling thread ("" when none).  Replaces
+ * mlx_set_error_handler's message delivery (mlx/c/error.h:15-24). */
+const char *vkv_last_error(void);
+int vkv_abi_version(void);
+/* Count of HIP devices visible to the library (0 on a host without a GPU). */
+int vkv_device_count(int32_t *count);
+
+/* ------------------------------------------------ quantization operators */
+
+/* mlx_quantize (mlx/c/ops.h:801-808) -> affine_quantize
+ * (mlx-generated/metal/quantized.h:2393-2497), affine mode only.
+ * w: [..., D] f16/bf16/f32, last dim contiguous, D % group_size == 0.
+ * Writes wq [..., D*bits/32] u32, scales/biases [..., D/group_size] of w's
+ * dtype (all contiguous, caller-allocated).  bits in {4, 8}. */
+int vkv_quantize_affine(const vkv_array *w, int32_t group_size, int32_t bits,
+                        vkv_array *wq, vkv_array *scales, vkv_array *biases,
+                        void *stream);
+
+/* mlx_dequantize (mlx/c/ops.h:359-369) -> affine_dequantize
+ * (quantized.h:2498-2560): out = scale * q + bias, one fp32 fused
+ * multiply-add rounded once to the output dtype (scales' dtype). */
+int vkv_dequantize_affine(const vkv_array *wq, const vkv_array *scales,
+                          const vkv_array *biases, int32_t group_size, int32_t bits,
+                          vkv_array *out, void *stream);
+
+/* ----------------------------------------------------------- attention */
+
+enum { VKV_MASK_NONE = 0, VKV_MASK_CAUSAL = 1, VKV_MASK_ARRAY = 2 };
+
+/* mlx_fast_scaled_dot_product_attention (mlx/c/fast.h:189-198) as called
+ * by MLXFast.scaledDotProductAttention (MLX/MLXFast.swift:203-218):
+ * q [B,Hq,L,D], k [B,Hkv,T,D], v [B,Hkv,T,Dv] (strided, same float dtype),
+ * Hq % Hkv == 0 (GQA without tiling).  fp32 softmax and accumulation.
+ * mask_mode VKV_MASK_ARRAY takes a bool or float (additive) mask array
+ * broadcastable to [B,Hq,L,T] (stride 0 on broadcast dims).  out [B,Hq,L,Dv]
+ * in q's dtype.  A row with no visible key yields zeros. */
+int vkv_sdpa(const vkv_array *q, const vkv_array *k, const vkv_array *v, float scale,
+             int32_t mask_mode, const vkv_array *mask, vkv_array *out, void *stream);
+
+/* quantizedScaledDotProductAttention (MLXLMCommon/KVCache.swift:1909-1997)
+ * over quantized tuples in the reference layout: k_wq [B,Hkv,T,D*bits/32]
+ * u32, k_scales/k_biases [B,Hkv,T,D/group] (likewise v_*).  Queries are
+ * scaled in their own dtype first (T(q * T(scale))), masked scores are
+ * filled with the dtype's lowest value before the softmax, so a fully masked
+ * row averages V (unlike vkv_sdpa). */
+int vkv_quantized_sdpa(const vkv_array *q, const vkv_array *k_wq,
+                       const vkv_array *k_scales, const vkv_array *k_biases,
+                       const vkv_array *v_wq, const vkv_array *v_scales,
+                       const vkv_array *v_biases, int32_t group_size, int32_t bits,
+                       float scale, int32_t mask_mode, const vkv_array *mask,
+                       vkv_array *out, void *stream);
+
+/* Decode attention over paged KV: one query token per sequence.
+ * q [n_seqs, Hq, D] (strided), out [n_seqs, Hq, Dv] in q's dtype.  For
+ * affine views the arithmetic is the reference's quantized SDPA
+ * (KVCache.swift:1909-1997, queries scaled in their dtype); for float views
+ * it is MLXFast SDPA (sdpa_vector.h:15-177).  Sequence s attends to its
+ * seq_lens[s] tokens; a sequence of length 0 yields zeros.  Replaces the
+ * reference's pad-and-concatenate batching (BatchEngine/BatchKVCache.swift:
+ * 83-113, 177-193) for the continuous-batching decode step. */
+int vkv_paged_sdpa(const vkv_array *q, const vkv_paged_view *kv, float scale,
+                   vkv_array *out, void *stream);
+
+/* Absorbed-latent MLA decode (MLXLLM/Models/GLM4MOELite.swift:233-290 via
+ * MLXLMCommon/AttentionUtils.swift:43-75): one shared latent head; kv is a
+ * keys-only affine view (entries of head_dim = 576 dims, values = first
+ * v_head_dim = 512 dims).  q [n_seqs, H, head_dim] bf16, out [n_seqs, H,
+ * v_head_dim] bf16.  QK^T and PV run as bf16/f16 MFMA contractions over the
+ * H query heads. */
+int vkv_mla_decode(const vkv_array *q, const vkv_paged_view *kv, float scale,
+                   vkv_array *out, void *stream);
+
+/* ------------------------------------------------------- per-layer caches */
+
+enum {
+  VKV_CACHE_SIMPLE = 0,    /* KVCacheSimple    KVCache.swift:452-596 */
+  VKV_CACHE_ROTATING = 1,  /* RotatingKVCache  KVCache.swift:605-958 */
+  VKV_CACHE_QUANTIZED = 2  /* QuantizedKVCache KVCache.swift:961-1221 */
+};
+
+typedef struct vkv_cache_params {
+  int32_t kind;
+  int32_t step;        /* growth step, default 256 (KVCache.swift:455, :966) */
+  int32_t max_size;    /* rotating window (RotatingKVCache.init maxSize) */
+  int32_t keep;        /* rotating keep prefix */
+  int32_t group_size;  /* quantized: 64 */
+  int32_t bits;        /* quantized: 4 or 8 (default 8, KVCache.swift:970) */
+} vkv_cache_params;
+
+/* Cache construction: KVCacheSimple(), RotatingKVCache(maxSize:keep:step:),
+ * QuantizedKVCache(groupSize:bits:).  Zero fields take the reference
+ * defaults (step 256, group 64, bits 8, keep 0). */
+int vkv_cache_create(const vkv_cache_params *params, vkv_cache *out);
+int vkv_cache_destroy(vkv_cache cache);
+/* copy() (KVCache.swift:583-591, :947-954, :1188-1195): deep, independent. */
+int vkv_cache_copy(vkv_cache cache, void *stream, vkv_cache *out);
+
+/* update(keys:values:) (KVCache.swift:465-508, :791-799).  keys [B,Hkv,S,D],
+ * values [B,Hkv,S,Dv] (strided).  out_keys/out_values receive views of the
+ * cached K/V exactly as the reference returns them (trimmed to offset, or the
+ * whole ring once a rotating cache has wrapped).  Fails on a quantized cache
+ * like the reference traps (KVCache.swift:1126-1130). */
+int vkv_cache_update(vkv_cache cache, const vkv_array *keys, const vkv_array *values,
+                     void *stream, vkv_array *out_keys, vkv_array *out_values);
+
+/* updateQuantized(keys:values:) (KVCache.swift:1049-1122): quantizes the new
+ * tokens (affine, bit-exact with quantized.h:2393-2497) into the cache and
+ * returns the whole cache as a paged view for vkv_paged_sdpa (queries
+ * [B,Hq,D] for one decode token).  The reference-layout tuples are available
+ * from vkv_cache_state(). */
+int vkv_cache_update_quantized(vkv_cache cache, const vkv_array *keys,
+                               const vkv_array *values, void *stream,
+                               vkv_paged_view *out);
+
+/* offset / maxSize / isTrimmable / trim(n) (KVCache.swift:38-77). */
+int vkv_cache_offset(vkv_cache cache, int64_t *offset);
+int vkv_cache_max_size(vkv_cache cache, int64_t *max_size); /* -1 = none */
+int vkv_cache_is_trimmable(vkv_cache cache, int32_t *trimmable);
+int vkv_cache_trim(vkv_cache cache, int64_t n, int64_t *trimmed);
+/* Physical token capacity (the reference's keys.dim(2)); no protocol
+ * counterpart, exposed so growth can be checked against the reference. */
+int vkv_cache_capacity(vkv_cache cache, int64_t *capacity);
+
+/* state getter (KVCache.swift:527-547, :801-823, :1133-1166): fills
+ * `arrays` (room for 6) and *count: 2 for float caches (views), 6 for the
+ * quantized cache (keys wq/scales/biases, values wq/scales/biases in the
+ * reference layout, materialized into cache-owned memory). */
+int vkv_cache_state(vkv_cache cache, void *stream, vkv_array *arrays, int32_t *count);
+/* state setter: copies the arrays in (2 or 6, reference layout).  For
+ * KVCacheSimple the offset becomes dim(2); for the rotating and quantized
+ * caches offset comes from metaState, as in the reference. */
+int vkv_cache_set_state(vkv_cache cache, const vkv_array *arrays, int32_t count,
+                        void *stream);
+/* metaState (KVCache.swift:824-853, :1168-1177): NUL-separated strings in
+ * buf; *count receives the number of strings. */
+int vkv_cache_meta_state(vkv_cache cache, char *buf, int64_t buf_len, int32_t *count);
+int vkv_cache_set_meta_state(vkv_cache cache, const char *const *strings, int32_t count);
+
+/* makeMask(n:windowSize:returnArray:) (KVCache.swift:287-311, :890-927).
+ * window <= 0 means nil.  *mode receives VKV_MASK_*; for VKV_MASK_ARRAY,
+ * *mask receives a bool array owned by the cache ([n, offset+n] or the
+ * rolled [maskSize] row of the rotating single-token case). */
+int vkv_cache_make_mask(vkv_cache cache, int32_t n, int32_t window, int32_t return_array,
+                        void *stream, int32_t *mode, vkv_array *mask);
+
+/* KVCacheSimple.toQuantized (KVCache.swift:561-581) and
+ * QuantizedKVCache.toUnquantized (:1199-1220); new handles. */
+int vkv_cache_to_quantized(vkv_cache simple, int32_t group_size, int32_t bits,
+                           void *stream, vkv_cache *out);
+int vkv_cache_to_unquantized(vkv_cache quantized, void *stream, vkv_cache *out);
+/* RotatingKVCache.temporallyOrderedKV (KVCache.swift:876-887) and
+ * KVCacheSimple.readKV (:516-525): K/V in temporal order, trimmed to offset,
+ * without changing the cache state. */
+int vkv_cache_read_kv(vkv_cache cache, void *stream, vkv_array *keys, vkv_array *values);
+
+/* ---------------------------------------------------- paged block pool */
+
+typedef struct vkv_pool_params {
+  int32_t num_blocks;   /* pool size in blocks (block 0 is reserved as the
+                           null sentinel, PagedCacheManager.swift:86-92) */
+  int32_t block_size;   /* tokens per block */
+  int32_t n_layers;
+  int32_t n_kv_heads;
+  int32_t head_dim;
+  int32_t v_head_dim;   /* 0 = head_dim; keys-only pools ignore it */
+  int32_t dtype;        /* element dtype of appended K/V (and of scales) */
+  int32_t bits;         /* 0 = float blocks, 4/8 = affine quantized blocks */
+  int32_t group_size;   /* 64 */
+  int32_t flags;        /* VKV_VIEW_KEYS_ONLY for an MLA latent pool */
+} vkv_pool_params;
+
+int vkv_pool_create(const vkv_pool_params *params, vkv_pool *out);
+int vkv_pool_destroy(vkv_pool pool);
+/* Bytes of device memory the pool holds. */
+int vkv_pool_bytes(vkv_pool pool, int64_t *bytes);
+/* Build the attention view of one layer over caller block tables. */
+int vkv_pool_view(vkv_pool pool, int32_t layer, const int32_t *block_table,
+                  int32_t table_stride, const int32_t *seq_lens, int32_t n_seqs,
+                  int32_t max_len, vkv_paged_view *out);
+
+/* Scatter new tokens into pool blocks (quantizing on the way for affine
+ * pools).  keys [N,Hkv,D], values [N,Hkv,Dv] (strided; a [1,H,T,D] cache
+ * array is passed as [T,H,D] with strides {D, T*D, 1}); slot_mapping
+ * device int32 [N], slot = block_id * block_size + offset_in_block.  Replaces
+ * the reference's per-sequence slice assignment (KVCache.swift:498-502,
+ * :1105-1116) and block split (CacheCoordinator.swift:1238-1272).  Quantized
+ * codes, scales and biases are bit-exact with the reference quantizer. */
+int vkv_paged_append(vkv_pool pool, int32_t layer, const vkv_array *keys,
+                     const vkv_array *values, const int32_t *slot_mapping, int64_t n_tokens,
+                     void *stream);
+
+/* Gather (dequant-on-read) into contiguous arrays keys [n_seqs,Hkv,T,D],
+ * values [n_seqs,Hkv,T,Dv] (T = view max_len; tokens past a sequence's
+ * length are left untouched), in the view's dtype.  restoreLayerData's
+ * concatenation (CacheHelpers.swift:431-552) without the copies. */
+int vkv_paged_gather(const vkv_paged_view *kv, vkv_array *keys, vkv_array *values,
+                     void *stream);
+/* Gather the raw affine codes into the reference layout: out[0..5] =
+ * keys wq [n,H,T,D*bits/32] u32, keys scales, keys biases [n,H,T,D/g],
+ * values wq, scales, biases (keys-only views fill out[0..2]). */
+int vkv_paged_gather_quantized(const vkv_paged_view *kv, vkv_array *out, void *stream);
+/* Copy whole blocks (all layers): dst[i] <- src[i] (host arrays of block
+ * ids); copy-on-write of a shared partial block and the store copy of the
+ * prefix cache. */
+int vkv_pool_copy_blocks(vkv_pool pool, const int32_t *src, const int32_t *dst, int32_t n,
+                         void *stream);
+
+/* ------------------------------------------ prefix cache (PagedCacheManager) */
+
+/* PagedCacheManager(blockSize:maxBlocks:modelKey:) (PagedCacheManager.swift:
+ * 80-96).  model_key may be NULL.  `pool` may be NULL (bookkeeping only);
+ * when given, block ids are pool block ids and stores copy KV on device. */
+int vkv_prefix_create(int32_t block_size, int32_t max_blocks, const char *model_key,
+                      vkv_pool pool, vkv_prefix *out);
+int vkv_prefix_destroy(vkv_prefix mgr);
+/* allocateBlock (:104-127): *block = -1 when the pool is exhausted. */
+int vkv_prefix_allocate(vkv_prefix mgr, int32_t *block);
+/* freeBlock (:135-156). */
+int vkv_prefix_free(vkv_prefix mgr, int32_t block);
+/* CacheCoordinator.release(blocks:) (Cache/CacheCoordinator.swift:351-358):
+ * frees `blocks` leaves first (reverse order) so roots stay the newest LRU
+ * entries. */
+int vkv_prefix_release(vkv_prefix mgr, const int32_t *blocks, int32_t n);
+/* Extra reference for a block shared by another sequence (fork). */
+int vkv_prefix_incref(vkv_prefix mgr, int32_t block);
+int vkv_prefix_ref_count(vkv_prefix mgr, int32_t block, int32_t *ref_count);
+/* findCachedBlock(hash:) (:164-180): *block = -1 on a miss. */
+int vkv_prefix_find(vkv_prefix mgr, const char *hash, int32_t *block);
+/* registerBlock(_:hash:) (:187-192). */
+int vkv_prefix_register(vkv_prefix mgr, int32_t block, const char *hash);
+/* clear() (:195-217). */
+int vkv_prefix_clear(vkv_prefix mgr);
+/* storeTokenSequence(tokens:layerData:mediaSalt:) (:229-310).  Chunks
+ * [0, n_data_chunks) have KV; with a pool, chunk i's KV is copied on
+ * `stream` from pool block src_blocks[i] into the newly allocated block. */
+int vkv_prefix_store(vkv_prefix mgr, const int64_t *tokens, int64_t n_tokens,
+                     const char *media_salt, int32_t n_data_chunks,
+                     const int32_t *src_blocks, void *stream);
+/* fetchPrefix(tokens:mediaSalt:) (:320-376): pins and returns the matched
+ * blocks (up to `capacity`), *n_blocks and *matched_tokens (0 = nil). */
+int vkv_prefix_fetch(vkv_prefix mgr, const int64_t *tokens, int64_t n_tokens,
+                     const char *media_salt, int32_t *blocks, int32_t capacity,
+                     int32_t *n_blocks, int64_t *matched_tokens);
+
+/* CacheStats (PagedCacheManager.swift:10-17). */
+typedef struct vkv_prefix_stats {
+  int64_t total_blocks, allocated_blocks, free_blocks, cache_hits, cache_misses, evictions;
+} vkv_prefix_stats;
+int vkv_prefix_stats_get(vkv_prefix mgr, vkv_prefix_stats *out);
+/* Block metadata: token count of a stored block (-1 if none). */
+int vkv_prefix_block_tokens(vkv_prefix mgr, int32_t block, int32_t *n_tokens);
+
+/* CacheBlock.computeBlockHash (CacheBlock.swift:110-146): SHA-256 over
+ * modelKey UTF-8, "|media:" + salt, parent hash UTF-8, then the tokens as
+ * raw little-endian Int64 bytes; 64 lowercase hex chars + NUL into out[65]. */
+int vkv_block_hash(const char *parent_hash, const int64_t *tokens, int64_t n_tokens,
+                   const char *model_key, const char *media_salt, char *out);
+
+/* Strided copy between two arrays of the same shape and element size
+ * (materializes a view returned by a cache into caller memory).  Replaces
+ * the reference's `x * 1` owned copy (KVCache.swift:100-102). */
+int vkv_array_copy(const vkv_array *src, vkv_array *dst, void *stream);
+
+/* ------------------------------------------------------------ synthetic */
+
+/* Fill a contiguous f16/bf16/f32 device buffer with counter-based normal
+ * samples (SplitMix64 -> Box-Muller in fp32 -> round to dtype), value i
+ * depends only on (seed, i).  `std` scales the samples.  Benchmark input
+ * generator; no reference counterpart. */
+int vkv_fill_normal(void *data, int32_t dtype, int64_t n, uint64_t seed, float std,
+                    void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VKV_H */

@@ -1,0 +1,146 @@
+"""GPU parity of the stateless operators through the C ABI against the CPU
+oracle: affine quantize / dequantize (bit-exact), float SDPA and quantized
+SDPA (tolerance), on seeded inputs including the reference's own known
+answers."""
+import numpy as np
+import pytest
+import torch
+
+import mlx_random as mr
+import oracle as O
+import vkv
+from gpu_util import attn_tol, dev, host, rand_bits, values
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [O.F16, O.BF16, O.F32])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_quantize_bit_exact(dtype, bits, group):
+    rng = np.random.default_rng(100 * bits + group + dtype)
+    w = rand_bits(rng, (3, 5, 7, 256), dtype, outliers=4)
+    # edge rows: zeros, constant, all negative, one huge value, tiny values
+    w[0, 0, 0] = O.from_f32(np.zeros(256, np.float32), dtype)
+    w[0, 0, 1] = O.from_f32(np.full(256, 3.25, np.float32), dtype)
+    w[0, 0, 2] = O.from_f32(-np.abs(rng.standard_normal(256)).astype(np.float32) - 0.1, dtype)
+    big = np.zeros(256, np.float32)
+    big[17] = 1000.0
+    w[0, 0, 3] = O.from_f32(big, dtype)
+    w[0, 0, 4] = O.from_f32((rng.standard_normal(256) * 1e-6).astype(np.float32), dtype)
+    wq, sc, bi = vkv.quantized(dev(w, dtype), group_size=group, bits=bits)
+    torch.cuda.synchronize()
+    rq, rs, rb, ties = O.quantize(w, dtype, group, bits)
+    assert np.array_equal(host(wq), rq)
+    assert np.array_equal(host(sc).view(rs.dtype), rs)
+    assert np.array_equal(host(bi).view(rb.dtype), rb)
+
+
+def test_quantize_strided_input_and_reference_aggregate(golden):
+    """A non-contiguous view quantizes like its contiguous copy; the seed-869
+    reference aggregate (IntegrationTests.swift:3890-3923) holds on the GPU."""
+    g = golden["quantize_uniform_8bit"]
+    w = mr.uniform(mr.KeySequence(g["seed"]), tuple(g["shape"]))
+    wq, sc, bi = vkv.quantized(dev(w, O.F32), group_size=64, bits=8)
+    wsum = int(host(wq).astype(np.uint64).sum()) % (1 << 32)
+    assert np.float32(wsum) == np.float32(g["wq_sum"])
+    assert abs(host(sc).astype(np.float64).sum() - g["scales_sum"]) < 1e-5 * abs(g["scales_sum"])
+    rng = np.random.default_rng(3)
+    base = dev(rand_bits(rng, (4, 6, 9, 128), O.BF16), O.BF16)
+    view = base.transpose(1, 2)  # [4, 9, 6, 128], last dim contiguous
+    a = vkv.quantized(view, 64, 4)
+    b = vkv.quantized(view.contiguous(), 64, 4)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("dtype", [O.F16, O.BF16, O.F32])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequantize_bit_exact(dtype, bits):
+    rng = np.random.default_rng(7 + bits + dtype)
+    w = rand_bits(rng, (16, 128), dtype, outliers=2)
+    rq, rs, rb, _ = O.quantize(w, dtype, 64, bits)
+    out = vkv.dequantized(torch.from_numpy(rq.view(np.int32)).cuda(), dev(rs, dtype),
+                          dev(rb, dtype), 64, bits)
+    ref = O.dequantize(rq, rs, rb, dtype, 64, bits)
+    assert np.array_equal(host(out).view(ref.dtype), ref)
+
+
+def test_sdpa_reference_known_answer(golden):
+    """MLXFastKernelTests.swift:101-111 on the GPU."""
+    g = golden["fast_sdpa_output"]
+    s = mr.KeySequence(g["seed"])
+    q, k, v = (mr.uniform(s, tuple(g[n])) for n in ("q_shape", "kv_shape", "kv_shape"))
+    out = vkv.scaled_dot_product_attention(dev(q, O.F32), dev(k, O.F32), dev(v, O.F32), g["scale"])
+    assert abs(float(out.double().sum()) - g["sum"]) <= g["accuracy"]
+
+
+@pytest.mark.parametrize("dtype", [O.F16, O.BF16, O.F32])
+@pytest.mark.parametrize("shape", [(1, 32, 8, 1, 513, 128), (2, 8, 2, 3, 77, 80),
+                                   (1, 4, 4, 1, 4100, 64), (3, 16, 8, 1, 1, 256)])
+def test_sdpa_matches_oracle(dtype, shape):
+    B, Hq, Hkv, L, T, D = shape
+    rng = np.random.default_rng(T + D + dtype)
+    q, k, v = (rand_bits(rng, s, dtype) for s in ((B, Hq, L, D), (B, Hkv, T, D), (B, Hkv, T, D)))
+    scale = D ** -0.5
+    out = vkv.scaled_dot_product_attention(dev(q, dtype), dev(k, dtype), dev(v, dtype), scale)
+    f = lambda a: O.to_f32(a, dtype) if dtype != O.F32 else a
+    ref = O.sdpa(f(q), f(k), f(v), scale)
+    got = values(out, dtype)
+    assert (np.abs(got - ref) <= attn_tol(dtype, ref)).all()
+
+
+@pytest.mark.parametrize("mask", ["causal", "bool", "add", "bool_empty_row"])
+def test_sdpa_masks(mask):
+    dtype = O.BF16
+    rng = np.random.default_rng(11)
+    B, Hq, Hkv, L, T, D = 2, 8, 4, 5, 37, 128
+    q, k, v = (rand_bits(rng, s, dtype) for s in ((B, Hq, L, D), (B, Hkv, T, D), (B, Hkv, T, D)))
+    if mask == "causal":
+        m_dev, m_ref = "causal", "causal"
+    elif mask.startswith("bool"):
+        m = rng.random((B, 1, L, T)) > 0.4
+        if mask == "bool_empty_row":
+            m[1, 0, 2] = False  # fully masked row -> zeros
+        m_dev, m_ref = torch.from_numpy(m).cuda(), m
+    else:
+        m = (rng.standard_normal((L, T)) * 3).astype(np.float32)
+        m[0, :5] = -np.inf
+        m_dev, m_ref = torch.from_numpy(m).cuda(), m
+    out = vkv.scaled_dot_product_attention(dev(q, dtype), dev(k, dtype), dev(v, dtype), 0.1,
+                                           mask=m_dev)
+    f = lambda a: O.to_f32(a, dtype)
+    ref = O.sdpa(f(q), f(k), f(v), 0.1, mask=m_ref)
+    got = values(out, dtype)
+    assert (np.abs(got - ref) <= attn_tol(dtype, ref)).all()
+    if mask == "bool_empty_row":
+        assert (got[1, :, 2] == 0).all()
+
+
+@pytest.mark.parametrize("dtype", [O.F16, O.BF16])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("mask", [None, "causal", "bool"])
+def test_quantized_sdpa_matches_oracle(dtype, bits, mask):
+    rng = np.random.default_rng(bits * 3 + dtype)
+    B, Hq, Hkv, L, T, D = 2, 32, 8, 1 if mask is None else 4, 300, 128
+    q = rand_bits(rng, (B, Hq, L, D), dtype)
+    kx, vx = (rand_bits(rng, (B, Hkv, T, D), dtype, outliers=4) for _ in range(2))
+    kq, ks, kb, _ = O.quantize(kx, dtype, 64, bits)
+    vq, vs, vb, _ = O.quantize(vx, dtype, 64, bits)
+    m_dev = m_ref = None
+    if mask == "causal":
+        m_dev = m_ref = "causal"
+    elif mask == "bool":
+        m = rng.random((B, Hq, L, T)) > 0.5
+        m[0, 3, 1] = False  # fully masked row -> mean of V (finfo.min fill)
+        m_dev, m_ref = torch.from_numpy(m).cuda(), m
+    t = lambda a: torch.from_numpy(a.view(np.int32)).cuda()
+    scale = D ** -0.5
+    out = vkv.quantized_scaled_dot_product_attention(
+        dev(q, dtype), (t(kq), dev(ks, dtype), dev(kb, dtype)), (t(vq), dev(vs, dtype), dev(vb, dtype)),
+        scale, mask=m_dev, group_size=64, bits=bits)
+    f = lambda a: O.to_f32(a, dtype)
+    ref = O.quantized_sdpa(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), scale, 64, bits,
+                           mask=m_ref)
+    got = values(out, dtype)
+    assert (np.abs(got - ref) <= attn_tol(dtype, ref)).all()

@@ -1,0 +1,166 @@
+"""GPU parity of the paged block pool: append through slot mappings into
+randomly permuted block tables with refcounted shared prefix blocks,
+gather (raw codes bit-exact with the oracle quantizer, dequant-on-read
+bit-exact with the oracle dequantizer, float blocks bit-exact), decode
+attention over mixed-length sequences (tolerance vs the oracle), and the
+prefix cache storing/fetching device blocks."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import vkv
+from gpu_util import attn_tol, dev, host, rand_bits, values
+
+pytestmark = pytest.mark.gpu
+
+
+class Paged:
+    """A small continuous-batching scene: sequences with random block
+    tables drawn from a pool, the first `n_share` sharing a prefix."""
+
+    def __init__(self, rng, bits, dtype=O.BF16, n_seqs=6, bs=32, Hkv=8, D=128, nblocks=96,
+                 share_tokens=64, n_share=3, max_len=300, lens=None):
+        self.rng, self.bits, self.dtype, self.bs, self.Hkv, self.D = rng, bits, dtype, bs, Hkv, D
+        self.pool = vkv.PagedPool(nblocks, bs, 1, Hkv, D, dtype=dtype, bits=bits)
+        self.mgr = vkv.PagedCacheManager(bs, nblocks, pool=self.pool)
+        if lens is None:
+            lens = [int(x) for x in rng.integers(share_tokens + 1, max_len, n_seqs)]
+            lens[-1] = 1  # a one-token sequence
+        self.lens = list(lens)
+        self.tokens = [rand_bits(rng, (L, Hkv, D), dtype, outliers=2) for L in self.lens]
+        self.vals = [rand_bits(rng, (L, Hkv, D), dtype, outliers=2) for L in self.lens]
+        n_sh_blocks = share_tokens // bs
+        shared = [self.mgr.allocate_block() for _ in range(n_sh_blocks)]
+        self.tables = []
+        for s, L in enumerate(self.lens):
+            nb = (L + bs - 1) // bs + 1  # room for a decode step
+            own = [self.mgr.allocate_block() for _ in range(nb)]
+            if s < n_share:
+                for b in shared:
+                    self.mgr.incref(b)
+                own[:n_sh_blocks] = shared
+                # sharing sequences see the same prefix tokens
+                self.tokens[s][:share_tokens] = self.tokens[0][:share_tokens]
+                self.vals[s][:share_tokens] = self.vals[0][:share_tokens]
+            self.tables.append(own)
+        self.share_tokens, self.n_share = share_tokens, n_share
+        self.width = max(len(t) for t in self.tables)
+
+    def slots(self, s, positions):
+        return [self.tables[s][p // self.bs] * self.bs + p % self.bs for p in positions]
+
+    def append_all(self):
+        keys, vals, slots = [], [], []
+        for s, L in enumerate(self.lens):
+            start = self.share_tokens if 0 < s < self.n_share else 0
+            keys.append(self.tokens[s][start:])
+            vals.append(self.vals[s][start:])
+            slots += self.slots(s, range(start, L))
+        k = np.concatenate(keys)
+        v = np.concatenate(vals)
+        sl = torch.tensor(slots, dtype=torch.int32, device="cuda")
+        self.pool.append(0, dev(k, self.dtype), dev(v, self.dtype), sl)
+
+    def view(self):
+        tab = np.full((len(self.lens), self.width), -1, np.int32)
+        for s, t in enumerate(self.tables):
+            tab[s, :len(t)] = t
+        self.tab_dev = torch.from_numpy(tab).cuda()
+        self.len_dev = torch.tensor(self.lens, dtype=torch.int32, device="cuda")
+        return self.pool.view(0, self.tab_dev, self.len_dev, max(self.lens))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("dtype", [O.BF16, O.F16])
+def test_paged_quantized_append_gather_attention(bits, dtype):
+    rng = np.random.default_rng(bits * 10 + dtype)
+    P = Paged(rng, bits, dtype)
+    P.append_all()
+    view = P.view()
+    (kq, ks, kb), (vq, vs, vb) = vkv.paged_gather_quantized(view)
+    kd, vd = vkv.paged_gather(view)
+    torch.cuda.synchronize()
+    Hq, scale = 32, P.D ** -0.5
+    q = rand_bits(rng, (len(P.lens), Hq, P.D), dtype)
+    out = values(vkv.paged_attention(dev(q, dtype), view, scale), dtype)
+    f = lambda a: O.to_f32(a, dtype)
+    for s, L in enumerate(P.lens):
+        for which, src, got in ((0, P.tokens[s], (kq, ks, kb)), (1, P.vals[s], (vq, vs, vb))):
+            x = np.ascontiguousarray(src.transpose(1, 0, 2))  # [H, L, D]
+            rq, rs, rb, _ = O.quantize(x, dtype, 64, bits)
+            assert np.array_equal(host(got[0][s, :, :L]), rq), (s, which)
+            assert np.array_equal(host(got[1][s, :, :L]).view(rs.dtype), rs)
+            assert np.array_equal(host(got[2][s, :, :L]).view(rb.dtype), rb)
+            deq = O.dequantize(rq, rs, rb, dtype, 64, bits)
+            assert np.array_equal(host((kd, vd)[which][s, :, :L]), deq)
+        rk = O.quantize(np.ascontiguousarray(P.tokens[s].transpose(1, 0, 2)), dtype, 64, bits)
+        rv = O.quantize(np.ascontiguousarray(P.vals[s].transpose(1, 0, 2)), dtype, 64, bits)
+        ref = O.quantized_sdpa(f(q[s])[None, :, None], dtype, rk[0][None], f(rk[1])[None],
+                               f(rk[2])[None], rv[0][None], f(rv[1])[None], f(rv[2])[None], scale,
+                               64, bits)[0, :, 0]
+        assert (np.abs(out[s] - ref) <= attn_tol(dtype, ref)).all(), s
+
+
+def test_paged_decode_step_crosses_block_boundary():
+    dtype, bits = O.BF16, 4
+    rng = np.random.default_rng(21)
+    P = Paged(rng, bits, dtype, n_share=0, lens=[63, 64, 65, 1])
+    P.append_all()
+    # one decode token per sequence at position len
+    k1 = rand_bits(rng, (4, 8, 128), dtype)
+    v1 = rand_bits(rng, (4, 8, 128), dtype)
+    slots = [P.slots(s, [L])[0] for s, L in enumerate(P.lens)]
+    P.pool.append(0, dev(k1, dtype), dev(v1, dtype), torch.tensor(slots, dtype=torch.int32, device="cuda"))
+    for s in range(4):
+        P.tokens[s] = np.concatenate([P.tokens[s], k1[s:s + 1]])
+        P.vals[s] = np.concatenate([P.vals[s], v1[s:s + 1]])
+        P.lens[s] += 1
+    view = P.view()
+    (kq, ks, kb), (vq, _, _) = vkv.paged_gather_quantized(view)
+    for s, L in enumerate(P.lens):
+        rq = O.quantize(np.ascontiguousarray(P.vals[s].transpose(1, 0, 2)), dtype, 64, bits)[0]
+        assert np.array_equal(host(vq[s, :, :L]), rq)
+
+
+@pytest.mark.parametrize("dtype", [O.BF16, O.F16, O.F32])
+def test_paged_float_pool(dtype):
+    rng = np.random.default_rng(31 + dtype)
+    P = Paged(rng, 0, dtype, n_seqs=5, bs=16)
+    P.append_all()
+    view = P.view()
+    kd, vd = vkv.paged_gather(view)
+    q = rand_bits(rng, (len(P.lens), 32, 128), dtype)
+    out = values(vkv.paged_attention(dev(q, dtype), view, 0.09), dtype)
+    f = (lambda a: O.to_f32(a, dtype)) if dtype != O.F32 else (lambda a: a)
+    for s, L in enumerate(P.lens):
+        k = np.ascontiguousarray(P.tokens[s].transpose(1, 0, 2))
+        v = np.ascontiguousarray(P.vals[s].transpose(1, 0, 2))
+        assert np.array_equal(host(kd[s, :, :L]), k) and np.array_equal(host(vd[s, :, :L]), v)
+        ref = O.sdpa(f(q[s])[None, :, None], f(k)[None], f(v)[None], 0.09)[0, :, 0]
+        assert (np.abs(out[s] - ref) <= attn_tol(dtype, ref)).all()
+
+
+def test_prefix_store_fetch_copies_device_blocks():
+    """storeTokenSequence copies each chunk's KV into fresh pool blocks;
+    fetchPrefix returns them and a gather through them restores the KV
+    (restoreLayerData, CacheHelpers.swift:431-552)."""
+    dtype, bits = O.BF16, 4
+    rng = np.random.default_rng(41)
+    P = Paged(rng, bits, dtype, n_seqs=2, n_share=0, max_len=150)
+    P.append_all()
+    L = P.lens[0]
+    toks = [int(x) for x in rng.integers(0, 1000, L)]
+    n_chunks = (L + P.bs - 1) // P.bs
+    P.mgr.store_token_sequence(toks, n_chunks, src_blocks=P.tables[0][:n_chunks])
+    r = P.mgr.fetch_prefix(toks + [5, 6])
+    assert r is not None
+    matched, remaining, blocks = r
+    assert matched == L and remaining == [5, 6] and len(blocks) == n_chunks
+    assert not set(blocks) & set(P.tables[0])  # copies, not the live blocks
+    tab = torch.tensor([blocks], dtype=torch.int32, device="cuda")
+    lens = torch.tensor([L], dtype=torch.int32, device="cuda")
+    (kq, _, _), (vq, _, _) = vkv.paged_gather_quantized(P.pool.view(0, tab, lens, L))
+    rq = O.quantize(np.ascontiguousarray(P.tokens[0].transpose(1, 0, 2)), dtype, 64, bits)[0]
+    assert np.array_equal(host(kq[0]), rq)
+    P.mgr.release(blocks)

@@ -1,0 +1,826 @@
+// vkv_capi.cpp -- the extern "C" boundary declared in include/vkv.h.
+// Every entry point converts C++ exceptions into a non-zero return and a
+// thread-local message, the mlx-c convention
+// (Libraries/CmlxDistributedShim/MlxCDistributed.cpp:11-28).
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "vkv_host.h"
+
+using namespace vkv;
+
+namespace {
+thread_local std::string g_error;
+
+template <class F>
+int guard(F&& f) {
+  try {
+    f();
+    g_error.clear();
+    return 0;
+  } catch (const std::exception& e) {
+    g_error = e.what();
+  } catch (...) {
+    g_error = "unknown error";
+  }
+  return 1;
+}
+
+void need(const void* p, const char* what) {
+  if (!p) throw Error(std::string(what) + " is NULL");
+}
+
+bool is_float(int dt) { return dt == VKV_F32 || dt == VKV_F16 || dt == VKV_BF16; }
+
+bool contiguous(const vkv_array& a) {
+  int64_t s = 1;
+  for (int i = a.ndim - 1; i >= 0; i--) {
+    if (a.shape[i] != 1 && a.strides[i] != s) return false;
+    s *= a.shape[i];
+  }
+  return true;
+}
+
+int64_t numel(const vkv_array& a) {
+  int64_t n = 1;
+  for (int i = 0; i < a.ndim; i++) n *= a.shape[i];
+  return n;
+}
+
+// Right-aligned broadcast of a mask to [B,H,L,T]: element strides, 0 on
+// broadcast dims.
+void mask_strides(const vkv_array& m, const int64_t* target, int64_t* out) {
+  if (m.ndim < 1 || m.ndim > 4) throw Error("mask must have 1 to 4 dims");
+  for (int i = 0; i < 4; i++) out[i] = 0;
+  for (int i = 0; i < m.ndim; i++) {
+    const int ti = 4 - m.ndim + i;
+    if (m.shape[i] == target[ti]) out[ti] = m.strides[i];
+    else if (m.shape[i] == 1) out[ti] = 0;
+    else throw Error("mask shape does not broadcast to [B, H, L, T]");
+  }
+}
+
+int32_t choose_parts(int64_t rows_x_heads, int64_t max_len, int32_t* part_tokens) {
+  const int64_t target_wgs = 2048;
+  int64_t parts = std::max<int64_t>(1, (target_wgs + rows_x_heads - 1) / std::max<int64_t>(1, rows_x_heads));
+  parts = std::min<int64_t>(parts, std::max<int64_t>(1, (max_len + 31) / 32));
+  int64_t pt = (max_len + parts - 1) / parts;
+  pt = std::max<int64_t>(32, (pt + 31) / 32 * 32);
+  *part_tokens = static_cast<int32_t>(pt);
+  return static_cast<int32_t>(std::max<int64_t>(1, (max_len + pt - 1) / pt));
+}
+
+void run_attention(int dtype, int bits, int group, bool vdm, bool qsem, AttnArgs& a, int64_t rows,
+                   int64_t max_len, hipStream_t st) {
+  a.n_parts = choose_parts(rows * a.Hkv, max_len, &a.part_tokens);
+  if (a.n_parts > 1) {
+    const size_t per = static_cast<size_t>(rows) * a.Hq * a.n_parts;
+    float* ws = attention_workspace(st, per * (a.Dv + 2));
+    a.ws_o = ws;
+    a.ws_ml = ws + per * a.Dv;
+  }
+  launch_attention(dtype, bits, group, vdm, qsem, a, rows, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* vkv_last_error(void) { return g_error.c_str(); }
+
+int vkv_abi_version(void) { return VKV_ABI_VERSION; }
+
+int vkv_device_count(int32_t* count) {
+  return guard([&] {
+    need(count, "count");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    *count = n;
+  });
+}
+
+// ------------------------------------------------------------ quantization
+
+int vkv_quantize_affine(const vkv_array* w, int32_t group_size, int32_t bits, vkv_array* wq,
+                        vkv_array* scales, vkv_array* biases, void* stream) {
+  return guard([&] {
+    need(w, "w");
+    need(wq, "wq");
+    need(scales, "scales");
+    need(biases, "biases");
+    if (!is_float(w->dtype)) throw Error("w must be f32, f16 or bf16");
+    if (w->ndim < 1 || w->ndim > 4) throw Error("w must have 1 to 4 dims");
+    if (w->strides[w->ndim - 1] != 1) throw Error("w last dim must be contiguous");
+    const int64_t D = w->shape[w->ndim - 1];
+    if (D % group_size) throw Error("last dim must be divisible by group_size");
+    const int64_t rows = D ? numel(*w) / D : 0;
+    if (wq->dtype != VKV_U32 || numel(*wq) * 32 != rows * D * bits || !contiguous(*wq))
+      throw Error("wq must be contiguous u32 with D*bits/32 words per row");
+    if (scales->dtype != w->dtype || biases->dtype != w->dtype ||
+        numel(*scales) != rows * (D / group_size) || numel(*biases) != numel(*scales) ||
+        !contiguous(*scales) || !contiguous(*biases))
+      throw Error("scales/biases must be contiguous [..., D/group_size] of w's dtype");
+    int64_t e[3] = {1, 1, 1}, s[3] = {0, 0, 0};
+    for (int i = 0; i < w->ndim - 1; i++) {
+      e[3 - (w->ndim - 1) + i] = w->shape[i];
+      s[3 - (w->ndim - 1) + i] = w->strides[i];
+    }
+    RowSrc src{w->data, e[0], e[1], e[2], s[0], s[1], s[2]};
+    RowDst dst{};
+    dst.wq = wq->data;
+    dst.scales = scales->data;
+    dst.biases = biases->data;
+    launch_quantize_rows(w->dtype, bits, group_size, 0, src, dst, rows, static_cast<int>(D), S(stream));
+  });
+}
+
+int vkv_dequantize_affine(const vkv_array* wq, const vkv_array* scales, const vkv_array* biases,
+                          int32_t group_size, int32_t bits, vkv_array* out, void* stream) {
+  return guard([&] {
+    need(wq, "wq");
+    need(scales, "scales");
+    need(biases, "biases");
+    need(out, "out");
+    if (!contiguous(*wq) || !contiguous(*scales) || !contiguous(*biases) || !contiguous(*out))
+      throw Error("dequantize operands must be contiguous");
+    if (bits != 4 && bits != 8) throw Error("bits must be 4 or 8");
+    const int64_t D = out->shape[out->ndim - 1];
+    const int64_t rows = D ? numel(*out) / D : 0;
+    if (numel(*wq) * 32 != rows * D * bits) throw Error("wq does not match out");
+    if (out->dtype != scales->dtype || biases->dtype != scales->dtype)
+      throw Error("out, scales and biases must share a dtype");
+    launch_dequantize(out->dtype, bits, group_size, static_cast<const uint32_t*>(wq->data),
+                      scales->data, biases->data, out->data, rows, static_cast<int>(D), S(stream));
+  });
+}
+
+// ---------------------------------------------------------------- attention
+
+int vkv_sdpa(const vkv_array* q, const vkv_array* k, const vkv_array* v, float scale,
+             int32_t mask_mode, const vkv_array* mask, vkv_array* out, void* stream) {
+  return guard([&] {
+    need(q, "q");
+    need(k, "k");
+    need(v, "v");
+    need(out, "out");
+    if (q->ndim != 4 || k->ndim != 4 || v->ndim != 4 || out->ndim != 4)
+      throw Error("q, k, v and out must be 4-D");
+    if (q->dtype != k->dtype || q->dtype != v->dtype || q->dtype != out->dtype || !is_float(q->dtype))
+      throw Error("q, k, v and out must share a float dtype");
+    if (q->strides[3] != 1 || k->strides[3] != 1 || v->strides[3] != 1 || out->strides[3] != 1)
+      throw Error("last dims must be contiguous");
+    const int64_t B = q->shape[0], Hq = q->shape[1], L = q->shape[2], D = q->shape[3];
+    const int64_t Hkv = k->shape[1], T = k->shape[2], Dv = v->shape[3];
+    if (k->shape[0] != B || v->shape[0] != B || v->shape[1] != Hkv || v->shape[2] != T ||
+        k->shape[3] != D || Hq % Hkv)
+      throw Error("q/k/v shapes are inconsistent");
+    if (out->shape[0] != B || out->shape[1] != Hq || out->shape[2] != L || out->shape[3] != Dv)
+      throw Error("out must be [B, Hq, L, Dv]");
+    const int es = elem_bytes(q->dtype);
+    AttnArgs a{};
+    a.q = q->data;
+    a.q_sb = q->strides[0];
+    a.q_sh = q->strides[1];
+    a.q_sl = q->strides[2];
+    a.L = static_cast<int32_t>(L);
+    a.Hq = static_cast<int32_t>(Hq);
+    a.Hkv = static_cast<int32_t>(Hkv);
+    a.D = static_cast<int32_t>(D);
+    a.Dv = static_cast<int32_t>(Dv);
+    a.scale = scale;
+    a.kv.kc = Comp{static_cast<const uint8_t*>(k->data), k->strides[0] * es, k->strides[1] * es,
+                   k->strides[2] * es};
+    a.kv.vc = Comp{static_cast<const uint8_t*>(v->data), v->strides[0] * es, v->strides[1] * es,
+                   v->strides[2] * es};
+    a.kv.T = static_cast<int32_t>(T);
+    a.out = out->data;
+    a.o_sb = out->strides[0];
+    a.o_sh = out->strides[1];
+    a.o_sl = out->strides[2];
+    if (mask_mode == VKV_MASK_CAUSAL) {
+      a.mask_mode = 1;
+    } else if (mask_mode == VKV_MASK_ARRAY) {
+      need(mask, "mask");
+      const int64_t target[4] = {B, Hq, L, T};
+      int64_t ms[4];
+      mask_strides(*mask, target, ms);
+      if (mask->dtype == VKV_BOOL || mask->dtype == VKV_U8) a.mask_mode = 2;
+      else if (mask->dtype == VKV_F32) a.mask_mode = 3;
+      else throw Error("mask must be bool or f32 (additive)");
+      a.mask = mask->data;
+      a.m_sb = ms[0];
+      a.m_sh = ms[1];
+      a.m_sl = ms[2];
+      a.m_st = ms[3];
+    } else if (mask_mode != VKV_MASK_NONE) {
+      throw Error("unknown mask mode");
+    }
+    run_attention(q->dtype, 0, 64, false, false, a, B * L, T, S(stream));
+  });
+}
+
+int vkv_quantized_sdpa(const vkv_array* q, const vkv_array* k_wq, const vkv_array* k_scales,
+                       const vkv_array* k_biases, const vkv_array* v_wq, const vkv_array* v_scales,
+                       const vkv_array* v_biases, int32_t group_size, int32_t bits, float scale,
+                       int32_t mask_mode, const vkv_array* mask, vkv_array* out, void* stream) {
+  return guard([&] {
+    const vkv_array* arrs[6] = {k_wq, k_scales, k_biases, v_wq, v_scales, v_biases};
+    need(q, "q");
+    need(out, "out");
+    for (auto* x : arrs) {
+      need(x, "quantized tuple array");
+      if (x->ndim != 4 || x->strides[3] != 1) throw Error("quantized tuples must be 4-D, last dim contiguous");
+    }
+    if (group_size != 64) throw Error("quantized attention supports group_size 64");
+    if (bits != 4 && bits != 8) throw Error("bits must be 4 or 8");
+    if (q->ndim != 4 || out->ndim != 4 || q->strides[3] != 1 || out->strides[3] != 1)
+      throw Error("q and out must be 4-D with a contiguous last dim");
+    const int64_t B = q->shape[0], Hq = q->shape[1], L = q->shape[2], D = q->shape[3];
+    const int64_t Hkv = k_wq->shape[1], T = k_wq->shape[2];
+    if (k_wq->shape[3] * 32 != D * bits || v_wq->shape[3] * 32 != D * bits || Hq % Hkv ||
+        k_wq->shape[0] != B || v_wq->shape[2] != T || k_scales->shape[3] != D / group_size)
+      throw Error("quantized tuples do not match q");
+    if (k_scales->dtype != q->dtype || v_scales->dtype != q->dtype || out->dtype != q->dtype)
+      throw Error("q, scales, biases and out must share a dtype");
+    const int es = elem_bytes(q->dtype);
+    AttnArgs a{};
+    a.q = q->data;
+    a.q_sb = q->strides[0];
+    a.q_sh = q->strides[1];
+    a.q_sl = q->strides[2];
+    a.L = static_cast<int32_t>(L);
+    a.Hq = static_cast<int32_t>(Hq);
+    a.Hkv = static_cast<int32_t>(Hkv);
+    a.D = static_cast<int32_t>(D);
+    a.Dv = static_cast<int32_t>(D);
+    a.scale = scale;
+    auto comp = [&](const vkv_array* x, int esz) {
+      return Comp{static_cast<const uint8_t*>(x->data), x->strides[0] * esz, x->strides[1] * esz,
+                  x->strides[2] * esz};
+    };
+    a.kv.kc = comp(k_wq, 4);
+    a.kv.ks = comp(k_scales, es);
+    a.kv.kb = comp(k_biases, es);
+    a.kv.vc = comp(v_wq, 4);
+    a.kv.vs = comp(v_scales, es);
+    a.kv.vb = comp(v_biases, es);
+    a.kv.T = static_cast<int32_t>(T);
+    a.out = out->data;
+    a.o_sb = out->strides[0];
+    a.o_sh = out->strides[1];
+    a.o_sl = out->strides[2];
+    if (mask_mode == VKV_MASK_CAUSAL) {
+      a.mask_mode = 1;
+    } else if (mask_mode == VKV_MASK_ARRAY) {
+      need(mask, "mask");
+      const int64_t target[4] = {B, Hq, L, T};
+      int64_t ms[4];
+      mask_strides(*mask, target, ms);
+      if (mask->dtype == VKV_BOOL || mask->dtype == VKV_U8) a.mask_mode = 2;
+      else if (mask->dtype == VKV_F32) a.mask_mode = 3;
+      else throw Error("mask must be bool or f32 (additive)");
+      a.mask = mask->data;
+      a.m_sb = ms[0];
+      a.m_sh = ms[1];
+      a.m_sl = ms[2];
+      a.m_st = ms[3];
+    } else if (mask_mode != VKV_MASK_NONE) {
+      throw Error("unknown mask mode");
+    }
+    run_attention(q->dtype, bits, group_size, false, true, a, B * L, T, S(stream));
+  });
+}
+
+int vkv_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_array* out,
+                   void* stream) {
+  return guard([&] {
+    need(q, "q");
+    need(kv, "kv");
+    need(out, "out");
+    if (q->ndim != 3 || out->ndim != 3 || q->strides[2] != 1 || out->strides[2] != 1)
+      throw Error("q and out must be [n_seqs, Hq, D] with a contiguous last dim");
+    if (q->dtype != kv->dtype || out->dtype != kv->dtype) throw Error("q/out dtype must match the view");
+    if (q->shape[0] != kv->n_seqs || q->shape[2] != kv->head_dim || out->shape[0] != kv->n_seqs ||
+        out->shape[1] != q->shape[1] || out->shape[2] != kv->v_head_dim)
+      throw Error("q/out shapes do not match the view");
+    if (q->shape[1] % kv->n_kv_heads) throw Error("query heads must be a multiple of kv heads");
+    if (!kv->block_table) throw Error("view has no block table");
+    AttnArgs a{};
+    a.q = q->data;
+    a.q_sb = q->strides[0];
+    a.q_sh = q->strides[1];
+    a.q_sl = 0;
+    a.L = 1;
+    a.Hq = static_cast<int32_t>(q->shape[1]);
+    a.Hkv = kv->n_kv_heads;
+    a.D = kv->head_dim;
+    a.Dv = kv->v_head_dim;
+    a.scale = scale;
+    a.kv = kvsrc_from_view(*kv);
+    a.out = out->data;
+    a.o_sb = out->strides[0];
+    a.o_sh = out->strides[1];
+    a.o_sl = 0;
+    const bool keys_only = (kv->flags & VKV_VIEW_KEYS_ONLY) != 0;
+    run_attention(kv->dtype, kv->bits, kv->group_size, kv->bits > 0 && !keys_only, kv->bits > 0, a,
+                  kv->n_seqs, kv->max_len, S(stream));
+  });
+}
+
+int vkv_mla_decode(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_array* out,
+                   void* stream) {
+  return guard([&] {
+    (void)q;
+    (void)kv;
+    (void)scale;
+    (void)out;
+    (void)stream;
+    throw Error("vkv_mla_decode: not built yet");
+  });
+}
+
+// ------------------------------------------------------------------ caches
+
+int vkv_cache_create(const vkv_cache_params* params, vkv_cache* out) {
+  return guard([&] {
+    need(params, "params");
+    need(out, "out");
+    auto h = new vkv_cache_s;
+    h->impl = make_cache(*params);
+    *out = h;
+  });
+}
+
+int vkv_cache_destroy(vkv_cache cache) {
+  return guard([&] { delete cache; });
+}
+
+int vkv_cache_copy(vkv_cache cache, void* stream, vkv_cache* out) {
+  return guard([&] {
+    need(cache, "cache");
+    need(out, "out");
+    auto h = new vkv_cache_s;
+    h->impl = cache->impl->copy(S(stream));
+    *out = h;
+  });
+}
+
+int vkv_cache_update(vkv_cache cache, const vkv_array* keys, const vkv_array* values, void* stream,
+                     vkv_array* out_keys, vkv_array* out_values) {
+  return guard([&] {
+    need(cache, "cache");
+    if (cache->impl->kind() == VKV_CACHE_QUANTIZED)
+      throw Error("`update` was called on `QuantizedKVCache`. Use `updateQuantized` instead.");
+    need(keys, "keys");
+    need(values, "values");
+    need(out_keys, "out_keys");
+    need(out_values, "out_values");
+    cache->impl->update(*keys, *values, S(stream), out_keys, out_values);
+  });
+}
+
+int vkv_cache_update_quantized(vkv_cache cache, const vkv_array* keys, const vkv_array* values,
+                               void* stream, vkv_paged_view* out) {
+  return guard([&] {
+    need(cache, "cache");
+    need(keys, "keys");
+    need(values, "values");
+    need(out, "out");
+    cache->impl->update_quantized(*keys, *values, S(stream), out);
+  });
+}
+
+int vkv_cache_offset(vkv_cache cache, int64_t* offset) {
+  return guard([&] {
+    need(cache, "cache");
+    need(offset, "offset");
+    *offset = cache->impl->offset;
+  });
+}
+
+int vkv_cache_max_size(vkv_cache cache, int64_t* max_size) {
+  return guard([&] {
+    need(cache, "cache");
+    need(max_size, "max_size");
+    *max_size = cache->impl->max_size();
+  });
+}
+
+int vkv_cache_is_trimmable(vkv_cache cache, int32_t* trimmable) {
+  return guard([&] {
+    need(cache, "cache");
+    need(trimmable, "trimmable");
+    *trimmable = cache->impl->trimmable() ? 1 : 0;
+  });
+}
+
+int vkv_cache_trim(vkv_cache cache, int64_t n, int64_t* trimmed) {
+  return guard([&] {
+    need(cache, "cache");
+    int64_t t = cache->impl->trim(n);
+    if (trimmed) *trimmed = t;
+  });
+}
+
+int vkv_cache_capacity(vkv_cache cache, int64_t* capacity) {
+  return guard([&] {
+    need(cache, "cache");
+    need(capacity, "capacity");
+    *capacity = cache->impl->capacity();
+  });
+}
+
+int vkv_cache_state(vkv_cache cache, void* stream, vkv_array* arrays, int32_t* count) {
+  return guard([&] {
+    need(cache, "cache");
+    need(arrays, "arrays");
+    need(count, "count");
+    *count = cache->impl->state(S(stream), arrays);
+  });
+}
+
+int vkv_cache_set_state(vkv_cache cache, const vkv_array* arrays, int32_t count, void* stream) {
+  return guard([&] {
+    need(cache, "cache");
+    if (count > 0) need(arrays, "arrays");
+    cache->impl->set_state(arrays, count, S(stream));
+  });
+}
+
+int vkv_cache_meta_state(vkv_cache cache, char* buf, int64_t buf_len, int32_t* count) {
+  return guard([&] {
+    need(cache, "cache");
+    need(buf, "buf");
+    need(count, "count");
+    auto v = cache->impl->meta_state();
+    int64_t need_len = 0;
+    for (auto& s : v) need_len += static_cast<int64_t>(s.size()) + 1;
+    if (need_len > buf_len) throw Error("metaState buffer too small");
+    char* p = buf;
+    for (auto& s : v) {
+      memcpy(p, s.c_str(), s.size() + 1);
+      p += s.size() + 1;
+    }
+    *count = static_cast<int32_t>(v.size());
+  });
+}
+
+int vkv_cache_set_meta_state(vkv_cache cache, const char* const* strings, int32_t count) {
+  return guard([&] {
+    need(cache, "cache");
+    std::vector<std::string> v;
+    for (int i = 0; i < count; i++) {
+      need(strings[i], "metaState string");
+      v.emplace_back(strings[i]);
+    }
+    cache->impl->set_meta_state(v);
+  });
+}
+
+int vkv_cache_make_mask(vkv_cache cache, int32_t n, int32_t window, int32_t return_array, void* stream,
+                        int32_t* mode, vkv_array* mask) {
+  return guard([&] {
+    need(cache, "cache");
+    need(mode, "mode");
+    vkv_array m{};
+    *mode = cache->impl->make_mask(n, window, return_array != 0, S(stream), &m);
+    if (mask) *mask = m;
+  });
+}
+
+int vkv_cache_to_quantized(vkv_cache simple, int32_t group_size, int32_t bits, void* stream,
+                           vkv_cache* out) {
+  return guard([&] {
+    need(simple, "cache");
+    need(out, "out");
+    auto* s = dynamic_cast<SimpleCache*>(simple->impl.get());
+    if (!s) throw Error("toQuantized needs a KVCacheSimple");
+    auto h = new vkv_cache_s;
+    try {
+      h->impl = s->to_quantized(group_size > 0 ? group_size : 64, bits > 0 ? bits : 4, S(stream));
+    } catch (...) {
+      delete h;
+      throw;
+    }
+    *out = h;
+  });
+}
+
+int vkv_cache_to_unquantized(vkv_cache quantized, void* stream, vkv_cache* out) {
+  return guard([&] {
+    need(quantized, "cache");
+    need(out, "out");
+    auto* q = dynamic_cast<QuantizedCache*>(quantized->impl.get());
+    if (!q) throw Error("toUnquantized needs a QuantizedKVCache");
+    auto h = new vkv_cache_s;
+    try {
+      h->impl = q->to_unquantized(S(stream));
+    } catch (...) {
+      delete h;
+      throw;
+    }
+    *out = h;
+  });
+}
+
+int vkv_cache_read_kv(vkv_cache cache, void* stream, vkv_array* keys, vkv_array* values) {
+  return guard([&] {
+    need(cache, "cache");
+    need(keys, "keys");
+    need(values, "values");
+    cache->impl->read_kv(S(stream), keys, values);
+  });
+}
+
+// -------------------------------------------------------------------- pool
+
+int vkv_pool_create(const vkv_pool_params* params, vkv_pool* out) {
+  return guard([&] {
+    need(params, "params");
+    need(out, "out");
+    auto h = new vkv_pool_s;
+    try {
+      h->impl = std::make_unique<Pool>(*params);
+    } catch (...) {
+      delete h;
+      throw;
+    }
+    *out = h;
+  });
+}
+
+int vkv_pool_destroy(vkv_pool pool) {
+  return guard([&] { delete pool; });
+}
+
+int vkv_pool_bytes(vkv_pool pool, int64_t* bytes) {
+  return guard([&] {
+    need(pool, "pool");
+    need(bytes, "bytes");
+    *bytes = static_cast<int64_t>(pool->impl->mem.size());
+  });
+}
+
+int vkv_pool_view(vkv_pool pool, int32_t layer, const int32_t* block_table, int32_t table_stride,
+                  const int32_t* seq_lens, int32_t n_seqs, int32_t max_len, vkv_paged_view* out) {
+  return guard([&] {
+    need(pool, "pool");
+    need(out, "out");
+    *out = pool->impl->view(layer, block_table, table_stride, seq_lens, n_seqs, max_len);
+  });
+}
+
+int vkv_paged_append(vkv_pool pool, int32_t layer, const vkv_array* keys, const vkv_array* values,
+                     const int32_t* slot_mapping, int64_t n_tokens, void* stream) {
+  return guard([&] {
+    need(pool, "pool");
+    need(keys, "keys");
+    pool->impl->append(layer, *keys, values, slot_mapping, n_tokens, S(stream));
+  });
+}
+
+int vkv_paged_gather(const vkv_paged_view* kv, vkv_array* keys, vkv_array* values, void* stream) {
+  return guard([&] {
+    need(kv, "kv");
+    vkv_array* outs[2] = {keys, values};
+    KVSrc src = kvsrc_from_view(*kv);
+    for (int which = 0; which < 2; which++) {
+      vkv_array* o = outs[which];
+      if (!o) continue;
+      const int D = which ? kv->v_head_dim : kv->head_dim;
+      if (o->ndim != 4 || !contiguous(*o) || o->dtype != kv->dtype || o->shape[0] != kv->n_seqs ||
+          o->shape[1] != kv->n_kv_heads || o->shape[2] != kv->max_len || o->shape[3] != D)
+        throw Error("gather output must be contiguous [n_seqs, Hkv, max_len, D] in the view dtype");
+      GatherArgs g{};
+      g.kv = src;
+      g.n_seqs = kv->n_seqs;
+      g.H = kv->n_kv_heads;
+      g.T = kv->max_len;
+      g.D = D;
+      g.which = which;
+      g.bits = kv->bits;
+      g.group = kv->group_size;
+      g.dtype = kv->dtype;
+      g.out = o->data;
+      launch_gather(g, 0, S(stream));
+    }
+  });
+}
+
+int vkv_paged_gather_quantized(const vkv_paged_view* kv, vkv_array* out, void* stream) {
+  return guard([&] {
+    need(kv, "kv");
+    need(out, "out");
+    if (kv->bits == 0) throw Error("code gather needs an affine view");
+    const bool keys_only = (kv->flags & VKV_VIEW_KEYS_ONLY) != 0;
+    KVSrc src = kvsrc_from_view(*kv);
+    const int D = kv->head_dim;
+    const int64_t W = static_cast<int64_t>(D) * kv->bits / 32, G = D / kv->group_size;
+    for (int which = 0; which < (keys_only ? 1 : 2); which++) {
+      vkv_array* o = out + 3 * which;
+      for (int i = 0; i < 3; i++) {
+        const int64_t last = i == 0 ? W : G;
+        if (o[i].ndim != 4 || !contiguous(o[i]) || o[i].shape[0] != kv->n_seqs ||
+            o[i].shape[1] != kv->n_kv_heads || o[i].shape[2] != kv->max_len || o[i].shape[3] != last)
+          throw Error("code gather outputs must be contiguous reference-layout arrays");
+      }
+      GatherArgs g{};
+      g.kv = src;
+      g.n_seqs = kv->n_seqs;
+      g.H = kv->n_kv_heads;
+      g.T = kv->max_len;
+      g.D = D;
+      g.which = which;
+      g.bits = kv->bits;
+      g.group = kv->group_size;
+      g.dtype = kv->dtype;
+      g.out = o[0].data;
+      g.out_s = o[1].data;
+      g.out_b = o[2].data;
+      if (keys_only) g.kv.v_dim_stride = 0;
+      launch_gather(g, 1, S(stream));
+    }
+  });
+}
+
+int vkv_pool_copy_blocks(vkv_pool pool, const int32_t* src, const int32_t* dst, int32_t n, void* stream) {
+  return guard([&] {
+    need(pool, "pool");
+    if (n <= 0) return;
+    need(src, "src");
+    need(dst, "dst");
+    Pool& p = *pool->impl;
+    for (int i = 0; i < n; i++)
+      if (src[i] < 0 || src[i] >= p.p.num_blocks || dst[i] < 0 || dst[i] >= p.p.num_blocks)
+        throw Error("block id out of range");
+    launch_copy_blocks(p.mem.bytes(), p.layer_bytes, p.p.n_layers, p.block_bytes, src, dst, n, S(stream));
+  });
+}
+
+// ------------------------------------------------------------ prefix cache
+
+int vkv_prefix_create(int32_t block_size, int32_t max_blocks, const char* model_key, vkv_pool pool,
+                      vkv_prefix* out) {
+  return guard([&] {
+    need(out, "out");
+    auto h = new vkv_prefix_s;
+    try {
+      h->impl = std::make_unique<PrefixManager>(block_size, max_blocks, model_key,
+                                                pool ? pool->impl.get() : nullptr);
+    } catch (...) {
+      delete h;
+      throw;
+    }
+    *out = h;
+  });
+}
+
+int vkv_prefix_destroy(vkv_prefix mgr) {
+  return guard([&] { delete mgr; });
+}
+
+int vkv_prefix_allocate(vkv_prefix mgr, int32_t* block) {
+  return guard([&] {
+    need(mgr, "mgr");
+    need(block, "block");
+    *block = mgr->impl->allocate();
+  });
+}
+
+int vkv_prefix_free(vkv_prefix mgr, int32_t block) {
+  return guard([&] {
+    need(mgr, "mgr");
+    mgr->impl->free_block(block);
+  });
+}
+
+int vkv_prefix_release(vkv_prefix mgr, const int32_t* blocks, int32_t n) {
+  return guard([&] {
+    need(mgr, "mgr");
+    if (n > 0) need(blocks, "blocks");
+    for (int32_t i = n - 1; i >= 0; i--) mgr->impl->free_block(blocks[i]);
+  });
+}
+
+int vkv_prefix_incref(vkv_prefix mgr, int32_t block) {
+  return guard([&] {
+    need(mgr, "mgr");
+    mgr->impl->incref(block);
+  });
+}
+
+int vkv_prefix_ref_count(vkv_prefix mgr, int32_t block, int32_t* ref_count) {
+  return guard([&] {
+    need(mgr, "mgr");
+    need(ref_count, "ref_count");
+    *ref_count = mgr->impl->ref_count(block);
+  });
+}
+
+int vkv_prefix_find(vkv_prefix mgr, const char* hash, int32_t* block) {
+  return guard([&] {
+    need(mgr, "mgr");
+    need(hash, "hash");
+    need(block, "block");
+    *block = mgr->impl->find(hash);
+  });
+}
+
+int vkv_prefix_register(vkv_prefix mgr, int32_t block, const char* hash) {
+  return guard([&] {
+    need(mgr, "mgr");
+    need(hash, "hash");
+    mgr->impl->register_block(block, hash);
+  });
+}
+
+int vkv_prefix_clear(vkv_prefix mgr) {
+  return guard([&] {
+    need(mgr, "mgr");
+    mgr->impl->clear();
+  });
+}
+
+int vkv_prefix_store(vkv_prefix mgr, const int64_t* tokens, int64_t n_tokens, const char* media_salt,
+                     int32_t n_data_chunks, const int32_t* src_blocks, void* stream) {
+  return guard([&] {
+    need(mgr, "mgr");
+    if (n_tokens > 0) need(tokens, "tokens");
+    mgr->impl->store(tokens, n_tokens, media_salt, n_data_chunks, src_blocks, S(stream));
+  });
+}
+
+int vkv_prefix_fetch(vkv_prefix mgr, const int64_t* tokens, int64_t n_tokens, const char* media_salt,
+                     int32_t* blocks, int32_t capacity, int32_t* n_blocks, int64_t* matched_tokens) {
+  return guard([&] {
+    need(mgr, "mgr");
+    need(n_blocks, "n_blocks");
+    need(matched_tokens, "matched_tokens");
+    if (capacity > 0) need(blocks, "blocks");
+    if (n_tokens > 0) need(tokens, "tokens");
+    mgr->impl->fetch(tokens, n_tokens, media_salt, blocks, capacity, n_blocks, matched_tokens);
+  });
+}
+
+int vkv_prefix_stats_get(vkv_prefix mgr, vkv_prefix_stats* out) {
+  return guard([&] {
+    need(mgr, "mgr");
+    need(out, "out");
+    *out = mgr->impl->stats();
+  });
+}
+
+int vkv_prefix_block_tokens(vkv_prefix mgr, int32_t block, int32_t* n_tokens) {
+  return guard([&] {
+    need(mgr, "mgr");
+    need(n_tokens, "n_tokens");
+    *n_tokens = mgr->impl->block_tokens(block);
+  });
+}
+
+int vkv_block_hash(const char* parent_hash, const int64_t* tokens, int64_t n_tokens,
+                   const char* model_key, const char* media_salt, char* out) {
+  return guard([&] {
+    need(out, "out");
+    if (n_tokens > 0) need(tokens, "tokens");
+    std::string p = parent_hash ? parent_hash : "", k = model_key ? model_key : "",
+                s = media_salt ? media_salt : "";
+    std::string h = PrefixManager::block_hash(parent_hash ? &p : nullptr, tokens, n_tokens,
+                                              model_key ? &k : nullptr, media_salt ? &s : nullptr);
+    memcpy(out, h.c_str(), 65);
+  });
+}
+
+int vkv_array_copy(const vkv_array* src, vkv_array* dst, void* stream) {
+  return guard([&] {
+    need(src, "src");
+    need(dst, "dst");
+    if (src->ndim != dst->ndim || src->ndim < 1 || src->ndim > 4) throw Error("copy needs equal ranks 1..4");
+    for (int i = 0; i < src->ndim; i++)
+      if (src->shape[i] != dst->shape[i]) throw Error("copy needs equal shapes");
+    auto esz = [](int dt) { return dt == VKV_F32 || dt == VKV_U32 || dt == VKV_I32 ? 4 : dt == VKV_U8 || dt == VKV_BOOL ? 1 : 2; };
+    if (esz(src->dtype) != esz(dst->dtype)) throw Error("copy needs equal element sizes");
+    int64_t n[4] = {1, 1, 1, 1}, ss[4] = {0, 0, 0, 0}, ds[4] = {0, 0, 0, 0};
+    for (int i = 0; i < src->ndim; i++) {
+      n[4 - src->ndim + i] = src->shape[i];
+      ss[4 - src->ndim + i] = src->strides[i];
+      ds[4 - src->ndim + i] = dst->strides[i];
+    }
+    launch_copy4d(esz(src->dtype), src->data, n, ss, dst->data, ds, S(stream));
+  });
+}
+
+// --------------------------------------------------------------- synthetic
+
+int vkv_fill_normal(void* data, int32_t dtype, int64_t n, uint64_t seed, float std, void* stream) {
+  return guard([&] {
+    if (n > 0) need(data, "data");
+    if (!is_float(dtype)) throw Error("dtype must be f32, f16 or bf16");
+    launch_fill_normal(dtype, data, n, seed, std, S(stream));
+  });
+}
+
+}  // extern "C"

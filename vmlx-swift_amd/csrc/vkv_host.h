@@ -1,0 +1,274 @@
+// vkv_host.h -- host-side objects behind the C ABI: device buffers, the
+// per-layer caches (KVCacheSimple / RotatingKVCache / QuantizedKVCache
+// state machines), the paged block pool and the prefix-cache manager.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <list>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/vkv.h"
+#include "vkv_internal.h"
+
+namespace vkv {
+
+// Owned device allocation.  hipFree synchronizes the device, so a buffer can
+// be dropped while work that reads it is still queued.
+class DevBuf {
+ public:
+  DevBuf() = default;
+  explicit DevBuf(size_t bytes) { alloc(bytes); }
+  ~DevBuf() { release(); }
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  DevBuf(DevBuf&& o) noexcept : p_(o.p_), n_(o.n_) { o.p_ = nullptr; o.n_ = 0; }
+  DevBuf& operator=(DevBuf&& o) noexcept {
+    if (this != &o) {
+      release();
+      p_ = o.p_;
+      n_ = o.n_;
+      o.p_ = nullptr;
+      o.n_ = 0;
+    }
+    return *this;
+  }
+  void alloc(size_t bytes) {
+    release();
+    if (bytes) VKV_HIP(hipMalloc(&p_, bytes));
+    n_ = bytes;
+  }
+  void release() {
+    if (p_) (void)hipFree(p_);
+    p_ = nullptr;
+    n_ = 0;
+  }
+  void* get() const { return p_; }
+  uint8_t* bytes() const { return static_cast<uint8_t*>(p_); }
+  size_t size() const { return n_; }
+
+ private:
+  void* p_ = nullptr;
+  size_t n_ = 0;
+};
+
+inline hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+
+// A dense [B,H,cap,D] float buffer with the reference's 4-D array semantics.
+struct Dense4 {
+  std::shared_ptr<DevBuf> buf;
+  int dtype = 2;
+  int64_t B = 0, H = 0, cap = 0, D = 0;
+  bool empty() const { return !buf; }
+  int64_t bytes_per_el() const { return elem_bytes(dtype); }
+  vkv_array view(int64_t len) const;  // [B,H,len,D] over [.., cap, ..]
+};
+
+// Base of the per-layer caches (protocol KVCache, KVCache.swift:38-77).
+class Cache {
+ public:
+  virtual ~Cache() = default;
+  int64_t offset = 0;
+  virtual int kind() const = 0;
+  virtual int64_t max_size() const { return -1; }
+  virtual bool trimmable() const { return false; }
+  virtual int64_t trim(int64_t) { return 0; }
+  virtual int64_t capacity() const = 0;
+  virtual void update(const vkv_array&, const vkv_array&, hipStream_t, vkv_array*, vkv_array*) {
+    throw Error("update(keys:values:) is not available on this cache");
+  }
+  virtual void update_quantized(const vkv_array&, const vkv_array&, hipStream_t, vkv_paged_view*) {
+    throw Error("updateQuantized is only available on QuantizedKVCache");
+  }
+  virtual int state(hipStream_t, vkv_array* out) = 0;
+  virtual void set_state(const vkv_array* arrays, int count, hipStream_t) = 0;
+  virtual std::vector<std::string> meta_state() const { return {""}; }
+  virtual void set_meta_state(const std::vector<std::string>& v);
+  virtual std::unique_ptr<Cache> copy(hipStream_t) = 0;
+  virtual void read_kv(hipStream_t, vkv_array* k, vkv_array* v) = 0;
+  // BaseKVCache.makeMask (KVCache.swift:287-311)
+  virtual int make_mask(int n, int window, bool return_array, hipStream_t st, vkv_array* mask);
+
+ protected:
+  DevBuf mask_buf_;
+  int causal_array_mask(int n, int64_t off, int window, hipStream_t st, vkv_array* mask);
+};
+
+std::unique_ptr<Cache> make_cache(const vkv_cache_params& p);
+
+class SimpleCache : public Cache {
+ public:
+  explicit SimpleCache(int step) : step_(step) {}
+  int kind() const override { return VKV_CACHE_SIMPLE; }
+  bool trimmable() const override { return true; }
+  int64_t trim(int64_t n) override;
+  int64_t capacity() const override { return k_.cap; }
+  void update(const vkv_array& k, const vkv_array& v, hipStream_t st, vkv_array* ok,
+              vkv_array* ov) override;
+  int state(hipStream_t, vkv_array* out) override;
+  void set_state(const vkv_array* a, int count, hipStream_t st) override;
+  std::unique_ptr<Cache> copy(hipStream_t st) override;
+  void read_kv(hipStream_t, vkv_array* k, vkv_array* v) override;
+  std::unique_ptr<Cache> to_quantized(int group, int bits, hipStream_t st);
+  int step_;
+  Dense4 k_, v_;
+};
+
+class RotatingCache : public Cache {
+ public:
+  RotatingCache(int max_size, int keep, int step) : keep_(keep), max_(max_size), step_(step) {}
+  int kind() const override { return VKV_CACHE_ROTATING; }
+  int64_t max_size() const override { return max_; }
+  bool trimmable() const override { return offset < max_; }
+  int64_t trim(int64_t n) override;
+  int64_t capacity() const override { return k_.cap; }
+  void update(const vkv_array& k, const vkv_array& v, hipStream_t st, vkv_array* ok,
+              vkv_array* ov) override;
+  int state(hipStream_t, vkv_array* out) override;
+  void set_state(const vkv_array* a, int count, hipStream_t st) override;
+  std::vector<std::string> meta_state() const override;
+  void set_meta_state(const std::vector<std::string>& v) override;
+  std::unique_ptr<Cache> copy(hipStream_t st) override;
+  void read_kv(hipStream_t st, vkv_array* k, vkv_array* v) override;
+  int make_mask(int n, int window, bool return_array, hipStream_t st, vkv_array* mask) override;
+  int64_t keep_, max_, step_;
+  int64_t idx_ = 0;
+  Dense4 k_, v_;
+  Dense4 ordered_k_, ordered_v_;  // temporallyOrderedKV result
+
+ private:
+  void update_concat(const vkv_array& k, const vkv_array& v, hipStream_t st);
+  bool update_in_place(const vkv_array& k, const vkv_array& v, hipStream_t st);
+  bool can_update_in_place(int64_t S) const;
+  Dense4 temporal_order(const Dense4& a, hipStream_t st) const;
+  Dense4 trim_cat(int64_t trim_size, const Dense4& a, const vkv_array* append, hipStream_t st) const;
+  void outputs(vkv_array* ok, vkv_array* ov) const;
+};
+
+// QuantizedKVCache on paged storage: 32-token blocks, block id j*B + b for
+// batch row b's j-th block, so growth never moves a block.
+class QuantizedCache : public Cache {
+ public:
+  static constexpr int kBlock = 32;
+  QuantizedCache(int group, int bits, int step) : group_(group), bits_(bits), step_(step) {}
+  int kind() const override { return VKV_CACHE_QUANTIZED; }
+  bool trimmable() const override { return true; }
+  int64_t trim(int64_t n) override;
+  int64_t capacity() const override { return cap_; }
+  void update_quantized(const vkv_array& k, const vkv_array& v, hipStream_t st,
+                        vkv_paged_view* out) override;
+  int state(hipStream_t st, vkv_array* out) override;
+  void set_state(const vkv_array* a, int count, hipStream_t st) override;
+  std::vector<std::string> meta_state() const override;
+  void set_meta_state(const std::vector<std::string>& v) override;
+  std::unique_ptr<Cache> copy(hipStream_t st) override;
+  void read_kv(hipStream_t st, vkv_array* k, vkv_array* v) override;
+  std::unique_ptr<Cache> to_unquantized(hipStream_t st);
+  vkv_paged_view view() const;
+  // make room for `cap` tokens per row (reference growth arithmetic is done
+  // by the caller); keeps existing blocks in place.
+  void reserve(int64_t B, int64_t H, int64_t D, int64_t cap, int dtype, hipStream_t st);
+  int group_, bits_, step_;
+  int dtype_ = 2;
+  int64_t B_ = 0, H_ = 0, D_ = 0, cap_ = 0;
+  int64_t nblk_ = 0;  // blocks per row
+  int64_t head_bytes_ = 0, block_bytes_ = 0;
+  int64_t codes_bytes_ = 0, sb_bytes_ = 0;
+  DevBuf store_;
+  DevBuf table_;  // int32 [B][nblk_]
+  DevBuf state_buf_[6];
+  DevBuf kv_buf_[2];
+};
+
+class Pool {
+ public:
+  explicit Pool(const vkv_pool_params& p);
+  vkv_pool_params p;
+  int64_t codes_bytes = 0, sb_bytes = 0, head_bytes = 0, block_bytes = 0, layer_bytes = 0;
+  int32_t kc_off = 0, vc_off = 0, ks_off = 0, kb_off = 0, vs_off = 0, vb_off = 0;
+  DevBuf mem;
+  vkv_paged_view view(int layer, const int32_t* table, int32_t stride, const int32_t* lens,
+                      int32_t n, int32_t max_len) const;
+  void append(int layer, const vkv_array& k, const vkv_array* v, const int32_t* slots, int64_t n,
+              hipStream_t st);
+};
+
+// Chunk layout shared by the pool and the quantized cache.
+struct ChunkLayout {
+  int64_t codes, sb, head;
+  int32_t kc, vc, ks, kb, vs, vb;
+};
+ChunkLayout chunk_layout(int bits, int dtype, int block_size, int D, int Dv, int group,
+                         bool keys_only);
+
+KVSrc kvsrc_from_view(const vkv_paged_view& v);
+
+// PagedCacheManager (Cache/PagedCacheManager.swift) on host, optionally
+// bound to a device pool.
+class PrefixManager {
+ public:
+  PrefixManager(int block_size, int max_blocks, const char* model_key, Pool* pool);
+  int32_t allocate();
+  void free_block(int32_t b);
+  void incref(int32_t b);
+  int32_t ref_count(int32_t b);
+  int32_t find(const std::string& hash);
+  void register_block(int32_t b, const std::string& hash);
+  void clear();
+  void store(const int64_t* tokens, int64_t n, const char* salt, int n_data,
+             const int32_t* src_blocks, hipStream_t st);
+  void fetch(const int64_t* tokens, int64_t n, const char* salt, int32_t* blocks, int cap,
+             int32_t* n_blocks, int64_t* matched);
+  vkv_prefix_stats stats();
+  int32_t block_tokens(int32_t b);
+  static std::string block_hash(const std::string* parent, const int64_t* tokens, int64_t n,
+                                const std::string* model_key, const std::string* salt);
+
+ private:
+  struct Block {
+    bool has_hash = false;
+    std::string hash;
+    std::vector<int64_t> tokens;
+    bool has_data = false;
+    int32_t ref = 0;
+    // free-queue links
+    int32_t prev = -1, next = -1;
+    bool queued = false;
+  };
+  void q_append(int32_t b);
+  int32_t q_pop_first();
+  bool q_remove(int32_t b);
+  void reset(int32_t b);
+  int32_t alloc_locked();
+  void free_locked(int32_t b);
+  int32_t partial_prefix(const std::string* parent, const std::vector<int64_t>& chunk,
+                         const std::string* salt);
+  std::mutex mu_;
+  int block_size_, max_blocks_;
+  bool has_key_;
+  std::string key_;
+  Pool* pool_;
+  std::vector<Block> blocks_;
+  int32_t head_ = -1, tail_ = -1;
+  std::unordered_map<std::string, int32_t> map_;
+  vkv_prefix_stats stats_{};
+};
+
+// Split-K workspace for the attention kernels (one per stream).
+float* attention_workspace(hipStream_t st, size_t floats);
+
+}  // namespace vkv
+
+struct vkv_cache_s {
+  std::unique_ptr<vkv::Cache> impl;
+};
+struct vkv_pool_s {
+  std::unique_ptr<vkv::Pool> impl;
+};
+struct vkv_prefix_s {
+  std::unique_ptr<vkv::PrefixManager> impl;
+};

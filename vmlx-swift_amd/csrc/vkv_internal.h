@@ -1,0 +1,140 @@
+// vkv_internal.h -- kernel argument blocks and launchers shared by the host
+// code (vkv_capi.cpp) and the HIP kernels (vkv_kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <stdexcept>
+#include <string>
+
+namespace vkv {
+
+struct Error : std::runtime_error {
+  explicit Error(const std::string& m) : std::runtime_error(m) {}
+};
+
+#define VKV_CHECK(cond, msg)                                      \
+  do {                                                            \
+    if (!(cond)) throw ::vkv::Error(std::string(msg));            \
+  } while (0)
+
+#define VKV_HIP(call)                                                              \
+  do {                                                                             \
+    hipError_t e_ = (call);                                                        \
+    if (e_ != hipSuccess)                                                          \
+      throw ::vkv::Error(std::string(#call) + ": " + hipGetErrorString(e_));       \
+  } while (0)
+
+inline int elem_bytes(int dtype) { return dtype == 0 ? 4 : 2; }
+
+// Rows of a strided tensor whose last dim (D) is contiguous.  Row r is
+// (i0, i1, i2) with r = (i0 * e1 + i1) * e2 + i2; strides in elements.
+struct RowSrc {
+  const void* ptr;
+  int64_t e0, e1, e2;
+  int64_t s0, s1, s2;
+};
+
+// Where quantized / float rows land.
+struct RowDst {
+  // reference layout (mode 0): contiguous wq [rows][D*bits/32], scales and
+  // biases [rows][D/group]; float copy (mode 0, bits 0): out [rows][D].
+  void* wq;
+  void* scales;
+  void* biases;
+  // paged (mode 1): chunk = base + block * block_bytes + head * head_bytes.
+  uint8_t* base;
+  int64_t block_bytes, head_bytes;
+  int32_t block_size;
+  int32_t is_v;              // V rows: dim-major codes
+  int32_t c_off, s_off, b_off;  // codes / scales / biases offsets in a chunk
+  // slot of token n (n = row / e2 for paged rows ordered (token, head)):
+  const int32_t* slots;      // explicit [N] (slot = block*bs + offset), or
+  const int32_t* table;      // block table [e0][table_stride] with
+  int32_t table_stride;      //   token n -> (b = n / seq_S, pos = start + n % seq_S)
+  int32_t seq_S, start;
+};
+
+// One component (codes, scales, biases, or float values) of K or V.
+// Dense: byte address of (seq s, head h, token t) = ptr + s*sb + h*sh + t*st.
+// Paged: ptr + block*sb + h*sh + t_in_block*st, block from the table.
+struct Comp {
+  const uint8_t* ptr;
+  int64_t sb, sh, st;
+};
+
+struct KVSrc {
+  Comp kc, ks, kb, vc, vs, vb;
+  const int32_t* table;   // nullptr = dense
+  int32_t table_stride;
+  int32_t block_size;
+  int64_t v_dim_stride;   // dim-major V codes: bytes between dim rows
+  const int32_t* seq_lens;  // nullptr = every row has T tokens
+  int32_t T;
+};
+
+struct AttnArgs {
+  const void* q;
+  int64_t q_sb, q_sh, q_sl;  // element strides of q (batch row, head, l)
+  int32_t L, Hq, Hkv, D, Dv;
+  float scale;
+  KVSrc kv;
+  int32_t mask_mode;       // 0 none, 1 causal, 2 bool array, 3 additive array
+  const void* mask;
+  int64_t m_sb, m_sh, m_sl, m_st;
+  void* out;
+  int64_t o_sb, o_sh, o_sl;
+  int32_t part_tokens, n_parts;
+  float* ws_o;             // [rows][Hq][n_parts][Dv]
+  float* ws_ml;            // [rows][Hq][n_parts][2] (max, sum)
+};
+
+// ---- launchers (vkv_kernels.hip) ----
+void launch_quantize_rows(int dtype, int bits, int group, int mode, const RowSrc& src,
+                          const RowDst& dst, int64_t rows, int D, hipStream_t st);
+void launch_copy_rows(int dtype, int mode, const RowSrc& src, const RowDst& dst, int64_t rows,
+                      int D, hipStream_t st);
+void launch_dequantize(int dtype, int bits, int group, const uint32_t* wq, const void* scales,
+                       const void* biases, void* out, int64_t rows, int D, hipStream_t st);
+// Gather rows of paged/dense KV into dense arrays.  which: 0 = keys, 1 = values.
+// out_kind: 0 = values in dtype (dequantized when bits > 0), 1 = reference
+// layout codes (+ scales, biases).
+struct GatherArgs {
+  KVSrc kv;
+  int32_t n_seqs, H, T, D, which, bits, group, dtype;
+  void* out;        // [n,H,T,D] values, or [n,H,T,D*bits/32] u32 codes
+  void* out_s;      // [n,H,T,D/group]
+  void* out_b;
+};
+void launch_gather(const GatherArgs& g, int out_kind, hipStream_t st);
+// Strided 4-D copy (element size 2 or 4): dst[i] = src[i].
+void launch_copy4d(int esize, const void* src, const int64_t* shape, const int64_t* sstr,
+                   void* dst, const int64_t* dstr, hipStream_t st);
+void launch_fill_normal(int dtype, void* data, int64_t n, uint64_t seed, float std,
+                        hipStream_t st);
+void launch_attention(int dtype, int bits, int group, bool v_dim_major, bool quant_semantics,
+                      const AttnArgs& a, int64_t rows, hipStream_t st);
+// Block pairs passed by value to the block-copy kernel.
+struct BlockPairs {
+  static constexpr int kMax = 256;
+  int32_t src[kMax];
+  int32_t dst[kMax];
+};
+// src/dst are host arrays of block ids.
+void launch_copy_blocks(const uint8_t* base, int64_t layer_bytes, int n_layers,
+                        int64_t block_bytes, const int32_t* src, const int32_t* dst, int n,
+                        hipStream_t st);
+void launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t st);
+// Scatter reference-layout affine rows (codes + scales + biases) into paged
+// chunks: the inverse of the code gather (used by QuantizedKVCache.state=).
+struct ScatterCodesArgs {
+  const uint32_t* wq;       // [n,H,T,D*bits/32] contiguous
+  const void* scales;       // [n,H,T,D/group]
+  const void* biases;
+  int32_t n_seqs, H, T, D, bits, group, dtype, is_v;
+  RowDst dst;               // paged destination, slots from table (seq_S = T)
+};
+void launch_scatter_codes(const ScatterCodesArgs& a, hipStream_t st);
+
+}  // namespace vkv

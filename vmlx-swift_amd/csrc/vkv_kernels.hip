@@ -1,0 +1,937 @@
+// vkv_kernels.hip -- gfx950 kernels of the KV-cache engine: affine
+// quantize-on-append (dense and paged, bit-exact with the reference
+// quantizer), scatter/gather, dequant-on-read, strided copies, and the
+// generic split-K decode attention used for float and quantized caches.
+//
+// Reference arithmetic: Source/Cmlx/mlx-generated/metal/quantized.h:2393-2560
+// (affine quantize / dequantize) and sdpa_vector.h:15-394 (decode SDPA and
+// its two-pass combine); Libraries/MLXLMCommon/KVCache.swift:1909-1997
+// (quantized SDPA semantics).
+#include "vkv_device.h"
+#include "vkv_internal.h"
+
+#include <algorithm>
+
+namespace vkv {
+
+// ----------------------------------------------------------------- helpers
+
+__device__ __forceinline__ const uint8_t* row_ptr(const RowSrc& s, int64_t row, int esize) {
+  int64_t i2 = row % s.e2;
+  int64_t r1 = row / s.e2;
+  int64_t i1 = r1 % s.e1;
+  int64_t i0 = r1 / s.e1;
+  return static_cast<const uint8_t*>(s.ptr) + (i0 * s.s0 + i1 * s.s1 + i2 * s.s2) * esize;
+}
+
+// Slot (block * block_size + offset) of paged token n; < 0 means skip.
+__device__ __forceinline__ int64_t token_slot(const RowDst& d, int64_t n) {
+  if (d.slots) return d.slots[n];
+  int64_t b = n / d.seq_S;
+  int64_t pos = d.start + n % d.seq_S;
+  int32_t blk = d.table[b * d.table_stride + pos / d.block_size];
+  if (blk < 0) return -1;
+  return static_cast<int64_t>(blk) * d.block_size + pos % d.block_size;
+}
+
+template <int DT>
+__device__ __forceinline__ void load8(const uint8_t* p, float* v) {
+  using E = Elem<DT>;
+  const typename E::T* q = reinterpret_cast<const typename E::T*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; i++) v[i] = E::load(q + i);
+}
+
+// ------------------------------------------------------- affine quantize
+//
+// One thread owns 8 consecutive values of a row; GROUP/8 neighbouring lanes
+// form one quantization group and reduce min/max with xor-shuffles.  The
+// arithmetic is the reference's, operation for operation, in fp32 with
+// IEEE division and round-half-away-from-zero:
+//   running min starts at Limits<T>::max, running max at 0
+//     (quantized.h:2422-2431);
+//   scale = max((max - min) / n_bins, 1e-7), negated when max is the edge,
+//   q0 = round(edge / scale), scale = edge / q0, bias = edge unless q0 == 0
+//     (:2436-2443);
+//   code = min(round((w - bias) / scale), n_bins) with the unrounded scale
+//     (:2458), scale/bias stored rounded to T (:2447-2450).
+// mode 0 writes the reference layout; mode 1 writes a paged chunk (K rows
+// token-major, V rows dim-major).
+template <int DT, int BITS, int GROUP, int MODE>
+__global__ void __launch_bounds__(256) quantize_rows_kernel(RowSrc src, RowDst dst, int64_t rows,
+                                                            int D) {
+  using E = Elem<DT>;
+  constexpr int TEAM = GROUP / 8;
+  constexpr float n_bins = static_cast<float>((1 << BITS) - 1);
+  const int tpr = D / 8;
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t row = gtid / tpr;
+  const int j = static_cast<int>(gtid % tpr);
+  const bool active = row < rows;
+
+  float v[8];
+  if (active) {
+    load8<DT>(row_ptr(src, row, E::kBytes) + static_cast<int64_t>(j) * 8 * E::kBytes, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = 0.0f;
+  }
+  float w_min = E::kMax;
+  float w_max = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    w_min = fminf(w_min, v[i]);
+    w_max = fmaxf(w_max, v[i]);
+  }
+  w_min = wave_min(w_min, TEAM);
+  w_max = wave_max(w_max, TEAM);
+  if (!active) return;
+
+  float scale = fmaxf((w_max - w_min) / n_bins, 1e-7f);
+  const bool side = fabsf(w_min) > fabsf(w_max);
+  scale = side ? scale : -scale;
+  const float edge = side ? w_min : w_max;
+  const float q0 = roundf(edge / scale);
+  const bool at_zero = q0 == 0.0f;
+  scale = at_zero ? scale : edge / q0;
+  const float bias = at_zero ? 0.0f : edge;
+
+  uint32_t code[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    float x = fminf(roundf((v[i] - bias) / scale), n_bins);
+    code[i] = x > 0.0f ? static_cast<uint32_t>(x) : 0u;
+  }
+  const int G = D / GROUP;
+  const int g = (j * 8) / GROUP;
+  const bool group_leader = (j % TEAM) == 0;
+  const typename E::T s_t = E::from_f32(scale);
+  const typename E::T b_t = E::from_f32(bias);
+
+  if constexpr (MODE == 0) {
+    uint32_t* wq = static_cast<uint32_t*>(dst.wq) + row * (D * BITS / 32);
+    if constexpr (BITS == 4) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int i = 0; i < 8; i++) w |= code[i] << (4 * i);
+      wq[j] = w;
+    } else {
+      uint32_t w0 = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
+      uint32_t w1 = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
+      wq[2 * j] = w0;
+      wq[2 * j + 1] = w1;
+    }
+    if (group_leader) {
+      static_cast<typename E::T*>(dst.scales)[row * G + g] = s_t;
+      static_cast<typename E::T*>(dst.biases)[row * G + g] = b_t;
+    }
+  } else {
+    const int64_t n = row / src.e2;
+    const int64_t h = row % src.e2;
+    const int64_t slot = token_slot(dst, n);
+    if (slot < 0) return;
+    const int64_t blk = slot / dst.block_size;
+    const int tib = static_cast<int>(slot % dst.block_size);
+    uint8_t* chunk = dst.base + blk * dst.block_bytes + h * dst.head_bytes;
+    if (!dst.is_v) {
+      uint8_t* c = chunk + dst.c_off + static_cast<int64_t>(tib) * (D * BITS / 8);
+      if constexpr (BITS == 4) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) w |= code[i] << (4 * i);
+        reinterpret_cast<uint32_t*>(c)[j] = w;
+      } else {
+        uint32_t w0 = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
+        uint32_t w1 = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
+        reinterpret_cast<uint32_t*>(c)[2 * j] = w0;
+        reinterpret_cast<uint32_t*>(c)[2 * j + 1] = w1;
+      }
+    } else {
+      // dim-major: dim d's row holds block_size codes, token tib at bit
+      // position tib*BITS of the row (little-endian words).
+      const int64_t row_bytes = static_cast<int64_t>(dst.block_size) * BITS / 8;
+      uint8_t* c = chunk + dst.c_off;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int d = j * 8 + i;
+        if constexpr (BITS == 8) {
+          c[d * row_bytes + tib] = static_cast<uint8_t>(code[i]);
+        } else {
+          uint32_t* word = reinterpret_cast<uint32_t*>(c + d * row_bytes) + tib / 8;
+          const int sh = 4 * (tib % 8);
+          atomicAnd(word, ~(0xFu << sh));
+          atomicOr(word, code[i] << sh);
+        }
+      }
+    }
+    if (group_leader) {
+      reinterpret_cast<typename E::T*>(chunk + dst.s_off)[tib * G + g] = s_t;
+      reinterpret_cast<typename E::T*>(chunk + dst.b_off)[tib * G + g] = b_t;
+    }
+  }
+}
+
+// Float rows: mode 0 copies to contiguous out (dst.wq), mode 1 scatters to
+// paged chunks (token-major K or V at dst.c_off).
+template <int ESIZE, int MODE>
+__global__ void __launch_bounds__(256) copy_rows_kernel(RowSrc src, RowDst dst, int64_t rows, int D) {
+  const int tpr = (D + 7) / 8;
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t row = gtid / tpr;
+  const int j = static_cast<int>(gtid % tpr);
+  if (row >= rows) return;
+  const uint8_t* s = row_ptr(src, row, ESIZE) + static_cast<int64_t>(j) * 8 * ESIZE;
+  uint8_t* o;
+  if constexpr (MODE == 0) {
+    o = static_cast<uint8_t*>(dst.wq) + (row * D + j * 8) * ESIZE;
+  } else {
+    const int64_t n = row / src.e2;
+    const int64_t h = row % src.e2;
+    const int64_t slot = token_slot(dst, n);
+    if (slot < 0) return;
+    const int64_t blk = slot / dst.block_size;
+    const int64_t tib = slot % dst.block_size;
+    o = dst.base + blk * dst.block_bytes + h * dst.head_bytes + dst.c_off +
+        (tib * D + j * 8) * ESIZE;
+  }
+  const int cnt = min(8, D - j * 8);
+  if constexpr (ESIZE == 2) {
+    const uint16_t* a = reinterpret_cast<const uint16_t*>(s);
+    uint16_t* b = reinterpret_cast<uint16_t*>(o);
+    for (int i = 0; i < cnt; i++) b[i] = a[i];
+  } else {
+    const uint32_t* a = reinterpret_cast<const uint32_t*>(s);
+    uint32_t* b = reinterpret_cast<uint32_t*>(o);
+    for (int i = 0; i < cnt; i++) b[i] = a[i];
+  }
+}
+
+// quantized.h:2498-2560: out = scale * q + bias, here one fp32 fma rounded
+// once to T.  Thread per 8 values, contiguous operands.
+template <int DT, int BITS>
+__global__ void __launch_bounds__(256) dequantize_kernel(const uint32_t* wq, const void* scales,
+                                                         const void* biases, void* out, int64_t rows,
+                                                         int D, int group) {
+  using E = Elem<DT>;
+  const int tpr = D / 8;
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t row = gtid / tpr;
+  const int j = static_cast<int>(gtid % tpr);
+  if (row >= rows) return;
+  const int G = D / group;
+  const int g = j * 8 / group;
+  const float s = E::load(static_cast<const typename E::T*>(scales) + row * G + g);
+  const float b = E::load(static_cast<const typename E::T*>(biases) + row * G + g);
+  const uint32_t* w = wq + row * (D * BITS / 32);
+  typename E::T* o = static_cast<typename E::T*>(out) + row * D + j * 8;
+  if constexpr (BITS == 4) {
+    uint32_t x = w[j];
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = E::from_f32(fmaf(s, static_cast<float>((x >> (4 * i)) & 15u), b));
+  } else {
+    uint32_t x0 = w[2 * j], x1 = w[2 * j + 1];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      o[i] = E::from_f32(fmaf(s, static_cast<float>((x0 >> (8 * i)) & 255u), b));
+      o[4 + i] = E::from_f32(fmaf(s, static_cast<float>((x1 >> (8 * i)) & 255u), b));
+    }
+  }
+}
+
+// ---------------------------------------------------------------- KV access
+
+struct TokLoc {
+  int64_t blk;  // block id (paged) or sequence index (dense)
+  int64_t tib;  // token index inside the block (or sequence)
+};
+
+__device__ __forceinline__ TokLoc locate(const KVSrc& kv, int64_t s, int64_t t) {
+  TokLoc r;
+  if (kv.table) {
+    r.blk = kv.table[s * kv.table_stride + t / kv.block_size];
+    r.tib = t % kv.block_size;
+  } else {
+    r.blk = s;
+    r.tib = t;
+  }
+  return r;
+}
+
+__device__ __forceinline__ const uint8_t* at(const Comp& c, const TokLoc& l, int64_t h) {
+  return c.ptr + l.blk * c.sb + h * c.sh + l.tib * c.st;
+}
+
+// code of element d of a token-major codes row
+template <int BITS>
+__device__ __forceinline__ uint32_t code_tm(const uint8_t* row, int d) {
+  if constexpr (BITS == 8) return row[d];
+  return (row[d >> 1] >> (4 * (d & 1))) & 15u;
+}
+
+// Key element (token at l, dim d) as float.
+template <int DT, int BITS>
+__device__ __forceinline__ float key_at(const KVSrc& kv, const TokLoc& l, int64_t h, int d,
+                                        int group) {
+  using E = Elem<DT>;
+  if constexpr (BITS == 0) {
+    return E::load(reinterpret_cast<const typename E::T*>(at(kv.kc, l, h)) + d);
+  } else {
+    const int g = d / group;
+    const float s = E::load(reinterpret_cast<const typename E::T*>(at(kv.ks, l, h)) + g);
+    const float b = E::load(reinterpret_cast<const typename E::T*>(at(kv.kb, l, h)) + g);
+    return fmaf(s, static_cast<float>(code_tm<BITS>(at(kv.kc, l, h), d)), b);
+  }
+}
+
+template <int DT, int BITS, bool VDM>
+__device__ __forceinline__ float value_at(const KVSrc& kv, const TokLoc& l, int64_t h, int d,
+                                          int group) {
+  using E = Elem<DT>;
+  if constexpr (BITS == 0) {
+    return E::load(reinterpret_cast<const typename E::T*>(at(kv.vc, l, h)) + d);
+  } else {
+    const int g = d / group;
+    const float s = E::load(reinterpret_cast<const typename E::T*>(at(kv.vs, l, h)) + g);
+    const float b = E::load(reinterpret_cast<const typename E::T*>(at(kv.vb, l, h)) + g);
+    uint32_t c;
+    if constexpr (VDM) {
+      const uint8_t* row = kv.vc.ptr + l.blk * kv.vc.sb + h * kv.vc.sh + d * kv.v_dim_stride;
+      c = code_tm<BITS>(row, static_cast<int>(l.tib));
+    } else {
+      c = code_tm<BITS>(at(kv.vc, l, h), d);
+    }
+    return fmaf(s, static_cast<float>(c), b);
+  }
+}
+
+// --------------------------------------------------------------- gather
+//
+// Thread per (seq, head, token, 8 dims).  out_kind 0: values (dequantized
+// when bits > 0) into [n,H,T,D] of dtype; out_kind 1: reference-layout codes.
+template <int DT, int BITS, int KIND, bool VDM>
+__global__ void __launch_bounds__(256) gather_kernel(GatherArgs g) {
+  using E = Elem<DT>;
+  const int tpr = (g.D + 7) / 8;
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t row = gtid / tpr;  // (s, h, t)
+  const int j = static_cast<int>(gtid % tpr);
+  const int64_t total = static_cast<int64_t>(g.n_seqs) * g.H * g.T;
+  if (row >= total) return;
+  const int64_t t = row % g.T;
+  const int64_t h = (row / g.T) % g.H;
+  const int64_t s = row / (static_cast<int64_t>(g.T) * g.H);
+  const int64_t len = g.kv.seq_lens ? g.kv.seq_lens[s] : g.kv.T;
+  if (t >= len) return;
+  const TokLoc l = locate(g.kv, s, t);
+  const int d0 = j * 8;
+  const int cnt = min(8, g.D - d0);
+  if constexpr (KIND == 0) {
+    typename E::T* o = static_cast<typename E::T*>(g.out) + row * g.D + d0;
+    for (int i = 0; i < cnt; i++) {
+      float x = g.which == 0 ? key_at<DT, BITS>(g.kv, l, h, d0 + i, g.group)
+                             : value_at<DT, BITS, VDM>(g.kv, l, h, d0 + i, g.group);
+      o[i] = E::from_f32(x);
+    }
+  } else {
+    // codes of dims [d0, d0+8) re-packed little-endian into the reference layout
+    const Comp& cc = g.which == 0 ? g.kv.kc : g.kv.vc;
+    uint32_t code[8];
+    for (int i = 0; i < 8; i++) {
+      const int d = d0 + i;
+      if (VDM && g.which == 1) {
+        const uint8_t* r = cc.ptr + l.blk * cc.sb + h * cc.sh + d * g.kv.v_dim_stride;
+        code[i] = code_tm<BITS>(r, static_cast<int>(l.tib));
+      } else {
+        code[i] = code_tm<BITS>(at(cc, l, h), d);
+      }
+    }
+    uint32_t* wq = static_cast<uint32_t*>(g.out) + row * (g.D * BITS / 32);
+    if constexpr (BITS == 4) {
+      uint32_t w = 0;
+      for (int i = 0; i < 8; i++) w |= code[i] << (4 * i);
+      wq[j] = w;
+    } else {
+      wq[2 * j] = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
+      wq[2 * j + 1] = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
+    }
+    if (d0 % g.group == 0) {
+      const int G = g.D / g.group;
+      const int gi = d0 / g.group;
+      const Comp& sc = g.which == 0 ? g.kv.ks : g.kv.vs;
+      const Comp& bc = g.which == 0 ? g.kv.kb : g.kv.vb;
+      static_cast<typename E::T*>(g.out_s)[row * G + gi] =
+          reinterpret_cast<const typename E::T*>(at(sc, l, h))[gi];
+      static_cast<typename E::T*>(g.out_b)[row * G + gi] =
+          reinterpret_cast<const typename E::T*>(at(bc, l, h))[gi];
+    }
+  }
+}
+
+// Reference-layout affine rows -> paged chunks (inverse of the code gather).
+template <int ESIZE, int BITS>
+__global__ void __launch_bounds__(256) scatter_codes_kernel(ScatterCodesArgs a) {
+  const int tpr = a.D / 8;
+  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t row = gtid / tpr;  // (s, h, t)
+  const int j = static_cast<int>(gtid % tpr);
+  const int64_t total = static_cast<int64_t>(a.n_seqs) * a.H * a.T;
+  if (row >= total) return;
+  const int64_t t = row % a.T;
+  const int64_t h = (row / a.T) % a.H;
+  const int64_t s = row / (static_cast<int64_t>(a.T) * a.H);
+  const RowDst& d = a.dst;
+  const int32_t blk = d.table[s * d.table_stride + t / d.block_size];
+  if (blk < 0) return;
+  const int tib = static_cast<int>(t % d.block_size);
+  uint8_t* chunk = d.base + static_cast<int64_t>(blk) * d.block_bytes + h * d.head_bytes;
+  const uint32_t* w = a.wq + row * (a.D * BITS / 32);
+  uint32_t code[8];
+  if constexpr (BITS == 4) {
+    const uint32_t x = w[j];
+    for (int i = 0; i < 8; i++) code[i] = (x >> (4 * i)) & 15u;
+  } else {
+    const uint32_t x0 = w[2 * j], x1 = w[2 * j + 1];
+    for (int i = 0; i < 4; i++) {
+      code[i] = (x0 >> (8 * i)) & 255u;
+      code[4 + i] = (x1 >> (8 * i)) & 255u;
+    }
+  }
+  if (!a.is_v) {
+    uint32_t* c = reinterpret_cast<uint32_t*>(chunk + d.c_off + static_cast<int64_t>(tib) * (a.D * BITS / 8));
+    if constexpr (BITS == 4) c[j] = w[j];
+    else { c[2 * j] = w[2 * j]; c[2 * j + 1] = w[2 * j + 1]; }
+  } else {
+    const int64_t row_bytes = static_cast<int64_t>(d.block_size) * BITS / 8;
+    uint8_t* c = chunk + d.c_off;
+    for (int i = 0; i < 8; i++) {
+      const int dd = j * 8 + i;
+      if constexpr (BITS == 8) {
+        c[dd * row_bytes + tib] = static_cast<uint8_t>(code[i]);
+      } else {
+        uint32_t* word = reinterpret_cast<uint32_t*>(c + dd * row_bytes) + tib / 8;
+        const int sh = 4 * (tib % 8);
+        atomicAnd(word, ~(0xFu << sh));
+        atomicOr(word, code[i] << sh);
+      }
+    }
+  }
+  if ((j * 8) % a.group == 0) {
+    const int G = a.D / a.group;
+    const int g = j * 8 / a.group;
+    const uint8_t* sp = static_cast<const uint8_t*>(a.scales) + (row * G + g) * ESIZE;
+    const uint8_t* bp = static_cast<const uint8_t*>(a.biases) + (row * G + g) * ESIZE;
+    uint8_t* so = chunk + d.s_off + (static_cast<int64_t>(tib) * G + g) * ESIZE;
+    uint8_t* bo = chunk + d.b_off + (static_cast<int64_t>(tib) * G + g) * ESIZE;
+    for (int i = 0; i < ESIZE; i++) {
+      so[i] = sp[i];
+      bo[i] = bp[i];
+    }
+  }
+}
+
+// ------------------------------------------------------------ copy4d
+
+template <typename U>
+__global__ void __launch_bounds__(256) copy4d_kernel(const U* src, U* dst, int64_t n0, int64_t n1,
+                                                     int64_t n2, int64_t n3, int64_t s0, int64_t s1,
+                                                     int64_t s2, int64_t s3, int64_t d0, int64_t d1,
+                                                     int64_t d2, int64_t d3) {
+  const int64_t total = n0 * n1 * n2 * n3;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    int64_t i3 = i % n3;
+    int64_t r = i / n3;
+    int64_t i2 = r % n2;
+    r /= n2;
+    int64_t i1 = r % n1;
+    int64_t i0 = r / n1;
+    dst[i0 * d0 + i1 * d1 + i2 * d2 + i3 * d3] = src[i0 * s0 + i1 * s1 + i2 * s2 + i3 * s3];
+  }
+}
+
+// Whole-block copy across all layers (copy-on-write, prefix store).  The
+// (src, dst) pairs travel in the kernel arguments, so no device staging
+// buffer has to outlive the launch.
+__global__ void __launch_bounds__(256) copy_blocks_kernel(uint8_t* base, int64_t layer_bytes,
+                                                          int64_t block_bytes, BlockPairs pairs) {
+  const int pair = blockIdx.y;
+  const int layer = blockIdx.z;
+  const int64_t words = block_bytes / 16;
+  const uint4* s = reinterpret_cast<const uint4*>(base + layer * layer_bytes +
+                                                  static_cast<int64_t>(pairs.src[pair]) * block_bytes);
+  uint4* d = reinterpret_cast<uint4*>(base + layer * layer_bytes +
+                                      static_cast<int64_t>(pairs.dst[pair]) * block_bytes);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < words;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    d[i] = s[i];
+}
+
+__global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = v;
+}
+
+// ------------------------------------------------------------ synthetic
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256) fill_normal_kernel(void* data, int64_t n, uint64_t seed,
+                                                          float std) {
+  using E = Elem<DT>;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const uint64_t r = splitmix64(seed * 0x100000001B3ull + static_cast<uint64_t>(i));
+    const float u1 = (static_cast<float>(r >> 40) + 1.0f) * (1.0f / 16777216.0f);
+    const float u2 = static_cast<float>((r >> 16) & 0xFFFFFFu) * (1.0f / 16777216.0f);
+    const float z = sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+    static_cast<typename E::T*>(data)[i] = E::from_f32(z * std);
+  }
+}
+
+// ------------------------------------------------------------ attention
+//
+// Split-K decode attention, one workgroup (256 threads) per (partition,
+// kv head, query row).  A workgroup walks its partition in tiles of 32
+// tokens: 8 lanes per token form scores for the REP query heads that share
+// the kv head (one K read serves all of them), one wave updates the running
+// max / sum (online softmax, sdpa_vector.h:116-131), and each thread then
+// accumulates P.V for one value dim.  Partials (unnormalised o, max, sum)
+// are combined by attn_combine_kernel exactly as sdpa_vector_2pass_2 does
+// (sdpa_vector.h:320-394); a single-partition launch normalises in place.
+//
+// QSEM selects the quantized-SDPA semantics of KVCache.swift:1909-1997:
+// queries scaled in T, masked scores set to T's lowest value (so a fully
+// masked row averages V).  Otherwise MLXFast semantics: queries scaled in
+// fp32, masked keys skipped, an empty row yields zeros.
+constexpr int kTile = 32;
+constexpr int kMaxD = 256;
+constexpr int kGroup = 64;  // affine attention group size
+
+template <int DT, int BITS, int REP, bool VDM, bool QSEM>
+__global__ void __launch_bounds__(256) attn_partial_kernel(AttnArgs a, int h_off, int rep_total) {
+  using E = Elem<DT>;
+  __shared__ float qs[REP][kMaxD];
+  __shared__ float sc[REP][kTile];
+  __shared__ float alpha_s[REP];
+  __shared__ float red[256 * REP];
+
+  const int tid = threadIdx.x;
+  const int part = blockIdx.x;
+  const int hk = blockIdx.y;
+  const int64_t row = blockIdx.z;  // b * L + l
+  const int64_t b = row / a.L;
+  const int l = static_cast<int>(row % a.L);
+  const int D = a.D, Dv = a.Dv;
+  const int64_t T = a.kv.seq_lens ? a.kv.seq_lens[b] : a.kv.T;
+  const int64_t t_begin = static_cast<int64_t>(part) * a.part_tokens;
+  const int64_t t_end = min<int64_t>(T, t_begin + a.part_tokens);
+  const float lowest = -E::kMax;
+
+  // queries of the REP heads sharing kv head hk
+  const float scale_t = QSEM ? round_to<DT>(a.scale) : a.scale;
+  for (int i = tid; i < REP * D; i += 256) {
+    const int r = i / D, d = i % D;
+    const int h = hk * rep_total + h_off + r;
+    const float qv = E::load(static_cast<const typename E::T*>(a.q) + b * a.q_sb + h * a.q_sh +
+                             static_cast<int64_t>(l) * a.q_sl + d);
+    qs[r][d] = QSEM ? round_to<DT>(qv * scale_t) : qv * scale_t;
+  }
+
+  // Phase-C thread layout: value dim `vd`, token subset `sub`.
+  const int n_sub = max(1, 256 / Dv);
+  const int vd = tid % Dv;
+  const int sub = tid / Dv;
+  const bool c_active = sub < n_sub && tid < n_sub * Dv;
+  float o[REP];
+#pragma unroll
+  for (int r = 0; r < REP; r++) o[r] = 0.0f;
+  float m_run = -3.402823466e38f, l_run = 0.0f;  // lanes r < REP of wave 0 own head r
+  __syncthreads();
+
+  for (int64_t t0 = t_begin; t0 < t_end; t0 += kTile) {
+    // ---- phase A: scores
+    {
+      const int tt = tid / 8, lane = tid % 8;
+      const int64_t t = t0 + tt;
+      float acc[REP];
+#pragma unroll
+      for (int r = 0; r < REP; r++) acc[r] = 0.0f;
+      if (t < t_end) {
+        const TokLoc loc = locate(a.kv, b, t);
+        for (int d = lane; d < D; d += 8) {
+          const float kv = key_at<DT, BITS>(a.kv, loc, hk, d, kGroup);
+#pragma unroll
+          for (int r = 0; r < REP; r++) acc[r] = fmaf(qs[r][d], kv, acc[r]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < REP; r++) acc[r] = wave_sum(acc[r], 8);
+      if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < REP; r++) {
+          float s = acc[r];
+          bool vis = t < t_end;
+          if (vis && a.mask_mode != 0) {
+            const int h = hk * rep_total + h_off + r;
+            if (a.mask_mode == 1) {
+              vis = t <= T - a.L + l;
+            } else {
+              const int64_t mo = b * a.m_sb + h * a.m_sh + l * a.m_sl + t * a.m_st;
+              if (a.mask_mode == 2) {
+                vis = static_cast<const uint8_t*>(a.mask)[mo] != 0;
+              } else {
+                const float add = static_cast<const float*>(a.mask)[mo];
+                if (QSEM) {
+                  s += add;
+                } else {
+                  vis = add >= -3.402823466e38f;
+                  s += add;
+                }
+              }
+            }
+            if (QSEM && !vis && t < t_end) {
+              s = lowest;
+              vis = true;
+            }
+          }
+          sc[r][tt] = vis ? s : -INFINITY;
+        }
+      }
+    }
+    __syncthreads();
+    // ---- phase B: online softmax update (wave 0, lane = token in tile)
+    if (tid < 64) {
+      const int tt = tid & 31;
+#pragma unroll
+      for (int r = 0; r < REP; r++) {
+        const float s = sc[r][tt];
+        float tmax = wave_max(tid < 32 ? s : -INFINITY, 64);
+        const float m_old = __shfl(m_run, r, 64);
+        const float m_new = fmaxf(m_old, tmax);
+        const float p = (tid < 32 && s != -INFINITY) ? __expf(s - m_new) : 0.0f;
+        const float psum = wave_sum(p, 64);
+        const float al = __expf(m_old - m_new);
+        if (tid < 32) sc[r][tt] = p;
+        if (tid == r) {
+          m_run = m_new;
+          l_run = l_run * al + psum;
+          alpha_s[r] = al;
+        }
+      }
+    }
+    __syncthreads();
+    // ---- phase C: o = o * alpha + sum_t p_t v_t
+    if (c_active) {
+#pragma unroll
+      for (int r = 0; r < REP; r++) o[r] *= alpha_s[r];
+      for (int tt = sub; tt < kTile; tt += n_sub) {
+        const int64_t t = t0 + tt;
+        if (t >= t_end) break;
+        const TokLoc loc = locate(a.kv, b, t);
+        const float vv = value_at<DT, BITS, VDM>(a.kv, loc, hk, vd, kGroup);
+#pragma unroll
+        for (int r = 0; r < REP; r++) o[r] = fmaf(sc[r][tt], vv, o[r]);
+      }
+    }
+    __syncthreads();
+  }
+
+  // combine the token subsets of phase C
+  if (c_active) {
+#pragma unroll
+    for (int r = 0; r < REP; r++) red[(r * n_sub + sub) * Dv + vd] = o[r];
+  }
+  if (tid < REP) {
+    qs[tid][0] = m_run;  // reuse: per-head max / sum
+    qs[tid][1] = l_run;
+  }
+  __syncthreads();
+  for (int i = tid; i < REP * Dv; i += 256) {
+    const int r = i / Dv, d = i % Dv;
+    float acc = 0.0f;
+    for (int s2 = 0; s2 < n_sub; s2++) acc += red[(r * n_sub + s2) * Dv + d];
+    const float m = qs[r][0], lsum = qs[r][1];
+    const int h = hk * rep_total + h_off + r;
+    if (a.n_parts == 1) {
+      const float v = lsum > 0.0f ? acc / lsum : 0.0f;
+      static_cast<typename E::T*>(a.out)[b * a.o_sb + h * a.o_sh + static_cast<int64_t>(l) * a.o_sl +
+                                         d] = E::from_f32(v);
+    } else {
+      const int64_t base = ((row * a.Hq + h) * a.n_parts + part);
+      a.ws_o[base * Dv + d] = acc;
+      if (d == 0) {
+        a.ws_ml[base * 2] = m;
+        a.ws_ml[base * 2 + 1] = lsum;
+      }
+    }
+  }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
+  using E = Elem<DT>;
+  const int64_t rh = blockIdx.x;  // row * Hq + h
+  const int64_t row = rh / a.Hq;
+  const int h = static_cast<int>(rh % a.Hq);
+  const int64_t b = row / a.L;
+  const int l = static_cast<int>(row % a.L);
+  const float* ml = a.ws_ml + rh * a.n_parts * 2;
+  float M = -3.402823466e38f;
+  for (int p = 0; p < a.n_parts; p++) M = fmaxf(M, ml[2 * p]);
+  float Lsum = 0.0f;
+  for (int p = 0; p < a.n_parts; p++) Lsum += __expf(ml[2 * p] - M) * ml[2 * p + 1];
+  for (int d = threadIdx.x; d < a.Dv; d += blockDim.x) {
+    float acc = 0.0f;
+    for (int p = 0; p < a.n_parts; p++)
+      acc += __expf(ml[2 * p] - M) * a.ws_o[(rh * a.n_parts + p) * a.Dv + d];
+    const float v = Lsum > 0.0f ? acc / Lsum : 0.0f;
+    static_cast<typename E::T*>(a.out)[b * a.o_sb + h * a.o_sh + static_cast<int64_t>(l) * a.o_sl +
+                                       d] = E::from_f32(v);
+  }
+}
+
+// ------------------------------------------------------------ launchers
+
+static inline unsigned blocks_for(int64_t threads) {
+  return static_cast<unsigned>((threads + 255) / 256);
+}
+
+template <int DT>
+static void quantize_dispatch(int bits, int group, int mode, const RowSrc& src, const RowDst& dst,
+                              int64_t rows, int D, hipStream_t st) {
+  const unsigned nb = blocks_for(rows * (D / 8));
+#define VKV_Q(B, G, M) \
+  hipLaunchKernelGGL((quantize_rows_kernel<DT, B, G, M>), dim3(nb), dim3(256), 0, st, src, dst, rows, D)
+#define VKV_QM(B, G) \
+  do { if (mode == 0) VKV_Q(B, G, 0); else VKV_Q(B, G, 1); } while (0)
+#define VKV_QG(B)                               \
+  do {                                          \
+    if (group == 32) VKV_QM(B, 32);             \
+    else if (group == 64) VKV_QM(B, 64);        \
+    else if (group == 128) VKV_QM(B, 128);      \
+    else throw Error("group_size must be 32, 64 or 128"); \
+  } while (0)
+  if (bits == 4) VKV_QG(4);
+  else if (bits == 8) VKV_QG(8);
+  else throw Error("bits must be 4 or 8");
+#undef VKV_QG
+#undef VKV_QM
+#undef VKV_Q
+}
+
+void launch_quantize_rows(int dtype, int bits, int group, int mode, const RowSrc& src,
+                          const RowDst& dst, int64_t rows, int D, hipStream_t st) {
+  if (rows <= 0) return;
+  VKV_CHECK(D % group == 0 && D % 8 == 0, "last dim must be a multiple of group_size");
+  switch (dtype) {
+    case kF32: quantize_dispatch<kF32>(bits, group, mode, src, dst, rows, D, st); break;
+    case kF16: quantize_dispatch<kF16>(bits, group, mode, src, dst, rows, D, st); break;
+    case kBF16: quantize_dispatch<kBF16>(bits, group, mode, src, dst, rows, D, st); break;
+    default: throw Error("unsupported dtype");
+  }
+  VKV_HIP(hipGetLastError());
+}
+
+void launch_copy_rows(int dtype, int mode, const RowSrc& src, const RowDst& dst, int64_t rows,
+                      int D, hipStream_t st) {
+  if (rows <= 0) return;
+  const unsigned nb = blocks_for(rows * ((D + 7) / 8));
+  if (elem_bytes(dtype) == 2) {
+    if (mode == 0) hipLaunchKernelGGL((copy_rows_kernel<2, 0>), dim3(nb), dim3(256), 0, st, src, dst, rows, D);
+    else hipLaunchKernelGGL((copy_rows_kernel<2, 1>), dim3(nb), dim3(256), 0, st, src, dst, rows, D);
+  } else {
+    if (mode == 0) hipLaunchKernelGGL((copy_rows_kernel<4, 0>), dim3(nb), dim3(256), 0, st, src, dst, rows, D);
+    else hipLaunchKernelGGL((copy_rows_kernel<4, 1>), dim3(nb), dim3(256), 0, st, src, dst, rows, D);
+  }
+  VKV_HIP(hipGetLastError());
+}
+
+void launch_dequantize(int dtype, int bits, int group, const uint32_t* wq, const void* scales,
+                       const void* biases, void* out, int64_t rows, int D, hipStream_t st) {
+  if (rows <= 0) return;
+  VKV_CHECK(D % group == 0 && group % 8 == 0, "last dim must be a multiple of group_size");
+  const unsigned nb = blocks_for(rows * (D / 8));
+#define VKV_DQ(DT, B) \
+  hipLaunchKernelGGL((dequantize_kernel<DT, B>), dim3(nb), dim3(256), 0, st, wq, scales, biases, out, rows, D, group)
+#define VKV_DQB(DT) do { if (bits == 4) VKV_DQ(DT, 4); else if (bits == 8) VKV_DQ(DT, 8); else throw Error("bits must be 4 or 8"); } while (0)
+  switch (dtype) {
+    case kF32: VKV_DQB(kF32); break;
+    case kF16: VKV_DQB(kF16); break;
+    case kBF16: VKV_DQB(kBF16); break;
+    default: throw Error("unsupported dtype");
+  }
+#undef VKV_DQB
+#undef VKV_DQ
+  VKV_HIP(hipGetLastError());
+}
+
+template <int DT, int BITS>
+static void gather_dispatch_kind(const GatherArgs& g, int out_kind, hipStream_t st) {
+  const unsigned nb = blocks_for(static_cast<int64_t>(g.n_seqs) * g.H * g.T * ((g.D + 7) / 8));
+  const bool vdm = g.kv.v_dim_stride > 0;
+  if (out_kind == 0) {
+    if (vdm) hipLaunchKernelGGL((gather_kernel<DT, BITS, 0, true>), dim3(nb), dim3(256), 0, st, g);
+    else hipLaunchKernelGGL((gather_kernel<DT, BITS, 0, false>), dim3(nb), dim3(256), 0, st, g);
+  } else {
+    if constexpr (BITS > 0) {
+      if (vdm) hipLaunchKernelGGL((gather_kernel<DT, BITS, 1, true>), dim3(nb), dim3(256), 0, st, g);
+      else hipLaunchKernelGGL((gather_kernel<DT, BITS, 1, false>), dim3(nb), dim3(256), 0, st, g);
+    } else {
+      throw Error("code gather needs an affine view");
+    }
+  }
+}
+
+template <int DT>
+static void gather_dispatch(const GatherArgs& g, int out_kind, hipStream_t st) {
+  if (g.bits == 0) gather_dispatch_kind<DT, 0>(g, out_kind, st);
+  else if (g.bits == 4) gather_dispatch_kind<DT, 4>(g, out_kind, st);
+  else if (g.bits == 8) gather_dispatch_kind<DT, 8>(g, out_kind, st);
+  else throw Error("bits must be 0, 4 or 8");
+}
+
+void launch_gather(const GatherArgs& g, int out_kind, hipStream_t st) {
+  if (static_cast<int64_t>(g.n_seqs) * g.H * g.T == 0) return;
+  switch (g.dtype) {
+    case kF32: gather_dispatch<kF32>(g, out_kind, st); break;
+    case kF16: gather_dispatch<kF16>(g, out_kind, st); break;
+    case kBF16: gather_dispatch<kBF16>(g, out_kind, st); break;
+    default: throw Error("unsupported dtype");
+  }
+  VKV_HIP(hipGetLastError());
+}
+
+void launch_scatter_codes(const ScatterCodesArgs& a, hipStream_t st) {
+  const int64_t rows = static_cast<int64_t>(a.n_seqs) * a.H * a.T;
+  if (rows <= 0) return;
+  const unsigned nb = blocks_for(rows * (a.D / 8));
+  const int es = elem_bytes(a.dtype);
+  if (a.bits == 4 && es == 2) hipLaunchKernelGGL((scatter_codes_kernel<2, 4>), dim3(nb), dim3(256), 0, st, a);
+  else if (a.bits == 4) hipLaunchKernelGGL((scatter_codes_kernel<4, 4>), dim3(nb), dim3(256), 0, st, a);
+  else if (a.bits == 8 && es == 2) hipLaunchKernelGGL((scatter_codes_kernel<2, 8>), dim3(nb), dim3(256), 0, st, a);
+  else if (a.bits == 8) hipLaunchKernelGGL((scatter_codes_kernel<4, 8>), dim3(nb), dim3(256), 0, st, a);
+  else throw Error("bits must be 4 or 8");
+  VKV_HIP(hipGetLastError());
+}
+
+void launch_copy4d(int esize, const void* src, const int64_t* n, const int64_t* s, void* dst,
+                   const int64_t* d, hipStream_t st) {
+  const int64_t total = n[0] * n[1] * n[2] * n[3];
+  if (total <= 0) return;
+  const unsigned nb = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 65536));
+  if (esize == 2) {
+    hipLaunchKernelGGL((copy4d_kernel<uint16_t>), dim3(nb), dim3(256), 0, st,
+                       static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), n[0], n[1],
+                       n[2], n[3], s[0], s[1], s[2], s[3], d[0], d[1], d[2], d[3]);
+  } else if (esize == 4) {
+    hipLaunchKernelGGL((copy4d_kernel<uint32_t>), dim3(nb), dim3(256), 0, st,
+                       static_cast<const uint32_t*>(src), static_cast<uint32_t*>(dst), n[0], n[1],
+                       n[2], n[3], s[0], s[1], s[2], s[3], d[0], d[1], d[2], d[3]);
+  } else if (esize == 1) {
+    hipLaunchKernelGGL((copy4d_kernel<uint8_t>), dim3(nb), dim3(256), 0, st,
+                       static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), n[0], n[1],
+                       n[2], n[3], s[0], s[1], s[2], s[3], d[0], d[1], d[2], d[3]);
+  } else {
+    throw Error("copy4d: element size must be 1, 2 or 4");
+  }
+  VKV_HIP(hipGetLastError());
+}
+
+void launch_copy_blocks(const uint8_t* base, int64_t layer_bytes, int n_layers, int64_t block_bytes,
+                        const int32_t* src, const int32_t* dst, int n, hipStream_t st) {
+  VKV_CHECK(block_bytes % 16 == 0, "block bytes must be a multiple of 16");
+  const unsigned gx = static_cast<unsigned>(std::min<int64_t>((block_bytes / 16 + 255) / 256, 64));
+  for (int done = 0; done < n; done += BlockPairs::kMax) {
+    BlockPairs bp;
+    const int cnt = std::min(n - done, BlockPairs::kMax);
+    for (int i = 0; i < cnt; i++) {
+      bp.src[i] = src[done + i];
+      bp.dst[i] = dst[done + i];
+    }
+    hipLaunchKernelGGL(copy_blocks_kernel, dim3(gx, cnt, n_layers), dim3(256), 0, st,
+                       const_cast<uint8_t*>(base), layer_bytes, block_bytes, bp);
+    VKV_HIP(hipGetLastError());
+  }
+}
+
+void launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t st) {
+  if (n <= 0) return;
+  const unsigned nb = static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 4096));
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(nb), dim3(256), 0, st, p, n, v);
+  VKV_HIP(hipGetLastError());
+}
+
+void launch_fill_normal(int dtype, void* data, int64_t n, uint64_t seed, float std, hipStream_t st) {
+  if (n <= 0) return;
+  const unsigned nb = static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 1 << 16));
+  switch (dtype) {
+    case kF32: hipLaunchKernelGGL((fill_normal_kernel<kF32>), dim3(nb), dim3(256), 0, st, data, n, seed, std); break;
+    case kF16: hipLaunchKernelGGL((fill_normal_kernel<kF16>), dim3(nb), dim3(256), 0, st, data, n, seed, std); break;
+    case kBF16: hipLaunchKernelGGL((fill_normal_kernel<kBF16>), dim3(nb), dim3(256), 0, st, data, n, seed, std); break;
+    default: throw Error("unsupported dtype");
+  }
+  VKV_HIP(hipGetLastError());
+}
+
+template <int DT, int BITS, bool VDM, bool QSEM>
+static void attn_dispatch_rep(const AttnArgs& a, int64_t rows, hipStream_t st) {
+  const int rep = a.Hq / a.Hkv;
+  dim3 grid(a.n_parts, a.Hkv, static_cast<unsigned>(rows));
+  int done = 0;
+  while (done < rep) {
+    const int left = rep - done;
+    const int chunk = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+#define VKV_A(R) \
+  hipLaunchKernelGGL((attn_partial_kernel<DT, BITS, R, VDM, QSEM>), grid, dim3(256), 0, st, a, done, rep)
+    if (chunk == 8) VKV_A(8);
+    else if (chunk == 4) VKV_A(4);
+    else if (chunk == 2) VKV_A(2);
+    else VKV_A(1);
+#undef VKV_A
+    done += chunk;
+  }
+  if (a.n_parts > 1)
+    hipLaunchKernelGGL((attn_combine_kernel<DT>), dim3(static_cast<unsigned>(rows * a.Hq)), dim3(256),
+                       0, st, a);
+}
+
+template <int DT>
+static void attn_dispatch(int bits, bool vdm, bool qsem, const AttnArgs& a, int64_t rows,
+                          hipStream_t st) {
+  if (bits == 0) {
+    if (qsem) throw Error("quantized semantics need an affine cache");
+    attn_dispatch_rep<DT, 0, false, false>(a, rows, st);
+  } else if (bits == 4) {
+    if (vdm) attn_dispatch_rep<DT, 4, true, true>(a, rows, st);
+    else attn_dispatch_rep<DT, 4, false, true>(a, rows, st);
+  } else if (bits == 8) {
+    if (vdm) attn_dispatch_rep<DT, 8, true, true>(a, rows, st);
+    else attn_dispatch_rep<DT, 8, false, true>(a, rows, st);
+  } else {
+    throw Error("bits must be 0, 4 or 8");
+  }
+}
+
+void launch_attention(int dtype, int bits, int group, bool v_dim_major, bool quant_semantics,
+                      const AttnArgs& a, int64_t rows, hipStream_t st) {
+  if (rows <= 0) return;
+  VKV_CHECK(a.D <= kMaxD && a.Dv <= kMaxD, "head dims above 256 are not supported here");
+  VKV_CHECK(a.Hq % a.Hkv == 0, "query heads must be a multiple of kv heads");
+  VKV_CHECK(bits == 0 || group == 64, "affine attention supports group_size 64");
+  switch (dtype) {
+    case kF32: attn_dispatch<kF32>(bits, v_dim_major, quant_semantics, a, rows, st); break;
+    case kF16: attn_dispatch<kF16>(bits, v_dim_major, quant_semantics, a, rows, st); break;
+    case kBF16: attn_dispatch<kBF16>(bits, v_dim_major, quant_semantics, a, rows, st); break;
+    default: throw Error("unsupported dtype");
+  }
+  VKV_HIP(hipGetLastError());
+}
+
+}  // namespace vkv

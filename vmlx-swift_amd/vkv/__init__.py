@@ -1,0 +1,568 @@
+"""Python mirror of the vmlx-swift KV-cache surface over libvkv.so (C ABI).
+
+The engine itself is C++/HIP (``csrc/``); this module is a thin ctypes
+binding whose classes keep the reference's names and argument meaning so
+that tests read like the reference's own (``KVCacheSimple``,
+``RotatingKVCache``, ``QuantizedKVCache``, ``PagedCacheManager``,
+``quantized`` / ``dequantized``, ``scaled_dot_product_attention``,
+``quantized_scaled_dot_product_attention``).  Device arrays are torch
+tensors on the HIP device (torch is the allocator and stream provider only).
+
+The library must be built (``make -C vmlx-swift_amd``); importing this
+module without it raises instead of falling back to any CPU path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional, Sequence
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)
+LIB_PATH = os.path.join(PKG, "libvkv.so")
+
+F32, F16, BF16, U32, I32, U8, BOOL = 0, 1, 2, 3, 4, 5, 6
+MASK_NONE, MASK_CAUSAL, MASK_ARRAY = 0, 1, 2
+CACHE_SIMPLE, CACHE_ROTATING, CACHE_QUANTIZED = 0, 1, 2
+VIEW_KEYS_ONLY = 1
+
+
+class VKVError(RuntimeError):
+    pass
+
+
+class Array(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("dtype", C.c_int32), ("ndim", C.c_int32),
+                ("shape", C.c_int64 * 4), ("strides", C.c_int64 * 4)]
+
+
+class PagedView(C.Structure):
+    _fields_ = [("base", C.c_void_p), ("dtype", C.c_int32), ("bits", C.c_int32),
+                ("group_size", C.c_int32), ("n_kv_heads", C.c_int32), ("head_dim", C.c_int32),
+                ("v_head_dim", C.c_int32), ("block_size", C.c_int32), ("flags", C.c_int32),
+                ("block_bytes", C.c_int64), ("head_bytes", C.c_int64),
+                ("block_table", C.c_void_p), ("table_stride", C.c_int32),
+                ("seq_lens", C.c_void_p), ("n_seqs", C.c_int32), ("max_len", C.c_int32)]
+
+
+class CacheParams(C.Structure):
+    _fields_ = [("kind", C.c_int32), ("step", C.c_int32), ("max_size", C.c_int32),
+                ("keep", C.c_int32), ("group_size", C.c_int32), ("bits", C.c_int32)]
+
+
+class PoolParams(C.Structure):
+    _fields_ = [("num_blocks", C.c_int32), ("block_size", C.c_int32), ("n_layers", C.c_int32),
+                ("n_kv_heads", C.c_int32), ("head_dim", C.c_int32), ("v_head_dim", C.c_int32),
+                ("dtype", C.c_int32), ("bits", C.c_int32), ("group_size", C.c_int32),
+                ("flags", C.c_int32)]
+
+
+class PrefixStats(C.Structure):
+    _fields_ = [("total_blocks", C.c_int64), ("allocated_blocks", C.c_int64),
+                ("free_blocks", C.c_int64), ("cache_hits", C.c_int64),
+                ("cache_misses", C.c_int64), ("evictions", C.c_int64)]
+
+
+# Every symbol include/vkv.h declares.
+EXPORTS = (
+    "vkv_last_error", "vkv_abi_version", "vkv_device_count", "vkv_quantize_affine",
+    "vkv_dequantize_affine", "vkv_sdpa", "vkv_quantized_sdpa", "vkv_paged_sdpa",
+    "vkv_mla_decode", "vkv_cache_create", "vkv_cache_destroy", "vkv_cache_copy",
+    "vkv_cache_update", "vkv_cache_update_quantized", "vkv_cache_offset", "vkv_cache_max_size",
+    "vkv_cache_is_trimmable", "vkv_cache_trim", "vkv_cache_capacity", "vkv_cache_state",
+    "vkv_cache_set_state", "vkv_cache_meta_state", "vkv_cache_set_meta_state",
+    "vkv_cache_make_mask", "vkv_cache_to_quantized", "vkv_cache_to_unquantized",
+    "vkv_cache_read_kv", "vkv_pool_create", "vkv_pool_destroy", "vkv_pool_bytes",
+    "vkv_pool_view", "vkv_paged_append", "vkv_paged_gather", "vkv_paged_gather_quantized",
+    "vkv_pool_copy_blocks", "vkv_prefix_create", "vkv_prefix_destroy", "vkv_prefix_allocate",
+    "vkv_prefix_free", "vkv_prefix_release", "vkv_prefix_incref", "vkv_prefix_ref_count", "vkv_prefix_find",
+    "vkv_prefix_register", "vkv_prefix_clear", "vkv_prefix_store", "vkv_prefix_fetch",
+    "vkv_prefix_stats_get", "vkv_prefix_block_tokens", "vkv_block_hash", "vkv_array_copy",
+    "vkv_fill_normal",
+)
+
+_lib = None
+
+
+def lib():
+    """Load libvkv.so (raises when it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise VKVError(f"{LIB_PATH} is missing: build it with `make -C {PKG}`")
+        L = C.CDLL(LIB_PATH)
+        L.vkv_last_error.restype = C.c_char_p
+        for name in EXPORTS:
+            f = getattr(L, name)
+            if name != "vkv_last_error":
+                f.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def _chk(rc):
+    if rc != 0:
+        raise VKVError(lib().vkv_last_error().decode())
+
+
+# ----------------------------------------------------------------- tensors
+def _torch():
+    import torch
+
+    return torch
+
+
+def _dtype_code(t) -> int:
+    torch = _torch()
+    m = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.int32: I32,
+         torch.uint8: U8, torch.bool: BOOL}
+    return m[t.dtype]
+
+
+def arr(t, dtype: Optional[int] = None) -> Array:
+    """vkv_array describing a torch tensor (no copy)."""
+    a = Array()
+    a.data = t.data_ptr() if t.numel() else None
+    a.dtype = _dtype_code(t) if dtype is None else dtype
+    a.ndim = t.dim()
+    for i in range(t.dim()):
+        a.shape[i] = t.shape[i]
+        a.strides[i] = t.stride(i)
+    return a
+
+
+def _torch_dtype(code):
+    torch = _torch()
+    return {F32: torch.float32, F16: torch.float16, BF16: torch.bfloat16, U32: torch.int32,
+            I32: torch.int32, U8: torch.uint8, BOOL: torch.bool}[code]
+
+
+def stream_ptr(stream=None):
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+def to_torch(a: Array, stream=None):
+    """Materialize a library-owned array into a fresh contiguous tensor.
+    u32 arrays come back as int32 tensors with the same bits."""
+    torch = _torch()
+    shape = tuple(a.shape[i] for i in range(a.ndim))
+    out = torch.empty(shape, dtype=_torch_dtype(a.dtype), device="cuda")
+    if out.numel():
+        dst = arr(out, a.dtype)
+        _chk(lib().vkv_array_copy(C.byref(a), C.byref(dst), stream_ptr(stream)))
+    return out
+
+
+# ------------------------------------------------------------------- ops
+def quantized(w, group_size: int = 64, bits: int = 4, stream=None):
+    """mlx `quantized(_:groupSize:bits:)` (Source/MLX/Ops.swift:2368-2391),
+    affine mode: returns (wq int32-as-u32, scales, biases)."""
+    torch = _torch()
+    D = w.shape[-1]
+    wq = torch.empty(w.shape[:-1] + (D * bits // 32,), dtype=torch.int32, device=w.device)
+    sc = torch.empty(w.shape[:-1] + (D // group_size,), dtype=w.dtype, device=w.device)
+    bi = torch.empty_like(sc)
+    a_wq, a_sc, a_bi = arr(wq, U32), arr(sc), arr(bi)
+    _chk(lib().vkv_quantize_affine(C.byref(arr(w)), group_size, bits, C.byref(a_wq),
+                                   C.byref(a_sc), C.byref(a_bi), stream_ptr(stream)))
+    return wq, sc, bi
+
+
+def dequantized(wq, scales, biases, group_size: int = 64, bits: int = 4, stream=None):
+    """mlx `dequantized(...)` (Source/MLX/Ops.swift:1146-1163), affine mode."""
+    torch = _torch()
+    D = wq.shape[-1] * 32 // bits
+    out = torch.empty(wq.shape[:-1] + (D,), dtype=scales.dtype, device=wq.device)
+    a_out = arr(out)
+    _chk(lib().vkv_dequantize_affine(C.byref(arr(wq, U32)), C.byref(arr(scales)),
+                                     C.byref(arr(biases)), group_size, bits, C.byref(a_out),
+                                     stream_ptr(stream)))
+    return out
+
+
+def _mask_args(mask):
+    if mask is None:
+        return MASK_NONE, None
+    if isinstance(mask, str):
+        assert mask == "causal"
+        return MASK_CAUSAL, None
+    return MASK_ARRAY, C.byref(arr(mask))
+
+
+def scaled_dot_product_attention(queries, keys, values, scale: float, mask=None, stream=None):
+    """MLXFast.scaledDotProductAttention (Source/MLX/MLXFast.swift:203-218)."""
+    torch = _torch()
+    B, Hq, L, _ = queries.shape
+    out = torch.empty((B, Hq, L, values.shape[3]), dtype=queries.dtype, device=queries.device)
+    mode, m = _mask_args(mask)
+    a_out = arr(out)
+    _chk(lib().vkv_sdpa(C.byref(arr(queries)), C.byref(arr(keys)), C.byref(arr(values)),
+                        C.c_float(scale), mode, m, C.byref(a_out), stream_ptr(stream)))
+    return out
+
+
+def quantized_scaled_dot_product_attention(queries, quantized_keys, quantized_values,
+                                           scale: float, mask=None, group_size: int = 64,
+                                           bits: int = 8, stream=None):
+    """quantizedScaledDotProductAttention (MLXLMCommon/KVCache.swift:1909-1997)
+    over reference-layout tuples (wq, scales, biases)."""
+    torch = _torch()
+    out = torch.empty_like(queries)
+    (kw, ks, kb), (vw, vs, vb) = quantized_keys, quantized_values
+    mode, m = _mask_args(mask)
+    a_out = arr(out)
+    _chk(lib().vkv_quantized_sdpa(
+        C.byref(arr(queries)), C.byref(arr(kw, U32)), C.byref(arr(ks)), C.byref(arr(kb)),
+        C.byref(arr(vw, U32)), C.byref(arr(vs)), C.byref(arr(vb)), group_size, bits,
+        C.c_float(scale), mode, m, C.byref(a_out), stream_ptr(stream)))
+    return out
+
+
+def paged_attention(queries, view: PagedView, scale: float, stream=None):
+    """Decode attention over paged KV: queries [n_seqs, Hq, D]."""
+    torch = _torch()
+    out = torch.empty((queries.shape[0], queries.shape[1], view.v_head_dim), dtype=queries.dtype,
+                      device=queries.device)
+    a_out = arr(out)
+    _chk(lib().vkv_paged_sdpa(C.byref(arr(queries)), C.byref(view), C.c_float(scale),
+                              C.byref(a_out), stream_ptr(stream)))
+    return out
+
+
+def mla_decode(queries, view: PagedView, scale: float, stream=None):
+    torch = _torch()
+    out = torch.empty((queries.shape[0], queries.shape[1], view.v_head_dim), dtype=queries.dtype,
+                      device=queries.device)
+    a_out = arr(out)
+    _chk(lib().vkv_mla_decode(C.byref(arr(queries)), C.byref(view), C.c_float(scale),
+                              C.byref(a_out), stream_ptr(stream)))
+    return out
+
+
+def fill_normal(t, seed: int, std: float = 1.0, stream=None):
+    _chk(lib().vkv_fill_normal(C.c_void_p(t.data_ptr()), _dtype_code(t), t.numel(),
+                               C.c_uint64(seed), C.c_float(std), stream_ptr(stream)))
+    return t
+
+
+def block_hash(parent_hash: Optional[str], tokens: Sequence[int], model_key: Optional[str] = None,
+               media_salt: Optional[str] = None) -> str:
+    """CacheBlock.computeBlockHash (Cache/CacheBlock.swift:110-146)."""
+    toks = (C.c_int64 * max(1, len(tokens)))(*tokens)
+    out = C.create_string_buffer(65)
+    _chk(lib().vkv_block_hash(
+        parent_hash.encode() if parent_hash is not None else None, toks, len(tokens),
+        model_key.encode() if model_key is not None else None,
+        media_salt.encode() if media_salt is not None else None, out))
+    return out.value.decode()
+
+
+# ------------------------------------------------------------------ caches
+class _Cache:
+    def __init__(self, params: CacheParams, handle=None):
+        self._h = C.c_void_p()
+        if handle is not None:
+            self._h = handle
+        else:
+            _chk(lib().vkv_cache_create(C.byref(params), C.byref(self._h)))
+
+    def __del__(self):
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.vkv_cache_destroy(self._h)
+            self._h = None
+
+    @property
+    def offset(self) -> int:
+        v = C.c_int64()
+        _chk(lib().vkv_cache_offset(self._h, C.byref(v)))
+        return v.value
+
+    @property
+    def max_size(self) -> Optional[int]:
+        v = C.c_int64()
+        _chk(lib().vkv_cache_max_size(self._h, C.byref(v)))
+        return None if v.value < 0 else v.value
+
+    @property
+    def capacity(self) -> int:
+        v = C.c_int64()
+        _chk(lib().vkv_cache_capacity(self._h, C.byref(v)))
+        return v.value
+
+    @property
+    def is_trimmable(self) -> bool:
+        v = C.c_int32()
+        _chk(lib().vkv_cache_is_trimmable(self._h, C.byref(v)))
+        return bool(v.value)
+
+    def trim(self, n: int) -> int:
+        v = C.c_int64()
+        _chk(lib().vkv_cache_trim(self._h, n, C.byref(v)))
+        return v.value
+
+    def update(self, keys, values, stream=None):
+        """update(keys:values:) -> (keys, values) as library-owned views."""
+        ok, ov = Array(), Array()
+        _chk(lib().vkv_cache_update(self._h, C.byref(arr(keys)), C.byref(arr(values)),
+                                    stream_ptr(stream), C.byref(ok), C.byref(ov)))
+        return ok, ov
+
+    def state_views(self, stream=None):
+        arrs = (Array * 6)()
+        n = C.c_int32()
+        _chk(lib().vkv_cache_state(self._h, stream_ptr(stream), arrs, C.byref(n)))
+        return [arrs[i] for i in range(n.value)]
+
+    @property
+    def state(self):
+        """state getter, materialized as torch tensors."""
+        return [to_torch(a) for a in self.state_views()]
+
+    @state.setter
+    def state(self, tensors):
+        kinds = [U32 if (t.dtype == _torch().int32) else None for t in tensors]
+        arrs = (Array * max(1, len(tensors)))(*[arr(t, k) for t, k in zip(tensors, kinds)])
+        _chk(lib().vkv_cache_set_state(self._h, arrs, len(tensors), stream_ptr()))
+
+    @property
+    def meta_state(self):
+        buf = C.create_string_buffer(4096)
+        n = C.c_int32()
+        _chk(lib().vkv_cache_meta_state(self._h, buf, 4096, C.byref(n)))
+        parts = buf.raw.split(b"\0")
+        return [p.decode() for p in parts[: n.value]]
+
+    @meta_state.setter
+    def meta_state(self, strings):
+        arrs = (C.c_char_p * max(1, len(strings)))(*[s.encode() for s in strings])
+        _chk(lib().vkv_cache_set_meta_state(self._h, arrs, len(strings)))
+
+    def make_mask(self, n: int, window_size: Optional[int] = None, return_array: bool = False):
+        """makeMask(n:windowSize:returnArray:) -> ('none'|'causal'|tensor)."""
+        mode = C.c_int32()
+        m = Array()
+        _chk(lib().vkv_cache_make_mask(self._h, n, window_size or 0, int(return_array),
+                                       stream_ptr(), C.byref(mode), C.byref(m)))
+        if mode.value == MASK_NONE:
+            return "none"
+        if mode.value == MASK_CAUSAL:
+            return "causal"
+        return to_torch(m)
+
+    def read_kv(self):
+        k, v = Array(), Array()
+        _chk(lib().vkv_cache_read_kv(self._h, stream_ptr(), C.byref(k), C.byref(v)))
+        return to_torch(k), to_torch(v)
+
+    def copy(self):
+        h = C.c_void_p()
+        _chk(lib().vkv_cache_copy(self._h, stream_ptr(), C.byref(h)))
+        new = object.__new__(type(self))
+        _Cache.__init__(new, None, handle=h)
+        return new
+
+
+class KVCacheSimple(_Cache):
+    """KVCacheSimple (MLXLMCommon/KVCache.swift:452-596)."""
+
+    def __init__(self, step: int = 256):
+        super().__init__(CacheParams(CACHE_SIMPLE, step, 0, 0, 0, 0))
+
+    def to_quantized(self, group_size: int = 64, bits: int = 4):
+        h = C.c_void_p()
+        _chk(lib().vkv_cache_to_quantized(self._h, group_size, bits, stream_ptr(), C.byref(h)))
+        q = object.__new__(QuantizedKVCache)
+        _Cache.__init__(q, None, handle=h)
+        q.group_size, q.bits = group_size, bits
+        return q
+
+
+class RotatingKVCache(_Cache):
+    """RotatingKVCache (MLXLMCommon/KVCache.swift:605-958)."""
+
+    def __init__(self, max_size: int, keep: int = 0, step: int = 256):
+        super().__init__(CacheParams(CACHE_ROTATING, step, max_size, keep, 0, 0))
+
+
+class QuantizedKVCache(_Cache):
+    """QuantizedKVCache (MLXLMCommon/KVCache.swift:961-1221)."""
+
+    def __init__(self, group_size: int = 64, bits: int = 8):
+        super().__init__(CacheParams(CACHE_QUANTIZED, 256, 0, 0, group_size, bits))
+        self.group_size, self.bits = group_size, bits
+
+    def update_quantized(self, keys, values, stream=None) -> PagedView:
+        v = PagedView()
+        _chk(lib().vkv_cache_update_quantized(self._h, C.byref(arr(keys)), C.byref(arr(values)),
+                                              stream_ptr(stream), C.byref(v)))
+        return v
+
+    def to_unquantized(self):
+        h = C.c_void_p()
+        _chk(lib().vkv_cache_to_unquantized(self._h, stream_ptr(), C.byref(h)))
+        s = object.__new__(KVCacheSimple)
+        _Cache.__init__(s, None, handle=h)
+        return s
+
+
+# -------------------------------------------------------------------- pool
+class PagedPool:
+    """Device block pool: [layer][block][kv head] chunks."""
+
+    def __init__(self, num_blocks, block_size, n_layers, n_kv_heads, head_dim, dtype=BF16,
+                 bits=0, group_size=64, v_head_dim=0, flags=0):
+        self.params = PoolParams(num_blocks, block_size, n_layers, n_kv_heads, head_dim,
+                                 v_head_dim, dtype, bits, group_size, flags)
+        self._h = C.c_void_p()
+        _chk(lib().vkv_pool_create(C.byref(self.params), C.byref(self._h)))
+
+    def __del__(self):
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.vkv_pool_destroy(self._h)
+            self._h = None
+
+    @property
+    def nbytes(self) -> int:
+        v = C.c_int64()
+        _chk(lib().vkv_pool_bytes(self._h, C.byref(v)))
+        return v.value
+
+    def view(self, layer, block_table, seq_lens, max_len) -> PagedView:
+        v = PagedView()
+        _chk(lib().vkv_pool_view(self._h, layer, C.c_void_p(block_table.data_ptr()),
+                                 block_table.stride(0),
+                                 C.c_void_p(seq_lens.data_ptr()) if seq_lens is not None else None,
+                                 block_table.shape[0], max_len, C.byref(v)))
+        v._keep = (block_table, seq_lens)
+        return v
+
+    def append(self, layer, keys, values, slot_mapping, stream=None):
+        _chk(lib().vkv_paged_append(self._h, layer, C.byref(arr(keys)),
+                                    C.byref(arr(values)) if values is not None else None,
+                                    C.c_void_p(slot_mapping.data_ptr()), keys.shape[0],
+                                    stream_ptr(stream)))
+
+    def copy_blocks(self, src, dst, stream=None):
+        n = len(src)
+        a = (C.c_int32 * max(1, n))(*src)
+        b = (C.c_int32 * max(1, n))(*dst)
+        _chk(lib().vkv_pool_copy_blocks(self._h, a, b, n, stream_ptr(stream)))
+
+
+def paged_gather(view: PagedView, stream=None):
+    """Dequant-on-read gather -> (keys, values) [n, Hkv, max_len, D]."""
+    torch = _torch()
+    dt = _torch_dtype(view.dtype)
+    k = torch.zeros((view.n_seqs, view.n_kv_heads, view.max_len, view.head_dim), dtype=dt,
+                    device="cuda")
+    keys_only = bool(view.flags & VIEW_KEYS_ONLY)
+    v = None if keys_only else torch.zeros(
+        (view.n_seqs, view.n_kv_heads, view.max_len, view.v_head_dim), dtype=dt, device="cuda")
+    ak = arr(k)
+    av = arr(v) if v is not None else None
+    _chk(lib().vkv_paged_gather(C.byref(view), C.byref(ak), C.byref(av) if av is not None else None,
+                                stream_ptr(stream)))
+    return k, v
+
+
+def paged_gather_quantized(view: PagedView, stream=None):
+    """Raw affine codes in the reference layout: ((wq, s, b), (wq, s, b))."""
+    torch = _torch()
+    dt = _torch_dtype(view.dtype)
+    n, H, T, D = view.n_seqs, view.n_kv_heads, view.max_len, view.head_dim
+    W, G = D * view.bits // 32, D // view.group_size
+    outs = []
+    for _ in range(2):
+        outs += [torch.zeros((n, H, T, W), dtype=torch.int32, device="cuda"),
+                 torch.zeros((n, H, T, G), dtype=dt, device="cuda"),
+                 torch.zeros((n, H, T, G), dtype=dt, device="cuda")]
+    arrs = (Array * 6)(*[arr(t, U32 if i % 3 == 0 else None) for i, t in enumerate(outs)])
+    _chk(lib().vkv_paged_gather_quantized(C.byref(view), arrs, stream_ptr(stream)))
+    return tuple(outs[:3]), tuple(outs[3:])
+
+
+# ------------------------------------------------------------ prefix cache
+class PagedCacheManager:
+    """PagedCacheManager (MLXLMCommon/Cache/PagedCacheManager.swift)."""
+
+    def __init__(self, block_size: int = 64, max_blocks: int = 1000,
+                 model_key: Optional[str] = None, pool: Optional[PagedPool] = None):
+        self.block_size, self.max_blocks = block_size, max_blocks
+        self._pool = pool
+        self._h = C.c_void_p()
+        _chk(lib().vkv_prefix_create(block_size, max_blocks,
+                                     model_key.encode() if model_key is not None else None,
+                                     pool._h if pool is not None else None, C.byref(self._h)))
+
+    def __del__(self):
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.vkv_prefix_destroy(self._h)
+            self._h = None
+
+    def allocate_block(self) -> Optional[int]:
+        b = C.c_int32()
+        _chk(lib().vkv_prefix_allocate(self._h, C.byref(b)))
+        return None if b.value < 0 else b.value
+
+    def free_block(self, block: int):
+        _chk(lib().vkv_prefix_free(self._h, block))
+
+    def release(self, blocks: Sequence[int]):
+        """CacheCoordinator.release(blocks:): leaves first."""
+        a = (C.c_int32 * max(1, len(blocks)))(*blocks)
+        _chk(lib().vkv_prefix_release(self._h, a, len(blocks)))
+
+    def incref(self, block: int):
+        _chk(lib().vkv_prefix_incref(self._h, block))
+
+    def ref_count(self, block: int) -> int:
+        v = C.c_int32()
+        _chk(lib().vkv_prefix_ref_count(self._h, block, C.byref(v)))
+        return v.value
+
+    def token_count(self, block: int) -> int:
+        v = C.c_int32()
+        _chk(lib().vkv_prefix_block_tokens(self._h, block, C.byref(v)))
+        return v.value
+
+    def find_cached_block(self, hash_: str) -> Optional[int]:
+        b = C.c_int32()
+        _chk(lib().vkv_prefix_find(self._h, hash_.encode(), C.byref(b)))
+        return None if b.value < 0 else b.value
+
+    def register_block(self, block: int, hash_: str):
+        _chk(lib().vkv_prefix_register(self._h, block, hash_.encode()))
+
+    def clear(self):
+        _chk(lib().vkv_prefix_clear(self._h))
+
+    def store_token_sequence(self, tokens: Sequence[int], n_data_chunks: int,
+                             src_blocks: Optional[Sequence[int]] = None,
+                             media_salt: Optional[str] = None, stream=None):
+        toks = (C.c_int64 * max(1, len(tokens)))(*tokens)
+        src = (C.c_int32 * max(1, len(src_blocks)))(*src_blocks) if src_blocks else None
+        _chk(lib().vkv_prefix_store(self._h, toks, len(tokens),
+                                    media_salt.encode() if media_salt is not None else None,
+                                    n_data_chunks, src,
+                                    stream_ptr(stream) if self._pool is not None else None))
+
+    def fetch_prefix(self, tokens: Sequence[int], media_salt: Optional[str] = None):
+        """-> None or (matched_tokens, remaining_tokens, blocks)."""
+        toks = (C.c_int64 * max(1, len(tokens)))(*tokens)
+        cap = len(tokens) + 1
+        blocks = (C.c_int32 * cap)()
+        nb, matched = C.c_int32(), C.c_int64()
+        _chk(lib().vkv_prefix_fetch(self._h, toks, len(tokens),
+                                    media_salt.encode() if media_salt is not None else None,
+                                    blocks, cap, C.byref(nb), C.byref(matched)))
+        if nb.value == 0:
+            return None
+        return matched.value, list(tokens[matched.value:]), [blocks[i] for i in range(nb.value)]
+
+    @property
+    def stats(self) -> dict:
+        s = PrefixStats()
+        _chk(lib().vkv_prefix_stats_get(self._h, C.byref(s)))
+        return {f: getattr(s, f) for f, _ in PrefixStats._fields_}
