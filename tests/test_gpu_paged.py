@@ -164,3 +164,42 @@ def test_prefix_store_fetch_copies_device_blocks():
     rq = O.quantize(np.ascontiguousarray(P.tokens[0].transpose(1, 0, 2)), dtype, 64, bits)[0]
     assert np.array_equal(host(kq[0]), rq)
     P.mgr.release(blocks)
+
+
+@pytest.mark.parametrize("bits,D,rep,bs,Hkv", [(4, 128, 4, 32, 8), (4, 64, 1, 64, 2), (8, 128, 2, 32, 4),
+                                               (4, 128, 8, 64, 2), (8, 64, 16, 32, 1), (4, 128, 3, 32, 2)])
+def test_paged_decode_shapes_and_partitions(bits, D, rep, bs, Hkv):
+    """The matrix-core decode path across GQA factors, head dims, pool
+    block sizes (sub-blocks of 32) and sequences long enough to be split
+    into several partitions, against the oracle."""
+    dtype = O.BF16
+    rng = np.random.default_rng(bits * 1000 + D + rep * 7 + bs)
+    lens = [5000, 31, 32, 33, 700, 0 + 1]
+    nblocks = sum((L + bs - 1) // bs + 1 for L in lens) + 4
+    P = Paged(rng, bits, dtype, bs=bs, Hkv=Hkv, D=D, nblocks=nblocks, n_share=0, lens=lens)
+    P.append_all()
+    view = P.view()
+    Hq = Hkv * rep
+    q = rand_bits(rng, (len(lens), Hq, D), dtype)
+    out = values(vkv.paged_attention(dev(q, dtype), view, D ** -0.5), dtype)
+    f = lambda a: O.to_f32(a, dtype)
+    for s, L in enumerate(lens):
+        rk = O.quantize(np.ascontiguousarray(P.tokens[s].transpose(1, 0, 2)), dtype, 64, bits)
+        rv = O.quantize(np.ascontiguousarray(P.vals[s].transpose(1, 0, 2)), dtype, 64, bits)
+        ref = O.quantized_sdpa(f(q[s])[None, :, None], dtype, rk[0][None], f(rk[1])[None],
+                               f(rk[2])[None], rv[0][None], f(rv[1])[None], f(rv[2])[None],
+                               D ** -0.5, 64, bits)[0, :, 0]
+        assert (np.abs(out[s] - ref) <= attn_tol(dtype, ref)).all(), s
+
+
+def test_generic_and_matrix_core_paths_agree(monkeypatch):
+    dtype, bits = O.BF16, 4
+    rng = np.random.default_rng(77)
+    P = Paged(rng, bits, dtype, n_seqs=5)
+    P.append_all()
+    view = P.view()
+    q = dev(rand_bits(rng, (len(P.lens), 32, 128), dtype), dtype)
+    fast = values(vkv.paged_attention(q, view, 0.088), dtype)
+    monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
+    slow = values(vkv.paged_attention(q, view, 0.088), dtype)
+    assert np.abs(fast - slow).max() <= 2e-2

@@ -5,6 +5,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <string>
 #include <vector>
 
@@ -73,7 +74,7 @@ int32_t choose_parts(int64_t rows_x_heads, int64_t max_len, int32_t* part_tokens
   return static_cast<int32_t>(std::max<int64_t>(1, (max_len + pt - 1) / pt));
 }
 
-void run_attention(int dtype, int bits, int group, bool vdm, bool qsem, AttnArgs& a, int64_t rows,
+void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64_t rows,
                    int64_t max_len, hipStream_t st) {
   a.n_parts = choose_parts(rows * a.Hkv, max_len, &a.part_tokens);
   if (a.n_parts > 1) {
@@ -82,7 +83,7 @@ void run_attention(int dtype, int bits, int group, bool vdm, bool qsem, AttnArgs
     a.ws_o = ws;
     a.ws_ml = ws + per * a.Dv;
   }
-  launch_attention(dtype, bits, group, vdm, qsem, a, rows, st);
+  launch_attention(dtype, bits, group, qsem, a, rows, st);
 }
 
 }  // namespace
@@ -218,7 +219,7 @@ int vkv_sdpa(const vkv_array* q, const vkv_array* k, const vkv_array* v, float s
     } else if (mask_mode != VKV_MASK_NONE) {
       throw Error("unknown mask mode");
     }
-    run_attention(q->dtype, 0, 64, false, false, a, B * L, T, S(stream));
+    run_attention(q->dtype, 0, 64, false, a, B * L, T, S(stream));
   });
 }
 
@@ -290,7 +291,7 @@ int vkv_quantized_sdpa(const vkv_array* q, const vkv_array* k_wq, const vkv_arra
     } else if (mask_mode != VKV_MASK_NONE) {
       throw Error("unknown mask mode");
     }
-    run_attention(q->dtype, bits, group_size, false, true, a, B * L, T, S(stream));
+    run_attention(q->dtype, bits, group_size, true, a, B * L, T, S(stream));
   });
 }
 
@@ -308,6 +309,51 @@ int vkv_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vk
       throw Error("q/out shapes do not match the view");
     if (q->shape[1] % kv->n_kv_heads) throw Error("query heads must be a multiple of kv heads");
     if (!kv->block_table) throw Error("view has no block table");
+    const bool keys_only = (kv->flags & VKV_VIEW_KEYS_ONLY) != 0;
+    const int rep = static_cast<int>(q->shape[1] / kv->n_kv_heads);
+    if (kv->bits > 0 && !keys_only && !getenv("VKV_GENERIC_ATTENTION") &&
+        qdecode_supported(kv->dtype, kv->bits, kv->head_dim, kv->block_size, rep, kv->group_size)) {
+      // matrix-core path (vkv_decode.hip)
+      KVSrc src = kvsrc_from_view(*kv);
+      DecodeArgs d{};
+      d.q = static_cast<const uint16_t*>(q->data);
+      d.q_ss = q->strides[0];
+      d.q_sh = q->strides[1];
+      d.out = static_cast<uint16_t*>(out->data);
+      d.o_ss = out->strides[0];
+      d.o_sh = out->strides[1];
+      d.scale = scale;
+      d.base = src.base;
+      d.block_bytes = src.block_bytes;
+      d.head_bytes = src.head_bytes;
+      d.kc_off = src.kc_off;
+      d.vc_off = src.vc_off;
+      d.sb_off = src.sb_off;
+      d.table = kv->block_table;
+      d.table_stride = kv->table_stride;
+      d.block_size = kv->block_size;
+      d.seq_lens = kv->seq_lens;
+      d.max_len = kv->max_len;
+      d.Hq = static_cast<int32_t>(q->shape[1]);
+      d.Hkv = kv->n_kv_heads;
+      d.rep = rep;
+      // partitions of 32-token blocks: aim for >= 2048 busy workgroups, at
+      // most 16 blocks (4 per wave) per workgroup
+      const int64_t max_blocks = (static_cast<int64_t>(kv->max_len) + 31) / 32;
+      const int64_t units = max_blocks * kv->n_kv_heads * kv->n_seqs;
+      int64_t pb = (units + 2047) / 2048;
+      pb = std::min<int64_t>(16, std::max<int64_t>(4, (pb + 3) / 4 * 4));
+      d.part_blocks = static_cast<int32_t>(pb);
+      d.n_parts = static_cast<int32_t>(std::max<int64_t>(1, (max_blocks + pb - 1) / pb));
+      if (d.n_parts > 1) {
+        const size_t per = static_cast<size_t>(kv->n_seqs) * d.Hq * d.n_parts;
+        float* ws = attention_workspace(S(stream), per * (kv->head_dim + 2));
+        d.ws_o = ws;
+        d.ws_ml = ws + per * kv->head_dim;
+      }
+      launch_qdecode(d, kv->bits, kv->head_dim, kv->n_seqs, S(stream));
+      return;
+    }
     AttnArgs a{};
     a.q = q->data;
     a.q_sb = q->strides[0];
@@ -324,9 +370,8 @@ int vkv_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vk
     a.o_sb = out->strides[0];
     a.o_sh = out->strides[1];
     a.o_sl = 0;
-    const bool keys_only = (kv->flags & VKV_VIEW_KEYS_ONLY) != 0;
-    run_attention(kv->dtype, kv->bits, kv->group_size, kv->bits > 0 && !keys_only, kv->bits > 0, a,
-                  kv->n_seqs, kv->max_len, S(stream));
+    run_attention(kv->dtype, kv->bits, kv->group_size, kv->bits > 0, a, kv->n_seqs, kv->max_len,
+                  S(stream));
   });
 }
 
@@ -640,7 +685,6 @@ int vkv_paged_gather_quantized(const vkv_paged_view* kv, vkv_array* out, void* s
       g.out = o[0].data;
       g.out_s = o[1].data;
       g.out_b = o[2].data;
-      if (keys_only) g.kv.v_dim_stride = 0;
       launch_gather(g, 1, S(stream));
     }
   });

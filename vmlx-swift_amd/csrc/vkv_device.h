@@ -60,6 +60,59 @@ __device__ __forceinline__ float round_to(float f) {
   return Elem<DT>::to_f32(Elem<DT>::from_f32(f));
 }
 
+// ---------------------------------------------------------------------------
+// Affine paged chunk format (block_size % 32 == 0, head_dim % 32 == 0).
+// One (block, kv head) chunk holds K codes, V codes, then the scale/bias
+// area.  The word orders are chosen so that each lane of the decode kernel
+// reads its MFMA operands with one contiguous 16-byte load:
+//  * K codes are token-major (a row of D*bits/32 words per token).  Within a
+//    row, original word w (the reference's little-endian packing: element i
+//    of the row lives in word i*bits/32) is stored at position
+//      4-bit: kg*(D/32) + s            with s = w / 4, kg = w % 4
+//      8-bit: (kg*(D/32) + s)*2 + h    with q = w / 2, s = q / 4, kg = q % 4,
+//                                      h = w % 2
+//    i.e. the words one MFMA lane group (kg) needs for every 32-dim K step
+//    (s) are adjacent.
+//  * V codes are dim-major per 32-token sub-block: the 8 tokens
+//    8*kg .. 8*kg+7 of dim d = 16*mt + m share one word (4-bit; two words
+//    for 8-bit) at
+//      4-bit: (kg*16 + m)*(D/16) + mt
+//      8-bit: ((kg*16 + m)*(D/16) + mt)*2 + (q/4)
+//    token 8*kg + q sits at bit bits*(q % (32/bits)) of its word.
+//  * scale/bias: per token 4*G values (2*G when keys-only) of the element
+//    dtype: [K: (scale, bias) x G][V: (scale, bias) x G].
+__device__ __forceinline__ int64_t qk_word_off(int64_t t, int w, int D, int bits) {
+  const int row_words = D * bits / 32;
+  int idx;
+  if (bits == 4) {
+    idx = (w & 3) * (D / 32) + (w >> 2);
+  } else {
+    const int q = w >> 1;
+    idx = ((q & 3) * (D / 32) + (q >> 2)) * 2 + (w & 1);
+  }
+  return (t * row_words + idx) * 4;
+}
+
+__device__ __forceinline__ int64_t qv_word_off(int64_t t, int d, int D, int bits, int* shift) {
+  const int64_t sb = t >> 5;
+  const int tt = static_cast<int>(t & 31);
+  const int kg = tt >> 3, q = tt & 7, m = d & 15, mt = d >> 4, NT = D >> 4;
+  int64_t idx = sb * static_cast<int64_t>(D) * bits;
+  if (bits == 4) {
+    idx += (kg * 16 + m) * NT + mt;
+    *shift = 4 * q;
+  } else {
+    idx += ((kg * 16 + m) * NT + mt) * 2 + (q >> 2);
+    *shift = 8 * (q & 3);
+  }
+  return idx * 4;
+}
+
+__device__ __forceinline__ int64_t qsb_index(int64_t t, int which, int g, int sel, int G,
+                                             bool keys_only) {
+  return t * (keys_only ? 2 * G : 4 * G) + which * 2 * G + g * 2 + sel;
+}
+
 __device__ __forceinline__ float wave_max(float v, int width) {
   for (int o = width / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, width));
   return v;

@@ -230,15 +230,8 @@ std::unique_ptr<Cache> SimpleCache::to_quantized(int group, int bits, hipStream_
       RowSrc src{a.data, a.shape[0], a.shape[2], a.shape[1], a.strides[0], a.strides[2], a.strides[1]};
       ChunkLayout L = chunk_layout(bits, a.dtype, QuantizedCache::kBlock, static_cast<int>(q->D_),
                                    static_cast<int>(q->D_), group, false);
-      RowDst dst{};
-      dst.base = q->store_.bytes();
-      dst.block_bytes = q->block_bytes_;
-      dst.head_bytes = q->head_bytes_;
-      dst.block_size = QuantizedCache::kBlock;
-      dst.is_v = which;
-      dst.c_off = which ? L.vc : L.kc;
-      dst.s_off = which ? L.vs : L.ks;
-      dst.b_off = which ? L.vb : L.kb;
+      RowDst dst = affine_dst(q->store_.bytes(), q->block_bytes_, q->head_bytes_,
+                              QuantizedCache::kBlock, L, which, static_cast<int>(q->D_) / group, false);
       dst.table = static_cast<const int32_t*>(q->table_.get());
       dst.table_stride = static_cast<int32_t>(q->nblk_);
       dst.seq_S = static_cast<int32_t>(offset);
@@ -496,27 +489,32 @@ ChunkLayout chunk_layout(int bits, int dtype, int block_size, int D, int Dv, int
     L.vc = static_cast<int32_t>(L.codes);
     L.head = L.codes + static_cast<int64_t>(block_size) * Dv * es;
   } else {
+    // K codes | V codes | per-token scale/bias (format in vkv_device.h)
+    const int G = D / group;
     L.codes = static_cast<int64_t>(block_size) * D * bits / 8;
-    L.sb = static_cast<int64_t>(block_size) * (D / group) * es;
+    L.sb = static_cast<int64_t>(block_size) * (keys_only ? 2 * G : 4 * G) * es;
     L.kc = 0;
-    if (keys_only) {
-      L.ks = static_cast<int32_t>(L.codes);
-      L.kb = static_cast<int32_t>(L.codes + L.sb);
-      L.vc = L.kc;
-      L.vs = L.ks;
-      L.vb = L.kb;
-      L.head = L.codes + 2 * L.sb;
-    } else {
-      L.vc = static_cast<int32_t>(L.codes);
-      L.ks = static_cast<int32_t>(2 * L.codes);
-      L.kb = static_cast<int32_t>(2 * L.codes + L.sb);
-      L.vs = static_cast<int32_t>(2 * L.codes + 2 * L.sb);
-      L.vb = static_cast<int32_t>(2 * L.codes + 3 * L.sb);
-      L.head = 2 * L.codes + 4 * L.sb;
-    }
+    L.vc = keys_only ? 0 : static_cast<int32_t>(L.codes);
+    L.sbo = static_cast<int32_t>(keys_only ? L.codes : 2 * L.codes);
+    L.head = L.sbo + L.sb;
   }
   L.head = (L.head + 127) / 128 * 128;  // keep every chunk 128-byte aligned
   return L;
+}
+
+RowDst affine_dst(uint8_t* base, int64_t block_bytes, int64_t head_bytes, int block_size,
+                  const ChunkLayout& L, int which, int G, bool keys_only) {
+  RowDst d{};
+  d.base = base;
+  d.block_bytes = block_bytes;
+  d.head_bytes = head_bytes;
+  d.block_size = block_size;
+  d.is_v = which;
+  d.c_off = which ? L.vc : L.kc;
+  d.s_off = L.sbo;
+  d.G = G;
+  d.keys_only = keys_only ? 1 : 0;
+  return d;
 }
 
 void QuantizedCache::reserve(int64_t B, int64_t H, int64_t D, int64_t cap, int dtype,
@@ -602,15 +600,8 @@ void QuantizedCache::update_quantized(const vkv_array& k, const vkv_array& v, hi
   for (int which = 0; which < 2; which++) {
     const vkv_array& a = *arr[which];
     RowSrc src{a.data, a.shape[0], a.shape[2], a.shape[1], a.strides[0], a.strides[2], a.strides[1]};
-    RowDst dst{};
-    dst.base = store_.bytes();
-    dst.block_bytes = block_bytes_;
-    dst.head_bytes = head_bytes_;
-    dst.block_size = kBlock;
-    dst.is_v = which;
-    dst.c_off = which ? L.vc : L.kc;
-    dst.s_off = which ? L.vs : L.ks;
-    dst.b_off = which ? L.vb : L.kb;
+    RowDst dst = affine_dst(store_.bytes(), block_bytes_, head_bytes_, kBlock, L, which,
+                            static_cast<int>(D_ / group_), false);
     dst.table = static_cast<const int32_t*>(table_.get());
     dst.table_stride = static_cast<int32_t>(nblk_);
     dst.seq_S = static_cast<int32_t>(Sn);
@@ -712,13 +703,8 @@ void QuantizedCache::set_state(const vkv_array* a, int count, hipStream_t st) {
     s.group = group_;
     s.dtype = dtype_;
     s.is_v = which;
-    s.dst.base = store_.bytes();
-    s.dst.block_bytes = block_bytes_;
-    s.dst.head_bytes = head_bytes_;
-    s.dst.block_size = kBlock;
-    s.dst.c_off = which ? L.vc : L.kc;
-    s.dst.s_off = which ? L.vs : L.ks;
-    s.dst.b_off = which ? L.vb : L.kb;
+    s.dst = affine_dst(store_.bytes(), block_bytes_, head_bytes_, kBlock, L, which,
+                       static_cast<int>(D_ / group_), false);
     s.dst.table = static_cast<const int32_t*>(table_.get());
     s.dst.table_stride = static_cast<int32_t>(nblk_);
     launch_scatter_codes(s, st);
@@ -804,21 +790,13 @@ Pool::Pool(const vkv_pool_params& pp) : p(pp) {
     if (p.bits != 4 && p.bits != 8) throw Error("bits must be 0, 4 or 8");
     if (p.head_dim % p.group_size || (!keys_only && p.v_head_dim != p.head_dim))
       throw Error("affine pools need head_dim % group_size == 0 and equal K/V dims");
-    if (p.block_size % 8) throw Error("affine pools need block_size % 8 == 0");
+    if (p.block_size % 32 || p.head_dim % 32)
+      throw Error("affine pools need block_size and head_dim multiples of 32");
   }
   if (p.dtype != VKV_F16 && p.dtype != VKV_BF16 && p.dtype != VKV_F32)
     throw Error("pool dtype must be f16, bf16 or f32");
-  ChunkLayout L = chunk_layout(p.bits, p.dtype, p.block_size, p.head_dim, p.v_head_dim, p.group_size,
-                               keys_only);
-  codes_bytes = L.codes;
-  sb_bytes = L.sb;
+  L = chunk_layout(p.bits, p.dtype, p.block_size, p.head_dim, p.v_head_dim, p.group_size, keys_only);
   head_bytes = L.head;
-  kc_off = L.kc;
-  vc_off = L.vc;
-  ks_off = L.ks;
-  kb_off = L.kb;
-  vs_off = L.vs;
-  vb_off = L.vb;
   block_bytes = head_bytes * p.n_kv_heads;
   layer_bytes = block_bytes * p.num_blocks;
   mem.alloc(static_cast<size_t>(layer_bytes * p.n_layers));
@@ -873,20 +851,12 @@ void Pool::append(int layer, const vkv_array& k, const vkv_array* v, const int32
   for (int which = 0; which < passes; which++) {
     const vkv_array& a = which ? *v : k;
     RowSrc src{a.data, 1, n, a.shape[1], 0, a.strides[0], a.strides[1]};
-    RowDst dst{};
-    dst.base = base;
-    dst.block_bytes = block_bytes;
-    dst.head_bytes = head_bytes;
-    dst.block_size = p.block_size;
-    dst.is_v = which;
+    RowDst dst = affine_dst(base, block_bytes, head_bytes, p.block_size, L, which,
+                            p.bits ? p.head_dim / p.group_size : 0, keys_only);
     dst.slots = slots;
     if (p.bits == 0) {
-      dst.c_off = which ? vc_off : kc_off;
       launch_copy_rows(p.dtype, 1, src, dst, n * a.shape[1], static_cast<int>(a.shape[2]), st);
     } else {
-      dst.c_off = which ? vc_off : kc_off;
-      dst.s_off = which ? vs_off : ks_off;
-      dst.b_off = which ? vb_off : kb_off;
       launch_quantize_rows(p.dtype, p.bits, p.group_size, 1, src, dst, n * a.shape[1],
                            static_cast<int>(a.shape[2]), st);
     }
@@ -906,21 +876,17 @@ KVSrc kvsrc_from_view(const vkv_paged_view& v) {
     s.kc = Comp{base + L.kc, BB, HB, static_cast<int64_t>(v.head_dim) * es};
     s.vc = Comp{base + L.vc, BB, HB, static_cast<int64_t>(v.v_head_dim) * es};
   } else {
-    const int G = v.head_dim / v.group_size;
-    s.kc = Comp{base + L.kc, BB, HB, static_cast<int64_t>(v.head_dim) * v.bits / 8};
-    s.ks = Comp{base + L.ks, BB, HB, static_cast<int64_t>(G) * es};
-    s.kb = Comp{base + L.kb, BB, HB, static_cast<int64_t>(G) * es};
-    if (keys_only) {
-      s.vc = s.kc;
-      s.vs = s.ks;
-      s.vb = s.kb;
-      s.v_dim_stride = 0;
-    } else {
-      s.vc = Comp{base + L.vc, BB, HB, 0};
-      s.vs = Comp{base + L.vs, BB, HB, static_cast<int64_t>(G) * es};
-      s.vb = Comp{base + L.vb, BB, HB, static_cast<int64_t>(G) * es};
-      s.v_dim_stride = static_cast<int64_t>(v.block_size) * v.bits / 8;
-    }
+    if (v.block_size % 32 || v.head_dim % 32) throw Error("affine views need block_size and head_dim multiples of 32");
+    s.qfmt = 1;
+    s.base = base;
+    s.block_bytes = BB;
+    s.head_bytes = HB;
+    s.kc_off = L.kc;
+    s.vc_off = L.vc;
+    s.sb_off = L.sbo;
+    s.G = v.head_dim / v.group_size;
+    s.keys_only = keys_only ? 1 : 0;
+    s.D = v.head_dim;
   }
   s.table = v.block_table;
   s.table_stride = v.table_stride;

@@ -68,6 +68,17 @@ struct Dense4 {
   vkv_array view(int64_t len) const;  // [B,H,len,D] over [.., cap, ..]
 };
 
+// Chunk layout shared by the pool and the quantized cache: byte sizes of one
+// matrix's codes (or float values) and of the scale/bias area, the chunk
+// size, and the offsets of K, V and the scale/bias area.
+struct ChunkLayout {
+  int64_t codes, sb, head;
+  int32_t kc, vc, sbo;
+};
+// A paged affine destination for K (which 0) or V (which 1) rows.
+RowDst affine_dst(uint8_t* base, int64_t block_bytes, int64_t head_bytes, int block_size,
+                  const ChunkLayout& L, int which, int G, bool keys_only);
+
 // Base of the per-layer caches (protocol KVCache, KVCache.swift:38-77).
 class Cache {
  public:
@@ -188,8 +199,8 @@ class Pool {
  public:
   explicit Pool(const vkv_pool_params& p);
   vkv_pool_params p;
-  int64_t codes_bytes = 0, sb_bytes = 0, head_bytes = 0, block_bytes = 0, layer_bytes = 0;
-  int32_t kc_off = 0, vc_off = 0, ks_off = 0, kb_off = 0, vs_off = 0, vb_off = 0;
+  int64_t head_bytes = 0, block_bytes = 0, layer_bytes = 0;
+  ChunkLayout L{};
   DevBuf mem;
   vkv_paged_view view(int layer, const int32_t* table, int32_t stride, const int32_t* lens,
                       int32_t n, int32_t max_len) const;
@@ -197,11 +208,6 @@ class Pool {
               hipStream_t st);
 };
 
-// Chunk layout shared by the pool and the quantized cache.
-struct ChunkLayout {
-  int64_t codes, sb, head;
-  int32_t kc, vc, ks, kb, vs, vb;
-};
 ChunkLayout chunk_layout(int bits, int dtype, int block_size, int D, int Dv, int group,
                          bool keys_only);
 

@@ -47,8 +47,11 @@ struct RowDst {
   uint8_t* base;
   int64_t block_bytes, head_bytes;
   int32_t block_size;
-  int32_t is_v;              // V rows: dim-major codes
-  int32_t c_off, s_off, b_off;  // codes / scales / biases offsets in a chunk
+  int32_t is_v;              // V rows (affine: dim-major codes)
+  int32_t c_off;             // codes (or float values) of this matrix in a chunk
+  int32_t s_off;             // affine: scale/bias area of the chunk
+  int32_t G;                 // affine: groups per row
+  int32_t keys_only;         // affine: chunk holds keys only (MLA latent)
   // slot of token n (n = row / e2 for paged rows ordered (token, head)):
   const int32_t* slots;      // explicit [N] (slot = block*bs + offset), or
   const int32_t* table;      // block table [e0][table_stride] with
@@ -65,13 +68,19 @@ struct Comp {
 };
 
 struct KVSrc {
-  Comp kc, ks, kb, vc, vs, vb;
+  Comp kc, ks, kb, vc, vs, vb;  // dense layouts and float blocks
   const int32_t* table;   // nullptr = dense
   int32_t table_stride;
   int32_t block_size;
-  int64_t v_dim_stride;   // dim-major V codes: bytes between dim rows
   const int32_t* seq_lens;  // nullptr = every row has T tokens
   int32_t T;
+  // Affine paged chunks (qfmt != 0): chunk = base + block*block_bytes +
+  // head*head_bytes, codes/scale-bias addressed by the chunk format.
+  int32_t qfmt;
+  const uint8_t* base;
+  int64_t block_bytes, head_bytes;
+  int32_t kc_off, vc_off, sb_off;
+  int32_t G, keys_only, D;
 };
 
 struct AttnArgs {
@@ -113,8 +122,31 @@ void launch_copy4d(int esize, const void* src, const int64_t* shape, const int64
                    void* dst, const int64_t* dstr, hipStream_t st);
 void launch_fill_normal(int dtype, void* data, int64_t n, uint64_t seed, float std,
                         hipStream_t st);
-void launch_attention(int dtype, int bits, int group, bool v_dim_major, bool quant_semantics,
+void launch_attention(int dtype, int bits, int group, bool quant_semantics,
                       const AttnArgs& a, int64_t rows, hipStream_t st);
+// MFMA decode attention over paged affine bf16 KV (vkv_decode.hip).
+struct DecodeArgs {
+  const uint16_t* q;         // [n_seqs][Hq][D] bf16
+  int64_t q_ss, q_sh;        // element strides
+  uint16_t* out;             // [n_seqs][Hq][D] bf16
+  int64_t o_ss, o_sh;
+  float scale;
+  const uint8_t* base;       // layer base of the chunk pool
+  int64_t block_bytes, head_bytes;
+  int32_t kc_off, vc_off, sb_off;
+  const int32_t* table;
+  int32_t table_stride;
+  int32_t block_size;        // tokens per pool block (a multiple of 32)
+  const int32_t* seq_lens;   // nullptr = every sequence holds max_len tokens
+  int32_t max_len;
+  int32_t Hq, Hkv, rep;
+  int32_t part_blocks, n_parts;
+  float* ws_o;               // [n_seqs][Hq][n_parts][D]
+  float* ws_ml;              // [n_seqs][Hq][n_parts][2]
+};
+bool qdecode_supported(int dtype, int bits, int D, int block_size, int rep, int group);
+void launch_qdecode(const DecodeArgs& a, int bits, int D, int n_seqs, hipStream_t st);
+
 // Block pairs passed by value to the block-copy kernel.
 struct BlockPairs {
   static constexpr int kMax = 256;

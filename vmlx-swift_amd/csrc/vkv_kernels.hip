@@ -42,6 +42,42 @@ __device__ __forceinline__ void load8(const uint8_t* p, float* v) {
   for (int i = 0; i < 8; i++) v[i] = E::load(q + i);
 }
 
+// Store the 8 codes of dims [8j, 8j+8) of token `tib` into a paged chunk
+// (format in vkv_device.h).  V codes of one word belong to 8 different
+// tokens, so a 4-bit V store is a read-modify-write done with two atomics on
+// the containing word (other tokens' nibbles may be written concurrently).
+template <int BITS>
+__device__ __forceinline__ void store_chunk_codes(uint8_t* chunk, const RowDst& dst, int tib, int j,
+                                                  int D, const uint32_t* code) {
+  uint8_t* c = chunk + dst.c_off;
+  if (!dst.is_v) {
+    if constexpr (BITS == 4) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int i = 0; i < 8; i++) w |= code[i] << (4 * i);
+      *reinterpret_cast<uint32_t*>(c + qk_word_off(tib, j, D, 4)) = w;
+    } else {
+      const uint32_t w0 = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
+      const uint32_t w1 = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
+      *reinterpret_cast<uint32_t*>(c + qk_word_off(tib, 2 * j, D, 8)) = w0;
+      *reinterpret_cast<uint32_t*>(c + qk_word_off(tib, 2 * j + 1, D, 8)) = w1;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      int sh;
+      const int64_t off = qv_word_off(tib, j * 8 + i, D, BITS, &sh);
+      if constexpr (BITS == 8) {
+        c[off + sh / 8] = static_cast<uint8_t>(code[i]);
+      } else {
+        uint32_t* word = reinterpret_cast<uint32_t*>(c + off);
+        atomicAnd(word, ~(0xFu << sh));
+        atomicOr(word, code[i] << sh);
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------- affine quantize
 //
 // One thread owns 8 consecutive values of a row; GROUP/8 neighbouring lanes
@@ -133,40 +169,11 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(RowSrc src, RowDst d
     const int64_t blk = slot / dst.block_size;
     const int tib = static_cast<int>(slot % dst.block_size);
     uint8_t* chunk = dst.base + blk * dst.block_bytes + h * dst.head_bytes;
-    if (!dst.is_v) {
-      uint8_t* c = chunk + dst.c_off + static_cast<int64_t>(tib) * (D * BITS / 8);
-      if constexpr (BITS == 4) {
-        uint32_t w = 0;
-#pragma unroll
-        for (int i = 0; i < 8; i++) w |= code[i] << (4 * i);
-        reinterpret_cast<uint32_t*>(c)[j] = w;
-      } else {
-        uint32_t w0 = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
-        uint32_t w1 = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
-        reinterpret_cast<uint32_t*>(c)[2 * j] = w0;
-        reinterpret_cast<uint32_t*>(c)[2 * j + 1] = w1;
-      }
-    } else {
-      // dim-major: dim d's row holds block_size codes, token tib at bit
-      // position tib*BITS of the row (little-endian words).
-      const int64_t row_bytes = static_cast<int64_t>(dst.block_size) * BITS / 8;
-      uint8_t* c = chunk + dst.c_off;
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const int d = j * 8 + i;
-        if constexpr (BITS == 8) {
-          c[d * row_bytes + tib] = static_cast<uint8_t>(code[i]);
-        } else {
-          uint32_t* word = reinterpret_cast<uint32_t*>(c + d * row_bytes) + tib / 8;
-          const int sh = 4 * (tib % 8);
-          atomicAnd(word, ~(0xFu << sh));
-          atomicOr(word, code[i] << sh);
-        }
-      }
-    }
+    store_chunk_codes<BITS>(chunk, dst, tib, j, D, code);
     if (group_leader) {
-      reinterpret_cast<typename E::T*>(chunk + dst.s_off)[tib * G + g] = s_t;
-      reinterpret_cast<typename E::T*>(chunk + dst.b_off)[tib * G + g] = b_t;
+      typename E::T* sbp = reinterpret_cast<typename E::T*>(chunk + dst.s_off);
+      sbp[qsb_index(tib, dst.is_v, g, 0, dst.G, dst.keys_only)] = s_t;
+      sbp[qsb_index(tib, dst.is_v, g, 1, dst.G, dst.keys_only)] = b_t;
     }
   }
 }
@@ -268,38 +275,52 @@ __device__ __forceinline__ uint32_t code_tm(const uint8_t* row, int d) {
   return (row[d >> 1] >> (4 * (d & 1))) & 15u;
 }
 
-// Key element (token at l, dim d) as float.
+// Raw affine code of element d of the token at `l` (which: 0 = K, 1 = V)
+// with its stored scale and bias, for either the paged chunk format or the
+// reference layout.  Values of a keys-only (MLA) chunk are its key entries.
 template <int DT, int BITS>
-__device__ __forceinline__ float key_at(const KVSrc& kv, const TokLoc& l, int64_t h, int d,
-                                        int group) {
+__device__ __forceinline__ uint32_t qcode(const KVSrc& kv, const TokLoc& l, int64_t h, int d,
+                                          int which, int group, float* s, float* b) {
   using E = Elem<DT>;
-  if constexpr (BITS == 0) {
-    return E::load(reinterpret_cast<const typename E::T*>(at(kv.kc, l, h)) + d);
-  } else {
-    const int g = d / group;
-    const float s = E::load(reinterpret_cast<const typename E::T*>(at(kv.ks, l, h)) + g);
-    const float b = E::load(reinterpret_cast<const typename E::T*>(at(kv.kb, l, h)) + g);
-    return fmaf(s, static_cast<float>(code_tm<BITS>(at(kv.kc, l, h), d)), b);
+  const int g = d / group;
+  if (kv.qfmt) {
+    const uint8_t* chunk = kv.base + l.blk * kv.block_bytes + h * kv.head_bytes;
+    const typename E::T* sb = reinterpret_cast<const typename E::T*>(chunk + kv.sb_off);
+    const bool ko = kv.keys_only != 0;
+    const int w = (which && !ko) ? 1 : 0;
+    *s = E::load(sb + qsb_index(l.tib, w, g, 0, kv.G, ko));
+    *b = E::load(sb + qsb_index(l.tib, w, g, 1, kv.G, ko));
+    if (w == 0) {
+      constexpr int per = 32 / BITS;
+      const uint32_t word = *reinterpret_cast<const uint32_t*>(
+          chunk + kv.kc_off + qk_word_off(l.tib, d / per, kv.D, BITS));
+      return (word >> (BITS * (d % per))) & ((1u << BITS) - 1u);
+    }
+    int sh;
+    const uint32_t word =
+        *reinterpret_cast<const uint32_t*>(chunk + kv.vc_off + qv_word_off(l.tib, d, kv.D, BITS, &sh));
+    return (word >> sh) & ((1u << BITS) - 1u);
   }
+  const Comp& cc = which ? kv.vc : kv.kc;
+  const Comp& sc = which ? kv.vs : kv.ks;
+  const Comp& bc = which ? kv.vb : kv.kb;
+  *s = E::load(reinterpret_cast<const typename E::T*>(at(sc, l, h)) + g);
+  *b = E::load(reinterpret_cast<const typename E::T*>(at(bc, l, h)) + g);
+  return code_tm<BITS>(at(cc, l, h), d);
 }
 
-template <int DT, int BITS, bool VDM>
-__device__ __forceinline__ float value_at(const KVSrc& kv, const TokLoc& l, int64_t h, int d,
-                                          int group) {
+// K (which 0) or V (which 1) element as float: float blocks load it,
+// affine blocks dequantize it as fp32 scale * code + bias.
+template <int DT, int BITS>
+__device__ __forceinline__ float kv_at(const KVSrc& kv, const TokLoc& l, int64_t h, int d, int which,
+                                       int group) {
   using E = Elem<DT>;
   if constexpr (BITS == 0) {
-    return E::load(reinterpret_cast<const typename E::T*>(at(kv.vc, l, h)) + d);
+    const Comp& c = which ? kv.vc : kv.kc;
+    return E::load(reinterpret_cast<const typename E::T*>(at(c, l, h)) + d);
   } else {
-    const int g = d / group;
-    const float s = E::load(reinterpret_cast<const typename E::T*>(at(kv.vs, l, h)) + g);
-    const float b = E::load(reinterpret_cast<const typename E::T*>(at(kv.vb, l, h)) + g);
-    uint32_t c;
-    if constexpr (VDM) {
-      const uint8_t* row = kv.vc.ptr + l.blk * kv.vc.sb + h * kv.vc.sh + d * kv.v_dim_stride;
-      c = code_tm<BITS>(row, static_cast<int>(l.tib));
-    } else {
-      c = code_tm<BITS>(at(kv.vc, l, h), d);
-    }
+    float s, b;
+    const uint32_t c = qcode<DT, BITS>(kv, l, h, d, which, group, &s, &b);
     return fmaf(s, static_cast<float>(c), b);
   }
 }
@@ -308,7 +329,7 @@ __device__ __forceinline__ float value_at(const KVSrc& kv, const TokLoc& l, int6
 //
 // Thread per (seq, head, token, 8 dims).  out_kind 0: values (dequantized
 // when bits > 0) into [n,H,T,D] of dtype; out_kind 1: reference-layout codes.
-template <int DT, int BITS, int KIND, bool VDM>
+template <int DT, int BITS, int KIND>
 __global__ void __launch_bounds__(256) gather_kernel(GatherArgs g) {
   using E = Elem<DT>;
   const int tpr = (g.D + 7) / 8;
@@ -327,24 +348,12 @@ __global__ void __launch_bounds__(256) gather_kernel(GatherArgs g) {
   const int cnt = min(8, g.D - d0);
   if constexpr (KIND == 0) {
     typename E::T* o = static_cast<typename E::T*>(g.out) + row * g.D + d0;
-    for (int i = 0; i < cnt; i++) {
-      float x = g.which == 0 ? key_at<DT, BITS>(g.kv, l, h, d0 + i, g.group)
-                             : value_at<DT, BITS, VDM>(g.kv, l, h, d0 + i, g.group);
-      o[i] = E::from_f32(x);
-    }
+    for (int i = 0; i < cnt; i++) o[i] = E::from_f32(kv_at<DT, BITS>(g.kv, l, h, d0 + i, g.which, g.group));
   } else {
     // codes of dims [d0, d0+8) re-packed little-endian into the reference layout
-    const Comp& cc = g.which == 0 ? g.kv.kc : g.kv.vc;
     uint32_t code[8];
-    for (int i = 0; i < 8; i++) {
-      const int d = d0 + i;
-      if (VDM && g.which == 1) {
-        const uint8_t* r = cc.ptr + l.blk * cc.sb + h * cc.sh + d * g.kv.v_dim_stride;
-        code[i] = code_tm<BITS>(r, static_cast<int>(l.tib));
-      } else {
-        code[i] = code_tm<BITS>(at(cc, l, h), d);
-      }
-    }
+    float s = 0.0f, b = 0.0f;
+    for (int i = 0; i < 8; i++) code[i] = qcode<DT, BITS>(g.kv, l, h, d0 + i, g.which, g.group, &s, &b);
     uint32_t* wq = static_cast<uint32_t*>(g.out) + row * (g.D * BITS / 32);
     if constexpr (BITS == 4) {
       uint32_t w = 0;
@@ -355,14 +364,11 @@ __global__ void __launch_bounds__(256) gather_kernel(GatherArgs g) {
       wq[2 * j + 1] = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
     }
     if (d0 % g.group == 0) {
+      // s and b of the group holding dims [d0, d0+8) (exact stored values)
       const int G = g.D / g.group;
       const int gi = d0 / g.group;
-      const Comp& sc = g.which == 0 ? g.kv.ks : g.kv.vs;
-      const Comp& bc = g.which == 0 ? g.kv.kb : g.kv.vb;
-      static_cast<typename E::T*>(g.out_s)[row * G + gi] =
-          reinterpret_cast<const typename E::T*>(at(sc, l, h))[gi];
-      static_cast<typename E::T*>(g.out_b)[row * G + gi] =
-          reinterpret_cast<const typename E::T*>(at(bc, l, h))[gi];
+      static_cast<typename E::T*>(g.out_s)[row * G + gi] = E::from_f32(s);
+      static_cast<typename E::T*>(g.out_b)[row * G + gi] = E::from_f32(b);
     }
   }
 }
@@ -396,32 +402,14 @@ __global__ void __launch_bounds__(256) scatter_codes_kernel(ScatterCodesArgs a) 
       code[4 + i] = (x1 >> (8 * i)) & 255u;
     }
   }
-  if (!a.is_v) {
-    uint32_t* c = reinterpret_cast<uint32_t*>(chunk + d.c_off + static_cast<int64_t>(tib) * (a.D * BITS / 8));
-    if constexpr (BITS == 4) c[j] = w[j];
-    else { c[2 * j] = w[2 * j]; c[2 * j + 1] = w[2 * j + 1]; }
-  } else {
-    const int64_t row_bytes = static_cast<int64_t>(d.block_size) * BITS / 8;
-    uint8_t* c = chunk + d.c_off;
-    for (int i = 0; i < 8; i++) {
-      const int dd = j * 8 + i;
-      if constexpr (BITS == 8) {
-        c[dd * row_bytes + tib] = static_cast<uint8_t>(code[i]);
-      } else {
-        uint32_t* word = reinterpret_cast<uint32_t*>(c + dd * row_bytes) + tib / 8;
-        const int sh = 4 * (tib % 8);
-        atomicAnd(word, ~(0xFu << sh));
-        atomicOr(word, code[i] << sh);
-      }
-    }
-  }
+  store_chunk_codes<BITS>(chunk, d, tib, j, a.D, code);
   if ((j * 8) % a.group == 0) {
     const int G = a.D / a.group;
     const int g = j * 8 / a.group;
     const uint8_t* sp = static_cast<const uint8_t*>(a.scales) + (row * G + g) * ESIZE;
     const uint8_t* bp = static_cast<const uint8_t*>(a.biases) + (row * G + g) * ESIZE;
-    uint8_t* so = chunk + d.s_off + (static_cast<int64_t>(tib) * G + g) * ESIZE;
-    uint8_t* bo = chunk + d.b_off + (static_cast<int64_t>(tib) * G + g) * ESIZE;
+    uint8_t* so = chunk + d.s_off + qsb_index(tib, d.is_v, g, 0, d.G, d.keys_only) * ESIZE;
+    uint8_t* bo = chunk + d.s_off + qsb_index(tib, d.is_v, g, 1, d.G, d.keys_only) * ESIZE;
     for (int i = 0; i < ESIZE; i++) {
       so[i] = sp[i];
       bo[i] = bp[i];
@@ -514,7 +502,7 @@ constexpr int kTile = 32;
 constexpr int kMaxD = 256;
 constexpr int kGroup = 64;  // affine attention group size
 
-template <int DT, int BITS, int REP, bool VDM, bool QSEM>
+template <int DT, int BITS, int REP, bool QSEM>
 __global__ void __launch_bounds__(256) attn_partial_kernel(AttnArgs a, int h_off, int rep_total) {
   using E = Elem<DT>;
   __shared__ float qs[REP][kMaxD];
@@ -566,7 +554,7 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(AttnArgs a, int h_off
       if (t < t_end) {
         const TokLoc loc = locate(a.kv, b, t);
         for (int d = lane; d < D; d += 8) {
-          const float kv = key_at<DT, BITS>(a.kv, loc, hk, d, kGroup);
+          const float kv = kv_at<DT, BITS>(a.kv, loc, hk, d, 0, kGroup);
 #pragma unroll
           for (int r = 0; r < REP; r++) acc[r] = fmaf(qs[r][d], kv, acc[r]);
         }
@@ -635,7 +623,7 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(AttnArgs a, int h_off
         const int64_t t = t0 + tt;
         if (t >= t_end) break;
         const TokLoc loc = locate(a.kv, b, t);
-        const float vv = value_at<DT, BITS, VDM>(a.kv, loc, hk, vd, kGroup);
+        const float vv = kv_at<DT, BITS>(a.kv, loc, hk, vd, 1, kGroup);
 #pragma unroll
         for (int r = 0; r < REP; r++) o[r] = fmaf(sc[r][tt], vv, o[r]);
       }
@@ -775,14 +763,11 @@ void launch_dequantize(int dtype, int bits, int group, const uint32_t* wq, const
 template <int DT, int BITS>
 static void gather_dispatch_kind(const GatherArgs& g, int out_kind, hipStream_t st) {
   const unsigned nb = blocks_for(static_cast<int64_t>(g.n_seqs) * g.H * g.T * ((g.D + 7) / 8));
-  const bool vdm = g.kv.v_dim_stride > 0;
   if (out_kind == 0) {
-    if (vdm) hipLaunchKernelGGL((gather_kernel<DT, BITS, 0, true>), dim3(nb), dim3(256), 0, st, g);
-    else hipLaunchKernelGGL((gather_kernel<DT, BITS, 0, false>), dim3(nb), dim3(256), 0, st, g);
+    hipLaunchKernelGGL((gather_kernel<DT, BITS, 0>), dim3(nb), dim3(256), 0, st, g);
   } else {
     if constexpr (BITS > 0) {
-      if (vdm) hipLaunchKernelGGL((gather_kernel<DT, BITS, 1, true>), dim3(nb), dim3(256), 0, st, g);
-      else hipLaunchKernelGGL((gather_kernel<DT, BITS, 1, false>), dim3(nb), dim3(256), 0, st, g);
+      hipLaunchKernelGGL((gather_kernel<DT, BITS, 1>), dim3(nb), dim3(256), 0, st, g);
     } else {
       throw Error("code gather needs an affine view");
     }
@@ -880,7 +865,7 @@ void launch_fill_normal(int dtype, void* data, int64_t n, uint64_t seed, float s
   VKV_HIP(hipGetLastError());
 }
 
-template <int DT, int BITS, bool VDM, bool QSEM>
+template <int DT, int BITS, bool QSEM>
 static void attn_dispatch_rep(const AttnArgs& a, int64_t rows, hipStream_t st) {
   const int rep = a.Hq / a.Hkv;
   dim3 grid(a.n_parts, a.Hkv, static_cast<unsigned>(rows));
@@ -889,7 +874,7 @@ static void attn_dispatch_rep(const AttnArgs& a, int64_t rows, hipStream_t st) {
     const int left = rep - done;
     const int chunk = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
 #define VKV_A(R) \
-  hipLaunchKernelGGL((attn_partial_kernel<DT, BITS, R, VDM, QSEM>), grid, dim3(256), 0, st, a, done, rep)
+  hipLaunchKernelGGL((attn_partial_kernel<DT, BITS, R, QSEM>), grid, dim3(256), 0, st, a, done, rep)
     if (chunk == 8) VKV_A(8);
     else if (chunk == 4) VKV_A(4);
     else if (chunk == 2) VKV_A(2);
@@ -903,32 +888,29 @@ static void attn_dispatch_rep(const AttnArgs& a, int64_t rows, hipStream_t st) {
 }
 
 template <int DT>
-static void attn_dispatch(int bits, bool vdm, bool qsem, const AttnArgs& a, int64_t rows,
-                          hipStream_t st) {
+static void attn_dispatch(int bits, bool qsem, const AttnArgs& a, int64_t rows, hipStream_t st) {
   if (bits == 0) {
     if (qsem) throw Error("quantized semantics need an affine cache");
-    attn_dispatch_rep<DT, 0, false, false>(a, rows, st);
+    attn_dispatch_rep<DT, 0, false>(a, rows, st);
   } else if (bits == 4) {
-    if (vdm) attn_dispatch_rep<DT, 4, true, true>(a, rows, st);
-    else attn_dispatch_rep<DT, 4, false, true>(a, rows, st);
+    attn_dispatch_rep<DT, 4, true>(a, rows, st);
   } else if (bits == 8) {
-    if (vdm) attn_dispatch_rep<DT, 8, true, true>(a, rows, st);
-    else attn_dispatch_rep<DT, 8, false, true>(a, rows, st);
+    attn_dispatch_rep<DT, 8, true>(a, rows, st);
   } else {
     throw Error("bits must be 0, 4 or 8");
   }
 }
 
-void launch_attention(int dtype, int bits, int group, bool v_dim_major, bool quant_semantics,
+void launch_attention(int dtype, int bits, int group, bool quant_semantics,
                       const AttnArgs& a, int64_t rows, hipStream_t st) {
   if (rows <= 0) return;
   VKV_CHECK(a.D <= kMaxD && a.Dv <= kMaxD, "head dims above 256 are not supported here");
   VKV_CHECK(a.Hq % a.Hkv == 0, "query heads must be a multiple of kv heads");
   VKV_CHECK(bits == 0 || group == 64, "affine attention supports group_size 64");
   switch (dtype) {
-    case kF32: attn_dispatch<kF32>(bits, v_dim_major, quant_semantics, a, rows, st); break;
-    case kF16: attn_dispatch<kF16>(bits, v_dim_major, quant_semantics, a, rows, st); break;
-    case kBF16: attn_dispatch<kBF16>(bits, v_dim_major, quant_semantics, a, rows, st); break;
+    case kF32: attn_dispatch<kF32>(bits, quant_semantics, a, rows, st); break;
+    case kF16: attn_dispatch<kF16>(bits, quant_semantics, a, rows, st); break;
+    case kBF16: attn_dispatch<kBF16>(bits, quant_semantics, a, rows, st); break;
     default: throw Error("unsupported dtype");
   }
   VKV_HIP(hipGetLastError());
