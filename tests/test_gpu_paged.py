@@ -167,11 +167,13 @@ def test_prefix_store_fetch_copies_device_blocks():
 
 
 @pytest.mark.parametrize("bits,D,rep,bs,Hkv", [(4, 128, 4, 32, 8), (4, 64, 1, 64, 2), (8, 128, 2, 32, 4),
-                                               (4, 128, 8, 64, 2), (8, 64, 16, 32, 1), (4, 128, 3, 32, 2)])
+                                               (4, 128, 8, 64, 2), (8, 64, 16, 32, 1), (4, 128, 3, 32, 2),
+                                               (8, 256, 2, 32, 2), (4, 256, 2, 64, 1), (8, 128, 5, 96, 2),
+                                               (4, 64, 12, 32, 1)])
 def test_paged_decode_shapes_and_partitions(bits, D, rep, bs, Hkv):
-    """The matrix-core decode path across GQA factors, head dims, pool
-    block sizes (sub-blocks of 32) and sequences long enough to be split
-    into several partitions, against the oracle."""
+    """The matrix-core decode path across GQA factors (head groups of 4 and
+    8), head dims, pool block sizes (sub-blocks of 32) and sequences long
+    enough to be split into several partitions, against the oracle."""
     dtype = O.BF16
     rng = np.random.default_rng(bits * 1000 + D + rep * 7 + bs)
     lens = [5000, 31, 32, 33, 700, 0 + 1]
@@ -203,3 +205,32 @@ def test_generic_and_matrix_core_paths_agree(monkeypatch):
     monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
     slow = values(vkv.paged_attention(q, view, 0.088), dtype)
     assert np.abs(fast - slow).max() <= 2e-2
+
+
+@pytest.mark.parametrize("part_steps", ["1", "3", "64"])
+def test_decode_partition_sizes_agree(monkeypatch, part_steps):
+    """Partitions of 1 step (most waves of a workgroup idle), an odd size
+    and one partition per sequence give the same output within fp32
+    rounding of the merge order."""
+    dtype, bits = O.BF16, 4
+    rng = np.random.default_rng(91)
+    P = Paged(rng, bits, dtype, n_seqs=5, n_share=2, max_len=900, nblocks=200)
+    P.append_all()
+    view = P.view()
+    q = dev(rand_bits(rng, (len(P.lens), 32, 128), dtype), dtype)
+    base = values(vkv.paged_attention(q, view, 0.088), dtype)
+    monkeypatch.setenv("VKV_PART_STEPS", part_steps)
+    got = values(vkv.paged_attention(q, view, 0.088), dtype)
+    for _ in range(2):  # counters are left at zero for the next launch
+        again = values(vkv.paged_attention(q, view, 0.088), dtype)
+        assert np.array_equal(again, got)
+    assert np.abs(base - got).max() <= 2e-2
+    f = lambda a: O.to_f32(a, dtype)
+    qh = host(q)
+    for s, L in enumerate(P.lens):
+        rk = O.quantize(np.ascontiguousarray(P.tokens[s].transpose(1, 0, 2)), dtype, 64, bits)
+        rv = O.quantize(np.ascontiguousarray(P.vals[s].transpose(1, 0, 2)), dtype, 64, bits)
+        ref = O.quantized_sdpa(f(qh[s])[None, :, None], dtype, rk[0][None], f(rk[1])[None],
+                               f(rk[2])[None], rv[0][None], f(rv[1])[None], f(rv[2])[None], 0.088,
+                               64, bits)[0, :, 0]
+        assert (np.abs(got[s] - ref) <= attn_tol(dtype, ref)).all(), s

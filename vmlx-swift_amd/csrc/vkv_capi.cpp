@@ -337,14 +337,16 @@ int vkv_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vk
       d.Hq = static_cast<int32_t>(q->shape[1]);
       d.Hkv = kv->n_kv_heads;
       d.rep = rep;
-      // partitions of 32-token blocks: aim for >= 2048 busy workgroups, at
-      // most 16 blocks (4 per wave) per workgroup
-      const int64_t max_blocks = (static_cast<int64_t>(kv->max_len) + 31) / 32;
-      const int64_t units = max_blocks * kv->n_kv_heads * kv->n_seqs;
-      int64_t pb = (units + 2047) / 2048;
-      pb = std::min<int64_t>(16, std::max<int64_t>(4, (pb + 3) / 4 * 4));
-      d.part_blocks = static_cast<int32_t>(pb);
-      d.n_parts = static_cast<int32_t>(std::max<int64_t>(1, (max_blocks + pb - 1) / pb));
+      // partitions of 64-token steps: about 512 workgroups (two per CU) over
+      // the grid's upper bound, 4..64 steps (1..16 per wave) each; a
+      // partition costs a set-up and a pipeline fill, so fewer is better
+      const int64_t max_steps = (static_cast<int64_t>(kv->max_len) + 63) / 64;
+      const int64_t units = max_steps * kv->n_kv_heads * kv->n_seqs;
+      int64_t ps = (units + 511) / 512;
+      ps = std::min<int64_t>(64, std::max<int64_t>(4, (ps + 3) / 4 * 4));
+      if (const char* e = getenv("VKV_PART_STEPS")) ps = std::min(64, std::max(1, atoi(e)));
+      d.part_steps = static_cast<int32_t>(ps);
+      d.n_parts = static_cast<int32_t>(std::max<int64_t>(1, (max_steps + ps - 1) / ps));
       if (d.n_parts > 1) {
         const size_t per = static_cast<size_t>(kv->n_seqs) * d.Hq * d.n_parts;
         float* ws = attention_workspace(S(stream), per * (kv->head_dim + 2));

@@ -8,33 +8,50 @@
 // sdpa_vector_2pass_2 merges them
 // (Source/Cmlx/mlx-generated/metal/sdpa_vector.h:320-394).
 //
-// Why matrix cores: with 4 query heads per KV head every 4-bit KV byte feeds
-// about 7 multiply-adds; at 8 TB/s that is ~110 TFLOP/s of fp32 FMA, more
-// than the vector ALUs sustain.  Both contractions therefore run as
-// 16x16x32 bf16 MFMAs directly on the codes:
+// Arithmetic.  Both contractions run as 16x16x32 bf16 MFMAs directly on the
+// codes, so the vector ALUs only unpack codes and run the softmax:
 //   * a 4-bit code c enters as bf16(128 + c), bit pattern 0x4300 | c, which
-//     is exact; an 8-bit code is split into nibbles c = 16*hi + lo, the hi
-//     half meeting a partner operand pre-scaled by 16 (exact in bf16);
+//     is exact; an 8-bit code c = 16*hi + lo enters as two operands,
+//     bf16(128 + lo) = 0x4300 | lo and bf16(2048 + 16*hi) = 0x4500 | hi, whose
+//     sum is c + 2176 (MAG);
 //   * per-(token, group) scale s and bias b are applied around the
-//     contraction:  q.(s*c + b) = s * q.(128 + c) + (b - 128 s) * sum(q), and
-//     sum_t p_t (s_t c_t + b_t) = sum_t P_t (128 + c_t)
-//                                 + sum_t p_t b_t - 128 * sum_t P_t
+//     contraction:  q.(s*c + b) = s * q.(MAG + c) + (b - MAG s) * sum(q), and
+//     sum_t p_t (s_t c_t + b_t) = sum_t P_t (MAG + c_t)
+//                                 + sum_t p_t (b_t + C0 s_t) - (MAG + C0) sum_t P_t
 //     with P_t = p_t s_t carried as two bf16 operands (hi + lo, about 16
-//     significant bits): a single bf16 P would put a 2^-9 relative error on
-//     the code part s*c, which the bias then cancels only partly.  The
-//     offset sum uses the same hi + lo values the MFMA consumed, so it
-//     cancels to fp32 rounding.  (For 8-bit the offset is 128 + 16*128.)
+//     significant bits between them; a single bf16 P would put a 2^-9
+//     relative error on the code part s*c).  The offset sum uses the same
+//     hi + lo values the MFMA consumed, so it cancels to fp32 rounding, and
+//     the centre C0 (the code midpoint) leaves a residual error of the size
+//     of the value's own deviation from its group midpoint.
 //
-// Work decomposition: a workgroup (4 waves) owns one (partition of 32-token
-// blocks, kv head, sequence) and its waves take the partition's blocks round
-// robin.  Lane = 16*lg + lrow.  The score MFMA (A = queries, B = key codes)
-// leaves token lrow of the tile and query head 4*lg + i in accumulator
-// register i; the output MFMA (A = value codes, B = probabilities) leaves
-// value dim 16*tile + 4*lg + i and query head lrow.  Probabilities move
-// between the two layouts through a per-wave LDS tile.  The running max is
-// refreshed lazily (only when a block's max exceeds it by more than kTau),
-// which keeps the accumulator rescale off the common path; probabilities are
-// then bounded by e^kTau, well inside bf16 range.
+// Work layout.  A 64-token step of one (sequence, kv head) is one pass.  The
+// score MFMA is block diagonal: with HP query heads per part (HP = 4 for up
+// to 4 query heads per kv head, else 8; more than 8 are split into head
+// groups of 8 on separate workgroups) the 16 output columns are PP = 16 / HP
+// parts x HP heads, and the 32-element K dimension is split between the parts, so one
+// 16x16 output tile carries 16 * PP tokens x HP heads and every lane holds 4
+// live scores.  Lane l = n + 16 lg (n = column) sees tokens
+// 32 s + 8 lg + off(q, i) of head n % HP, where (s, q) enumerate the parts of
+// the step and off() is the order in which the value operand's K dimension
+// visits the 8 tokens of a value word.  The probabilities of head h then
+// reach the P.V operand of lane h + 16 lg by DPP row rotations (no LDS), and
+// the P.V output holds value dim 16 t + 4 lg + i of head n in lane n + 16 lg.
+// The running max is refreshed lazily (only when a score exceeds it by more
+// than kTau), which needs no cross-lane reduction on the common path and
+// bounds probabilities by e^kTau.
+//
+// Workgroup = 4 waves = (partition of steps, kv head and head group,
+// sequence); waves take
+// the partition's steps round robin, with the next step's loads in flight
+// while the current one computes when the per-step operands fit in
+// registers twice.  A sequence that fits one partition is written directly;
+// longer ones leave per-partition partials that qdecode_combine_kernel
+// merges.  (Merging in the last workgroup to finish would need device-scope
+// release/acquire fences, which on gfx950 write back and invalidate the
+// XCD's whole L2 and cost more than the extra launch.)
+#include <utility>
+
 #include "vkv_device.h"
 #include "vkv_internal.h"
 
@@ -45,72 +62,100 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+// global-memory views: KV loads must not become flat loads, which would
+// also count against the LDS wait counter
+typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;
+typedef __attribute__((address_space(1))) const u32x2_t g_u32x2_t;
+typedef __attribute__((address_space(1))) const uint32_t g_u32_t;
 
 constexpr float kTau = 8.0f;
 constexpr int kWaves = 4;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kMaxPartSteps = 64;  // 64-token steps per workgroup partition, at most
+
+template <int... Is, class F>
+__device__ __forceinline__ void sfor_impl(std::integer_sequence<int, Is...>, F&& f) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [0, N).
+template <int N, class F>
+__device__ __forceinline__ void sfor(F&& f) {
+  sfor_impl(std::make_integer_sequence<int, N>{}, f);
+}
 
 __device__ __forceinline__ f32x4_t mfma(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-// 8 nibbles -> 8 bf16 (128 + nibble); register p holds nibbles (p, p + 4).
-__device__ __forceinline__ u32x4_t nib_magic(uint32_t w) {
+// The bf16 exponent patterns OR-ed onto the codes, held in VGPRs the
+// compiler cannot see through: with both the mask and the pattern as
+// literals it emits v_and + v_or, with the pattern in a register one
+// v_and_or_b32.
+struct Magic {
+  uint32_t m128, m2048;  // 0x43004300 (128 + c), 0x45004500 (2048 + 16 c)
+  __device__ __forceinline__ Magic() : m128(0x43004300u), m2048(0x45004500u) {
+    asm volatile("" : "+v"(m128), "+v"(m2048));
+  }
+};
+
+// 8 nibbles -> 8 bf16 (128 + nibble); register r holds nibbles (r, r + 4).
+__device__ __forceinline__ u32x4_t nib_magic(uint32_t w, const Magic& mg) {
   u32x4_t r;
-  r[0] = (w & 0x000F000Fu) | 0x43004300u;
-  r[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  r[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  r[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  r[0] = (w & 0x000F000Fu) | mg.m128;
+  r[1] = ((w >> 4) & 0x000F000Fu) | mg.m128;
+  r[2] = ((w >> 8) & 0x000F000Fu) | mg.m128;
+  r[3] = ((w >> 12) & 0x000F000Fu) | mg.m128;
   return r;
 }
 
-// 8 bytes (x then y) -> low / high nibbles as bf16 (128 + nibble); register
-// order (b0, b2), (b1, b3) of x, then of y.
-__device__ __forceinline__ void byte_magic(uint32_t x, uint32_t y, u32x4_t& lo, u32x4_t& hi) {
-  lo[0] = (x & 0x000F000Fu) | 0x43004300u;
-  lo[1] = ((x >> 8) & 0x000F000Fu) | 0x43004300u;
-  lo[2] = (y & 0x000F000Fu) | 0x43004300u;
-  lo[3] = ((y >> 8) & 0x000F000Fu) | 0x43004300u;
-  hi[0] = ((x >> 4) & 0x000F000Fu) | 0x43004300u;
-  hi[1] = ((x >> 12) & 0x000F000Fu) | 0x43004300u;
-  hi[2] = ((y >> 4) & 0x000F000Fu) | 0x43004300u;
-  hi[3] = ((y >> 12) & 0x000F000Fu) | 0x43004300u;
+// 8 bytes (x then y) -> low nibbles as bf16 (128 + lo) and high nibbles as
+// bf16 (2048 + 16 hi); register order (b0, b2), (b1, b3) of x, then of y.
+__device__ __forceinline__ void byte_magic(uint32_t x, uint32_t y, const Magic& mg, u32x4_t& lo,
+                                           u32x4_t& hi) {
+  lo[0] = (x & 0x000F000Fu) | mg.m128;
+  lo[1] = ((x >> 8) & 0x000F000Fu) | mg.m128;
+  lo[2] = (y & 0x000F000Fu) | mg.m128;
+  lo[3] = ((y >> 8) & 0x000F000Fu) | mg.m128;
+  hi[0] = ((x >> 4) & 0x000F000Fu) | mg.m2048;
+  hi[1] = ((x >> 12) & 0x000F000Fu) | mg.m2048;
+  hi[2] = ((y >> 4) & 0x000F000Fu) | mg.m2048;
+  hi[3] = ((y >> 12) & 0x000F000Fu) | mg.m2048;
 }
 
-// Dim (within an 8-dim unit) / token (within an 8-token group) carried by
-// MFMA K element j of a lane: 4-bit pairs (p, p+4), 8-bit pairs (0,2),(1,3).
+// Dim (within an 8-dim unit) carried by MFMA K element j of a key operand:
+// 4-bit registers pair nibbles (p, p + 4), 8-bit pair bytes (0, 2), (1, 3).
 template <int BITS>
 __device__ __forceinline__ int kslot(int j) {
   if constexpr (BITS == 4) return (j & 1) ? (j >> 1) + 4 : (j >> 1);
   const int r = j & 3;
   return (j & 4) | (r == 1 ? 2 : r == 2 ? 1 : r);
 }
-// inverse of kslot (both maps are involutions for 8-bit)
+
+// Token (within the 8 tokens of a value word) of score register i of a lane
+// whose part is q: the pairs (i0, i1) and (i2, i3) are exactly the token
+// pairs one value-operand register holds, so a lane packs its own pairs.
 template <int BITS>
-__device__ __forceinline__ int kpos(int q) {
-  if constexpr (BITS == 4) return q < 4 ? 2 * q : 2 * (q - 4) + 1;
-  return kslot<8>(q);
+__device__ __forceinline__ int tok_off(int q, int i) {
+  if constexpr (BITS == 4) return 2 * q + (i >> 1) + 4 * (i & 1);
+  return 4 * q + 2 * (i & 1) + (i >> 1);
 }
 
-template <int N>
-__device__ __forceinline__ float ror(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + N, 0xF, 0xF, false));
+// Value of lane (lane + K) within this lane's row of 16 (DPP row_ror:N
+// reads lane (i - N) mod 16).
+template <int K>
+__device__ __forceinline__ uint32_t row_read(uint32_t x) {
+  if constexpr (K == 0) {
+    return x;
+  } else {
+    return __builtin_amdgcn_update_dpp(0u, x, 0x120 + (16 - K), 0xF, 0xF, false);
+  }
 }
-// reductions over the 16 lanes of a DPP row
-__device__ __forceinline__ float row16_max(float x) {
-  x = fmaxf(x, ror<8>(x));
-  x = fmaxf(x, ror<4>(x));
-  x = fmaxf(x, ror<2>(x));
-  return fmaxf(x, ror<1>(x));
+template <int K>
+__device__ __forceinline__ float row_readf(float x) {
+  return __uint_as_float(row_read<K>(__float_as_uint(x)));
 }
-__device__ __forceinline__ float row16_sum(float x) {
-  x += ror<8>(x);
-  x += ror<4>(x);
-  x += ror<2>(x);
-  return x + ror<1>(x);
-}
-
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // N consecutive words with the widest loads the count allows (the address
 // is aligned to the load width by the chunk format).
@@ -119,20 +164,20 @@ __device__ __forceinline__ void load_words(const uint8_t* p, uint32_t* out) {
   if constexpr (N % 4 == 0) {
 #pragma unroll
     for (int v = 0; v < N / 4; v++) {
-      const u32x4_t x = reinterpret_cast<const u32x4_t*>(p)[v];
+      const u32x4_t x = ((g_u32x4_t*)p)[v];
 #pragma unroll
       for (int e = 0; e < 4; e++) out[4 * v + e] = x[e];
     }
   } else if constexpr (N % 2 == 0) {
 #pragma unroll
     for (int v = 0; v < N / 2; v++) {
-      const u32x2_t x = reinterpret_cast<const u32x2_t*>(p)[v];
+      const u32x2_t x = ((g_u32x2_t*)p)[v];
       out[2 * v] = x[0];
       out[2 * v + 1] = x[1];
     }
   } else {
 #pragma unroll
-    for (int v = 0; v < N; v++) out[v] = reinterpret_cast<const uint32_t*>(p)[v];
+    for (int v = 0; v < N; v++) out[v] = ((g_u32_t*)p)[v];
   }
 }
 
@@ -142,297 +187,417 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
-template <int BITS, int D>
-__global__ void __launch_bounds__(256, 2) qdecode_mfma_kernel(DecodeArgs a) {
-  constexpr int G = D / 64;                          // quantization groups per row
-  constexpr int KS = D / 32;                         // 32-dim K steps
-  constexpr int NT = D / 16;                         // 16-dim output tiles
-  constexpr int KW = (BITS == 4) ? KS : 2 * KS;      // key words per lane per token
-  constexpr int VW = (BITS == 4) ? NT : 2 * NT;      // value words per lane
-  constexpr int ROW = D * BITS / 8;                  // key code bytes per token
-  constexpr int SBV = 4 * G;                         // scale/bias values per token
-  constexpr int NP = (BITS == 4) ? 1 : 2;            // probability tiles (x1, x16)
-  constexpr float MAG = (BITS == 4) ? 128.0f : 2176.0f;
-  constexpr float C0 = (BITS == 4) ? 8.0f : 128.0f;  // code midpoint
+// LDS-only barrier: orders LDS traffic across the workgroup but leaves
+// global loads in flight (a plain __syncthreads waits for them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
-  // One LDS region serves three phases: the queries (qf) until the MFMA
-  // operands are built, the per-wave probability tiles (ptile: x1 / x16
-  // copies, each split into bf16 hi + lo parts) during the block loop, and
-  // the per-wave output staging (fin_o) after it.
-  constexpr int QF_BYTES = 16 * D * 4;
-  constexpr int PT_BYTES = kWaves * NP * 2 * G * 16 * 32 * 2;
-  constexpr int FIN_BYTES = kWaves * 16 * (D + 1) * 4;
-  constexpr int U1 = QF_BYTES > PT_BYTES ? QF_BYTES : PT_BYTES;
-  __shared__ __attribute__((aligned(16))) uint8_t smem_u[U1 > FIN_BYTES ? U1 : FIN_BYTES];
-  float(*qf)[D] = reinterpret_cast<float(*)[D]>(smem_u);
-  float(*fin_o)[16][D + 1] = reinterpret_cast<float(*)[16][D + 1]>(smem_u);
-  typedef uint16_t ptile_t[NP][2][G][16][32];
-  ptile_t* ptile = reinterpret_cast<ptile_t*>(smem_u);
-  __shared__ float sqs[16][G];
-  __shared__ float fin_s[kWaves][16][2 + G];
+template <int BITS, int D, int HP>
+struct QD {
+  static constexpr int G = D / 64;            // quantization groups per row
+  static constexpr int PP = 16 / HP;          // token parts of a score tile
+  static constexpr int TT = 4 / PP;           // score tiles per 64-token step
+  static constexpr int SPW = 4 / PP;          // lane groups per part
+  static constexpr int SL = D * PP / 32;      // score K slices (8 dims per lane)
+  static constexpr int UW = BITS / 4;         // words per 8-dim unit
+  static constexpr int RUN = (D / 32) * UW;   // key words of one lane-group run
+  static constexpr int NT = D / 16;           // 16-dim output tiles
+  static constexpr int VW = NT * UW;          // value words per lane per sub-block
+  static constexpr int ROW = D * BITS / 8;    // key code bytes per token
+  static constexpr int SBW = 2 * G;           // scale/bias words per token (K, V)
+  static constexpr int QROW = 16 * SPW + 1;   // query-table entries per slice
+  static constexpr float MAG = (BITS == 4) ? 128.0f : 2176.0f;
+  static constexpr float C0 = (BITS == 4) ? 8.0f : 128.0f;
+  // per-step operand registers; steps are double buffered when they fit
+  static constexpr int BUF = D * UW / 4 + HP * D / 32;
+  static constexpr bool kPrefetch = BUF <= 48;
+
+  struct Buf {
+    uint32_t kw[TT][PP][RUN];    // key words of this lane's token, per tile
+    uint32_t sb[TT][4][SBW];     // scale/bias of the 4 scored tokens, per tile
+    uint32_t vw[2][VW];          // value words, per 32-token sub-block
+  };
+};
+
+template <int BITS, int D, int HP>
+__global__ void __launch_bounds__(256, (D >= 256) ? 1 : 2) qdecode_kernel(DecodeArgs a) {
+  using C = QD<BITS, D, HP>;
+  constexpr int G = C::G, PP = C::PP, TT = C::TT, SPW = C::SPW, SL = C::SL;
+  constexpr int RUN = C::RUN, NT = C::NT, VW = C::VW, ROW = C::ROW, SBW = C::SBW;
+  constexpr int QROW = C::QROW;
+  constexpr float MAG = C::MAG, C0 = C::C0;
+  using Buf = typename C::Buf;
+
+  // LDS: the query table (score B operands) during the step loop, the
+  // per-wave results after it.
+  constexpr int QT_BYTES = SL * QROW * 16;
+  constexpr int FIN_BYTES = kWaves * HP * D * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[QT_BYTES > FIN_BYTES ? QT_BYTES : FIN_BYTES];
+  __shared__ float qf[HP][D + 1];
+  __shared__ float sqs[HP][G];
+  __shared__ int32_t sblk[2 * kMaxPartSteps];  // pool block of each sub-block
+  __shared__ float fin_s[kWaves][HP][2];
+  u32x4_t* qtab = reinterpret_cast<u32x4_t*>(smem);
+  float(*fin_o)[HP][D] = reinterpret_cast<float(*)[HP][D]>(smem);
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, lrow = lane & 15, lg = lane >> 4;
-  const int part = blockIdx.x, hk = blockIdx.y, seq = blockIdx.z;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int lane = tid & 63, n = lane & 15, lg = lane >> 4;
+  const int part = blockIdx.x, seq = blockIdx.z;
   const int rep = a.rep;
+  const int n_hg = (rep + HP - 1) / HP;  // head groups of HP query heads
+  const int hk = blockIdx.y / n_hg, hg = blockIdx.y % n_hg;
+  const int nh = min(HP, rep - hg * HP);  // query heads of this workgroup
+  // first query head of the group, and its (sequence, head) row
+  const int64_t hq0 = static_cast<int64_t>(hk) * rep + hg * HP;
+  const int64_t rh0 = static_cast<int64_t>(seq) * a.Hq + hq0;
   const int len = a.seq_lens ? a.seq_lens[seq] : a.max_len;
-  const int nblk = (len + 31) >> 5;
-  const int b0 = part * a.part_blocks;
-  const int b1 = min(nblk, b0 + a.part_blocks);
+  const int nstep = (len + 63) >> 6;
+  // balanced partitions: parts_used pieces of at most part_steps steps
+  const int parts_used = (nstep + a.part_steps - 1) / a.part_steps;
+  if (part >= parts_used) {
+    if (nstep == 0 && part == 0) {  // empty sequence: zero output
+      for (int idx = tid; idx < nh * D; idx += 256)
+        a.out[seq * a.o_ss + (hq0 + idx / D) * a.o_sh + idx % D] = 0;
+    }
+    return;
+  }
+  const int span = (nstep + parts_used - 1) / parts_used;  // <= part_steps
+  const int st0 = part * span;                              // < nstep
+  const int st1 = min(nstep, st0 + span);
+  const int nsub = (len + 31) >> 5;
+  const int subs = a.block_size >> 5;  // 32-token sub-blocks per pool block
+  const int32_t* table = a.table + static_cast<int64_t>(seq) * a.table_stride;
+  const uint8_t* head_base = a.base + static_cast<int64_t>(hk) * a.head_bytes;
 
-  // ---- queries of this kv head's query heads, scaled in bf16
+  // this lane's roles: score column (part p, head h); key-operand lane
+  // group (part pA, unit slot wA)
+  const int p = n / HP, h = n % HP;
+  const int pA = lg / SPW, wA = lg % SPW;
+
+  // direct: read the block table from memory (the first step, issued
+  // before the LDS copy of the partition's table slice exists)
+  auto load_step = [&](int stp, Buf& b, bool direct) {
+    const uint8_t* cb[2];
+    int t0[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      const int sbi = min(2 * stp + s, nsub - 1);
+      const int64_t blk =
+          direct ? table[sbi / subs] : __builtin_amdgcn_readfirstlane(sblk[sbi - 2 * st0]);
+      cb[s] = head_base + blk * a.block_bytes;
+      t0[s] = (sbi % subs) * 32;
+    }
+#pragma unroll
+    for (int tau = 0; tau < TT; tau++) {
+      {  // key row of token 8 (n / 4) + off(q, n % 4) of part (tau, pA)
+        const int c = tau * PP + pA, s = c >> 1, q = c & 1;
+        const int t = t0[s] + 8 * (n >> 2) + tok_off<BITS>(q, n & 3);
+        const uint8_t* row = cb[s] + a.kc_off + static_cast<int64_t>(t) * ROW;
+#pragma unroll
+        for (int rho = 0; rho < PP; rho++)
+          load_words<RUN>(row + (rho * SPW + wA) * RUN * 4, b.kw[tau][rho]);
+      }
+      {  // scale/bias of the tokens this lane scores (column part p)
+        const int c = tau * PP + p, s = c >> 1, q = c & 1;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int t = t0[s] + 8 * lg + tok_off<BITS>(q, i);
+          load_words<SBW>(cb[s] + a.sb_off + static_cast<int64_t>(t) * SBW * 4, b.sb[tau][i]);
+        }
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+      load_words<VW>(cb[s] + a.vc_off + t0[s] * ROW + (lg * 16 + n) * VW * 4, b.vw[s]);
+  };
+
+  // Global loads complete in issue order (one wait counter), so the set-up
+  // reads (table slice, queries) are issued before the first step's KV
+  // loads, which then stay in flight while the set-up uses them.  Every
+  // load here is unconditional (clamped indices): a load under a branch
+  // makes the compiler wait for all outstanding loads at the join.
+  constexpr int QPT = (HP * D + 255) / 256;  // query elements per thread
+  const int n_sub_part = 2 * (st1 - st0);  // <= 2 * kMaxPartSteps <= 256
+  const int32_t my_blk = table[min(2 * st0 + tid, nsub - 1) / subs];
+  uint16_t qraw[QPT];
+#pragma unroll
+  for (int j = 0; j < QPT; j++) {
+    const int i = tid + 256 * j, r = min(i / D, nh - 1), d = i % D;
+    qraw[j] = a.q[seq * a.q_ss + (hq0 + r) * a.q_sh + d];
+  }
+  Buf bufA, bufB;
+  int step = st0 + wave;
+  load_step(min(step, st1 - 1), bufA, true);  // in flight during the set-up
+  const Magic mg;
+  if (tid < n_sub_part) sblk[tid] = my_blk;  // the partition's block-table slice
+  // ---- queries of the group's heads, scaled in bf16; rows >= nh are 0
   const float scale_t = round_to<kBF16>(a.scale);
-  for (int i = tid; i < 16 * D; i += 256) {
-    const int r = i / D, d = i % D;
-    float v = 0.0f;
-    if (r < rep) {
-      const int64_t h = static_cast<int64_t>(hk) * rep + r;
-      v = round_to<kBF16>(bf16_to_f32(a.q[seq * a.q_ss + h * a.q_sh + d]) * scale_t);
+#pragma unroll
+  for (int j = 0; j < QPT; j++) {
+    const int i = tid + 256 * j;
+    const float v = round_to<kBF16>(bf16_to_f32(qraw[j]) * scale_t);
+    if (i < HP * D) qf[i / D][i % D] = (i / D < nh) ? v : 0.0f;
+  }
+  lds_barrier();
+  // query table: entry (slice sg, column nn, unit slot w) holds the 8 dims
+  // of unit sg * SPW + w of head nn % HP in the key operand's K order;
+  // entry 16 * SPW of every slice is zero (lanes outside the column's part)
+  for (int e = tid; e < SL * QROW; e += 256) {
+    const int sg = e / QROW, r = e % QROW;
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (r < 16 * SPW) {
+      const int nn = r / SPW, w = r % SPW;
+      const int unit = sg * SPW + w;
+      const float* qrow = qf[nn % HP];
+#pragma unroll
+      for (int pr = 0; pr < 4; pr++)
+        v[pr] = pack_bf16(qrow[8 * unit + kslot<BITS>(2 * pr)], qrow[8 * unit + kslot<BITS>(2 * pr + 1)]);
     }
-    qf[r][d] = v;
+    qtab[e] = v;
   }
-  __syncthreads();
-  if (tid < 16 * G) {
-    const int r = tid / G, g = tid % G;
-    float s = 0.0f;
-    for (int d = 0; d < 64; d++) s += qf[r][g * 64 + d];
-    sqs[r][g] = s;
+  // sum of each head's bf16 queries per group: 32 lanes per (head, group)
+  for (int rg = tid >> 5; rg < HP * G; rg += 8) {
+    const int r = rg / G, g = rg % G, j = tid & 31;
+    float s = qf[r][g * 64 + j] + qf[r][g * 64 + j + 32];
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 32);
+    if (j == 0) sqs[r][g] = s;
   }
-  // score-MFMA A operands: row = head lrow, K = the 8 dims of unit 4s + lg
-  u32x4_t aq[KS];
-  u32x4_t aq16[BITS == 8 ? KS : 1];
+  lds_barrier();
+  float sq[G];
 #pragma unroll
-  for (int s = 0; s < KS; s++) {
-    const int unit = 4 * s + lg;
-#pragma unroll
-    for (int p = 0; p < 4; p++) {
-      const float x0 = qf[lrow][8 * unit + kslot<BITS>(2 * p)];
-      const float x1 = qf[lrow][8 * unit + kslot<BITS>(2 * p + 1)];
-      aq[s][p] = pack_bf16(x0, x1);
-      if constexpr (BITS == 8) aq16[s][p] = pack_bf16(16.0f * x0, 16.0f * x1);
-    }
-  }
-  __syncthreads();
-  float sq[4][G];
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int g = 0; g < G; g++) sq[i][g] = sqs[4 * lg + i][g];
+  for (int g = 0; g < G; g++) sq[g] = sqs[h][g];
+  const u32x4_t* qlane = qtab + ((pA == p) ? n * SPW + wA : 16 * SPW);
 
   f32x4_t oacc[NT];
 #pragma unroll
   for (int t = 0; t < NT; t++) oacc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m_run[4], l_run[4], corr[4][G];
+  float m_run = -INFINITY, l_run = 0.0f, corr[G];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    m_run[i] = -INFINITY;
-    l_run[i] = 0.0f;
-#pragma unroll
-    for (int g = 0; g < G; g++) corr[i][g] = 0.0f;
-  }
+  for (int g = 0; g < G; g++) corr[g] = 0.0f;
 
-  const int subs = a.block_size >> 5;  // 32-token sub-blocks per pool block
-  for (int b = b0 + wave; b < b1; b += kWaves) {
-    const int64_t blk = a.table[static_cast<int64_t>(seq) * a.table_stride + b / subs];
-    const int sub = b % subs;
-    const uint8_t* chunk = a.base + blk * a.block_bytes + static_cast<int64_t>(hk) * a.head_bytes;
-    // ---- loads: key codes and scale/bias of tokens lrow, lrow+16; value codes
-    uint32_t kw[2][KW];
-    uint32_t sb[2][SBV / 2];
+  auto compute_step = [&](int stp, const Buf& b) {
+    // ---- scores: acc[tau][g] = q . (MAG + c) over group g's dims
+    f32x4_t acc[TT][G];
 #pragma unroll
-    for (int tile = 0; tile < 2; tile++) {
-      const int t = sub * 32 + tile * 16 + lrow;
-      load_words<KW>(chunk + a.kc_off + t * ROW + lg * KW * 4, kw[tile]);
-      load_words<SBV / 2>(chunk + a.sb_off + t * SBV * 2, sb[tile]);
-    }
-    uint32_t vw[VW];
-    load_words<VW>(chunk + a.vc_off + sub * 32 * ROW + (lg * 16 + lrow) * VW * 4, vw);
-
-    // ---- scores of query heads 4*lg + i for tokens (tile*16 + lrow)
-    float sc[2][4];
+    for (int tau = 0; tau < TT; tau++)
 #pragma unroll
-    for (int tile = 0; tile < 2; tile++) {
-      f32x4_t acc[G];
+      for (int g = 0; g < G; g++) acc[tau][g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // query slices are read kQA ahead of their MFMAs; the scheduling
+    // barrier keeps the compiler from issuing every slice's LDS read up front
+    constexpr int kQA = SL < 4 ? SL : 4;
+    u32x4_t qring[kQA];
 #pragma unroll
-      for (int g = 0; g < G; g++) {
-        acc[g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < kQA; j++) qring[j] = qlane[j * QROW];
 #pragma unroll
-        for (int k2 = 0; k2 < 2; k2++) {
-          const int s = 2 * g + k2;
-          if constexpr (BITS == 4) {
-            acc[g] = mfma(aq[s], nib_magic(kw[tile][s]), acc[g]);
-          } else {
-            u32x4_t lo, hi;
-            byte_magic(kw[tile][2 * s], kw[tile][2 * s + 1], lo, hi);
-            acc[g] = mfma(aq16[s], hi, acc[g]);
-            acc[g] = mfma(aq[s], lo, acc[g]);
-          }
+    for (int sg = 0; sg < SL; sg++) {
+      const u32x4_t qb = qring[sg % kQA];
+      if (sg + kQA < SL) qring[sg % kQA] = qlane[(sg + kQA) * QROW];
+      const int g = sg / (SL / G), rho = sg % PP, k = sg / PP;
+#pragma unroll
+      for (int tau = 0; tau < TT; tau++) {
+        if constexpr (BITS == 4) {
+          acc[tau][g] = mfma(nib_magic(b.kw[tau][rho][k], mg), qb, acc[tau][g]);
+        } else {
+          u32x4_t lo, hi;
+          byte_magic(b.kw[tau][rho][2 * k], b.kw[tau][rho][2 * k + 1], mg, lo, hi);
+          acc[tau][g] = mfma(lo, qb, acc[tau][g]);
+          acc[tau][g] = mfma(hi, qb, acc[tau][g]);
         }
       }
-      const int tok = b * 32 + tile * 16 + lrow;
-      float ks[G], u[G];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    float sc[TT][4], vs[TT][4][G], vb[TT][4][G];
 #pragma unroll
-      for (int g = 0; g < G; g++) {
-        const uint32_t w = sb[tile][g];  // (scale, bias) of key group g
-        ks[g] = bf_lo(w);
-        u[g] = fmaf(-MAG, ks[g], bf_hi(w));
-      }
+    for (int tau = 0; tau < TT; tau++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         float s = 0.0f;
 #pragma unroll
-        for (int g = 0; g < G; g++) s = fmaf(u[g], sq[i][g], s);
+        for (int g = 0; g < G; g++) {
+          const uint32_t kwd = b.sb[tau][i][g], vwd = b.sb[tau][i][G + g];
+          const float ks = bf_lo(kwd);
+          s = fmaf(fmaf(-MAG, ks, bf_hi(kwd)), sq[g], s);
+          s = fmaf(ks, acc[tau][g][i], s);
+          vs[tau][i][g] = bf_lo(vwd);
+          vb[tau][i][g] = bf_hi(vwd);
+        }
+        sc[tau][i] = s;
+      }
+    if (stp * 64 + 64 > len) {  // the sequence ends inside this step
 #pragma unroll
-        for (int g = 0; g < G; g++) s = fmaf(ks[g], acc[g][i], s);
-        sc[tile][i] = (tok < len && 4 * lg + i < rep) ? s : -INFINITY;
+      for (int tau = 0; tau < TT; tau++) {
+        const int c = tau * PP + p, s = c >> 1, q = c & 1;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const bool ok = stp * 64 + 32 * s + 8 * lg + tok_off<BITS>(q, i) < len;
+          sc[tau][i] = ok ? sc[tau][i] : -INFINITY;
+#pragma unroll
+          for (int g = 0; g < G; g++) {
+            vs[tau][i][g] = ok ? vs[tau][i][g] : 0.0f;
+            vb[tau][i][g] = ok ? vb[tau][i][g] : 0.0f;
+          }
+        }
       }
     }
 
-    // ---- online softmax, max refreshed lazily
-    float mx[4];
+    // ---- online softmax with a lazily refreshed max
     bool need = false;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      mx[i] = row16_max(fmaxf(sc[0][i], sc[1][i]));
-      need |= mx[i] > m_run[i] + kTau;
+    for (int tau = 0; tau < TT; tau++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) need |= sc[tau][i] > m_run + kTau;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int tau = 0; tau < TT; tau++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) mx = fmaxf(mx, sc[tau][i]);
+      // max over the lanes of head h: the other parts of the row, other rows
+#pragma unroll
+      for (int o = HP; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const bool up = mx > m_run + kTau;
+      const float alpha = up ? (m_run == -INFINITY ? 0.0f : exp2f((m_run - mx) * kLog2e)) : 1.0f;
+      m_run = up ? mx : m_run;
+      l_run *= alpha;
+#pragma unroll
+      for (int g = 0; g < G; g++) corr[g] *= alpha;
+      // the P.V accumulators of lane n + 16 lg carry head n = h for n < HP
+#pragma unroll
+      for (int t = 0; t < NT; t++) oacc[t] *= alpha;
     }
-    if (__any(need)) {
-      float alpha[4];
+    const float m2 = fmaxf(m_run * kLog2e, -3.402823466e38f);
+    float pr[TT][4];
+#pragma unroll
+    for (int tau = 0; tau < TT; tau++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const bool up = mx[i] > m_run[i] + kTau;
-        alpha[i] = up ? (m_run[i] == -INFINITY ? 0.0f : __expf(m_run[i] - mx[i])) : 1.0f;
-        if (up) m_run[i] = mx[i];
-        l_run[i] *= alpha[i];
-#pragma unroll
-        for (int g = 0; g < G; g++) corr[i][g] *= alpha[i];
-      }
-      // output accumulators carry head lrow: alpha of head lrow lives in
-      // register (lrow % 4) of lane group lrow / 4
-      float al = 1.0f;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float v = __shfl(alpha[i], 16 * (lrow >> 2));
-        if ((lrow & 3) == i) al = v;
-      }
-#pragma unroll
-      for (int t = 0; t < NT; t++) oacc[t] *= al;
-    }
-    float p[2][4];
-#pragma unroll
-    for (int tile = 0; tile < 2; tile++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        p[tile][i] = sc[tile][i] == -INFINITY ? 0.0f : __expf(sc[tile][i] - m_run[i]);
-        l_run[i] += p[tile][i];
+        pr[tau][i] = exp2f(fmaf(sc[tau][i], kLog2e, -m2));
+        l_run += pr[tau][i];
       }
 
-    // ---- probability operands p*s_v (bf16) into LDS in the value operand's
-    // K order; the same rounded values feed the offset correction.  The
-    // correction re-centres the codes on their midpoint C0: with
-    // P = bf16(p s) = p s (1 + e), the MFMA term sum P (MAG + c) plus
-    // sum p (b + C0 s) - (MAG + C0) sum P equals the exact result up to
-    // sum p s (c - C0) e, an error of the size of bf16-rounding the value
-    // itself rather than its (often much larger) code part s*c.
-    const int col0 = kpos<BITS>(lrow & 7) + (lrow & 8);
-    const int col1 = col0 + 16;
+    // ---- P = p * s_v as bf16 hi + lo pairs, in value-operand register order
+    uint32_t pk[TT][2][G][2];  // [tile][pair][group][hi, lo]
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-      const uint32_t v0 = sb[0][G + g], v1 = sb[1][G + g];  // (scale, bias) of value group g
-      const float vs0 = bf_lo(v0), vs1 = bf_lo(v1);
-      const float vb0 = fmaf(C0, vs0, bf_hi(v0)), vb1 = fmaf(C0, vs1, bf_hi(v1));
+    for (int tau = 0; tau < TT; tau++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        // p*s as hi + lo bf16 (about 16 significant bits between them)
-        const float pv0 = p[0][i] * vs0, pv1 = p[1][i] * vs1;
-        const uint32_t ph = pack_bf16(pv0, pv1);
-        const uint32_t pl = pack_bf16(pv0 - bf_lo(ph), pv1 - bf_hi(ph));
-        uint16_t* rh = ptile[wave][0][0][g][4 * lg + i];
-        uint16_t* rl = ptile[wave][0][1][g][4 * lg + i];
-        rh[col0] = static_cast<uint16_t>(ph);
-        rh[col1] = static_cast<uint16_t>(ph >> 16);
-        rl[col0] = static_cast<uint16_t>(pl);
-        rl[col1] = static_cast<uint16_t>(pl >> 16);
-        if constexpr (BITS == 8) {  // x16 copies are exact rescalings
-          const uint32_t ph16 = pack_bf16(16.0f * bf_lo(ph), 16.0f * bf_hi(ph));
-          const uint32_t pl16 = pack_bf16(16.0f * bf_lo(pl), 16.0f * bf_hi(pl));
-          uint16_t* rh16 = ptile[wave][1][0][g][4 * lg + i];
-          uint16_t* rl16 = ptile[wave][1][1][g][4 * lg + i];
-          rh16[col0] = static_cast<uint16_t>(ph16);
-          rh16[col1] = static_cast<uint16_t>(ph16 >> 16);
-          rl16[col0] = static_cast<uint16_t>(pl16);
-          rl16[col1] = static_cast<uint16_t>(pl16 >> 16);
+      for (int pi = 0; pi < 2; pi++)
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+          const int i0 = 2 * pi, i1 = 2 * pi + 1;
+          const float P0 = pr[tau][i0] * vs[tau][i0][g], P1 = pr[tau][i1] * vs[tau][i1][g];
+          const uint32_t ph = pack_bf16(P0, P1);
+          const float h0 = bf_lo(ph), h1 = bf_hi(ph);
+          const uint32_t pl = pack_bf16(P0 - h0, P1 - h1);
+          pk[tau][pi][g][0] = ph;
+          pk[tau][pi][g][1] = pl;
+          float cc = corr[g];
+          cc = fmaf(pr[tau][i0], fmaf(C0, vs[tau][i0][g], vb[tau][i0][g]), cc);
+          cc = fmaf(pr[tau][i1], fmaf(C0, vs[tau][i1][g], vb[tau][i1][g]), cc);
+          cc = fmaf(-(MAG + C0), (h0 + h1) + (bf_lo(pl) + bf_hi(pl)), cc);
+          corr[g] = cc;
         }
-        float c = fmaf(p[0][i], vb0, corr[i][g]);
-        c = fmaf(p[1][i], vb1, c);
-        c = fmaf(-(MAG + C0), bf_lo(ph) + bf_lo(pl), c);
-        corr[i][g] = fmaf(-(MAG + C0), bf_hi(ph) + bf_hi(pl), c);
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- O^T[dim][head] += V^T . P'^T
-    u32x4_t bp[NP][2][G];
+    // ---- O^T[dim][head] += V^T . P, one 32-token sub-block per K step
+    sfor<2>([&](auto s_) {
+      constexpr int s = decltype(s_)::value;
+      u32x4_t bpv[G][2];
+      sfor<4>([&](auto r_) {
+        constexpr int r = decltype(r_)::value;
+        constexpr int c = 2 * s + (r >> 1), ts = c / PP, ps = c % PP, pi = r & 1;
 #pragma unroll
-    for (int n = 0; n < NP; n++)
+        for (int g = 0; g < G; g++) {
+          bpv[g][0][r] = row_read<ps * HP>(pk[ts][pi][g][0]);
+          bpv[g][1][r] = row_read<ps * HP>(pk[ts][pi][g][1]);
+        }
+      });
 #pragma unroll
-      for (int hl = 0; hl < 2; hl++)
+      for (int t = 0; t < NT; t++) {
+        const int g = t / (NT / G);
+        if constexpr (BITS == 4) {
+          const u32x4_t av = nib_magic(b.vw[s][t], mg);
+          oacc[t] = mfma(av, bpv[g][0], oacc[t]);
+          oacc[t] = mfma(av, bpv[g][1], oacc[t]);
+        } else {
+          u32x4_t lo, hi;
+          byte_magic(b.vw[s][2 * t], b.vw[s][2 * t + 1], mg, lo, hi);
+          oacc[t] = mfma(lo, bpv[g][0], oacc[t]);
+          oacc[t] = mfma(lo, bpv[g][1], oacc[t]);
+          oacc[t] = mfma(hi, bpv[g][0], oacc[t]);
+          oacc[t] = mfma(hi, bpv[g][1], oacc[t]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    });
+  };
+
+  if constexpr (C::kPrefetch) {
+    // The next step's loads are issued unconditionally (clamped to the last
+    // step, whose data is then re-read from cache): a conditional load
+    // makes the compiler merge the buffer registers at the join, which
+    // waits for the loads right after issuing them.
+    while (step < st1) {
+      const int nx = step + kWaves;
+      load_step(min(nx, st1 - 1), bufB, false);
+      __builtin_amdgcn_sched_barrier(0);  // issue the loads before any compute
+      compute_step(step, bufA);
+      if (nx >= st1) break;
+      const int nx2 = nx + kWaves;
+      load_step(min(nx2, st1 - 1), bufA, false);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_step(nx, bufB);
+      step = nx2;
+    }
+  } else {
+    while (step < st1) {
+      compute_step(step, bufA);
+      step += kWaves;
+      if (step < st1) load_step(step, bufA, false);
+    }
+  }
+
+  // ---- per-wave totals of head h: sum over the parts of the row, then rows
+  float lsum = l_run, csum[G];
 #pragma unroll
-        for (int g = 0; g < G; g++)
-          bp[n][hl][g] = *reinterpret_cast<const u32x4_t*>(&ptile[wave][n][hl][g][lrow][8 * lg]);
+  for (int g = 0; g < G; g++) csum[g] = corr[g];
+  sfor<PP>([&](auto k_) {
+    constexpr int k = decltype(k_)::value;
+    if constexpr (k > 0 && (k & (k - 1)) == 0) {  // offsets HP, 2 HP, ... below 16
+      lsum += row_readf<k * HP>(lsum);
+#pragma unroll
+      for (int g = 0; g < G; g++) csum[g] += row_readf<k * HP>(csum[g]);
+    }
+  });
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    csum[g] += __shfl_xor(csum[g], 16);
+    csum[g] += __shfl_xor(csum[g], 32);
+  }
+  __syncthreads();  // the query table is dead; its LDS becomes fin_o
+  if (n < HP && lg == 0) {
+    fin_s[wave][n][0] = m_run;
+    fin_s[wave][n][1] = lsum;
+  }
+  if (n < nh) {
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-      const int g = t / 4;
-      if constexpr (BITS == 4) {
-        const u32x4_t av = nib_magic(vw[t]);
-        oacc[t] = mfma(av, bp[0][0][g], oacc[t]);
-        oacc[t] = mfma(av, bp[0][1][g], oacc[t]);
-      } else {
-        u32x4_t lo, hi;
-        byte_magic(vw[2 * t], vw[2 * t + 1], lo, hi);
-        oacc[t] = mfma(hi, bp[1][0][g], oacc[t]);
-        oacc[t] = mfma(hi, bp[1][1][g], oacc[t]);
-        oacc[t] = mfma(lo, bp[0][0][g], oacc[t]);
-        oacc[t] = mfma(lo, bp[0][1][g], oacc[t]);
-      }
-    }
-    // the next block rewrites this wave's tile only after every lane read it
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
-
-  // ---- per-wave results: m, l, corrections (per head, token-lane layout)
-  float lsum[4], csum[4][G];
+      const float cg = csum[t / (NT / G)];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    lsum[i] = row16_sum(l_run[i]);
-#pragma unroll
-    for (int g = 0; g < G; g++) csum[i][g] = row16_sum(corr[i][g]);
-  }
-  if (lrow == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      fin_s[wave][4 * lg + i][0] = m_run[i];
-      fin_s[wave][4 * lg + i][1] = lsum[i];
-#pragma unroll
-      for (int g = 0; g < G; g++) fin_s[wave][4 * lg + i][2 + g] = csum[i][g];
+      for (int i = 0; i < 4; i++) fin_o[wave][n][16 * t + 4 * lg + i] = oacc[t][i] + cg;
     }
   }
   __syncthreads();
-  // output tile t, register i: value dim 16t + 4lg + i, head lrow
-#pragma unroll
-  for (int t = 0; t < NT; t++) {
-    const float c = fin_s[wave][lrow][2 + t / 4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) fin_o[wave][lrow][16 * t + 4 * lg + i] = oacc[t][i] + c;
-  }
-  __syncthreads();
 
-  // ---- merge the 4 waves, then write the partition's partial or the output
-  for (int idx = tid; idx < rep * D; idx += 256) {
+  // ---- merge the waves; write the output or this partition's partial
+  for (int idx = tid; idx < nh * D; idx += 256) {
     const int r = idx / D, d = idx % D;
     float M = -INFINITY;
 #pragma unroll
@@ -442,61 +607,78 @@ __global__ void __launch_bounds__(256, 2) qdecode_mfma_kernel(DecodeArgs a) {
     for (int w = 0; w < kWaves; w++) {
       const float mw = fin_s[w][r][0];
       if (mw == -INFINITY) continue;
-      const float f = __expf(mw - M);
+      const float f = exp2f((mw - M) * kLog2e);
       o = fmaf(f, fin_o[w][r][d], o);
       L = fmaf(f, fin_s[w][r][1], L);
     }
-    const int64_t h = static_cast<int64_t>(hk) * rep + r;
-    if (a.n_parts == 1) {
-      a.out[seq * a.o_ss + h * a.o_sh + d] = f32_to_bf16(L > 0.0f ? o / L : 0.0f);
+    if (parts_used == 1) {
+      a.out[seq * a.o_ss + (hq0 + r) * a.o_sh + d] = f32_to_bf16(L > 0.0f ? o / L : 0.0f);
     } else {
-      const int64_t base = (static_cast<int64_t>(seq) * a.Hq + h) * a.n_parts + part;
-      a.ws_o[base * D + d] = o;
+      const int64_t slot = (rh0 + r) * a.n_parts + part;
+      a.ws_o[slot * D + d] = o;
       if (d == 0) {
-        a.ws_ml[base * 2] = M == -INFINITY ? -3.402823466e38f : M;
-        a.ws_ml[base * 2 + 1] = L;
+        a.ws_ml[slot * 2] = M;
+        a.ws_ml[slot * 2 + 1] = L;
       }
     }
   }
 }
 
-// Merge of the partition partials (sdpa_vector.h:320-394).
+// Merge of the partition partials of sequences longer than one partition
+// (sdpa_vector.h:320-394).  Block = one (sequence, query head).
 __global__ void __launch_bounds__(256) qdecode_combine_kernel(DecodeArgs a, int D) {
   const int64_t rh = blockIdx.x;  // seq * Hq + h
-  const int64_t seq = rh / a.Hq;
+  const int seq = static_cast<int>(rh / a.Hq);
   const int64_t h = rh % a.Hq;
+  const int len = a.seq_lens ? a.seq_lens[seq] : a.max_len;
+  const int parts_used = ((len + 63) / 64 + a.part_steps - 1) / a.part_steps;
+  if (parts_used <= 1) return;  // written by the partition itself
   const float* ml = a.ws_ml + rh * a.n_parts * 2;
-  float M = -3.402823466e38f;
-  for (int p = 0; p < a.n_parts; p++) M = fmaxf(M, ml[2 * p]);
+  float M = -INFINITY;
+  for (int pp = 0; pp < parts_used; pp++) M = fmaxf(M, ml[2 * pp]);
   float L = 0.0f;
-  for (int p = 0; p < a.n_parts; p++) L += __expf(ml[2 * p] - M) * ml[2 * p + 1];
+  for (int pp = 0; pp < parts_used; pp++) L = fmaf(exp2f((ml[2 * pp] - M) * kLog2e), ml[2 * pp + 1], L);
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    const float* wo = a.ws_o + rh * a.n_parts * D + d;
     float o = 0.0f;
-    for (int p = 0; p < a.n_parts; p++) o += __expf(ml[2 * p] - M) * a.ws_o[(rh * a.n_parts + p) * D + d];
+    for (int pp = 0; pp < parts_used; pp++)
+      o = fmaf(exp2f((ml[2 * pp] - M) * kLog2e), wo[static_cast<int64_t>(pp) * D], o);
     a.out[seq * a.o_ss + h * a.o_sh + d] = f32_to_bf16(L > 0.0f ? o / L : 0.0f);
   }
 }
 
+static int heads_per_part(int rep) { return rep <= 4 ? 4 : 8; }
+
+int qdecode_head_groups(int rep) { return (rep + heads_per_part(rep) - 1) / heads_per_part(rep); }
+
 bool qdecode_supported(int dtype, int bits, int D, int block_size, int rep, int group) {
-  return dtype == kBF16 && (bits == 4 || bits == 8) && (D == 64 || D == 128) &&
+  return dtype == kBF16 && (bits == 4 || bits == 8) && (D == 64 || D == 128 || D == 256) &&
          block_size % 32 == 0 && rep >= 1 && rep <= 16 && group == 64;
 }
 
+template <int BITS, int D>
+static void launch_d(const DecodeArgs& a, dim3 grid, hipStream_t st) {
+  if (heads_per_part(a.rep) == 4)
+    hipLaunchKernelGGL((qdecode_kernel<BITS, D, 4>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((qdecode_kernel<BITS, D, 8>), grid, dim3(256), 0, st, a);
+}
+
 void launch_qdecode(const DecodeArgs& a, int bits, int D, int n_seqs, hipStream_t st) {
-  dim3 grid(a.n_parts, a.Hkv, n_seqs);
-#define VKV_QD(B, DD) hipLaunchKernelGGL((qdecode_mfma_kernel<B, DD>), grid, dim3(256), 0, st, a)
+  const dim3 grid(a.n_parts, a.Hkv * qdecode_head_groups(a.rep), n_seqs);
   if (bits == 4) {
-    if (D == 64) VKV_QD(4, 64);
-    else VKV_QD(4, 128);
+    if (D == 64) launch_d<4, 64>(a, grid, st);
+    else if (D == 128) launch_d<4, 128>(a, grid, st);
+    else launch_d<4, 256>(a, grid, st);
   } else {
-    if (D == 64) VKV_QD(8, 64);
-    else VKV_QD(8, 128);
+    if (D == 64) launch_d<8, 64>(a, grid, st);
+    else if (D == 128) launch_d<8, 128>(a, grid, st);
+    else launch_d<8, 256>(a, grid, st);
   }
-#undef VKV_QD
   VKV_HIP(hipGetLastError());
   if (a.n_parts > 1) {
-    hipLaunchKernelGGL(qdecode_combine_kernel, dim3(static_cast<unsigned>(n_seqs) * a.Hq), dim3(128), 0,
-                       st, a, D);
+    hipLaunchKernelGGL(qdecode_combine_kernel, dim3(static_cast<unsigned>(n_seqs) * a.Hq),
+                       dim3(D >= 256 ? 256 : D), 0, st, a, D);
     VKV_HIP(hipGetLastError());
   }
 }

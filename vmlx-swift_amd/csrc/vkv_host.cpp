@@ -1228,4 +1228,5 @@ float* attention_workspace(hipStream_t st, size_t floats) {
   return static_cast<float*>(b.get());
 }
 
+
 }  // namespace vkv

@@ -140,11 +140,14 @@ struct DecodeArgs {
   const int32_t* seq_lens;   // nullptr = every sequence holds max_len tokens
   int32_t max_len;
   int32_t Hq, Hkv, rep;
-  int32_t part_blocks, n_parts;
-  float* ws_o;               // [n_seqs][Hq][n_parts][D]
-  float* ws_ml;              // [n_seqs][Hq][n_parts][2]
+  int32_t part_steps;        // 64-token steps per workgroup partition
+  int32_t n_parts;           // partitions per sequence (grid x)
+  float* ws_o;               // [n_seqs][Hq][n_parts][D] partial outputs
+  float* ws_ml;              // [n_seqs][Hq][n_parts][2] partial (max, sum)
 };
 bool qdecode_supported(int dtype, int bits, int D, int block_size, int rep, int group);
+// workgroups per (sequence, kv head): query heads are taken 4 or 8 at a time
+int qdecode_head_groups(int rep);
 void launch_qdecode(const DecodeArgs& a, int bits, int D, int n_seqs, hipStream_t st);
 
 // Block pairs passed by value to the block-copy kernel.
