@@ -11,7 +11,9 @@ sequence.  Synthetic data, generated on the GPU; all inputs are resident in
 HBM before timing starts.  The step writes the decode token at the same
 position each step, so every step does identical work.
 
-Prints one JSON line (see DESIGN.md for the field definitions).
+Prints one JSON line: "value" is the whole-step KV-read rate (appends included),
+"attention" and "roofline" time the paged decode call alone, "traffic" is the
+PMC-measured HBM bytes per decode launch, "cpu_baseline" times the C oracle.
 """
 import argparse
 import json
@@ -34,7 +36,39 @@ def parse():
     p.add_argument("--layers", type=int, default=32)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-threads", type=int, default=0)
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only run a plain 1 GiB device copy (vkv_array_copy) 5 times: the "
+                        "reference reading for the FETCH_SIZE / WRITE_SIZE counters")
     return p.parse_args()
+
+
+def pmc_traffic():
+    """HBM bytes per decode launch from the committed PMC summary (two
+    rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by a 1 GiB copy
+    calibration); None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "qdecode_config3_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    for line in open(path):
+        parts = line.split()
+        if len(parts) == 2 and not line.startswith("#"):
+            vals[parts[0]] = int(parts[1])
+    if "read_bytes" not in vals or "write_bytes" not in vals:
+        return None
+    return vals["read_bytes"] + vals["write_bytes"]
+
+
+def calibrate_copy(torch, vkv):
+    n = 1 << 28  # f32 elements = 1 GiB read + 1 GiB written per launch
+    a = torch.ones((1, 1, n // 64, 64), dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(5):
+        vkv._chk(vkv.lib().vkv_array_copy(vkv.C.byref(vkv.arr(a)), vkv.C.byref(vkv.arr(b)),
+                                          vkv.stream_ptr()))
+    torch.cuda.synchronize()
+    assert bool((b == 1).all())
+    print(json.dumps({"calibrate_copy_bytes_per_launch": 4 * n, "launches": 5}), flush=True)
 
 
 def build_scene(torch, vkv, layers, seed=3):
@@ -107,33 +141,47 @@ def build_scene(torch, vkv, layers, seed=3):
     return pool, sc
 
 
-def cpu_baseline(threads):
-    """The CPU oracle (C restatement of the reference arithmetic) on a bounded
-    sample of the same workload: 8 sequences x 2048 tokens, 32 query heads."""
+def cpu_baseline(threads, min_seconds=10.0):
+    """The CPU oracle (C restatement of the reference arithmetic, fp64,
+    OpenMP) on one layer of the same workload: the 64 config-3 sequences
+    (same lengths as the GPU scene), 8 KV / 32 query heads, 4-bit g64.
+    Passes are repeated until at least `min_seconds` of CPU time."""
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
+    H, Hq, D = 8, 32, 128
+    lens = (np.random.default_rng(3).integers(128, 8193, 64) + 1).astype(np.int32)
+    rows = lens.astype(np.int64) * H          # [H, T] rows per sequence
+    tok_off = np.concatenate([[0], np.cumsum(rows)[:-1]]).astype(np.int64)
+    total = int(rows.sum())
+    # quantize a 64K-row random pool, then tile it: values do not change
+    # the oracle's running time
     rng = np.random.default_rng(5)
-    n, T, H, Hq, D = 8, 2048, 8, 32, 128
-    x = O.from_f32(rng.standard_normal((n, H, T, D)).astype(np.float32), O.BF16)
-    kq, ks, kb, _ = O.quantize(x, O.BF16, 64, 4)
-    vq, vs, vb, _ = O.quantize(x[:, :, ::-1].copy(), O.BF16, 64, 4)
+    pool = O.from_f32(rng.standard_normal((65536, D)).astype(np.float32), O.BF16)
+    kq0, ks0, kb0, _ = O.quantize(pool, O.BF16, 64, 4)
+    vq0, vs0, vb0, _ = O.quantize(pool[::-1].copy(), O.BF16, 64, 4)
     f = lambda a: O.to_f32(a, O.BF16)
-    ks, kb, vs, vb = f(ks), f(kb), f(vs), f(vb)
-    q = f(O.from_f32(rng.standard_normal((n, Hq, D)).astype(np.float32), O.BF16))
-    lens = np.full(n, T, np.int32)
-    off = np.arange(n, dtype=np.int64) * H * T
+    tile = lambda a: np.resize(a, (total,) + a.shape[1:])
+    kq, vq = tile(kq0), tile(vq0)
+    ks, kb, vs, vb = tile(f(ks0)), tile(f(kb0)), tile(f(vs0)), tile(f(vb0))
+    q = f(O.from_f32(rng.standard_normal((len(lens), Hq, D)).astype(np.float32), O.BF16))
+    passes = 0
     t0 = time.perf_counter()
-    O.quantized_decode_batch(q, O.BF16, kq, ks, kb, vq, vs, vb, lens, off, H, D ** -0.5, 64, 4,
-                             threads=threads)
-    dt = time.perf_counter() - t0
-    byts = n * T * H * BYTES_PER_TOKEN_HEAD
+    while True:
+        O.quantized_decode_batch(q, O.BF16, kq, ks, kb, vq, vs, vb, lens, tok_off, H, D ** -0.5,
+                                 64, 4, threads=threads)
+        passes += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds:
+            break
+    byts = passes * int(lens.sum()) * H * BYTES_PER_TOKEN_HEAD
     return {"value": round(byts / dt / 1e9, 4), "unit": "GB/s", "cores": threads,
             "kind": "port",
-            "sample": f"{n} sequences x {T} tokens, 8 KV / 32 query heads, 4-bit g64, one layer, "
-                      f"{dt:.2f} s, C oracle (fp64 restatement of the reference arithmetic)"}
+            "sample": f"one config-3 layer: 64 sequences ({int(lens.sum())} tokens) x 8 KV / 32 "
+                      f"query heads, 4-bit g64; {passes} passes in {dt:.1f} s; C oracle (fp64 "
+                      f"restatement of the reference arithmetic, OpenMP, {threads} threads)"}
 
 
 def main():
@@ -148,6 +196,9 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     torch.cuda.set_device(0)
+    if args.calibrate_copy:
+        calibrate_copy(torch, vkv)
+        return
     layers = args.layers
     pool, sc = build_scene(torch, vkv, layers)
     stream = torch.cuda.current_stream()
@@ -230,7 +281,8 @@ def main():
                    "ms_per_layer": round(app_avg_ms, 5),
                    "tokens_per_s": round(append_tokens / (app_avg_ms * 1e-3), 1)},
         "roofline": {"bound": "hbm", "achieved": round(att_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(att_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(att_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": pmc_traffic()},
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
