@@ -207,11 +207,12 @@ def test_generic_and_matrix_core_paths_agree(monkeypatch):
     assert np.abs(fast - slow).max() <= 2e-2
 
 
-@pytest.mark.parametrize("part_steps", ["1", "3", "64"])
-def test_decode_partition_sizes_agree(monkeypatch, part_steps):
-    """Partitions of 1 step (most waves of a workgroup idle), an odd size
-    and one partition per sequence give the same output within fp32
-    rounding of the merge order."""
+@pytest.mark.parametrize("waves", ["1", "7", "5000"])
+def test_decode_wave_counts_agree(monkeypatch, waves):
+    """The fewest waves (the longest ranges, each crossing many sequence and
+    head segments), an odd count, and more waves than units (one unit each,
+    most waves idle) give the same output within fp32 rounding of the merge
+    order, and repeated launches give identical bits."""
     dtype, bits = O.BF16, 4
     rng = np.random.default_rng(91)
     P = Paged(rng, bits, dtype, n_seqs=5, n_share=2, max_len=900, nblocks=200)
@@ -219,9 +220,9 @@ def test_decode_partition_sizes_agree(monkeypatch, part_steps):
     view = P.view()
     q = dev(rand_bits(rng, (len(P.lens), 32, 128), dtype), dtype)
     base = values(vkv.paged_attention(q, view, 0.088), dtype)
-    monkeypatch.setenv("VKV_PART_STEPS", part_steps)
+    monkeypatch.setenv("VKV_DECODE_WAVES", waves)
     got = values(vkv.paged_attention(q, view, 0.088), dtype)
-    for _ in range(2):  # counters are left at zero for the next launch
+    for _ in range(2):
         again = values(vkv.paged_attention(q, view, 0.088), dtype)
         assert np.array_equal(again, got)
     assert np.abs(base - got).max() <= 2e-2

@@ -311,7 +311,14 @@ int vkv_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vk
     if (!kv->block_table) throw Error("view has no block table");
     const bool keys_only = (kv->flags & VKV_VIEW_KEYS_ONLY) != 0;
     const int rep = static_cast<int>(q->shape[1] / kv->n_kv_heads);
-    if (kv->bits > 0 && !keys_only && !getenv("VKV_GENERIC_ATTENTION") &&
+    // the matrix-core kernel loads queries 16 bytes and stores outputs 8
+    // bytes at a time
+    const bool aligned = (reinterpret_cast<uintptr_t>(q->data) % 16 == 0) &&
+                         q->strides[0] % 8 == 0 && q->strides[1] % 8 == 0 &&
+                         (reinterpret_cast<uintptr_t>(out->data) % 8 == 0) &&
+                         out->strides[0] % 4 == 0 && out->strides[1] % 4 == 0;
+    if (kv->bits > 0 && !keys_only && aligned && kv->max_len <= qdecode_max_len() &&
+        !getenv("VKV_GENERIC_ATTENTION") &&
         qdecode_supported(kv->dtype, kv->bits, kv->head_dim, kv->block_size, rep, kv->group_size)) {
       // matrix-core path (vkv_decode.hip)
       KVSrc src = kvsrc_from_view(*kv);
@@ -337,23 +344,15 @@ int vkv_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vk
       d.Hq = static_cast<int32_t>(q->shape[1]);
       d.Hkv = kv->n_kv_heads;
       d.rep = rep;
-      // partitions of 64-token steps: about 512 workgroups (two per CU) over
-      // the grid's upper bound, 4..64 steps (1..16 per wave) each; a
-      // partition costs a set-up and a pipeline fill, so fewer is better
-      const int64_t max_steps = (static_cast<int64_t>(kv->max_len) + 63) / 64;
-      const int64_t units = max_steps * kv->n_kv_heads * kv->n_seqs;
-      int64_t ps = (units + 511) / 512;
-      ps = std::min<int64_t>(64, std::max<int64_t>(4, (ps + 3) / 4 * 4));
-      if (const char* e = getenv("VKV_PART_STEPS")) ps = std::min(64, std::max(1, atoi(e)));
-      d.part_steps = static_cast<int32_t>(ps);
-      d.n_parts = static_cast<int32_t>(std::max<int64_t>(1, (max_steps + ps - 1) / ps));
-      if (d.n_parts > 1) {
-        const size_t per = static_cast<size_t>(kv->n_seqs) * d.Hq * d.n_parts;
-        float* ws = attention_workspace(S(stream), per * (kv->head_dim + 2));
-        d.ws_o = ws;
-        d.ws_ml = ws + per * kv->head_dim;
-      }
-      launch_qdecode(d, kv->bits, kv->head_dim, kv->n_seqs, S(stream));
+      d.n_seqs = kv->n_seqs;
+      int want = 0;
+      if (const char* e = getenv("VKV_DECODE_WAVES")) want = std::max(1, atoi(e));
+      d.n_waves = want;  // 0 = choose per launch
+      const int chunk = std::min(kv->n_seqs, qdecode_max_seqs());
+      const int w_max = qdecode_waves(chunk, kv->n_kv_heads, rep, kv->max_len, want);
+      d.ws = attention_workspace(
+          S(stream), qdecode_workspace_floats(chunk, kv->n_kv_heads, rep, kv->head_dim, w_max));
+      launch_qdecode(d, kv->bits, kv->head_dim, S(stream));
       return;
     }
     AttnArgs a{};

@@ -41,15 +41,19 @@
 // than kTau), which needs no cross-lane reduction on the common path and
 // bounds probabilities by e^kTau.
 //
-// Workgroup = 4 waves = (partition of steps, kv head and head group,
-// sequence); waves take
-// the partition's steps round robin, with the next step's loads in flight
-// while the current one computes when the per-step operands fit in
-// registers twice.  A sequence that fits one partition is written directly;
-// longer ones leave per-partition partials that qdecode_combine_kernel
-// merges.  (Merging in the last workgroup to finish would need device-scope
-// release/acquire fences, which on gfx950 write back and invalidate the
-// XCD's whole L2 and cost more than the extra launch.)
+// Work split.  The (sequence, kv head, head group, 64-token step) units of
+// the whole batch are laid end to end and every wave (one per workgroup)
+// takes an equal contiguous range of them, so mixed sequence lengths cost
+// no load imbalance.  A range crosses a few (sequence, head) segments; at
+// each boundary the wave finalizes the segment (the output itself when the
+// segment covers the whole sequence, else an (o, max, sum) partial that
+// qdecode_combine_kernel merges, as sdpa_vector_2pass_2 merges) and
+// rebuilds its wave-local query table.  The next unit's KV loads, and the
+// queries of the next unit's segment, are in flight while the current unit
+// computes.  (Merging partials in the last wave to finish would need
+// device-scope release/acquire fences, which on gfx950 write back and
+// invalidate the XCD's whole L2 and cost more than the extra launch.)
+#include <algorithm>
 #include <utility>
 
 #include "vkv_device.h"
@@ -70,9 +74,15 @@ typedef __attribute__((address_space(1))) const u32x2_t g_u32x2_t;
 typedef __attribute__((address_space(1))) const uint32_t g_u32_t;
 
 constexpr float kTau = 8.0f;
-constexpr int kWaves = 4;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kMaxPartSteps = 64;  // 64-token steps per workgroup partition, at most
+
+// 2^x with the hardware v_exp_f32 (results below 2^-126 flush to zero,
+// which is immaterial for softmax weights; exp2f adds a denormal-safe
+// rescaling around it).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+constexpr int kMaxRange = 64;   // units (64-token steps) per wave, at most
+constexpr int kMaxSeqs = 256;   // sequences per launch (the host splits larger batches)
+constexpr int kMaxParts = 32;   // partials per (sequence, head pair), at most
 
 template <int... Is, class F>
 __device__ __forceinline__ void sfor_impl(std::integer_sequence<int, Is...>, F&& f) {
@@ -149,7 +159,9 @@ __device__ __forceinline__ uint32_t row_read(uint32_t x) {
   if constexpr (K == 0) {
     return x;
   } else {
-    return __builtin_amdgcn_update_dpp(0u, x, 0x120 + (16 - K), 0xF, 0xF, false);
+    // mov_dpp has no "old" operand (all lanes are written), so the compiler
+    // does not materialize one first
+    return __builtin_amdgcn_mov_dpp(x, 0x120 + (16 - K), 0xF, 0xF, false);
   }
 }
 template <int K>
@@ -181,18 +193,36 @@ __device__ __forceinline__ void load_words(const uint8_t* p, uint32_t* out) {
   }
 }
 
+// x *= a in place.  The rescale runs in a rarely taken branch; tying the
+// product to its source register keeps the compiler from renaming the
+// accumulators there and copying them back on the common path.
+__device__ __forceinline__ void scale_inplace(f32x4_t& x, float a) {
+#pragma unroll
+  for (int e = 0; e < 4; e++) asm volatile("v_mul_f32 %0, %1, %0" : "+v"(x[e]) : "v"(a));
+}
+
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
-// LDS-only barrier: orders LDS traffic across the workgroup but leaves
-// global loads in flight (a plain __syncthreads waits for them).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+// Orders one wave's LDS writes before its later LDS reads by other lanes
+// (no workgroup barrier: every workgroup is a single wave).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
 }
 
 template <int BITS, int D, int HP>
@@ -209,6 +239,8 @@ struct QD {
   static constexpr int ROW = D * BITS / 8;    // key code bytes per token
   static constexpr int SBW = 2 * G;           // scale/bias words per token (K, V)
   static constexpr int QROW = 16 * SPW + 1;   // query-table entries per slice
+  static constexpr int QCH = HP * D / 8;      // 8-dim query chunks of a head group
+  static constexpr int QPL = (QCH + 63) / 64; // query chunks per lane
   static constexpr float MAG = (BITS == 4) ? 128.0f : 2176.0f;
   static constexpr float C0 = (BITS == 4) ? 8.0f : 128.0f;
   // per-step operand registers; steps are double buffered when they fit
@@ -222,156 +254,258 @@ struct QD {
   };
 };
 
+// One wave per workgroup; see the header comment for the work split.
+// Two waves per SIMD (256 VGPRs each) up to D = 128, one for D = 256.
 template <int BITS, int D, int HP>
-__global__ void __launch_bounds__(256, (D >= 256) ? 1 : 2) qdecode_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((D >= 256) ? 1 : 2)))
+qdecode_kernel(DecodeArgs a) {
   using C = QD<BITS, D, HP>;
   constexpr int G = C::G, PP = C::PP, TT = C::TT, SPW = C::SPW, SL = C::SL;
   constexpr int RUN = C::RUN, NT = C::NT, VW = C::VW, ROW = C::ROW, SBW = C::SBW;
-  constexpr int QROW = C::QROW;
+  constexpr int QROW = C::QROW, QCH = C::QCH, QPL = C::QPL;
   constexpr float MAG = C::MAG, C0 = C::C0;
   using Buf = typename C::Buf;
+  constexpr int QT_ENTRIES = SL * QROW;
+  static_assert(QT_ENTRIES * 16 >= kMaxSeqs * 8, "the sequence scan reuses the query table");
 
-  // LDS: the query table (score B operands) during the step loop, the
-  // per-wave results after it.
-  constexpr int QT_BYTES = SL * QROW * 16;
-  constexpr int FIN_BYTES = kWaves * HP * D * 4;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[QT_BYTES > FIN_BYTES ? QT_BYTES : FIN_BYTES];
-  __shared__ float qf[HP][D + 1];
-  __shared__ float sqs[HP][G];
-  __shared__ int32_t sblk[2 * kMaxPartSteps];  // pool block of each sub-block
-  __shared__ float fin_s[kWaves][HP][2];
-  u32x4_t* qtab = reinterpret_cast<u32x4_t*>(smem);
-  float(*fin_o)[HP][D] = reinterpret_cast<float(*)[HP][D]>(smem);
+  // LDS (all private to the wave): the score B operands, the KV chunk of
+  // every 32-token sub-block of the range, and the range's segments.  The
+  // per-sequence unit prefix of the set-up lives in the query table's space.
+  __shared__ u32x4_t qtab[QT_ENTRIES];
+  __shared__ int64_t sub_off[2 * kMaxRange];  // chunk byte offset (block, kv head)
+  __shared__ int32_t sub_t0[2 * kMaxRange];   // first token of the sub-block in its block
+  __shared__ int32_t seg_tab[kMaxRange][6];   // seq, pair, first step, units, len, first unit
+  __shared__ int32_t seq_len[kMaxSeqs];
+  int32_t* seq_cum = reinterpret_cast<int32_t*>(qtab);
+  int32_t* seq_nst = seq_cum + kMaxSeqs;
 
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  const int lane = tid & 63, n = lane & 15, lg = lane >> 4;
-  const int part = blockIdx.x, seq = blockIdx.z;
-  const int rep = a.rep;
-  const int n_hg = (rep + HP - 1) / HP;  // head groups of HP query heads
-  const int hk = blockIdx.y / n_hg, hg = blockIdx.y % n_hg;
-  const int nh = min(HP, rep - hg * HP);  // query heads of this workgroup
-  // first query head of the group, and its (sequence, head) row
-  const int64_t hq0 = static_cast<int64_t>(hk) * rep + hg * HP;
-  const int64_t rh0 = static_cast<int64_t>(seq) * a.Hq + hq0;
-  const int len = a.seq_lens ? a.seq_lens[seq] : a.max_len;
-  const int nstep = (len + 63) >> 6;
-  // balanced partitions: parts_used pieces of at most part_steps steps
-  const int parts_used = (nstep + a.part_steps - 1) / a.part_steps;
-  if (part >= parts_used) {
-    if (nstep == 0 && part == 0) {  // empty sequence: zero output
-      for (int idx = tid; idx < nh * D; idx += 256)
-        a.out[seq * a.o_ss + (hq0 + idx / D) * a.o_sh + idx % D] = 0;
-    }
-    return;
-  }
-  const int span = (nstep + parts_used - 1) / parts_used;  // <= part_steps
-  const int st0 = part * span;                              // < nstep
-  const int st1 = min(nstep, st0 + span);
-  const int nsub = (len + 31) >> 5;
+  const int lane = threadIdx.x, n = lane & 15, lg = lane >> 4;
+  const int w = blockIdx.x, W = gridDim.x;
+  const int rep = a.rep, n_hg = (rep + HP - 1) / HP, HG = a.Hkv * n_hg;
+  const int ns = a.n_seqs;
   const int subs = a.block_size >> 5;  // 32-token sub-blocks per pool block
-  const int32_t* table = a.table + static_cast<int64_t>(seq) * a.table_stride;
-  const uint8_t* head_base = a.base + static_cast<int64_t>(hk) * a.head_bytes;
-
   // this lane's roles: score column (part p, head h); key-operand lane
   // group (part pA, unit slot wA)
   const int p = n / HP, h = n % HP;
   const int pA = lg / SPW, wA = lg % SPW;
 
-  // direct: read the block table from memory (the first step, issued
-  // before the LDS copy of the partition's table slice exists)
-  auto load_step = [&](int stp, Buf& b, bool direct) {
-    const uint8_t* cb[2];
-    int t0[2];
+  // ---- units per sequence (steps x head pairs) and their prefix sums
+  int carry = 0, max_nst = 0;
+  for (int s0 = 0; s0 < ns; s0 += 64) {
+    const int s = s0 + lane;
+    const int len = (s < ns) ? (a.seq_lens ? a.seq_lens[s] : a.max_len) : 0;
+    const int nst = (len + 63) >> 6;
+    const int incl = wave_incl_scan(nst * HG, lane);
+    if (s < ns) {
+      seq_cum[s] = carry + incl - nst * HG;
+      seq_nst[s] = nst;
+      seq_len[s] = len;
+    }
+    carry += __shfl(incl, 63);
+    max_nst = max(max_nst, nst);
+  }
+  wave_lds_sync();
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) max_nst = max(max_nst, __shfl_xor(max_nst, o));
+  const int U = __builtin_amdgcn_readfirstlane(carry);
+  if (w == 0) {  // empty sequences: zero output
+    for (int s = 0; s < ns; s++) {
+      if (seq_nst[s] != 0) continue;
+      for (int idx = lane; idx < a.Hq * D; idx += 64)
+        a.out[s * a.o_ss + (idx / D) * a.o_sh + idx % D] = 0;
+    }
+  }
+  // units per wave: W ranges (<= kMaxRange units, by the host's choice of
+  // W), and at least max_nst / (kMaxParts - 1) so that no pair is split
+  // into more than kMaxParts partials
+  const int cper = max((U + W - 1) / W, (max_nst + kMaxParts - 2) / (kMaxParts - 1));
+  const int u0 = w * cper;
+  if (u0 >= U) return;
+  const int u1 = min(U, u0 + cper);
+  const int nunits = u1 - u0;
+
+  // ---- the range's segments: maximal runs of units in one (seq, pair)
+  int nseg = 0;
+  {
+    // the last sequence whose prefix is <= u0: count them, 64 at a time
+    int cnt = 0;
+    for (int s0 = 0; s0 < ns; s0 += 64) {
+      const int s = s0 + lane;
+      cnt += __popcll(__builtin_amdgcn_ballot_w64(s < ns && seq_cum[s] <= u0));
+    }
+    int ss = cnt - 1, u = u0;
+    while (u < u1) {
+      while (seq_nst[ss] == 0) ss++;
+      const int nst = seq_nst[ss];
+      const int local = u - seq_cum[ss];
+      const int j = local / nst, t = local % nst;
+      const int take = min(u1 - u, nst - t);
+      if (lane == 0) {
+        seg_tab[nseg][0] = ss;
+        seg_tab[nseg][1] = j;
+        seg_tab[nseg][2] = t;
+        seg_tab[nseg][3] = take;
+        seg_tab[nseg][4] = seq_len[ss];
+        seg_tab[nseg][5] = u - u0;
+      }
+      nseg++;
+      u += take;
+      if (t + take == nst && j == HG - 1) ss++;
+    }
+  }
+  wave_lds_sync();
+
+  // ---- block-table slice: the chunk of each sub-block of the range.  These
+  // loads, then the first segment's queries, are issued before any KV load
+  // (global loads complete in issue order, so later set-up loads would wait
+  // for the KV data).
+  int64_t my_off[2];
+  int32_t my_t0[2];
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const int e = lane + 64 * r, ui = min(e >> 1, nunits - 1);
+    int k = 0;
+    for (int kk = 1; kk < nseg; kk++)
+      if (seg_tab[kk][5] <= ui) k = kk;
+    const int seq = seg_tab[k][0], j = seg_tab[k][1];
+    const int step = seg_tab[k][2] + (ui - seg_tab[k][5]);
+    const int nsub = (seg_tab[k][4] + 31) >> 5;
+    const int sbi = min(2 * step + (e & 1), nsub - 1);
+    const int64_t blk = a.table[static_cast<int64_t>(seq) * a.table_stride + sbi / subs];
+    my_off[r] = blk * a.block_bytes + static_cast<int64_t>(j / n_hg) * a.head_bytes;
+    my_t0[r] = (sbi % subs) * 32;
+  }
+  // queries of segment k's head group: 8 dims (16 bytes) per chunk
+  auto load_q = [&](int k, u32x4_t* qr) {
+    const int seq = seg_tab[k][0], j = seg_tab[k][1];
+    const int64_t hq0 = static_cast<int64_t>(j / n_hg) * rep + (j % n_hg) * HP;
+    const int nh = min(HP, rep - (j % n_hg) * HP);
+#pragma unroll
+    for (int c = 0; c < QPL; c++) {
+      const int ci = min(lane + 64 * c, QCH - 1), r = min(ci / (D / 8), nh - 1);
+      qr[c] = *(g_u32x4_t*)(a.q + seq * a.q_ss + (hq0 + r) * a.q_sh + 8 * (ci % (D / 8)));
+    }
+  };
+  u32x4_t qpre[QPL];
+  load_q(0, qpre);
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const int e = lane + 64 * r;
+    if (e < 2 * kMaxRange) {
+      sub_off[e] = my_off[r];
+      sub_t0[e] = my_t0[r];
+    }
+  }
+  // the zero entry of every query-table slice (lanes outside a column's part)
+  for (int sg = lane; sg < SL; sg += 64) qtab[sg * QROW + 16 * SPW] = u32x4_t{0u, 0u, 0u, 0u};
+  wave_lds_sync();
+
+  // ---- per-unit loads
+  // This lane's byte offsets from a 32-token sub-block's two scalar bases
+  // (codes: chunk + first token * ROW; scale/bias: chunk + first token *
+  // SBW * 4); tile tau's key row and scored tokens sit in sub-block ks / ss.
+  int32_t k_lane[TT], sb_lane[TT];
+  int ks_sub[TT], ss_sub[TT];
+#pragma unroll
+  for (int tau = 0; tau < TT; tau++) {
+    const int c = tau * PP + pA, c2 = tau * PP + p;
+    ks_sub[tau] = c >> 1;
+    k_lane[tau] = a.kc_off + (8 * (n >> 2) + tok_off<BITS>(c & 1, n & 3)) * ROW + wA * RUN * 4;
+    ss_sub[tau] = c2 >> 1;
+    sb_lane[tau] = a.sb_off + (8 * lg + tok_off<BITS>(c2 & 1, 0)) * SBW * 4;
+  }
+  const int32_t v_lane = a.vc_off + (lg * 16 + n) * VW * 4;
+  auto load_step = [&](int ui, Buf& b) {
+    const uint8_t* bc[2];  // codes base of each sub-block
+    const uint8_t* bs[2];  // scale/bias base
 #pragma unroll
     for (int s = 0; s < 2; s++) {
-      const int sbi = min(2 * stp + s, nsub - 1);
-      const int64_t blk =
-          direct ? table[sbi / subs] : __builtin_amdgcn_readfirstlane(sblk[sbi - 2 * st0]);
-      cb[s] = head_base + blk * a.block_bytes;
-      t0[s] = (sbi % subs) * 32;
+      const uint8_t* cb = a.base + __builtin_amdgcn_readfirstlane(sub_off[2 * ui + s]);
+      const int t0 = __builtin_amdgcn_readfirstlane(sub_t0[2 * ui + s]);
+      bc[s] = cb + t0 * ROW;
+      bs[s] = cb + t0 * SBW * 4;
     }
 #pragma unroll
     for (int tau = 0; tau < TT; tau++) {
-      {  // key row of token 8 (n / 4) + off(q, n % 4) of part (tau, pA)
-        const int c = tau * PP + pA, s = c >> 1, q = c & 1;
-        const int t = t0[s] + 8 * (n >> 2) + tok_off<BITS>(q, n & 3);
-        const uint8_t* row = cb[s] + a.kc_off + static_cast<int64_t>(t) * ROW;
+      const uint8_t* row = (ks_sub[tau] ? bc[1] : bc[0]) + k_lane[tau];
 #pragma unroll
-        for (int rho = 0; rho < PP; rho++)
-          load_words<RUN>(row + (rho * SPW + wA) * RUN * 4, b.kw[tau][rho]);
-      }
-      {  // scale/bias of the tokens this lane scores (column part p)
-        const int c = tau * PP + p, s = c >> 1, q = c & 1;
+      for (int rho = 0; rho < PP; rho++) load_words<RUN>(row + rho * SPW * RUN * 4, b.kw[tau][rho]);
+      const uint8_t* sbp = (ss_sub[tau] ? bs[1] : bs[0]) + sb_lane[tau];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int t = t0[s] + 8 * lg + tok_off<BITS>(q, i);
-          load_words<SBW>(cb[s] + a.sb_off + static_cast<int64_t>(t) * SBW * 4, b.sb[tau][i]);
-        }
-      }
+      for (int i = 0; i < 4; i++)
+        load_words<SBW>(sbp + (tok_off<BITS>(0, i) - tok_off<BITS>(0, 0)) * SBW * 4, b.sb[tau][i]);
     }
 #pragma unroll
-    for (int s = 0; s < 2; s++)
-      load_words<VW>(cb[s] + a.vc_off + t0[s] * ROW + (lg * 16 + n) * VW * 4, b.vw[s]);
+    for (int s = 0; s < 2; s++) load_words<VW>(bc[s] + v_lane, b.vw[s]);
   };
 
-  // Global loads complete in issue order (one wait counter), so the set-up
-  // reads (table slice, queries) are issued before the first step's KV
-  // loads, which then stay in flight while the set-up uses them.  Every
-  // load here is unconditional (clamped indices): a load under a branch
-  // makes the compiler wait for all outstanding loads at the join.
-  constexpr int QPT = (HP * D + 255) / 256;  // query elements per thread
-  const int n_sub_part = 2 * (st1 - st0);  // <= 2 * kMaxPartSteps <= 256
-  const int32_t my_blk = table[min(2 * st0 + tid, nsub - 1) / subs];
-  uint16_t qraw[QPT];
-#pragma unroll
-  for (int j = 0; j < QPT; j++) {
-    const int i = tid + 256 * j, r = min(i / D, nh - 1), d = i % D;
-    qraw[j] = a.q[seq * a.q_ss + (hq0 + r) * a.q_sh + d];
-  }
   Buf bufA, bufB;
-  int step = st0 + wave;
-  load_step(min(step, st1 - 1), bufA, true);  // in flight during the set-up
+  load_step(0, bufA);
   const Magic mg;
-  if (tid < n_sub_part) sblk[tid] = my_blk;  // the partition's block-table slice
-  // ---- queries of the group's heads, scaled in bf16; rows >= nh are 0
   const float scale_t = round_to<kBF16>(a.scale);
+
+  // ---- segment state
+  int k = 0;             // current segment
+  int seg_seq = 0, seg_j = 0, seg_t = 0, seg_take = 0, seg_len = 0, seg_first = 0, nh = 0;
+  float sq[G];
+  // query table of segment kk from its prefetched chunks: entry (slice sg,
+  // column nn, unit slot ws) holds unit sg * SPW + ws of head nn % HP in the
+  // key operand's K order; sq = each head's bf16 query sum per group
+  auto setup_segment = [&](int kk, const u32x4_t* qr) {
+    seg_seq = __builtin_amdgcn_readfirstlane(seg_tab[kk][0]);
+    seg_j = __builtin_amdgcn_readfirstlane(seg_tab[kk][1]);
+    seg_t = __builtin_amdgcn_readfirstlane(seg_tab[kk][2]);
+    seg_take = __builtin_amdgcn_readfirstlane(seg_tab[kk][3]);
+    seg_len = __builtin_amdgcn_readfirstlane(seg_tab[kk][4]);
+    seg_first = __builtin_amdgcn_readfirstlane(seg_tab[kk][5]);
+    nh = min(HP, rep - (seg_j % n_hg) * HP);
+    float part[QPL][G];
 #pragma unroll
-  for (int j = 0; j < QPT; j++) {
-    const int i = tid + 256 * j;
-    const float v = round_to<kBF16>(bf16_to_f32(qraw[j]) * scale_t);
-    if (i < HP * D) qf[i / D][i % D] = (i / D < nh) ? v : 0.0f;
-  }
-  lds_barrier();
-  // query table: entry (slice sg, column nn, unit slot w) holds the 8 dims
-  // of unit sg * SPW + w of head nn % HP in the key operand's K order;
-  // entry 16 * SPW of every slice is zero (lanes outside the column's part)
-  for (int e = tid; e < SL * QROW; e += 256) {
-    const int sg = e / QROW, r = e % QROW;
-    u32x4_t v = {0u, 0u, 0u, 0u};
-    if (r < 16 * SPW) {
-      const int nn = r / SPW, w = r % SPW;
-      const int unit = sg * SPW + w;
-      const float* qrow = qf[nn % HP];
+    for (int c = 0; c < QPL; c++) {
+      const int ci = lane + 64 * c;
+      const int r = ci / (D / 8), unit = ci % (D / 8);
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        v[2 * e] = round_to<kBF16>(bf_lo(qr[c][e]) * scale_t);
+        v[2 * e + 1] = round_to<kBF16>(bf_hi(qr[c][e]) * scale_t);
+      }
+      const bool live = ci < QCH && r < nh;
+      float sum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        v[e] = live ? v[e] : 0.0f;
+        sum += v[e];
+      }
+      u32x4_t ent;
 #pragma unroll
       for (int pr = 0; pr < 4; pr++)
-        v[pr] = pack_bf16(qrow[8 * unit + kslot<BITS>(2 * pr)], qrow[8 * unit + kslot<BITS>(2 * pr + 1)]);
+        ent[pr] = pack_bf16(v[kslot<BITS>(2 * pr)], v[kslot<BITS>(2 * pr + 1)]);
+      if (ci < QCH) {
+        const int sg = unit / SPW, ws = unit % SPW;
+#pragma unroll
+        for (int pp = 0; pp < PP; pp++) qtab[sg * QROW + (r + pp * HP) * SPW + ws] = ent;
+      }
+      // group sums: the 8 chunks of a (head, group) are 8 adjacent lanes
+      sum += __shfl_xor(sum, 1);
+      sum += __shfl_xor(sum, 2);
+      sum += __shfl_xor(sum, 4);
+#pragma unroll
+      for (int g = 0; g < G; g++) {
+        const int src = h * (D / 8) + 8 * g;  // chunk holding (head h, group g)
+        const float x = __shfl(sum, src % 64);
+        part[c][g] = (src / 64 == c) ? x : 0.0f;
+      }
     }
-    qtab[e] = v;
-  }
-  // sum of each head's bf16 queries per group: 32 lanes per (head, group)
-  for (int rg = tid >> 5; rg < HP * G; rg += 8) {
-    const int r = rg / G, g = rg % G, j = tid & 31;
-    float s = qf[r][g * 64 + j] + qf[r][g * 64 + j + 32];
 #pragma unroll
-    for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o, 32);
-    if (j == 0) sqs[r][g] = s;
-  }
-  lds_barrier();
-  float sq[G];
+    for (int g = 0; g < G; g++) {
+      sq[g] = 0.0f;
 #pragma unroll
-  for (int g = 0; g < G; g++) sq[g] = sqs[h][g];
-  const u32x4_t* qlane = qtab + ((pA == p) ? n * SPW + wA : 16 * SPW);
+      for (int c = 0; c < QPL; c++) sq[g] += part[c][g];
+    }
+    wave_lds_sync();
+  };
+  setup_segment(0, qpre);
 
   f32x4_t oacc[NT];
 #pragma unroll
@@ -379,8 +513,10 @@ __global__ void __launch_bounds__(256, (D >= 256) ? 1 : 2) qdecode_kernel(Decode
   float m_run = -INFINITY, l_run = 0.0f, corr[G];
 #pragma unroll
   for (int g = 0; g < G; g++) corr[g] = 0.0f;
+  const u32x4_t* qlane = qtab + ((pA == p) ? n * SPW + wA : 16 * SPW);
 
   auto compute_step = [&](int stp, const Buf& b) {
+    const int len = seg_len;
     // ---- scores: acc[tau][g] = q . (MAG + c) over group g's dims
     f32x4_t acc[TT][G];
 #pragma unroll
@@ -391,20 +527,24 @@ __global__ void __launch_bounds__(256, (D >= 256) ? 1 : 2) qdecode_kernel(Decode
     // barrier keeps the compiler from issuing every slice's LDS read up front
     constexpr int kQA = SL < 4 ? SL : 4;
     u32x4_t qring[kQA];
+    // slices in group-interleaved order, so consecutive MFMAs feed
+    // independent accumulators
+    auto slice = [](int o) { return (o % G) * (SL / G) + o / G; };
 #pragma unroll
-    for (int j = 0; j < kQA; j++) qring[j] = qlane[j * QROW];
+    for (int jj = 0; jj < kQA; jj++) qring[jj] = qlane[slice(jj) * QROW];
 #pragma unroll
-    for (int sg = 0; sg < SL; sg++) {
-      const u32x4_t qb = qring[sg % kQA];
-      if (sg + kQA < SL) qring[sg % kQA] = qlane[(sg + kQA) * QROW];
-      const int g = sg / (SL / G), rho = sg % PP, k = sg / PP;
+    for (int o = 0; o < SL; o++) {
+      const int sg = slice(o);
+      const u32x4_t qb = qring[o % kQA];
+      if (o + kQA < SL) qring[o % kQA] = qlane[slice(o + kQA) * QROW];
+      const int g = sg / (SL / G), rho = sg % PP, kq = sg / PP;
 #pragma unroll
       for (int tau = 0; tau < TT; tau++) {
         if constexpr (BITS == 4) {
-          acc[tau][g] = mfma(nib_magic(b.kw[tau][rho][k], mg), qb, acc[tau][g]);
+          acc[tau][g] = mfma(nib_magic(b.kw[tau][rho][kq], mg), qb, acc[tau][g]);
         } else {
           u32x4_t lo, hi;
-          byte_magic(b.kw[tau][rho][2 * k], b.kw[tau][rho][2 * k + 1], mg, lo, hi);
+          byte_magic(b.kw[tau][rho][2 * kq], b.kw[tau][rho][2 * kq + 1], mg, lo, hi);
           acc[tau][g] = mfma(lo, qb, acc[tau][g]);
           acc[tau][g] = mfma(hi, qb, acc[tau][g]);
         }
@@ -429,6 +569,7 @@ __global__ void __launch_bounds__(256, (D >= 256) ? 1 : 2) qdecode_kernel(Decode
         sc[tau][i] = s;
       }
     if (stp * 64 + 64 > len) {  // the sequence ends inside this step
+      asm volatile("");  // a real branch: keeps the masking off the common path
 #pragma unroll
       for (int tau = 0; tau < TT; tau++) {
         const int c = tau * PP + p, s = c >> 1, q = c & 1;
@@ -446,17 +587,12 @@ __global__ void __launch_bounds__(256, (D >= 256) ? 1 : 2) qdecode_kernel(Decode
     }
 
     // ---- online softmax with a lazily refreshed max
-    bool need = false;
+    float mx = -INFINITY;
 #pragma unroll
     for (int tau = 0; tau < TT; tau++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) need |= sc[tau][i] > m_run + kTau;
-    if (__builtin_amdgcn_ballot_w64(need)) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int tau = 0; tau < TT; tau++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) mx = fmaxf(mx, sc[tau][i]);
+      for (int i = 0; i < 4; i++) mx = fmaxf(mx, sc[tau][i]);
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + kTau)) {
       // max over the lanes of head h: the other parts of the row, other rows
 #pragma unroll
       for (int o = HP; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
@@ -468,9 +604,10 @@ __global__ void __launch_bounds__(256, (D >= 256) ? 1 : 2) qdecode_kernel(Decode
       l_run *= alpha;
 #pragma unroll
       for (int g = 0; g < G; g++) corr[g] *= alpha;
-      // the P.V accumulators of lane n + 16 lg carry head n = h for n < HP
+      // the P.V accumulators of lane n + 16 lg carry head n = h for n < HP;
+      // a new segment starts with m_run = -inf, so alpha = 0 also clears them
 #pragma unroll
-      for (int t = 0; t < NT; t++) oacc[t] *= alpha;
+      for (int t = 0; t < NT; t++) scale_inplace(oacc[t], alpha);
     }
     const float m2 = fmaxf(m_run * kLog2e, -3.402823466e38f);
     float pr[TT][4];
@@ -478,7 +615,7 @@ __global__ void __launch_bounds__(256, (D >= 256) ? 1 : 2) qdecode_kernel(Decode
     for (int tau = 0; tau < TT; tau++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        pr[tau][i] = exp2f(fmaf(sc[tau][i], kLog2e, -m2));
+        pr[tau][i] = fast_exp2(fmaf(sc[tau][i], kLog2e, -m2));
         l_run += pr[tau][i];
       }
 
@@ -497,10 +634,13 @@ __global__ void __launch_bounds__(256, (D >= 256) ? 1 : 2) qdecode_kernel(Decode
           const uint32_t pl = pack_bf16(P0 - h0, P1 - h1);
           pk[tau][pi][g][0] = ph;
           pk[tau][pi][g][1] = pl;
+          // the offset uses the fp32 P: hi + lo differs from it by the
+          // rounding of lo (~2^-17 P), which times MAG + C0 stays far
+          // below the output's own rounding
           float cc = corr[g];
           cc = fmaf(pr[tau][i0], fmaf(C0, vs[tau][i0][g], vb[tau][i0][g]), cc);
           cc = fmaf(pr[tau][i1], fmaf(C0, vs[tau][i1][g], vb[tau][i1][g]), cc);
-          cc = fmaf(-(MAG + C0), (h0 + h1) + (bf_lo(pl) + bf_hi(pl)), cc);
+          cc = fmaf(-(MAG + C0), P0 + P1, cc);
           corr[g] = cc;
         }
 
@@ -537,113 +677,152 @@ __global__ void __launch_bounds__(256, (D >= 256) ? 1 : 2) qdecode_kernel(Decode
     });
   };
 
+  // ---- end of a segment: the output itself, or this wave's partial
+  auto finalize = [&]() {
+    float lsum = l_run, csum[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) csum[g] = corr[g];
+    sfor<PP>([&](auto k_) {
+      constexpr int kk = decltype(k_)::value;
+      if constexpr (kk > 0 && (kk & (kk - 1)) == 0) {  // offsets HP, 2 HP, ... below 16
+        lsum += row_readf<kk * HP>(lsum);
+#pragma unroll
+        for (int g = 0; g < G; g++) csum[g] += row_readf<kk * HP>(csum[g]);
+      }
+    });
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      csum[g] += __shfl_xor(csum[g], 16);
+      csum[g] += __shfl_xor(csum[g], 32);
+    }
+    const int nst = (seg_len + 63) >> 6;
+    const bool whole = seg_t == 0 && seg_take == nst;
+    // the pair's units start at unit pa; its partials take the slots of the
+    // waves wa..wb that cover it
+    const int pa = u0 + seg_first - seg_t;
+    const int wa = pa / cper, wb = (pa + nst - 1) / cper;
+    const int64_t pair = static_cast<int64_t>(seg_seq) * HG + seg_j;
+    if (seg_t + seg_take == nst && lane == 0)
+      reinterpret_cast<int32_t*>(a.ws_ml + a.ws_hdr)[pair] = wb - wa + 1;
+    const int64_t hq0 = static_cast<int64_t>(seg_j / n_hg) * rep + (seg_j % n_hg) * HP;
+    if (n < nh) {
+      if (whole) {
+        const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+        uint16_t* o = a.out + seg_seq * a.o_ss + (hq0 + n) * a.o_sh + 4 * lg;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          const float cg = csum[t / (NT / G)];
+          u32x2_t v;
+          v[0] = f32_to_bf16((oacc[t][0] + cg) * inv) | (uint32_t(f32_to_bf16((oacc[t][1] + cg) * inv)) << 16);
+          v[1] = f32_to_bf16((oacc[t][2] + cg) * inv) | (uint32_t(f32_to_bf16((oacc[t][3] + cg) * inv)) << 16);
+          *reinterpret_cast<u32x2_t*>(o + 16 * t) = v;
+        }
+      } else {
+        const int64_t slot = pair * kMaxParts + (w - wa);
+        float* o = a.ws_o + (slot * HP + n) * D + 4 * lg;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          const float cg = csum[t / (NT / G)];
+          *reinterpret_cast<f32x4_t*>(o + 16 * t) =
+              f32x4_t{oacc[t][0] + cg, oacc[t][1] + cg, oacc[t][2] + cg, oacc[t][3] + cg};
+        }
+        if (lg == 0) {
+          a.ws_ml[(slot * HP + n) * 2] = m_run;
+          a.ws_ml[(slot * HP + n) * 2 + 1] = lsum;
+        }
+      }
+    }
+    // the next segment's first step refreshes the max from -inf, which
+    // scales the accumulators, l_run and corr by zero
+    m_run = -INFINITY;
+  };
+
+  // ---- the range: unit ui computes while unit ui + 1 (and the queries of
+  // its segment) load.  Prefetches are unconditional, clamped to the last
+  // unit: a conditional load makes the compiler merge the buffer registers
+  // at the join, which waits for the loads right after issuing them.
+  auto unit = [&](int ui, const Buf& cur, Buf& nxt) -> bool {
+    const int nx = min(ui + 1, nunits - 1);
+    const int knx = (k + 1 < nseg && nx >= __builtin_amdgcn_readfirstlane(seg_tab[k + 1][5])) ? k + 1 : k;
+    load_q(knx, qpre);
+    load_step(nx, nxt);
+    __builtin_amdgcn_sched_barrier(0);  // issue the loads before any compute
+    compute_step(seg_t + (ui - seg_first), cur);
+    if (ui == seg_first + seg_take - 1) {  // last unit of the segment
+      finalize();
+      if (ui + 1 == nunits) return false;
+      k++;
+      setup_segment(k, qpre);
+    }
+    return ui + 1 < nunits;
+  };
   if constexpr (C::kPrefetch) {
-    // The next step's loads are issued unconditionally (clamped to the last
-    // step, whose data is then re-read from cache): a conditional load
-    // makes the compiler merge the buffer registers at the join, which
-    // waits for the loads right after issuing them.
-    while (step < st1) {
-      const int nx = step + kWaves;
-      load_step(min(nx, st1 - 1), bufB, false);
-      __builtin_amdgcn_sched_barrier(0);  // issue the loads before any compute
-      compute_step(step, bufA);
-      if (nx >= st1) break;
-      const int nx2 = nx + kWaves;
-      load_step(min(nx2, st1 - 1), bufA, false);
-      __builtin_amdgcn_sched_barrier(0);
-      compute_step(nx, bufB);
-      step = nx2;
+    for (int ui = 0;; ui += 2) {
+      if (!unit(ui, bufA, bufB)) break;
+      if (!unit(ui + 1, bufB, bufA)) break;
     }
   } else {
-    while (step < st1) {
-      compute_step(step, bufA);
-      step += kWaves;
-      if (step < st1) load_step(step, bufA, false);
-    }
-  }
-
-  // ---- per-wave totals of head h: sum over the parts of the row, then rows
-  float lsum = l_run, csum[G];
-#pragma unroll
-  for (int g = 0; g < G; g++) csum[g] = corr[g];
-  sfor<PP>([&](auto k_) {
-    constexpr int k = decltype(k_)::value;
-    if constexpr (k > 0 && (k & (k - 1)) == 0) {  // offsets HP, 2 HP, ... below 16
-      lsum += row_readf<k * HP>(lsum);
-#pragma unroll
-      for (int g = 0; g < G; g++) csum[g] += row_readf<k * HP>(csum[g]);
-    }
-  });
-  lsum += __shfl_xor(lsum, 16);
-  lsum += __shfl_xor(lsum, 32);
-#pragma unroll
-  for (int g = 0; g < G; g++) {
-    csum[g] += __shfl_xor(csum[g], 16);
-    csum[g] += __shfl_xor(csum[g], 32);
-  }
-  __syncthreads();  // the query table is dead; its LDS becomes fin_o
-  if (n < HP && lg == 0) {
-    fin_s[wave][n][0] = m_run;
-    fin_s[wave][n][1] = lsum;
-  }
-  if (n < nh) {
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-      const float cg = csum[t / (NT / G)];
-#pragma unroll
-      for (int i = 0; i < 4; i++) fin_o[wave][n][16 * t + 4 * lg + i] = oacc[t][i] + cg;
-    }
-  }
-  __syncthreads();
-
-  // ---- merge the waves; write the output or this partition's partial
-  for (int idx = tid; idx < nh * D; idx += 256) {
-    const int r = idx / D, d = idx % D;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; w++) M = fmaxf(M, fin_s[w][r][0]);
-    float o = 0.0f, L = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; w++) {
-      const float mw = fin_s[w][r][0];
-      if (mw == -INFINITY) continue;
-      const float f = exp2f((mw - M) * kLog2e);
-      o = fmaf(f, fin_o[w][r][d], o);
-      L = fmaf(f, fin_s[w][r][1], L);
-    }
-    if (parts_used == 1) {
-      a.out[seq * a.o_ss + (hq0 + r) * a.o_sh + d] = f32_to_bf16(L > 0.0f ? o / L : 0.0f);
-    } else {
-      const int64_t slot = (rh0 + r) * a.n_parts + part;
-      a.ws_o[slot * D + d] = o;
-      if (d == 0) {
-        a.ws_ml[slot * 2] = M;
-        a.ws_ml[slot * 2 + 1] = L;
+    for (int ui = 0;; ui++) {
+      const int knx = (k + 1 < nseg && ui + 1 >= seg_tab[k + 1][5]) ? k + 1 : k;
+      load_q(knx, qpre);
+      compute_step(seg_t + (ui - seg_first), bufA);
+      if (ui == seg_first + seg_take - 1) {
+        finalize();
+        if (ui + 1 == nunits) break;
+        k++;
+        setup_segment(k, qpre);
       }
+      load_step(ui + 1, bufA);
     }
   }
 }
 
-// Merge of the partition partials of sequences longer than one partition
-// (sdpa_vector.h:320-394).  Block = one (sequence, query head).
-__global__ void __launch_bounds__(256) qdecode_combine_kernel(DecodeArgs a, int D) {
-  const int64_t rh = blockIdx.x;  // seq * Hq + h
-  const int seq = static_cast<int>(rh / a.Hq);
-  const int64_t h = rh % a.Hq;
+// Merge of the partials of (sequence, head pair)s that several waves
+// share (sdpa_vector.h:320-394).  Block = one (sequence, pair), thread =
+// one (head, dim).
+template <int HP>
+__global__ void __launch_bounds__(1024) qdecode_combine_kernel(DecodeArgs a, int D) {
+  const int rep = a.rep, n_hg = (rep + HP - 1) / HP, HG = a.Hkv * n_hg;
+  const int P = blockIdx.x, seq = P / HG, j = P % HG;
   const int len = a.seq_lens ? a.seq_lens[seq] : a.max_len;
-  const int parts_used = ((len + 63) / 64 + a.part_steps - 1) / a.part_steps;
-  if (parts_used <= 1) return;  // written by the partition itself
-  const float* ml = a.ws_ml + rh * a.n_parts * 2;
-  float M = -INFINITY;
-  for (int pp = 0; pp < parts_used; pp++) M = fmaxf(M, ml[2 * pp]);
-  float L = 0.0f;
-  for (int pp = 0; pp < parts_used; pp++) L = fmaf(exp2f((ml[2 * pp] - M) * kLog2e), ml[2 * pp + 1], L);
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    const float* wo = a.ws_o + rh * a.n_parts * D + d;
-    float o = 0.0f;
-    for (int pp = 0; pp < parts_used; pp++)
-      o = fmaf(exp2f((ml[2 * pp] - M) * kLog2e), wo[static_cast<int64_t>(pp) * D], o);
-    a.out[seq * a.o_ss + h * a.o_sh + d] = f32_to_bf16(L > 0.0f ? o / L : 0.0f);
+  const int K = reinterpret_cast<const int32_t*>(a.ws_ml + a.ws_hdr)[P];
+  if (len == 0 || K <= 1) return;  // written by the decode kernel itself
+  const int64_t hq0 = static_cast<int64_t>(j / n_hg) * rep + (j % n_hg) * HP;
+  const int nh = min(HP, rep - (j % n_hg) * HP);
+  const int64_t slot0 = static_cast<int64_t>(P) * kMaxParts;
+  for (int idx = threadIdx.x; idx < nh * D; idx += blockDim.x) {
+    const int r = idx / D, d = idx % D;
+    // eight partials per round; the loads are unconditional (clamped to the
+    // last partial) because a conditional load waits for every load before it
+    float M = -INFINITY, L = 0.0f, o = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += 8) {
+      float mm[8], ll[8], oo[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const int64_t slot = (slot0 + min(k0 + q, K - 1)) * HP + r;
+        mm[q] = a.ws_ml[slot * 2];
+        ll[q] = a.ws_ml[slot * 2 + 1];
+        oo[q] = a.ws_o[slot * D + d];
+      }
+#pragma unroll
+      for (int q = 0; q < 8; q++) mm[q] = k0 + q < K ? mm[q] : -INFINITY;
+      float Mn = M;
+#pragma unroll
+      for (int q = 0; q < 8; q++) Mn = fmaxf(Mn, mm[q]);
+      const float f = M == -INFINITY ? 0.0f : exp2f((M - Mn) * kLog2e);
+      L *= f;
+      o *= f;
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const float e = mm[q] == -INFINITY ? 0.0f : exp2f((mm[q] - Mn) * kLog2e);
+        L = fmaf(e, ll[q], L);
+        o = fmaf(e, oo[q], o);
+      }
+      M = Mn;
+    }
+    a.out[seq * a.o_ss + (hq0 + r) * a.o_sh + d] = f32_to_bf16(L > 0.0f ? o / L : 0.0f);
   }
 }
 
@@ -656,30 +835,67 @@ bool qdecode_supported(int dtype, int bits, int D, int block_size, int rep, int 
          block_size % 32 == 0 && rep >= 1 && rep <= 16 && group == 64;
 }
 
-template <int BITS, int D>
-static void launch_d(const DecodeArgs& a, dim3 grid, hipStream_t st) {
-  if (heads_per_part(a.rep) == 4)
-    hipLaunchKernelGGL((qdecode_kernel<BITS, D, 4>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((qdecode_kernel<BITS, D, 8>), grid, dim3(256), 0, st, a);
+int qdecode_waves(int n_seqs, int Hkv, int rep, int max_len, int want) {
+  const int64_t units = static_cast<int64_t>(n_seqs) * Hkv * qdecode_head_groups(rep) *
+                        ((static_cast<int64_t>(max_len) + 63) / 64);
+  const int64_t need = (units + kMaxRange - 1) / kMaxRange;  // ranges of at most kMaxRange units
+  // one round of resident waves (2 per SIMD x 4 SIMDs x 256 CUs)
+  int64_t waves = want > 0 ? want : std::min<int64_t>(2048, (units + 3) / 4);
+  waves = std::max<int64_t>({waves, need, 1});
+  return static_cast<int>(waves);
 }
 
-void launch_qdecode(const DecodeArgs& a, int bits, int D, int n_seqs, hipStream_t st) {
-  const dim3 grid(a.n_parts, a.Hkv * qdecode_head_groups(a.rep), n_seqs);
-  if (bits == 4) {
-    if (D == 64) launch_d<4, 64>(a, grid, st);
-    else if (D == 128) launch_d<4, 128>(a, grid, st);
-    else launch_d<4, 256>(a, grid, st);
+size_t qdecode_workspace_floats(int n_seqs, int Hkv, int rep, int D, int) {
+  const int hp = heads_per_part(rep);
+  const size_t pairs = static_cast<size_t>(n_seqs) * Hkv * qdecode_head_groups(rep);
+  return pairs * kMaxParts * hp * (D + 2) + pairs;  // + one partial count (int32) per pair
+}
+
+int qdecode_max_seqs() { return kMaxSeqs; }
+
+// Longest sequence the decode kernel takes: ranges of at most kMaxRange
+// units with at most kMaxParts partials per pair.
+int qdecode_max_len() { return kMaxRange * (kMaxParts - 1) * 64; }
+
+template <int BITS, int D>
+static void launch_d(const DecodeArgs& a, hipStream_t st) {
+  const dim3 grid(a.n_waves), block(64);
+  const int pairs = a.n_seqs * a.Hkv * qdecode_head_groups(a.rep);
+  if (heads_per_part(a.rep) == 4) {
+    hipLaunchKernelGGL((qdecode_kernel<BITS, D, 4>), grid, block, 0, st, a);
+    VKV_HIP(hipGetLastError());
+    hipLaunchKernelGGL(qdecode_combine_kernel<4>, dim3(pairs), dim3(4 * D), 0, st, a, D);
   } else {
-    if (D == 64) launch_d<8, 64>(a, grid, st);
-    else if (D == 128) launch_d<8, 128>(a, grid, st);
-    else launch_d<8, 256>(a, grid, st);
+    hipLaunchKernelGGL((qdecode_kernel<BITS, D, 8>), grid, block, 0, st, a);
+    VKV_HIP(hipGetLastError());
+    hipLaunchKernelGGL(qdecode_combine_kernel<8>, dim3(pairs), dim3(std::min(1024, 8 * D)), 0, st, a, D);
   }
   VKV_HIP(hipGetLastError());
-  if (a.n_parts > 1) {
-    hipLaunchKernelGGL(qdecode_combine_kernel, dim3(static_cast<unsigned>(n_seqs) * a.Hq),
-                       dim3(D >= 256 ? 256 : D), 0, st, a, D);
-    VKV_HIP(hipGetLastError());
+}
+
+void launch_qdecode(const DecodeArgs& a0, int bits, int D, hipStream_t st) {
+  // at most kMaxSeqs sequences per launch
+  for (int s0 = 0; s0 < a0.n_seqs; s0 += kMaxSeqs) {
+    DecodeArgs a = a0;
+    a.n_seqs = std::min(kMaxSeqs, a0.n_seqs - s0);
+    a.n_waves = qdecode_waves(a.n_seqs, a.Hkv, a.rep, a.max_len, a0.n_waves);
+    const size_t slots = static_cast<size_t>(a.n_seqs) * a.Hkv * qdecode_head_groups(a.rep) * kMaxParts;
+    a.ws_o = a0.ws;
+    a.ws_ml = a0.ws + slots * heads_per_part(a.rep) * D;
+    a.ws_hdr = static_cast<int32_t>(slots * heads_per_part(a.rep) * 2);
+    a.q += s0 * a0.q_ss;
+    a.out += s0 * a0.o_ss;
+    a.table += static_cast<int64_t>(s0) * a0.table_stride;
+    if (a.seq_lens) a.seq_lens += s0;
+    if (bits == 4) {
+      if (D == 64) launch_d<4, 64>(a, st);
+      else if (D == 128) launch_d<4, 128>(a, st);
+      else launch_d<4, 256>(a, st);
+    } else {
+      if (D == 64) launch_d<8, 64>(a, st);
+      else if (D == 128) launch_d<8, 128>(a, st);
+      else launch_d<8, 256>(a, st);
+    }
   }
 }
 

@@ -140,15 +140,25 @@ struct DecodeArgs {
   const int32_t* seq_lens;   // nullptr = every sequence holds max_len tokens
   int32_t max_len;
   int32_t Hq, Hkv, rep;
-  int32_t part_steps;        // 64-token steps per workgroup partition
-  int32_t n_parts;           // partitions per sequence (grid x)
-  float* ws_o;               // [n_seqs][Hq][n_parts][D] partial outputs
-  float* ws_ml;              // [n_seqs][Hq][n_parts][2] partial (max, sum)
+  int32_t n_seqs;
+  int32_t n_waves;           // decode waves per launch (0 = choose)
+  float* ws;                 // split-K workspace, qdecode_workspace_floats floats
+  float* ws_o;               // set per launch: partial outputs [slot][head][D]
+  float* ws_ml;              //                 partial (max, sum) [slot][head][2]
+  int32_t ws_hdr;            //   then (as int32 at ws_ml + ws_hdr) the number
+                             //   of partials of each (sequence, head pair)
 };
 bool qdecode_supported(int dtype, int bits, int D, int block_size, int rep, int group);
-// workgroups per (sequence, kv head): query heads are taken 4 or 8 at a time
+// (sequence, kv head) pairs are split into head groups of 4 or 8 query heads
 int qdecode_head_groups(int rep);
-void launch_qdecode(const DecodeArgs& a, int bits, int D, int n_seqs, hipStream_t st);
+// sequences per launch, at most (larger batches are launched in slices)
+int qdecode_max_seqs();
+// longest sequence (tokens) the matrix-core decode takes
+int qdecode_max_len();
+// decode waves for a launch of n_seqs sequences (want > 0 overrides)
+int qdecode_waves(int n_seqs, int Hkv, int rep, int max_len, int want);
+size_t qdecode_workspace_floats(int n_seqs, int Hkv, int rep, int D, int n_waves);
+void launch_qdecode(const DecodeArgs& a, int bits, int D, hipStream_t st);
 
 // Block pairs passed by value to the block-copy kernel.
 struct BlockPairs {
