@@ -6,8 +6,8 @@ Workload ("Paged continuous batching"): a pool of
 tables are random permutations of pool ids; 32 sequences share one
 refcounted 2048-token prefix (64 blocks).  One step = for each of the
 --layers layers: append one token per sequence plus one 512-token
-chunked-prefill chunk, then decode attention (32 query heads) over every
-sequence.  Synthetic data, generated on the GPU; all inputs are resident in
+chunked-prefill chunk (one append call for the step's 576 new tokens), then
+decode attention (32 query heads) over every sequence.  Synthetic data, generated on the GPU; all inputs are resident in
 HBM before timing starts.  The step writes the decode token at the same
 position each step, so every step does identical work.
 
@@ -135,6 +135,12 @@ def build_scene(torch, vkv, layers, seed=3):
     sc["dv"] = vkv.fill_normal(torch.empty((layers, n_seqs, H, D), dtype=torch.bfloat16, **dev), 9)
     sc["pk"] = vkv.fill_normal(torch.empty((layers, prefill, H, D), dtype=torch.bfloat16, **dev), 10)
     sc["pv"] = vkv.fill_normal(torch.empty((layers, prefill, H, D), dtype=torch.bfloat16, **dev), 11)
+    # a step's new tokens (the decode token of every sequence, then the
+    # prefill chunk) are appended with one call per layer, as a batching
+    # engine issues them
+    sc["ak"] = torch.cat([sc["dk"], sc["pk"]], dim=1).contiguous()
+    sc["av"] = torch.cat([sc["dv"], sc["pv"]], dim=1).contiguous()
+    sc["all_slots"] = torch.cat([sc["dec_slots"], sc["pre_slots"]]).contiguous()
     sc["out"] = torch.empty((layers, n_seqs, Hq, D), dtype=torch.bfloat16, **dev)
     sc["views"] = [pool.view(l, sc["table"], sc["seq_lens"], sc["max_len"]) for l in range(layers)]
     torch.cuda.synchronize()
@@ -208,8 +214,7 @@ def main():
         for l in range(layers):
             if ev is not None:
                 ev[0][l].record(stream)
-            pool.append(l, sc["dk"][l], sc["dv"][l], sc["dec_slots"])
-            pool.append(l, sc["pk"][l], sc["pv"][l], sc["pre_slots"])
+            pool.append(l, sc["ak"][l], sc["av"][l], sc["all_slots"])
             if ev is not None:
                 ev[1][l].record(stream)
             o = sc["out"][l]

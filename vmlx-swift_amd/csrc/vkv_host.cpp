@@ -847,6 +847,21 @@ void Pool::append(int layer, const vkv_array& k, const vkv_array* v, const int32
     if (v->shape[0] < n) throw Error("values hold fewer than n_tokens rows");
   }
   uint8_t* base = mem.bytes() + static_cast<int64_t>(layer) * layer_bytes;
+  if (p.bits != 0 && append_affine_supported(p.bits, p.group_size, p.head_dim) &&
+      (keys_only || p.v_head_dim == p.head_dim)) {
+    // K and V in one launch
+    const int G = p.head_dim / p.group_size;
+    RowSrc sk{k.data, 1, n, k.shape[1], 0, k.strides[0], k.strides[1]};
+    RowSrc sv = sk;
+    if (!keys_only) sv = RowSrc{v->data, 1, n, v->shape[1], 0, v->strides[0], v->strides[1]};
+    RowDst dk = affine_dst(base, block_bytes, head_bytes, p.block_size, L, 0, G, keys_only);
+    RowDst dv = keys_only ? dk : affine_dst(base, block_bytes, head_bytes, p.block_size, L, 1, G, false);
+    dk.slots = slots;
+    dv.slots = slots;
+    launch_append_affine(p.dtype, p.bits, p.group_size, sk, sv, dk, dv, n, p.n_kv_heads, p.head_dim,
+                         !keys_only, st);
+    return;
+  }
   const int passes = keys_only ? 1 : 2;
   for (int which = 0; which < passes; which++) {
     const vkv_array& a = which ? *v : k;

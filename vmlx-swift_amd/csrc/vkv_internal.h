@@ -104,6 +104,12 @@ void launch_quantize_rows(int dtype, int bits, int group, int mode, const RowSrc
                           const RowDst& dst, int64_t rows, int D, hipStream_t st);
 void launch_copy_rows(int dtype, int mode, const RowSrc& src, const RowDst& dst, int64_t rows,
                       int D, hipStream_t st);
+// Paged append of ntok tokens x H heads of K (and V when with_v) in one
+// launch; rows of the sources are (token, head), D = head dim of both.
+bool append_affine_supported(int bits, int group, int D);
+void launch_append_affine(int dtype, int bits, int group, const RowSrc& sk, const RowSrc& sv,
+                          const RowDst& dk, const RowDst& dv, int64_t ntok, int H, int D, bool with_v,
+                          hipStream_t st);
 void launch_dequantize(int dtype, int bits, int group, const uint32_t* wq, const void* scales,
                        const void* biases, void* out, int64_t rows, int D, hipStream_t st);
 // Gather rows of paged/dense KV into dense arrays.  which: 0 = keys, 1 = values.

@@ -178,6 +178,108 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(RowSrc src, RowDst d
   }
 }
 
+// Paged append of K and V in one launch (Pool::append): block = 8
+// consecutive tokens x HB heads x the D/8 threads of a row (256 threads);
+// blockIdx.z selects K (0) or V (1).  The arithmetic is that of
+// quantize_rows_kernel.  4-bit V words hold 8 tokens of one dim: when the
+// block's 8 tokens fill exactly one aligned 8-token group of a block (a
+// prefill chunk), the words are assembled in LDS and written with plain
+// stores; otherwise (decode tokens of different sequences, ragged groups)
+// each nibble is merged atomically.
+template <int DT, int BITS, int GROUP>
+__global__ void __launch_bounds__(256) append_affine_kernel(RowSrc sk, RowSrc sv, RowDst dk, RowDst dv,
+                                                            int64_t ntok, int H, int D) {
+  using E = Elem<DT>;
+  constexpr int TEAM = GROUP / 8;
+  constexpr float n_bins = static_cast<float>((1 << BITS) - 1);
+  const int which = blockIdx.z;
+  const RowSrc src = which ? sv : sk;
+  const RowDst dst = which ? dv : dk;
+  const int tpr = D / 8, hb = 256 / (8 * tpr);
+  const int tid = threadIdx.x;
+  const int i = tid / (hb * tpr), hl = (tid / tpr) % hb, j = tid % tpr;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 8 + i;
+  const int h = blockIdx.y * hb + hl;
+  const bool active = n < ntok && h < H;
+
+  float v[8];
+  if (active) {
+    load8<DT>(row_ptr(src, n * H + h, E::kBytes) + static_cast<int64_t>(j) * 8 * E::kBytes, v);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = 0.0f;
+  }
+  float w_min = E::kMax, w_max = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    w_min = fminf(w_min, v[e]);
+    w_max = fmaxf(w_max, v[e]);
+  }
+  w_min = wave_min(w_min, TEAM);
+  w_max = wave_max(w_max, TEAM);
+  float scale = fmaxf((w_max - w_min) / n_bins, 1e-7f);
+  const bool side = fabsf(w_min) > fabsf(w_max);
+  scale = side ? scale : -scale;
+  const float edge = side ? w_min : w_max;
+  const float q0 = roundf(edge / scale);
+  const bool at_zero = q0 == 0.0f;
+  scale = at_zero ? scale : edge / q0;
+  const float bias = at_zero ? 0.0f : edge;
+  uint32_t code[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const float x = fminf(roundf((v[e] - bias) / scale), n_bins);
+    code[e] = x > 0.0f ? static_cast<uint32_t>(x) : 0u;
+  }
+  const int64_t slot = active ? token_slot(dst, n) : -1;
+  const int g = (j * 8) / GROUP;
+  if (slot >= 0 && (j % TEAM) == 0) {
+    uint8_t* chunk = dst.base + (slot / dst.block_size) * dst.block_bytes + h * dst.head_bytes;
+    const int tib = static_cast<int>(slot % dst.block_size);
+    typename E::T* sbp = reinterpret_cast<typename E::T*>(chunk + dst.s_off);
+    sbp[qsb_index(tib, dst.is_v, g, 0, dst.G, dst.keys_only)] = E::from_f32(scale);
+    sbp[qsb_index(tib, dst.is_v, g, 1, dst.G, dst.keys_only)] = E::from_f32(bias);
+  }
+  if (BITS == 8 || which == 0) {  // K words and 8-bit V bytes are whole stores
+    if (slot >= 0) {
+      uint8_t* chunk = dst.base + (slot / dst.block_size) * dst.block_bytes + h * dst.head_bytes;
+      store_chunk_codes<BITS>(chunk, dst, static_cast<int>(slot % dst.block_size), j, D, code);
+    }
+    return;
+  }
+  // ---- 4-bit V
+  __shared__ int64_t tok_slot[8];
+  __shared__ uint8_t vcode[8][256];  // [token][head * D + dim], hb * D = 256
+  if (hl == 0 && j == 0) tok_slot[i] = (n < ntok) ? token_slot(dst, n) : -1;
+  __syncthreads();
+  const int64_t s0 = tok_slot[0];
+  bool aligned = s0 >= 0 && s0 % 8 == 0;
+#pragma unroll
+  for (int t = 1; t < 8; t++) aligned = aligned && tok_slot[t] == s0 + t;
+  if (!aligned) {
+    if (slot >= 0) {
+      uint8_t* chunk = dst.base + (slot / dst.block_size) * dst.block_bytes + h * dst.head_bytes;
+      store_chunk_codes<BITS>(chunk, dst, static_cast<int>(slot % dst.block_size), j, D, code);
+    }
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e++) vcode[i][hl * D + 8 * j + e] = static_cast<uint8_t>(code[e]);
+  __syncthreads();
+  // thread (head hh, dim d) writes the word of the 8 tokens
+  const int hh = tid / D, d = tid % D;
+  if (tid < hb * D && blockIdx.y * hb + hh < H) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int t = 0; t < 8; t++) w |= static_cast<uint32_t>(vcode[t][hh * D + d]) << (4 * t);
+    uint8_t* chunk = dst.base + (s0 / dst.block_size) * dst.block_bytes +
+                     static_cast<int64_t>(blockIdx.y * hb + hh) * dst.head_bytes;
+    int sh;
+    const int64_t off = qv_word_off(s0 % dst.block_size, d, D, 4, &sh);
+    *reinterpret_cast<uint32_t*>(chunk + dst.c_off + off) = w;
+  }
+}
+
 // Float rows: mode 0 copies to contiguous out (dst.wq), mode 1 scatters to
 // paged chunks (token-major K or V at dst.c_off).
 template <int ESIZE, int MODE>
@@ -722,6 +824,44 @@ void launch_quantize_rows(int dtype, int bits, int group, int mode, const RowSrc
     case kF32: quantize_dispatch<kF32>(bits, group, mode, src, dst, rows, D, st); break;
     case kF16: quantize_dispatch<kF16>(bits, group, mode, src, dst, rows, D, st); break;
     case kBF16: quantize_dispatch<kBF16>(bits, group, mode, src, dst, rows, D, st); break;
+    default: throw Error("unsupported dtype");
+  }
+  VKV_HIP(hipGetLastError());
+}
+
+template <int DT>
+static void append_dispatch(int bits, int group, const RowSrc& sk, const RowSrc& sv, const RowDst& dk,
+                            const RowDst& dv, int64_t ntok, int H, int D, bool with_v, hipStream_t st) {
+  const int hb = 256 / D;
+  const dim3 grid(static_cast<unsigned>((ntok + 7) / 8), (H + hb - 1) / hb, with_v ? 2 : 1);
+#define VKV_A(B, G) \
+  hipLaunchKernelGGL((append_affine_kernel<DT, B, G>), grid, dim3(256), 0, st, sk, sv, dk, dv, ntok, H, D)
+#define VKV_AG(B)                         \
+  do {                                    \
+    if (group == 32) VKV_A(B, 32);        \
+    else if (group == 64) VKV_A(B, 64);   \
+    else VKV_A(B, 128);                   \
+  } while (0)
+  if (bits == 4) VKV_AG(4);
+  else VKV_AG(8);
+#undef VKV_AG
+#undef VKV_A
+}
+
+bool append_affine_supported(int bits, int group, int D) {
+  return (bits == 4 || bits == 8) && (group == 32 || group == 64 || group == 128) && D % group == 0 &&
+         (D == 32 || D == 64 || D == 128 || D == 256);
+}
+
+void launch_append_affine(int dtype, int bits, int group, const RowSrc& sk, const RowSrc& sv,
+                          const RowDst& dk, const RowDst& dv, int64_t ntok, int H, int D, bool with_v,
+                          hipStream_t st) {
+  if (ntok <= 0) return;
+  VKV_CHECK(append_affine_supported(bits, group, D), "append_affine: unsupported geometry");
+  switch (dtype) {
+    case kF32: append_dispatch<kF32>(bits, group, sk, sv, dk, dv, ntok, H, D, with_v, st); break;
+    case kF16: append_dispatch<kF16>(bits, group, sk, sv, dk, dv, ntok, H, D, with_v, st); break;
+    case kBF16: append_dispatch<kBF16>(bits, group, sk, sv, dk, dv, ntok, H, D, with_v, st); break;
     default: throw Error("unsupported dtype");
   }
   VKV_HIP(hipGetLastError());
