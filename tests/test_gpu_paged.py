@@ -235,3 +235,56 @@ def test_decode_wave_counts_agree(monkeypatch, waves):
                                f(rk[2])[None], rv[0][None], f(rv[1])[None], f(rv[2])[None], 0.088,
                                64, bits)[0, :, 0]
         assert (np.abs(got[s] - ref) <= attn_tol(dtype, ref)).all(), s
+
+
+def test_append_aligned_groups_ragged_and_scattered_slots():
+    """One append call mixing an 8-aligned prefill run (V words assembled in
+    LDS), a run starting mid-group, single tokens scattered over blocks
+    (nibbles merged atomically) and a skipped token (slot -1); the gathered
+    codes are bit-exact with the oracle quantizer, and tokens already in
+    the touched words survive."""
+    dtype, bits, bs, H, D = O.BF16, 4, 32, 4, 128
+    rng = np.random.default_rng(55)
+    nblocks = 12
+    pool = vkv.PagedPool(nblocks, bs, 1, H, D, dtype=dtype, bits=bits)
+    # sequence A: blocks 1, 2 (positions 0..40 aligned run of 41 tokens)
+    # sequence B: block 3, positions 3..21 (starts mid-group)
+    # sequence C..F: one token each at position 5 of blocks 4..7
+    ta, tb = [1, 2], [3]
+    slots = [ta[p // bs] * bs + p % bs for p in range(41)]
+    slots += [tb[0] * bs + p for p in range(3, 22)]
+    singles = [4 * bs + 5, 5 * bs + 5, 6 * bs + 5, 7 * bs + 5]
+    slots += singles + [-1]
+    n = len(slots)
+    k = rand_bits(rng, (n, H, D), dtype, outliers=2)
+    v = rand_bits(rng, (n, H, D), dtype, outliers=2)
+    # first fill the words the single tokens share, to check they survive
+    pre = [4 * bs + p for p in range(8)]
+    pk = rand_bits(rng, (8, H, D), dtype)
+    pv = rand_bits(rng, (8, H, D), dtype)
+    pre_slots = [x for x in pre if x != 4 * bs + 5]
+    pool.append(0, dev(pk[:7], dtype), dev(pv[:7], dtype),
+                torch.tensor(pre_slots, dtype=torch.int32, device="cuda"))
+    pool.append(0, dev(k, dtype), dev(v, dtype), torch.tensor(slots, dtype=torch.int32, device="cuda"))
+    # views: A (41 tokens), B positions 3..21 read as a 22-token sequence,
+    # block 4 as an 8-token sequence holding the pre-filled tokens + single
+    tab = torch.tensor([[1, 2], [3, 0], [4, 0]], dtype=torch.int32, device="cuda")
+    lens = torch.tensor([41, 22, 8], dtype=torch.int32, device="cuda")
+    (kq, ks, kb), (vq, vs, vb) = vkv.paged_gather_quantized(pool.view(0, tab, lens, 41))
+    want_k = {0: (k[:41], 0), 1: (k[41:60], 3)}
+    want_v = {0: (v[:41], 0), 1: (v[41:60], 3)}
+    for s in (0, 1):
+        for src, got in ((want_k[s], (kq, ks, kb)), (want_v[s], (vq, vs, vb))):
+            x, off = src
+            rq, rs, rb, _ = O.quantize(np.ascontiguousarray(x.transpose(1, 0, 2)), dtype, 64, bits)
+            L = x.shape[0]
+            assert np.array_equal(host(got[0][s, :, off:off + L]), rq), s
+            assert np.array_equal(host(got[1][s, :, off:off + L]).view(rs.dtype), rs), s
+            assert np.array_equal(host(got[2][s, :, off:off + L]).view(rb.dtype), rb), s
+    # block 4: positions 0..7 = pre-filled tokens with the single token at 5
+    seq_k = np.concatenate([pk[:5], k[60:61], pk[5:7]])
+    seq_v = np.concatenate([pv[:5], v[60:61], pv[5:7]])
+    for x, got in ((seq_k, (kq, ks, kb)), (seq_v, (vq, vs, vb))):
+        rq, rs, rb, _ = O.quantize(np.ascontiguousarray(x.transpose(1, 0, 2)), dtype, 64, bits)
+        assert np.array_equal(host(got[0][2, :, :8]), rq)
+        assert np.array_equal(host(got[1][2, :, :8]).view(rs.dtype), rs)
