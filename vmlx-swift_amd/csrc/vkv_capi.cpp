@@ -379,12 +379,53 @@ int vkv_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vk
 int vkv_mla_decode(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_array* out,
                    void* stream) {
   return guard([&] {
-    (void)q;
-    (void)kv;
-    (void)scale;
-    (void)out;
-    (void)stream;
-    throw Error("vkv_mla_decode: not built yet");
+    need(q, "q");
+    need(kv, "kv");
+    need(out, "out");
+    if (!(kv->flags & VKV_VIEW_KEYS_ONLY)) throw Error("vkv_mla_decode needs a keys-only (latent) view");
+    if (kv->n_kv_heads != 1) throw Error("an MLA latent view has one kv head");
+    if (q->ndim != 3 || out->ndim != 3 || q->strides[2] != 1 || out->strides[2] != 1)
+      throw Error("q and out must be [n_seqs, H, D] with a contiguous last dim");
+    if (q->dtype != kv->dtype || out->dtype != kv->dtype) throw Error("q/out dtype must match the view");
+    if (q->shape[0] != kv->n_seqs || q->shape[2] != kv->head_dim || out->shape[0] != kv->n_seqs ||
+        out->shape[1] != q->shape[1] || out->shape[2] != kv->v_head_dim)
+      throw Error("q/out shapes do not match the view");
+    if (!kv->block_table) throw Error("view has no block table");
+    const bool aligned = (reinterpret_cast<uintptr_t>(q->data) % 16 == 0) &&
+                         q->strides[0] % 8 == 0 && q->strides[1] % 8 == 0;
+    if (!aligned || getenv("VKV_GENERIC_ATTENTION") ||
+        !mla_supported(kv->dtype, kv->bits, kv->group_size, kv->head_dim, kv->v_head_dim,
+                       kv->n_kv_heads, kv->block_size)) {
+      // other latent geometries run on the generic paged kernel
+      if (vkv_paged_sdpa(q, kv, scale, out, stream) != 0) throw Error(vkv_last_error());
+      return;
+    }
+    // matrix-core path (vkv_mla.hip)
+    KVSrc src = kvsrc_from_view(*kv);
+    MlaArgs m{};
+    m.q = static_cast<const uint16_t*>(q->data);
+    m.q_ss = q->strides[0];
+    m.q_sh = q->strides[1];
+    m.out = static_cast<uint16_t*>(out->data);
+    m.o_ss = out->strides[0];
+    m.o_sh = out->strides[1];
+    m.scale = scale;
+    m.base = src.base;
+    m.block_bytes = src.block_bytes;
+    m.sb_off = src.sb_off;
+    m.table = kv->block_table;
+    m.table_stride = kv->table_stride;
+    m.block_size = kv->block_size;
+    m.seq_lens = kv->seq_lens;
+    m.max_len = kv->max_len;
+    m.H = static_cast<int32_t>(q->shape[1]);
+    m.n_seqs = kv->n_seqs;
+    if (m.H < 1 || m.n_seqs < 1) return;
+    int want = 0;
+    if (const char* e = getenv("VKV_MLA_SPLITS")) want = std::max(1, atoi(e));
+    const size_t ws = mla_plan(m, want);
+    if (ws) m.ws_o = attention_workspace(S(stream), ws);
+    launch_mla(m, S(stream));
   });
 }
 

@@ -166,6 +166,33 @@ int qdecode_waves(int n_seqs, int Hkv, int rep, int max_len, int want);
 size_t qdecode_workspace_floats(int n_seqs, int Hkv, int rep, int D, int n_waves);
 void launch_qdecode(const DecodeArgs& a, int bits, int D, hipStream_t st);
 
+// Absorbed-latent MLA decode over a keys-only 8-bit paged view (vkv_mla.hip):
+// 576-dim entries (512 latent + 64 rope), values = the first 512 dims, one
+// kv head, queries and output bf16.
+struct MlaArgs {
+  const uint16_t* q;         // [n_seqs, H, 576] bf16
+  int64_t q_ss, q_sh;        // element strides (sequence, head)
+  uint16_t* out;             // [n_seqs, H, 512] bf16
+  int64_t o_ss, o_sh;
+  float scale;
+  const uint8_t* base;       // block 0 of the layer
+  int64_t block_bytes;
+  int32_t sb_off;            // scale/bias area offset within a chunk
+  const int32_t* table;
+  int32_t table_stride, block_size;
+  const int32_t* seq_lens;   // nullptr = every sequence holds max_len
+  int32_t max_len, H, n_seqs;
+  int32_t n_splits, split_len;  // token splits per sequence and their length
+  float* ws_o;               // split partials [seq][split][head][512]
+  float* ws_ml;              //                (max, sum) [seq][split][head][2]
+};
+bool mla_supported(int dtype, int bits, int group, int head_dim, int v_head_dim, int n_kv_heads,
+                   int block_size);
+// Token splits for a launch (want > 0 overrides); sets a.n_splits and
+// a.split_len and returns the workspace floats the launch needs.
+size_t mla_plan(MlaArgs& a, int want);
+void launch_mla(const MlaArgs& a, hipStream_t st);
+
 // Block pairs passed by value to the block-copy kernel.
 struct BlockPairs {
   static constexpr int kMax = 256;
