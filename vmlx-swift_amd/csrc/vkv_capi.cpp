@@ -393,7 +393,8 @@ int vkv_mla_decode(const vkv_array* q, const vkv_paged_view* kv, float scale, vk
     if (!kv->block_table) throw Error("view has no block table");
     const bool aligned = (reinterpret_cast<uintptr_t>(q->data) % 16 == 0) &&
                          q->strides[0] % 8 == 0 && q->strides[1] % 8 == 0;
-    if (!aligned || getenv("VKV_GENERIC_ATTENTION") ||
+    // (the matrix-core kernel takes the max of the raw scores, so scale > 0)
+    if (!aligned || !(scale > 0.0f) || getenv("VKV_GENERIC_ATTENTION") ||
         !mla_supported(kv->dtype, kv->bits, kv->group_size, kv->head_dim, kv->v_head_dim,
                        kv->n_kv_heads, kv->block_size)) {
       // other latent geometries run on the generic paged kernel
@@ -424,7 +425,7 @@ int vkv_mla_decode(const vkv_array* q, const vkv_paged_view* kv, float scale, vk
     int want = 0;
     if (const char* e = getenv("VKV_MLA_SPLITS")) want = std::max(1, atoi(e));
     const size_t ws = mla_plan(m, want);
-    if (ws) m.ws_o = attention_workspace(S(stream), ws);
+    if (ws) m.ws_o = reinterpret_cast<uint16_t*>(attention_workspace(S(stream), ws));
     launch_mla(m, S(stream));
   });
 }

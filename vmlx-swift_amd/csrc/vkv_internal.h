@@ -183,7 +183,7 @@ struct MlaArgs {
   const int32_t* seq_lens;   // nullptr = every sequence holds max_len
   int32_t max_len, H, n_seqs;
   int32_t n_splits, split_len;  // token splits per sequence and their length
-  float* ws_o;               // split partials [seq][split][head][512]
+  uint16_t* ws_o;            // split partials o/l (bf16) [seq][split][head][512]
   float* ws_ml;              //                (max, sum) [seq][split][head][2]
 };
 bool mla_supported(int dtype, int bits, int group, int head_dim, int v_head_dim, int n_kv_heads,

@@ -69,7 +69,9 @@ constexpr int kDB = kDV / 16;             // 16-dim output tiles
 constexpr int kSbRow = (kDK / 64) * 4;    // (scale, bias) bytes per token
 constexpr int kRawCodes = kTile * kDK;    // code bytes of a tile
 constexpr int kRawBytes = kRawCodes + 2048;  // codes | scale/bias | landing pad
-constexpr int kStages = 4;                // raw staging buffers
+constexpr int kStages = 2;                // raw staging buffers
+constexpr int kKeyBufs = 3;               // bf16 key tiles (PV, QK, dequant target)
+constexpr bool kSoftmaxInPV = false;      // spread the next tile's softmax over P.V
 constexpr int kDmaPerWave = 5;            // 16-byte x 64-lane loads per wave per tile
 constexpr int kPieces = kTile * (kDK / 8) / 256;  // dequant pieces per thread
 constexpr int kMaxSplits = 64;
@@ -116,14 +118,19 @@ template <int HB>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 mla_kernel(const MlaArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t raw[kStages][kRawBytes];
-  __shared__ __attribute__((aligned(16))) uint16_t kt[2][kTile * kRow];
-  __shared__ __attribute__((aligned(16))) int restart_flag[1][4];
+  __shared__ __attribute__((aligned(16))) uint16_t kt[kKeyBufs][kTile * kRow];
+  __shared__ __attribute__((aligned(16))) int restart_flag[4];
+  __shared__ __attribute__((aligned(16))) uint8_t zero_sb[kSbRow + 12];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, n = lane & 15, g = lane >> 4;
   const int split = blockIdx.x, b = blockIdx.y;
-  const int len = a.seq_lens ? a.seq_lens[b] : a.max_len;
+  const int len =
+      a.seq_lens ? *(reinterpret_cast<const __attribute__((address_space(4))) int32_t*>(
+                       reinterpret_cast<uintptr_t>(a.seq_lens)) +
+                   b)
+                 : a.max_len;
   const int t0 = split * a.split_len;
   const int t1 = min(len, t0 + a.split_len);
   const int ntiles = t1 > t0 ? (t1 - t0 + kTile - 1) / kTile : 0;
@@ -150,15 +157,28 @@ mla_kernel(const MlaArgs a) {
     return;
   }
 
-  // ---- raw tile loads: wave w issues loads w, w+4, ..., w+16 of the 20
-  // (18 x 1 KB of codes, then the scale/bias bytes with a landing pad)
-  auto issue = [&](int i) {
-    const int ic = min(i, ntiles - 1);
-    const int ts = t0 + kTile * ic;
-    const int blk = ts / a.block_size, off = ts - blk * a.block_size;
-    const uint8_t* chunk =
-        a.base + static_cast<int64_t>(a.table[static_cast<int64_t>(b) * a.table_stride + blk]) *
-                     a.block_bytes;
+  // ---- raw tile loads.  chunk_of(i) is the (block, kv head 0) chunk that
+  // holds tile i (tiles past the end reload the last one); issue(i, chunk)
+  // puts tile i's code bytes and scale/bias bytes into raw[i % 2].  Wave w
+  // issues loads w, w+4, ..., w+16 of the 20: 18 x 1 KB of codes, then the
+  // scale/bias bytes, whose 128-byte tail is loaded by 8 lanes while the
+  // other 56 re-read byte 0 into the landing pad.
+  auto tile_off = [&](int i) __attribute__((always_inline)) {  // token offset of tile i within its block
+    const int ts = t0 + kTile * min(i, ntiles - 1);
+    return ts % a.block_size;
+  };
+  // (the table is read through the scalar path: a vector load here would
+  // make the compiler wait for every tile load in flight before using it)
+  auto chunk_of = [&](int i) __attribute__((always_inline)) {
+    const int ts = t0 + kTile * min(i, ntiles - 1);
+    const int64_t idx = static_cast<int64_t>(b) * a.table_stride + ts / a.block_size;
+    const int32_t blk = *(reinterpret_cast<const __attribute__((address_space(4))) int32_t*>(
+                            reinterpret_cast<uintptr_t>(a.table)) +
+                        idx);
+    return a.base + static_cast<int64_t>(blk) * a.block_bytes;
+  };
+  auto issue = [&](int i, const uint8_t* chunk) __attribute__((always_inline)) {
+    const int off = tile_off(i);
     const uint8_t* codes = chunk + off * kDK;
     const uint8_t* sb = chunk + a.sb_off + off * kSbRow;
     const uint32_t lds = lds_addr(&raw[i & (kStages - 1)][0]);
@@ -173,37 +193,35 @@ mla_kernel(const MlaArgs a) {
     } else if (wave == 2) {
       dma16(sb + 16 * lane, lds + kRawCodes);
     } else {
-      // 128 bytes remain; the other lanes re-read byte 0 into the pad
       dma16(sb + (lane < 8 ? 1024 + 16 * lane : 0), lds + kRawCodes + 1024);
     }
   };
 
-  // ---- dequant pieces of this thread: token tk (fixed) and 8-dim storage
-  // positions 8k + pp, k = 0..8.  Within 16 lanes: 4 tokens x 4 adjacent
-  // positions, which keeps the 16-byte LDS stores free of bank conflicts.
-  const int l16 = lane & 15, grp = lane >> 4;
-  const int tk = 8 * wave + 4 * (grp & 1) + (l16 >> 2);
-  const int pp = 4 * (grp >> 1) + (l16 & 3);
+  // ---- dequant pieces of this thread: token tk, octet residue r = q % 4
+  // and parity h, pieces j = 0..8 = dims 8q..8q+7 with q = 8j + 4h + r.
+  // The chunk format stores octet q at position (q % 4) * 18 + q / 4 of a
+  // token row, so piece j reads position 18r + 2j + h, scale/bias group j,
+  // and writes LDS dims 8q: every offset is a lane base plus 16j / 4j / 64j.
+  // A 16-lane group holds tokens t and t + 8 x 4 residues x 2 parities,
+  // which keeps its 16-byte LDS stores on 16 distinct bank quads.
+  const int pr = tid & 3, ph = (tid >> 2) & 1, g16 = tid >> 4;
+  const int tk = (g16 & 7) + 16 * (g16 >> 3) + 8 * ((tid >> 3) & 1);
+  const int raw_off = tk * kDK + 144 * pr + 8 * ph;  // bytes within a raw tile
+  const int sb_off = kRawCodes + tk * kSbRow;         // bytes within a raw tile
+  const int kt_off = tk * kRow + 32 * ph + 8 * pr;    // bf16 within a key tile
   struct Piece {
     u32x2_t c;
     uint32_t sb;
   };
-  // dims 8q..8q+7 sit at storage position (q % 4) * 18 + q / 4 of a token row
-  auto piece_q = [&](int k, int pp) {
-    const int p = 8 * k + pp;
-    const int run = (p >= 18) + (p >= 36) + (p >= 54);
-    return 4 * (p - 18 * run) + run;
-  };
-  auto piece_read = [&](const uint8_t* r, int k, int pp) {
+  // sbp = scale/bias row of the token (the zero row for tokens past the end)
+  auto piece_read = [&](const uint8_t* rc, const uint8_t* sbp, int j) __attribute__((always_inline)) {
     Piece pc;
-    pc.c = *reinterpret_cast<const u32x2_t*>(r + tk * kDK + 8 * (8 * k + pp));
-    pc.sb = *reinterpret_cast<const uint32_t*>(r + kRawCodes + tk * kSbRow +
-                                               4 * (piece_q(k, pp) >> 3));
+    pc.c = *reinterpret_cast<const u32x2_t*>(rc + 16 * j);
+    pc.sb = *reinterpret_cast<const uint32_t*>(sbp + 4 * j);
     return pc;
   };
-  auto piece_write = [&](const Piece& pc, uint16_t* dst, bool valid, int k, int pp) {
-    const uint32_t sbw = valid ? pc.sb : 0u;  // tokens past the end become zeros
-    const float s = __uint_as_float(sbw << 16), bb = __uint_as_float(sbw & 0xFFFF0000u);
+  auto piece_write = [&](const Piece& pc, uint16_t* dst, int j) __attribute__((always_inline)) {
+    const float s = __uint_as_float(pc.sb << 16), bb = __uint_as_float(pc.sb & 0xFFFF0000u);
     u32x4_t w;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
@@ -213,13 +231,23 @@ mla_kernel(const MlaArgs a) {
       w[2 * h + 1] = pack_bf16(fmaf(s, static_cast<float>((x >> 16) & 0xFF), bb),
                                fmaf(s, static_cast<float>(x >> 24), bb));
     }
-    *reinterpret_cast<u32x4_t*>(dst + 8 * piece_q(k, pp)) = w;
+    *reinterpret_cast<u32x4_t*>(dst + 64 * j) = w;
   };
-  auto dequant_all = [&](int i) {
+  // tile i: raw[i % 2] -> kt[i % 3]
+  // (ob: an opaque zero that keeps the per-buffer addresses from being
+  // hoisted out of the tile loop and held in registers)
+  auto piece_src = [&](int i, int ob, const uint8_t*& rc, const uint8_t*& sbp,
+                       uint16_t*& dst) __attribute__((always_inline)) {
     const uint8_t* r = &raw[i & (kStages - 1)][0];
-    uint16_t* dst = &kt[i & 1][tk * kRow];
-    const bool valid = t0 + kTile * i + tk < t1;
-    sfor<kPieces>([&](auto K) { piece_write(piece_read(r, K, pp), dst, valid, K, pp); });
+    rc = r + raw_off + ob;
+    sbp = (t0 + kTile * i + tk < t1) ? r + sb_off + ob : zero_sb;
+    dst = &kt[i % kKeyBufs][kt_off + ob];
+  };
+  auto dequant_all = [&](int i) __attribute__((always_inline)) {
+    const uint8_t *rc, *sbp;
+    uint16_t* dst;
+    piece_src(i, 0, rc, sbp, dst);
+    sfor<kPieces>([&](auto J) { piece_write(piece_read(rc, sbp, J), dst, J); });
   };
 
   // ---- queries (B operand of the score MFMA): head hw + 16 hb + n,
@@ -239,6 +267,136 @@ mla_kernel(const MlaArgs a) {
 #pragma unroll
   for (int hb = 0; hb < HB; hb++) m_est[hb] = -INFINITY;
 
+  // ---- scores S^T [32 tokens x 16*HB heads] of tile j (kt[j % 3]), with
+  // tile j+1's dequant (raw[(j+1) % 2] -> kt[(j+1) % 3]) interleaved: piece
+  // k's LDS reads one step before its stores
+  f32x4_t s[2][HB];
+  auto qk_dequant = [&](int j, int ob) __attribute__((always_inline)) {
+    const uint16_t* K = &kt[j % kKeyBufs][0];
+    const uint8_t *rcn, *sbn;
+    uint16_t* dn;
+    piece_src(j + 1, ob, rcn, sbn, dn);
+    const uint16_t* kr0 = K + n * kRow + 8 * g + ob;
+    const uint16_t* kr1 = kr0 + 16 * kRow;
+#pragma unroll
+    for (int tb = 0; tb < 2; tb++)
+#pragma unroll
+      for (int hb = 0; hb < HB; hb++) s[tb][hb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    u32x4_t ka[2][2];
+    ka[0][0] = *reinterpret_cast<const u32x4_t*>(kr0);
+    ka[0][1] = *reinterpret_cast<const u32x4_t*>(kr1);
+    Piece pc[2];
+    pc[0] = piece_read(rcn, sbn, 0);
+    sfor<kChunks>([&](auto C) {
+      constexpr int c = decltype(C)::value;
+      if constexpr (c + 1 < kChunks) {
+        ka[(c + 1) & 1][0] = *reinterpret_cast<const u32x4_t*>(kr0 + 32 * (c + 1));
+        ka[(c + 1) & 1][1] = *reinterpret_cast<const u32x4_t*>(kr1 + 32 * (c + 1));
+      }
+      if constexpr (c % 2 == 0 && c / 2 + 1 < kPieces)
+        pc[(c / 2 + 1) & 1] = piece_read(rcn, sbn, c / 2 + 1);
+      if constexpr (c % 2 == 1) piece_write(pc[(c / 2) & 1], dn, c / 2);
+#pragma unroll
+      for (int hb = 0; hb < HB; hb++) {
+        s[0][hb] = mfma(ka[c & 1][0], qf[hb][c], s[0][hb]);
+        s[1][hb] = mfma(ka[c & 1][1], qf[hb][c], s[1][hb]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // ---- softmax of tile j, part 1: mask the tokens past the end (last
+  // tile only), check the scores against the fixed running max.  Returns
+  // true when the split must be run again.
+  auto softmax_check = [&](int j, int ob) __attribute__((always_inline)) {
+    const int rem = t1 - (t0 + kTile * j);
+    if (rem < kTile) {
+      asm volatile("");  // keep this a branch: the mask is for one tile in many
+      const int r4 = rem - 4 * g - ob;
+#pragma unroll
+      for (int tb = 0; tb < 2; tb++)
+#pragma unroll
+        for (int hb = 0; hb < HB; hb++)
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if (16 * tb + e >= r4) s[tb][hb][e] = -INFINITY;
+    }
+    float mloc[HB];
+    bool need = false;
+#pragma unroll
+    for (int hb = 0; hb < HB; hb++) {
+      // scale > 0, so the largest score maps to the largest logit
+      mloc[hb] = fmaxf(fmaxf(fmaxf(s[0][hb][0], s[0][hb][1]), fmaxf(s[0][hb][2], s[0][hb][3])),
+                       fmaxf(fmaxf(s[1][hb][0], s[1][hb][1]), fmaxf(s[1][hb][2], s[1][hb][3]))) *
+                 cl;
+      need |= mloc[hb] > m_run[hb] + kTau;
+    }
+    bool redo = false;
+    if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+      for (int hb = 0; hb < HB; hb++) {
+        float mx = mloc[hb];
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        m_est[hb] = fmaxf(m_est[hb], mx);
+      }
+      if (j == 0) {
+        // nothing accumulated yet: take the max as is
+#pragma unroll
+        for (int hb = 0; hb < HB; hb++) m_run[hb] = m_est[hb];
+      } else {
+        redo = true;
+      }
+    }
+    return redo;
+  };
+  // part 2, one (tb, hb) quarter at a time: probabilities of the lane's 4
+  // tokens, summed into l_run and packed into the P.V operand
+  auto softmax_part = [&](int tb, int hb, u32x4_t (&pn)[HB]) __attribute__((always_inline)) {
+    float p[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      p[e] = fast_exp2(fmaf(s[tb][hb][e], cl, -m_run[hb]));
+      l_run[hb] += p[e];
+    }
+    pn[hb][2 * tb] = pack_bf16(p[0], p[1]);
+    pn[hb][2 * tb + 1] = pack_bf16(p[2], p[3]);
+  };
+
+  // ---- P V of tile i (kt[i % 3], probabilities p) with tile j = i+1's
+  // probabilities computed in between (into pn).  Value operand of dim
+  // 16 db + n: tokens 4g..4g+3 and 16+4g..16+4g+3 (two transposing reads),
+  // two output tiles ahead.
+  auto pv_softmax = [&](int i, int ob, const u32x4_t (&p)[HB], u32x4_t (&pn)[HB])
+                        __attribute__((always_inline)) {
+    // vr0 is made opaque so that the 64 read addresses below are formed
+    // from it inside the loop instead of being hoisted out of it and held
+    // in (spilled) registers
+    uint32_t vr0 = lds_addr(&kt[i % kKeyBufs][(4 * g + (n >> 2)) * kRow + 4 * (n & 3) + ob]);
+    asm volatile("" : "+v"(vr0));
+    auto vload = [&](int db) __attribute__((always_inline)) {
+      const i16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          reinterpret_cast<l_i16x4_t*>(static_cast<uintptr_t>(vr0 + 32 * db)));
+      const i16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          reinterpret_cast<l_i16x4_t*>(static_cast<uintptr_t>(vr0 + 32 * db + 32 * kRow)));
+      const u32x2_t w0 = __builtin_bit_cast(u32x2_t, v0), w1 = __builtin_bit_cast(u32x2_t, v1);
+      return u32x4_t{w0[0], w0[1], w1[0], w1[1]};
+    };
+    constexpr int kVA = 3;  // value operands in flight
+    u32x4_t vb[kVA + 1];
+    sfor<kVA>([&](auto D) { vb[D] = vload(D); });
+    sfor<kDB>([&](auto D) {
+      constexpr int db = decltype(D)::value;
+      if constexpr (db + kVA < kDB) vb[(db + kVA) % (kVA + 1)] = vload(db + kVA);
+      // next tile's softmax in quarters, spread over the first output tiles
+      if constexpr (kSoftmaxInPV && db % 4 == 1 && db / 4 < 2 * HB)
+        softmax_part((db / 4) & 1, (db / 4) >> 1, pn);
+#pragma unroll
+      for (int hb = 0; hb < HB; hb++) o[hb][db] = mfma(p[hb], vb[db % (kVA + 1)], o[hb][db]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
   // The running max starts at the first tile's max and is otherwise fixed:
   // probabilities up to 2^kTau are exact enough in fp32/bf16.  A score that
   // exceeds it by more than kTau makes the workgroup run the split again,
@@ -246,7 +404,12 @@ mla_kernel(const MlaArgs a) {
   // run never needs a third.  (The accumulators are never rescaled: a
   // rescale branch in the loop makes the compiler copy all of them on every
   // tile.)
-  auto run = [&]() -> bool {
+  //
+  // Pipeline (one barrier per tile): iteration i runs QK(i+1) with
+  // dequant(i+2) interleaved, then P V(i) with softmax(i+1) interleaved;
+  // three key tiles (PV, QK, dequant target) and two raw stages (the one
+  // being dequantized and the one in flight).
+  auto run = [&]() __attribute__((always_inline)) -> bool {
 #pragma unroll
     for (int hb = 0; hb < HB; hb++) {
 #pragma unroll
@@ -254,138 +417,51 @@ mla_kernel(const MlaArgs a) {
       m_run[hb] = m_est[hb];
       l_run[hb] = 0.f;
     }
-    // prologue: tiles 0..2 in flight, tile 0 dequantized
-    issue(0);
-    issue(1);
-    issue(2);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kDmaPerWave) : "memory");
+    if (tid < (kSbRow + 12) / 4) reinterpret_cast<uint32_t*>(zero_sb)[tid] = 0u;
+    issue(0, chunk_of(0));
+    issue(1, chunk_of(1));
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerWave) : "memory");
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     dequant_all(0);
-
-    int redo = 0;
-    for (int i = 0; i < ntiles; i++) {
-      issue(i + 3);
-      // tile i+1's raw bytes are the oldest but two tiles of loads
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kDmaPerWave) : "memory");
-      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      const uint16_t* K = &kt[i & 1][0];
-      // scores S^T [32 tokens x 16*HB heads], with tile i+1's dequant
-      // interleaved (piece k's LDS reads one step before its stores)
-      // the piece offsets are recomputed each tile (a few VALU ops) rather
-      // than held in 27 registers across the loop
-      int ppv = pp;
-      asm volatile("" : "+v"(ppv));
-      const uint8_t* rn = &raw[(i + 1) & (kStages - 1)][0];
-      uint16_t* dn = &kt[(i + 1) & 1][tk * kRow];
-      const bool vn = t0 + kTile * (i + 1) + tk < t1;
-      const uint16_t* kr0 = K + n * kRow + 8 * g;
-      const uint16_t* kr1 = kr0 + 16 * kRow;
-      f32x4_t s[2][HB];
-#pragma unroll
-      for (int tb = 0; tb < 2; tb++)
-#pragma unroll
-        for (int hb = 0; hb < HB; hb++) s[tb][hb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      u32x4_t ka[3][2];
-      ka[0][0] = *reinterpret_cast<const u32x4_t*>(kr0);
-      ka[0][1] = *reinterpret_cast<const u32x4_t*>(kr1);
-      ka[1][0] = *reinterpret_cast<const u32x4_t*>(kr0 + 32);
-      ka[1][1] = *reinterpret_cast<const u32x4_t*>(kr1 + 32);
-      Piece pc[2];
-      pc[0] = piece_read(rn, 0, ppv);
-      sfor<kChunks>([&](auto C) {
-        constexpr int c = decltype(C)::value;
-        if constexpr (c + 2 < kChunks) {
-          ka[(c + 2) % 3][0] = *reinterpret_cast<const u32x4_t*>(kr0 + 32 * (c + 2));
-          ka[(c + 2) % 3][1] = *reinterpret_cast<const u32x4_t*>(kr1 + 32 * (c + 2));
-        }
-        if constexpr (c % 2 == 0 && c / 2 + 1 < kPieces)
-          pc[(c / 2 + 1) & 1] = piece_read(rn, c / 2 + 1, ppv);
-        if constexpr (c % 2 == 1) piece_write(pc[(c / 2) & 1], dn, vn, c / 2, ppv);
-#pragma unroll
-        for (int hb = 0; hb < HB; hb++) {
-          s[0][hb] = mfma(ka[c % 3][0], qf[hb][c], s[0][hb]);
-          s[1][hb] = mfma(ka[c % 3][1], qf[hb][c], s[1][hb]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      });
-
-      // softmax (log2 domain) against the fixed running max
-      const int rem = t1 - (t0 + kTile * i);
-      float x[HB][2][4], mloc[HB];
-      bool need = false;
-#pragma unroll
-      for (int hb = 0; hb < HB; hb++) {
-        mloc[hb] = -INFINITY;
-#pragma unroll
-        for (int tb = 0; tb < 2; tb++)
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            float v = s[tb][hb][e] * cl;
-            if (rem < kTile && 16 * tb + 4 * g + e >= rem) v = -INFINITY;
-            x[hb][tb][e] = v;
-            mloc[hb] = fmaxf(mloc[hb], v);
-          }
-        need |= mloc[hb] > m_run[hb] + kTau;
-      }
-      if (__builtin_amdgcn_ballot_w64(need)) {
-#pragma unroll
-        for (int hb = 0; hb < HB; hb++) {
-          float mx = mloc[hb];
-          mx = fmaxf(mx, __shfl_xor(mx, 16));
-          mx = fmaxf(mx, __shfl_xor(mx, 32));
-          m_est[hb] = fmaxf(m_est[hb], mx);
-        }
-        if (i == 0) {
-          // nothing accumulated yet: take the max as is
-#pragma unroll
-          for (int hb = 0; hb < HB; hb++) m_run[hb] = m_est[hb];
-        } else {
-          redo = 1;
-        }
-      }
-      u32x4_t pa[HB];
-#pragma unroll
-      for (int hb = 0; hb < HB; hb++) {
-        float p[2][4];
-        float ls = 0.f;
-#pragma unroll
-        for (int tb = 0; tb < 2; tb++)
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            p[tb][e] = fast_exp2(x[hb][tb][e] - m_run[hb]);
-            ls += p[tb][e];
-          }
-        l_run[hb] += ls;
-        pa[hb] = u32x4_t{pack_bf16(p[0][0], p[0][1]), pack_bf16(p[0][2], p[0][3]),
-                         pack_bf16(p[1][0], p[1][1]), pack_bf16(p[1][2], p[1][3])};
-      }
-
-      // P V: value operand of dim 16 db + n, tokens 4g..4g+3 and
-      // 16+4g..16+4g+3 (two transposing reads), four output tiles ahead
-      const uint16_t* vr0 = K + (4 * g + (n >> 2)) * kRow + 4 * (n & 3);
-      const uint16_t* vr1 = vr0 + 16 * kRow;
-      auto vload = [&](int db) {
-        const i16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((l_i16x4_t*)(vr0 + 16 * db));
-        const i16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((l_i16x4_t*)(vr1 + 16 * db));
-        const u32x2_t w0 = __builtin_bit_cast(u32x2_t, v0), w1 = __builtin_bit_cast(u32x2_t, v1);
-        return u32x4_t{w0[0], w0[1], w1[0], w1[1]};
-      };
-      constexpr int kVA = 4;  // value operands in flight
-      u32x4_t vb[kVA + 1];
-      sfor<kVA>([&](auto D) { vb[D] = vload(D); });
-      sfor<kDB>([&](auto D) {
-        constexpr int db = decltype(D)::value;
-        if constexpr (db + kVA < kDB) vb[(db + kVA) % (kVA + 1)] = vload(db + kVA);
-#pragma unroll
-        for (int hb = 0; hb < HB; hb++) o[hb][db] = mfma(pa[hb], vb[db % (kVA + 1)], o[hb][db]);
-        __builtin_amdgcn_sched_barrier(0);
-      });
-    }
-    // every raw-tile load has landed before the staging buffers are reused
-    // or the workgroup ends; then agree on a second run
-    if (lane == 0) restart_flag[0][wave] = redo;
     asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    const u32x4_t f = *reinterpret_cast<const u32x4_t*>(&restart_flag[0][0]);
+    issue(2, chunk_of(2));
+    const uint8_t* cnext = chunk_of(3);
+    qk_dequant(0, 0);
+    bool redo = softmax_check(0, 0);
+    u32x4_t p[HB];
+#pragma unroll
+    for (int hb = 0; hb < HB; hb++)
+#pragma unroll
+      for (int tb = 0; tb < 2; tb++) softmax_part(tb, hb, p);
+
+    for (int i = 0; i < ntiles; i++) {
+      // raw(i+2) has landed and K(i+1) is complete in every wave; PV(i-1)
+      // is done with kt[(i+2) % 3] and dequant(i+1) with raw[(i+1) % 2]
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      int ob = 0;
+      asm volatile("" : "+v"(ob));
+      issue(i + 3, cnext);
+      cnext = chunk_of(i + 4);
+      qk_dequant(i + 1, ob);
+      redo |= softmax_check(i + 1, ob);
+      u32x4_t pn[HB];
+      if constexpr (!kSoftmaxInPV) {
+#pragma unroll
+        for (int hb = 0; hb < HB; hb++)
+#pragma unroll
+          for (int tb = 0; tb < 2; tb++) softmax_part(tb, hb, pn);
+      }
+      pv_softmax(i, ob, p, pn);
+#pragma unroll
+      for (int hb = 0; hb < HB; hb++) p[hb] = pn[hb];
+    }
+    // the extra tile ntiles was all masked: its probabilities are zero and
+    // its sum is not added (l_run got zeros); every raw-tile load has landed
+    // before the staging buffers are reused or the workgroup ends; then
+    // agree on a second run
+    if (lane == 0) restart_flag[wave] = redo ? 1 : 0;
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const u32x4_t f = *reinterpret_cast<const u32x4_t*>(&restart_flag[0]);
     const bool any = (f[0] | f[1] | f[2] | f[3]) != 0;
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     return any;
@@ -398,40 +474,35 @@ mla_kernel(const MlaArgs a) {
     float lt = l_run[hb];
     lt += __shfl_xor(lt, 16);
     lt += __shfl_xor(lt, 32);  // sum of head hw + 16 hb + n
-    if (a.n_splits == 1) {
-      const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-      float ir[4];
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    float ir[4];
 #pragma unroll
-      for (int e = 0; e < 4; e++) ir[e] = __shfl(inv, 4 * g + e);
+    for (int e = 0; e < 4; e++) ir[e] = __shfl(inv, 4 * g + e);
+    // whole sequence: the output; a split: its normalized partial (bf16)
+    // and (max, sum)
+    uint16_t* dst = a.n_splits == 1 ? a.out : a.ws_o;
+    const int64_t dss = a.n_splits == 1 ? a.o_ss : static_cast<int64_t>(a.H) * kDV;
+    const int64_t dsh = a.n_splits == 1 ? a.o_sh : kDV;
+    const int64_t row = a.n_splits == 1 ? b : static_cast<int64_t>(slot);
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int h = hw + 16 * hb + 4 * g + e;
-        if (h < a.H) {
-          uint16_t* op = a.out + b * a.o_ss + static_cast<int64_t>(h) * a.o_sh + n;
+    for (int e = 0; e < 4; e++) {
+      const int h = hw + 16 * hb + 4 * g + e;
+      if (h < a.H) {
+        uint16_t* op = dst + row * dss + static_cast<int64_t>(h) * dsh + n;
 #pragma unroll
-          for (int db = 0; db < kDB; db++) op[16 * db] = f32_to_bf16(o[hb][db][e] * ir[e]);
-        }
+        for (int db = 0; db < kDB; db++) op[16 * db] = f32_to_bf16(o[hb][db][e] * ir[e]);
       }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int h = hw + 16 * hb + 4 * g + e;
-        if (h < a.H) {
-          float* op = a.ws_o + (slot * a.H + h) * kDV + n;
-#pragma unroll
-          for (int db = 0; db < kDB; db++) op[16 * db] = o[hb][db][e];
-        }
-      }
-      const int h = hw + 16 * hb + n;
-      if (g == 0 && h < a.H) {
-        a.ws_ml[(slot * a.H + h) * 2] = m_run[hb];
-        a.ws_ml[(slot * a.H + h) * 2 + 1] = lt;
-      }
+    }
+    const int h = hw + 16 * hb + n;
+    if (a.n_splits > 1 && g == 0 && h < a.H) {
+      a.ws_ml[(slot * a.H + h) * 2] = m_run[hb];
+      a.ws_ml[(slot * a.H + h) * 2 + 1] = lt;
     }
   }
 }
 
 // Merge of the split partials of one (sequence, head): 128 threads x 4 dims.
+// Partial s holds o_s / l_s (bf16) with its max m_s and sum l_s (log2 units).
 __global__ void __launch_bounds__(128) mla_combine_kernel(const MlaArgs a) {
   const int h = blockIdx.x, b = blockIdx.y;
   const int d = 4 * threadIdx.x;
@@ -446,11 +517,13 @@ __global__ void __launch_bounds__(128) mla_combine_kernel(const MlaArgs a) {
   for (int s = 0; s < a.n_splits; s++) {
     const float* ml = a.ws_ml + ((s0 + s) * a.H + h) * 2;
     const float l = ml[1];
-    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(a.ws_o + ((s0 + s) * a.H + h) * kDV + d);
-    const float w = l > 0.f ? fast_exp2(ml[0] - M) : 0.f;
-    den += w * l;
+    const u32x2_t v = *reinterpret_cast<const u32x2_t*>(a.ws_o + ((s0 + s) * a.H + h) * kDV + d);
+    const float w = l > 0.f ? fast_exp2(ml[0] - M) * l : 0.f;
+    den += w;
+    const float x[4] = {__uint_as_float(v[0] << 16), __uint_as_float(v[0] & 0xFFFF0000u),
+                        __uint_as_float(v[1] << 16), __uint_as_float(v[1] & 0xFFFF0000u)};
 #pragma unroll
-    for (int e = 0; e < 4; e++) acc[e] = l > 0.f ? acc[e] + w * v[e] : acc[e];
+    for (int e = 0; e < 4; e++) acc[e] = l > 0.f ? fmaf(w, x[e], acc[e]) : acc[e];
   }
   const float inv = den > 0.f ? 1.0f / den : 0.f;
   uint16_t* op = a.out + b * a.o_ss + static_cast<int64_t>(h) * a.o_sh + d;
@@ -488,12 +561,14 @@ size_t mla_plan(MlaArgs& a, int want) {
   a.split_len = per * kTile;
   a.n_splits = (max_tiles + per - 1) / per;
   if (a.n_splits == 1) return 0;
-  return static_cast<size_t>(a.n_seqs) * a.n_splits * a.H * (kDV + 2);
+  // bf16 partial outputs, then (max, sum) pairs, in floats
+  return static_cast<size_t>(a.n_seqs) * a.n_splits * a.H * (kDV / 2 + 2);
 }
 
 void launch_mla(const MlaArgs& a0, hipStream_t st) {
   MlaArgs a = a0;
-  if (a.n_splits > 1) a.ws_ml = a.ws_o + static_cast<size_t>(a.n_seqs) * a.n_splits * a.H * kDV;
+  if (a.n_splits > 1)
+    a.ws_ml = reinterpret_cast<float*>(a.ws_o + static_cast<size_t>(a.n_seqs) * a.n_splits * a.H * kDV);
   const int hb = a.H > 64 ? 2 : 1;
   const dim3 grid(a.n_splits, a.n_seqs, (a.H + 64 * hb - 1) / (64 * hb));
   if (hb == 2)
