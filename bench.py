@@ -13,7 +13,9 @@ position each step, so every step does identical work.
 
 Prints one JSON line: "value" is the whole-step KV-read rate (appends included),
 "attention" and "roofline" time the paged decode call alone, "traffic" is the
-PMC-measured HBM bytes per decode launch, "cpu_baseline" times the C oracle.
+PMC-measured HBM bytes per decode launch, "cpu_baseline" times the C oracle,
+and "mla" is the MLA latent decode workload (32 x 16384 tokens, 128 heads) with
+its MFMA roofline.
 """
 import argparse
 import json
@@ -25,6 +27,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "vmlx-swift_amd"))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 BYTES_PER_TOKEN_HEAD = 144  # 4-bit K+V codes (2 x 64 B) + 2 groups x (scale+bias) x 2 B x 2
 
 
@@ -36,6 +39,8 @@ def parse():
     p.add_argument("--layers", type=int, default=32)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-threads", type=int, default=0)
+    p.add_argument("--no-mla", action="store_true",
+                   help="skip the MLA latent decode measurement (config 5)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 1 GiB device copy (vkv_array_copy) 5 times: the "
                         "reference reading for the FETCH_SIZE / WRITE_SIZE counters")
@@ -147,6 +152,65 @@ def build_scene(torch, vkv, layers, seed=3):
     return pool, sc
 
 
+def mla_measure(torch, vkv, steps, warmup):
+    """Config 5: MLA absorbed decode over an 8-bit g64 latent pool (576-dim
+    entries, 64-token blocks), 32 sequences x 16384 tokens, 128 query heads.
+    One step = one vkv_mla_decode call (main kernel + split combine), timed
+    with HIP events on the launching stream."""
+    B, T, H, DK, DV, BS = 32, 16384, 128, 576, 512, 64
+    nb = B * T // BS + 1
+    pool = vkv.PagedPool(nb, BS, 1, 1, DK, dtype=vkv.BF16, bits=8, group_size=64, v_head_dim=DV,
+                         flags=vkv.VIEW_KEYS_ONLY)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    table = (torch.randperm(nb - 1, device="cuda", generator=gen).int() + 1).view(B, T // BS)
+    table = table.contiguous()
+    slots = (table.view(-1, 1) * BS + torch.arange(BS, device="cuda", dtype=torch.int32)).view(-1)
+    chunk = 65536
+    x = torch.empty((chunk, 1, DK), dtype=torch.bfloat16, device="cuda")
+    for c in range(0, B * T, chunk):
+        vkv.fill_normal(x, seed=17 + c, std=0.5)   # latent ~ N(0, 0.5)
+        pool.append(0, x, None, slots[c:c + chunk].contiguous())
+    lens = torch.full((B,), T, dtype=torch.int32, device="cuda")
+    view = pool.view(0, table, lens, T)
+    q = torch.empty((B, H, DK), dtype=torch.bfloat16, device="cuda")
+    vkv.fill_normal(q, seed=23)
+    out = torch.empty((B, H, DV), dtype=torch.bfloat16, device="cuda")
+    scale = 192 ** -0.5
+    stream = torch.cuda.current_stream()
+
+    def call():
+        vkv._chk(vkv.lib().vkv_mla_decode(
+            vkv.C.byref(vkv.arr(q)), vkv.C.byref(view), vkv.C.c_float(scale),
+            vkv.C.byref(vkv.arr(out)), vkv.stream_ptr()))
+
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    kv_bytes = B * T * (DK + (DK // 64) * 4)          # 612 B per entry
+    flops = 2.0 * H * B * T * (DK + DV)
+    tflops = flops / (ms * 1e-3) / 1e12
+    del pool
+    return {
+        "workload": "MLA absorbed decode: 32 seqs x 16384 tokens, 576-dim latent+rope entries "
+                    "8-bit g64 (9 groups) in 64-token pages, 128 query heads, out 512 dims",
+        "ms_per_step": round(ms, 4),
+        "kv_gbs": round(kv_bytes / (ms * 1e-3) / 1e9, 1),
+        "tflops": round(tflops, 1),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "finite": bool(torch.isfinite(out.float()).all()),
+    }
+
+
 def cpu_baseline(threads, min_seconds=10.0):
     """The CPU oracle (C restatement of the reference arithmetic, fp64,
     OpenMP) on one layer of the same workload: the 64 config-3 sequences
@@ -255,6 +319,7 @@ def main():
     gbs_step = logical * layers / (ms_per_step * 1e-3) / 1e9
     att_gbs = logical / (att_avg_ms * 1e-3) / 1e9
     append_tokens = sc["n_seqs"] + sc["prefill"]
+    mla = None if args.no_mla else mla_measure(torch, vkv, args.steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
@@ -289,6 +354,7 @@ def main():
                      "unit": "GB/s", "frac": round(att_gbs / HBM_PEAK_GBS, 4),
                      "traffic": pmc_traffic()},
         "cpu_baseline": cpu,
+        "mla": mla,
     }
     print(json.dumps(rec), flush=True)
 
