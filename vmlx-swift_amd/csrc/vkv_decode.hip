@@ -42,17 +42,21 @@
 // bounds probabilities by e^kTau.
 //
 // Work split.  The (sequence, kv head, head group, 64-token step) units of
-// the whole batch are laid end to end and every wave (one per workgroup)
-// takes an equal contiguous range of them, so mixed sequence lengths cost
-// no load imbalance.  A range crosses a few (sequence, head) segments; at
-// each boundary the wave finalizes the segment (the output itself when the
+// the whole batch are laid end to end, each (sequence, head group) pair led
+// by kSegCost extra cost units for its finalize, and every wave takes an
+// equal contiguous range of cost units, so mixed sequence lengths cost no
+// load imbalance.  A range crosses a few (sequence, head) segments; at each
+// boundary the wave finalizes the segment (the output itself when the
 // segment covers the whole sequence, else an (o, max, sum) partial that
-// qdecode_combine_kernel merges, as sdpa_vector_2pass_2 merges) and
-// rebuilds its wave-local query table.  The next unit's KV loads, and the
-// queries of the next unit's segment, are in flight while the current unit
-// computes.  (Merging partials in the last wave to finish would need
-// device-scope release/acquire fences, which on gfx950 write back and
-// invalidate the XCD's whole L2 and cost more than the extra launch.)
+// qdecode_combine_kernel merges, as sdpa_vector_2pass_2 merges) and rebuilds
+// its wave-local query table.  The next unit's KV loads are in flight while
+// the current unit computes, and the next segment's queries while the
+// current segment does.  Up to 128 dims a workgroup is the 8 waves of one CU
+// (two per SIMD), and the two waves of a SIMD trade instruction-issue
+// priority so that neither finishes long before the other.  (Merging
+// partials in the last wave to finish would need device-scope
+// release/acquire fences, which on gfx950 write back and invalidate the
+// XCD's whole L2 and cost more than the extra launch.)
 #include <algorithm>
 #include <utility>
 
@@ -83,6 +87,12 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 constexpr int kMaxRange = 64;   // units (64-token steps) per wave, at most
 constexpr int kMaxSeqs = 256;   // sequences per launch (the host splits larger batches)
 constexpr int kMaxParts = 32;   // partials per (sequence, head pair), at most
+// Work-split cost of a (sequence, head pair) beyond its 64-token steps: the
+// finalize and set-up at a segment boundary take about as long as a step
+// (0.7 steps measured at 128 dims, 4 bits), so the ranges count each pair
+// as steps + kSegCost units and a range that crosses many short sequences
+// gets fewer steps.
+constexpr int kSegCost = 1;
 
 template <int... Is, class F>
 __device__ __forceinline__ void sfor_impl(std::integer_sequence<int, Is...>, F&& f) {
@@ -254,12 +264,21 @@ struct QD {
   };
 };
 
-// One wave per workgroup; see the header comment for the work split.
-// Two waves per SIMD (256 VGPRs each) up to D = 128, one for D = 256.
+// Waves per workgroup.  Up to D = 128 two waves share each SIMD (256 VGPRs
+// each) and a workgroup is the 8 waves of one CU, so that the two waves of a
+// SIMD can balance their progress; D = 256 runs one wave per SIMD.
+template <int D>
+constexpr int qd_waves() { return D >= 256 ? 1 : 8; }
+
+// See the header comment for the work split.  Every wave works on its own
+// range with its own LDS tables; the waves of a workgroup only share their
+// SIMD placement and unit counters.
 template <int BITS, int D, int HP>
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu((D >= 256) ? 1 : 2)))
+__global__ void __launch_bounds__(64 * qd_waves<D>())
+__attribute__((amdgpu_waves_per_eu((D >= 256) ? 1 : 2)))
 qdecode_kernel(DecodeArgs a) {
   using C = QD<BITS, D, HP>;
+  constexpr int WPG = qd_waves<D>();
   constexpr int G = C::G, PP = C::PP, TT = C::TT, SPW = C::SPW, SL = C::SL;
   constexpr int RUN = C::RUN, NT = C::NT, VW = C::VW, ROW = C::ROW, SBW = C::SBW;
   constexpr int QROW = C::QROW, QCH = C::QCH, QPL = C::QPL;
@@ -268,19 +287,45 @@ qdecode_kernel(DecodeArgs a) {
   constexpr int QT_ENTRIES = SL * QROW;
   static_assert(QT_ENTRIES * 16 >= kMaxSeqs * 8, "the sequence scan reuses the query table");
 
-  // LDS (all private to the wave): the score B operands, the KV chunk of
-  // every 32-token sub-block of the range, and the range's segments.  The
+  // LDS (one set per wave): the score B operands, the KV chunk of every
+  // 32-token sub-block of the range, and the range's segments.  The
   // per-sequence unit prefix of the set-up lives in the query table's space.
-  __shared__ u32x4_t qtab[QT_ENTRIES];
-  __shared__ int64_t sub_off[2 * kMaxRange];  // chunk byte offset (block, kv head)
-  __shared__ int32_t sub_t0[2 * kMaxRange];   // first token of the sub-block in its block
-  __shared__ int32_t seg_tab[kMaxRange][6];   // seq, pair, first step, units, len, first unit
-  __shared__ int32_t seq_len[kMaxSeqs];
+  __shared__ u32x4_t qtab_g[WPG][QT_ENTRIES];
+  __shared__ int64_t sub_off_g[WPG][2 * kMaxRange];  // chunk byte offset (block, kv head)
+  __shared__ int32_t sub_t0_g[WPG][2 * kMaxRange];   // first token of the sub-block in its block
+  // per segment: seq, pair, first step, steps, len, first unit of the range,
+  // cost position of the pair's first step
+  __shared__ int32_t seg_tab_g[WPG][kMaxRange][7];
+  __shared__ int32_t seq_len_g[WPG][kMaxSeqs];
+  __shared__ int32_t simd_of[WPG];  // SIMD of each wave of the workgroup
+  __shared__ int32_t done_of[WPG];  // units each wave has started
+  const int wv = WPG > 1 ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6) : 0;
+  u32x4_t* qtab = qtab_g[wv];
+  int64_t* sub_off = sub_off_g[wv];
+  int32_t* sub_t0 = sub_t0_g[wv];
+  int32_t(*seg_tab)[7] = seg_tab_g[wv];
+  int32_t* seq_len = seq_len_g[wv];
   int32_t* seq_cum = reinterpret_cast<int32_t*>(qtab);
   int32_t* seq_nst = seq_cum + kMaxSeqs;
 
-  const int lane = threadIdx.x, n = lane & 15, lg = lane >> 4;
-  const int w = blockIdx.x, W = gridDim.x;
+  const int lane = threadIdx.x & 63, n = lane & 15, lg = lane >> 4;
+  const int w = blockIdx.x * WPG + wv, W = gridDim.x * WPG;
+
+  // The wave that shares this wave's SIMD (-1: none).  Of two waves on a
+  // SIMD the older one wins instruction issue, so left alone it finishes
+  // its range long before the younger one, which then runs alone; instead
+  // the wave that is behind raises its priority (below).
+  int partner = -1;
+  if constexpr (WPG > 1) {
+    uint32_t hw_id;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw_id));
+    simd_of[wv] = (hw_id >> 4) & 3;  // HW_ID[5:4]: SIMD
+    done_of[wv] = 0;
+    __syncthreads();
+    for (int o = 0; o < WPG; o++)
+      if (o != wv && simd_of[o] == simd_of[wv]) partner = o;
+    partner = __builtin_amdgcn_readfirstlane(partner);
+  }
   const int rep = a.rep, n_hg = (rep + HP - 1) / HP, HG = a.Hkv * n_hg;
   const int ns = a.n_seqs;
   const int subs = a.block_size >> 5;  // 32-token sub-blocks per pool block
@@ -289,15 +334,17 @@ qdecode_kernel(DecodeArgs a) {
   const int p = n / HP, h = n % HP;
   const int pA = lg / SPW, wA = lg % SPW;
 
-  // ---- units per sequence (steps x head pairs) and their prefix sums
+  // ---- cost per sequence ((steps + kSegCost) x head pairs) and its prefix
+  // sums; a pair's cost units are kSegCost lead-in units, then its steps
   int carry = 0, max_nst = 0;
   for (int s0 = 0; s0 < ns; s0 += 64) {
     const int s = s0 + lane;
     const int len = (s < ns) ? (a.seq_lens ? a.seq_lens[s] : a.max_len) : 0;
     const int nst = (len + 63) >> 6;
-    const int incl = wave_incl_scan(nst * HG, lane);
+    const int cost = nst > 0 ? (nst + kSegCost) * HG : 0;
+    const int incl = wave_incl_scan(cost, lane);
     if (s < ns) {
-      seq_cum[s] = carry + incl - nst * HG;
+      seq_cum[s] = carry + incl - cost;
       seq_nst[s] = nst;
       seq_len[s] = len;
     }
@@ -307,6 +354,7 @@ qdecode_kernel(DecodeArgs a) {
   wave_lds_sync();
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) max_nst = max(max_nst, __shfl_xor(max_nst, o));
+  max_nst = __builtin_amdgcn_readfirstlane(max_nst);
   const int U = __builtin_amdgcn_readfirstlane(carry);
   if (w == 0) {  // empty sequences: zero output
     for (int s = 0; s < ns; s++) {
@@ -315,17 +363,17 @@ qdecode_kernel(DecodeArgs a) {
         a.out[s * a.o_ss + (idx / D) * a.o_sh + idx % D] = 0;
     }
   }
-  // units per wave: W ranges (<= kMaxRange units, by the host's choice of
-  // W), and at least max_nst / (kMaxParts - 1) so that no pair is split
-  // into more than kMaxParts partials
+  // cost units per wave: W ranges (<= kMaxRange units, by the host's
+  // choice of W), and at least max_nst / (kMaxParts - 1) so that no pair is
+  // split into more than kMaxParts partials
   const int cper = max((U + W - 1) / W, (max_nst + kMaxParts - 2) / (kMaxParts - 1));
   const int u0 = w * cper;
   if (u0 >= U) return;
   const int u1 = min(U, u0 + cper);
-  const int nunits = u1 - u0;
 
-  // ---- the range's segments: maximal runs of units in one (seq, pair)
-  int nseg = 0;
+  // ---- the range's segments: maximal runs of steps in one (seq, pair); the
+  // range's steps are its units 0 .. nunits - 1
+  int nseg = 0, nunits = 0;
   {
     // the last sequence whose prefix is <= u0: count them, 64 at a time
     int cnt = 0;
@@ -336,23 +384,29 @@ qdecode_kernel(DecodeArgs a) {
     int ss = cnt - 1, u = u0;
     while (u < u1) {
       while (seq_nst[ss] == 0) ss++;
-      const int nst = seq_nst[ss];
+      const int nst = seq_nst[ss], per = nst + kSegCost;
       const int local = u - seq_cum[ss];
-      const int j = local / nst, t = local % nst;
-      const int take = min(u1 - u, nst - t);
-      if (lane == 0) {
-        seg_tab[nseg][0] = ss;
-        seg_tab[nseg][1] = j;
-        seg_tab[nseg][2] = t;
-        seg_tab[nseg][3] = take;
-        seg_tab[nseg][4] = seq_len[ss];
-        seg_tab[nseg][5] = u - u0;
+      const int j = local / per, t = local % per - kSegCost;  // t < 0: lead-in
+      const int t0 = max(t, 0);
+      const int take = min(nst, t + (u1 - u)) - t0;
+      if (take > 0) {
+        if (lane == 0) {
+          seg_tab[nseg][0] = ss;
+          seg_tab[nseg][1] = j;
+          seg_tab[nseg][2] = t0;
+          seg_tab[nseg][3] = take;
+          seg_tab[nseg][4] = seq_len[ss];
+          seg_tab[nseg][5] = nunits;
+          seg_tab[nseg][6] = seq_cum[ss] + j * per + kSegCost;
+        }
+        nseg++;
+        nunits += take;
       }
-      nseg++;
-      u += take;
-      if (t + take == nst && j == HG - 1) ss++;
+      u += per - (t + kSegCost);  // on to the next pair
+      if (j == HG - 1) ss++;
     }
   }
+  if (nunits == 0) return;  // the range holds lead-in units only
   wave_lds_sync();
 
   // ---- block-table slice: the chunk of each sub-block of the range.  These
@@ -446,7 +500,7 @@ qdecode_kernel(DecodeArgs a) {
 
   // ---- segment state
   int k = 0;             // current segment
-  int seg_seq = 0, seg_j = 0, seg_t = 0, seg_take = 0, seg_len = 0, seg_first = 0, nh = 0;
+  int seg_seq = 0, seg_j = 0, seg_t = 0, seg_take = 0, seg_len = 0, seg_first = 0, seg_pa = 0, nh = 0;
   float sq[G];
   // query table of segment kk from its prefetched chunks: entry (slice sg,
   // column nn, unit slot ws) holds unit sg * SPW + ws of head nn % HP in the
@@ -458,6 +512,7 @@ qdecode_kernel(DecodeArgs a) {
     seg_take = __builtin_amdgcn_readfirstlane(seg_tab[kk][3]);
     seg_len = __builtin_amdgcn_readfirstlane(seg_tab[kk][4]);
     seg_first = __builtin_amdgcn_readfirstlane(seg_tab[kk][5]);
+    seg_pa = __builtin_amdgcn_readfirstlane(seg_tab[kk][6]);
     nh = min(HP, rep - (seg_j % n_hg) * HP);
     float part[QPL][G];
 #pragma unroll
@@ -506,6 +561,8 @@ qdecode_kernel(DecodeArgs a) {
     wave_lds_sync();
   };
   setup_segment(0, qpre);
+  // the next segment's queries load while this segment's units compute
+  load_q(min(1, nseg - 1), qpre);
 
   f32x4_t oacc[NT];
 #pragma unroll
@@ -701,7 +758,7 @@ qdecode_kernel(DecodeArgs a) {
     const bool whole = seg_t == 0 && seg_take == nst;
     // the pair's units start at unit pa; its partials take the slots of the
     // waves wa..wb that cover it
-    const int pa = u0 + seg_first - seg_t;
+    const int pa = seg_pa;
     const int wa = pa / cper, wb = (pa + nst - 1) / cper;
     const int64_t pair = static_cast<int64_t>(seg_seq) * HG + seg_j;
     if (seg_t + seg_take == nst && lane == 0)
@@ -739,40 +796,56 @@ qdecode_kernel(DecodeArgs a) {
     m_run = -INFINITY;
   };
 
-  // ---- the range: unit ui computes while unit ui + 1 (and the queries of
-  // its segment) load.  Prefetches are unconditional, clamped to the last
-  // unit: a conditional load makes the compiler merge the buffer registers
-  // at the join, which waits for the loads right after issuing them.
-  auto unit = [&](int ui, const Buf& cur, Buf& nxt) -> bool {
-    const int nx = min(ui + 1, nunits - 1);
-    const int knx = (k + 1 < nseg && nx >= __builtin_amdgcn_readfirstlane(seg_tab[k + 1][5])) ? k + 1 : k;
-    load_q(knx, qpre);
-    load_step(nx, nxt);
-    __builtin_amdgcn_sched_barrier(0);  // issue the loads before any compute
+  // ---- the range: unit ui computes while unit ui + 1 loads, and the next
+  // segment's queries load at the start of each segment.  Prefetches are
+  // unconditional, clamped to the last unit: a conditional load makes the
+  // compiler merge the buffer registers at the join, which waits for the
+  // loads right after issuing them.  The loop over unit pairs has its only
+  // exit at its end: an exit between the two halves gives the wait-count
+  // analysis a path on which the second half's loads were never issued, and
+  // it then waits for every load in flight before issuing the next ones.
+  auto unit = [&](int ui, const Buf& cur, Buf& nxt, auto prefetch) {
+    if constexpr (decltype(prefetch)::value) {
+      load_step(min(ui + 1, nunits - 1), nxt);
+      __builtin_amdgcn_sched_barrier(0);  // issue the loads before any compute
+    }
+    if constexpr (WPG > 1) {
+      if (partner >= 0) {
+        __hip_atomic_store(&done_of[wv], ui, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const int other = __builtin_amdgcn_readfirstlane(
+            __hip_atomic_load(&done_of[partner], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+        if (other > ui) __builtin_amdgcn_s_setprio(1);       // behind: issue first
+        else if (other < ui) __builtin_amdgcn_s_setprio(0);  // ahead: yield
+      }
+    }
     compute_step(seg_t + (ui - seg_first), cur);
     if (ui == seg_first + seg_take - 1) {  // last unit of the segment
       finalize();
-      if (ui + 1 == nunits) return false;
-      k++;
-      setup_segment(k, qpre);
+      if (k + 1 < nseg) {
+        k++;
+        setup_segment(k, qpre);
+        load_q(min(k + 1, nseg - 1), qpre);
+      }
     }
-    return ui + 1 < nunits;
   };
   if constexpr (C::kPrefetch) {
-    for (int ui = 0;; ui += 2) {
-      if (!unit(ui, bufA, bufB)) break;
-      if (!unit(ui + 1, bufB, bufA)) break;
+    // pairs of units, the loop's only exit at its end; an odd last unit
+    // follows on its own
+    int ui = 0;
+    for (; ui + 1 < nunits; ui += 2) {
+      unit(ui, bufA, bufB, std::true_type{});
+      unit(ui + 1, bufB, bufA, std::true_type{});
     }
+    if (ui < nunits) unit(ui, bufA, bufB, std::false_type{});
   } else {
     for (int ui = 0;; ui++) {
-      const int knx = (k + 1 < nseg && ui + 1 >= seg_tab[k + 1][5]) ? k + 1 : k;
-      load_q(knx, qpre);
       compute_step(seg_t + (ui - seg_first), bufA);
       if (ui == seg_first + seg_take - 1) {
         finalize();
         if (ui + 1 == nunits) break;
         k++;
         setup_segment(k, qpre);
+        load_q(min(k + 1, nseg - 1), qpre);
       }
       load_step(ui + 1, bufA);
     }
@@ -836,8 +909,9 @@ bool qdecode_supported(int dtype, int bits, int D, int block_size, int rep, int 
 }
 
 int qdecode_waves(int n_seqs, int Hkv, int rep, int max_len, int want) {
+  // cost units (steps + kSegCost per pair), at most
   const int64_t units = static_cast<int64_t>(n_seqs) * Hkv * qdecode_head_groups(rep) *
-                        ((static_cast<int64_t>(max_len) + 63) / 64);
+                        ((static_cast<int64_t>(max_len) + 63) / 64 + kSegCost);
   const int64_t need = (units + kMaxRange - 1) / kMaxRange;  // ranges of at most kMaxRange units
   // one round of resident waves (2 per SIMD x 4 SIMDs x 256 CUs)
   int64_t waves = want > 0 ? want : std::min<int64_t>(2048, (units + 3) / 4);
@@ -859,7 +933,8 @@ int qdecode_max_len() { return kMaxRange * (kMaxParts - 1) * 64; }
 
 template <int BITS, int D>
 static void launch_d(const DecodeArgs& a, hipStream_t st) {
-  const dim3 grid(a.n_waves), block(64);
+  constexpr int wpg = qd_waves<D>();
+  const dim3 grid((a.n_waves + wpg - 1) / wpg), block(64 * wpg);
   const int pairs = a.n_seqs * a.Hkv * qdecode_head_groups(a.rep);
   if (heads_per_part(a.rep) == 4) {
     hipLaunchKernelGGL((qdecode_kernel<BITS, D, 4>), grid, block, 0, st, a);
