@@ -51,12 +51,14 @@
 // qdecode_combine_kernel merges, as sdpa_vector_2pass_2 merges) and rebuilds
 // its wave-local query table.  The next unit's KV loads are in flight while
 // the current unit computes, and the next segment's queries while the
-// current segment does.  Up to 128 dims a workgroup is the 8 waves of one CU
-// (two per SIMD), and the two waves of a SIMD trade instruction-issue
-// priority so that neither finishes long before the other.  (Merging
-// partials in the last wave to finish would need device-scope
-// release/acquire fences, which on gfx950 write back and invalidate the
-// XCD's whole L2 and cost more than the extra launch.)
+// current segment does.  Up to 128 dims a workgroup is the 8 waves of one
+// CU (two per SIMD), and the two waves of a SIMD trade instruction-issue
+// priority so that neither finishes long before the other.  (Merging the
+// partials in the kernel, by the wave that counts a pair's last partial,
+// measured slower than the separate merge launch: with agent-coherent
+// stores the count must wait for every load in flight, and with
+// device-scope fences each partial writes back and invalidates the XCD's
+// L2.)
 #include <algorithm>
 #include <utility>
 
@@ -225,14 +227,37 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave.
+// Inclusive prefix sum over the 64 lanes of a wave: DPP row shifts within
+// each row of 16 lanes, then the totals of the rows before.
 __device__ __forceinline__ int wave_incl_scan(int x, int lane) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31);
+  const int r2 = __builtin_amdgcn_readlane(x, 47);
+  return x + (lane >= 16 ? r0 : 0) + (lane >= 32 ? r1 : 0) + (lane >= 48 ? r2 : 0);
+}
+
+// Maximum over the 64 lanes of a wave (a scalar).
+__device__ __forceinline__ int wave_max(int x) {
+  x = max(x, static_cast<int>(row_read<8>(static_cast<uint32_t>(x))));
+  x = max(x, static_cast<int>(row_read<4>(static_cast<uint32_t>(x))));
+  x = max(x, static_cast<int>(row_read<2>(static_cast<uint32_t>(x))));
+  x = max(x, static_cast<int>(row_read<1>(static_cast<uint32_t>(x))));
+  return max(max(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+             max(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+
+// Lane s % 64 of register s / 64 of a per-sequence table held in NR
+// registers (s uniform).
+template <int NR>
+__device__ __forceinline__ int seq_at(const int (&t)[NR], int s) {
+  int v = __builtin_amdgcn_readlane(t[0], s & 63);
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  return x;
+  for (int r = 1; r < NR; r++)
+    if ((s >> 6) == r) v = __builtin_amdgcn_readlane(t[r], s & 63);
+  return v;
 }
 
 template <int BITS, int D, int HP>
@@ -296,7 +321,6 @@ qdecode_kernel(DecodeArgs a) {
   // per segment: seq, pair, first step, steps, len, first unit of the range,
   // cost position of the pair's first step
   __shared__ int32_t seg_tab_g[WPG][kMaxRange][7];
-  __shared__ int32_t seq_len_g[WPG][kMaxSeqs];
   __shared__ int32_t simd_of[WPG];  // SIMD of each wave of the workgroup
   __shared__ int32_t done_of[WPG];  // units each wave has started
   const int wv = WPG > 1 ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6) : 0;
@@ -304,12 +328,21 @@ qdecode_kernel(DecodeArgs a) {
   int64_t* sub_off = sub_off_g[wv];
   int32_t* sub_t0 = sub_t0_g[wv];
   int32_t(*seg_tab)[7] = seg_tab_g[wv];
-  int32_t* seq_len = seq_len_g[wv];
-  int32_t* seq_cum = reinterpret_cast<int32_t*>(qtab);
-  int32_t* seq_nst = seq_cum + kMaxSeqs;
 
   const int lane = threadIdx.x & 63, n = lane & 15, lg = lane >> 4;
   const int w = blockIdx.x * WPG + wv, W = gridDim.x * WPG;
+  const int ns = a.n_seqs;
+
+  // ---- sequence lengths first (the set-up is a chain of dependent loads):
+  // lane l of register r holds sequence 64 r + l
+  constexpr int SR = kMaxSeqs / 64;
+  int len_r[SR];
+#pragma unroll
+  for (int r = 0; r < SR; r++) {
+    const int s = 64 * r + lane;
+    len_r[r] = 0;
+    if (64 * r < ns) len_r[r] = (s < ns) ? (a.seq_lens ? a.seq_lens[s] : a.max_len) : 0;
+  }
 
   // The wave that shares this wave's SIMD (-1: none).  Of two waves on a
   // SIMD the older one wins instruction issue, so left alone it finishes
@@ -321,13 +354,15 @@ qdecode_kernel(DecodeArgs a) {
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw_id));
     simd_of[wv] = (hw_id >> 4) & 3;  // HW_ID[5:4]: SIMD
     done_of[wv] = 0;
-    __syncthreads();
+    // LDS-only fences: the length loads stay in flight across the barrier
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     for (int o = 0; o < WPG; o++)
       if (o != wv && simd_of[o] == simd_of[wv]) partner = o;
     partner = __builtin_amdgcn_readfirstlane(partner);
   }
   const int rep = a.rep, n_hg = (rep + HP - 1) / HP, HG = a.Hkv * n_hg;
-  const int ns = a.n_seqs;
   const int subs = a.block_size >> 5;  // 32-token sub-blocks per pool block
   // this lane's roles: score column (part p, head h); key-operand lane
   // group (part pA, unit slot wA)
@@ -335,32 +370,36 @@ qdecode_kernel(DecodeArgs a) {
   const int pA = lg / SPW, wA = lg % SPW;
 
   // ---- cost per sequence ((steps + kSegCost) x head pairs) and its prefix
-  // sums; a pair's cost units are kSegCost lead-in units, then its steps
+  // sums, in registers like the lengths; a pair's cost units are kSegCost
+  // lead-in units, then its steps
+  int cum_r[SR], nst_r[SR];
   int carry = 0, max_nst = 0;
-  for (int s0 = 0; s0 < ns; s0 += 64) {
-    const int s = s0 + lane;
-    const int len = (s < ns) ? (a.seq_lens ? a.seq_lens[s] : a.max_len) : 0;
-    const int nst = (len + 63) >> 6;
-    const int cost = nst > 0 ? (nst + kSegCost) * HG : 0;
-    const int incl = wave_incl_scan(cost, lane);
-    if (s < ns) {
-      seq_cum[s] = carry + incl - cost;
-      seq_nst[s] = nst;
-      seq_len[s] = len;
-    }
-    carry += __shfl(incl, 63);
-    max_nst = max(max_nst, nst);
-  }
-  wave_lds_sync();
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) max_nst = max(max_nst, __shfl_xor(max_nst, o));
-  max_nst = __builtin_amdgcn_readfirstlane(max_nst);
+  for (int r = 0; r < SR; r++) {
+    cum_r[r] = 0;
+    nst_r[r] = 0;
+    if (64 * r < ns) {
+      const int nst = (len_r[r] + 63) >> 6;
+      const int cost = nst > 0 ? (nst + kSegCost) * HG : 0;
+      const int incl = wave_incl_scan(cost, lane);
+      cum_r[r] = carry + incl - cost;
+      nst_r[r] = nst;
+      carry += __builtin_amdgcn_readlane(incl, 63);
+      max_nst = max(max_nst, nst);
+    }
+  }
+  max_nst = wave_max(max_nst);
   const int U = __builtin_amdgcn_readfirstlane(carry);
   if (w == 0) {  // empty sequences: zero output
-    for (int s = 0; s < ns; s++) {
-      if (seq_nst[s] != 0) continue;
-      for (int idx = lane; idx < a.Hq * D; idx += 64)
-        a.out[s * a.o_ss + (idx / D) * a.o_sh + idx % D] = 0;
+#pragma unroll
+    for (int r = 0; r < SR; r++) {
+      uint64_t empty = __builtin_amdgcn_ballot_w64(64 * r + lane < ns && nst_r[r] == 0);
+      while (empty) {
+        const int s = 64 * r + __builtin_ctzll(empty);
+        empty &= empty - 1;
+        for (int idx = lane; idx < a.Hq * D; idx += 64)
+          a.out[s * a.o_ss + (idx / D) * a.o_sh + idx % D] = 0;
+      }
     }
   }
   // cost units per wave: W ranges (<= kMaxRange units, by the host's
@@ -372,20 +411,24 @@ qdecode_kernel(DecodeArgs a) {
   const int u1 = min(U, u0 + cper);
 
   // ---- the range's segments: maximal runs of steps in one (seq, pair); the
-  // range's steps are its units 0 .. nunits - 1
+  // range's steps are its units 0 .. nunits - 1.  The walk runs on scalars;
+  // lane e of the block-table slice (below) picks the segment of its unit
+  // e / 2 on the way (units past the range map to the range's last unit).
   int nseg = 0, nunits = 0;
+  int sel_seq[2] = {0, 0}, sel_j[2] = {0, 0}, sel_step[2] = {0, 0}, sel_len[2] = {1, 1};
+  int seq0 = 0, j0 = 0;  // the first segment's (sequence, pair)
   {
-    // the last sequence whose prefix is <= u0: count them, 64 at a time
+    // the last sequence whose prefix is <= u0
     int cnt = 0;
-    for (int s0 = 0; s0 < ns; s0 += 64) {
-      const int s = s0 + lane;
-      cnt += __popcll(__builtin_amdgcn_ballot_w64(s < ns && seq_cum[s] <= u0));
-    }
-    int ss = cnt - 1, u = u0;
+#pragma unroll
+    for (int r = 0; r < SR; r++)
+      cnt += __popcll(__builtin_amdgcn_ballot_w64(64 * r + lane < ns && cum_r[r] <= u0));
+    int ss = max(cnt - 1, 0), u = u0;
     while (u < u1) {
-      while (seq_nst[ss] == 0) ss++;
-      const int nst = seq_nst[ss], per = nst + kSegCost;
-      const int local = u - seq_cum[ss];
+      while (ss < ns - 1 && seq_at(nst_r, ss) == 0) ss++;
+      const int nst = max(seq_at(nst_r, ss), 1), per = nst + kSegCost;
+      const int cum = seq_at(cum_r, ss), len = seq_at(len_r, ss);
+      const int local = u - cum;
       const int j = local / per, t = local % per - kSegCost;  // t < 0: lead-in
       const int t0 = max(t, 0);
       const int take = min(nst, t + (u1 - u)) - t0;
@@ -395,9 +438,22 @@ qdecode_kernel(DecodeArgs a) {
           seg_tab[nseg][1] = j;
           seg_tab[nseg][2] = t0;
           seg_tab[nseg][3] = take;
-          seg_tab[nseg][4] = seq_len[ss];
+          seg_tab[nseg][4] = len;
           seg_tab[nseg][5] = nunits;
-          seg_tab[nseg][6] = seq_cum[ss] + j * per + kSegCost;
+          seg_tab[nseg][6] = cum + j * per + kSegCost;
+        }
+        if (nseg == 0) {
+          seq0 = ss;
+          j0 = j;
+        }
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+          const int ui = (lane + 64 * r) >> 1;
+          const bool sel = ui >= nunits;
+          sel_seq[r] = sel ? ss : sel_seq[r];
+          sel_j[r] = sel ? j : sel_j[r];
+          sel_step[r] = sel ? t0 + min(ui - nunits, take - 1) : sel_step[r];
+          sel_len[r] = sel ? len : sel_len[r];
         }
         nseg++;
         nunits += take;
@@ -407,7 +463,6 @@ qdecode_kernel(DecodeArgs a) {
     }
   }
   if (nunits == 0) return;  // the range holds lead-in units only
-  wave_lds_sync();
 
   // ---- block-table slice: the chunk of each sub-block of the range.  These
   // loads, then the first segment's queries, are issued before any KV load
@@ -417,21 +472,18 @@ qdecode_kernel(DecodeArgs a) {
   int32_t my_t0[2];
 #pragma unroll
   for (int r = 0; r < 2; r++) {
-    const int e = lane + 64 * r, ui = min(e >> 1, nunits - 1);
-    int k = 0;
-    for (int kk = 1; kk < nseg; kk++)
-      if (seg_tab[kk][5] <= ui) k = kk;
-    const int seq = seg_tab[k][0], j = seg_tab[k][1];
-    const int step = seg_tab[k][2] + (ui - seg_tab[k][5]);
-    const int nsub = (seg_tab[k][4] + 31) >> 5;
-    const int sbi = min(2 * step + (e & 1), nsub - 1);
-    const int64_t blk = a.table[static_cast<int64_t>(seq) * a.table_stride + sbi / subs];
-    my_off[r] = blk * a.block_bytes + static_cast<int64_t>(j / n_hg) * a.head_bytes;
+    const int e = lane + 64 * r;
+    const int nsub = (sel_len[r] + 31) >> 5;
+    const int sbi = max(min(2 * sel_step[r] + (e & 1), nsub - 1), 0);
+    const int64_t blk = a.table[static_cast<int64_t>(sel_seq[r]) * a.table_stride + sbi / subs];
+    my_off[r] = blk * a.block_bytes + static_cast<int64_t>(sel_j[r] / n_hg) * a.head_bytes;
     my_t0[r] = (sbi % subs) * 32;
   }
-  // queries of segment k's head group: 8 dims (16 bytes) per chunk
-  auto load_q = [&](int k, u32x4_t* qr) {
-    const int seq = seg_tab[k][0], j = seg_tab[k][1];
+  // (The lambdas below are forced inline: called from several places, the
+  // compiler would otherwise outline them as functions.)
+  // queries of the head group of pair j of sequence seq: 8 dims (16 bytes)
+  // per chunk
+  auto load_q_sj = [&](int seq, int j, u32x4_t* qr) __attribute__((always_inline)) {
     const int64_t hq0 = static_cast<int64_t>(j / n_hg) * rep + (j % n_hg) * HP;
     const int nh = min(HP, rep - (j % n_hg) * HP);
 #pragma unroll
@@ -440,8 +492,12 @@ qdecode_kernel(DecodeArgs a) {
       qr[c] = *(g_u32x4_t*)(a.q + seq * a.q_ss + (hq0 + r) * a.q_sh + 8 * (ci % (D / 8)));
     }
   };
+  // ... of segment k
+  auto load_q = [&](int k, u32x4_t* qr) __attribute__((always_inline)) {
+    load_q_sj(__builtin_amdgcn_readfirstlane(seg_tab[k][0]), __builtin_amdgcn_readfirstlane(seg_tab[k][1]), qr);
+  };
   u32x4_t qpre[QPL];
-  load_q(0, qpre);
+  load_q_sj(seq0, j0, qpre);
 #pragma unroll
   for (int r = 0; r < 2; r++) {
     const int e = lane + 64 * r;
@@ -469,7 +525,7 @@ qdecode_kernel(DecodeArgs a) {
     sb_lane[tau] = a.sb_off + (8 * lg + tok_off<BITS>(c2 & 1, 0)) * SBW * 4;
   }
   const int32_t v_lane = a.vc_off + (lg * 16 + n) * VW * 4;
-  auto load_step = [&](int ui, Buf& b) {
+  auto load_step = [&](int ui, Buf& b) __attribute__((always_inline)) {
     const uint8_t* bc[2];  // codes base of each sub-block
     const uint8_t* bs[2];  // scale/bias base
 #pragma unroll
@@ -505,7 +561,7 @@ qdecode_kernel(DecodeArgs a) {
   // query table of segment kk from its prefetched chunks: entry (slice sg,
   // column nn, unit slot ws) holds unit sg * SPW + ws of head nn % HP in the
   // key operand's K order; sq = each head's bf16 query sum per group
-  auto setup_segment = [&](int kk, const u32x4_t* qr) {
+  auto setup_segment = [&](int kk, const u32x4_t* qr) __attribute__((always_inline)) {
     seg_seq = __builtin_amdgcn_readfirstlane(seg_tab[kk][0]);
     seg_j = __builtin_amdgcn_readfirstlane(seg_tab[kk][1]);
     seg_t = __builtin_amdgcn_readfirstlane(seg_tab[kk][2]);
@@ -572,7 +628,7 @@ qdecode_kernel(DecodeArgs a) {
   for (int g = 0; g < G; g++) corr[g] = 0.0f;
   const u32x4_t* qlane = qtab + ((pA == p) ? n * SPW + wA : 16 * SPW);
 
-  auto compute_step = [&](int stp, const Buf& b) {
+  auto compute_step = [&](int stp, const Buf& b) __attribute__((always_inline)) {
     const int len = seg_len;
     // ---- scores: acc[tau][g] = q . (MAG + c) over group g's dims
     f32x4_t acc[TT][G];
@@ -735,7 +791,7 @@ qdecode_kernel(DecodeArgs a) {
   };
 
   // ---- end of a segment: the output itself, or this wave's partial
-  auto finalize = [&]() {
+  auto finalize = [&]() __attribute__((always_inline)) {
     float lsum = l_run, csum[G];
 #pragma unroll
     for (int g = 0; g < G; g++) csum[g] = corr[g];
@@ -804,7 +860,7 @@ qdecode_kernel(DecodeArgs a) {
   // exit at its end: an exit between the two halves gives the wait-count
   // analysis a path on which the second half's loads were never issued, and
   // it then waits for every load in flight before issuing the next ones.
-  auto unit = [&](int ui, const Buf& cur, Buf& nxt, auto prefetch) {
+  auto unit = [&](int ui, const Buf& cur, Buf& nxt, auto prefetch) __attribute__((always_inline)) {
     if constexpr (decltype(prefetch)::value) {
       load_step(min(ui + 1, nunits - 1), nxt);
       __builtin_amdgcn_sched_barrier(0);  // issue the loads before any compute
