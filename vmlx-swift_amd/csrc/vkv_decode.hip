@@ -909,50 +909,77 @@ qdecode_kernel(DecodeArgs a) {
 }
 
 // Merge of the partials of (sequence, head pair)s that several waves
-// share (sdpa_vector.h:320-394).  Block = one (sequence, pair), thread =
-// one (head, dim).
+// share (sdpa_vector.h:320-394).  Block = one (sequence, pair), thread = 4
+// dims of one head.  The pair's partial count, its length and its first
+// kFirst partials load together (the partial slots past the count hold
+// stale data, which the merge masks), so a pair of up to kFirst partials
+// costs one round trip to memory.
 template <int HP>
-__global__ void __launch_bounds__(1024) qdecode_combine_kernel(DecodeArgs a, int D) {
+__global__ void __launch_bounds__(512) qdecode_combine_kernel(DecodeArgs a, int D) {
+  constexpr int kFirst = 4;
   const int rep = a.rep, n_hg = (rep + HP - 1) / HP, HG = a.Hkv * n_hg;
   const int P = blockIdx.x, seq = P / HG, j = P % HG;
   const int len = a.seq_lens ? a.seq_lens[seq] : a.max_len;
   const int K = reinterpret_cast<const int32_t*>(a.ws_ml + a.ws_hdr)[P];
-  if (len == 0 || K <= 1) return;  // written by the decode kernel itself
   const int64_t hq0 = static_cast<int64_t>(j / n_hg) * rep + (j % n_hg) * HP;
   const int nh = min(HP, rep - (j % n_hg) * HP);
   const int64_t slot0 = static_cast<int64_t>(P) * kMaxParts;
-  for (int idx = threadIdx.x; idx < nh * D; idx += blockDim.x) {
-    const int r = idx / D, d = idx % D;
-    // eight partials per round; the loads are unconditional (clamped to the
-    // last partial) because a conditional load waits for every load before it
-    float M = -INFINITY, L = 0.0f, o = 0.0f;
-    for (int k0 = 0; k0 < K; k0 += 8) {
-      float mm[8], ll[8], oo[8];
+  const int r = threadIdx.x / (D / 4), d = 4 * (threadIdx.x % (D / 4));
+  if (r >= HP) return;
+  float M = -INFINITY, L = 0.0f;
+  f32x4_t o = {0.f, 0.f, 0.f, 0.f};
+  auto merge = [&](int k0, int cnt, const f32x2_t* ml, const f32x4_t* oo) __attribute__((always_inline)) {
+    float mm[kFirst];
+    float Mn = M;
 #pragma unroll
-      for (int q = 0; q < 8; q++) {
-        const int64_t slot = (slot0 + min(k0 + q, K - 1)) * HP + r;
-        mm[q] = a.ws_ml[slot * 2];
-        ll[q] = a.ws_ml[slot * 2 + 1];
-        oo[q] = a.ws_o[slot * D + d];
-      }
-#pragma unroll
-      for (int q = 0; q < 8; q++) mm[q] = k0 + q < K ? mm[q] : -INFINITY;
-      float Mn = M;
-#pragma unroll
-      for (int q = 0; q < 8; q++) Mn = fmaxf(Mn, mm[q]);
-      const float f = M == -INFINITY ? 0.0f : exp2f((M - Mn) * kLog2e);
-      L *= f;
-      o *= f;
-#pragma unroll
-      for (int q = 0; q < 8; q++) {
-        const float e = mm[q] == -INFINITY ? 0.0f : exp2f((mm[q] - Mn) * kLog2e);
-        L = fmaf(e, ll[q], L);
-        o = fmaf(e, oo[q], o);
-      }
-      M = Mn;
+    for (int q = 0; q < kFirst; q++) {
+      mm[q] = (q < cnt && k0 + q < K) ? ml[q][0] : -INFINITY;
+      Mn = fmaxf(Mn, mm[q]);
     }
-    a.out[seq * a.o_ss + (hq0 + r) * a.o_sh + d] = f32_to_bf16(L > 0.0f ? o / L : 0.0f);
+    const float f = M == -INFINITY ? 0.0f : exp2f((M - Mn) * kLog2e);
+    L *= f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[e] *= f;
+#pragma unroll
+    for (int q = 0; q < kFirst; q++) {
+      // stale slots: weight 0, and their (possibly non-finite) values are
+      // selected away rather than multiplied by it
+      const bool live = mm[q] != -INFINITY;
+      const float w = live ? exp2f((mm[q] - Mn) * kLog2e) : 0.0f;
+      L = fmaf(w, live ? ml[q][1] : 0.0f, L);
+#pragma unroll
+      for (int e = 0; e < 4; e++) o[e] = fmaf(w, live ? oo[q][e] : 0.0f, o[e]);
+    }
+    M = Mn;
+  };
+  {
+    f32x2_t ml[kFirst];
+    f32x4_t oo[kFirst];
+#pragma unroll
+    for (int q = 0; q < kFirst; q++) {
+      const int64_t slot = (slot0 + q) * HP + r;
+      ml[q] = *reinterpret_cast<const f32x2_t*>(a.ws_ml + slot * 2);
+      oo[q] = *reinterpret_cast<const f32x4_t*>(a.ws_o + slot * D + d);
+    }
+    if (len == 0 || K <= 1 || r >= nh) return;  // written by the decode kernel itself
+    merge(0, kFirst, ml, oo);
   }
+  for (int k0 = kFirst; k0 < K; k0 += kFirst) {
+    f32x2_t ml[kFirst];
+    f32x4_t oo[kFirst];
+#pragma unroll
+    for (int q = 0; q < kFirst; q++) {
+      const int64_t slot = (slot0 + min(k0 + q, K - 1)) * HP + r;
+      ml[q] = *reinterpret_cast<const f32x2_t*>(a.ws_ml + slot * 2);
+      oo[q] = *reinterpret_cast<const f32x4_t*>(a.ws_o + slot * D + d);
+    }
+    merge(k0, kFirst, ml, oo);
+  }
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  u32x2_t v;
+  v[0] = f32_to_bf16(o[0] * inv) | (uint32_t(f32_to_bf16(o[1] * inv)) << 16);
+  v[1] = f32_to_bf16(o[2] * inv) | (uint32_t(f32_to_bf16(o[3] * inv)) << 16);
+  *reinterpret_cast<u32x2_t*>(a.out + seq * a.o_ss + (hq0 + r) * a.o_sh + d) = v;
 }
 
 static int heads_per_part(int rep) { return rep <= 4 ? 4 : 8; }
@@ -995,11 +1022,11 @@ static void launch_d(const DecodeArgs& a, hipStream_t st) {
   if (heads_per_part(a.rep) == 4) {
     hipLaunchKernelGGL((qdecode_kernel<BITS, D, 4>), grid, block, 0, st, a);
     VKV_HIP(hipGetLastError());
-    hipLaunchKernelGGL(qdecode_combine_kernel<4>, dim3(pairs), dim3(4 * D), 0, st, a, D);
+    hipLaunchKernelGGL(qdecode_combine_kernel<4>, dim3(pairs), dim3(D), 0, st, a, D);
   } else {
     hipLaunchKernelGGL((qdecode_kernel<BITS, D, 8>), grid, block, 0, st, a);
     VKV_HIP(hipGetLastError());
-    hipLaunchKernelGGL(qdecode_combine_kernel<8>, dim3(pairs), dim3(std::min(1024, 8 * D)), 0, st, a, D);
+    hipLaunchKernelGGL(qdecode_combine_kernel<8>, dim3(pairs), dim3(2 * D), 0, st, a, D);
   }
   VKV_HIP(hipGetLastError());
 }
