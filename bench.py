@@ -12,10 +12,11 @@ HBM before timing starts.  The step writes the decode token at the same
 position each step, so every step does identical work.
 
 Prints one JSON line: "value" is the whole-step KV-read rate (appends included),
-"attention" and "roofline" time the paged decode call alone, "traffic" is the
-PMC-measured HBM bytes per decode launch, "cpu_baseline" times the C oracle,
-and "mla" is the MLA latent decode workload (32 x 16384 tokens, 128 heads) with
-its MFMA roofline.
+"attention" times the paged decode call (decode kernel + split-K merge),
+"roofline" the decode kernel alone (the library's event pair around it, on
+its launch stream), "traffic" is the PMC-measured HBM bytes per decode launch,
+"cpu_baseline" times the C oracle, and "mla" is the MLA latent decode workload
+(32 x 16384 tokens, 128 heads) with the MFMA roofline of its attention kernel.
 """
 import argparse
 import json
@@ -195,9 +196,18 @@ def mla_measure(torch, vkv, steps, warmup):
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
+    # the attention kernel alone (without the split merge), from the
+    # library's event pair around it, over the same number of calls
+    vkv.kernel_timing(True)
+    for _ in range(steps):
+        call()
+    k_ms, k_n = vkv.kernel_timing_read(vkv.TIME_MLA)
+    vkv.kernel_timing(False)
+    k_ms /= max(k_n, 1)
     kv_bytes = B * T * (DK + (DK // 64) * 4)          # 612 B per entry
     flops = 2.0 * H * B * T * (DK + DV)
     tflops = flops / (ms * 1e-3) / 1e12
+    k_tflops = flops / (k_ms * 1e-3) / 1e12
     del pool
     return {
         "workload": "MLA absorbed decode: 32 seqs x 16384 tokens, 576-dim latent+rope entries "
@@ -205,8 +215,10 @@ def mla_measure(torch, vkv, steps, warmup):
         "ms_per_step": round(ms, 4),
         "kv_gbs": round(kv_bytes / (ms * 1e-3) / 1e9, 1),
         "tflops": round(tflops, 1),
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "kernel_ms": round(k_ms, 5),
+        "roofline": {"bound": "mfma", "achieved": round(k_tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(k_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "kernel": "mla_kernel"},
         "finite": bool(torch.isfinite(out.float()).all()),
     }
 
@@ -301,6 +313,8 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = t0.elapsed_time(t1) / args.steps
     # per-kernel timing inside the same kind of steps
+    # and the decode kernel alone (the attention call less its split-K
+    # merge), from the library's event pair around that kernel
     app_ms = att_ms = 0.0
     for _ in range(args.steps):
         ev = [[torch.cuda.Event(enable_timing=True) for _ in range(layers)] for _ in range(3)]
@@ -309,15 +323,22 @@ def main():
         for l in range(layers):
             app_ms += ev[0][l].elapsed_time(ev[1][l])
             att_ms += ev[1][l].elapsed_time(ev[2][l])
+    vkv.kernel_timing(True)   # a pass of its own: the extra events add gaps
+    for _ in range(args.steps):
+        step()
+    dec_ms, dec_n = vkv.kernel_timing_read(vkv.TIME_DECODE)
+    vkv.kernel_timing(False)
     n_att = args.steps * layers
     att_avg_ms = att_ms / n_att
     app_avg_ms = app_ms / n_att
+    dec_avg_ms = dec_ms / max(dec_n, 1)
 
     lens = sc["lens"] + 1
     logical = int(lens.sum()) * sc["H"] * BYTES_PER_TOKEN_HEAD
     unique = logical - (len(sc["sharers"]) - 1) * sc["share_tokens"] * sc["H"] * BYTES_PER_TOKEN_HEAD
     gbs_step = logical * layers / (ms_per_step * 1e-3) / 1e9
     att_gbs = logical / (att_avg_ms * 1e-3) / 1e9
+    dec_gbs = logical / (dec_avg_ms * 1e-3) / 1e9
     append_tokens = sc["n_seqs"] + sc["prefill"]
     mla = None if args.no_mla else mla_measure(torch, vkv, args.steps, args.warmup)
     cpu = None
@@ -346,13 +367,14 @@ def main():
         },
         "attention": {"ms_per_layer": round(att_avg_ms, 5), "gbs_logical": round(att_gbs, 1),
                       "gbs_unique": round(unique / (att_avg_ms * 1e-3) / 1e9, 1),
-                      "pct_hbm_peak": round(100 * att_gbs / HBM_PEAK_GBS, 2)},
+                      "pct_hbm_peak": round(100 * att_gbs / HBM_PEAK_GBS, 2),
+                      "decode_kernel_ms": round(dec_avg_ms, 5)},
         "append": {"tokens_per_layer_step": append_tokens,
                    "ms_per_layer": round(app_avg_ms, 5),
                    "tokens_per_s": round(append_tokens / (app_avg_ms * 1e-3), 1)},
-        "roofline": {"bound": "hbm", "achieved": round(att_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(att_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": pmc_traffic()},
+        "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": pmc_traffic(), "kernel": "qdecode_kernel"},
         "cpu_baseline": cpu,
         "mla": mla,
     }

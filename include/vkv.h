@@ -370,6 +370,19 @@ int vkv_block_hash(const char *parent_hash, const int64_t *tokens, int64_t n_tok
  * the reference's `x * 1` owned copy (KVCache.swift:100-102). */
 int vkv_array_copy(const vkv_array *src, vkv_array *dst, void *stream);
 
+/* ------------------------------------------------------- kernel timing */
+
+/* Kernel timing, a measurement aid with no counterpart in the reference:
+ * while enabled, the paged decode attention launcher (kind 0: its matrix-core
+ * decode kernel, without the split-K merge) and the MLA launcher (kind 1: its
+ * attention kernel) launch that kernel with a start/stop HIP event pair
+ * (hipExtLaunchKernel), recorded at the kernel's own start and end.  vkv_kernel_timing_read waits for the launches of a kind
+ * recorded so far and returns their total milliseconds and count, then
+ * forgets them. */
+enum { VKV_TIME_DECODE = 0, VKV_TIME_MLA = 1 };
+int vkv_kernel_timing(int32_t enable);
+int vkv_kernel_timing_read(int32_t kind, double *total_ms, int32_t *count);
+
 /* ------------------------------------------------------------ synthetic */
 
 /* Fill a contiguous f16/bf16/f32 device buffer with counter-based normal

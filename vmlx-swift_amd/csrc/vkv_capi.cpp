@@ -900,6 +900,23 @@ int vkv_array_copy(const vkv_array* src, vkv_array* dst, void* stream) {
   });
 }
 
+// ----------------------------------------------------------- kernel timing
+
+int vkv_kernel_timing(int32_t enable) {
+  return guard([&] { timing_enable(enable != 0); });
+}
+
+int vkv_kernel_timing_read(int32_t kind, double* total_ms, int32_t* count) {
+  return guard([&] {
+    need(total_ms, "total_ms");
+    need(count, "count");
+    if (kind < 0 || kind >= kTimeKinds) throw Error("unknown timing kind");
+    int c = 0;
+    timing_read(kind, total_ms, &c);
+    *count = c;
+  });
+}
+
 // --------------------------------------------------------------- synthetic
 
 int vkv_fill_normal(void* data, int32_t dtype, int64_t n, uint64_t seed, float std, void* stream) {

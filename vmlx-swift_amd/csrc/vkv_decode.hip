@@ -63,6 +63,8 @@
 #include <utility>
 
 #include "vkv_device.h"
+#include <hip/hip_ext.h>
+
 #include "vkv_internal.h"
 
 namespace vkv {
@@ -1019,13 +1021,16 @@ static void launch_d(const DecodeArgs& a, hipStream_t st) {
   constexpr int wpg = qd_waves<D>();
   const dim3 grid((a.n_waves + wpg - 1) / wpg), block(64 * wpg);
   const int pairs = a.n_seqs * a.Hkv * qdecode_head_groups(a.rep);
+  const TimedLaunch tl = timing_prepare(kTimeDecode);
   if (heads_per_part(a.rep) == 4) {
-    hipLaunchKernelGGL((qdecode_kernel<BITS, D, 4>), grid, block, 0, st, a);
+    hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, 4>), grid, block, 0, st, tl.start, tl.stop, 0, a);
     VKV_HIP(hipGetLastError());
+    timing_commit(tl);
     hipLaunchKernelGGL(qdecode_combine_kernel<4>, dim3(pairs), dim3(D), 0, st, a, D);
   } else {
-    hipLaunchKernelGGL((qdecode_kernel<BITS, D, 8>), grid, block, 0, st, a);
+    hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, 8>), grid, block, 0, st, tl.start, tl.stop, 0, a);
     VKV_HIP(hipGetLastError());
+    timing_commit(tl);
     hipLaunchKernelGGL(qdecode_combine_kernel<8>, dim3(pairs), dim3(2 * D), 0, st, a, D);
   }
   VKV_HIP(hipGetLastError());

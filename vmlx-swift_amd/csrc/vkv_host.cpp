@@ -1229,6 +1229,73 @@ vkv_prefix_stats PrefixManager::stats() {
   return stats_;
 }
 
+// ------------------------------------------------------------ kernel timing
+
+namespace {
+struct Timing {
+  std::mutex mu;
+  bool on = false;
+  std::vector<hipEvent_t> pool;                      // idle events
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> rec[kTimeKinds];
+  hipEvent_t take() {
+    if (pool.empty()) {
+      hipEvent_t e;
+      VKV_HIP(hipEventCreate(&e));
+      return e;
+    }
+    hipEvent_t e = pool.back();
+    pool.pop_back();
+    return e;
+  }
+};
+Timing& timing() {
+  static Timing* t = new Timing();
+  return *t;
+}
+}  // namespace
+
+void timing_enable(bool on) {
+  Timing& t = timing();
+  std::lock_guard<std::mutex> g(t.mu);
+  t.on = on;
+}
+
+TimedLaunch timing_prepare(int kind) {
+  Timing& t = timing();
+  std::lock_guard<std::mutex> g(t.mu);
+  TimedLaunch r;
+  r.kind = kind;
+  if (t.on) {
+    r.start = t.take();
+    r.stop = t.take();
+  }
+  return r;
+}
+
+void timing_commit(const TimedLaunch& r) {
+  if (!r.start) return;
+  Timing& t = timing();
+  std::lock_guard<std::mutex> g(t.mu);
+  t.rec[r.kind].emplace_back(r.start, r.stop);
+}
+
+void timing_read(int kind, double* total_ms, int* count) {
+  Timing& t = timing();
+  std::lock_guard<std::mutex> g(t.mu);
+  double sum = 0.0;
+  for (auto& pr : t.rec[kind]) {
+    VKV_HIP(hipEventSynchronize(pr.second));
+    float ms = 0.0f;
+    VKV_HIP(hipEventElapsedTime(&ms, pr.first, pr.second));
+    sum += ms;
+    t.pool.push_back(pr.first);
+    t.pool.push_back(pr.second);
+  }
+  *total_ms = sum;
+  *count = static_cast<int>(t.rec[kind].size());
+  t.rec[kind].clear();
+}
+
 // ------------------------------------------------------------ workspace
 
 float* attention_workspace(hipStream_t st, size_t floats) {

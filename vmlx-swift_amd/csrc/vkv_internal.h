@@ -193,6 +193,21 @@ bool mla_supported(int dtype, int bits, int group, int head_dim, int v_head_dim,
 size_t mla_plan(MlaArgs& a, int want);
 void launch_mla(const MlaArgs& a, hipStream_t st);
 
+// Kernel timing (a measurement aid): while enabled, launchers start their
+// main kernel with hipExtLaunchKernelGGL and a start/stop event pair, which
+// the runtime records at the kernel's own start and end.
+enum { kTimeDecode = 0, kTimeMla = 1, kTimeKinds = 2 };
+struct TimedLaunch {
+  int kind = 0;
+  hipEvent_t start = nullptr, stop = nullptr;  // null when timing is off
+};
+TimedLaunch timing_prepare(int kind);
+void timing_commit(const TimedLaunch& t);  // after the launch
+void timing_enable(bool on);
+// Waits for the recorded launches of a kind; total milliseconds and count,
+// then forgets them.
+void timing_read(int kind, double* total_ms, int* count);
+
 // Block pairs passed by value to the block-copy kernel.
 struct BlockPairs {
   static constexpr int kMax = 256;

@@ -52,6 +52,8 @@
 #include <utility>
 
 #include "vkv_device.h"
+#include <hip/hip_ext.h>
+
 #include "vkv_internal.h"
 
 // Scale/bias row of zeros, read in place of the rows of tokens past the end.
@@ -559,11 +561,13 @@ void launch_mla(const MlaArgs& a0, hipStream_t st) {
     a.ws_ml = reinterpret_cast<float*>(a.ws_o + static_cast<size_t>(a.n_seqs) * a.n_splits * a.H * kDV);
   const int hb = a.H > 64 ? 2 : 1;
   const dim3 grid(a.n_splits, a.n_seqs, (a.H + 64 * hb - 1) / (64 * hb));
+  const TimedLaunch tl = timing_prepare(kTimeMla);
   if (hb == 2)
-    hipLaunchKernelGGL(mla_kernel<2>, grid, dim3(256), 0, st, a);
+    hipExtLaunchKernelGGL(mla_kernel<2>, grid, dim3(256), 0, st, tl.start, tl.stop, 0, a);
   else
-    hipLaunchKernelGGL(mla_kernel<1>, grid, dim3(256), 0, st, a);
+    hipExtLaunchKernelGGL(mla_kernel<1>, grid, dim3(256), 0, st, tl.start, tl.stop, 0, a);
   VKV_HIP(hipGetLastError());
+  timing_commit(tl);
   if (a.n_splits > 1) {
     hipLaunchKernelGGL(mla_combine_kernel, dim3(a.H, a.n_seqs), dim3(128), 0, st, a);
     VKV_HIP(hipGetLastError());

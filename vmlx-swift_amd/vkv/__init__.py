@@ -78,8 +78,9 @@ EXPORTS = (
     "vkv_prefix_free", "vkv_prefix_release", "vkv_prefix_incref", "vkv_prefix_ref_count", "vkv_prefix_find",
     "vkv_prefix_register", "vkv_prefix_clear", "vkv_prefix_store", "vkv_prefix_fetch",
     "vkv_prefix_stats_get", "vkv_prefix_block_tokens", "vkv_block_hash", "vkv_array_copy",
-    "vkv_fill_normal",
+    "vkv_kernel_timing", "vkv_kernel_timing_read", "vkv_fill_normal",
 )
+TIME_DECODE, TIME_MLA = 0, 1
 
 _lib = None
 
@@ -239,6 +240,21 @@ def mla_decode(queries, view: PagedView, scale: float, stream=None):
     _chk(lib().vkv_mla_decode(C.byref(arr(queries)), C.byref(view), C.c_float(scale),
                               C.byref(a_out), stream_ptr(stream)))
     return out
+
+
+def kernel_timing(enable: bool):
+    """Start (True) or stop recording event pairs around the decode and MLA
+    kernels (a measurement aid; see vkv_kernel_timing)."""
+    _chk(lib().vkv_kernel_timing(C.c_int32(1 if enable else 0)))
+
+
+def kernel_timing_read(kind: int):
+    """(total milliseconds, launches) recorded for kind TIME_DECODE or
+    TIME_MLA since the last read; waits for those launches."""
+    ms = C.c_double()
+    n = C.c_int32()
+    _chk(lib().vkv_kernel_timing_read(C.c_int32(kind), C.byref(ms), C.byref(n)))
+    return ms.value, n.value
 
 
 def fill_normal(t, seed: int, std: float = 1.0, stream=None):
