@@ -184,13 +184,23 @@ int vkv_mla_decode(const vkv_array *q, const vkv_paged_view *kv, float scale,
 enum {
   VKV_CACHE_SIMPLE = 0,    /* KVCacheSimple    KVCache.swift:452-596 */
   VKV_CACHE_ROTATING = 1,  /* RotatingKVCache  KVCache.swift:605-958 */
-  VKV_CACHE_QUANTIZED = 2  /* QuantizedKVCache KVCache.swift:961-1221 */
+  VKV_CACHE_QUANTIZED = 2, /* QuantizedKVCache KVCache.swift:961-1221 */
+  /* CompilableKVCache (CompilableKVCache.swift:40-262): fixed [B,H,max,D]
+   * buffers, max = params.max_size (default 4096), write offset in device
+   * memory; update returns the whole buffers and makeMask always an array
+   * mask [n, max] built on the device. */
+  VKV_CACHE_COMPILABLE = 3,
+  /* CompilableRotatingKVCache (BatchEngine/CompilableRotatingKVCache.swift:
+   * 1-265): a RotatingKVCache whose buffers are allocated at maxSize once and
+   * whose ring index and offset live in device memory. */
+  VKV_CACHE_COMPILABLE_ROTATING = 4
 };
 
 typedef struct vkv_cache_params {
   int32_t kind;
   int32_t step;        /* growth step, default 256 (KVCache.swift:455, :966) */
-  int32_t max_size;    /* rotating window (RotatingKVCache.init maxSize) */
+  int32_t max_size;    /* rotating window (RotatingKVCache.init maxSize);
+                          CompilableKVCache maxLength (default 4096) */
   int32_t keep;        /* rotating keep prefix */
   int32_t group_size;  /* quantized: 64 */
   int32_t bits;        /* quantized: 4 or 8 (default 8, KVCache.swift:970) */
@@ -223,6 +233,9 @@ int vkv_cache_update_quantized(vkv_cache cache, const vkv_array *keys,
 
 /* offset / maxSize / isTrimmable / trim(n) (KVCache.swift:38-77). */
 int vkv_cache_offset(vkv_cache cache, int64_t *offset);
+/* offset setter (BaseKVCache.offset, KVCache.swift:256-262; the device
+ * counter of the fixed-buffer caches, CompilableKVCache.swift:96-104). */
+int vkv_cache_set_offset(vkv_cache cache, int64_t offset);
 int vkv_cache_max_size(vkv_cache cache, int64_t *max_size); /* -1 = none */
 int vkv_cache_is_trimmable(vkv_cache cache, int32_t *trimmable);
 int vkv_cache_trim(vkv_cache cache, int64_t n, int64_t *trimmed);
@@ -261,6 +274,39 @@ int vkv_cache_to_unquantized(vkv_cache quantized, void *stream, vkv_cache *out);
  * KVCacheSimple.readKV (:516-525): K/V in temporal order, trimmed to offset,
  * without changing the cache state. */
 int vkv_cache_read_kv(vkv_cache cache, void *stream, vkv_array *keys, vkv_array *values);
+
+/* Fixed-buffer device-offset caches (VKV_CACHE_COMPILABLE*).  A decode
+ * step made of vkv_cache_update, vkv_cache_make_mask and attention on these
+ * caches reads no value back to the host, so it can be captured in a HIP
+ * graph once and replayed (the reference's compile() path).  offset and
+ * state/metaState read the device counters back (synchronizing), like the
+ * reference's .item(). */
+
+/* CompilableKVCache(from:maxLength:) (CompilableKVCache.swift:62-86): a new
+ * cache holding src's state (2 float arrays) at positions [0, len) of
+ * zeroed max_length buffers, offset = len. */
+int vkv_cache_to_compilable(vkv_cache src, int64_t max_length, void *stream, vkv_cache *out);
+/* CompilableRotatingKVCache(from:) (CompilableRotatingKVCache.swift:91-150):
+ * a new cache with src's keep/maxSize/step, ring index and offset, and its
+ * buffers extended with zeros to maxSize. */
+int vkv_cache_to_compilable_rotating(vkv_cache rotating, void *stream, vkv_cache *out);
+/* innerState: the arrays a captured step reads and writes in place —
+ * keys and values [B,H,max,D], then the counters as int32 [1] device arrays:
+ * the offset (CompilableKVCache.swift:108-113), or the ring index then the
+ * offset (CompilableRotatingKVCache.swift:255-264).  `arrays` has room for 4. */
+int vkv_cache_inner_state(vkv_cache cache, vkv_array *arrays, int32_t *count);
+
+/* dynamicSliceUpdate(src, update:, start:, axes: [axis])
+ * (DynamicSlice.swift:50-71): dst[..., start + i, ...] = update[..., i, ...]
+ * along `axis`, in place, where start is the int32 at device address
+ * `start` read by the kernel (clamped to [0, dim - update dim]).  Up to 4-D,
+ * same element size, strided. */
+int vkv_dynamic_slice_update(vkv_array *dst, const vkv_array *update, const int32_t *start,
+                             int32_t axis, void *stream);
+/* dynamicSlice(src, start:, axes: [axis], sliceSize:) (DynamicSlice.swift:
+ * 21-48): out = src[..., start : start + out dim, ...] along `axis`. */
+int vkv_dynamic_slice(const vkv_array *src, const int32_t *start, int32_t axis, vkv_array *out,
+                      void *stream);
 
 /* ---------------------------------------------------- paged block pool */
 

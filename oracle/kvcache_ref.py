@@ -195,6 +195,136 @@ class RotatingKVCacheRef:
         return "none"
 
 
+def dynamic_slice_update_ref(dst, update, start, axis):
+    """dynamicSliceUpdate (DynamicSlice.swift:50-71) on numpy arrays: a copy
+    of dst with update written at `start` along axis.  Starts are clamped so
+    the update fits (the XLA dynamic_update_slice rule; the reference only
+    issues in-range starts)."""
+    out = dst.copy()
+    s = int(min(max(start, 0), dst.shape[axis] - update.shape[axis]))
+    idx = [slice(None)] * dst.ndim
+    idx[axis] = slice(s, s + update.shape[axis])
+    out[tuple(idx)] = update
+    return out
+
+
+def dynamic_slice_ref(src, start, axis, size):
+    """dynamicSlice (DynamicSlice.swift:21-48), clamped like the update."""
+    s = int(min(max(start, 0), src.shape[axis] - size))
+    idx = [slice(None)] * src.ndim
+    idx[axis] = slice(s, s + size)
+    return src[tuple(idx)].copy()
+
+
+class CompilableKVCacheRef:
+    """CompilableKVCache.swift:40-262: fixed [B, H, maxLength, D] buffers,
+    update writes at offset and returns the whole buffers, makeMask is always
+    an array mask over the buffer."""
+
+    def __init__(self, max_length=4096, step=256):
+        self.max_length, self.step = max_length, step
+        self.keys = self.values = None
+        self.offset = 0
+
+    @classmethod
+    def from_state(cls, state, max_length=4096):  # :62-86
+        c = cls(max_length)
+        if len(state) >= 2:
+            c.state = state
+        return c
+
+    def update(self, k, v):  # :115-149
+        if self.keys is None:
+            B, H, _, D = k.shape
+            self.keys = np.zeros((B, H, self.max_length, D), k.dtype)
+            self.values = np.zeros((B, H, self.max_length, v.shape[3]), v.dtype)
+        self.keys = dynamic_slice_update_ref(self.keys, k, self.offset, 2)
+        self.values = dynamic_slice_update_ref(self.values, v, self.offset, 2)
+        self.offset += k.shape[2]
+        return self.keys, self.values
+
+    def make_mask(self, n, window=None):  # :167-193
+        linds = (self.offset + np.arange(n))[:, None]
+        rinds = np.arange(self.max_length)[None]
+        m = linds >= rinds
+        if window is not None:
+            m &= rinds >= linds - (window - 1)
+        return m
+
+    @property
+    def state(self):  # :197-211
+        if self.keys is None:
+            return []
+        if self.offset == self.keys.shape[2]:
+            return [self.keys, self.values]
+        return [self.keys[:, :, :self.offset], self.values[:, :, :self.offset]]
+
+    @state.setter
+    def state(self, arrays):  # :212-225
+        k, v = arrays[0], arrays[1]
+        L = k.shape[2]
+        self.keys = np.zeros(k.shape[:2] + (self.max_length, k.shape[3]), k.dtype)
+        self.values = np.zeros(v.shape[:2] + (self.max_length, v.shape[3]), v.dtype)
+        self.keys[:, :, :L] = k
+        self.values[:, :, :L] = v
+        self.offset = L
+
+    def trim(self, n):  # :229-240
+        t = min(self.offset, n)
+        self.offset -= t
+        return t
+
+
+class CompilableRotatingKVCacheRef:
+    """BatchEngine/CompilableRotatingKVCache.swift:1-265, with the counters
+    as plain ints (the reference keeps them in MLXArrays)."""
+
+    def __init__(self, max_size, keep=0, step=256):
+        self.max_size, self.keep, self.step = max_size, keep, step
+        self.keys = self.values = None
+        self.idx = 0
+        self.offset = 0
+
+    @classmethod
+    def from_rotating(cls, r):  # :91-150
+        c = cls(r.max_size, r.keep, r.step)
+        c.idx, c.offset = r.idx, r.offset
+        if r.keys is not None:
+            cur = r.keys.shape[2]
+            if cur < c.max_size:
+                pad = c.max_size - cur
+                B, H, _, D = r.keys.shape
+                c.keys = _cat([r.keys, np.zeros((B, H, pad, D), r.keys.dtype)])
+                c.values = _cat([r.values, np.zeros((B, H, pad, r.values.shape[3]), r.values.dtype)])
+            else:
+                c.keys, c.values = r.keys.copy(), r.values.copy()
+        return c
+
+    def update(self, k, v):  # :157-207
+        if self.keys is None:
+            B, H, _, D = k.shape
+            self.keys = np.zeros((B, H, self.max_size, D), k.dtype)
+            self.values = np.zeros((B, H, self.max_size, v.shape[3]), v.dtype)
+        self.keys = dynamic_slice_update_ref(self.keys, k, self.idx, 2)
+        self.values = dynamic_slice_update_ref(self.values, v, self.idx, 2)
+        adv = self.idx + k.shape[2]
+        if self.keep > 0:
+            rot = self.keep + (adv - self.keep) % (self.max_size - self.keep)
+        else:
+            rot = adv % self.max_size
+        self.idx = adv if adv < self.max_size else rot
+        self.offset += k.shape[2]
+        return self.keys, self.values
+
+    def make_mask(self, n, window=None):  # :233-260
+        linds = (self.offset + np.arange(n))[:, None]
+        rinds = np.arange(self.max_size)[None]
+        m = np.where(linds >= self.max_size, True, linds >= rinds)
+        if window is not None:
+            m &= rinds >= linds - (window - 1)
+        return m
+
+
 def causal_mask(n, offset, window=None):
     """createCausalMask (KVCache.swift:314-336)."""
     r = np.arange(offset + n)[None]

@@ -485,7 +485,14 @@ int vkv_cache_offset(vkv_cache cache, int64_t* offset) {
   return guard([&] {
     need(cache, "cache");
     need(offset, "offset");
-    *offset = cache->impl->offset;
+    *offset = cache->impl->current_offset();
+  });
+}
+
+int vkv_cache_set_offset(vkv_cache cache, int64_t offset) {
+  return guard([&] {
+    need(cache, "cache");
+    cache->impl->set_offset(offset);
   });
 }
 
@@ -594,6 +601,112 @@ int vkv_cache_to_quantized(vkv_cache simple, int32_t group_size, int32_t bits, v
       throw;
     }
     *out = h;
+  });
+}
+
+int vkv_cache_to_compilable(vkv_cache src, int64_t max_length, void* stream, vkv_cache* out) {
+  return guard([&] {
+    need(src, "cache");
+    need(out, "out");
+    if (max_length <= 0) throw Error("maxLength must be > 0");
+    auto c = std::make_unique<CompilableCache>(max_length, 256);
+    vkv_array s[6];
+    const int n = src->impl->state(S(stream), s);
+    c->init_from(s, n, S(stream));
+    auto h = new vkv_cache_s;
+    h->impl = std::move(c);
+    *out = h;
+  });
+}
+
+int vkv_cache_to_compilable_rotating(vkv_cache rotating, void* stream, vkv_cache* out) {
+  return guard([&] {
+    need(rotating, "cache");
+    need(out, "out");
+    if (rotating->impl->kind() != VKV_CACHE_ROTATING)
+      throw Error("CompilableRotatingKVCache(from:) needs a RotatingKVCache");
+    const auto* r = static_cast<const RotatingCache*>(rotating->impl.get());
+    auto c = std::make_unique<CompilableRotatingCache>(static_cast<int>(r->max_), static_cast<int>(r->keep_),
+                                                       static_cast<int>(r->step_));
+    c->init_from(*r, S(stream));
+    auto h = new vkv_cache_s;
+    h->impl = std::move(c);
+    *out = h;
+  });
+}
+
+int vkv_cache_inner_state(vkv_cache cache, vkv_array* arrays, int32_t* count) {
+  return guard([&] {
+    need(cache, "cache");
+    need(arrays, "arrays");
+    need(count, "count");
+    if (auto* c = dynamic_cast<CompilableCache*>(cache->impl.get()))
+      *count = c->inner_state(arrays);
+    else if (auto* r = dynamic_cast<CompilableRotatingCache*>(cache->impl.get()))
+      *count = r->inner_state(arrays);
+    else
+      throw Error("innerState is exposed for the fixed-buffer (compilable) caches only");
+  });
+}
+
+static int dtype_bytes(int dt) {
+  return dt == VKV_F32 || dt == VKV_U32 || dt == VKV_I32 ? 4 : dt == VKV_U8 || dt == VKV_BOOL ? 1 : 2;
+}
+
+static DynCopy dyn_args(const vkv_array& a, const vkv_array& b, const int32_t* start, int axis,
+                        bool on_dst) {
+  // a: the array the start applies to, b: the other side; shapes are b's
+  if (a.ndim != b.ndim || a.ndim < 1 || a.ndim > 4) throw Error("arrays must have the same rank, 1 to 4");
+  if (axis < 0) axis += a.ndim;
+  if (axis < 0 || axis >= a.ndim) throw Error("axis out of range");
+  if (dtype_bytes(a.dtype) != dtype_bytes(b.dtype)) throw Error("element sizes differ");
+  for (int i = 0; i < a.ndim; i++)
+    if (i != axis && a.shape[i] != b.shape[i]) throw Error("shapes differ outside the slice axis");
+  if (b.shape[axis] > a.shape[axis]) throw Error("the slice is larger than the array along the axis");
+  need(start, "start");
+  DynCopy c{};
+  const int pad = 4 - a.ndim;
+  for (int i = 0; i < 4; i++) {
+    const int j = i - pad;
+    c.shape[i] = j < 0 ? 1 : b.shape[j];
+    const int64_t as = j < 0 ? 0 : a.strides[j], bs = j < 0 ? 0 : b.strides[j];
+    c.sstr[i] = on_dst ? bs : as;
+    c.dstr[i] = on_dst ? as : bs;
+  }
+  c.src = static_cast<const uint8_t*>(on_dst ? b.data : a.data);
+  c.dst = static_cast<uint8_t*>(on_dst ? a.data : b.data);
+  c.axis = axis + pad;
+  c.on_dst = on_dst ? 1 : 0;
+  c.limit = a.shape[axis];
+  c.start = start;
+  return c;
+}
+
+int vkv_dynamic_slice_update(vkv_array* dst, const vkv_array* update, const int32_t* start, int32_t axis,
+                             void* stream) {
+  return guard([&] {
+    need(dst, "dst");
+    need(update, "update");
+    const DynCopy c = dyn_args(*dst, *update, start, axis, true);
+    if (c.shape[0] * c.shape[1] * c.shape[2] * c.shape[3] > 0) {
+      need(dst->data, "dst data");
+      need(update->data, "update data");
+    }
+    launch_dyn_copy(dtype_bytes(dst->dtype), c, S(stream));
+  });
+}
+
+int vkv_dynamic_slice(const vkv_array* src, const int32_t* start, int32_t axis, vkv_array* out,
+                      void* stream) {
+  return guard([&] {
+    need(src, "src");
+    need(out, "out");
+    const DynCopy c = dyn_args(*src, *out, start, axis, false);
+    if (c.shape[0] * c.shape[1] * c.shape[2] * c.shape[3] > 0) {
+      need(src->data, "src data");
+      need(out->data, "out data");
+    }
+    launch_dyn_copy(dtype_bytes(src->dtype), c, S(stream));
   });
 }
 

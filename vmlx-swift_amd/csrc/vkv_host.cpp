@@ -131,6 +131,12 @@ std::unique_ptr<Cache> make_cache(const vkv_cache_params& p) {
       if (group != 32 && group != 64 && group != 128) throw Error("group_size must be 32, 64 or 128");
       return std::make_unique<QuantizedCache>(group, bits, 256);
     }
+    case VKV_CACHE_COMPILABLE:
+      return std::make_unique<CompilableCache>(p.max_size > 0 ? p.max_size : 4096, step);
+    case VKV_CACHE_COMPILABLE_ROTATING:
+      if (p.max_size <= 0) throw Error("CompilableRotatingKVCache requires maxSize > 0");
+      if (p.keep < 0 || p.keep >= p.max_size) throw Error("keep must be in [0, maxSize)");
+      return std::make_unique<CompilableRotatingCache>(p.max_size, p.keep, step);
     default: throw Error("unknown cache kind");
   }
 }
@@ -475,6 +481,345 @@ int RotatingCache::make_mask(int n, int window, bool return_array, hipStream_t s
     return VKV_MASK_ARRAY;
   }
   return VKV_MASK_NONE;
+}
+
+// ------------------------------------------------------ CompilableKVCache
+
+static DevBuf make_counters() {
+  DevBuf c(2 * sizeof(int32_t));
+  VKV_HIP(hipMemset(c.get(), 0, c.size()));
+  return c;
+}
+
+static vkv_array counter_array(const DevBuf& c, int slot) {
+  vkv_array a{};
+  a.data = static_cast<int32_t*>(c.get()) + slot;
+  a.dtype = VKV_I32;
+  a.ndim = 1;
+  a.shape[0] = 1;
+  a.strides[0] = 1;
+  return a;
+}
+
+static std::pair<int64_t, int64_t> read_counters(const DevBuf& c, hipStream_t last) {
+  if (last) VKV_HIP(hipStreamSynchronize(last));
+  int32_t h[2];
+  VKV_HIP(hipMemcpy(h, c.get(), sizeof(h), hipMemcpyDeviceToHost));
+  return {h[0], h[1]};
+}
+
+// d[:, :, start + i, :] = a[:, :, i, :] with start the int32 at `start`
+// (dynamicSliceUpdate along axis 2, DynamicSlice.swift:50-71)
+static void write_at_device_offset(const Dense4& d, const vkv_array& a, const int32_t* start,
+                                   hipStream_t st) {
+  DynCopy c{};
+  c.src = static_cast<const uint8_t*>(a.data);
+  c.dst = d.buf->bytes();
+  const int64_t dstr[4] = {d.H * d.cap * d.D, d.cap * d.D, d.D, 1};
+  for (int i = 0; i < 4; i++) {
+    c.sstr[i] = a.strides[i];
+    c.dstr[i] = dstr[i];
+    c.shape[i] = a.shape[i];
+  }
+  c.axis = 2;
+  c.on_dst = 1;
+  c.limit = d.cap;
+  c.start = start;
+  launch_dyn_copy(elem_bytes(a.dtype), c, st);
+}
+
+static void check_kv_pair(const vkv_array& k, const vkv_array& v) {
+  check4(k, "keys");
+  check4(v, "values");
+  if (k.shape[0] != v.shape[0] || k.shape[1] != v.shape[1] || k.shape[2] != v.shape[2] ||
+      k.dtype != v.dtype)
+    throw Error("keys and values must agree in batch, heads, length and dtype");
+}
+
+static void check_fits(const Dense4& d, const vkv_array& a, const char* name) {
+  if (d.B != a.shape[0] || d.H != a.shape[1] || d.D != a.shape[3] || d.dtype != a.dtype)
+    throw Error(std::string(name) + " do not match the cache's fixed buffers");
+}
+
+static int full_mask(std::map<int, DevBuf>& masks, const DevBuf& ctr, int n, int64_t cols, int window,
+                     int ring, hipStream_t st, vkv_array* mask) {
+  if (n < 1) throw Error("n must be >= 1");
+  DevBuf& b = masks[n];
+  const size_t need = static_cast<size_t>(n) * cols;
+  if (b.size() < need) b.alloc(need);
+  launch_offset_mask(static_cast<const int32_t*>(ctr.get()), n, static_cast<int>(cols), window, ring,
+                     b.bytes(), st);
+  *mask = vkv_array{};
+  mask->data = b.get();
+  mask->dtype = VKV_BOOL;
+  mask->ndim = 2;
+  mask->shape[0] = n;
+  mask->shape[1] = cols;
+  mask->strides[0] = cols;
+  mask->strides[1] = 1;
+  return VKV_MASK_ARRAY;
+}
+
+CompilableCache::CompilableCache(int64_t max_length, int step)
+    : max_(max_length), step_(step), ctr_(make_counters()) {}
+
+std::pair<int64_t, int64_t> CompilableCache::counters() const { return read_counters(ctr_, last_); }
+
+void CompilableCache::alloc_buffers(const vkv_array& k, const vkv_array& v, int64_t len,
+                                    hipStream_t st) {
+  k_ = alloc_dense(k.shape[0], k.shape[1], len, k.shape[3], k.dtype, true, st);
+  v_ = alloc_dense(v.shape[0], v.shape[1], len, v.shape[3], v.dtype, true, st);
+}
+
+// update(keys:values:) (CompilableKVCache.swift:115-149): allocate zeroed
+// [B, H, maxLength, D] buffers on first use, write the new tokens at the
+// device offset, advance it on the device, return the whole buffers.
+void CompilableCache::update(const vkv_array& k, const vkv_array& v, hipStream_t st, vkv_array* ok,
+                             vkv_array* ov) {
+  check_kv_pair(k, v);
+  if (k_.empty()) {
+    alloc_buffers(k, v, max_, st);
+  } else {
+    check_fits(k_, k, "keys");
+    check_fits(v_, v, "values");
+  }
+  const int64_t S = k.shape[2];
+  if (S > max_) throw Error("update is longer than the cache's maxLength");
+  int32_t* ctr = static_cast<int32_t*>(ctr_.get());
+  write_at_device_offset(k_, k, ctr, st);
+  write_at_device_offset(v_, v, ctr, st);
+  launch_counter_advance(ctr, static_cast<int>(S), 0, 0, 0, st);
+  last_ = st;
+  *ok = k_.view(max_);
+  *ov = v_.view(max_);
+}
+
+// state getter (CompilableKVCache.swift:197-211): the whole buffers when
+// full, else [.., ..<offset, ..]
+int CompilableCache::state(hipStream_t, vkv_array* out) {
+  if (k_.empty()) return 0;
+  const int64_t off = std::max<int64_t>(0, std::min<int64_t>(counters().first, k_.cap));
+  out[0] = k_.view(off);
+  out[1] = v_.view(off);
+  return 2;
+}
+
+// state setter (CompilableKVCache.swift:212-225): fresh zeroed maxLength
+// buffers holding the arrays at [0, len), offset = len
+void CompilableCache::set_state(const vkv_array* a, int count, hipStream_t st) {
+  if (count != 2) throw Error("CompilableKVCache state must have exactly 2 arrays (keys, values)");
+  check_kv_pair(a[0], a[1]);
+  const int64_t len = a[0].shape[2];
+  if (len > max_) throw Error("state is longer than the cache's maxLength");
+  alloc_buffers(a[0], a[1], max_, st);
+  copy_tokens(k_, 0, a[0], 0, len, st);
+  copy_tokens(v_, 0, a[1], 0, len, st);
+  launch_counter_set(static_cast<int32_t*>(ctr_.get()), static_cast<int32_t>(len), 0, st);
+  last_ = st;
+}
+
+void CompilableCache::init_from(const vkv_array* state, int count, hipStream_t st) {
+  if (count < 2) return;  // an empty source: nothing to copy
+  for (int i = 0; i < 2; i++)
+    if (state[i].dtype != VKV_F32 && state[i].dtype != VKV_F16 && state[i].dtype != VKV_BF16)
+      throw Error("CompilableKVCache(from:) needs a cache whose state is float keys and values");
+  set_state(state, 2, st);
+}
+
+void CompilableCache::set_offset(int64_t v) {
+  launch_counter_set(static_cast<int32_t*>(ctr_.get()), static_cast<int32_t>(v), 0, last_);
+}
+
+// trim (CompilableKVCache.swift:229-240): moves the device offset back
+int64_t CompilableCache::trim(int64_t n) {
+  const int64_t cur = counters().first;
+  const int64_t t = std::min(cur, n);
+  launch_counter_set(static_cast<int32_t*>(ctr_.get()), static_cast<int32_t>(cur - t), 0, last_);
+  return t;
+}
+
+// copy (CompilableKVCache.swift:242-257): independent buffers and counter
+std::unique_ptr<Cache> CompilableCache::copy(hipStream_t st) {
+  if (last_ && last_ != st) VKV_HIP(hipStreamSynchronize(last_));
+  auto c = std::make_unique<CompilableCache>(max_, static_cast<int>(step_));
+  if (!k_.empty()) {
+    c->k_ = alloc_dense(k_.B, k_.H, k_.cap, k_.D, k_.dtype, false, st);
+    c->v_ = alloc_dense(v_.B, v_.H, v_.cap, v_.D, v_.dtype, false, st);
+    copy_dense(c->k_, 0, k_, 0, k_.cap, st);
+    copy_dense(c->v_, 0, v_, 0, v_.cap, st);
+  }
+  VKV_HIP(hipMemcpyAsync(c->ctr_.get(), ctr_.get(), ctr_.size(), hipMemcpyDeviceToDevice, st));
+  c->last_ = st;
+  return c;
+}
+
+void CompilableCache::read_kv(hipStream_t st, vkv_array* k, vkv_array* v) {
+  vkv_array s[2];
+  if (state(st, s) != 2) throw Error("nothing cached yet");
+  *k = s[0];
+  *v = s[1];
+}
+
+// makeMask (CompilableKVCache.swift:167-193): always an array mask over the
+// whole buffer, built on the device from the offset
+int CompilableCache::make_mask(int n, int window, bool, hipStream_t st, vkv_array* mask) {
+  return full_mask(masks_, ctr_, n, max_, window, 0, st, mask);
+}
+
+int CompilableCache::inner_state(vkv_array* out) {
+  int c = 0;
+  if (!k_.empty()) {
+    out[c++] = k_.view(k_.cap);
+    out[c++] = v_.view(v_.cap);
+  }
+  out[c++] = counter_array(ctr_, 0);
+  return c;
+}
+
+// --------------------------------------------- CompilableRotatingKVCache
+
+CompilableRotatingCache::CompilableRotatingCache(int max_size, int keep, int step)
+    : RotatingCache(max_size, keep, step), ctr_(make_counters()) {}
+
+void CompilableRotatingCache::pull() const {
+  auto* self = const_cast<CompilableRotatingCache*>(this);
+  const auto c = read_counters(ctr_, last_);
+  self->offset = c.first;
+  self->idx_ = c.second;
+}
+
+void CompilableRotatingCache::push(hipStream_t st) {
+  launch_counter_set(static_cast<int32_t*>(ctr_.get()), static_cast<int32_t>(offset),
+                     static_cast<int32_t>(idx_), st);
+  last_ = st;
+}
+
+int64_t CompilableRotatingCache::current_offset() {
+  pull();
+  return offset;
+}
+
+void CompilableRotatingCache::set_offset(int64_t v) {
+  pull();
+  offset = v;
+  push(last_);
+}
+
+bool CompilableRotatingCache::trimmable() const {
+  pull();
+  return offset < max_;
+}
+
+int64_t CompilableRotatingCache::trim(int64_t n) {
+  pull();
+  const int64_t t = RotatingCache::trim(n);
+  push(last_);
+  return t;
+}
+
+// update (CompilableRotatingKVCache.swift:157-207): allocate the buffers at
+// maxSize on first use, write at the device ring index, advance the index
+// with the ring wrap and the offset on the device, return the whole buffers.
+void CompilableRotatingCache::update(const vkv_array& k, const vkv_array& v, hipStream_t st,
+                                     vkv_array* ok, vkv_array* ov) {
+  check_kv_pair(k, v);
+  if (k_.empty()) {
+    k_ = alloc_dense(k.shape[0], k.shape[1], max_, k.shape[3], k.dtype, true, st);
+    v_ = alloc_dense(v.shape[0], v.shape[1], max_, v.shape[3], v.dtype, true, st);
+  } else {
+    check_fits(k_, k, "keys");
+    check_fits(v_, v, "values");
+  }
+  const int64_t S = k.shape[2];
+  if (S > k_.cap) throw Error("update is longer than the ring");
+  int32_t* ctr = static_cast<int32_t*>(ctr_.get());
+  write_at_device_offset(k_, k, ctr + 1, st);
+  write_at_device_offset(v_, v, ctr + 1, st);
+  launch_counter_advance(ctr, static_cast<int>(S), 1, static_cast<int>(max_), static_cast<int>(keep_),
+                         st);
+  last_ = st;
+  *ok = k_.view(k_.cap);
+  *ov = v_.view(v_.cap);
+}
+
+int CompilableRotatingCache::state(hipStream_t st, vkv_array* out) {
+  pull();
+  return RotatingCache::state(st, out);
+}
+
+// state setter: the arrays become the buffers (RotatingKVCache.swift
+// :813-822), extended with zeros to maxSize so that device-offset writes
+// stay in place (the promotion of CompilableRotatingKVCache.swift:113-140)
+void CompilableRotatingCache::set_state(const vkv_array* a, int count, hipStream_t st) {
+  if (count != 2) throw Error("RotatingKVCache state must have exactly 2 arrays");
+  check_kv_pair(a[0], a[1]);
+  const int64_t len = a[0].shape[2];
+  const int64_t cap = std::max<int64_t>(len, max_);
+  k_ = alloc_dense(a[0].shape[0], a[0].shape[1], cap, a[0].shape[3], a[0].dtype, len < cap, st);
+  v_ = alloc_dense(a[1].shape[0], a[1].shape[1], cap, a[1].shape[3], a[1].dtype, len < cap, st);
+  copy_tokens(k_, 0, a[0], 0, len, st);
+  copy_tokens(v_, 0, a[1], 0, len, st);
+  last_ = st;
+}
+
+std::vector<std::string> CompilableRotatingCache::meta_state() const {
+  pull();
+  return RotatingCache::meta_state();
+}
+
+void CompilableRotatingCache::set_meta_state(const std::vector<std::string>& v) {
+  RotatingCache::set_meta_state(v);
+  push(last_);
+}
+
+std::unique_ptr<Cache> CompilableRotatingCache::copy(hipStream_t st) {
+  if (last_ && last_ != st) VKV_HIP(hipStreamSynchronize(last_));
+  auto c = std::make_unique<CompilableRotatingCache>(static_cast<int>(max_), static_cast<int>(keep_),
+                                                     static_cast<int>(step_));
+  if (!k_.empty()) {
+    c->k_ = alloc_dense(k_.B, k_.H, k_.cap, k_.D, k_.dtype, false, st);
+    c->v_ = alloc_dense(v_.B, v_.H, v_.cap, v_.D, v_.dtype, false, st);
+    copy_dense(c->k_, 0, k_, 0, k_.cap, st);
+    copy_dense(c->v_, 0, v_, 0, v_.cap, st);
+  }
+  VKV_HIP(hipMemcpyAsync(c->ctr_.get(), ctr_.get(), ctr_.size(), hipMemcpyDeviceToDevice, st));
+  c->last_ = st;
+  return c;
+}
+
+void CompilableRotatingCache::read_kv(hipStream_t st, vkv_array* k, vkv_array* v) {
+  pull();
+  RotatingCache::read_kv(st, k, v);
+}
+
+// makeMask (CompilableRotatingKVCache.swift:233-260): causal over the whole
+// buffer, all true once the ring is full, then the window
+int CompilableRotatingCache::make_mask(int n, int window, bool, hipStream_t st, vkv_array* mask) {
+  return full_mask(masks_, ctr_, n, max_, window, 1, st, mask);
+}
+
+int CompilableRotatingCache::inner_state(vkv_array* out) {
+  int c = 0;
+  if (!k_.empty()) {
+    out[c++] = k_.view(k_.cap);
+    out[c++] = v_.view(v_.cap);
+  }
+  out[c++] = counter_array(ctr_, 1);
+  out[c++] = counter_array(ctr_, 0);
+  return c;
+}
+
+void CompilableRotatingCache::init_from(const RotatingCache& src, hipStream_t st) {
+  offset = src.offset;
+  idx_ = src.idx_;
+  if (!src.k_.empty()) {
+    const int64_t cap = std::max<int64_t>(src.k_.cap, max_);
+    k_ = alloc_dense(src.k_.B, src.k_.H, cap, src.k_.D, src.k_.dtype, src.k_.cap < cap, st);
+    v_ = alloc_dense(src.v_.B, src.v_.H, cap, src.v_.D, src.v_.dtype, src.v_.cap < cap, st);
+    copy_dense(k_, 0, src.k_, 0, src.k_.cap, st);
+    copy_dense(v_, 0, src.v_, 0, src.v_.cap, st);
+  }
+  push(st);
 }
 
 // -------------------------------------------------------- QuantizedKVCache

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <list>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -84,6 +85,11 @@ class Cache {
  public:
   virtual ~Cache() = default;
   int64_t offset = 0;
+  // offset as the protocol reports it (the fixed-buffer caches keep theirs
+  // in device memory and read it back here)
+  virtual int64_t current_offset() { return offset; }
+  // BaseKVCache.offset setter (KVCache.swift:256-262)
+  virtual void set_offset(int64_t v) { offset = v; }
   virtual int kind() const = 0;
   virtual int64_t max_size() const { return -1; }
   virtual bool trimmable() const { return false; }
@@ -158,6 +164,77 @@ class RotatingCache : public Cache {
   Dense4 temporal_order(const Dense4& a, hipStream_t st) const;
   Dense4 trim_cat(int64_t trim_size, const Dense4& a, const vkv_array* append, hipStream_t st) const;
   void outputs(vkv_array* ok, vkv_array* ov) const;
+};
+
+// Fixed-buffer caches with the write position in device memory
+// (CompilableKVCache.swift:40-262, BatchEngine/CompilableRotatingKVCache.
+// swift:1-265): [B, H, max, D] buffers allocated once, updates written at
+// the device counter by a kernel that reads it, the counters advanced on
+// the device, the full buffers returned, and the mask built on the device,
+// so a decode step issues no host read and can be captured in a HIP graph.
+// Counters: int32 [2] = (offset, ring write index).
+class CompilableCache : public Cache {
+ public:
+  CompilableCache(int64_t max_length, int step);
+  int kind() const override { return VKV_CACHE_COMPILABLE; }
+  int64_t current_offset() override { return counters().first; }
+  // CompilableKVCache.offset setter (CompilableKVCache.swift:96-104)
+  void set_offset(int64_t v) override;
+  bool trimmable() const override { return true; }
+  int64_t trim(int64_t n) override;
+  int64_t capacity() const override { return k_.cap; }
+  void update(const vkv_array& k, const vkv_array& v, hipStream_t st, vkv_array* ok,
+              vkv_array* ov) override;
+  int state(hipStream_t, vkv_array* out) override;
+  void set_state(const vkv_array* a, int count, hipStream_t st) override;
+  std::unique_ptr<Cache> copy(hipStream_t st) override;
+  void read_kv(hipStream_t, vkv_array* k, vkv_array* v) override;
+  int make_mask(int n, int window, bool return_array, hipStream_t st, vkv_array* mask) override;
+  // innerState (CompilableKVCache.swift:108-113): keys, values, offset
+  int inner_state(vkv_array* out);
+  // CompilableKVCache(from:maxLength:) (CompilableKVCache.swift:62-86)
+  void init_from(const vkv_array* state, int count, hipStream_t st);
+  std::pair<int64_t, int64_t> counters() const;  // host read of (offset, idx)
+  int64_t max_, step_;
+  Dense4 k_, v_;
+  DevBuf ctr_;
+  hipStream_t last_ = nullptr;  // stream of the last device write
+
+ protected:
+  void alloc_buffers(const vkv_array& k, const vkv_array& v, int64_t len, hipStream_t st);
+  std::map<int, DevBuf> masks_;  // one mask buffer per row count, never moved
+};
+
+class CompilableRotatingCache : public RotatingCache {
+ public:
+  CompilableRotatingCache(int max_size, int keep, int step);
+  int kind() const override { return VKV_CACHE_COMPILABLE_ROTATING; }
+  int64_t current_offset() override;
+  void set_offset(int64_t v) override;
+  int64_t trim(int64_t n) override;
+  bool trimmable() const override;
+  int64_t capacity() const override { return k_.cap; }
+  void update(const vkv_array& k, const vkv_array& v, hipStream_t st, vkv_array* ok,
+              vkv_array* ov) override;
+  int state(hipStream_t, vkv_array* out) override;
+  void set_state(const vkv_array* a, int count, hipStream_t st) override;
+  std::vector<std::string> meta_state() const override;
+  void set_meta_state(const std::vector<std::string>& v) override;
+  std::unique_ptr<Cache> copy(hipStream_t st) override;
+  void read_kv(hipStream_t st, vkv_array* k, vkv_array* v) override;
+  int make_mask(int n, int window, bool return_array, hipStream_t st, vkv_array* mask) override;
+  // innerState (CompilableRotatingKVCache.swift:255-264): keys, values,
+  // ring index, offset
+  int inner_state(vkv_array* out);
+  // CompilableRotatingKVCache(from:) (CompilableRotatingKVCache.swift:91-150)
+  void init_from(const RotatingCache& src, hipStream_t st);
+  DevBuf ctr_;
+  mutable hipStream_t last_ = nullptr;
+
+ private:
+  void pull() const;  // counters -> offset, idx_ (host mirrors)
+  void push(hipStream_t st);
+  std::map<int, DevBuf> masks_;
 };
 
 // QuantizedKVCache on paged storage: 32-token blocks, block id j*B + b for

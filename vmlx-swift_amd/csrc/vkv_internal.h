@@ -193,6 +193,30 @@ bool mla_supported(int dtype, int bits, int group, int head_dim, int v_head_dim,
 size_t mla_plan(MlaArgs& a, int want);
 void launch_mla(const MlaArgs& a, hipStream_t st);
 
+// ---- device-offset operations (vkv_compile.hip)
+// A copy of a block of up to 4 dims whose start along `axis` is the int32
+// at `start` (device memory), clamped to [0, limit - shape[axis]]: on the
+// destination side for a slice update, on the source side for a slice.
+struct DynCopy {
+  const uint8_t* src;
+  int64_t sstr[4];     // element strides
+  uint8_t* dst;
+  int64_t dstr[4];
+  int64_t shape[4];    // the copied block
+  int32_t axis;
+  int32_t on_dst;      // 1: dst index += start (update); 0: src index += start (slice)
+  int64_t limit;       // extent of the offset side along axis
+  const int32_t* start;
+};
+void launch_dyn_copy(int esize, const DynCopy& c, hipStream_t st);
+// Write counters of the fixed-buffer caches: ctr[0] = offset, ctr[1] = ring
+// write index.  Advance by n (with the ring wrap when ring != 0), or set.
+void launch_counter_advance(int32_t* ctr, int n, int ring, int max_size, int keep, hipStream_t st);
+void launch_counter_set(int32_t* ctr, int32_t offset, int32_t idx, hipStream_t st);
+// [n, cols] bool mask from the device offset (see vkv_compile.hip).
+void launch_offset_mask(const int32_t* ctr, int n, int cols, int window, int ring, uint8_t* mask,
+                        hipStream_t st);
+
 // Kernel timing (a measurement aid): while enabled, launchers start their
 // main kernel with hipExtLaunchKernelGGL and a start/stop event pair, which
 // the runtime records at the kernel's own start and end.

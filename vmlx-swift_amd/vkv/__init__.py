@@ -24,6 +24,7 @@ LIB_PATH = os.path.join(PKG, "libvkv.so")
 F32, F16, BF16, U32, I32, U8, BOOL = 0, 1, 2, 3, 4, 5, 6
 MASK_NONE, MASK_CAUSAL, MASK_ARRAY = 0, 1, 2
 CACHE_SIMPLE, CACHE_ROTATING, CACHE_QUANTIZED = 0, 1, 2
+CACHE_COMPILABLE, CACHE_COMPILABLE_ROTATING = 3, 4
 VIEW_KEYS_ONLY = 1
 
 
@@ -79,6 +80,8 @@ EXPORTS = (
     "vkv_prefix_register", "vkv_prefix_clear", "vkv_prefix_store", "vkv_prefix_fetch",
     "vkv_prefix_stats_get", "vkv_prefix_block_tokens", "vkv_block_hash", "vkv_array_copy",
     "vkv_kernel_timing", "vkv_kernel_timing_read", "vkv_fill_normal",
+    "vkv_cache_to_compilable", "vkv_cache_to_compilable_rotating", "vkv_cache_inner_state",
+    "vkv_dynamic_slice_update", "vkv_dynamic_slice", "vkv_cache_set_offset",
 )
 TIME_DECODE, TIME_MLA = 0, 1
 
@@ -183,23 +186,34 @@ def dequantized(wq, scales, biases, group_size: int = 64, bits: int = 4, stream=
     return out
 
 
+def _as_array(x):
+    """A library-owned Array passes through; a tensor is described."""
+    return x if isinstance(x, Array) else arr(x)
+
+
 def _mask_args(mask):
     if mask is None:
         return MASK_NONE, None
     if isinstance(mask, str):
         assert mask == "causal"
         return MASK_CAUSAL, None
-    return MASK_ARRAY, C.byref(arr(mask))
+    return MASK_ARRAY, C.byref(_as_array(mask))
 
 
-def scaled_dot_product_attention(queries, keys, values, scale: float, mask=None, stream=None):
-    """MLXFast.scaledDotProductAttention (Source/MLX/MLXFast.swift:203-218)."""
+def scaled_dot_product_attention(queries, keys, values, scale: float, mask=None, stream=None,
+                                 out=None):
+    """MLXFast.scaledDotProductAttention (Source/MLX/MLXFast.swift:203-218).
+    keys, values and an array mask may be tensors or library-owned Arrays
+    (the views a cache returns); `out` may be given (nothing is allocated
+    then, as a captured HIP graph needs)."""
     torch = _torch()
     B, Hq, L, _ = queries.shape
-    out = torch.empty((B, Hq, L, values.shape[3]), dtype=queries.dtype, device=queries.device)
+    a_k, a_v = _as_array(keys), _as_array(values)
+    if out is None:
+        out = torch.empty((B, Hq, L, a_v.shape[3]), dtype=queries.dtype, device=queries.device)
     mode, m = _mask_args(mask)
     a_out = arr(out)
-    _chk(lib().vkv_sdpa(C.byref(arr(queries)), C.byref(arr(keys)), C.byref(arr(values)),
+    _chk(lib().vkv_sdpa(C.byref(arr(queries)), C.byref(a_k), C.byref(a_v),
                         C.c_float(scale), mode, m, C.byref(a_out), stream_ptr(stream)))
     return out
 
@@ -294,6 +308,10 @@ class _Cache:
         v = C.c_int64()
         _chk(lib().vkv_cache_offset(self._h, C.byref(v)))
         return v.value
+
+    @offset.setter
+    def offset(self, value: int):
+        _chk(lib().vkv_cache_set_offset(self._h, C.c_int64(value)))
 
     @property
     def max_size(self) -> Optional[int]:
@@ -400,6 +418,80 @@ class RotatingKVCache(_Cache):
 
     def __init__(self, max_size: int, keep: int = 0, step: int = 256):
         super().__init__(CacheParams(CACHE_ROTATING, step, max_size, keep, 0, 0))
+
+
+class _FixedBuffer(_Cache):
+    def inner_state(self):
+        """innerState: the fixed buffers and the int32 [1] device counters,
+        as library-owned arrays (write them in place only)."""
+        arrs = (Array * 4)()
+        n = C.c_int32()
+        _chk(lib().vkv_cache_inner_state(self._h, arrs, C.byref(n)))
+        return [arrs[i] for i in range(n.value)]
+
+
+def _wrap(cls, h):
+    new = object.__new__(cls)
+    _Cache.__init__(new, None, handle=h)
+    return new
+
+
+class CompilableKVCache(_FixedBuffer):
+    """CompilableKVCache (MLXLMCommon/CompilableKVCache.swift:40-262): fixed
+    [B, H, max_length, D] buffers, write offset in device memory; update
+    returns the whole buffers and make_mask an array mask built on the
+    device, so a decode step can be captured in a HIP graph."""
+
+    def __init__(self, max_length: int = 4096, step: int = 256):
+        super().__init__(CacheParams(CACHE_COMPILABLE, step, max_length, 0, 0, 0))
+
+    @classmethod
+    def from_cache(cls, cache, max_length: int = 4096):
+        """CompilableKVCache(from:maxLength:) (CompilableKVCache.swift:62-86)."""
+        h = C.c_void_p()
+        _chk(lib().vkv_cache_to_compilable(cache._h, C.c_int64(max_length), stream_ptr(),
+                                           C.byref(h)))
+        return _wrap(cls, h)
+
+
+class CompilableRotatingKVCache(_FixedBuffer):
+    """CompilableRotatingKVCache (BatchEngine/CompilableRotatingKVCache.swift:
+    1-265): a RotatingKVCache with maxSize buffers allocated once and its ring
+    index and offset in device memory."""
+
+    def __init__(self, max_size: int, keep: int = 0, step: int = 256):
+        super().__init__(CacheParams(CACHE_COMPILABLE_ROTATING, step, max_size, keep, 0, 0))
+
+    @classmethod
+    def from_rotating(cls, rotating):
+        """CompilableRotatingKVCache(from:) (CompilableRotatingKVCache.swift:91-150)."""
+        h = C.c_void_p()
+        _chk(lib().vkv_cache_to_compilable_rotating(rotating._h, stream_ptr(), C.byref(h)))
+        return _wrap(cls, h)
+
+
+def dynamic_slice_update(dst, update, start, axis: int, stream=None):
+    """dynamicSliceUpdate (MLXLMCommon/DynamicSlice.swift:50-71), in place:
+    dst[..., s + i, ...] = update[..., i, ...] along axis, with s the int32
+    in the device tensor `start` (clamped so the update fits)."""
+    a_d, a_u = arr(dst), arr(update)
+    _chk(lib().vkv_dynamic_slice_update(C.byref(a_d), C.byref(a_u), C.c_void_p(start.data_ptr()),
+                                        axis, stream_ptr(stream)))
+    return dst
+
+
+def dynamic_slice(src, start, axis: int, size: int, stream=None):
+    """dynamicSlice (MLXLMCommon/DynamicSlice.swift:21-48): src[..., s : s + size, ...]
+    along axis with s read from the device tensor `start`."""
+    torch = _torch()
+    ax = axis % src.dim()
+    shape = list(src.shape)
+    shape[ax] = size
+    out = torch.empty(shape, dtype=src.dtype, device=src.device)
+    a_s, a_o = arr(src), arr(out)
+    _chk(lib().vkv_dynamic_slice(C.byref(a_s), C.c_void_p(start.data_ptr()), axis, C.byref(a_o),
+                                 stream_ptr(stream)))
+    return out
 
 
 class QuantizedKVCache(_Cache):
