@@ -179,6 +179,20 @@ int vkv_paged_sdpa(const vkv_array *q, const vkv_paged_view *kv, float scale,
 int vkv_mla_decode(const vkv_array *q, const vkv_paged_view *kv, float scale,
                    vkv_array *out, void *stream);
 
+/* attentionWithCacheUpdate(queries:keys:values:cache:scale:mask:)
+ * (AttentionUtils.swift:77-143), one call: with cache == NULL, SDPA over
+ * keys/values; with a QuantizedKVCache, updateQuantized then quantized SDPA
+ * over the whole cache (the matrix-core decode kernel for one query token
+ * without a mask); with any other cache, update then SDPA over the returned
+ * keys/values, where a VKV_MASK_NONE mask is replaced by the cache's own
+ * array mask if makeMask(n:windowSize:nil:returnArray:true) gives one
+ * (called after the update, as the reference does).  q [B,Hq,L,D],
+ * keys/values [B,Hkv,L,D] (the new tokens), out [B,Hq,L,Dv]. */
+int vkv_attention_with_cache_update(const vkv_array *q, const vkv_array *keys,
+                                    const vkv_array *values, vkv_cache cache, float scale,
+                                    int32_t mask_mode, const vkv_array *mask, vkv_array *out,
+                                    void *stream);
+
 /* ------------------------------------------------------- per-layer caches */
 
 enum {

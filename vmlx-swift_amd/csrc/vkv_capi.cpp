@@ -158,7 +158,37 @@ int vkv_dequantize_affine(const vkv_array* wq, const vkv_array* scales, const vk
   });
 }
 
+}  // extern "C"
+
 // ---------------------------------------------------------------- attention
+
+namespace {
+// The attention mask arguments: none, causal, or a bool / additive f32
+// array broadcast to [B, Hq, L, T].
+void set_mask(AttnArgs& a, int32_t mask_mode, const vkv_array* mask, int64_t B, int64_t Hq,
+              int64_t L, int64_t T) {
+  if (mask_mode == VKV_MASK_CAUSAL) {
+    a.mask_mode = 1;
+  } else if (mask_mode == VKV_MASK_ARRAY) {
+    need(mask, "mask");
+    const int64_t target[4] = {B, Hq, L, T};
+    int64_t ms[4];
+    mask_strides(*mask, target, ms);
+    if (mask->dtype == VKV_BOOL || mask->dtype == VKV_U8) a.mask_mode = 2;
+    else if (mask->dtype == VKV_F32) a.mask_mode = 3;
+    else throw Error("mask must be bool or f32 (additive)");
+    a.mask = mask->data;
+    a.m_sb = ms[0];
+    a.m_sh = ms[1];
+    a.m_sl = ms[2];
+    a.m_st = ms[3];
+  } else if (mask_mode != VKV_MASK_NONE) {
+    throw Error("unknown mask mode");
+  }
+}
+}  // namespace
+
+extern "C" {
 
 int vkv_sdpa(const vkv_array* q, const vkv_array* k, const vkv_array* v, float scale,
              int32_t mask_mode, const vkv_array* mask, vkv_array* out, void* stream) {
@@ -201,24 +231,7 @@ int vkv_sdpa(const vkv_array* q, const vkv_array* k, const vkv_array* v, float s
     a.o_sb = out->strides[0];
     a.o_sh = out->strides[1];
     a.o_sl = out->strides[2];
-    if (mask_mode == VKV_MASK_CAUSAL) {
-      a.mask_mode = 1;
-    } else if (mask_mode == VKV_MASK_ARRAY) {
-      need(mask, "mask");
-      const int64_t target[4] = {B, Hq, L, T};
-      int64_t ms[4];
-      mask_strides(*mask, target, ms);
-      if (mask->dtype == VKV_BOOL || mask->dtype == VKV_U8) a.mask_mode = 2;
-      else if (mask->dtype == VKV_F32) a.mask_mode = 3;
-      else throw Error("mask must be bool or f32 (additive)");
-      a.mask = mask->data;
-      a.m_sb = ms[0];
-      a.m_sh = ms[1];
-      a.m_sl = ms[2];
-      a.m_st = ms[3];
-    } else if (mask_mode != VKV_MASK_NONE) {
-      throw Error("unknown mask mode");
-    }
+    set_mask(a, mask_mode, mask, B, Hq, L, T);
     run_attention(q->dtype, 0, 64, false, a, B * L, T, S(stream));
   });
 }
@@ -273,24 +286,7 @@ int vkv_quantized_sdpa(const vkv_array* q, const vkv_array* k_wq, const vkv_arra
     a.o_sb = out->strides[0];
     a.o_sh = out->strides[1];
     a.o_sl = out->strides[2];
-    if (mask_mode == VKV_MASK_CAUSAL) {
-      a.mask_mode = 1;
-    } else if (mask_mode == VKV_MASK_ARRAY) {
-      need(mask, "mask");
-      const int64_t target[4] = {B, Hq, L, T};
-      int64_t ms[4];
-      mask_strides(*mask, target, ms);
-      if (mask->dtype == VKV_BOOL || mask->dtype == VKV_U8) a.mask_mode = 2;
-      else if (mask->dtype == VKV_F32) a.mask_mode = 3;
-      else throw Error("mask must be bool or f32 (additive)");
-      a.mask = mask->data;
-      a.m_sb = ms[0];
-      a.m_sh = ms[1];
-      a.m_sl = ms[2];
-      a.m_st = ms[3];
-    } else if (mask_mode != VKV_MASK_NONE) {
-      throw Error("unknown mask mode");
-    }
+    set_mask(a, mask_mode, mask, B, Hq, L, T);
     run_attention(q->dtype, bits, group_size, true, a, B * L, T, S(stream));
   });
 }
@@ -373,6 +369,80 @@ int vkv_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vk
     a.o_sl = 0;
     run_attention(kv->dtype, kv->bits, kv->group_size, kv->bits > 0, a, kv->n_seqs, kv->max_len,
                   S(stream));
+  });
+}
+
+int vkv_attention_with_cache_update(const vkv_array* q, const vkv_array* keys, const vkv_array* values,
+                                    vkv_cache cache, float scale, int32_t mask_mode,
+                                    const vkv_array* mask, vkv_array* out, void* stream) {
+  return guard([&] {
+    need(q, "q");
+    need(keys, "keys");
+    need(values, "values");
+    need(out, "out");
+    auto call = [](int rc) {
+      if (rc != 0) throw Error(g_error);
+    };
+    if (!cache) {  // AttentionUtils.swift:85-93
+      call(vkv_sdpa(q, keys, values, scale, mask_mode, mask, out, stream));
+      return;
+    }
+    if (q->ndim != 4 || out->ndim != 4) throw Error("q and out must be 4-D");
+    if (cache->impl->kind() == VKV_CACHE_QUANTIZED) {  // :94-105
+      vkv_paged_view view{};
+      call(vkv_cache_update_quantized(cache, keys, values, stream, &view));
+      const int64_t B = q->shape[0], Hq = q->shape[1], L = q->shape[2];
+      if (q->dtype != view.dtype || out->dtype != view.dtype) throw Error("q/out dtype must match the cache");
+      if (q->shape[3] != view.head_dim || out->shape[0] != B || out->shape[1] != Hq ||
+          out->shape[2] != L || out->shape[3] != view.v_head_dim || B != view.n_seqs ||
+          Hq % view.n_kv_heads)
+        throw Error("q/out shapes do not match the cache");
+      if (L == 1 && mask_mode == VKV_MASK_NONE) {
+        // one decode token: the paged decode path over [B, Hq, D] views
+        vkv_array q3 = *q, o3 = *out;
+        q3.ndim = o3.ndim = 3;
+        q3.shape[2] = q->shape[3];
+        q3.strides[2] = q->strides[3];
+        o3.shape[2] = out->shape[3];
+        o3.strides[2] = out->strides[3];
+        call(vkv_paged_sdpa(&q3, &view, scale, &o3, stream));
+        return;
+      }
+      if (q->strides[3] != 1 || out->strides[3] != 1) throw Error("last dims must be contiguous");
+      AttnArgs a{};
+      a.q = q->data;
+      a.q_sb = q->strides[0];
+      a.q_sh = q->strides[1];
+      a.q_sl = q->strides[2];
+      a.L = static_cast<int32_t>(L);
+      a.Hq = static_cast<int32_t>(Hq);
+      a.Hkv = view.n_kv_heads;
+      a.D = view.head_dim;
+      a.Dv = view.v_head_dim;
+      a.scale = scale;
+      a.kv = kvsrc_from_view(view);
+      a.out = out->data;
+      a.o_sb = out->strides[0];
+      a.o_sh = out->strides[1];
+      a.o_sl = out->strides[2];
+      set_mask(a, mask_mode, mask, B, Hq, L, view.max_len);
+      run_attention(view.dtype, view.bits, view.group_size, true, a, B * L, view.max_len, S(stream));
+      return;
+    }
+    // :106-142: update, then the cache's array mask when none was given
+    vkv_array ck{}, cv{};
+    call(vkv_cache_update(cache, keys, values, stream, &ck, &cv));
+    int32_t mode = mask_mode;
+    const vkv_array* m = mask;
+    vkv_array cm{};
+    if (mask_mode == VKV_MASK_NONE) {
+      const int cmode = cache->impl->make_mask(static_cast<int>(q->shape[2]), 0, true, S(stream), &cm);
+      if (cmode == VKV_MASK_ARRAY) {
+        mode = VKV_MASK_ARRAY;
+        m = &cm;
+      }
+    }
+    call(vkv_sdpa(q, &ck, &cv, scale, mode, m, out, stream));
   });
 }
 

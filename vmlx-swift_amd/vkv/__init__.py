@@ -82,6 +82,7 @@ EXPORTS = (
     "vkv_kernel_timing", "vkv_kernel_timing_read", "vkv_fill_normal",
     "vkv_cache_to_compilable", "vkv_cache_to_compilable_rotating", "vkv_cache_inner_state",
     "vkv_dynamic_slice_update", "vkv_dynamic_slice", "vkv_cache_set_offset",
+    "vkv_attention_with_cache_update",
 )
 TIME_DECODE, TIME_MLA = 0, 1
 
@@ -215,6 +216,26 @@ def scaled_dot_product_attention(queries, keys, values, scale: float, mask=None,
     a_out = arr(out)
     _chk(lib().vkv_sdpa(C.byref(arr(queries)), C.byref(a_k), C.byref(a_v),
                         C.c_float(scale), mode, m, C.byref(a_out), stream_ptr(stream)))
+    return out
+
+
+def attention_with_cache_update(queries, keys, values, cache, scale: float, mask=None,
+                                stream=None, out=None):
+    """attentionWithCacheUpdate (MLXLMCommon/AttentionUtils.swift:77-143):
+    updates `cache` (None: no cache) with the new keys/values and attends the
+    queries [B, Hq, L, D] over the cached K/V; see
+    vkv_attention_with_cache_update for the routing."""
+    torch = _torch()
+    B, Hq, L, _ = queries.shape
+    if out is None:
+        dv = values.shape[3]
+        out = torch.empty((B, Hq, L, dv), dtype=queries.dtype, device=queries.device)
+    mode, m = _mask_args(mask)
+    a_out = arr(out)
+    _chk(lib().vkv_attention_with_cache_update(
+        C.byref(arr(queries)), C.byref(arr(keys)), C.byref(arr(values)),
+        cache._h if cache is not None else None, C.c_float(scale), mode, m, C.byref(a_out),
+        stream_ptr(stream)))
     return out
 
 
