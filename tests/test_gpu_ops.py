@@ -90,6 +90,46 @@ def test_sdpa_matches_oracle(dtype, shape):
     assert (np.abs(got - ref) <= attn_tol(dtype, ref)).all()
 
 
+@pytest.mark.parametrize("dtype", [O.BF16, O.F16, O.F32])
+@pytest.mark.parametrize("Hq,Hkv,D", [(16, 8, 256), (32, 8, 128), (12, 4, 64), (12, 1, 128), (8, 8, 64)])
+@pytest.mark.parametrize("mask", [None, "bool", "add"])
+def test_sdpa_decode_one_token(dtype, Hq, Hkv, D, mask, monkeypatch):
+    """One query token over dense K/V (the dense decode kernel): GQA 1 to 12
+    (head groups of up to 8), K/V as strided views of a longer buffer (a
+    cache's [.., cap, D] storage), lengths that end inside a 64-token step,
+    per-head bool masks with an empty row, additive masks; against the oracle
+    and against the generic kernel."""
+    rng = np.random.default_rng(Hq * 7 + D + dtype + (0 if mask is None else len(mask)))
+    B, T, cap = 3, 1000, 1100
+    q = rand_bits(rng, (B, Hq, 1, D), dtype)
+    kb = rand_bits(rng, (B, Hkv, cap, D), dtype)
+    vb = rand_bits(rng, (B, Hkv, cap, D), dtype)
+    k_dev, v_dev = dev(kb, dtype)[:, :, :T], dev(vb, dtype)[:, :, :T]
+    k, v = kb[:, :, :T], vb[:, :, :T]
+    if mask == "bool":
+        m = rng.random((B, Hq, 1, T)) > 0.3
+        m[1, 2, 0] = False  # fully masked row -> zeros
+        m_dev, m_ref = torch.from_numpy(m).cuda(), m
+    elif mask == "add":
+        m = (rng.standard_normal((1, T)) * 2).astype(np.float32)
+        m[0, :7] = -np.inf
+        m_dev, m_ref = torch.from_numpy(m).cuda(), m
+    else:
+        m_dev = m_ref = None
+    scale = D ** -0.5
+    out = vkv.scaled_dot_product_attention(dev(q, dtype), k_dev, v_dev, scale, mask=m_dev)
+    f = lambda a: O.to_f32(a, dtype) if dtype != O.F32 else a
+    ref = O.sdpa(f(q), f(k), f(v), scale, mask=m_ref)
+    got = values(out, dtype)
+    assert (np.abs(got - ref) <= attn_tol(dtype, ref)).all()
+    if mask == "bool":
+        assert (got[1, 2, 0] == 0).all()
+    monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
+    gen = values(vkv.scaled_dot_product_attention(dev(q, dtype), k_dev, v_dev, scale, mask=m_dev),
+                 dtype)
+    assert (np.abs(got - gen) <= attn_tol(dtype, ref)).all()
+
+
 @pytest.mark.parametrize("mask", ["causal", "bool", "add", "bool_empty_row"])
 def test_sdpa_masks(mask):
     dtype = O.BF16

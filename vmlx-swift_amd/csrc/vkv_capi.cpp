@@ -76,6 +76,17 @@ int32_t choose_parts(int64_t rows_x_heads, int64_t max_len, int32_t* part_tokens
 
 void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64_t rows,
                    int64_t max_len, hipStream_t st) {
+  if (fdecode_supported(dtype, bits, qsem, a) && !getenv("VKV_GENERIC_ATTENTION")) {
+    a.n_parts = fdecode_parts(rows * a.Hkv, max_len, &a.part_tokens);
+    if (a.n_parts > 1) {
+      const size_t per = static_cast<size_t>(rows) * a.Hq * a.n_parts;
+      float* ws = attention_workspace(st, per * (a.Dv + 2));
+      a.ws_o = ws;
+      a.ws_ml = ws + per * a.Dv;
+    }
+    launch_fdecode(dtype, a, rows, st);
+    return;
+  }
   a.n_parts = choose_parts(rows * a.Hkv, max_len, &a.part_tokens);
   if (a.n_parts > 1) {
     const size_t per = static_cast<size_t>(rows) * a.Hq * a.n_parts;

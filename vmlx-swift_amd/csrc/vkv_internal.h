@@ -130,6 +130,15 @@ void launch_fill_normal(int dtype, void* data, int64_t n, uint64_t seed, float s
                         hipStream_t st);
 void launch_attention(int dtype, int bits, int group, bool quant_semantics,
                       const AttnArgs& a, int64_t rows, hipStream_t st);
+// The split-K merge of launch_attention's partials (a.n_parts > 1).
+void launch_attn_combine(int dtype, const AttnArgs& a, int64_t rows, hipStream_t st);
+// One-token decode over dense float K/V (vkv_fdecode.hip): whether a call
+// qualifies (float, L = 1, dense, D = Dv in {64, 128, 256}, 16-byte aligned
+// rows), its token split (about 2048 waves, 64-token steps), and the launch
+// (with the merge when a.n_parts > 1).
+bool fdecode_supported(int dtype, int bits, bool qsem, const AttnArgs& a);
+int fdecode_parts(int64_t rows_x_heads, int64_t T, int32_t* part_tokens);
+void launch_fdecode(int dtype, const AttnArgs& a, int64_t rows, hipStream_t st);
 // MFMA decode attention over paged affine bf16 KV (vkv_decode.hip).
 struct DecodeArgs {
   const uint16_t* q;         // [n_seqs][Hq][D] bf16

@@ -1041,6 +1041,17 @@ static void attn_dispatch(int bits, bool qsem, const AttnArgs& a, int64_t rows, 
   }
 }
 
+void launch_attn_combine(int dtype, const AttnArgs& a, int64_t rows, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(rows * a.Hq));
+  switch (dtype) {
+    case kF32: hipLaunchKernelGGL((attn_combine_kernel<kF32>), grid, dim3(256), 0, st, a); break;
+    case kF16: hipLaunchKernelGGL((attn_combine_kernel<kF16>), grid, dim3(256), 0, st, a); break;
+    case kBF16: hipLaunchKernelGGL((attn_combine_kernel<kBF16>), grid, dim3(256), 0, st, a); break;
+    default: throw Error("unsupported dtype");
+  }
+  VKV_HIP(hipGetLastError());
+}
+
 void launch_attention(int dtype, int bits, int group, bool quant_semantics,
                       const AttnArgs& a, int64_t rows, hipStream_t st) {
   if (rows <= 0) return;
