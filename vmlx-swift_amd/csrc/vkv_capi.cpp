@@ -482,8 +482,12 @@ int vkv_mla_decode(const vkv_array* q, const vkv_paged_view* kv, float scale, vk
       if (vkv_paged_sdpa(q, kv, scale, out, stream) != 0) throw Error(vkv_last_error());
       return;
     }
-    // matrix-core path (vkv_mla.hip)
     KVSrc src = kvsrc_from_view(*kv);
+    if (!mla_layout_supported(src.base, src.block_bytes, src.sb_off)) {
+      if (vkv_paged_sdpa(q, kv, scale, out, stream) != 0) throw Error(vkv_last_error());
+      return;
+    }
+    // matrix-core path (vkv_mla.hip)
     MlaArgs m{};
     m.q = static_cast<const uint16_t*>(q->data);
     m.q_ss = q->strides[0];

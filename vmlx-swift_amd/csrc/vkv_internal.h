@@ -199,6 +199,8 @@ bool mla_supported(int dtype, int bits, int group, int head_dim, int v_head_dim,
                    int block_size);
 // Token splits for a launch (want > 0 overrides); sets a.n_splits and
 // a.split_len and returns the workspace floats the launch needs.
+// The chunk geometry the kernel's 16-byte raw-tile loads need.
+bool mla_layout_supported(const uint8_t* base, int64_t block_bytes, int64_t sb_off);
 size_t mla_plan(MlaArgs& a, int want);
 void launch_mla(const MlaArgs& a, hipStream_t st);
 

@@ -13,37 +13,41 @@
 // probabilities enter the second contraction as bf16.
 //
 // Work layout.  A workgroup of 4 waves (one per SIMD) owns one (sequence,
-// token split, group of 64*HB query heads); per 32-token tile:
-//   * every thread loads 9 (token, 8-dim) pieces of raw codes and their
-//     scale/bias straight into registers one tile ahead, and dequantizes
-//     them into a bf16 [32][576] LDS key tile (double buffered);
-//   * wave w computes the scores of its 16*HB heads, S^T = K Q^T, with
-//     16x16x32 bf16 MFMAs (A = key rows from LDS, B = its queries, held in
-//     registers), so lane l holds head l % 16 for tokens 4*(l/16) + i and
-//     16 + 4*(l/16) + i; softmax against a fixed running max; the
-//     probabilities of all heads meet in an LDS tile;
-//   * wave w then accumulates output dims [128w, 128w + 128) of every head
-//     of the group: A = probabilities from LDS, B = the key tile read with
-//     the transposing LDS load ds_read_b64_tr_b16 (within each 16-lane
-//     group, lane i receives element i % 4 of the 8 bytes that lane
-//     4*e + i / 4 addressed, so pointing those lanes at 4 consecutive dims
-//     of tokens Tb + e hands lane i dim i of tokens Tb .. Tb + 3 -- exactly
-//     the tokens the probability operand pairs it with), while the next
-//     tile is dequantized.
-// Each key element is read from LDS once per wave for the scores and once
-// per workgroup for the values, which keeps the LDS below the matrix cores'
-// rate.  Split partials (o / l in bf16, running max, sum) are merged by
+// token split, group of 128 query heads) and walks the split 32 tokens at
+// a time, all contractions on v_mfma_f32_32x32x16_bf16:
+//   * raw tiles (codes and scale/bias of 32 entries, 19584 contiguous
+//     bytes of a page) go from HBM straight into LDS with
+//     global_load_lds_dwordx4, three tiles ahead, so no registers hold them;
+//   * each thread dequantizes 9 (entry, 8-dim) pieces of the next tile from
+//     the raw stage into a bf16 key tile (double buffered), spread over the
+//     matrix-core work of the current tile;
+//   * scores: wave w computes S^T = K Q^T for heads 32w..32w+31 (A = key
+//     rows from LDS, B = the queries: 32 of 36 16-dim chunks in registers,
+//     the rope chunks in LDS); lane l then holds head l % 32 for tokens
+//     8 (j / 4) + 4 (l / 32) + j % 4, j = 0..15;
+//   * softmax against a fixed running max; those 16 probabilities are, in
+//     that order, the wave's own A operands of the P.V contraction (k-step
+//     ks = tokens 16 ks .. 16 ks + 15, lane l / 32 picking tokens
+//     {0-3, 8-11} or {4-7, 12-15} of it), so the wave starts P.V on its own
+//     heads from registers while the other waves' probabilities meet in an
+//     LDS tile;
+//   * P.V: wave w accumulates output dims 128w..128w+127 of all 128 heads
+//     (256 fp32 accumulators); B = values read with the transposing LDS
+//     load ds_read_b64_tr_b16 (within 16 lanes, lane i receives element
+//     i % 4 of the 8 bytes lane 4e + i / 4 addressed: pointing those lanes
+//     at 4 consecutive dims of token T + e hands lane i dim i of tokens
+//     T .. T + 3, the tokens its probability operand pairs it with).
+// Split partials (o / l in bf16, running max, sum) are merged by
 // mla_combine_kernel as sdpa_vector_2pass_2 merges them
 // (Source/Cmlx/mlx-generated/metal/sdpa_vector.h:320-394).
 //
-// LDS key tile layout.  Row t (token) holds the 72 8-dim pieces in the
-// chunk format's storage order (piece q at position p = (q % 4) * 18 +
-// q / 4, i.e. run p / 18 = q % 4, index p % 18 = q / 4), 16 bytes each, at
-// slot 24 * (p / 18) + p % 18 + (t % 16) of a 112-slot (1792-byte) row.
-// The score operand (16 rows, one position) and the transposing reads (8
-// rows, two pieces one run apart) land on distinct banks; the dequant
-// stores (tokens t and t + 8, 8 adjacent positions) do too except where
-// the 8 positions cross a run.
+// LDS key tile: row t (entry) = 72 16-byte pieces (piece q = dims 8q..8q+7)
+// at slot q ^ kswz(t), kswz(t) = 4 t1 ^ t2 ^ 2 t3 (t_b = bit b of t), rows
+// 1152 bytes apart.  The score operand reads (32 rows, two adjacent
+// pieces), the transposing value reads (4 rows x 32 bytes per 16 lanes) and
+// the dequant stores (2 rows x 8 pieces per 16 lanes) each touch 16
+// distinct bank quads per 256 bytes (checked on the CPU against a 64-bank
+// model).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -56,9 +60,6 @@
 
 #include "vkv_internal.h"
 
-// Scale/bias row of zeros, read in place of the rows of tokens past the end.
-__device__ uint32_t vkv_mla_zero_sb[16];
-
 namespace vkv {
 namespace {
 
@@ -66,48 +67,49 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;
-typedef __attribute__((address_space(1))) const u32x2_t g_u32x2_t;
-typedef __attribute__((address_space(1))) const uint32_t g_u32_t;
-typedef __attribute__((address_space(3))) i16x4_t l_i16x4_t;
 
-constexpr int kDK = 576;                  // entry dims (latent + rope)
-constexpr int kDV = 512;                  // value dims
-constexpr int kTile = 32;                 // tokens per tile
-constexpr int kPos = kDK / 8;             // 8-dim pieces per entry
-constexpr int kRowB = 112 * 16;           // bytes per LDS key row (112 slots)
-constexpr int kChunks = kDK / 32;         // K steps of the score MFMA
-constexpr int kDW = kDV / 4;              // output dims per wave
-constexpr int kDBW = kDW / 16;            // 16-dim output tiles per wave
-constexpr int kPRow = 40;                 // bf16 per probability row (32 + pad)
-constexpr int kSbRow = (kDK / 64) * 4;    // (scale, bias) bytes per token
-constexpr int kPieces = kTile * kPos / 256;  // dequant pieces per thread
-constexpr int kQReg = 16;                 // query chunks held in registers (rest in LDS)
-constexpr int kQL = kChunks - kQReg;      // query chunks read from LDS
+constexpr int kDK = 576;                   // entry dims (latent + rope)
+constexpr int kDV = 512;                   // value dims
+constexpr int kTile = 32;                  // tokens per tile
+constexpr int kHeads = 128;                // query heads per workgroup (32 per wave)
+constexpr int kChunks = kDK / 16;          // K steps of the score MFMA
+constexpr int kQReg = kDV / 16;            // query chunks held in registers
+constexpr int kKRow = kDK * 2;             // bytes per key-tile row
+constexpr int kKTile = kTile * kKRow;      // bytes per key tile
+constexpr int kSbRow = (kDK / 64) * 4;     // (scale, bias) bytes per entry
+constexpr int kRawCodes = kTile * kDK;     // code bytes per raw tile
+constexpr int kRawTile = kRawCodes + kTile * kSbRow;  // bytes per raw tile
+constexpr int kStages = 3;                 // raw tiles in flight
+constexpr int kDmaPerWave = 5;             // 16-byte-per-lane loads per wave per tile
+constexpr int kPRow = 80;                  // bytes per head row of the probability tile
+constexpr int kQRow = 144;                 // bytes per head row of the rope queries
+constexpr int kPieces = 9;                 // dequant pieces per thread per tile
+constexpr int kDqQK = 6;                   // of them during the scores, the rest during P.V
+constexpr int kKaAhead = 4;                // score operand reads issued this many steps ahead
+constexpr int kKaRing = kKaAhead + 1;
 constexpr int kMaxSplits = 64;
 constexpr float kTau = 64.0f;    // headroom of the fixed running max (log2)
 constexpr float kLog2e = 1.4426950408889634f;
 
-static_assert(kPieces == 9, "piece mapping assumes 9 x 8 dims per thread");
+// LDS block layout (bytes)
+constexpr int kLdsRaw = 0;
+constexpr int kLdsKt = kLdsRaw + kStages * kRawTile;
+constexpr int kLdsP = kLdsKt + 2 * kKTile;
+constexpr int kLdsQ = kLdsP + kHeads * kPRow;
+constexpr int kLdsL = kLdsQ + kHeads * kQRow;
+constexpr int kLdsFlag = kLdsL + kHeads * 4;
+constexpr int kLdsBytes = kLdsFlag + 16;
+static_assert(kLdsKt <= 65536, "raw stages below 64 KB");
+static_assert(kLdsBytes <= 160 * 1024, "LDS of one workgroup");
 
-// Storage position p of a token row holds dims 8q..8q+7 with
-// q = 4 * (p % 18) + p / 18; their scale/bias group is q / 8.
-constexpr int pos_group(int p) { return (4 * (p % 18) + p / 18) / 8; }
-// Piece k of a thread covers positions 8k + pb, pb = 0..7: 4-bit fields of
-// the group and 2-bit fields of the run p / 18, indexed by pb.
-constexpr uint32_t piece_groups(int k) {
-  uint32_t v = 0;
-  for (int pb = 0; pb < 8; pb++) v |= static_cast<uint32_t>(pos_group(8 * k + pb)) << (4 * pb);
-  return v;
-}
-constexpr uint32_t piece_runs(int k) {
-  uint32_t v = 0;
-  for (int pb = 0; pb < 8; pb++) v |= static_cast<uint32_t>((8 * k + pb) / 18) << (2 * pb);
-  return v;
-}
+static_assert(kRawTile % 16 == 0 && (kRawTile + 1023) / 1024 == 4 * kDmaPerWave,
+              "a raw tile is 20 wave-wide 16-byte loads");
+static_assert(kTile * (kDK / 8) == 256 * kPieces, "9 pieces per thread");
 
 template <int... Is, class F>
 __device__ __forceinline__ void sfor_impl(std::integer_sequence<int, Is...>, F&& f) {
@@ -118,15 +120,37 @@ __device__ __forceinline__ void sfor(F&& f) {
   sfor_impl(std::make_integer_sequence<int, N>{}, f);
 }
 
-__device__ __forceinline__ f32x4_t mfma(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+__device__ __forceinline__ f32x16_t mfma(const u32x4_t& a, const u32x4_t& b, const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// The score contraction's accumulator lives in VGPRs (the 256 AGPRs hold
+// the P.V accumulators), which the compiler's MFMA selection does not do on
+// its own here, so the score MFMAs are written out: the first with a zero
+// accumulator, the rest accumulating in place (back-to-back dependent
+// accumulation needs no wait states), and mfma_result_fence pads the wait
+// states an XDL result needs before a VALU instruction reads it (at most 19
+// for a 16-pass op; 24 here).
+__device__ __forceinline__ void mfma_v_first(f32x16_t& c, const u32x4_t& a, const u32x4_t& b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_v(f32x16_t& c, const u32x4_t& a, const u32x4_t& b) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_result_fence(f32x16_t& c) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(c));
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+
+// Key-tile slot swizzle of row t.
+__device__ __forceinline__ int kswz(int t) {
+  return (((t >> 1) & 1) << 2) ^ ((t >> 2) & 1) ^ (((t >> 3) & 1) << 1);
 }
 
 // LDS byte address of a __shared__ object.
@@ -140,311 +164,419 @@ template <class T>
 __device__ __forceinline__ __attribute__((address_space(3))) T* lds_ptr(uint32_t a) {
   return reinterpret_cast<__attribute__((address_space(3))) T*>(static_cast<uintptr_t>(a));
 }
-// A uniform 32-bit word through the scalar path (a vector load would make
-// the compiler wait for every load in flight before using it).
+// A uniform 32-bit word through the scalar path.
 __device__ __forceinline__ int32_t scalar_load(const int32_t* p, int64_t i) {
   return *(reinterpret_cast<const __attribute__((address_space(4))) int32_t*>(
                reinterpret_cast<uintptr_t>(p)) +
            i);
 }
 
-template <int HB>
+// 16 bytes per lane from base + voff to LDS lds + 16 * lane (the wave's
+// lanes fill lds .. lds + 1023 in lane order).  Issued as inline assembly
+// so the compiler neither waits for these loads at every LDS access nor at
+// every barrier: the kernel waits for them itself (vmcnt) before the
+// barrier that publishes a raw tile.
+__device__ __forceinline__ void dma16(const uint8_t* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, %2" ::"v"(voff), "s"(lds),
+               "s"(base)
+               : "memory", "m0");
+}
+// Workgroup barrier for LDS data (LDS ops complete first).  The raw-tile
+// loads are waited for separately with raw_wait.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+// At most one tile's raw loads (kDmaPerWave) still in flight.
+__device__ __forceinline__ void raw_wait_one_tile() {
+  asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+}
+__device__ __forceinline__ void raw_wait_two_tiles() {
+  asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+}
+static_assert(kDmaPerWave == 5, "raw_wait_* count 5 loads per tile");
+// Keeps memory operations on their side of this point, in the compiler's
+// passes and its scheduler, so the interleaving of operand reads, dequant
+// and matrix-core steps written below is the one issued.
+__device__ __forceinline__ void step_fence() { asm volatile("" ::: "memory"); }
+
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 mla_kernel(const MlaArgs a) {
-  constexpr int kHeads = 64 * HB;     // query heads of the workgroup
-  constexpr int kHB = kHeads / 16;    // their 16-head blocks
-  __shared__ __attribute__((aligned(16))) uint8_t kt[2][kTile * kRowB];
-  __shared__ __attribute__((aligned(16))) uint16_t pl[kHeads][kPRow];
-  __shared__ __attribute__((aligned(16))) float lsh[kHeads];
-  __shared__ __attribute__((aligned(16))) int restart_flag[4];
-  // query chunks kQReg.. of every head: [chunk][head][32 dims + 8 pad]
-  __shared__ __attribute__((aligned(16))) uint16_t qsh[kQL > 0 ? kQL : 1][kHeads][40];
+  // One LDS block, raw stages first: the raw-tile loads address LDS through
+  // M0, and keeping their destinations below 64 KB does not depend on how
+  // many M0 bits the load honours.
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+  uint8_t(*raw)[kRawTile] = reinterpret_cast<uint8_t(*)[kRawTile]>(lds + kLdsRaw);
+  uint8_t(*kt)[kKTile] = reinterpret_cast<uint8_t(*)[kKTile]>(lds + kLdsKt);
+  uint8_t* pt = lds + kLdsP;
+  uint8_t* qr = lds + kLdsQ;
+  float* lsh = reinterpret_cast<float*>(lds + kLdsL);
+  int* restart_flag = reinterpret_cast<int*>(lds + kLdsFlag);
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = tid & 63, n = lane & 15, g = lane >> 4;
+  const int lane = tid & 63, l32 = lane & 31, kg = lane >> 5;
   const int split = blockIdx.x, b = blockIdx.y;
   const int len = a.seq_lens ? scalar_load(a.seq_lens, b) : a.max_len;
   const int t0 = split * a.split_len;
   const int t1 = min(len, t0 + a.split_len);
   const int ntiles = t1 > t0 ? (t1 - t0 + kTile - 1) / kTile : 0;
   const int hg0 = blockIdx.z * kHeads;        // first head of the workgroup
-  const int hw = hg0 + wave * (16 * HB);      // first head this wave scores
+  const int hw = hg0 + 32 * wave;             // first head this wave scores
   const size_t slot = static_cast<size_t>(b) * a.n_splits + split;
 
   if (ntiles == 0) {
-    if (a.n_splits == 1) {
-      // an empty sequence yields zeros
-      for (int hb = 0; hb < HB; hb++) {
-        const int h = hw + 16 * hb + n;
-        if (h < a.H)
-          for (int d = g; d < kDV; d += 4) a.out[b * a.o_ss + h * a.o_sh + d] = 0;
-      }
-    } else if (g == 0) {
-      for (int hb = 0; hb < HB; hb++) {
-        const int h = hw + 16 * hb + n;
-        if (h < a.H) {
-          a.ws_ml[(slot * a.H + h) * 2] = -INFINITY;
-          a.ws_ml[(slot * a.H + h) * 2 + 1] = 0.0f;
-        }
+    const int h = hw + l32;
+    if (h < a.H) {
+      if (a.n_splits == 1) {
+        // an empty sequence yields zeros
+        for (int d = kg; d < kDV; d += 2) a.out[b * a.o_ss + h * a.o_sh + d] = 0;
+      } else if (kg == 0) {
+        a.ws_ml[(slot * a.H + h) * 2] = -INFINITY;
+        a.ws_ml[(slot * a.H + h) * 2 + 1] = 0.0f;
       }
     }
     return;
   }
 
-  // ---- raw pieces of this thread: token tk, storage positions 8k + pb
-  // (k = 0..8).  A 16-lane group covers tokens t and t + 8 x 8 adjacent
-  // positions (64 contiguous bytes of each token row).  The loads go to
-  // registers one tile ahead; tokens past the end read the zero
-  // scale/bias row, so they dequantize to zeros.  ob is an opaque zero
-  // (one per tile) that keeps the per-piece offsets from being hoisted out
-  // of the tile loop into registers.
-  const int l16 = tid & 15, pb = l16 & 7, grp = tid >> 4;
-  const int tk = (grp & 7) + 16 * (grp >> 3) + 8 * (l16 >> 3);
-  struct Raw {
-    u32x2_t c[kPieces];
-    uint32_t sb[kPieces];
-  };
-  auto load_raw_piece = [&](int i, int ob, int k, Raw& r) __attribute__((always_inline)) {
-    const int ts = t0 + kTile * min(i, ntiles - 1);
-    const int blk = ts / a.block_size, off = ts - blk * a.block_size;
-    const uint8_t* chunk =
-        a.base + static_cast<int64_t>(scalar_load(a.table, static_cast<int64_t>(b) * a.table_stride +
-                                                                blk)) *
-                     a.block_bytes;
-    const int pbo = pb + ob;
-    const uint8_t* cp = chunk + (off + tk) * kDK + 8 * pbo;
-    const bool valid = t0 + kTile * i + tk < t1;
-    const uint8_t* sp = valid ? chunk + a.sb_off + (off + tk) * kSbRow
-                              : reinterpret_cast<const uint8_t*>(vkv_mla_zero_sb);
-    r.c[k] = *(const g_u32x2_t*)(cp + 64 * k);
-    r.sb[k] = *(const g_u32_t*)(sp + 4 * ((piece_groups(k) >> (4 * pbo)) & 15));
-  };
-  auto dequant_piece = [&](const Raw& r, int i, int ob, int k) __attribute__((always_inline)) {
-    const int pbo = pb + ob;
-    uint8_t* dst = &kt[i & 1][tk * kRowB + 16 * (pbo + (tk & 15))];
-    const uint32_t sbw = r.sb[k];
-    const float s = __uint_as_float(sbw << 16), bb = __uint_as_float(sbw & 0xFFFF0000u);
-    u32x4_t w;
+  // ---- queries: chunk c (dims 16c + 8 kg .. +8) of head hw + l32 is the B
+  // operand of score step c; chunks 32..35 (rope dims) go to LDS.
+  u32x4_t qf[kQReg];
+  {
+    const int h = min(hw + l32, a.H - 1);
+    const uint16_t* qp = a.q + b * a.q_ss + static_cast<int64_t>(h) * a.q_sh + 8 * kg;
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const uint32_t x = r.c[k][h];
-      w[2 * h] = pack_bf16(fmaf(s, static_cast<float>(x & 0xFF), bb),
-                           fmaf(s, static_cast<float>((x >> 8) & 0xFF), bb));
-      w[2 * h + 1] = pack_bf16(fmaf(s, static_cast<float>((x >> 16) & 0xFF), bb),
-                               fmaf(s, static_cast<float>(x >> 24), bb));
-    }
-    // slot p + 6 * (p / 18) + (tk % 16), p = 8k + pb
-    *reinterpret_cast<u32x4_t*>(dst + 128 * k + 96 * ((piece_runs(k) >> (2 * pbo)) & 3)) = w;
-  };
-
-  // ---- queries (B operand of the score MFMA): head hw + 16 hb + n,
-  // dims 32 c + 8 g .. +8
-  u32x4_t qf[HB][kQReg];
-#pragma unroll
-  for (int hb = 0; hb < HB; hb++) {
-    const int h = min(hw + 16 * hb + n, a.H - 1);
-    const uint16_t* qp = a.q + b * a.q_ss + static_cast<int64_t>(h) * a.q_sh + 8 * g;
-#pragma unroll
-    for (int c = 0; c < kQReg; c++) qf[hb][c] = *(const g_u32x4_t*)(qp + 32 * c);
+    for (int c = 0; c < kQReg; c++) qf[c] = *(const g_u32x4_t*)(qp + 16 * c);
 #pragma unroll
     for (int c = kQReg; c < kChunks; c++)
-      *reinterpret_cast<u32x4_t*>(&qsh[c - kQReg][wave * 16 * HB + 16 * hb + n][8 * g]) =
-          *(const g_u32x4_t*)(qp + 32 * c);
+      *reinterpret_cast<u32x4_t*>(&qr[(32 * wave + l32) * kQRow + 32 * (c - kQReg) + 16 * kg]) =
+          *(const g_u32x4_t*)(qp + 16 * c);
   }
+  // the query loads complete here, before the raw-tile loads start (a
+  // compiler-inserted wait for them inside the tile loop would also wait
+  // for every raw load in flight)
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   const float cl = a.scale * kLog2e;
 
-  f32x4_t o[kHB][kDBW];  // output rows (heads) 16 hb' + 4g + e, dims 128 wave + 16 db' + n
-  float m_run[HB], l_run[HB], m_est[HB];
+  // ---- per-lane LDS addresses (the tile buffer and step parts are
+  // immediate offsets).  They are recomputed in every tile from an opaque
+  // copy of the thread index (a few VALU per tile): kept live across the
+  // tile loop they do not fit beside the queries, and the compiler would
+  // spill them to scratch, whose reloads wait for every raw-tile load in
+  // flight.
+  struct LaneAddr {
+    uint32_t ka[4];      // score A operand, step c: row l32, piece 2c + kg at
+                         // slot 8 (c / 4) + ((2 (c % 4) + kg) ^ kswz(l32))
+    uint32_t vb[2][2];   // value B operand [db % 2][token half]
+    uint32_t p, qr;      // probability tile / rope queries
+    uint32_t dq_code, dq_sb, dq_dst;
+    int dt;
+  };
+  auto lane_addr = [&]() __attribute__((always_inline)) -> LaneAddr {
+    int t = tid;
+    asm volatile("" : "+v"(t));
+    const int ln = t & 63, l2 = ln & 31, g2 = ln >> 5;
+    LaneAddr r;
 #pragma unroll
-  for (int hb = 0; hb < HB; hb++) m_est[hb] = -INFINITY;
-
-  // ---- scores S^T [32 tokens x 16*HB heads] of tile i.  Piece position
-  // 18g + c (dims 32c + 8g..) of row t sits at slot 24g + c + (t % 16).
-  f32x4_t s[2][HB];
-  auto qk = [&](int i, int ob, Raw& r) __attribute__((always_inline)) {
-    const uint32_t k0 =
-        lds_addr(&kt[i & 1][0]) + n * kRowB + 16 * (24 * g + n) + ob;
+    for (int m = 0; m < 4; m++)
+      r.ka[m] = lds_addr(&kt[0][0]) + l2 * kKRow + 16 * ((2 * m + g2) ^ kswz(l2));
+    // value B operand (dim block db, k-step ks, token half hf): lane
+    // 16 a4 + 4 e + jj reads token 16 ks + 8 hf + 4 (a4 / 2) + e, dims
+    // 128 wave + 32 db + 16 (a4 % 2) + 4 jj .. +4
+    const int a4 = ln >> 4, e = (ln >> 2) & 3, jj = ln & 3;
 #pragma unroll
-    for (int tb = 0; tb < 2; tb++)
+    for (int u = 0; u < 2; u++)
 #pragma unroll
-      for (int hb = 0; hb < HB; hb++) s[tb][hb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    u32x4_t ka[2][2];
-    ka[0][0] = *lds_ptr<const u32x4_t>(k0);
-    ka[0][1] = *lds_ptr<const u32x4_t>(k0 + 16 * kRowB);
-    sfor<kChunks>([&](auto C) {
-      constexpr int c = decltype(C)::value;
-      if constexpr (c + 1 < kChunks) {
-        ka[(c + 1) & 1][0] = *lds_ptr<const u32x4_t>(k0 + 16 * (c + 1));
-        ka[(c + 1) & 1][1] = *lds_ptr<const u32x4_t>(k0 + 16 * kRowB + 16 * (c + 1));
-      }
-      // tile i+1's dequant (from registers), each piece followed by tile
-      // i+2's load into the registers it frees: one piece every other step
-      if constexpr (c % 2 == 1) {
-        dequant_piece(r, i + 1, ob, c / 2);
-        load_raw_piece(i + 2, ob, c / 2, r);
-      }
-#pragma unroll
-      for (int hb = 0; hb < HB; hb++) {
-        u32x4_t qb;
-        if constexpr (c < kQReg)
-          qb = qf[hb][c];
-        else
-          qb = *reinterpret_cast<const u32x4_t*>(
-              &qsh[c - kQReg][wave * 16 * HB + 16 * hb + n][8 * g + ob]);
-        s[0][hb] = mfma(ka[c & 1][0], qb, s[0][hb]);
-        s[1][hb] = mfma(ka[c & 1][1], qb, s[1][hb]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    });
+      for (int hf = 0; hf < 2; hf++)
+        r.vb[u][hf] = lds_addr(&kt[0][0]) + (8 * hf + 4 * (a4 >> 1) + e) * kKRow +
+                      16 * (16 * wave + 4 * (u ^ (e >> 1)) + 2 * ((a4 & 1) ^ hf) +
+                            ((jj >> 1) ^ (a4 >> 1))) +
+                      8 * (jj & 1);
+    // probability tile: head row h at h * kPRow, k-step ks at +32 ks, lane
+    // half kg at +16 kg (8 bf16 = 8 tokens)
+    r.p = lds_addr(&pt[0]) + l2 * kPRow + 16 * g2;
+    r.qr = lds_addr(&qr[0]) + (32 * wave + l2) * kQRow + 16 * g2;
+    // dequant: thread (entry dt, piece column dj) takes pieces q = 8k + dj
+    // (group k).  The chunk format stores piece q of a row at position
+    // 18 (q % 4) + q / 4 (qk_word_off), here 18 (dj % 4) + dj / 4 + 2k.
+    r.dt = t >> 3;
+    const int dj = t & 7;
+    r.dq_code = lds_addr(&raw[0][0]) + r.dt * kDK + 8 * (18 * (dj & 3) + (dj >> 2));
+    r.dq_sb = lds_addr(&raw[0][0]) + kRawCodes + r.dt * kSbRow;
+    r.dq_dst = lds_addr(&kt[0][0]) + r.dt * kKRow + 16 * (dj ^ kswz(r.dt));
+    return r;
   };
 
-  // ---- softmax of tile i against the fixed running max: mask the tokens
-  // past the end (last tile only), check the scores, write the
-  // probabilities (bf16, the P.V operand layout: head row, tokens 4g..4g+3
-  // then 16+4g..16+4g+3) to the workgroup's probability tile.  Returns
-  // true when the split must be run again.
-  auto softmax = [&](int i, int ob) __attribute__((always_inline)) -> bool {
-    const int rem = t1 - (t0 + kTile * i);
-    if (rem < kTile) {
-      asm volatile("");  // keep this a branch: the mask is for one tile in many
-      const int r4 = rem - 4 * g - ob;
+  // ---- raw tile i (clamped to the last tile, so every wave issues the
+  // same number of loads per tile) -> raw stage s: wave w issues the
+  // 1024-byte pieces w, w + 4, .., w + 16 of the 20 (18 of codes, 2 of
+  // scale/bias; the last holds 128 bytes)
+  // page-table entry of tile i (clamped), read through the scalar path one
+  // tile before its loads are issued
+  auto table_entry = [&](int i) __attribute__((always_inline)) -> int32_t {
+    const int ts = t0 + kTile * min(i, ntiles - 1);
+    return scalar_load(a.table, static_cast<int64_t>(b) * a.table_stride + ts / a.block_size);
+  };
+  auto dma_tile = [&](int i, int s, int32_t entry) __attribute__((always_inline)) {
+    const int ts = t0 + kTile * min(i, ntiles - 1);
+    const int off = ts % a.block_size;
+    const uint8_t* chunk = a.base + static_cast<int64_t>(entry) * a.block_bytes;
+    const uint8_t* codes = chunk + off * kDK;
+    const uint8_t* sbs = chunk + a.sb_off + off * kSbRow;
+    const uint32_t dst = lds_addr(&raw[0][0]) + s * kRawTile;
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const uint32_t dma_voff = 16 * ln;
+    // pieces wave + 4n, n < 4, are codes; the fifth is code piece 16 or 17
+    // (waves 0, 1) or the scale/bias piece 18 or 19 (waves 2, 3)
 #pragma unroll
-      for (int tb = 0; tb < 2; tb++)
-#pragma unroll
-        for (int hb = 0; hb < HB; hb++)
-#pragma unroll
-          for (int e = 0; e < 4; e++)
-            if (16 * tb + e >= r4) s[tb][hb][e] = -INFINITY;
+    for (int n = 0; n < kDmaPerWave - 1; n++)
+      dma16(codes + 1024 * (wave + 4 * n), dma_voff, dst + 1024 * (wave + 4 * n));
+    if (wave < 2) {
+      dma16(codes + 1024 * (16 + wave), dma_voff, dst + 1024 * (16 + wave));
+    } else if (wave == 2) {
+      dma16(sbs, dma_voff, dst + kRawCodes);
+    } else if (lane < 8) {
+      dma16(sbs + 1024, dma_voff, dst + kRawCodes + 1024);
     }
-    float mloc[HB];
-    bool need = false;
-#pragma unroll
-    for (int hb = 0; hb < HB; hb++) {
-      // scale > 0, so the largest score maps to the largest logit
-      mloc[hb] = fmaxf(fmaxf(fmaxf(s[0][hb][0], s[0][hb][1]), fmaxf(s[0][hb][2], s[0][hb][3])),
-                       fmaxf(fmaxf(s[1][hb][0], s[1][hb][1]), fmaxf(s[1][hb][2], s[1][hb][3]))) *
-                 cl;
-      need |= mloc[hb] > m_run[hb] + kTau;
-    }
-    bool redo = false;
-    if (__builtin_amdgcn_ballot_w64(need)) {
-#pragma unroll
-      for (int hb = 0; hb < HB; hb++) {
-        float mx = mloc[hb];
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        m_est[hb] = fmaxf(m_est[hb], mx);
-      }
-      if (i == 0) {
-        // nothing accumulated yet: take the max as is
-#pragma unroll
-        for (int hb = 0; hb < HB; hb++) m_run[hb] = m_est[hb];
-      } else {
-        redo = true;
-      }
-    }
-#pragma unroll
-    for (int hb = 0; hb < HB; hb++) {
-      float p[2][4];
-#pragma unroll
-      for (int tb = 0; tb < 2; tb++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          p[tb][e] = fast_exp2(fmaf(s[tb][hb][e], cl, -m_run[hb]));
-          l_run[hb] += p[tb][e];
-        }
-      *reinterpret_cast<u32x4_t*>(&pl[wave * 16 * HB + 16 * hb + n][8 * g + ob]) =
-          u32x4_t{pack_bf16(p[0][0], p[0][1]), pack_bf16(p[0][2], p[0][3]),
-                  pack_bf16(p[1][0], p[1][1]), pack_bf16(p[1][2], p[1][3])};
-    }
-    return redo;
   };
 
-  // ---- P V of tile i for output dims [128 wave, 128 wave + 128) of all the
-  // workgroup's heads, with tile i+1's dequant (from registers) and tile
-  // i+2's raw loads interleaved.  Value operand of dim d = 128 wave +
-  // 16 db' + n: the pieces of dims d - (d % 8) live at storage position
-  // p = 18 (2 (db' % 2) + e) + 4 wave + db' / 2 (e = (n % 4) / 2), slot
-  // 24 (2 (db' % 2) + e) + 4 wave + db' / 2 + (row % 16).
-  auto pv = [&](int i, int ob) __attribute__((always_inline)) {
-    const int row = 4 * g + (n >> 2), e = (n & 3) >> 1;
-    const uint32_t v0 = lds_addr(&kt[i & 1][0]) + row * kRowB +
-                        16 * (24 * e + 4 * wave + (row & 15)) + 8 * (n & 1) + ob;
-    const uint16_t* prow = &pl[n][8 * g + ob];
-    // two halves of 4 output tiles: value operands of a half held, the
-    // probability operands streamed (read twice)
-    constexpr int kHalf = kDBW / 2;
-    sfor<2>([&](auto HH) {
-      constexpr int half = decltype(HH)::value;
-      u32x4_t vb[kHalf];
-      sfor<kHalf>([&](auto D) {
-        constexpr int db = half * kHalf + decltype(D)::value;
-        constexpr int off = 16 * (48 * (db & 1) + (db >> 1));
-        const i16x4_t x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr<i16x4_t>(v0 + off));
-        const i16x4_t x1 =
-            __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr<i16x4_t>(v0 + off + 16 * kRowB));
-        const u32x2_t w0 = __builtin_bit_cast(u32x2_t, x0), w1 = __builtin_bit_cast(u32x2_t, x1);
-        vb[decltype(D)::value] = u32x4_t{w0[0], w0[1], w1[0], w1[1]};
-      });
-      u32x4_t pa[2];
-      pa[0] = *reinterpret_cast<const u32x4_t*>(prow);
-      sfor<kHB>([&](auto H) {
-        constexpr int hb = decltype(H)::value;
-        if constexpr (hb + 1 < kHB)
-          pa[(hb + 1) & 1] = *reinterpret_cast<const u32x4_t*>(prow + 16 * kPRow * (hb + 1));
+  // ---- dequant of piece k of tile i: raw stage s -> key buffer nb
+  struct Dq {
+    u32x2_t c;
+    uint32_t sb;
+  };
+  auto dq_load = [&](const LaneAddr& la, int s, int k, Dq& r) __attribute__((always_inline)) {
+    r.c = *lds_ptr<const u32x2_t>(la.dq_code + s * kRawTile + 16 * k);
+    r.sb = *lds_ptr<const uint32_t>(la.dq_sb + s * kRawTile + 4 * k);
+  };
+  // The dequant of a piece runs in 6 parts, one per matrix-core step: a
+  // wave overlaps about 4 VALU instructions with each 32-cycle MFMA of its
+  // own, and a burst of more stalls the next MFMA.  Part 0 reads the
+  // scale/bias, parts 1-4 convert one pair of codes each, part 5 stores
+  // the piece.  Each part starts with an empty asm taking its inputs as
+  // operands, so its arithmetic cannot be hoisted into an earlier step
+  // (and the wait for the piece's LDS reads, issued a piece earlier into
+  // the other register set, lands at part 0).
+  struct DqOut {
+    u32x4_t w;
+    float sc, bi;
+  };
+  auto dq_part = [&](int part, Dq& r, DqOut& o, bool valid, const LaneAddr& la, int nb, int k)
+                     __attribute__((always_inline)) {
+    if (part == 0) {
+      asm volatile("" : "+v"(r.sb));
+      const uint32_t sbw = valid ? r.sb : 0u;  // entries past the end dequantize to zeros
+      o.sc = __uint_as_float(sbw << 16);
+      o.bi = __uint_as_float(sbw & 0xFFFF0000u);
+    } else if (part <= 4) {
+      const int j = part - 1;  // codes 2j, 2j + 1 of the piece
+      uint32_t x = r.c[j >> 1];
+      float sc = o.sc, bi = o.bi;
+      asm volatile("" : "+v"(x), "+v"(sc), "+v"(bi));
+      const int sh = 16 * (j & 1);
+      o.w[j] = pack_bf16(fmaf(sc, static_cast<float>((x >> sh) & 0xFF), bi),
+                         fmaf(sc, static_cast<float>((x >> (sh + 8)) & 0xFF), bi));
+    } else {
+      u32x4_t w = o.w;
+      asm volatile("" : "+v"(w));
+      *lds_ptr<u32x4_t>(la.dq_dst + nb * kKTile + 128 * k) = w;
+    }
+  };
+  auto dq_store = [&](const LaneAddr& la, Dq& r, bool valid, int nb, int k)
+                      __attribute__((always_inline)) {
+    DqOut o;
 #pragma unroll
-        for (int d = 0; d < kHalf; d++)
-          o[hb][half * kHalf + d] = mfma(pa[hb & 1], vb[d], o[hb][half * kHalf + d]);
-        __builtin_amdgcn_sched_barrier(0);
-      });
-    });
+    for (int part = 0; part < 6; part++) dq_part(part, r, o, valid, la, nb, k);
   };
 
-  // The running max starts at the first tile's max and is otherwise fixed:
-  // probabilities up to 2^kTau are exact enough in fp32/bf16.  A score that
-  // exceeds it by more than kTau makes the workgroup run the split again,
-  // with m_est = the largest score of the whole first run, so the second
-  // run never needs a third.  (The accumulators are never rescaled: a
-  // rescale branch in the loop makes the compiler copy all of them on every
-  // tile.)  Two barriers per tile: before the scores (key tile i complete,
-  // probability tile free) and before P.V (probabilities complete).
+  f32x16_t o[4][4];  // [head block (wave + hb) % 4][dim block]: 32 x 32 tiles
+  float m_run = -INFINITY, l_run = 0.f, m_est = -INFINITY;
+
+  // ---- one pass over the split.  Returns true when a later score
+  // exceeded the running max by more than kTau (the pass must be redone
+  // with m_est, the largest score it saw).
   auto run = [&]() __attribute__((always_inline)) -> bool {
 #pragma unroll
-    for (int hb = 0; hb < kHB; hb++)
+    for (int hb = 0; hb < 4; hb++)
 #pragma unroll
-      for (int db = 0; db < kDBW; db++) o[hb][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int hb = 0; hb < HB; hb++) {
-      m_run[hb] = m_est[hb];
-      l_run[hb] = 0.f;
-    }
-    Raw r;
-    sfor<kPieces>([&](auto K) { load_raw_piece(0, 0, K, r); });
-    sfor<kPieces>([&](auto K) {
-      dequant_piece(r, 0, 0, K);
-      load_raw_piece(1, 0, K, r);
-    });
+      for (int db = 0; db < 4; db++) o[hb][db] = f32x16_t{};
+    m_run = m_est;
+    l_run = 0.f;
     bool redo = false;
-    for (int i = 0; i < ntiles; i++) {
-      int ob = 0;
-      asm volatile("" : "+v"(ob));
-      __syncthreads();
-      qk(i, ob, r);
-      redo |= softmax(i, ob);
-      __syncthreads();
-      pv(i, ob);
-    }
-    // total sums of this wave's heads for the normalization by all waves,
-    // and agreement on a second run
+
+    // prologue: raw tiles 0..2 in flight, tile 0 dequantized
+    dma_tile(0, 0, table_entry(0));
+    dma_tile(1, 1, table_entry(1));
+    dma_tile(2, 2, table_entry(2));
+    int32_t entry_next = table_entry(3);
+    raw_wait_two_tiles();
+    lds_barrier();
+    {
+      const LaneAddr la = lane_addr();
+      const bool valid = t0 + la.dt < t1;
+      Dq r;
 #pragma unroll
-    for (int hb = 0; hb < HB; hb++) {
-      float lt = l_run[hb];
-      lt += __shfl_xor(lt, 16);
-      lt += __shfl_xor(lt, 32);
-      l_run[hb] = lt;
-      if (g == 0) lsh[wave * 16 * HB + 16 * hb + n] = lt;
+      for (int k = 0; k < kPieces; k++) {
+        dq_load(la, 0, k, r);
+        dq_store(la, r, valid, 0, k);
+      }
     }
+    raw_wait_one_tile();
+    lds_barrier();
+
+    // tile i: scores on key buffer i % 2, dequant of tile i + 1 (raw
+    // stage (i + 1) % 3) into buffer (i + 1) % 2, raw tile i + 3 into
+    // stage i % 3
+    auto tile = [&](int i, auto NB) __attribute__((always_inline)) {
+      constexpr int nb = decltype(NB)::value;
+      const int s_next = (i + 1) % kStages;
+      dma_tile(i + 3, i % kStages, entry_next);
+      entry_next = table_entry(i + 4);
+      // (after the last tile this dequantizes the clamped copy of it into
+      // the idle buffer: harmless, and keeps the tile branch-free)
+      const LaneAddr la = lane_addr();
+      const bool dq_valid = t0 + kTile * (i + 1) + la.dt < t1;
+
+      // -- scores S^T (32 tokens x 32 heads) with 6 dequant pieces
+      f32x16_t s;
+      u32x4_t ka[kKaRing], qrope[kChunks - kQReg];
+      Dq r[2];
+      DqOut dqo;
+      dq_load(la, s_next, 0, r[0]);
+#pragma unroll
+      for (int c = 0; c < kKaAhead; c++)
+        ka[c] = *lds_ptr<const u32x4_t>(la.ka[c & 3] + nb * kKTile + 128 * (c >> 2));
+      sfor<kChunks>([&](auto C) {
+        constexpr int c = decltype(C)::value;
+        constexpr int cn = c + kKaAhead;
+        if constexpr (cn < kChunks)
+          ka[cn % kKaRing] =
+              *lds_ptr<const u32x4_t>(la.ka[cn & 3] + nb * kKTile + 128 * (cn >> 2));
+        if constexpr (c + 2 >= kQReg && c + 2 < kChunks)
+          qrope[c + 2 - kQReg] = *lds_ptr<const u32x4_t>(la.qr + 32 * (c + 2 - kQReg));
+        if constexpr (c / 6 < kDqQK) {
+          constexpr int k = c / 6, part = c % 6;
+          if constexpr (part == 0 && k + 1 < kPieces) dq_load(la, s_next, k + 1, r[(k + 1) & 1]);
+          dq_part(part, r[k & 1], dqo, dq_valid, la, nb ^ 1, k);
+        }
+        if constexpr (c == 0)
+          mfma_v_first(s, ka[0], qf[0]);
+        else if constexpr (c < kQReg)
+          mfma_v(s, ka[c % kKaRing], qf[c]);
+        else
+          mfma_v(s, ka[c % kKaRing], qrope[c - kQReg]);
+        step_fence();
+      });
+
+      // -- value operands of this tile (independent of the softmax)
+      u32x4_t vb[4][2];
+#pragma unroll
+      for (int db = 0; db < 4; db++)
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+          const uint32_t off = nb * kKTile + ks * 16 * kKRow + 128 * (db >> 1);
+          const i16x4_t x0 =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr<i16x4_t>(la.vb[db & 1][0] + off));
+          const i16x4_t x1 =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr<i16x4_t>(la.vb[db & 1][1] + off));
+          const u32x2_t w0 = __builtin_bit_cast(u32x2_t, x0), w1 = __builtin_bit_cast(u32x2_t, x1);
+          vb[db][ks] = u32x4_t{w0[0], w0[1], w1[0], w1[1]};
+        }
+
+      // -- softmax against the fixed running max; tokens past the end
+      // (last tile only) are masked
+      mfma_result_fence(s);
+      {
+        const int rem = t1 - (t0 + kTile * i);
+        if (rem < kTile) {
+          asm volatile("");  // keep this a branch: one tile in many
+#pragma unroll
+          for (int j = 0; j < 16; j++)
+            if (8 * (j >> 2) + 4 * kg + (j & 3) >= rem) s[j] = -INFINITY;
+        }
+        float mx = s[0];
+#pragma unroll
+        for (int j = 1; j < 16; j++) mx = fmaxf(mx, s[j]);
+        // scale > 0, so the largest score maps to the largest logit
+        const float mloc = mx * cl;
+        if (__builtin_amdgcn_ballot_w64(mloc > m_run + kTau)) {
+          m_est = fmaxf(m_est, fmaxf(mloc, __shfl_xor(mloc, 32)));
+          if (i == 0)
+            m_run = m_est;  // nothing accumulated yet: take the max as is
+          else
+            redo = true;
+        }
+      }
+      u32x4_t pown[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) {
+        float p[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          p[e] = fast_exp2(fmaf(s[8 * ks + e], cl, -m_run));
+          l_run += p[e];
+        }
+        pown[ks] = u32x4_t{pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]),
+                           pack_bf16(p[6], p[7])};
+        *lds_ptr<u32x4_t>(la.p + wave * 32 * kPRow + 32 * ks) = pown[ks];
+      }
+      // -- P.V on the wave's own heads, from registers
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+        for (int db = 0; db < 4; db++) o[0][db] = mfma(pown[ks], vb[db][ks], o[0][db]);
+      step_fence();
+      lds_barrier();  // probabilities of every head complete
+      // -- P.V on the other waves' heads, with the remaining dequant
+      // (the next head block's operands are read one block ahead)
+      u32x4_t pa[2][2];
+      {
+        const uint32_t prow = la.p + ((wave + 1) & 3) * 32 * kPRow;
+        pa[0][0] = *lds_ptr<const u32x4_t>(prow);
+        pa[0][1] = *lds_ptr<const u32x4_t>(prow + 32);
+      }
+      sfor<3>([&](auto HB) {
+        constexpr int hb = decltype(HB)::value + 1;
+        const u32x4_t pa0 = pa[(hb - 1) & 1][0];
+        const u32x4_t pa1 = pa[(hb - 1) & 1][1];
+        if constexpr (hb < 3) {
+          const uint32_t prow = la.p + ((wave + hb + 1) & 3) * 32 * kPRow;
+          pa[hb & 1][0] = *lds_ptr<const u32x4_t>(prow);
+          pa[hb & 1][1] = *lds_ptr<const u32x4_t>(prow + 32);
+        }
+        constexpr int k = kDqQK + hb - 1;
+        // 8 MFMA steps, dequant parts 0..5 of piece k on the first six
+        sfor<8>([&](auto M) {
+          constexpr int m = decltype(M)::value;
+          if constexpr (m < 6 && k < kPieces) {
+            if constexpr (m == 0 && k + 1 < kPieces) dq_load(la, s_next, k + 1, r[(k + 1) & 1]);
+            dq_part(m, r[k & 1], dqo, dq_valid, la, nb ^ 1, k);
+          }
+          o[hb][m & 3] = mfma(m < 4 ? pa0 : pa1, vb[m & 3][m >> 2], o[hb][m & 3]);
+          step_fence();
+        });
+      });
+      // next tile's raw stage complete (this wave), then every wave's
+      // dequant, P.V reads and raw loads are done
+      raw_wait_one_tile();
+      lds_barrier();
+    };
+    static_assert(kDqQK + 3 == kPieces, "the dequant pieces fill the two phases");
+
+    int i = 0;
+    for (; i + 1 < ntiles; i += 2) {
+      tile(i, std::integral_constant<int, 0>{});
+      tile(i + 1, std::integral_constant<int, 1>{});
+    }
+    if (i < ntiles) tile(i, std::integral_constant<int, 0>{});
+    // drain the raw loads issued past the end before the stages are reused
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // total sums of this wave's heads (lanes l and l ^ 32 hold the two
+    // token halves), and agreement on a second pass
+    const float lt = l_run + __shfl_xor(l_run, 32);
+    l_run = lt;
+    if (kg == 0) lsh[32 * wave + l32] = lt;
     if (lane == 0) restart_flag[wave] = redo ? 1 : 0;
     __syncthreads();
     const u32x4_t f = *reinterpret_cast<const u32x4_t*>(&restart_flag[0]);
@@ -452,41 +584,42 @@ mla_kernel(const MlaArgs a) {
     __syncthreads();
     return any;
   };
-  // (one copy of the tile loop: a second inlined copy would keep values of
-  // both alive and spill)
+  // (one copy of the tile loop)
 #pragma nounroll
   for (int attempt = 0; attempt < 2; attempt++)
     if (!run()) break;
 
-  // ---- finalize: lane (n, g) holds output rows (heads) 16 hb' + 4g + e,
-  // dims 128 wave + 16 db' + n.  Whole sequence: the output; a split: its
+  // ---- finalize: lane (l32, kg) holds, in o[hb][db][r], head row
+  // 32 ((wave + hb) % 4) + 8 (r / 4) + 4 kg + r % 4 and dim
+  // 128 wave + 32 db + l32.  Whole sequence: the output; a split: its
   // normalized partial (bf16), and (max, sum) from the heads' score wave.
   uint16_t* dst = a.n_splits == 1 ? a.out : a.ws_o;
   const int64_t dss = a.n_splits == 1 ? a.o_ss : static_cast<int64_t>(a.H) * kDV;
   const int64_t dsh = a.n_splits == 1 ? a.o_sh : kDV;
   const int64_t drow = a.n_splits == 1 ? b : static_cast<int64_t>(slot);
 #pragma unroll
-  for (int hb = 0; hb < kHB; hb++) {
-    const f32x4_t lt = *reinterpret_cast<const f32x4_t*>(&lsh[16 * hb + 4 * g]);
+  for (int hb = 0; hb < 4; hb++) {
+    const int hl = 32 * ((wave + hb) & 3);
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const int h = hg0 + 16 * hb + 4 * g + e;
-      const float inv = lt[e] > 0.f ? 1.0f / lt[e] : 0.f;
-      if (h < a.H) {
-        uint16_t* op = dst + drow * dss + static_cast<int64_t>(h) * dsh + kDW * wave + n;
+    for (int m = 0; m < 4; m++) {
+      const f32x4_t lt = *reinterpret_cast<const f32x4_t*>(&lsh[hl + 8 * m + 4 * kg]);
 #pragma unroll
-        for (int db = 0; db < kDBW; db++) op[16 * db] = f32_to_bf16(o[hb][db][e] * inv);
+      for (int e = 0; e < 4; e++) {
+        const int h = hg0 + hl + 8 * m + 4 * kg + e;
+        const float inv = lt[e] > 0.f ? 1.0f / lt[e] : 0.f;
+        if (h < a.H) {
+          uint16_t* op = dst + drow * dss + static_cast<int64_t>(h) * dsh + 128 * wave + l32;
+#pragma unroll
+          for (int db = 0; db < 4; db++) op[32 * db] = f32_to_bf16(o[hb][db][4 * m + e] * inv);
+        }
       }
     }
   }
-  if (a.n_splits > 1 && g == 0) {
-#pragma unroll
-    for (int hb = 0; hb < HB; hb++) {
-      const int h = hw + 16 * hb + n;
-      if (h < a.H) {
-        a.ws_ml[(slot * a.H + h) * 2] = m_run[hb];
-        a.ws_ml[(slot * a.H + h) * 2 + 1] = l_run[hb];
-      }
+  if (a.n_splits > 1 && kg == 0) {
+    const int h = hw + l32;
+    if (h < a.H) {
+      a.ws_ml[(slot * a.H + h) * 2] = m_run;
+      a.ws_ml[(slot * a.H + h) * 2 + 1] = l_run;
     }
   }
 }
@@ -540,9 +673,13 @@ bool mla_supported(int dtype, int bits, int group, int head_dim, int v_head_dim,
          n_kv_heads == 1 && block_size > 0 && block_size % kTile == 0;
 }
 
+bool mla_layout_supported(const uint8_t* base, int64_t block_bytes, int64_t sb_off) {
+  // raw tiles are copied with 16-byte loads
+  return reinterpret_cast<uintptr_t>(base) % 16 == 0 && block_bytes % 16 == 0 && sb_off % 16 == 0;
+}
+
 size_t mla_plan(MlaArgs& a, int want) {
-  const int hb = a.H > 64 ? 2 : 1;
-  const int groups = (a.H + 64 * hb - 1) / (64 * hb);
+  const int groups = (a.H + kHeads - 1) / kHeads;
   const int max_tiles = std::max(1, (a.max_len + kTile - 1) / kTile);
   int splits = want > 0 ? want
                         : (device_cus() + a.n_seqs * groups - 1) / std::max(1, a.n_seqs * groups);
@@ -559,13 +696,9 @@ void launch_mla(const MlaArgs& a0, hipStream_t st) {
   MlaArgs a = a0;
   if (a.n_splits > 1)
     a.ws_ml = reinterpret_cast<float*>(a.ws_o + static_cast<size_t>(a.n_seqs) * a.n_splits * a.H * kDV);
-  const int hb = a.H > 64 ? 2 : 1;
-  const dim3 grid(a.n_splits, a.n_seqs, (a.H + 64 * hb - 1) / (64 * hb));
+  const dim3 grid(a.n_splits, a.n_seqs, (a.H + kHeads - 1) / kHeads);
   const TimedLaunch tl = timing_prepare(kTimeMla);
-  if (hb == 2)
-    hipExtLaunchKernelGGL(mla_kernel<2>, grid, dim3(256), 0, st, tl.start, tl.stop, 0, a);
-  else
-    hipExtLaunchKernelGGL(mla_kernel<1>, grid, dim3(256), 0, st, tl.start, tl.stop, 0, a);
+  hipExtLaunchKernelGGL(mla_kernel, grid, dim3(256), 0, st, tl.start, tl.stop, 0, a);
   VKV_HIP(hipGetLastError());
   timing_commit(tl);
   if (a.n_splits > 1) {
