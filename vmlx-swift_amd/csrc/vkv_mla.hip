@@ -370,16 +370,15 @@ mla_kernel(const MlaArgs a) {
       o.bi = __uint_as_float(sbw & 0xFFFF0000u);
     } else if (part <= 4) {
       const int j = part - 1;  // codes 2j, 2j + 1 of the piece
-      uint32_t x = r.c[j >> 1];
-      float sc = o.sc, bi = o.bi;
-      asm volatile("" : "+v"(x), "+v"(sc), "+v"(bi));
+      // (laundered in place: a copy would cost a move per register)
+      asm volatile("" : "+v"(r.c), "+v"(o.sc), "+v"(o.bi));
+      const uint32_t x = r.c[j >> 1];
       const int sh = 16 * (j & 1);
-      o.w[j] = pack_bf16(fmaf(sc, static_cast<float>((x >> sh) & 0xFF), bi),
-                         fmaf(sc, static_cast<float>((x >> (sh + 8)) & 0xFF), bi));
+      o.w[j] = pack_bf16(fmaf(o.sc, static_cast<float>((x >> sh) & 0xFF), o.bi),
+                         fmaf(o.sc, static_cast<float>((x >> (sh + 8)) & 0xFF), o.bi));
     } else {
-      u32x4_t w = o.w;
-      asm volatile("" : "+v"(w));
-      *lds_ptr<u32x4_t>(la.dq_dst + nb * kKTile + 128 * k) = w;
+      asm volatile("" : "+v"(o.w));
+      *lds_ptr<u32x4_t>(la.dq_dst + nb * kKTile + 128 * k) = o.w;
     }
   };
   auto dq_store = [&](const LaneAddr& la, Dq& r, bool valid, int nb, int k)
@@ -494,6 +493,13 @@ mla_kernel(const MlaArgs a) {
           for (int j = 0; j < 16; j++)
             if (8 * (j >> 2) + 4 * kg + (j & 3) >= rem) s[j] = -INFINITY;
         }
+      }
+      // A score above the running max by more than kTau: the first tile
+      // takes its max as the running max (nothing is accumulated yet), a
+      // later one makes the pass run again.  After the first tile the check
+      // runs behind the exponentials, so they overlap the own-head MFMAs
+      // (an overflow they may hold is discarded with the pass).
+      auto max_check = [&]() __attribute__((always_inline)) {
         float mx = s[0];
 #pragma unroll
         for (int j = 1; j < 16; j++) mx = fmaxf(mx, s[j]);
@@ -502,30 +508,30 @@ mla_kernel(const MlaArgs a) {
         if (__builtin_amdgcn_ballot_w64(mloc > m_run + kTau)) {
           m_est = fmaxf(m_est, fmaxf(mloc, __shfl_xor(mloc, 32)));
           if (i == 0)
-            m_run = m_est;  // nothing accumulated yet: take the max as is
+            m_run = m_est;
           else
             redo = true;
         }
-      }
-      u32x4_t pown[2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ks++) {
+      };
+      if (i == 0) max_check();
+      // -- probabilities of k-step ks, then P.V of the wave's own heads on
+      // them from registers while the next k-step's exponentials run
+      sfor<2>([&](auto KS) {
+        constexpr int ks = decltype(KS)::value;
         float p[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
           p[e] = fast_exp2(fmaf(s[8 * ks + e], cl, -m_run));
           l_run += p[e];
         }
-        pown[ks] = u32x4_t{pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]),
-                           pack_bf16(p[6], p[7])};
-        *lds_ptr<u32x4_t>(la.p + wave * 32 * kPRow + 32 * ks) = pown[ks];
-      }
-      // -- P.V on the wave's own heads, from registers
+        const u32x4_t pw = u32x4_t{pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]),
+                                   pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7])};
+        *lds_ptr<u32x4_t>(la.p + wave * 32 * kPRow + 32 * ks) = pw;
 #pragma unroll
-      for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-        for (int db = 0; db < 4; db++) o[0][db] = mfma(pown[ks], vb[db][ks], o[0][db]);
-      step_fence();
+        for (int db = 0; db < 4; db++) o[0][db] = mfma(pw, vb[db][ks], o[0][db]);
+        step_fence();
+      });
+      if (i != 0) max_check();
       lds_barrier();  // probabilities of every head complete
       // -- P.V on the other waves' heads, with the remaining dequant
       // (the next head block's operands are read one block ahead)
