@@ -632,27 +632,45 @@ mla_kernel(const MlaArgs a) {
 
 // Merge of the split partials of one (sequence, head): 128 threads x 4 dims.
 // Partial s holds o_s / l_s (bf16) with its max m_s and sum l_s (log2 units).
+// The (max, sum) pairs and the partial rows of up to 8 splits are loaded
+// before any is used, so a merge costs one memory round trip per 8 splits.
 __global__ void __launch_bounds__(128) mla_combine_kernel(const MlaArgs a) {
   const int h = blockIdx.x, b = blockIdx.y;
   const int d = 4 * threadIdx.x;
   const size_t s0 = static_cast<size_t>(b) * a.n_splits;
-  float M = -INFINITY;
-  for (int s = 0; s < a.n_splits; s++) {
-    const float* ml = a.ws_ml + ((s0 + s) * a.H + h) * 2;
-    if (ml[1] > 0.f) M = fmaxf(M, ml[0]);
-  }
-  float den = 0.f;
+  float M = -INFINITY, den = 0.f;
   f32x4_t acc{0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < a.n_splits; s++) {
-    const float* ml = a.ws_ml + ((s0 + s) * a.H + h) * 2;
-    const float l = ml[1];
-    const u32x2_t v = *reinterpret_cast<const u32x2_t*>(a.ws_o + ((s0 + s) * a.H + h) * kDV + d);
-    const float w = l > 0.f ? fast_exp2(ml[0] - M) * l : 0.f;
-    den += w;
-    const float x[4] = {__uint_as_float(v[0] << 16), __uint_as_float(v[0] & 0xFFFF0000u),
-                        __uint_as_float(v[1] << 16), __uint_as_float(v[1] & 0xFFFF0000u)};
+  for (int c = 0; c < a.n_splits; c += 8) {
+    f32x2_t ml[8];
+    u32x2_t v[8];
 #pragma unroll
-    for (int e = 0; e < 4; e++) acc[e] = l > 0.f ? fmaf(w, x[e], acc[e]) : acc[e];
+    for (int j = 0; j < 8; j++) {
+      const int s = min(c + j, a.n_splits - 1);  // (clamped slots are selected away)
+      ml[j] = *reinterpret_cast<const f32x2_t*>(a.ws_ml + ((s0 + s) * a.H + h) * 2);
+      v[j] = *reinterpret_cast<const u32x2_t*>(a.ws_o + ((s0 + s) * a.H + h) * kDV + d);
+    }
+    float Mc = M;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      if (c + j < a.n_splits && ml[j][1] > 0.f) Mc = fmaxf(Mc, ml[j][0]);
+    // rescale what the earlier chunks accumulated to the new max
+    const float r = Mc == -INFINITY ? 0.f : fast_exp2(M - Mc);
+    den *= r;
+#pragma unroll
+    for (int e = 0; e < 4; e++) acc[e] *= r;
+    M = Mc;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float l = ml[j][1];
+      if (c + j < a.n_splits && l > 0.f) {
+        const float w = fast_exp2(ml[j][0] - M) * l;
+        den += w;
+        acc[0] = fmaf(w, __uint_as_float(v[j][0] << 16), acc[0]);
+        acc[1] = fmaf(w, __uint_as_float(v[j][0] & 0xFFFF0000u), acc[1]);
+        acc[2] = fmaf(w, __uint_as_float(v[j][1] << 16), acc[2]);
+        acc[3] = fmaf(w, __uint_as_float(v[j][1] & 0xFFFF0000u), acc[3]);
+      }
+    }
   }
   const float inv = den > 0.f ? 1.0f / den : 0.f;
   uint16_t* op = a.out + b * a.o_ss + static_cast<int64_t>(h) * a.o_sh + d;
