@@ -451,8 +451,8 @@ mla_kernel(const MlaArgs a) {
         if constexpr (cn < kChunks)
           ka[cn % kKaRing] =
               *lds_ptr<const u32x4_t>(la.ka[cn & 3] + nb * kKTile + 128 * (cn >> 2));
-        if constexpr (c + 2 >= kQReg && c + 2 < kChunks)
-          qrope[c + 2 - kQReg] = *lds_ptr<const u32x4_t>(la.qr + 32 * (c + 2 - kQReg));
+        if constexpr (cn >= kQReg && cn < kChunks)
+          qrope[cn - kQReg] = *lds_ptr<const u32x4_t>(la.qr + 32 * (cn - kQReg));
         if constexpr (c / 6 < kDqQK) {
           constexpr int k = c / 6, part = c % 6;
           if constexpr (part == 0 && k + 1 < kPieces) dq_load(la, s_next, k + 1, r[(k + 1) & 1]);
