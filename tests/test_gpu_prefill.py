@@ -1,0 +1,136 @@
+"""GPU parity of multi-query attention (L >= 2 query tokens: chunked prefill)
+over dense bf16 / f16 K/V with no or a causal mask, the matrix-core path of
+vkv_sdpa (vkv_prefill.hip), against the oracle's SDPA and against the
+generic kernel (VKV_GENERIC_ATTENTION=1): GQA groups of 1, 4 and 8, key
+counts that are not multiples of the 32-token tile, query counts that are
+not multiples of the 256-row block, several key splits, strided slices of
+cache buffers and two batch rows."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import vkv
+from gpu_util import attn_tol, dev, rand_bits, values
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(rng, dtype, B, Hq, Hkv, L, T, mask, cap=None, monkeypatch=None, scale=None):
+    D = 128
+    scale = D ** -0.5 if scale is None else scale
+    q = rand_bits(rng, (B, Hq, L, D), dtype)
+    k = rand_bits(rng, (B, Hkv, T, D), dtype)
+    v = rand_bits(rng, (B, Hkv, T, D), dtype)
+    if cap:  # slices of larger (cache-like) buffers: token stride D, head stride cap * D
+        kb = torch.zeros((B, Hkv, cap, D), dtype=dev(k, dtype).dtype, device="cuda")
+        vb = torch.zeros_like(kb)
+        kb[:, :, :T] = dev(k, dtype)
+        vb[:, :, :T] = dev(v, dtype)
+        kd, vd = kb[:, :, :T], vb[:, :, :T]
+    else:
+        kd, vd = dev(k, dtype), dev(v, dtype)
+    got = values(vkv.scaled_dot_product_attention(dev(q, dtype), kd, vd, scale, mask=mask), dtype)
+    f = lambda a: O.to_f32(a, dtype)
+    ref = O.sdpa(f(q), f(k), f(v), scale, mask=mask)
+    bad = np.abs(got - ref) > attn_tol(dtype, ref)
+    assert not bad.any(), (np.abs(got - ref).max(), np.argwhere(bad)[:4])
+    if monkeypatch is not None:
+        monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
+        gen = values(vkv.scaled_dot_product_attention(dev(q, dtype), kd, vd, scale, mask=mask),
+                     dtype)
+        monkeypatch.delenv("VKV_GENERIC_ATTENTION")
+        assert (np.abs(got - gen) <= attn_tol(dtype, ref)).all()
+
+
+@pytest.mark.parametrize("dtype", [O.BF16, O.F16])
+@pytest.mark.parametrize("mask", [None, "causal"])
+@pytest.mark.parametrize("Hq,Hkv", [(32, 8), (8, 8), (16, 2)])
+def test_prefill_matches_oracle(dtype, mask, Hq, Hkv, monkeypatch):
+    rng = np.random.default_rng(dtype * 100 + Hq + Hkv + (mask == "causal"))
+    run_case(rng, dtype, 1, Hq, Hkv, 70, 301, mask, monkeypatch=monkeypatch)
+
+
+@pytest.mark.parametrize("L,T", [(2, 2), (2, 33), (31, 31), (64, 1000), (300, 700)])
+def test_prefill_lengths_causal(L, T):
+    rng = np.random.default_rng(L * 7 + T)
+    run_case(rng, O.BF16, 1, 32, 8, L, T, "causal")
+
+
+def test_prefill_no_mask_long_keys_many_splits():
+    # few query rows and many keys: several key splits merged
+    rng = np.random.default_rng(5)
+    run_case(rng, O.BF16, 1, 8, 8, 4, 4133, None)
+
+
+def test_prefill_chunk_over_cache_slice_two_rows():
+    # a 512-token chunk at the end of a 1500-token context, cache buffers of
+    # capacity 1792, two batch rows
+    rng = np.random.default_rng(9)
+    run_case(rng, O.BF16, 2, 8, 2, 512, 1500, "causal", cap=1792)
+
+
+def test_prefill_large_scores_rescale():
+    # scores that grow along the keys exercise the running-max rescale
+    rng = np.random.default_rng(13)
+    run_case(rng, O.BF16, 1, 16, 4, 40, 600, "causal", scale=0.5)
+
+
+def quantized_chunk(rng, bits, outliers):
+    """A 64-token causal chunk through the router over a QuantizedKVCache
+    holding a 300-token prefix: returns the output, the chunk's inputs and
+    the whole (prefix + chunk) K/V."""
+    dtype, Hq, Hkv, D, T0, L = O.BF16, 32, 8, 128, 300, 64
+    k0, v0 = (rand_bits(rng, (1, Hkv, T0, D), dtype, outliers=outliers) for _ in range(2))
+    k1, v1 = (rand_bits(rng, (1, Hkv, L, D), dtype, outliers=outliers) for _ in range(2))
+    q = rand_bits(rng, (1, Hq, L, D), dtype)
+    c = vkv.QuantizedKVCache(group_size=64, bits=bits)
+    c.update_quantized(dev(k0, dtype), dev(v0, dtype))
+
+    def step():
+        out = vkv.attention_with_cache_update(dev(q, dtype), dev(k1, dtype), dev(v1, dtype), c,
+                                              D ** -0.5, mask="causal")
+        assert c.trim(L) == L
+        return values(out, dtype)
+
+    return step, q, np.concatenate([k0, k1], axis=2), np.concatenate([v0, v1], axis=2)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantized_cache_chunk(bits, monkeypatch):
+    """Against the oracle's quantized SDPA on the same codes, and against the
+    generic path (which keeps the dequantized values unrounded)."""
+    dtype, D = O.BF16, 128
+    step, q, kx, vx = quantized_chunk(np.random.default_rng(bits), bits, 0)
+    got = step()
+    kq, ks, kb, _ = O.quantize(kx, dtype, 64, bits)
+    vq, vs, vb, _ = O.quantize(vx, dtype, 64, bits)
+    f = lambda a: O.to_f32(a, dtype)
+    ref = O.quantized_sdpa(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64, bits,
+                           mask="causal")
+    tol = attn_tol(dtype, ref)
+    assert (np.abs(got - ref) <= tol).all(), np.abs(got - ref).max()
+    monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
+    gen = step()
+    assert (np.abs(got - gen) <= tol).all()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantized_cache_chunk_outlier_channels(bits):
+    """Config-2 data (4 channels per head scaled x20): the chunk path attends
+    over the cache dequantized to bf16 (the values the reference's dequantize
+    produces) with the quantized-SDPA query rounding (queries times the
+    bf16-rounded scale, rounded to bf16); checked against the oracle's float
+    SDPA over exactly those operands."""
+    dtype, D = O.BF16, 128
+    step, q, kx, vx = quantized_chunk(np.random.default_rng(10 + bits), bits, 4)
+    got = step()
+    kq, ks, kb, _ = O.quantize(kx, dtype, 64, bits)
+    vq, vs, vb, _ = O.quantize(vx, dtype, 64, bits)
+    kd = O.dequantize(kq, ks, kb, dtype, 64, bits)
+    vd = O.dequantize(vq, vs, vb, dtype, 64, bits)
+    f = lambda a: O.to_f32(a, dtype)
+    st = f(O.from_f32(np.array([D ** -0.5], np.float32), dtype))[0]
+    qs = f(O.from_f32(f(q) * st, dtype))
+    ref = O.sdpa(qs, f(kd), f(vd), 1.0, mask="causal")
+    assert (np.abs(got - ref) <= attn_tol(dtype, ref)).all(), np.abs(got - ref).max()

@@ -74,6 +74,8 @@ int32_t choose_parts(int64_t rows_x_heads, int64_t max_len, int32_t* part_tokens
   return static_cast<int32_t>(std::max<int64_t>(1, (max_len + pt - 1) / pt));
 }
 
+constexpr int kGatherPrefillMinL = 16;
+
 void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64_t rows,
                    int64_t max_len, hipStream_t st) {
   if (fdecode_supported(dtype, bits, qsem, a) && !getenv("VKV_GENERIC_ATTENTION")) {
@@ -85,6 +87,67 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
       a.ws_ml = ws + per * a.Dv;
     }
     launch_fdecode(dtype, a, rows, st);
+    return;
+  }
+  // Quantized or paged K/V (a uniform length per row) with a chunk of query
+  // tokens: gather them to dense rows of the dtype (the dequantized values
+  // the reference's dequantize produces), then the matrix-core multi-query
+  // kernel on the copy.  Fewer query tokens stay on the generic kernel,
+  // which keeps the dequantized values unrounded (fp32) as the quantized
+  // matmul of the oracle does.
+  if ((bits > 0 || a.kv.table) && !a.kv.seq_lens && a.L >= kGatherPrefillMinL && a.kv.T > 0 &&
+      !getenv("VKV_GENERIC_ATTENTION")) {
+    AttnArgs d = a;
+    const int64_t batch = rows / a.L, T = a.kv.T;
+    const int64_t es = elem_bytes(dtype);
+    const int64_t per_head = T * a.D * es, kv_bytes = batch * a.Hkv * per_head;
+    d.kv = KVSrc{};
+    d.kv.T = a.kv.T;
+    d.kv.kc = Comp{nullptr, a.Hkv * per_head, per_head, a.D * es};
+    d.kv.vc = d.kv.kc;
+    // a stand-in base with the copy's alignment decides support first
+    d.kv.kc.ptr = d.kv.vc.ptr = reinterpret_cast<const uint8_t*>(uintptr_t{256});
+    if (a.D == a.Dv && prefill_supported(dtype, 0, d)) {
+      d.n_parts = prefill_parts(batch, a.Hkv, a.L, a.Hq / a.Hkv, T, &d.part_tokens);
+      const size_t copy_floats = static_cast<size_t>((2 * kv_bytes + 255) / 256 * 64);
+      const size_t per = static_cast<size_t>(rows) * a.Hq * d.n_parts;
+      float* ws = attention_workspace(st, copy_floats + (d.n_parts > 1 ? per * (a.Dv + 2) : 0));
+      uint8_t* kd = reinterpret_cast<uint8_t*>(ws);
+      uint8_t* vd = kd + kv_bytes;
+      for (int which = 0; which < 2; which++) {
+        GatherArgs g{};
+        g.kv = a.kv;
+        g.n_seqs = static_cast<int32_t>(batch);
+        g.H = a.Hkv;
+        g.T = static_cast<int32_t>(T);
+        g.D = a.D;
+        g.which = which;
+        g.bits = bits;
+        g.group = group;
+        g.dtype = dtype;
+        g.out = which ? vd : kd;
+        launch_gather(g, 0, st);
+      }
+      d.kv.kc.ptr = kd;
+      d.kv.vc.ptr = vd;
+      if (d.n_parts > 1) {
+        d.ws_o = ws + copy_floats;
+        d.ws_ml = d.ws_o + per * a.Dv;
+      }
+      launch_prefill(dtype, qsem, d, batch, st);
+      return;
+    }
+  }
+  if (prefill_supported(dtype, bits, a) && !getenv("VKV_GENERIC_ATTENTION")) {
+    const int64_t batch = rows / a.L;
+    a.n_parts = prefill_parts(batch, a.Hkv, a.L, a.Hq / a.Hkv, a.kv.T, &a.part_tokens);
+    if (a.n_parts > 1) {
+      const size_t per = static_cast<size_t>(rows) * a.Hq * a.n_parts;
+      float* ws = attention_workspace(st, per * (a.Dv + 2));
+      a.ws_o = ws;
+      a.ws_ml = ws + per * a.Dv;
+    }
+    launch_prefill(dtype, qsem, a, batch, st);
     return;
   }
   a.n_parts = choose_parts(rows * a.Hkv, max_len, &a.part_tokens);

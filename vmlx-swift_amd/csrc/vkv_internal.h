@@ -136,6 +136,11 @@ void launch_attn_combine(int dtype, const AttnArgs& a, int64_t rows, hipStream_t
 // qualifies (float, L = 1, dense, D = Dv in {64, 128, 256}, 16-byte aligned
 // rows), its token split (about 2048 waves, 64-token steps), and the launch
 // (with the merge when a.n_parts > 1).
+// Multi-query attention (L >= 2) over dense bf16 / f16 K/V, D = 128, no or
+// causal mask, on matrix cores (vkv_prefill.hip).
+bool prefill_supported(int dtype, int bits, const AttnArgs& a);
+int prefill_parts(int64_t batch, int Hkv, int64_t L, int rep, int64_t T, int32_t* part_tokens);
+void launch_prefill(int dtype, bool qsem, const AttnArgs& a, int64_t batch, hipStream_t st);
 bool fdecode_supported(int dtype, int bits, bool qsem, const AttnArgs& a);
 int fdecode_parts(int64_t rows_x_heads, int64_t T, int32_t* part_tokens);
 void launch_fdecode(int dtype, const AttnArgs& a, int64_t rows, hipStream_t st);
