@@ -15,7 +15,8 @@ Prints one JSON line: "value" is the whole-step KV-read rate (appends included),
 "attention" times the paged decode call (decode kernel + split-K merge),
 "roofline" the decode kernel alone (the library's event pair around it, on
 its launch stream), "traffic" is the PMC-measured HBM bytes per decode launch,
-"cpu_baseline" times the C oracle, and "mla" is the MLA latent decode workload
+"cpu_baseline" times the C oracle, "prefill" times a 512-token chunked-prefill
+attention step over a 4-bit cache, and "mla" is the MLA latent decode workload
 (32 x 16384 tokens, 128 heads) with the MFMA roofline of its attention kernel.
 """
 import argparse
@@ -151,6 +152,50 @@ def build_scene(torch, vkv, layers, seed=3):
     sc["views"] = [pool.view(l, sc["table"], sc["seq_lens"], sc["max_len"]) for l in range(layers)]
     torch.cuda.synchronize()
     return pool, sc
+
+
+def prefill_measure(torch, vkv, steps, warmup):
+    """The chunked-prefill step of a config-3-shaped layer: a 512-token
+    causal chunk appended to a 4-bit g64 QuantizedKVCache that holds a
+    4096-token prefix (32 query / 8 kv heads x 128, bf16), then attention of
+    the chunk over all 4608 tokens through attentionWithCacheUpdate.  One
+    step = one call (append + page gather + multi-query kernel), timed with
+    HIP events; the cache is trimmed back after each call."""
+    Hq, Hkv, D, T0, L = 32, 8, 128, 4096, 512
+    cache = vkv.QuantizedKVCache(group_size=64, bits=4)
+    k0 = torch.empty((1, Hkv, T0, D), dtype=torch.bfloat16, device="cuda")
+    v0 = torch.empty_like(k0)
+    vkv.fill_normal(k0, seed=31)
+    vkv.fill_normal(v0, seed=32)
+    cache.update_quantized(k0, v0)
+    q = torch.empty((1, Hq, L, D), dtype=torch.bfloat16, device="cuda")
+    k1 = torch.empty((1, Hkv, L, D), dtype=torch.bfloat16, device="cuda")
+    v1 = torch.empty_like(k1)
+    for t, sd in ((q, 33), (k1, 34), (v1, 35)):
+        vkv.fill_normal(t, seed=sd)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+
+    def call():
+        vkv.attention_with_cache_update(q, k1, v1, cache, D ** -0.5, mask="causal", out=out)
+        cache.trim(L)
+
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = 2.0 * 2 * Hq * D * L * (T0 + (L + 1) / 2)  # QK + PV over the causal keys
+    return {"workload": "chunked prefill: 512-token causal chunk over a 4096-token 4-bit g64 "
+                        "QuantizedKVCache, 32/8 heads x 128, bf16",
+            "ms_per_chunk": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+            "finite": bool(torch.isfinite(out.float()).all())}
 
 
 def mla_measure(torch, vkv, steps, warmup):
@@ -341,6 +386,7 @@ def main():
     dec_gbs = logical / (dec_avg_ms * 1e-3) / 1e9
     append_tokens = sc["n_seqs"] + sc["prefill"]
     mla = None if args.no_mla else mla_measure(torch, vkv, args.steps, args.warmup)
+    prefill = None if args.no_mla else prefill_measure(torch, vkv, args.steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
@@ -377,6 +423,7 @@ def main():
                      "traffic": pmc_traffic(), "kernel": "qdecode_kernel"},
         "cpu_baseline": cpu,
         "mla": mla,
+        "prefill": prefill,
     }
     print(json.dumps(rec), flush=True)
 
