@@ -764,26 +764,61 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(AttnArgs a, int h_off
   }
 }
 
+// One wave per (row, head): lane l merges dims l, l + 64, .. (Dv <= 256).
+// The (max, sum) pairs and partial rows of up to 8 parts are loaded before
+// any is used, so a merge costs one memory round trip per 8 parts.
 template <int DT>
-__global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int64_t n_rh) {
   using E = Elem<DT>;
-  const int64_t rh = blockIdx.x;  // row * Hq + h
+  const int64_t rh = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // row * Hq + h
+  if (rh >= n_rh) return;
+  const int lane = threadIdx.x & 63;
   const int64_t row = rh / a.Hq;
   const int h = static_cast<int>(rh % a.Hq);
   const int64_t b = row / a.L;
   const int l = static_cast<int>(row % a.L);
   const float* ml = a.ws_ml + rh * a.n_parts * 2;
-  float M = -3.402823466e38f;
-  for (int p = 0; p < a.n_parts; p++) M = fmaxf(M, ml[2 * p]);
-  float Lsum = 0.0f;
-  for (int p = 0; p < a.n_parts; p++) Lsum += __expf(ml[2 * p] - M) * ml[2 * p + 1];
-  for (int d = threadIdx.x; d < a.Dv; d += blockDim.x) {
-    float acc = 0.0f;
-    for (int p = 0; p < a.n_parts; p++)
-      acc += __expf(ml[2 * p] - M) * a.ws_o[(rh * a.n_parts + p) * a.Dv + d];
-    const float v = Lsum > 0.0f ? acc / Lsum : 0.0f;
-    static_cast<typename E::T*>(a.out)[b * a.o_sb + h * a.o_sh + static_cast<int64_t>(l) * a.o_sl +
-                                       d] = E::from_f32(v);
+  const float* wo = a.ws_o + rh * a.n_parts * a.Dv;
+  float M = -3.402823466e38f, den = 0.0f;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c = 0; c < a.n_parts; c += 8) {
+    float m[8], ls[8], v[8][4];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int p = min(c + j, a.n_parts - 1);  // (clamped slots are selected away)
+      m[j] = ml[2 * p];
+      ls[j] = ml[2 * p + 1];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int d = lane + 64 * i;
+        v[j][i] = d < a.Dv ? wo[static_cast<int64_t>(p) * a.Dv + d] : 0.0f;
+      }
+    }
+    float Mc = M;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      if (c + j < a.n_parts) Mc = fmaxf(Mc, m[j]);
+    const float r = __expf(M - Mc);
+    den *= r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] *= r;
+    M = Mc;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      if (c + j < a.n_parts) {
+        const float w = __expf(m[j] - M);
+        den += w * ls[j];
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = fmaf(w, v[j][i], acc[i]);
+      }
+    }
+  }
+  typename E::T* out = static_cast<typename E::T*>(a.out) + b * a.o_sb + h * a.o_sh +
+                       static_cast<int64_t>(l) * a.o_sl;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int d = lane + 64 * i;
+    if (d < a.Dv) out[d] = E::from_f32(den > 0.0f ? acc[i] / den : 0.0f);
   }
 }
 
@@ -1022,9 +1057,11 @@ static void attn_dispatch_rep(const AttnArgs& a, int64_t rows, hipStream_t st) {
 #undef VKV_A
     done += chunk;
   }
-  if (a.n_parts > 1)
-    hipLaunchKernelGGL((attn_combine_kernel<DT>), dim3(static_cast<unsigned>(rows * a.Hq)), dim3(256),
-                       0, st, a);
+  if (a.n_parts > 1) {
+    const int64_t n_rh = rows * a.Hq;
+    hipLaunchKernelGGL((attn_combine_kernel<DT>), dim3(static_cast<unsigned>((n_rh + 3) / 4)),
+                       dim3(256), 0, st, a, n_rh);
+  }
 }
 
 template <int DT>
@@ -1042,11 +1079,13 @@ static void attn_dispatch(int bits, bool qsem, const AttnArgs& a, int64_t rows, 
 }
 
 void launch_attn_combine(int dtype, const AttnArgs& a, int64_t rows, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(rows * a.Hq));
+  if (a.Dv > 256) throw Error("attention merge supports value dims up to 256");
+  const int64_t n_rh = rows * a.Hq;
+  const dim3 grid(static_cast<unsigned>((n_rh + 3) / 4));
   switch (dtype) {
-    case kF32: hipLaunchKernelGGL((attn_combine_kernel<kF32>), grid, dim3(256), 0, st, a); break;
-    case kF16: hipLaunchKernelGGL((attn_combine_kernel<kF16>), grid, dim3(256), 0, st, a); break;
-    case kBF16: hipLaunchKernelGGL((attn_combine_kernel<kBF16>), grid, dim3(256), 0, st, a); break;
+    case kF32: hipLaunchKernelGGL((attn_combine_kernel<kF32>), grid, dim3(256), 0, st, a, n_rh); break;
+    case kF16: hipLaunchKernelGGL((attn_combine_kernel<kF16>), grid, dim3(256), 0, st, a, n_rh); break;
+    case kBF16: hipLaunchKernelGGL((attn_combine_kernel<kBF16>), grid, dim3(256), 0, st, a, n_rh); break;
     default: throw Error("unsupported dtype");
   }
   VKV_HIP(hipGetLastError());
