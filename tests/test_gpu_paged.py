@@ -102,6 +102,24 @@ def test_paged_quantized_append_gather_attention(bits, dtype):
         assert (np.abs(out[s] - ref) <= attn_tol(dtype, ref)).all(), s
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 128])
+def test_paged_quantized_gather_f32_groups(bits, group):
+    """Dequant-on-read of f32 affine blocks (two 16-byte stores per 8 dims)
+    with groups of 32 and 128, bit-exact with the oracle dequantizer."""
+    dtype = O.F32
+    rng = np.random.default_rng(40 + bits + group)
+    P = Paged(rng, bits, dtype, n_seqs=4, D=128)
+    P.pool = vkv.PagedPool(96, P.bs, 1, P.Hkv, P.D, dtype=dtype, bits=bits, group_size=group)
+    P.append_all()
+    kd, vd = vkv.paged_gather(P.view())
+    for s, L in enumerate(P.lens):
+        for src, got in ((P.tokens[s], kd), (P.vals[s], vd)):
+            x = np.ascontiguousarray(src.transpose(1, 0, 2))
+            rq, rs, rb, _ = O.quantize(x, dtype, group, bits)
+            assert np.array_equal(host(got[s, :, :L]), O.dequantize(rq, rs, rb, dtype, group, bits)), s
+
+
 def test_paged_decode_step_crosses_block_boundary():
     dtype, bits = O.BF16, 4
     rng = np.random.default_rng(21)

@@ -114,20 +114,18 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
       float* ws = attention_workspace(st, copy_floats + (d.n_parts > 1 ? per * (a.Dv + 2) : 0));
       uint8_t* kd = reinterpret_cast<uint8_t*>(ws);
       uint8_t* vd = kd + kv_bytes;
-      for (int which = 0; which < 2; which++) {
-        GatherArgs g{};
-        g.kv = a.kv;
-        g.n_seqs = static_cast<int32_t>(batch);
-        g.H = a.Hkv;
-        g.T = static_cast<int32_t>(T);
-        g.D = a.D;
-        g.which = which;
-        g.bits = bits;
-        g.group = group;
-        g.dtype = dtype;
-        g.out = which ? vd : kd;
-        launch_gather(g, 0, st);
-      }
+      GatherArgs g{};
+      g.kv = a.kv;
+      g.n_seqs = static_cast<int32_t>(batch);
+      g.H = a.Hkv;
+      g.T = static_cast<int32_t>(T);
+      g.D = a.D;
+      g.bits = bits;
+      g.group = group;
+      g.dtype = dtype;
+      g.out = kd;
+      g.out_v = vd;
+      launch_gather(g, 0, st);
       d.kv.kc.ptr = kd;
       d.kv.vc.ptr = vd;
       if (d.n_parts > 1) {

@@ -942,6 +942,25 @@ void QuantizedCache::update_quantized(const vkv_array& k, const vkv_array& v, hi
   const vkv_array* arr[2] = {&k, &v};
   ChunkLayout L = chunk_layout(bits_, dtype_, kBlock, static_cast<int>(D_), static_cast<int>(D_), group_,
                                false);
+  if (append_affine_supported(bits_, group_, static_cast<int>(D_))) {
+    // K and V in one launch; a chunk of whole 8-token groups writes its
+    // 4-bit V words with plain stores instead of per-nibble atomics
+    const int G = static_cast<int>(D_ / group_);
+    RowSrc sk{k.data, B, Sn, H, k.strides[0], k.strides[2], k.strides[1]};
+    RowSrc sv{v.data, B, Sn, H, v.strides[0], v.strides[2], v.strides[1]};
+    RowDst dk = affine_dst(store_.bytes(), block_bytes_, head_bytes_, kBlock, L, 0, G, false);
+    RowDst dv = affine_dst(store_.bytes(), block_bytes_, head_bytes_, kBlock, L, 1, G, false);
+    for (RowDst* d : {&dk, &dv}) {
+      d->table = static_cast<const int32_t*>(table_.get());
+      d->table_stride = static_cast<int32_t>(nblk_);
+      d->seq_S = static_cast<int32_t>(Sn);
+      d->start = static_cast<int32_t>(prev);
+    }
+    launch_append_affine(dtype_, bits_, group_, sk, sv, dk, dv, B * Sn, static_cast<int>(H),
+                         static_cast<int>(D), true, st);
+    *out = view();
+    return;
+  }
   for (int which = 0; which < 2; which++) {
     const vkv_array& a = *arr[which];
     RowSrc src{a.data, a.shape[0], a.shape[2], a.shape[1], a.strides[0], a.strides[2], a.strides[1]};

@@ -121,6 +121,8 @@ struct GatherArgs {
   void* out;        // [n,H,T,D] values, or [n,H,T,D*bits/32] u32 codes
   void* out_s;      // [n,H,T,D/group]
   void* out_b;
+  void* out_v;      // values (out_kind 0): non-null gathers K into out and V
+                    //   into out_v in one call (which is then ignored)
 };
 void launch_gather(const GatherArgs& g, int out_kind, hipStream_t st);
 // Strided 4-D copy (element size 2 or 4): dst[i] = src[i].

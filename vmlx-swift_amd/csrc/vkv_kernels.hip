@@ -475,6 +475,115 @@ __global__ void __launch_bounds__(256) gather_kernel(GatherArgs g) {
   }
 }
 
+// Dequantizing gather, 8 dims per piece: one code word (4-bit) or two
+// (8-bit) and one scale/bias pair (a group spans a multiple of 8 dims), then
+// one 16-byte store of bf16/f16 (two of f32).  The values are those of
+// gather_kernel<.., 0>: the fp32 scale * code + bias rounded to the dtype.
+// blockIdx.y is the (seq, head) plane; with gridDim.z == 2, blockIdx.z picks
+// K (into out) or V (into out_v) in one launch.  A thread takes
+// kGatherPieces pieces 256 apart and issues all their loads before its first
+// store (one piece measured fastest: more workgroups keep more loads in
+// flight).  Needs D and group multiples of 8, 4-byte aligned code rows and a
+// 16-byte aligned output (gather8_ok).
+constexpr int kGatherPieces = 1;
+
+template <int DT, int BITS>
+__global__ void __launch_bounds__(256) gather_dequant8_kernel(GatherArgs g) {
+  using E = Elem<DT>;
+  constexpr uint32_t kMask = (1u << BITS) - 1u;
+  const int tpr = g.D >> 3;
+  const int plane = blockIdx.y, s = plane / g.H, h = plane - s * g.H;
+  const int len = min(g.T, static_cast<int>(g.kv.seq_lens ? g.kv.seq_lens[s] : g.kv.T));
+  if (len <= 0) return;  // an empty sequence may own no block
+  const KVSrc& kv = g.kv;
+  const bool ko = kv.keys_only != 0;
+  const int which = gridDim.z > 1 ? static_cast<int>(blockIdx.z) : g.which;
+  void* const out = which && gridDim.z > 1 ? g.out_v : g.out;
+  const int w = (which && !ko) ? 1 : 0;
+  uint32_t w0[kGatherPieces], w1[kGatherPieces], c4[kGatherPieces][8];
+  float sc[kGatherPieces], bi[kGatherPieces];
+  bool live[kGatherPieces];
+  int ti[kGatherPieces], d0[kGatherPieces];
+#pragma unroll
+  for (int k = 0; k < kGatherPieces; k++) {
+    const int idx = (blockIdx.x * kGatherPieces + k) * 256 + static_cast<int>(threadIdx.x);
+    ti[k] = idx / tpr;
+    d0[k] = (idx - ti[k] * tpr) * 8;
+    live[k] = ti[k] < len;
+    const int t = live[k] ? ti[k] : 0;  // dead pieces load token 0 (in bounds) and store nothing
+    TokLoc l;
+    if (kv.table) {
+      const int b = t / kv.block_size;
+      l.blk = kv.table[static_cast<int64_t>(s) * kv.table_stride + b];
+      l.tib = t - b * kv.block_size;
+    } else {
+      l.blk = s;
+      l.tib = t;
+    }
+    const int gi = d0[k] / g.group;
+    w0[k] = w1[k] = 0u;
+    if (kv.qfmt) {
+      const uint8_t* chunk = kv.base + l.blk * kv.block_bytes + h * kv.head_bytes;
+      const typename E::T* sb = reinterpret_cast<const typename E::T*>(chunk + kv.sb_off);
+      sc[k] = E::load(sb + qsb_index(l.tib, w, gi, 0, kv.G, ko));
+      bi[k] = E::load(sb + qsb_index(l.tib, w, gi, 1, kv.G, ko));
+      if (w == 0) {
+        // the 8 dims are original word d0/8 (4-bit) or words d0/4, d0/4 + 1
+        // (8-bit), which the chunk keeps side by side
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(
+            chunk + kv.kc_off + qk_word_off(l.tib, d0[k] * BITS / 32, kv.D, BITS));
+        w0[k] = p[0];
+        if (BITS == 8) w1[k] = p[1];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          int sh;
+          const uint32_t word = *reinterpret_cast<const uint32_t*>(
+              chunk + kv.vc_off + qv_word_off(l.tib, d0[k] + i, kv.D, BITS, &sh));
+          c4[k][i] = (word >> sh) & kMask;
+        }
+      }
+    } else {
+      const Comp& cc = which ? kv.vc : kv.kc;
+      const Comp& scp = which ? kv.vs : kv.ks;
+      const Comp& bcp = which ? kv.vb : kv.kb;
+      sc[k] = E::load(reinterpret_cast<const typename E::T*>(at(scp, l, h)) + gi);
+      bi[k] = E::load(reinterpret_cast<const typename E::T*>(at(bcp, l, h)) + gi);
+      const uint32_t* p = reinterpret_cast<const uint32_t*>(at(cc, l, h) + d0[k] * BITS / 8);
+      w0[k] = p[0];
+      if (BITS == 8) w1[k] = p[1];
+    }
+  }
+  const bool word_codes = !kv.qfmt || w == 0;
+#pragma unroll
+  for (int k = 0; k < kGatherPieces; k++) {
+    if (!live[k]) continue;
+    uint32_t c[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      c[i] = !word_codes ? c4[k][i]
+             : BITS == 4 ? (w0[k] >> (4 * i)) & kMask
+                         : ((i < 4 ? w0[k] : w1[k]) >> (8 * (i & 3))) & kMask;
+    typename E::T* o = static_cast<typename E::T*>(out) +
+                       (static_cast<int64_t>(plane) * g.T + ti[k]) * g.D + d0[k];
+    if constexpr (E::kBytes == 2) {
+      uint32_t pk[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        pk[i] = static_cast<uint32_t>(E::from_f32(fmaf(sc[k], static_cast<float>(c[2 * i]), bi[k]))) |
+                static_cast<uint32_t>(E::from_f32(fmaf(sc[k], static_cast<float>(c[2 * i + 1]), bi[k])))
+                    << 16;
+      *reinterpret_cast<uint4*>(o) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    } else {
+      float f[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) f[i] = fmaf(sc[k], static_cast<float>(c[i]), bi[k]);
+      reinterpret_cast<float4*>(o)[0] = make_float4(f[0], f[1], f[2], f[3]);
+      reinterpret_cast<float4*>(o)[1] = make_float4(f[4], f[5], f[6], f[7]);
+    }
+  }
+}
+
 // Reference-layout affine rows -> paged chunks (inverse of the code gather).
 template <int ESIZE, int BITS>
 __global__ void __launch_bounds__(256) scatter_codes_kernel(ScatterCodesArgs a) {
@@ -935,10 +1044,50 @@ void launch_dequantize(int dtype, int bits, int group, const uint32_t* wq, const
   VKV_HIP(hipGetLastError());
 }
 
+// Whether gather_dequant8_kernel's vector accesses fit the view.
+static bool gather8_ok(const GatherArgs& g) {
+  if (g.D % 8 || g.group % 8 || reinterpret_cast<uintptr_t>(g.out) % 16 ||
+      reinterpret_cast<uintptr_t>(g.out_v) % 16)
+    return false;
+  const auto a4 = [](int64_t x) { return x % 4 == 0; };
+  const KVSrc& kv = g.kv;
+  if (kv.qfmt)
+    return a4(static_cast<int64_t>(reinterpret_cast<uintptr_t>(kv.base))) && a4(kv.block_bytes) &&
+           a4(kv.head_bytes) && a4(kv.kc_off) && a4(kv.vc_off);
+  for (int which = 0; which < 2; which++) {
+    if (which != g.which && !g.out_v) continue;
+    const Comp& c = which ? kv.vc : kv.kc;
+    if (!(a4(static_cast<int64_t>(reinterpret_cast<uintptr_t>(c.ptr))) && a4(c.sb) && a4(c.sh) &&
+          a4(c.st)))
+      return false;
+  }
+  return true;
+}
+
 template <int DT, int BITS>
 static void gather_dispatch_kind(const GatherArgs& g, int out_kind, hipStream_t st) {
   const unsigned nb = blocks_for(static_cast<int64_t>(g.n_seqs) * g.H * g.T * ((g.D + 7) / 8));
   if (out_kind == 0) {
+    if constexpr (BITS > 0) {
+      const int64_t planes = static_cast<int64_t>(g.n_seqs) * g.H;
+      const int64_t per_plane = static_cast<int64_t>(g.T) * (g.D / 8);
+      if (gather8_ok(g) && planes > 0 && planes <= 65535 && per_plane > 0 && per_plane < (1 << 30)) {
+        const dim3 grid(static_cast<unsigned>((per_plane + 256 * kGatherPieces - 1) / (256 * kGatherPieces)),
+                        static_cast<unsigned>(planes), g.out_v ? 2u : 1u);
+        hipLaunchKernelGGL((gather_dequant8_kernel<DT, BITS>), grid, dim3(256), 0, st, g);
+        return;
+      }
+    }
+    if (g.out_v) {  // element-wise kernel: one launch per matrix
+      GatherArgs one = g;
+      one.out_v = nullptr;
+      for (int which = 0; which < 2; which++) {
+        one.which = which;
+        one.out = which ? g.out_v : g.out;
+        hipLaunchKernelGGL((gather_kernel<DT, BITS, 0>), dim3(nb), dim3(256), 0, st, one);
+      }
+      return;
+    }
     hipLaunchKernelGGL((gather_kernel<DT, BITS, 0>), dim3(nb), dim3(256), 0, st, g);
   } else {
     if constexpr (BITS > 0) {
