@@ -4,7 +4,9 @@ vkv_sdpa (vkv_prefill.hip), against the oracle's SDPA and against the
 generic kernel (VKV_GENERIC_ATTENTION=1): GQA groups of 1, 4 and 8, key
 counts that are not multiples of the 32-token tile, query counts that are
 not multiples of the 256-row block, several key splits, strided slices of
-cache buffers and two batch rows."""
+cache buffers and two batch rows.  Quantized K/V (a QuantizedKVCache's
+paged chunks, or reference-layout code/scale/bias arrays) with 16+ query
+tokens take the same kernel after a gather to bf16 rows."""
 import numpy as np
 import pytest
 import torch
@@ -134,3 +136,31 @@ def test_quantized_cache_chunk_outlier_channels(bits):
     qs = f(O.from_f32(f(q) * st, dtype))
     ref = O.sdpa(qs, f(kd), f(vd), 1.0, mask="causal")
     assert (np.abs(got - ref) <= attn_tol(dtype, ref)).all(), np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("L,mask", [(32, "causal"), (48, None)])
+def test_quantized_sdpa_reference_layout_chunk(bits, L, mask, monkeypatch):
+    """Stateless quantized SDPA over reference-layout (codes, scales, biases)
+    arrays with 16+ query tokens: gathered to bf16 rows, then the
+    matrix-core kernel; against the oracle's quantized SDPA and against the
+    generic path."""
+    dtype, B, Hq, Hkv, T, D = O.BF16, 2, 16, 4, 333, 128
+    rng = np.random.default_rng(60 + bits + L)
+    q = rand_bits(rng, (B, Hq, L, D), dtype)
+    kx, vx = (rand_bits(rng, (B, Hkv, T, D), dtype) for _ in range(2))
+    kq, ks, kb, _ = O.quantize(kx, dtype, 64, bits)
+    vq, vs, vb, _ = O.quantize(vx, dtype, 64, bits)
+    t = lambda a: torch.from_numpy(a.view(np.int32)).cuda()
+    args = (dev(q, dtype), (t(kq), dev(ks, dtype), dev(kb, dtype)),
+            (t(vq), dev(vs, dtype), dev(vb, dtype)), D ** -0.5)
+    run = lambda: values(vkv.quantized_scaled_dot_product_attention(
+        *args, mask=mask, group_size=64, bits=bits), dtype)
+    got = run()
+    f = lambda a: O.to_f32(a, dtype)
+    ref = O.quantized_sdpa(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64, bits,
+                           mask=mask)
+    tol = attn_tol(dtype, ref)
+    assert (np.abs(got - ref) <= tol).all(), np.abs(got - ref).max()
+    monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
+    assert (np.abs(got - run()) <= tol).all()
