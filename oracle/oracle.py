@@ -17,6 +17,11 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 F32, F16, BF16 = 0, 1, 2
 
+# quantized-SDPA arithmetic (vkvo_quantized_sdpa): exact fp64; the
+# reference's rounding on the vector (qmv) path; on the matrix (qmm) path;
+# and the vector path with a softmax computed in the query dtype.
+EXACT, QMV, QMM, QMV_ACC_T = 0, 1, 2, 3
+
 _lib = None
 
 
@@ -52,14 +57,16 @@ def _declare(L):
     L.vkvo_from_f32.argtypes = [vp, i64, i32, vp]
     L.vkvo_quantize.restype = i64
     L.vkvo_quantize.argtypes = [vp, i32, i64, i32, i32, i32, vp, vp, vp]
-    L.vkvo_dequantize.argtypes = [vp, vp, vp, i32, i64, i32, i32, i32, vp]
+    L.vkvo_dequantize.argtypes = [vp, vp, vp, i32, i64, i32, i32, i32, i32, vp]
+    L.vkvo_dequantize_rule_split.restype = i64
+    L.vkvo_dequantize_rule_split.argtypes = [vp, vp, vp, i32, i64, i32, i32, i32]
     L.vkvo_sdpa.argtypes = [vp, vp, vp] + [i32] * 7 + [f32, i32, vp, vp] + [i64] * 4 + [vp]
     L.vkvo_quantized_sdpa.argtypes = (
-        [vp, i32] + [vp] * 6 + [i32] * 8 + [f32, i32, vp, vp] + [i64] * 4 + [vp]
+        [vp, i32] + [vp] * 6 + [i32] * 8 + [f32, i32, vp, vp] + [i64] * 4 + [i32, vp, vp]
     )
     L.vkvo_mla_decode.argtypes = [vp, vp, vp, vp, i32, i32, i32, vp, i32, i32, i32, i32, f32, vp]
     L.vkvo_quantized_decode_batch.argtypes = (
-        [vp, i32] + [vp] * 6 + [i32, vp, vp, i32, i32, i32, i32, i32, f32, i32, vp]
+        [vp, i32] + [vp] * 6 + [i32, vp, vp, i32, i32, i32, i32, i32, f32, i32, i32, vp]
     )
 
 
@@ -97,16 +104,27 @@ def quantize(w: np.ndarray, dtype: int, group: int = 64, bits: int = 4):
     return wq, sc, bi, int(ties)
 
 
-def dequantize(wq, scales, biases, dtype: int, group: int = 64, bits: int = 4):
+def dequantize(wq, scales, biases, dtype: int, group: int = 64, bits: int = 4, rule: int = 0):
+    """rule 0: T(scale*q + bias) rounded once; rule 1: T(T(scale*q) + bias)."""
     wq = np.ascontiguousarray(wq, dtype=np.uint32)
     D = wq.shape[-1] * 32 // bits
     rows = wq.size // wq.shape[-1]
     out = np.empty(wq.shape[:-1] + (D,), np_dtype(dtype))
     lib().vkvo_dequantize(
         _p(wq), _p(np.ascontiguousarray(scales)), _p(np.ascontiguousarray(biases)),
-        dtype, rows, D, group, bits, _p(out)
+        dtype, rows, D, group, bits, rule, _p(out)
     )
     return out
+
+
+def dequantize_rule_split(wq, scales, biases, dtype: int, group: int = 64, bits: int = 4) -> int:
+    """Elements where the one- and two-rounding dequantize rules differ."""
+    wq = np.ascontiguousarray(wq, dtype=np.uint32)
+    D = wq.shape[-1] * 32 // bits
+    rows = wq.size // wq.shape[-1]
+    return int(lib().vkvo_dequantize_rule_split(
+        _p(wq), _p(np.ascontiguousarray(scales)), _p(np.ascontiguousarray(biases)),
+        dtype, rows, D, group, bits))
 
 
 def _mask_args(mask, B, H, L, T):
@@ -142,8 +160,13 @@ def sdpa(q, k, v, scale, mask=None):
     return out
 
 
-def quantized_sdpa(q, q_dtype, kq, ks, kb, vq, vs, vb, scale, group=64, bits=4, mask=None):
-    """Reference-layout quantized cache; scales/biases as f32 values."""
+def quantized_sdpa(q, q_dtype, kq, ks, kb, vq, vs, vb, scale, group=64, bits=4, mask=None,
+                   rounding=QMV, bound=False):
+    """Reference-layout quantized cache; scales/biases as f32 values.
+
+    rounding: EXACT, QMV (default: the reference's decode arithmetic), QMM
+    or QMV_ACC_T (see vkvo_quantized_sdpa).  With bound=True also returns
+    the per-output weight-rounding bound sum_t |w_t - p_t| |v_t|."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     B, Hq, L, D = q.shape
     Hkv, T = kq.shape[1], kq.shape[2]
@@ -152,9 +175,11 @@ def quantized_sdpa(q, q_dtype, kq, ks, kb, vq, vs, vb, scale, group=64, bits=4, 
              (vq, np.uint32), (vs, np.float32), (vb, np.float32))]
     mode, mb, mf, st, keep = _mask_args(mask, B, Hq, L, T)
     out = np.empty((B, Hq, L, D), np.float64)
+    wb = np.empty((B, Hq, L, D), np.float64) if bound else None
     lib().vkvo_quantized_sdpa(_p(q), q_dtype, *[_p(a) for a in arrs], B, Hq, Hkv, L, T, D,
-                              group, bits, scale, mode, _p(mb), _p(mf), *st, _p(out))
-    return out
+                              group, bits, scale, mode, _p(mb), _p(mf), *st, rounding,
+                              _p(out), _p(wb))
+    return (out, wb) if bound else out
 
 
 def mla_decode(q, cq, cs, cb, lens, scale, Dv=512, group=64, bits=8):
@@ -171,7 +196,7 @@ def mla_decode(q, cq, cs, cb, lens, scale, Dv=512, group=64, bits=8):
 
 
 def quantized_decode_batch(q, q_dtype, kq, ks, kb, vq, vs, vb, lens, tok_off, Hkv, scale,
-                           group=64, bits=4, threads=1):
+                           group=64, bits=4, threads=1, rounding=QMV):
     q = np.ascontiguousarray(q, dtype=np.float32)
     nseq, Hq, D = q.shape
     out = np.empty((nseq, Hq, D), np.float64)
@@ -180,5 +205,5 @@ def quantized_decode_batch(q, q_dtype, kq, ks, kb, vq, vs, vb, lens, tok_off, Hk
         _p(q), q_dtype, *[_p(a) for a in arrs], nseq,
         _p(np.ascontiguousarray(lens, dtype=np.int32)),
         _p(np.ascontiguousarray(tok_off, dtype=np.int64)), Hq, Hkv, D, group, bits, scale,
-        threads, _p(out))
+        rounding, threads, _p(out))
     return out

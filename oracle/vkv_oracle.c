@@ -10,12 +10,17 @@
  *   vkvo_quantize   -- IntegrationTests.swift:3890-3923 aggregates on the
  *                      reproduced MLX stream (seed 869), plus closed-form
  *                      invariants and a brute-force tiny-alphabet sweep.
- *   vkvo_dequantize -- |w - deq| <= |scale|/2 away from the clamp and exact
- *                      reconstruction of the group's edge element.
+ *   vkvo_dequantize -- both rules against independent library arithmetic
+ *                      (numpy fp64 + torch casts), |w - deq| <= |scale|/2
+ *                      away from the clamp, exact edge reconstruction; which
+ *                      rule the reference uses is unpinned (counted).
  *   vkvo_sdpa       -- MLXFastKernelTests.swift:101-111 known answer (seed 0),
  *                      single-key / uniform-score / fully-masked special cases.
- *   vkvo_quantized_sdpa -- equals vkvo_sdpa on the dequantized cache with the
- *                      input-dtype query scaling; fully masked row = mean(V).
+ *   vkvo_quantized_sdpa -- exact mode equals vkvo_sdpa on the dequantized
+ *                      cache with the input-dtype query scaling; rounding
+ *                      modes pinned by closed-form cases (scores closer than
+ *                      half a T ulp weigh the same; three equal scores give
+ *                      weights T(1/3)); fully masked row = mean(V).
  *   vkvo_mla_decode -- equals vkvo_sdpa with Hkv = 1 on dequantized entries.
  *   conversions     -- exhaustive bf16/f16 round trips and numpy's f16 cast.
  */
@@ -191,9 +196,23 @@ static inline uint32_t code_at(const uint32_t *row, int e, int bits) {
   return (row[e / per_word] >> (bits * (e % per_word))) & ((1u << bits) - 1u);
 }
 
-/* quantized.h:2498-2560 (affine_dequantize): scale * q + bias. */
+/* quantized.h:2498-2560 (affine_dequantize): out[i] = scale * d + bias with
+ * `T scale`, `T bias` (:2538-2539) and the code d an integer (:2548-2559).
+ * Evaluated in T, that expression rounds twice (the product to T, then the
+ * sum) unless the compiler contracts it into one fused multiply-add, which
+ * rounds once.  Which of the two the reference's build does is not fixed by
+ * any file in the reference tree (it depends on the Metal compiler's
+ * contraction setting), so both are restated: rule 0 = one rounding of the
+ * exact s*q + b (the fused form; this build's kernels), rule 1 = T(T(s*q) + b).
+ * vkvo_dequantize_rule_split counts the elements where they differ. */
+static inline float deq_rule(float s, float q, float b, int dtype, int rule) {
+  if (rule == 0 || dtype == 0) return round_to(fmaf(s, q, b), dtype);
+  return round_to(round_to(s * q, dtype) + b, dtype);
+}
+
 void vkvo_dequantize(const uint32_t *wq, const void *scales, const void *biases,
-                     int dtype, int64_t rows, int D, int group, int bits, void *out) {
+                     int dtype, int64_t rows, int D, int group, int bits, int rule,
+                     void *out) {
   const int words_per_row = D * bits / 32;
   const int groups = D / group;
   for (int64_t r = 0; r < rows; r++) {
@@ -201,9 +220,25 @@ void vkvo_dequantize(const uint32_t *wq, const void *scales, const void *biases,
       float s = load_val(scales, dtype, r * groups + e / group);
       float b = load_val(biases, dtype, r * groups + e / group);
       float q = (float)code_at(wq + r * words_per_row, e, bits);
-      store_val(out, dtype, r * D + e, fmaf(s, q, b));
+      store_val(out, dtype, r * D + e, deq_rule(s, q, b, dtype, rule));
     }
   }
+}
+
+int64_t vkvo_dequantize_rule_split(const uint32_t *wq, const void *scales,
+                                   const void *biases, int dtype, int64_t rows, int D,
+                                   int group, int bits) {
+  const int words_per_row = D * bits / 32;
+  const int groups = D / group;
+  int64_t n = 0;
+  for (int64_t r = 0; r < rows; r++)
+    for (int e = 0; e < D; e++) {
+      float s = load_val(scales, dtype, r * groups + e / group);
+      float b = load_val(biases, dtype, r * groups + e / group);
+      float q = (float)code_at(wq + r * words_per_row, e, bits);
+      n += deq_rule(s, q, b, dtype, 0) != deq_rule(s, q, b, dtype, 1);
+    }
+  return n;
 }
 
 static inline int mask_visible(int mask_mode, const uint8_t *bmask, const float *fmask,
@@ -261,45 +296,183 @@ void vkvo_sdpa(const float *q, const float *k, const float *v, int B, int Hq,
   free(vis);
 }
 
+/* Dequantized element of a reference-layout row: the exact value
+ * scale * q + bias (fp64, as qmv's fp32 `scale * sum(x q) + bias * sum(x)`
+ * forms it, quantized.h:1493-1648), or that value rounded once to the
+ * storage dtype when the multi-row qmm path first dequantizes its tiles into
+ * threadgroup memory of type T (quantized.h:568-576, :686-713). */
+static inline double deq_at(const uint32_t *row, const float *s, const float *b, int d,
+                            int group, int bits, int round_dt) {
+  const double x = (double)s[d / group] * (double)code_at(row, d, bits) + (double)b[d / group];
+  return round_dt >= 0 ? (double)round_to((float)x, round_dt) : x;
+}
+
+static inline double round_d(double x, int dtype) {
+  return (double)round_to((float)x, dtype);
+}
+
+/* Softmax weights of one row of scores (KVCache.swift:1982, softmax with
+ * precise: false).  rnd == 0: exact fp64.  Otherwise the scores sc[] already
+ * carry the reference's rounding and:
+ *   acc_t < 0 : internal arithmetic in fp32 (AccT = float), weights
+ *               T(exp(s - max) * (1 / sum)) rounded to wdt;
+ *   acc_t >= 0: internal arithmetic in AccT = T (softmax.h's default
+ *               template argument), modelled on softmax_single_row
+ *               (softmax.h): every op rounded to T, 4 values summed per
+ *               thread, then 32-thread and threadgroup sums each rounded
+ *               once (the hardware reduction order is not in the tree).
+ * pe[] receives the exact fp64 softmax of the same scores (the unrounded
+ * weights a kernel that does not round them would use). */
+static void softmax_row(const double *sc, int T, int rnd, int acc_t, int wdt, double *p,
+                        double *pe) {
+  double mx = -INFINITY;
+  for (int t = 0; t < T; t++) mx = sc[t] > mx ? sc[t] : mx;
+  double den = 0.0;
+  for (int t = 0; t < T; t++) {
+    pe[t] = exp(sc[t] - mx);
+    den += pe[t];
+  }
+  for (int t = 0; t < T; t++) pe[t] /= den;
+  if (!rnd) {
+    for (int t = 0; t < T; t++) p[t] = pe[t];
+    return;
+  }
+  if (acc_t < 0) {
+    double sum = 0.0;
+    for (int t = 0; t < T; t++) {
+      p[t] = (double)(float)exp((double)(float)(sc[t] - mx));
+      sum += p[t];
+    }
+    const float r = (float)(1.0 / (double)(float)sum);
+    for (int t = 0; t < T; t++) p[t] = round_d((double)((float)p[t] * r), wdt);
+    return;
+  }
+  double total = 0.0, simd = 0.0, thr = 0.0;
+  for (int t = 0; t < T; t++) {
+    p[t] = round_d(exp(round_d(sc[t] - mx, acc_t)), acc_t);
+    thr = round_d(thr + p[t], acc_t);
+    if ((t & 3) == 3 || t == T - 1) {
+      simd += thr;
+      thr = 0.0;
+    }
+    if ((t & 127) == 127 || t == T - 1) {
+      total += round_d(simd, acc_t);
+      simd = 0.0;
+    }
+  }
+  const double r = round_d(1.0 / round_d(total, acc_t), acc_t);
+  for (int t = 0; t < T; t++) p[t] = round_d(p[t] * r, acc_t);
+}
+
+/* Neighbours of the T value r (T = f16 or bf16): the adjacent representable
+ * values below and above. */
+static void t_neighbours(double r, int dtype, double *below, double *above) {
+  const float rf = (float)r;
+  if (dtype == 2) {
+    uint16_t h = vkvo_f32_to_bf16(rf);
+    const int neg = (h & 0x8000u) != 0;
+    uint16_t up = (uint16_t)(neg ? h - 1 : h + 1), dn = (uint16_t)(neg ? h + 1 : h - 1);
+    if ((h & 0x7fffu) == 0) { up = 0x0001u; dn = 0x8001u; }
+    *above = vkvo_bf16_to_f32(up);
+    *below = vkvo_bf16_to_f32(dn);
+  } else {
+    uint16_t h = vkvo_f32_to_f16(rf);
+    const int neg = (h & 0x8000u) != 0;
+    uint16_t up = (uint16_t)(neg ? h - 1 : h + 1), dn = (uint16_t)(neg ? h + 1 : h - 1);
+    if ((h & 0x7fffu) == 0) { up = 0x0001u; dn = 0x8001u; }
+    *above = vkvo_f16_to_f32(up);
+    *below = vkvo_f16_to_f32(dn);
+  }
+}
+
 /* One query row against one KV head of a quantized cache (reference layout
- * rows of length D).  Shared by the batch and the CPU-baseline entry. */
+ * rows of length D).  Shared by the batch and the CPU-baseline entry.
+ * rnd: 0 exact, 1 qmv rounding, 2 qmm rounding, 3 qmv rounding with an
+ * AccT = T softmax (see vkvo_quantized_sdpa).  sdt: dtype the scores are
+ * rounded to (the query dtype); fmask_f32: an f32 additive mask was added
+ * (MLX promotes T + f32 to f32, so the scores and weights stay f32).
+ * wb (optional), per output dim: the most the reference's two roundings can
+ * move the output against the exact softmax of the rounded scores:
+ *   sum_t |w_t - pe_t| |v_t|  (the weights stored in T), plus
+ *   for every score within eps_t = 2^-17 sum_d |q_d k_td| of a T rounding
+ *   boundary, the exact change of the output if that score rounded to the
+ *   other side: an fp32 accumulation (the reference's qmv, or any kernel)
+ *   lands on either side of such a boundary depending on its order of
+ *   summation.  2^-17 is twice the largest relative score error measured
+ *   for this build's decode kernel on x20-outlier data. */
 static void qsdpa_row(const float *qs, const uint32_t *kq, const float *ks,
                       const float *kb, const uint32_t *vq, const float *vs,
                       const float *vb, int T, int D, int group, int bits,
                       const double *add, const unsigned char *vis, double fill,
-                      double *sc, double *o) {
+                      int rnd, int sdt, double *sc, double *pw, double *pe, double *o,
+                      double *wb) {
   const int wpr = D * bits / 32;
   const int G = D / group;
-  double mx = -INFINITY;
+  const int deq_dt = rnd == 2 ? sdt : -1;
+  const int wdt = add ? 0 : sdt;
+  /* flip factors exp(n_t - r_t) for scores near a rounding boundary (0: none) */
+  double *flip = (wb && rnd) ? (double *)calloc((size_t)(T > 0 ? T : 1), sizeof(double)) : NULL;
+  const int acc_t = (rnd == 3 && !add) ? sdt : -1;
   for (int t = 0; t < T; t++) {
     double s = fill;
     if (!vis || vis[t]) {
       const uint32_t *kr = kq + (int64_t)t * wpr;
       s = 0.0;
+      double mag = 0.0;
       for (int d = 0; d < D; d++) {
-        double kv = (double)ks[(int64_t)t * G + d / group] * (double)code_at(kr, d, bits) +
-                    (double)kb[(int64_t)t * G + d / group];
+        const double kv = deq_at(kr, ks + (int64_t)t * G, kb + (int64_t)t * G, d, group, bits,
+                                 deq_dt);
         s += (double)qs[d] * kv;
+        mag += fabs((double)qs[d] * kv);
       }
-      if (add) s += add[t];
+      if (rnd) {
+        const double r = round_d(s, sdt);
+        if (flip) {
+          double below, above;
+          t_neighbours(r, sdt, &below, &above);
+          const double eps = ldexp(mag, -17);
+          if (fabs(s - 0.5 * (r + above)) < eps) flip[t] = exp(above - r);
+          if (fabs(s - 0.5 * (r + below)) < eps) flip[t] = exp(below - r);
+        }
+        s = r;
+      }
+      if (add) s = rnd ? (double)(float)(s + add[t]) : s + add[t];
     }
     sc[t] = s;
-    if (s > mx) mx = s;
   }
-  double den = 0.0;
+  softmax_row(sc, T, rnd, acc_t, wdt, pw, pe);
+  double *o1 = wb ? (double *)calloc((size_t)D, sizeof(double)) : NULL;
   for (int d = 0; d < D; d++) o[d] = 0.0;
+  if (wb)
+    for (int d = 0; d < D; d++) wb[d] = 0.0;
   for (int t = 0; t < T; t++) {
-    double p = exp(sc[t] - mx);
-    den += p;
     const uint32_t *vr = vq + (int64_t)t * wpr;
     for (int d = 0; d < D; d++) {
-      double vv = (double)vs[(int64_t)t * G + d / group] * (double)code_at(vr, d, bits) +
-                  (double)vb[(int64_t)t * G + d / group];
-      o[d] += p * vv;
+      const double vv = deq_at(vr, vs + (int64_t)t * G, vb + (int64_t)t * G, d, group, bits,
+                               deq_dt);
+      o[d] += pw[t] * vv;
+      if (wb) {
+        wb[d] += fabs(pw[t] - pe[t]) * fabs(vv);
+        o1[d] += pe[t] * vv;
+      }
     }
   }
-  if (den > 0.0)
-    for (int d = 0; d < D; d++) o[d] /= den;
+  if (flip) {
+    /* a flipped score t scales its exponential by f: the output becomes
+     * (o1 + (f - 1) pe_t v_t) / (1 + (f - 1) pe_t) */
+    for (int t = 0; t < T; t++) {
+      if (flip[t] == 0.0) continue;
+      const double a = (flip[t] - 1.0) * pe[t];
+      const uint32_t *vr = vq + (int64_t)t * wpr;
+      for (int d = 0; d < D; d++) {
+        const double vv = deq_at(vr, vs + (int64_t)t * G, vb + (int64_t)t * G, d, group, bits,
+                                 deq_dt);
+        wb[d] += fabs((o1[d] + a * vv) / (1.0 + a) - o1[d]);
+      }
+    }
+  }
+  free(flip);
+  free(o1);
 }
 
 /* KVCache.swift:1909-1997 (quantizedScaledDotProductAttention). */
@@ -309,16 +482,19 @@ void vkvo_quantized_sdpa(const float *q, int q_dtype, const uint32_t *kq,
                          int L, int T, int D, int group, int bits, float scale,
                          int mask_mode, const uint8_t *bmask, const float *fmask,
                          int64_t msb, int64_t msh, int64_t msl, int64_t mst,
-                         double *out) {
+                         int rounding, double *out, double *wbound) {
   const int rep = Hq / Hkv;
   const int wpr = D * bits / 32;
   const int G = D / group;
   const float scale_t = round_to(scale, q_dtype);
   const double fill = type_lowest(q_dtype);
+  const size_t nT = (size_t)(T > 0 ? T : 1);
   float *qs = (float *)malloc(sizeof(float) * (size_t)D);
-  double *sc = (double *)malloc(sizeof(double) * (size_t)(T > 0 ? T : 1));
-  double *add = (double *)malloc(sizeof(double) * (size_t)(T > 0 ? T : 1));
-  unsigned char *vis = (unsigned char *)malloc((size_t)(T > 0 ? T : 1));
+  double *sc = (double *)malloc(sizeof(double) * nT);
+  double *pw = (double *)malloc(sizeof(double) * nT);
+  double *pe = (double *)malloc(sizeof(double) * nT);
+  double *add = (double *)malloc(sizeof(double) * nT);
+  unsigned char *vis = (unsigned char *)malloc(nT);
   for (int b = 0; b < B; b++)
     for (int h = 0; h < Hq; h++)
       for (int l = 0; l < L; l++) {
@@ -326,6 +502,7 @@ void vkvo_quantized_sdpa(const float *q, int q_dtype, const uint32_t *kq,
         for (int d = 0; d < D; d++) qs[d] = round_to(qr[d] * scale_t, q_dtype);
         const int hk = h / rep;
         const int64_t kv_row0 = ((int64_t)b * Hkv + hk) * T;
+        const int64_t orow = (((int64_t)b * Hq + h) * L + l) * D;
         for (int t = 0; t < T; t++) {
           double a;
           int64_t mo = b * msb + h * msh + l * msl + t * mst;
@@ -340,16 +517,20 @@ void vkvo_quantized_sdpa(const float *q, int q_dtype, const uint32_t *kq,
           }
         }
         if (T == 0) {
-          double *o = out + (((int64_t)b * Hq + h) * L + l) * D;
-          for (int d = 0; d < D; d++) o[d] = 0.0;
+          for (int d = 0; d < D; d++) out[orow + d] = 0.0;
+          if (wbound)
+            for (int d = 0; d < D; d++) wbound[orow + d] = 0.0;
           continue;
         }
         qsdpa_row(qs, kq + kv_row0 * wpr, ks + kv_row0 * G, kb + kv_row0 * G,
                   vq + kv_row0 * wpr, vs + kv_row0 * G, vb + kv_row0 * G, T, D, group,
-                  bits, add, vis, fill, sc, out + (((int64_t)b * Hq + h) * L + l) * D);
+                  bits, mask_mode == 3 ? add : NULL, vis, fill, rounding, q_dtype, sc, pw, pe,
+                  out + orow, wbound ? wbound + orow : NULL);
       }
   free(qs);
   free(sc);
+  free(pw);
+  free(pe);
   free(add);
   free(vis);
 }
@@ -359,7 +540,7 @@ void vkvo_quantized_decode_batch(const float *q, int q_dtype, const uint32_t *kq
                                  const float *vs, const float *vb, int nseq,
                                  const int32_t *lens, const int64_t *tok_off, int Hq,
                                  int Hkv, int D, int group, int bits, float scale,
-                                 int threads, double *out) {
+                                 int rounding, int threads, double *out) {
   const int rep = Hq / Hkv;
   const int wpr = D * bits / 32;
   const int G = D / group;
@@ -373,6 +554,8 @@ void vkvo_quantized_decode_batch(const float *q, int q_dtype, const uint32_t *kq
   {
     float *qs = (float *)malloc(sizeof(float) * (size_t)D);
     double *sc = (double *)malloc(sizeof(double) * (size_t)maxT);
+    double *pw = (double *)malloc(sizeof(double) * (size_t)maxT);
+    double *pe = (double *)malloc(sizeof(double) * (size_t)maxT);
 #ifdef _OPENMP
 #pragma omp for schedule(dynamic, 1) collapse(2)
 #endif
@@ -384,11 +567,13 @@ void vkvo_quantized_decode_batch(const float *q, int q_dtype, const uint32_t *kq
         /* sequence s is stored [Hkv, T, ...] starting at token row tok_off[s] */
         const int64_t row0 = tok_off[s] + (int64_t)(h / rep) * T;
         qsdpa_row(qs, kq + row0 * wpr, ks + row0 * G, kb + row0 * G, vq + row0 * wpr,
-                  vs + row0 * G, vb + row0 * G, (int)T, D, group, bits, NULL, NULL, 0.0, sc,
-                  out + ((int64_t)s * Hq + h) * D);
+                  vs + row0 * G, vb + row0 * G, (int)T, D, group, bits, NULL, NULL, 0.0,
+                  rounding, q_dtype, sc, pw, pe, out + ((int64_t)s * Hq + h) * D, NULL);
       }
     free(qs);
     free(sc);
+    free(pw);
+    free(pe);
   }
 }
 

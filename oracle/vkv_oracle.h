@@ -35,11 +35,17 @@ void vkvo_from_f32(const float *src, int64_t n, int dtype, void *dst);
 int64_t vkvo_quantize(const void *w, int dtype, int64_t rows, int D, int group,
                       int bits, uint32_t *wq, void *scales, void *biases);
 
-/* Dequantize (quantized.h:2498-2560): out = T(scale * q + bias), evaluated
- * as one fp32 fused multiply-add of the stored (rounded) scale/bias, rounded
- * once to T. */
+/* Dequantize (quantized.h:2498-2560): out = scale * q + bias in T.
+ * rule 0: the exact value rounded once to T (a fused multiply-add; the rule
+ * this build's kernels use); rule 1: T(T(scale * q) + bias), two roundings.
+ * The reference tree does not fix which one its compiled kernel performs. */
 void vkvo_dequantize(const uint32_t *wq, const void *scales, const void *biases,
-                     int dtype, int64_t rows, int D, int group, int bits, void *out);
+                     int dtype, int64_t rows, int D, int group, int bits, int rule,
+                     void *out);
+/* Number of elements where rules 0 and 1 above give different values. */
+int64_t vkvo_dequantize_rule_split(const uint32_t *wq, const void *scales,
+                                   const void *biases, int dtype, int64_t rows, int D,
+                                   int group, int bits);
 
 /* ---- float decode SDPA (MLXFast.swift:173-218, sdpa_vector.h:15-177) ----
  * q [B,Hq,L,D], k [B,Hkv,T,D], v [B,Hkv,T,Dv] as f32 values (exact images of
@@ -58,16 +64,35 @@ void vkvo_sdpa(const float *q, const float *k, const float *v, int B, int Hq,
  * the input dtype: qs = T(q * T(scale)) (MLXArray+Ops.swift:235-237,
  * DType.swift:389-396).  Keys/values in the reference layout
  * [B,Hkv,T,D*bits/32] u32 with scales/biases [B,Hkv,T,D/group] given as f32
- * values of the stored dtype.  Scores/softmax/PV in f64.  Masks as in
- * vkvo_sdpa except that masked scores are filled with finfo(T).min before the
- * softmax (so a fully masked row averages V, KVCache.swift:1950-1975). */
+ * values of the stored dtype.  Masks as in vkvo_sdpa except that masked
+ * scores are filled with finfo(T).min before the softmax (so a fully masked
+ * row averages V, KVCache.swift:1950-1975).
+ * rounding selects the arithmetic:
+ *   0  exact: scores, softmax and P.V in f64 (the limit of every rounding);
+ *   1  the reference's rounding on the vector path (affine_qmv / qvm,
+ *      quantized.h:1493-1764): scores accumulated exactly from the exact
+ *      dequantized keys, then stored in T (quantizedMM returns the query
+ *      dtype, KVCache.swift:1945-1949); an f32 additive mask promotes them
+ *      to f32 (:1969); softmax (:1982) with fp32 internals and its weights
+ *      stored in T; P.V accumulated exactly over the T weights;
+ *   2  as 1 on the matrix path (affine_qmm, quantized.h:568-576, :686-713):
+ *      keys and values are first dequantized to T (rule 0 above);
+ *   3  as 1 with the softmax's internal arithmetic in T (softmax.h's default
+ *      template argument AccT = T under precise: false), used to measure
+ *      the spread between the two unpinned softmax precisions.
+ * wbound (optional, [B,Hq,L,D], rounding modes only): the most the
+ * reference's roundings can move each output away from the exact softmax of
+ * the rounded scores: sum_t |w_t - pe_t| |v_t| for the weights stored in T,
+ * plus, for each score within 2^-17 sum_d |q_d k_td| of a T rounding
+ * boundary (where any fp32 accumulation may land on either side), the exact
+ * output change of rounding it the other way. */
 void vkvo_quantized_sdpa(const float *q, int q_dtype, const uint32_t *kq,
                          const float *ks, const float *kb, const uint32_t *vq,
                          const float *vs, const float *vb, int B, int Hq, int Hkv,
                          int L, int T, int D, int group, int bits, float scale,
                          int mask_mode, const uint8_t *bmask, const float *fmask,
                          int64_t msb, int64_t msh, int64_t msl, int64_t mst,
-                         double *out);
+                         int rounding, double *out, double *wbound);
 
 /* ---- MLA absorbed-latent decode (GLM4MOELite.swift:233-290,
  * AttentionUtils.swift:43-75) ----
@@ -81,8 +106,8 @@ void vkvo_mla_decode(const float *q, const uint32_t *cq, const float *cs,
                      const float *cb, int B, int H, int T, const int32_t *lens,
                      int Dk, int Dv, int group, int bits, float scale, double *out);
 
-/* CPU-baseline entry: the same quantized decode as vkvo_quantized_sdpa for
- * L == 1 without a mask, over `nseq` independent sequences of lengths lens[],
+/* CPU-baseline entry: the same quantized decode as vkvo_quantized_sdpa (with
+ * its rounding modes) for L == 1 without a mask, over `nseq` independent sequences of lengths lens[],
  * each stored contiguously [Hkv,T_i,...] at the given element offsets.  Uses
  * up to `threads` OpenMP threads (1 = scalar). */
 void vkvo_quantized_decode_batch(const float *q, int q_dtype, const uint32_t *kq,
@@ -90,7 +115,7 @@ void vkvo_quantized_decode_batch(const float *q, int q_dtype, const uint32_t *kq
                                  const float *vs, const float *vb, int nseq,
                                  const int32_t *lens, const int64_t *tok_off, int Hq,
                                  int Hkv, int D, int group, int bits, float scale,
-                                 int threads, double *out);
+                                 int rounding, int threads, double *out);
 
 #ifdef __cplusplus
 }

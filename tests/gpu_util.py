@@ -46,3 +46,42 @@ def attn_tol(dtype: int, ref: np.ndarray) -> np.ndarray:
     ulp = {O.BF16: 2.0 ** -8, O.F16: 2.0 ** -11, O.F32: 2.0 ** -23}[dtype]
     atol = 1e-4 if dtype == O.F32 else 2e-2
     return atol + ulp * np.abs(ref)
+
+
+def qref(*args, rounding=O.QMV, **kw):
+    """The oracle's quantized SDPA with the reference's rounding (scores and
+    softmax weights stored in the query dtype; QMM also dequantizes K/V to
+    the dtype first) and the per-output weight-rounding bound."""
+    return O.quantized_sdpa(*args, rounding=rounding, bound=True, **kw)
+
+
+def qattn_tol(dtype: int, ref: np.ndarray, wb: np.ndarray) -> np.ndarray:
+    """Tolerance against the reference-rounded oracle: attn_tol plus the
+    oracle's rounding bound wb, i.e. what the reference's roundings can move
+    each output: the softmax weights stored in the dtype (sum_t |w_t - p_t|
+    |v_t|; the kernels keep them in fp32, since rounding them needs the
+    row's final max and sum before any P.V, i.e. a second pass), and scores
+    within fp32 accumulation error of a dtype rounding boundary, which any
+    fp32 implementation (the reference's included) may round either way."""
+    return attn_tol(dtype, ref) + wb
+
+
+def assert_within(got, ref, tol, ctx="", wb=None):
+    """Element-wise |got - ref| <= tol, reporting the worst element (index,
+    values, tolerance, the rounding bound there) instead of whole arrays."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    excess = np.abs(got - ref) - np.asarray(tol)
+    if not (excess <= 0).all():
+        i = np.unravel_index(np.nanargmax(np.where(np.isnan(excess), np.inf, excess)),
+                             excess.shape)
+        extra = f" bound {np.asarray(wb)[i]:.4g}" if wb is not None else ""
+        raise AssertionError(
+            f"{ctx}: {(~(excess <= 0)).sum()} of {excess.size} outside tolerance; worst at {i}: "
+            f"got {got[i]:.6g} ref {ref[i]:.6g} err {abs(got[i] - ref[i]):.4g} "
+            f"tol {np.asarray(tol)[i]:.4g}{extra}; max err {np.nanmax(np.abs(got - ref)):.4g}")
+
+
+def assert_qclose(got, ref, wb, dtype, ctx=""):
+    """assert_within against the reference-rounded oracle (qattn_tol)."""
+    assert_within(got, ref, qattn_tol(dtype, ref, wb), ctx, wb)

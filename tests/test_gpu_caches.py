@@ -10,7 +10,7 @@ import torch
 import kvcache_ref as R
 import oracle as O
 import vkv
-from gpu_util import attn_tol, dev, host, rand_bits, values
+from gpu_util import assert_qclose, assert_within, qattn_tol, qref, attn_tol, dev, host, rand_bits, values
 
 pytestmark = pytest.mark.gpu
 
@@ -144,9 +144,9 @@ def test_quantized_cache_matches_restatement(bits):
             out = vkv.paged_attention(dev(q, dtype), view, D ** -0.5)
             kq, ks, kb, vq, vs, vb = r.state
             f = lambda a: O.to_f32(a, dtype)
-            ref = O.quantized_sdpa(f(q)[:, :, None], dtype, kq, f(ks), f(kb), vq, f(vs), f(vb),
-                                   D ** -0.5, 64, bits)[:, :, 0]
-            assert (np.abs(values(out, dtype) - ref) <= attn_tol(dtype, ref)).all()
+            ref, wb = (x[:, :, 0] for x in qref(f(q)[:, :, None], dtype, kq, f(ks), f(kb), vq,
+                                                f(vs), f(vb), D ** -0.5, 64, bits))
+            assert_qclose(values(out, dtype), ref, wb, dtype, f"S {S} bits {bits}")
     st = c.state
     for got, want in zip(st, r.state):
         assert np.array_equal(host(got).view(want.dtype), want)

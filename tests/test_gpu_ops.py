@@ -9,7 +9,7 @@ import torch
 import mlx_random as mr
 import oracle as O
 import vkv
-from gpu_util import attn_tol, dev, host, rand_bits, values
+from gpu_util import assert_qclose, assert_within, qattn_tol, qref, attn_tol, dev, host, rand_bits, values
 
 pytestmark = pytest.mark.gpu
 
@@ -180,7 +180,7 @@ def test_quantized_sdpa_matches_oracle(dtype, bits, mask):
         dev(q, dtype), (t(kq), dev(ks, dtype), dev(kb, dtype)), (t(vq), dev(vs, dtype), dev(vb, dtype)),
         scale, mask=m_dev, group_size=64, bits=bits)
     f = lambda a: O.to_f32(a, dtype)
-    ref = O.quantized_sdpa(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), scale, 64, bits,
-                           mask=m_ref)
+    ref, wb = qref(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), scale, 64, bits,
+                   mask=m_ref)
     got = values(out, dtype)
-    assert (np.abs(got - ref) <= attn_tol(dtype, ref)).all()
+    assert_qclose(got, ref, wb, dtype, f"{dtype} {bits} {mask}")

@@ -10,7 +10,7 @@ import torch
 
 import oracle as O
 import vkv
-from gpu_util import attn_tol, dev, host, rand_bits, values
+from gpu_util import assert_qclose, assert_within, qattn_tol, qref, attn_tol, dev, host, rand_bits, values
 
 pytestmark = pytest.mark.gpu
 
@@ -96,10 +96,10 @@ def test_paged_quantized_append_gather_attention(bits, dtype):
             assert np.array_equal(host((kd, vd)[which][s, :, :L]), deq)
         rk = O.quantize(np.ascontiguousarray(P.tokens[s].transpose(1, 0, 2)), dtype, 64, bits)
         rv = O.quantize(np.ascontiguousarray(P.vals[s].transpose(1, 0, 2)), dtype, 64, bits)
-        ref = O.quantized_sdpa(f(q[s])[None, :, None], dtype, rk[0][None], f(rk[1])[None],
+        ref, wb = (x[0, :, 0] for x in qref(f(q[s])[None, :, None], dtype, rk[0][None], f(rk[1])[None],
                                f(rk[2])[None], rv[0][None], f(rv[1])[None], f(rv[2])[None], scale,
-                               64, bits)[0, :, 0]
-        assert (np.abs(out[s] - ref) <= attn_tol(dtype, ref)).all(), s
+                               64, bits))
+        assert_qclose(out[s], ref, wb, dtype, f"seq {s}")
 
 
 @pytest.mark.parametrize("bits", [4, 8])
@@ -206,10 +206,10 @@ def test_paged_decode_shapes_and_partitions(bits, D, rep, bs, Hkv):
     for s, L in enumerate(lens):
         rk = O.quantize(np.ascontiguousarray(P.tokens[s].transpose(1, 0, 2)), dtype, 64, bits)
         rv = O.quantize(np.ascontiguousarray(P.vals[s].transpose(1, 0, 2)), dtype, 64, bits)
-        ref = O.quantized_sdpa(f(q[s])[None, :, None], dtype, rk[0][None], f(rk[1])[None],
+        ref, wb = (x[0, :, 0] for x in qref(f(q[s])[None, :, None], dtype, rk[0][None], f(rk[1])[None],
                                f(rk[2])[None], rv[0][None], f(rv[1])[None], f(rv[2])[None],
-                               D ** -0.5, 64, bits)[0, :, 0]
-        assert (np.abs(out[s] - ref) <= attn_tol(dtype, ref)).all(), s
+                               D ** -0.5, 64, bits))
+        assert_qclose(out[s], ref, wb, dtype, f"seq {s}")
 
 
 def test_generic_and_matrix_core_paths_agree(monkeypatch):
@@ -249,10 +249,10 @@ def test_decode_wave_counts_agree(monkeypatch, waves):
     for s, L in enumerate(P.lens):
         rk = O.quantize(np.ascontiguousarray(P.tokens[s].transpose(1, 0, 2)), dtype, 64, bits)
         rv = O.quantize(np.ascontiguousarray(P.vals[s].transpose(1, 0, 2)), dtype, 64, bits)
-        ref = O.quantized_sdpa(f(qh[s])[None, :, None], dtype, rk[0][None], f(rk[1])[None],
+        ref, wb = (x[0, :, 0] for x in qref(f(qh[s])[None, :, None], dtype, rk[0][None], f(rk[1])[None],
                                f(rk[2])[None], rv[0][None], f(rv[1])[None], f(rv[2])[None], 0.088,
-                               64, bits)[0, :, 0]
-        assert (np.abs(got[s] - ref) <= attn_tol(dtype, ref)).all(), s
+                               64, bits))
+        assert_qclose(got[s], ref, wb, dtype, f"seq {s}")
 
 
 def test_append_aligned_groups_ragged_and_scattered_slots():

@@ -13,7 +13,7 @@ import torch
 
 import oracle as O
 import vkv
-from gpu_util import attn_tol, dev, rand_bits, values
+from gpu_util import assert_qclose, assert_within, qattn_tol, qref, attn_tol, dev, rand_bits, values
 
 pytestmark = pytest.mark.gpu
 
@@ -78,11 +78,11 @@ def test_prefill_large_scores_rescale():
     run_case(rng, O.BF16, 1, 16, 4, 40, 600, "causal", scale=0.5)
 
 
-def quantized_chunk(rng, bits, outliers):
-    """A 64-token causal chunk through the router over a QuantizedKVCache
-    holding a 300-token prefix: returns the output, the chunk's inputs and
-    the whole (prefix + chunk) K/V."""
-    dtype, Hq, Hkv, D, T0, L = O.BF16, 32, 8, 128, 300, 64
+def quantized_chunk(rng, bits, outliers, T0=300, L=64, Hkv=8):
+    """An L-token causal chunk through the router over a QuantizedKVCache
+    holding a T0-token prefix (GQA 4): returns the output, the chunk's
+    inputs and the whole (prefix + chunk) K/V."""
+    dtype, Hq, D = O.BF16, 4 * Hkv, 128
     k0, v0 = (rand_bits(rng, (1, Hkv, T0, D), dtype, outliers=outliers) for _ in range(2))
     k1, v1 = (rand_bits(rng, (1, Hkv, L, D), dtype, outliers=outliers) for _ in range(2))
     q = rand_bits(rng, (1, Hq, L, D), dtype)
@@ -108,34 +108,31 @@ def test_quantized_cache_chunk(bits, monkeypatch):
     kq, ks, kb, _ = O.quantize(kx, dtype, 64, bits)
     vq, vs, vb, _ = O.quantize(vx, dtype, 64, bits)
     f = lambda a: O.to_f32(a, dtype)
-    ref = O.quantized_sdpa(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64, bits,
-                           mask="causal")
-    tol = attn_tol(dtype, ref)
-    assert (np.abs(got - ref) <= tol).all(), np.abs(got - ref).max()
+    ref, wb = qref(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64, bits,
+                   mask="causal", rounding=O.QMM)
+    tol = qattn_tol(dtype, ref, wb)
+    assert_within(got, ref, tol, "oracle", wb)
     monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
     gen = step()
-    assert (np.abs(got - gen) <= tol).all()
+    assert_within(got, gen, attn_tol(dtype, ref) + 2 * wb, "generic", wb)
 
 
 @pytest.mark.parametrize("bits", [4, 8])
 def test_quantized_cache_chunk_outlier_channels(bits):
-    """Config-2 data (4 channels per head scaled x20): the chunk path attends
-    over the cache dequantized to bf16 (the values the reference's dequantize
-    produces) with the quantized-SDPA query rounding (queries times the
-    bf16-rounded scale, rounded to bf16); checked against the oracle's float
-    SDPA over exactly those operands."""
+    """Config-2 data (4 channels per head scaled x20), a 512-token chunk
+    over a 4096-token cache: against the reference's matrix-path rounding
+    (affine_qmm dequantizes K/V tiles to bf16, quantized.h:568-576,
+    :686-713; scores and weights stored in bf16, KVCache.swift:1945-1982)."""
     dtype, D = O.BF16, 128
-    step, q, kx, vx = quantized_chunk(np.random.default_rng(10 + bits), bits, 4)
+    step, q, kx, vx = quantized_chunk(np.random.default_rng(10 + bits), bits, 4, T0=3584,
+                                      L=512, Hkv=2)
     got = step()
     kq, ks, kb, _ = O.quantize(kx, dtype, 64, bits)
     vq, vs, vb, _ = O.quantize(vx, dtype, 64, bits)
-    kd = O.dequantize(kq, ks, kb, dtype, 64, bits)
-    vd = O.dequantize(vq, vs, vb, dtype, 64, bits)
     f = lambda a: O.to_f32(a, dtype)
-    st = f(O.from_f32(np.array([D ** -0.5], np.float32), dtype))[0]
-    qs = f(O.from_f32(f(q) * st, dtype))
-    ref = O.sdpa(qs, f(kd), f(vd), 1.0, mask="causal")
-    assert (np.abs(got - ref) <= attn_tol(dtype, ref)).all(), np.abs(got - ref).max()
+    ref, wb = qref(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64, bits,
+                   mask="causal", rounding=O.QMM)
+    assert_qclose(got, ref, wb, dtype, f"bits {bits}")
 
 
 @pytest.mark.parametrize("bits", [4, 8])
@@ -158,9 +155,9 @@ def test_quantized_sdpa_reference_layout_chunk(bits, L, mask, monkeypatch):
         *args, mask=mask, group_size=64, bits=bits), dtype)
     got = run()
     f = lambda a: O.to_f32(a, dtype)
-    ref = O.quantized_sdpa(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64, bits,
-                           mask=mask)
-    tol = attn_tol(dtype, ref)
-    assert (np.abs(got - ref) <= tol).all(), np.abs(got - ref).max()
+    ref, wb = qref(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64, bits,
+                   mask=mask, rounding=O.QMM)
+    tol = qattn_tol(dtype, ref, wb)
+    assert_within(got, ref, tol, "oracle", wb)
     monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
-    assert (np.abs(got - run()) <= tol).all()
+    assert_within(got, run(), attn_tol(dtype, ref) + 2 * wb, "generic", wb)

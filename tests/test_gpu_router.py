@@ -10,7 +10,7 @@ import pytest
 import kvcache_ref as R
 import oracle as O
 import vkv
-from gpu_util import attn_tol, dev, host, rand_bits, values
+from gpu_util import assert_qclose, assert_within, qattn_tol, qref, attn_tol, dev, host, rand_bits, values
 
 pytestmark = pytest.mark.gpu
 
@@ -61,10 +61,11 @@ def test_router_quantized_cache(bits):
                                               D ** -0.5, mask=mask)
         r.update_quantized(k, v, dtype)
         kq, ks, kb, vq, vs, vb = r.state
-        ref = O.quantized_sdpa(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64,
-                               bits, mask=mask)
+        # 16+ query tokens run on the matrix (qmm) path, fewer on the vector path
+        ref, wb = qref(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64,
+                       bits, mask=mask, rounding=O.QMM if L >= 16 else O.QMV)
         assert c.offset == r.offset
-        assert close(out, ref, dtype), L
+        assert_qclose(values(out, dtype), ref, wb, dtype, f"L {L}")
 
 
 def test_router_rotating_cache_decode():

@@ -3,19 +3,22 @@
 //
 // Semantics: quantizedScaledDotProductAttention
 // (Libraries/MLXLMCommon/KVCache.swift:1909-1997) for one query token per
-// sequence: queries scaled in bf16, scores q.dequant(K), softmax, P.dequant(V),
-// fp32 accumulation, output rounded to bf16.  Split-K partials are merged as
+// sequence: queries scaled in bf16, scores q.dequant(K) accumulated in fp32
+// and stored in bf16 as the reference's quantizedMM stores them, softmax,
+// P.dequant(V), fp32 accumulation, output rounded to bf16.  Split-K partials are merged as
 // sdpa_vector_2pass_2 merges them
 // (Source/Cmlx/mlx-generated/metal/sdpa_vector.h:320-394).
 //
 // Arithmetic.  Both contractions run as 16x16x32 bf16 MFMAs directly on the
 // codes, so the vector ALUs only unpack codes and run the softmax:
-//   * a 4-bit code c enters as bf16(128 + c), bit pattern 0x4300 | c, which
-//     is exact; an 8-bit code c = 16*hi + lo enters as two operands,
-//     bf16(128 + lo) = 0x4300 | lo and bf16(2048 + 16*hi) = 0x4500 | hi, whose
-//     sum is c + 2176 (MAG);
+//   * a 4-bit value code c enters as bf16(128 + c), bit pattern 0x4300 | c,
+//     which is exact; an 8-bit value code c = 16*hi + lo enters as two
+//     operands, bf16(128 + lo) = 0x4300 | lo and bf16(2048 + 16*hi) =
+//     0x4500 | hi, whose sum is c + 2176 (MAG); key codes use smaller
+//     offsets (KMAG = 16 + c, or 272 + c as bf16(16 + lo) + bf16(256 + 16 hi)),
+//     which keeps the fp32 score error small before its rounding to bf16;
 //   * per-(token, group) scale s and bias b are applied around the
-//     contraction:  q.(s*c + b) = s * q.(MAG + c) + (b - MAG s) * sum(q), and
+//     contraction:  q.(s*c + b) = s * q.(KMAG + c) + (b - KMAG s) * sum(q), and
 //     sum_t p_t (s_t c_t + b_t) = sum_t P_t (MAG + c_t)
 //                                 + sum_t p_t (b_t + C0 s_t) - (MAG + C0) sum_t P_t
 //     with P_t = p_t s_t carried as two bf16 operands (hi + lo, about 16
@@ -119,8 +122,10 @@ __device__ __forceinline__ f32x4_t mfma(const u32x4_t& a, const u32x4_t& b, cons
 // v_and_or_b32.
 struct Magic {
   uint32_t m128, m2048;  // 0x43004300 (128 + c), 0x45004500 (2048 + 16 c)
-  __device__ __forceinline__ Magic() : m128(0x43004300u), m2048(0x45004500u) {
-    asm volatile("" : "+v"(m128), "+v"(m2048));
+  uint32_t m16, m256;    // 0x41804180 (16 + c), 0x43804380 (256 + 16 c)
+  __device__ __forceinline__ Magic()
+      : m128(0x43004300u), m2048(0x45004500u), m16(0x41804180u), m256(0x43804380u) {
+    asm volatile("" : "+v"(m128), "+v"(m2048), "+v"(m16), "+v"(m256));
   }
 };
 
@@ -131,6 +136,22 @@ __device__ __forceinline__ u32x4_t nib_magic(uint32_t w, const Magic& mg) {
   r[1] = ((w >> 4) & 0x000F000Fu) | mg.m128;
   r[2] = ((w >> 8) & 0x000F000Fu) | mg.m128;
   r[3] = ((w >> 12) & 0x000F000Fu) | mg.m128;
+  return r;
+}
+
+// Key operands with small offsets: 8 nibbles -> bf16 (16 + nibble), whose
+// mantissa unit is 1/8, so the nibble goes in three bits up.  The score is
+// s * q.(KMAG + c) + (b - KMAG s) * sum(q); the fp32 rounding of the two
+// KMAG terms that cancel grows with KMAG, and the scores are rounded to
+// bf16 afterwards, so a small KMAG keeps them on the same side of a bf16
+// rounding boundary as the exact score far more often (16 against 128: ~4x
+// fewer flips on outlier data).
+__device__ __forceinline__ u32x4_t nib_magic_k(uint32_t w, const Magic& mg) {
+  u32x4_t r;
+  r[0] = ((w << 3) & 0x00780078u) | mg.m16;
+  r[1] = ((w >> 1) & 0x00780078u) | mg.m16;
+  r[2] = ((w >> 5) & 0x00780078u) | mg.m16;
+  r[3] = ((w >> 9) & 0x00780078u) | mg.m16;
   return r;
 }
 
@@ -146,6 +167,20 @@ __device__ __forceinline__ void byte_magic(uint32_t x, uint32_t y, const Magic& 
   hi[1] = ((x >> 12) & 0x000F000Fu) | mg.m2048;
   hi[2] = ((y >> 4) & 0x000F000Fu) | mg.m2048;
   hi[3] = ((y >> 12) & 0x000F000Fu) | mg.m2048;
+}
+
+// The same for key operands with small offsets: low nibbles as bf16
+// (16 + lo), high nibbles as bf16 (256 + 16 hi), KMAG = 272.
+__device__ __forceinline__ void byte_magic_k(uint32_t x, uint32_t y, const Magic& mg, u32x4_t& lo,
+                                             u32x4_t& hi) {
+  lo[0] = ((x << 3) & 0x00780078u) | mg.m16;
+  lo[1] = ((x >> 5) & 0x00780078u) | mg.m16;
+  lo[2] = ((y << 3) & 0x00780078u) | mg.m16;
+  lo[3] = ((y >> 5) & 0x00780078u) | mg.m16;
+  hi[0] = ((x >> 1) & 0x00780078u) | mg.m256;
+  hi[1] = ((x >> 9) & 0x00780078u) | mg.m256;
+  hi[2] = ((y >> 1) & 0x00780078u) | mg.m256;
+  hi[3] = ((y >> 9) & 0x00780078u) | mg.m256;
 }
 
 // Dim (within an 8-dim unit) carried by MFMA K element j of a key operand:
@@ -278,7 +313,8 @@ struct QD {
   static constexpr int QROW = 16 * SPW + 1;   // query-table entries per slice
   static constexpr int QCH = HP * D / 8;      // 8-dim query chunks of a head group
   static constexpr int QPL = (QCH + 63) / 64; // query chunks per lane
-  static constexpr float MAG = (BITS == 4) ? 128.0f : 2176.0f;
+  static constexpr float MAG = (BITS == 4) ? 128.0f : 2176.0f;   // value operands
+  static constexpr float KMAG = (BITS == 4) ? 16.0f : 272.0f;    // key operands
   static constexpr float C0 = (BITS == 4) ? 8.0f : 128.0f;
   // per-step operand registers; steps are double buffered when they fit
   static constexpr int BUF = D * UW / 4 + HP * D / 32;
@@ -309,7 +345,7 @@ qdecode_kernel(DecodeArgs a) {
   constexpr int G = C::G, PP = C::PP, TT = C::TT, SPW = C::SPW, SL = C::SL;
   constexpr int RUN = C::RUN, NT = C::NT, VW = C::VW, ROW = C::ROW, SBW = C::SBW;
   constexpr int QROW = C::QROW, QCH = C::QCH, QPL = C::QPL;
-  constexpr float MAG = C::MAG, C0 = C::C0;
+  constexpr float MAG = C::MAG, KMAG = C::KMAG, C0 = C::C0;
   using Buf = typename C::Buf;
   constexpr int QT_ENTRIES = SL * QROW;
   static_assert(QT_ENTRIES * 16 >= kMaxSeqs * 8, "the sequence scan reuses the query table");
@@ -632,7 +668,7 @@ qdecode_kernel(DecodeArgs a) {
 
   auto compute_step = [&](int stp, const Buf& b) __attribute__((always_inline)) {
     const int len = seg_len;
-    // ---- scores: acc[tau][g] = q . (MAG + c) over group g's dims
+    // ---- scores: acc[tau][g] = q . (KMAG + c) over group g's dims
     f32x4_t acc[TT][G];
 #pragma unroll
     for (int tau = 0; tau < TT; tau++)
@@ -656,10 +692,10 @@ qdecode_kernel(DecodeArgs a) {
 #pragma unroll
       for (int tau = 0; tau < TT; tau++) {
         if constexpr (BITS == 4) {
-          acc[tau][g] = mfma(nib_magic(b.kw[tau][rho][kq], mg), qb, acc[tau][g]);
+          acc[tau][g] = mfma(nib_magic_k(b.kw[tau][rho][kq], mg), qb, acc[tau][g]);
         } else {
           u32x4_t lo, hi;
-          byte_magic(b.kw[tau][rho][2 * kq], b.kw[tau][rho][2 * kq + 1], mg, lo, hi);
+          byte_magic_k(b.kw[tau][rho][2 * kq], b.kw[tau][rho][2 * kq + 1], mg, lo, hi);
           acc[tau][g] = mfma(lo, qb, acc[tau][g]);
           acc[tau][g] = mfma(hi, qb, acc[tau][g]);
         }
@@ -676,12 +712,14 @@ qdecode_kernel(DecodeArgs a) {
         for (int g = 0; g < G; g++) {
           const uint32_t kwd = b.sb[tau][i][g], vwd = b.sb[tau][i][G + g];
           const float ks = bf_lo(kwd);
-          s = fmaf(fmaf(-MAG, ks, bf_hi(kwd)), sq[g], s);
+          s = fmaf(fmaf(-KMAG, ks, bf_hi(kwd)), sq[g], s);
           s = fmaf(ks, acc[tau][g][i], s);
           vs[tau][i][g] = bf_lo(vwd);
           vb[tau][i][g] = bf_hi(vwd);
         }
-        sc[tau][i] = s;
+        // the reference stores the scores in the query dtype before the
+        // softmax (quantizedMM returns T, KVCache.swift:1945-1949)
+        sc[tau][i] = round_to<kBF16>(s);
       }
     if (stp * 64 + 64 > len) {  // the sequence ends inside this step
       asm volatile("");  // a real branch: keeps the masking off the common path

@@ -706,8 +706,8 @@ __global__ void __launch_bounds__(256) fill_normal_kernel(void* data, int64_t n,
 // (sdpa_vector.h:320-394); a single-partition launch normalises in place.
 //
 // QSEM selects the quantized-SDPA semantics of KVCache.swift:1909-1997:
-// queries scaled in T, masked scores set to T's lowest value (so a fully
-// masked row averages V).  Otherwise MLXFast semantics: queries scaled in
+// queries scaled in T, scores rounded to T, masked scores set to T's lowest
+// value (so a fully masked row averages V).  Otherwise MLXFast semantics: queries scaled in
 // fp32, masked keys skipped, an empty row yields zeros.
 constexpr int kTile = 32;
 constexpr int kMaxD = 256;
@@ -775,7 +775,9 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(AttnArgs a, int h_off
       if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < REP; r++) {
-          float s = acc[r];
+          // quantized SDPA stores the scores in the dtype (quantizedMM
+          // returns T, KVCache.swift:1945-1949) before the mask is applied
+          float s = QSEM ? round_to<DT>(acc[r]) : acc[r];
           bool vis = t < t_end;
           if (vis && a.mask_mode != 0) {
             const int h = hk * rep_total + h_off + r;

@@ -123,9 +123,9 @@ __device__ __forceinline__ void lds_barrier() {
 __device__ __forceinline__ void tile_wait_one() { asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); }
 __device__ __forceinline__ void tile_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// QSEM: the quantized-SDPA query scaling (queries times the scale rounded to
-// the dtype, rounded again, KVCache.swift:1909-1997) instead of fp32 scores
-// times the scale.
+// QSEM: the quantized-SDPA arithmetic (KVCache.swift:1909-1997): queries
+// times the scale rounded to the dtype, rounded again, instead of fp32 scores
+// times the scale; scores rounded to the dtype before the softmax.
 template <int DT, bool QSEM>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 prefill_kernel(const AttnArgs a, int rep) {
@@ -286,6 +286,12 @@ prefill_kernel(const AttnArgs a, int rep) {
 #pragma unroll
       for (int rb = 0; rb < 2; rb++) {
         f32x16_t& x = sc[rb];
+        if constexpr (QSEM) {
+          // the scores are stored in the dtype (quantizedMM returns T,
+          // KVCache.swift:1945-1949) before the mask and the softmax
+#pragma unroll
+          for (int j = 0; j < 16; j++) x[j] = round_to<DT>(x[j]);
+        }
         if (__builtin_amdgcn_ballot_w64(edge)) {
           const int64_t lim = min<int64_t>(kmax[rb], k_end - 1) - t0;
 #pragma unroll
