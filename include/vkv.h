@@ -430,6 +430,16 @@ int vkv_block_hash(const char *parent_hash, const int64_t *tokens, int64_t n_tok
  * the reference's `x * 1` owned copy (KVCache.swift:100-102). */
 int vkv_array_copy(const vkv_array *src, vkv_array *dst, void *stream);
 
+/* Attention workspace of a stream (no reference counterpart; the reference
+ * allocates per op through MLX's allocator).  The attention calls keep one
+ * split-K workspace per stream that only grows; an outgrown buffer is kept,
+ * not freed, because a HIP graph captured earlier on that stream still
+ * points at it, and growth during capture is refused (run the call once
+ * before capturing).  vkv_workspace_release frees the stream's workspace and
+ * every outgrown buffer (*bytes, optional, receives the total); call it only
+ * when no captured graph that used the stream will be replayed again. */
+int vkv_workspace_release(void *stream, int64_t *bytes);
+
 /* ------------------------------------------------------- kernel timing */
 
 /* Kernel timing, a measurement aid with no counterpart in the reference:

@@ -212,3 +212,69 @@ def test_prefix_manager_matches_restatement_randomized():
                 a.free_block(x)
                 b.free_block(x)
             assert a.stats == b.stats, (trial, step)
+
+
+def _desc(shape, dtype, addr=0x1000):
+    """A vkv_array descriptor with a placeholder device address (never
+    dereferenced: these calls fail validation before any launch)."""
+    a = vkv.Array()
+    a.data = C.c_void_p(addr)
+    a.dtype = dtype
+    a.ndim = len(shape)
+    st = 1
+    for i in reversed(range(len(shape))):
+        a.shape[i] = shape[i]
+        a.strides[i] = st
+        st *= shape[i]
+    return a
+
+
+def _qsdpa_args(B=2, Hq=8, Hkv=2, L=1, T=40, D=128, bits=4, g=64, dt=2):
+    q = _desc((B, Hq, L, D), dt)
+    k = [_desc((B, Hkv, T, D * bits // 32), 3), _desc((B, Hkv, T, D // g), dt),
+         _desc((B, Hkv, T, D // g), dt)]
+    v = [_desc((B, Hkv, T, D * bits // 32), 3), _desc((B, Hkv, T, D // g), dt),
+         _desc((B, Hkv, T, D // g), dt)]
+    out = _desc((B, Hq, L, D), dt)
+    return q, k, v, out
+
+
+def _call_qsdpa(q, k, v, out, bits=4):
+    L = vkv.lib()
+    return L.vkv_quantized_sdpa(C.byref(q), *[C.byref(x) for x in k + v], 64, bits,
+                                C.c_float(0.1), 0, None, C.byref(out), None)
+
+
+@pytest.mark.parametrize("case", [
+    "out_heads", "out_len", "out_dim", "out_dtype", "v_batch", "v_heads", "k_scales_T",
+    "v_biases_heads", "biases_dtype", "codes_dtype", "k_scales_last", "v_codes_last", "gqa",
+])
+def test_quantized_sdpa_rejects_mismatched_tuples(case):
+    """Every tuple array must be [B, Hkv, T, .] with the right last dim and
+    dtype, and out [B, Hq, L, D] in q's dtype; a mismatch is an error return
+    before any device work (no GPU needed)."""
+    q, k, v, out = _qsdpa_args()
+    bad = {
+        "out_heads": lambda: setattr_shape(out, 1, 4),
+        "out_len": lambda: setattr_shape(out, 2, 3),
+        "out_dim": lambda: setattr_shape(out, 3, 64),
+        "out_dtype": lambda: setattr(out, "dtype", 1),
+        "v_batch": lambda: setattr_shape(v[0], 0, 1),
+        "v_heads": lambda: setattr_shape(v[0], 1, 4),
+        "k_scales_T": lambda: setattr_shape(k[1], 2, 39),
+        "v_biases_heads": lambda: setattr_shape(v[2], 1, 1),
+        "biases_dtype": lambda: setattr(k[2], "dtype", 0),
+        "codes_dtype": lambda: setattr(k[0], "dtype", 2),
+        "k_scales_last": lambda: setattr_shape(k[1], 3, 4),
+        "v_codes_last": lambda: setattr_shape(v[0], 3, 32),
+        "gqa": lambda: [setattr_shape(x, 1, 3) for x in k + v],
+    }[case]
+    bad()
+    assert _call_qsdpa(q, k, v, out) == 1
+    msg = vkv.lib().vkv_last_error()
+    # a validation message, not a failed device call
+    assert b"must" in msg and b"device" not in msg and b"hip" not in msg, msg
+
+
+def setattr_shape(a, i, n):
+    a.shape[i] = n

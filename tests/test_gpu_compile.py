@@ -220,3 +220,67 @@ def test_compiled_decode_step_graph_replay():
     kc, vc = cap.state
     kt, vt = twin.state
     assert torch.equal(kc, kt) and torch.equal(vc, vt)
+
+
+def _paged_scene(rng, n_seqs, L, Hkv=8, D=128, bs=32, bits=4):
+    nb = n_seqs * ((L + bs - 1) // bs) + 1
+    pool = vkv.PagedPool(nb, bs, 1, Hkv, D, dtype=vkv.BF16, bits=bits)
+    tab = (1 + np.arange(n_seqs * ((L + bs - 1) // bs), dtype=np.int32)).reshape(n_seqs, -1)
+    slots = [int(tab[s, p // bs]) * bs + p % bs for s in range(n_seqs) for p in range(L)]
+    k = rand_bits(rng, (n_seqs * L, Hkv, D), O.BF16)
+    v = rand_bits(rng, (n_seqs * L, Hkv, D), O.BF16)
+    pool.append(0, dev(k, O.BF16), dev(v, O.BF16),
+                torch.tensor(slots, dtype=torch.int32, device="cuda"))
+    tab_dev = torch.from_numpy(tab).cuda()
+    lens = torch.full((n_seqs,), L, dtype=torch.int32, device="cuda")
+    return pool, pool.view(0, tab_dev, lens, L), (tab_dev, lens)
+
+
+def test_workspace_growth_after_capture_keeps_graph_valid():
+    """A paged decode step captured in a graph keeps the stream workspace
+    address it was captured with.  A larger eager call on the same stream
+    then grows the workspace; the outgrown buffer must stay allocated, so
+    later replays still equal the eager result.  Growth during a capture is
+    refused with an error instead of allocating."""
+    rng = np.random.default_rng(41)
+    D, Hq = 128, 32
+    small = _paged_scene(rng, 4, 1500)
+    big = _paged_scene(rng, 48, 700)
+    q_small = dev(rand_bits(rng, (4, Hq, D), O.BF16), O.BF16)
+    q_big = dev(rand_bits(rng, (48, Hq, D), O.BF16), O.BF16)
+    out = torch.empty((4, Hq, D), dtype=torch.bfloat16, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    print("workspace: warm + capture", flush=True)
+    with torch.cuda.stream(s):
+        vkv.paged_attention(q_small, small[1], D ** -0.5, out=torch.empty_like(out))
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            vkv.paged_attention(q_small, small[1], D ** -0.5, out=out)
+    torch.cuda.synchronize()
+    want = vkv.paged_attention(q_small, small[1], D ** -0.5)
+    print("workspace: grow on the capture stream", flush=True)
+    with torch.cuda.stream(s):
+        big_out = vkv.paged_attention(q_big, big[1], D ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(big_out, vkv.paged_attention(q_big, big[1], D ** -0.5))
+    for r in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), r
+    # growth under capture: a fresh stream has no workspace yet
+    s2 = torch.cuda.Stream()
+    g2 = torch.cuda.CUDAGraph()
+    print("workspace: growth under capture is refused", flush=True)
+    with pytest.raises(vkv.VKVError, match="graph capture"):
+        with torch.cuda.stream(s2):
+            with torch.cuda.graph(g2, stream=s2):
+                vkv.paged_attention(q_small, small[1], D ** -0.5, out=out)
+    torch.cuda.synchronize()
+    del g
+    torch.cuda.synchronize()
+    assert vkv.workspace_release(s) > 0

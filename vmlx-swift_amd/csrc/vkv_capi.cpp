@@ -76,13 +76,18 @@ int32_t choose_parts(int64_t rows_x_heads, int64_t max_len, int32_t* part_tokens
 
 constexpr int kGatherPrefillMinL = 16;
 
+// Split-K scratch: the per-stream workspace.
+float* workspace(hipStream_t st, size_t floats, bool) {
+  return attention_workspace(st, floats);
+}
+
 void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64_t rows,
-                   int64_t max_len, hipStream_t st) {
+                   int64_t max_len, hipStream_t st, bool noalloc = false) {
   if (fdecode_supported(dtype, bits, qsem, a) && !getenv("VKV_GENERIC_ATTENTION")) {
     a.n_parts = fdecode_parts(rows * a.Hkv, max_len, &a.part_tokens);
     if (a.n_parts > 1) {
       const size_t per = static_cast<size_t>(rows) * a.Hq * a.n_parts;
-      float* ws = attention_workspace(st, per * (a.Dv + 2));
+      float* ws = workspace(st, per * (a.Dv + 2), noalloc);
       a.ws_o = ws;
       a.ws_ml = ws + per * a.Dv;
     }
@@ -111,7 +116,7 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
       d.n_parts = prefill_parts(batch, a.Hkv, a.L, a.Hq / a.Hkv, T, &d.part_tokens);
       const size_t copy_floats = static_cast<size_t>((2 * kv_bytes + 255) / 256 * 64);
       const size_t per = static_cast<size_t>(rows) * a.Hq * d.n_parts;
-      float* ws = attention_workspace(st, copy_floats + (d.n_parts > 1 ? per * (a.Dv + 2) : 0));
+      float* ws = workspace(st, copy_floats + (d.n_parts > 1 ? per * (a.Dv + 2) : 0), noalloc);
       uint8_t* kd = reinterpret_cast<uint8_t*>(ws);
       uint8_t* vd = kd + kv_bytes;
       GatherArgs g{};
@@ -141,7 +146,7 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
     a.n_parts = prefill_parts(batch, a.Hkv, a.L, a.Hq / a.Hkv, a.kv.T, &a.part_tokens);
     if (a.n_parts > 1) {
       const size_t per = static_cast<size_t>(rows) * a.Hq * a.n_parts;
-      float* ws = attention_workspace(st, per * (a.Dv + 2));
+      float* ws = workspace(st, per * (a.Dv + 2), noalloc);
       a.ws_o = ws;
       a.ws_ml = ws + per * a.Dv;
     }
@@ -151,7 +156,7 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
   a.n_parts = choose_parts(rows * a.Hkv, max_len, &a.part_tokens);
   if (a.n_parts > 1) {
     const size_t per = static_cast<size_t>(rows) * a.Hq * a.n_parts;
-    float* ws = attention_workspace(st, per * (a.Dv + 2));
+    float* ws = workspace(st, per * (a.Dv + 2), noalloc);
     a.ws_o = ws;
     a.ws_ml = ws + per * a.Dv;
   }
@@ -324,13 +329,30 @@ int vkv_quantized_sdpa(const vkv_array* q, const vkv_array* k_wq, const vkv_arra
     if (bits != 4 && bits != 8) throw Error("bits must be 4 or 8");
     if (q->ndim != 4 || out->ndim != 4 || q->strides[3] != 1 || out->strides[3] != 1)
       throw Error("q and out must be 4-D with a contiguous last dim");
+    if (!is_float(q->dtype)) throw Error("q must be f32, f16 or bf16");
     const int64_t B = q->shape[0], Hq = q->shape[1], L = q->shape[2], D = q->shape[3];
     const int64_t Hkv = k_wq->shape[1], T = k_wq->shape[2];
-    if (k_wq->shape[3] * 32 != D * bits || v_wq->shape[3] * 32 != D * bits || Hq % Hkv ||
-        k_wq->shape[0] != B || v_wq->shape[2] != T || k_scales->shape[3] != D / group_size)
-      throw Error("quantized tuples do not match q");
-    if (k_scales->dtype != q->dtype || v_scales->dtype != q->dtype || out->dtype != q->dtype)
-      throw Error("q, scales, biases and out must share a dtype");
+    if (D % group_size || (D * bits) % 32) throw Error("head dim must be a multiple of group_size");
+    if (Hkv < 1 || Hq % Hkv) throw Error("query heads must be a multiple of kv heads");
+    // all six tuple arrays are [B, Hkv, T, last]: codes last = D*bits/32
+    // (u32), scales and biases last = D/group_size (q's dtype)
+    for (int i = 0; i < 6; i++) {
+      const vkv_array* x = arrs[i];
+      const bool codes = i % 3 == 0;
+      if (x->shape[0] != B || x->shape[1] != Hkv || x->shape[2] != T ||
+          x->shape[3] != (codes ? D * bits / 32 : D / group_size))
+        throw Error(std::string("quantized tuple ") + (i < 3 ? "keys" : "values") +
+                    (codes ? " wq" : i % 3 == 1 ? " scales" : " biases") +
+                    " must be [B, Hkv, T, " + (codes ? "D*bits/32]" : "D/group_size]") +
+                    " matching q and the keys");
+      if (codes ? x->dtype != VKV_U32 : x->dtype != q->dtype)
+        throw Error(codes ? "quantized codes must be u32"
+                          : "q, scales and biases must share a dtype");
+      if (!x->data && B * Hkv * T > 0) throw Error("quantized tuple array has no data");
+    }
+    if (out->dtype != q->dtype) throw Error("out must have q's dtype");
+    if (out->shape[0] != B || out->shape[1] != Hq || out->shape[2] != L || out->shape[3] != D)
+      throw Error("out must be [B, Hq, L, D]");
     const int es = elem_bytes(q->dtype);
     AttnArgs a{};
     a.q = q->data;
@@ -363,9 +385,13 @@ int vkv_quantized_sdpa(const vkv_array* q, const vkv_array* k_wq, const vkv_arra
   });
 }
 
-int vkv_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_array* out,
-                   void* stream) {
-  return guard([&] {
+}  // extern "C"
+
+namespace {
+// vkv_paged_sdpa.
+void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_array* out,
+                void* stream, bool noalloc) {
+  {
     need(q, "q");
     need(kv, "kv");
     need(out, "out");
@@ -418,8 +444,9 @@ int vkv_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vk
       d.n_waves = want;  // 0 = choose per launch
       const int chunk = std::min(kv->n_seqs, qdecode_max_seqs());
       const int w_max = qdecode_waves(chunk, kv->n_kv_heads, rep, kv->max_len, want);
-      d.ws = attention_workspace(
-          S(stream), qdecode_workspace_floats(chunk, kv->n_kv_heads, rep, kv->head_dim, w_max));
+      d.ws = workspace(S(stream),
+                       qdecode_workspace_floats(chunk, kv->n_kv_heads, rep, kv->head_dim, w_max),
+                       noalloc);
       launch_qdecode(d, kv->bits, kv->head_dim, S(stream));
       return;
     }
@@ -440,7 +467,22 @@ int vkv_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vk
     a.o_sh = out->strides[1];
     a.o_sl = 0;
     run_attention(kv->dtype, kv->bits, kv->group_size, kv->bits > 0, a, kv->n_seqs, kv->max_len,
-                  S(stream));
+                  S(stream), noalloc);
+  }
+}
+}  // namespace
+
+extern "C" {
+
+int vkv_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_array* out,
+                   void* stream) {
+  return guard([&] { paged_sdpa(q, kv, scale, out, stream, false); });
+}
+
+int vkv_workspace_release(void* stream, int64_t* bytes) {
+  return guard([&] {
+    const size_t n = workspace_release(S(stream));
+    if (bytes) *bytes = static_cast<int64_t>(n);
   });
 }
 

@@ -112,6 +112,33 @@ __global__ void __launch_bounds__(256) offset_mask_kernel(const int32_t* ctr, in
   }
 }
 
+// createCausalMask (KVCache.swift:314-336) with a host offset: [n, off + n]
+// bool, row i (the query at off + i) sees key j when off + i >= j and, with
+// a window, off + i < j + window.
+__global__ void __launch_bounds__(256) causal_mask_kernel(int32_t n, int64_t off, int32_t window,
+                                                          uint8_t* mask) {
+  const int64_t cols = off + n, total = static_cast<int64_t>(n) * cols;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < total;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t i = e / cols, j = e % cols;
+    bool m = off + i >= j;
+    if (window > 0) m = m && (off + i < j + window);
+    mask[e] = m;
+  }
+}
+
+// The rotating cache's single-token window mask (KVCache.swift:905-923):
+// roll(arange(size) >= size - window, shift) -- element j holds the base
+// element (j - shift) mod size.
+__global__ void __launch_bounds__(256) roll_mask_kernel(int64_t size, int64_t window,
+                                                        int64_t shift, uint8_t* mask) {
+  for (int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; j < size;
+       j += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t i = ((j - shift) % size + size) % size;
+    mask[j] = i >= size - window;
+  }
+}
+
 int blocks_for(int64_t n) {
   return static_cast<int>(std::min<int64_t>((n + 255) / 256, 4096));
 }
@@ -151,6 +178,21 @@ void launch_offset_mask(const int32_t* ctr, int n, int cols, int window, int rin
   if (total <= 0) return;
   hipLaunchKernelGGL(offset_mask_kernel, dim3(blocks_for(total)), dim3(256), 0, st, ctr, n, cols,
                      window, ring, mask);
+  VKV_HIP(hipGetLastError());
+}
+
+void launch_causal_mask(int n, int64_t off, int window, uint8_t* mask, hipStream_t st) {
+  const int64_t total = static_cast<int64_t>(n) * (off + n);
+  if (total <= 0) return;
+  hipLaunchKernelGGL(causal_mask_kernel, dim3(blocks_for(total)), dim3(256), 0, st, n, off, window,
+                     mask);
+  VKV_HIP(hipGetLastError());
+}
+
+void launch_roll_mask(int64_t size, int64_t window, int64_t shift, uint8_t* mask, hipStream_t st) {
+  if (size <= 0) return;
+  hipLaunchKernelGGL(roll_mask_kernel, dim3(blocks_for(size)), dim3(256), 0, st, size, window,
+                     shift, mask);
   VKV_HIP(hipGetLastError());
 }
 

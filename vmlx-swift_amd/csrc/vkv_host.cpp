@@ -78,19 +78,12 @@ static Dense4 dense_from_array(const vkv_array& a, hipStream_t st) {
   return d;
 }
 
-int Cache::causal_array_mask(int n, int64_t off, int window, hipStream_t, vkv_array* mask) {
-  // createCausalMask (KVCache.swift:314-336): [n, off + n] bool,
-  // row i (query at off + i) sees key j when off + i >= j (and within window)
+int Cache::causal_array_mask(int n, int64_t off, int window, hipStream_t st, vkv_array* mask) {
+  // createCausalMask (KVCache.swift:314-336): [n, off + n] bool, built on
+  // the device on `st` into a buffer that only grows
   const int64_t cols = off + n;
-  std::vector<uint8_t> m(static_cast<size_t>(n * cols));
-  for (int64_t i = 0; i < n; i++)
-    for (int64_t j = 0; j < cols; j++) {
-      bool v = off + i >= j;
-      if (window > 0) v = v && (off + i < j + window);
-      m[i * cols + j] = v;
-    }
-  mask_buf_.alloc(m.size() ? m.size() : 1);
-  if (!m.empty()) VKV_HIP(hipMemcpy(mask_buf_.get(), m.data(), m.size(), hipMemcpyHostToDevice));
+  mask_buf_.ensure(static_cast<size_t>(std::max<int64_t>(1, n * cols)));
+  launch_causal_mask(n, off, window, mask_buf_.bytes(), st);
   *mask = vkv_array{};
   mask->data = mask_buf_.get();
   mask->dtype = VKV_BOOL;
@@ -466,12 +459,9 @@ int RotatingCache::make_mask(int n, int window, bool return_array, hipStream_t s
     int64_t cur = idx_;
     if (cur >= max_) cur = 0;
     const int64_t size = offset < max_ ? offset + 1 : max_;
-    std::vector<uint8_t> base(static_cast<size_t>(size)), rolled(static_cast<size_t>(size));
-    for (int64_t i = 0; i < size; i++) base[i] = i >= size - window;
-    const int64_t shift = cur + 1;
-    for (int64_t i = 0; i < size; i++) rolled[(i + shift) % size] = base[i];  // roll(_:shift:)
-    mask_buf_.alloc(static_cast<size_t>(size));
-    VKV_HIP(hipMemcpy(mask_buf_.get(), rolled.data(), rolled.size(), hipMemcpyHostToDevice));
+    // roll(arange(size) >= size - window, shift: cur + 1), built on the device
+    mask_buf_.ensure(static_cast<size_t>(size));
+    launch_roll_mask(size, window, cur + 1, mask_buf_.bytes(), st);
     *mask = vkv_array{};
     mask->data = mask_buf_.get();
     mask->dtype = VKV_BOOL;
@@ -546,7 +536,7 @@ static int full_mask(std::map<int, DevBuf>& masks, const DevBuf& ctr, int n, int
   if (n < 1) throw Error("n must be >= 1");
   DevBuf& b = masks[n];
   const size_t need = static_cast<size_t>(n) * cols;
-  if (b.size() < need) b.alloc(need);
+  b.ensure(need);
   launch_offset_mask(static_cast<const int32_t*>(ctr.get()), n, static_cast<int>(cols), window, ring,
                      b.bytes(), st);
   *mask = vkv_array{};
@@ -995,9 +985,9 @@ int QuantizedCache::state(hipStream_t st, vkv_array* out) {
     DevBuf& c = state_buf_[3 * which];
     DevBuf& s = state_buf_[3 * which + 1];
     DevBuf& b = state_buf_[3 * which + 2];
-    c.alloc(static_cast<size_t>(std::max<int64_t>(1, B_ * H_ * T * W) * 4));
-    s.alloc(static_cast<size_t>(std::max<int64_t>(1, B_ * H_ * T * G) * es));
-    b.alloc(static_cast<size_t>(std::max<int64_t>(1, B_ * H_ * T * G) * es));
+    c.ensure(static_cast<size_t>(std::max<int64_t>(1, B_ * H_ * T * W) * 4));
+    s.ensure(static_cast<size_t>(std::max<int64_t>(1, B_ * H_ * T * G) * es));
+    b.ensure(static_cast<size_t>(std::max<int64_t>(1, B_ * H_ * T * G) * es));
     GatherArgs g{};
     g.kv = kv;
     g.n_seqs = static_cast<int32_t>(B_);
@@ -1104,7 +1094,7 @@ void QuantizedCache::read_kv(hipStream_t st, vkv_array* k, vkv_array* v) {
   KVSrc kv = kvsrc_from_view(vw);
   vkv_array* outs[2] = {k, v};
   for (int which = 0; which < 2; which++) {
-    kv_buf_[which].alloc(static_cast<size_t>(std::max<int64_t>(1, B_ * H_ * T * D_) * elem_bytes(dtype_)));
+    kv_buf_[which].ensure(static_cast<size_t>(std::max<int64_t>(1, B_ * H_ * T * D_) * elem_bytes(dtype_)));
     GatherArgs g{};
     g.kv = kv;
     g.n_seqs = static_cast<int32_t>(B_);
@@ -1662,17 +1652,52 @@ void timing_read(int kind, double* total_ms, int* count) {
 
 // ------------------------------------------------------------ workspace
 
-float* attention_workspace(hipStream_t st, size_t floats) {
+namespace {
+// Per-stream scratch of the attention launchers.  A HIP graph captured on a
+// stream keeps the workspace address it was captured with, so a buffer that
+// is outgrown is retired, not freed: it stays allocated until
+// vkv_workspace_release() for that stream (or the end of the process).
+// Growth inside a capture would record an allocation into the graph, so it
+// is refused there.
+struct StreamWorkspace {
+  DevBuf cur;
+  std::vector<DevBuf> retired;
+};
+std::mutex& ws_mutex() {
   static std::mutex mu;
-  static std::unordered_map<hipStream_t, DevBuf>* ws = new std::unordered_map<hipStream_t, DevBuf>();
-  std::lock_guard<std::mutex> g(mu);
-  DevBuf& b = (*ws)[st];
-  if (b.size() < floats * sizeof(float)) {
-    size_t want = std::max(floats * sizeof(float), b.size() * 2);
-    b.alloc(want);
+  return mu;
+}
+std::unordered_map<hipStream_t, StreamWorkspace>& ws_map() {
+  static auto* m = new std::unordered_map<hipStream_t, StreamWorkspace>();
+  return *m;
+}
+}  // namespace
+
+float* attention_workspace(hipStream_t st, size_t floats) {
+  std::lock_guard<std::mutex> g(ws_mutex());
+  StreamWorkspace& w = ws_map()[st];
+  if (w.cur.size() < floats * sizeof(float)) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    VKV_HIP(hipStreamIsCapturing(st, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+      throw Error("the attention workspace of this stream must grow (to " +
+                  std::to_string(floats * sizeof(float)) +
+                  " bytes) during HIP graph capture: run the same call once before capturing");
+    const size_t want = std::max(floats * sizeof(float), w.cur.size() * 2);
+    if (w.cur.size()) w.retired.push_back(std::move(w.cur));
+    w.cur.alloc(want);
   }
-  return static_cast<float*>(b.get());
+  return static_cast<float*>(w.cur.get());
 }
 
+size_t workspace_release(hipStream_t st) {
+  std::lock_guard<std::mutex> g(ws_mutex());
+  auto it = ws_map().find(st);
+  if (it == ws_map().end()) return 0;
+  size_t n = it->second.cur.size();
+  for (auto& b : it->second.retired) n += b.size();
+  ws_map().erase(it);  // hipFree waits for the device
+  return n;
+}
 
 }  // namespace vkv

@@ -43,6 +43,12 @@ class DevBuf {
     if (bytes) VKV_HIP(hipMalloc(&p_, bytes));
     n_ = bytes;
   }
+  // Grow to at least `bytes` (contents are not kept); a buffer that is
+  // large enough stays where it is, so views into it and work already
+  // queued on it keep their address, and no hipFree stalls the device.
+  void ensure(size_t bytes) {
+    if (bytes > n_) alloc(bytes);
+  }
   void release() {
     if (p_) (void)hipFree(p_);
     p_ = nullptr;
@@ -341,8 +347,12 @@ class PrefixManager {
   vkv_prefix_stats stats_{};
 };
 
-// Split-K workspace for the attention kernels (one per stream).
+// Split-K workspace for the attention kernels (one per stream).  It only
+// grows; outgrown buffers stay allocated (a captured graph may still use
+// them) until workspace_release(st), which frees them all and returns the
+// bytes released.  Growth during graph capture on `st` is an error.
 float* attention_workspace(hipStream_t st, size_t floats);
+size_t workspace_release(hipStream_t st);
 
 }  // namespace vkv
 

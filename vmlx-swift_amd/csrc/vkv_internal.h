@@ -234,6 +234,10 @@ void launch_counter_set(int32_t* ctr, int32_t offset, int32_t idx, hipStream_t s
 // [n, cols] bool mask from the device offset (see vkv_compile.hip).
 void launch_offset_mask(const int32_t* ctr, int n, int cols, int window, int ring, uint8_t* mask,
                         hipStream_t st);
+// [n, off + n] causal bool mask with a host offset (and window when > 0).
+void launch_causal_mask(int n, int64_t off, int window, uint8_t* mask, hipStream_t st);
+// [size] bool: roll(arange(size) >= size - window, shift).
+void launch_roll_mask(int64_t size, int64_t window, int64_t shift, uint8_t* mask, hipStream_t st);
 
 // Kernel timing (a measurement aid): while enabled, launchers start their
 // main kernel with hipExtLaunchKernelGGL and a start/stop event pair, which

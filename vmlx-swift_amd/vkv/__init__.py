@@ -82,7 +82,7 @@ EXPORTS = (
     "vkv_kernel_timing", "vkv_kernel_timing_read", "vkv_fill_normal",
     "vkv_cache_to_compilable", "vkv_cache_to_compilable_rotating", "vkv_cache_inner_state",
     "vkv_dynamic_slice_update", "vkv_dynamic_slice", "vkv_cache_set_offset",
-    "vkv_attention_with_cache_update",
+    "vkv_attention_with_cache_update", "vkv_workspace_release",
 )
 TIME_DECODE, TIME_MLA = 0, 1
 
@@ -256,15 +256,26 @@ def quantized_scaled_dot_product_attention(queries, quantized_keys, quantized_va
     return out
 
 
-def paged_attention(queries, view: PagedView, scale: float, stream=None):
-    """Decode attention over paged KV: queries [n_seqs, Hq, D]."""
+def paged_attention(queries, view: PagedView, scale: float, stream=None, out=None):
+    """Decode attention over paged KV: queries [n_seqs, Hq, D] (into `out`
+    when given)."""
     torch = _torch()
-    out = torch.empty((queries.shape[0], queries.shape[1], view.v_head_dim), dtype=queries.dtype,
-                      device=queries.device)
+    if out is None:
+        out = torch.empty((queries.shape[0], queries.shape[1], view.v_head_dim),
+                          dtype=queries.dtype, device=queries.device)
     a_out = arr(out)
     _chk(lib().vkv_paged_sdpa(C.byref(arr(queries)), C.byref(view), C.c_float(scale),
                               C.byref(a_out), stream_ptr(stream)))
     return out
+
+
+def workspace_release(stream=None) -> int:
+    """Free the attention workspace of a stream, outgrown buffers included
+    (only once no captured graph that used the stream is replayed again);
+    returns the bytes released."""
+    n = C.c_int64()
+    _chk(lib().vkv_workspace_release(stream_ptr(stream), C.byref(n)))
+    return n.value
 
 
 def mla_decode(queries, view: PagedView, scale: float, stream=None):
