@@ -170,6 +170,19 @@ int vkv_quantized_sdpa(const vkv_array *q, const vkv_array *k_wq,
 int vkv_paged_sdpa(const vkv_array *q, const vkv_paged_view *kv, float scale,
                    vkv_array *out, void *stream);
 
+/* vkv_paged_sdpa without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops or harnesses that forbid
+ * hipMalloc).  Same arguments, arithmetic and results as vkv_paged_sdpa;
+ * the split-K partials go to a fixed 64 MiB device array that the library
+ * holds on each GPU it runs on until the process ends, instead of the
+ * per-stream workspace.  A call whose partials do not fit (about 1000
+ * (sequence, kv head) pairs at head_dim 128 on the matrix-core path) fails
+ * with an error naming the size.  Calls share the array of their device:
+ * calls that overlap on one device (two streams, two threads) race. */
+int vkv_paged_sdpa_noalloc(const vkv_array *q, const vkv_paged_view *kv, float scale,
+                           vkv_array *out, void *stream);
+
 /* Absorbed-latent MLA decode (MLXLLM/Models/GLM4MOELite.swift:233-290 via
  * MLXLMCommon/AttentionUtils.swift:43-75): one shared latent head; kv is a
  * keys-only affine view (entries of head_dim = 576 dims, values = first

@@ -278,3 +278,13 @@ def test_quantized_sdpa_rejects_mismatched_tuples(case):
 
 def setattr_shape(a, i, n):
     a.shape[i] = n
+
+
+def test_noalloc_scratch_limit_is_checked_on_the_host():
+    """The no-allocation decode entry point is declared and exported; its
+    argument checks are the allocating call's (a NULL view fails)."""
+    L = vkv.lib()
+    q = _desc((1, 8, 128), 2)
+    out = _desc((1, 8, 128), 2)
+    assert L.vkv_paged_sdpa_noalloc(C.byref(q), None, C.c_float(0.1), C.byref(out), None) == 1
+    assert b"kv is NULL" in L.vkv_last_error()

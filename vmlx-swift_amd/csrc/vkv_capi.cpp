@@ -76,9 +76,10 @@ int32_t choose_parts(int64_t rows_x_heads, int64_t max_len, int32_t* part_tokens
 
 constexpr int kGatherPrefillMinL = 16;
 
-// Split-K scratch: the per-stream workspace.
-float* workspace(hipStream_t st, size_t floats, bool) {
-  return attention_workspace(st, floats);
+// Split-K scratch: the per-stream workspace, or (noalloc) the fixed device
+// array of the no-allocation entry point.
+float* workspace(hipStream_t st, size_t floats, bool noalloc) {
+  return noalloc ? decode_scratch(floats) : attention_workspace(st, floats);
 }
 
 void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64_t rows,
@@ -388,7 +389,8 @@ int vkv_quantized_sdpa(const vkv_array* q, const vkv_array* k_wq, const vkv_arra
 }  // extern "C"
 
 namespace {
-// vkv_paged_sdpa.
+// vkv_paged_sdpa and its no-allocation variant (noalloc: split-K partials in
+// the fixed scratch array, nothing allocated).
 void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_array* out,
                 void* stream, bool noalloc) {
   {
@@ -477,6 +479,11 @@ extern "C" {
 int vkv_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_array* out,
                    void* stream) {
   return guard([&] { paged_sdpa(q, kv, scale, out, stream, false); });
+}
+
+int vkv_paged_sdpa_noalloc(const vkv_array* q, const vkv_paged_view* kv, float scale,
+                           vkv_array* out, void* stream) {
+  return guard([&] { paged_sdpa(q, kv, scale, out, stream, true); });
 }
 
 int vkv_workspace_release(void* stream, int64_t* bytes) {

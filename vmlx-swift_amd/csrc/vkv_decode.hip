@@ -63,6 +63,8 @@
 // device-scope fences each partial writes back and invalidates the XCD's
 // L2.)
 #include <algorithm>
+#include <mutex>
+#include <string>
 #include <utility>
 
 #include "vkv_device.h"
@@ -1051,6 +1053,41 @@ size_t qdecode_workspace_floats(int n_seqs, int Hkv, int rep, int D, int) {
 }
 
 int qdecode_max_seqs() { return kMaxSeqs; }
+
+// ---- scratch of the no-allocation decode entry point (vkv_paged_sdpa_noalloc)
+// Its split-K partials live in this fixed array instead of a workspace the
+// library allocates, for callers that cannot allocate device memory.  Each
+// device the library runs on holds its own copy from module load until the
+// process ends.  Every call on a device shares that device's copy: calls
+// that overlap on one device race.  The partials need no clearing: each
+// launch writes every slot it later reads (the partial count of a pair is
+// written by the wave that ends it; empty sequences are never merged).
+constexpr size_t kScratchBytes = size_t{64} << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+size_t decode_scratch_bytes() { return kScratchBytes; }
+
+float* decode_scratch(size_t floats) {
+  if (floats > kScratchBytes / sizeof(float))
+    throw Error("the call needs " + std::to_string(floats * sizeof(float)) +
+                " bytes of split-K scratch; the no-allocation entry point holds " +
+                std::to_string(kScratchBytes) + " (fewer sequences per call fit)");
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  VKV_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) throw Error("device index out of range for the scratch table");
+  std::lock_guard<std::mutex> g(mu);
+  if (!addr[dev]) {
+    // the host-side name of a __device__ array is not its device address
+    void* p = nullptr;
+    VKV_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) throw Error("hipGetSymbolAddress(scratch) returned NULL");
+    addr[dev] = p;
+  }
+  return static_cast<float*>(addr[dev]);
+}
 
 // Longest sequence the decode kernel takes: ranges of at most kMaxRange
 // units with at most kMaxParts partials per pair.

@@ -181,6 +181,12 @@ int qdecode_max_len();
 int qdecode_waves(int n_seqs, int Hkv, int rep, int max_len, int want);
 size_t qdecode_workspace_floats(int n_seqs, int Hkv, int rep, int D, int n_waves);
 void launch_qdecode(const DecodeArgs& a, int bits, int D, hipStream_t st);
+// Scratch of the no-allocation decode entry point: a fixed device array in
+// vkv_decode.hip, of decode_scratch_bytes() bytes per device.  Returns its
+// device address on the current device (resolved once per device), or
+// throws when `floats` does not fit.
+float* decode_scratch(size_t floats);
+size_t decode_scratch_bytes();
 
 // Absorbed-latent MLA decode over a keys-only 8-bit paged view (vkv_mla.hip):
 // 576-dim entries (512 latent + 64 rope), values = the first 512 dims, one

@@ -82,7 +82,7 @@ EXPORTS = (
     "vkv_kernel_timing", "vkv_kernel_timing_read", "vkv_fill_normal",
     "vkv_cache_to_compilable", "vkv_cache_to_compilable_rotating", "vkv_cache_inner_state",
     "vkv_dynamic_slice_update", "vkv_dynamic_slice", "vkv_cache_set_offset",
-    "vkv_attention_with_cache_update", "vkv_workspace_release",
+    "vkv_attention_with_cache_update", "vkv_paged_sdpa_noalloc", "vkv_workspace_release",
 )
 TIME_DECODE, TIME_MLA = 0, 1
 
@@ -256,16 +256,20 @@ def quantized_scaled_dot_product_attention(queries, quantized_keys, quantized_va
     return out
 
 
-def paged_attention(queries, view: PagedView, scale: float, stream=None, out=None):
-    """Decode attention over paged KV: queries [n_seqs, Hq, D] (into `out`
-    when given)."""
+def paged_attention(queries, view: PagedView, scale: float, stream=None, out=None,
+                    noalloc: bool = False):
+    """Decode attention over paged KV: queries [n_seqs, Hq, D].  With
+    noalloc=True the call goes to vkv_paged_sdpa_noalloc (split-K partials in
+    the library's fixed device scratch; pass `out` to allocate nothing on
+    this side either)."""
     torch = _torch()
     if out is None:
         out = torch.empty((queries.shape[0], queries.shape[1], view.v_head_dim),
                           dtype=queries.dtype, device=queries.device)
     a_out = arr(out)
-    _chk(lib().vkv_paged_sdpa(C.byref(arr(queries)), C.byref(view), C.c_float(scale),
-                              C.byref(a_out), stream_ptr(stream)))
+    fn = lib().vkv_paged_sdpa_noalloc if noalloc else lib().vkv_paged_sdpa
+    _chk(fn(C.byref(arr(queries)), C.byref(view), C.c_float(scale), C.byref(a_out),
+            stream_ptr(stream)))
     return out
 
 
