@@ -373,6 +373,9 @@ def main():
         step()
     dec_ms, dec_n = vkv.kernel_timing_read(vkv.TIME_DECODE)
     vkv.kernel_timing(False)
+    torch.cuda.synchronize()
+    if not bool(torch.isfinite(sc["out"].float()).all()):
+        raise RuntimeError("the decode attention output holds non-finite values")
     n_att = args.steps * layers
     att_avg_ms = att_ms / n_att
     app_avg_ms = app_ms / n_att

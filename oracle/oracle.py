@@ -17,10 +17,13 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 F32, F16, BF16 = 0, 1, 2
 
-# quantized-SDPA arithmetic (vkvo_quantized_sdpa): exact fp64; the
-# reference's rounding on the vector (qmv) path; on the matrix (qmm) path;
-# and the vector path with a softmax computed in the query dtype.
-EXACT, QMV, QMM, QMV_ACC_T = 0, 1, 2, 3
+# quantized-SDPA arithmetic (vkvo_quantized_sdpa): exact fp64; scores and
+# weights rounded to the query dtype with an fp32 softmax on the vector (qmv)
+# and matrix (qmm) paths; the same with the softmax computed in the query
+# dtype (softmax(precise: false), the reference's arithmetic) on each path.
+EXACT, QMV, QMM, QMV_ACC_T, QMM_ACC_T = 0, 1, 2, 3, 4
+# the reference's decode (one query token) and multi-token arithmetic
+REF_DECODE, REF_CHUNK = QMV_ACC_T, QMM_ACC_T
 
 _lib = None
 

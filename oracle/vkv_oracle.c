@@ -311,18 +311,32 @@ static inline double round_d(double x, int dtype) {
   return (double)round_to((float)x, dtype);
 }
 
-/* Softmax weights of one row of scores (KVCache.swift:1982, softmax with
- * precise: false).  rnd == 0: exact fp64.  Otherwise the scores sc[] already
- * carry the reference's rounding and:
- *   acc_t < 0 : internal arithmetic in fp32 (AccT = float), weights
+/* Softmax weights of one row of scores (KVCache.swift:1982: softmax over the
+ * last axis with precise: false, Source/MLX/Ops.swift:2702-2710).
+ * rnd == 0: exact fp64.  Otherwise the scores sc[] already carry the
+ * reference's rounding and:
+ *   acc_t < 0 : internal arithmetic in fp32, weights
  *               T(exp(s - max) * (1 / sum)) rounded to wdt;
- *   acc_t >= 0: internal arithmetic in AccT = T (softmax.h's default
- *               template argument), modelled on softmax_single_row
- *               (softmax.h): every op rounded to T, 4 values summed per
- *               thread, then 32-thread and threadgroup sums each rounded
- *               once (the hardware reduction order is not in the tree).
+ *   acc_t >= 0: internal arithmetic in AccT = T, the kernels' default
+ *               template argument (softmax.h:10, :100), which the
+ *               non-precise softmax uses for T = f16/bf16; T's simd_sum and
+ *               simd_max reduce in fp32 and round once (bf16_math.h:328-378).
+ *               Rows of up to 4096 keys follow softmax_single_row
+ *               (softmax.h:10-98): 4 consecutive keys per thread summed in
+ *               T, 32-thread sums, then the sum of those; longer rows follow
+ *               softmax_looped (softmax.h:100-200) with 1024 threads, each
+ *               keeping a running (max, sum) over keys lid*4 + 4096 r + i,
+ *               rescaled by exp(old max - new max) at every level.  The
+ *               order of the fp32 additions inside one simd_sum is the
+ *               hardware's and is not in the tree (fp64 here).
  * pe[] receives the exact fp64 softmax of the same scores (the unrounded
  * weights a kernel that does not round them would use). */
+#define SOFTMAX_N_READS 4
+#define SOFTMAX_LOOPED_LIMIT 4096
+#define SOFTMAX_LOOPED_THREADS 1024
+
+static double t_exp(double x, int dt) { return round_d(exp(x), dt); }
+
 static void softmax_row(const double *sc, int T, int rnd, int acc_t, int wdt, double *p,
                         double *pe) {
   double mx = -INFINITY;
@@ -347,21 +361,63 @@ static void softmax_row(const double *sc, int T, int rnd, int acc_t, int wdt, do
     for (int t = 0; t < T; t++) p[t] = round_d((double)((float)p[t] * r), wdt);
     return;
   }
-  double total = 0.0, simd = 0.0, thr = 0.0;
-  for (int t = 0; t < T; t++) {
-    p[t] = round_d(exp(round_d(sc[t] - mx, acc_t)), acc_t);
-    thr = round_d(thr + p[t], acc_t);
-    if ((t & 3) == 3 || t == T - 1) {
-      simd += thr;
-      thr = 0.0;
+  const int dt = acc_t;
+  if (T <= SOFTMAX_LOOPED_LIMIT) {
+    /* softmax_single_row */
+    double total = 0.0, simd = 0.0, thr = 0.0;
+    for (int t = 0; t < T; t++) {
+      p[t] = t_exp(round_d(sc[t] - mx, dt), dt);
+      thr = round_d(thr + p[t], dt);
+      if ((t & 3) == 3 || t == T - 1) {
+        simd += thr;
+        thr = 0.0;
+      }
+      if ((t & 127) == 127 || t == T - 1) {
+        total += round_d(simd, dt);
+        simd = 0.0;
+      }
     }
-    if ((t & 127) == 127 || t == T - 1) {
-      total += round_d(simd, acc_t);
-      simd = 0.0;
-    }
+    const double r = round_d(1.0 / round_d(total, dt), dt);
+    for (int t = 0; t < T; t++) p[t] = round_d(p[t] * r, dt);
+    return;
   }
-  const double r = round_d(1.0 / round_d(total, acc_t), acc_t);
-  for (int t = 0; t < T; t++) p[t] = round_d(p[t] * r, acc_t);
+  /* softmax_looped: per-thread running max and sum */
+  const double fmin = -type_max(dt);
+  const int NT = SOFTMAX_LOOPED_THREADS, stride = SOFTMAX_N_READS * NT;
+  const int rounds = (T + stride - 1) / stride;
+  double lmax[SOFTMAX_LOOPED_THREADS], lsum[SOFTMAX_LOOPED_THREADS];
+  for (int lid = 0; lid < NT; lid++) {
+    double m = fmin, n = 0.0;
+    for (int r = 0; r < rounds; r++) {
+      double v[SOFTMAX_N_READS];
+      const int off = r * stride + lid * SOFTMAX_N_READS;
+      const double prev = m;
+      for (int i = 0; i < SOFTMAX_N_READS; i++) {
+        v[i] = off + i < T ? sc[off + i] : -INFINITY;
+        m = v[i] > m ? v[i] : m;
+      }
+      n = round_d(n * t_exp(round_d(prev - m, dt), dt), dt);
+      for (int i = 0; i < SOFTMAX_N_READS; i++)
+        n = round_d(n + t_exp(round_d(v[i] - m, dt), dt), dt);
+    }
+    lmax[lid] = m;
+    lsum[lid] = n;
+  }
+  double gmax = fmin, smax[SOFTMAX_LOOPED_THREADS / 32], ssum[SOFTMAX_LOOPED_THREADS / 32];
+  for (int g = 0; g < NT / 32; g++) {
+    double m = fmin, acc = 0.0;
+    for (int l = 0; l < 32; l++) m = lmax[g * 32 + l] > m ? lmax[g * 32 + l] : m;
+    for (int l = 0; l < 32; l++)
+      acc += round_d(lsum[g * 32 + l] * t_exp(round_d(lmax[g * 32 + l] - m, dt), dt), dt);
+    smax[g] = m;
+    ssum[g] = round_d(acc, dt);
+    gmax = m > gmax ? m : gmax;
+  }
+  double total = 0.0;
+  for (int g = 0; g < NT / 32; g++)
+    total += round_d(ssum[g] * t_exp(round_d(smax[g] - gmax, dt), dt), dt);
+  const double r = round_d(1.0 / round_d(total, dt), dt);
+  for (int t = 0; t < T; t++) p[t] = round_d(t_exp(round_d(sc[t] - gmax, dt), dt) * r, dt);
 }
 
 /* Neighbours of the T value r (T = f16 or bf16): the adjacent representable
@@ -408,11 +464,11 @@ static void qsdpa_row(const float *qs, const uint32_t *kq, const float *ks,
                       double *wb) {
   const int wpr = D * bits / 32;
   const int G = D / group;
-  const int deq_dt = rnd == 2 ? sdt : -1;
+  const int deq_dt = (rnd == 2 || rnd == 4) ? sdt : -1;
   const int wdt = add ? 0 : sdt;
   /* flip factors exp(n_t - r_t) for scores near a rounding boundary (0: none) */
   double *flip = (wb && rnd) ? (double *)calloc((size_t)(T > 0 ? T : 1), sizeof(double)) : NULL;
-  const int acc_t = (rnd == 3 && !add) ? sdt : -1;
+  const int acc_t = ((rnd == 3 || rnd == 4) && !add) ? sdt : -1;
   for (int t = 0; t < T; t++) {
     double s = fill;
     if (!vis || vis[t]) {

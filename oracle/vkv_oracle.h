@@ -73,13 +73,17 @@ void vkvo_sdpa(const float *q, const float *k, const float *v, int B, int Hq,
  *      quantized.h:1493-1764): scores accumulated exactly from the exact
  *      dequantized keys, then stored in T (quantizedMM returns the query
  *      dtype, KVCache.swift:1945-1949); an f32 additive mask promotes them
- *      to f32 (:1969); softmax (:1982) with fp32 internals and its weights
- *      stored in T; P.V accumulated exactly over the T weights;
+ *      to f32 (:1969); softmax (:1982) with fp32 internals (the arithmetic
+ *      of precise: true) and its weights stored in T; P.V accumulated
+ *      exactly over the T weights;
  *   2  as 1 on the matrix path (affine_qmm, quantized.h:568-576, :686-713):
  *      keys and values are first dequantized to T (rule 0 above);
- *   3  as 1 with the softmax's internal arithmetic in T (softmax.h's default
- *      template argument AccT = T under precise: false), used to measure
- *      the spread between the two unpinned softmax precisions.
+ *   3  as 1 with the softmax's internal arithmetic in T: the kernels'
+ *      default AccT = T (softmax.h:10, :100), which softmax(precise: false)
+ *      selects for f16/bf16 -- the reference's decode arithmetic; rows of
+ *      up to 4096 keys reduce as softmax_single_row, longer rows as
+ *      softmax_looped (see softmax_row in vkv_oracle.c);
+ *   4  as 3 on the matrix path: the reference's multi-token arithmetic.
  * wbound (optional, [B,Hq,L,D], rounding modes only): the most the
  * reference's roundings can move each output away from the exact softmax of
  * the rounded scores: sum_t |w_t - pe_t| |v_t| for the weights stored in T,

@@ -48,21 +48,24 @@ def attn_tol(dtype: int, ref: np.ndarray) -> np.ndarray:
     return atol + ulp * np.abs(ref)
 
 
-def qref(*args, rounding=O.QMV, **kw):
-    """The oracle's quantized SDPA with the reference's rounding (scores and
-    softmax weights stored in the query dtype; QMM also dequantizes K/V to
-    the dtype first) and the per-output weight-rounding bound."""
+def qref(*args, rounding=O.REF_DECODE, **kw):
+    """The oracle's quantized SDPA with the reference's arithmetic (scores
+    stored in the query dtype, softmax(precise: false) computed in that
+    dtype with its weights stored in it; REF_CHUNK also dequantizes K/V to
+    the dtype first) and the per-output rounding bound."""
     return O.quantized_sdpa(*args, rounding=rounding, bound=True, **kw)
 
 
 def qattn_tol(dtype: int, ref: np.ndarray, wb: np.ndarray) -> np.ndarray:
     """Tolerance against the reference-rounded oracle: attn_tol plus the
     oracle's rounding bound wb, i.e. what the reference's roundings can move
-    each output: the softmax weights stored in the dtype (sum_t |w_t - p_t|
-    |v_t|; the kernels keep them in fp32, since rounding them needs the
-    row's final max and sum before any P.V, i.e. a second pass), and scores
-    within fp32 accumulation error of a dtype rounding boundary, which any
-    fp32 implementation (the reference's included) may round either way."""
+    each output away from the exact softmax of its rounded scores: the
+    softmax computed and stored in the dtype (sum_t |w_t - p_t| |v_t|; the
+    kernels compute it in fp32 on the rounded scores, since rounding the
+    weights as the reference does needs the row's final max and normaliser
+    before any P.V, i.e. a second pass over the tokens), and scores within
+    fp32 accumulation error of a dtype rounding boundary, which any fp32
+    implementation (the reference's included) may round either way."""
     return attn_tol(dtype, ref) + wb
 
 

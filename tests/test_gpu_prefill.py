@@ -109,7 +109,7 @@ def test_quantized_cache_chunk(bits, monkeypatch):
     vq, vs, vb, _ = O.quantize(vx, dtype, 64, bits)
     f = lambda a: O.to_f32(a, dtype)
     ref, wb = qref(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64, bits,
-                   mask="causal", rounding=O.QMM)
+                   mask="causal", rounding=O.REF_CHUNK)
     tol = qattn_tol(dtype, ref, wb)
     assert_within(got, ref, tol, "oracle", wb)
     monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
@@ -131,7 +131,7 @@ def test_quantized_cache_chunk_outlier_channels(bits):
     vq, vs, vb, _ = O.quantize(vx, dtype, 64, bits)
     f = lambda a: O.to_f32(a, dtype)
     ref, wb = qref(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64, bits,
-                   mask="causal", rounding=O.QMM)
+                   mask="causal", rounding=O.REF_CHUNK)
     assert_qclose(got, ref, wb, dtype, f"bits {bits}")
 
 
@@ -156,7 +156,7 @@ def test_quantized_sdpa_reference_layout_chunk(bits, L, mask, monkeypatch):
     got = run()
     f = lambda a: O.to_f32(a, dtype)
     ref, wb = qref(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64, bits,
-                   mask=mask, rounding=O.QMM)
+                   mask=mask, rounding=O.REF_CHUNK)
     tol = qattn_tol(dtype, ref, wb)
     assert_within(got, ref, tol, "oracle", wb)
     monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")

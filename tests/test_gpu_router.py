@@ -63,7 +63,7 @@ def test_router_quantized_cache(bits):
         kq, ks, kb, vq, vs, vb = r.state
         # 16+ query tokens run on the matrix (qmm) path, fewer on the vector path
         ref, wb = qref(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64,
-                       bits, mask=mask, rounding=O.QMM if L >= 16 else O.QMV)
+                       bits, mask=mask, rounding=O.REF_CHUNK if L >= 16 else O.REF_DECODE)
         assert c.offset == r.offset
         assert_qclose(values(out, dtype), ref, wb, dtype, f"L {L}")
 
