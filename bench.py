@@ -18,6 +18,11 @@ its launch stream), "traffic" is the PMC-measured HBM bytes per decode launch,
 "cpu_baseline" times the C oracle, "prefill" times a 512-token chunked-prefill
 attention step over a 4-bit cache, and "mla" is the MLA latent decode workload
 (32 x 16384 tokens, 128 heads) with the MFMA roofline of its attention kernel.
+"configs" measures the other BASELINE workloads at their stated shapes, each
+with the roofline of its decode kernel: config 1 (KVCacheSimple fp16 decode
+steps), config 2 (QuantizedKVCache, 32 layers x batch 8 x 4096 tokens, 4 and
+8 bits) and config 4 (5 sliding-window + 1 global 8-bit layer at 32768).
+`--only <leg>` runs one workload alone (for profiling).
 """
 import argparse
 import json
@@ -43,6 +48,9 @@ def parse():
     p.add_argument("--cpu-threads", type=int, default=0)
     p.add_argument("--no-mla", action="store_true",
                    help="skip the MLA latent decode measurement (config 5)")
+    p.add_argument("--only", default="all",
+                   choices=["all", "config3", "config1", "config2", "config4", "mla", "prefill"],
+                   help="run one workload only (profiling); the JSON line needs 'all'")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 1 GiB device copy (vkv_array_copy) 5 times: the "
                         "reference reading for the FETCH_SIZE / WRITE_SIZE counters")
@@ -268,11 +276,205 @@ def mla_measure(torch, vkv, steps, warmup):
     }
 
 
-def cpu_baseline(threads, min_seconds=10.0):
-    """The CPU oracle (C restatement of the reference arithmetic, fp64,
-    OpenMP) on one layer of the same workload: the 64 config-3 sequences
-    (same lengths as the GPU scene), 8 KV / 32 query heads, 4-bit g64.
-    Passes are repeated until at least `min_seconds` of CPU time."""
+def _time_calls(torch, vkv, fn, steps, warmup, kind=None):
+    """Milliseconds per call of fn (HIP events on the current stream around
+    `steps` calls after `warmup`), and, when `kind` is given, the average
+    duration and count of the library-timed kernel of that kind over a
+    second set of `steps` calls."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    if kind is None:
+        return ms, None, 0
+    vkv.kernel_timing(True)
+    for _ in range(steps):
+        fn()
+    k_ms, k_n = vkv.kernel_timing_read(kind)
+    vkv.kernel_timing(False)
+    return ms, k_ms / max(k_n, 1), k_n
+
+
+def _roofline(byts, k_ms, kernel):
+    gbs = byts / (k_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "kernel": kernel,
+            "kernel_us": round(k_ms * 1e3, 2), "bytes_per_launch": int(byts)}
+
+
+def config1_measure(torch, vkv, steps, warmup):
+    """Config 1: KVCacheSimple single layer, fp16, batch 1, 8 KV heads x 128:
+    a 512-token prefill update, then 64 single-token decode steps, each an
+    update plus decode attention (32 query heads) through
+    attentionWithCacheUpdate.  One pass = the 64 decode steps; the cache is
+    trimmed back to 512 tokens between passes (capacity stays 768)."""
+    H, Hq, D, T0, N = 8, 32, 128, 512, 64
+    f16 = dict(dtype=torch.float16, device="cuda")
+    pk = vkv.fill_normal(torch.empty((1, H, T0, D), **f16), 41)
+    pv = vkv.fill_normal(torch.empty((1, H, T0, D), **f16), 42)
+    dk = vkv.fill_normal(torch.empty((N, 1, H, 1, D), **f16), 43)
+    dv = vkv.fill_normal(torch.empty((N, 1, H, 1, D), **f16), 44)
+    q = vkv.fill_normal(torch.empty((N, 1, Hq, 1, D), **f16), 45)
+    out = torch.empty((1, Hq, 1, D), **f16)
+
+    def prefill():
+        c = vkv.KVCacheSimple()
+        c.update(pk, pv)
+        return c
+
+    cache = prefill()
+
+    def decode_pass():
+        for i in range(N):
+            vkv.attention_with_cache_update(q[i], dk[i], dv[i], cache, D ** -0.5, out=out)
+        cache.trim(N)
+
+    pass_ms, k_ms, k_n = _time_calls(torch, vkv, decode_pass, steps, warmup, vkv.TIME_FDECODE)
+    pre_ms, _, _ = _time_calls(torch, vkv, prefill, steps, warmup)
+    kv_bytes = sum((T0 + i + 1) * H * D * 2 * 2 for i in range(N))  # K + V read per pass
+    step_ms = pass_ms / N
+    return {
+        "workload": "KVCacheSimple fp16, B1, 8/32 heads x 128: 512-token prefill update, then "
+                    "64 decode steps (update + SDPA through attentionWithCacheUpdate)",
+        "decode_step_us": round(step_ms * 1e3, 2),
+        "decode_tokens_per_s": round(1e3 / step_ms, 1),
+        "decode_kv_gbs": round(kv_bytes / (pass_ms * 1e-3) / 1e9, 1),
+        "prefill_update_us": round(pre_ms * 1e3, 2),
+        "roofline": _roofline(kv_bytes / N, k_ms, "fdecode_kernel"),
+        "note": "2.1-2.4 MB per step: launch-latency bound, not bandwidth bound",
+    }
+
+
+def _outlier_scale(torch, B, H, D, gen):
+    """[B, H, 1, D] multipliers: 20 on 4 random channels per (batch, head)."""
+    m = torch.ones((B, H, 1, D), dtype=torch.bfloat16, device="cuda")
+    ch = torch.rand((B, H, D), device="cuda", generator=gen).argsort(-1)[..., :4]
+    m.view(B, H, D).scatter_(-1, ch, 20.0)
+    return m
+
+
+def config2_measure(torch, vkv, steps, warmup, bits):
+    """Config 2: QuantizedKVCache at Llama-3-8B layer shapes -- 32 layers,
+    batch 8, 8 KV / 32 query heads x 128, a 4096-token context, bf16 K/V
+    ~ N(0,1) with 4 channels per head x20, affine g64 at `bits`.  One step =
+    for each layer, updateQuantized of one token and quantized decode
+    attention through attentionWithCacheUpdate; each cache is trimmed back by
+    the token after the step."""
+    layers, B, H, Hq, D, T0 = 32, 8, 8, 32, 128, 4096
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(200 + bits)
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    caches = [vkv.QuantizedKVCache(group_size=64, bits=bits) for _ in range(layers)]
+    stage = torch.empty((B, H, T0, D), **bf)
+    stage2 = torch.empty_like(stage)
+    for l, c in enumerate(caches):
+        m = _outlier_scale(torch, B, H, D, gen)
+        vkv.fill_normal(stage, 300 + 2 * l)
+        vkv.fill_normal(stage2, 301 + 2 * l)
+        c.update_quantized(stage * m, stage2 * m)
+    del stage, stage2
+    dk = vkv.fill_normal(torch.empty((layers, B, H, 1, D), **bf), 51)
+    dv = vkv.fill_normal(torch.empty((layers, B, H, 1, D), **bf), 52)
+    q = vkv.fill_normal(torch.empty((layers, B, Hq, 1, D), **bf), 53)
+    out = torch.empty((layers, B, Hq, 1, D), **bf)
+
+    def step():
+        for l, c in enumerate(caches):
+            vkv.attention_with_cache_update(q[l], dk[l], dv[l], c, D ** -0.5, out=out[l])
+        for c in caches:
+            c.trim(1)
+
+    ms, k_ms, k_n = _time_calls(torch, vkv, step, steps, warmup, vkv.TIME_DECODE)
+    per_tok = 2 * (D * bits // 8 + (D // 64) * 4)          # K + V codes + scale/bias
+    layer_bytes = B * H * (T0 + 1) * per_tok
+    finite = bool(torch.isfinite(out.float()).all())
+    del caches
+    return {
+        "workload": f"QuantizedKVCache {bits}-bit g64, 32 layers, B8, 8/32 heads x 128, "
+                    f"context 4096 (+1 decode token), x20 outlier channels",
+        "ms_per_step": round(ms, 4),
+        "step_kv_gbs": round(layers * layer_bytes / (ms * 1e-3) / 1e9, 1),
+        "roofline": _roofline(layer_bytes, k_ms, "qdecode_kernel"),
+        "finite": finite,
+    }
+
+
+def config4_measure(torch, vkv, steps, warmup):
+    """Config 4: Gemma-style layers at 16 query / 8 KV heads x 256, batch 4,
+    bf16 ~ N(0,1): 5 sliding-window layers (RotatingKVCache(maxSize: 1024),
+    filled past a wrap so every decode writes in place into a full ring) and
+    1 global layer (8-bit g64 QuantizedKVCache at a 32768-token context).
+    One step = a decode token through attentionWithCacheUpdate on each of
+    the 6 layers; the global cache is trimmed back after the step."""
+    B, Hq, H, D, M, T0, n_win = 4, 16, 8, 256, 1024, 32768, 5
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    wins = [vkv.RotatingKVCache(M) for _ in range(n_win)]
+    pre = torch.empty((B, H, M + 100, D), **bf)
+    for l, c in enumerate(wins):
+        vkv.fill_normal(pre, 400 + l)
+        c.update(pre[:, :, :M - 1], pre[:, :, :M - 1])
+        for t in range(M - 1, M + 100):          # fill the ring and wrap it
+            c.update(pre[:, :, t:t + 1], pre[:, :, t:t + 1])
+    del pre
+    glob = vkv.QuantizedKVCache(group_size=64, bits=8)
+    stage = vkv.fill_normal(torch.empty((B, H, T0 - 1, D), **bf), 410)
+    glob.update_quantized(stage, vkv.fill_normal(stage.clone(), 411))
+    del stage
+    dk = vkv.fill_normal(torch.empty((n_win + 1, B, H, 1, D), **bf), 61)
+    dv = vkv.fill_normal(torch.empty((n_win + 1, B, H, 1, D), **bf), 62)
+    q = vkv.fill_normal(torch.empty((n_win + 1, B, Hq, 1, D), **bf), 63)
+    out = torch.empty((n_win + 1, B, Hq, 1, D), **bf)
+    scale = D ** -0.5
+
+    def win_layers():
+        for l, c in enumerate(wins):
+            vkv.attention_with_cache_update(q[l], dk[l], dv[l], c, scale, out=out[l])
+
+    def glob_layer():
+        vkv.attention_with_cache_update(q[n_win], dk[n_win], dv[n_win], glob, scale, out=out[n_win])
+        glob.trim(1)
+
+    def step():
+        win_layers()
+        glob_layer()
+
+    ms, _, _ = _time_calls(torch, vkv, step, steps, warmup)
+    w_ms, wk_ms, _ = _time_calls(torch, vkv, win_layers, steps, warmup, vkv.TIME_FDECODE)
+    g_ms, gk_ms, _ = _time_calls(torch, vkv, glob_layer, steps, warmup, vkv.TIME_DECODE)
+    win_bytes = B * H * M * D * 2 * 2
+    glob_bytes = B * H * T0 * 2 * (D + (D // 64) * 4)
+    step_bytes = n_win * win_bytes + glob_bytes
+    finite = bool(torch.isfinite(out.float()).all())
+    return {
+        "workload": "Gemma-style: 5 sliding-window layers (RotatingKVCache maxSize 1024, full "
+                    "ring) + 1 global layer (8-bit g64, context 32768); B4, 16/8 heads x 256",
+        "ms_per_step": round(ms, 4),
+        "step_kv_gbs": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+        "window_layer_us": round(w_ms * 1e3 / n_win, 2),
+        "window_layer_pct_hbm_peak": round(100 * win_bytes / (w_ms / n_win * 1e-3) / 1e9
+                                           / HBM_PEAK_GBS, 2),
+        "global_layer_us": round(g_ms * 1e3, 2),
+        "roofline_window": _roofline(win_bytes, wk_ms, "fdecode_kernel"),
+        "roofline_global": _roofline(glob_bytes, gk_ms, "qdecode_kernel"),
+        "finite": finite,
+    }
+
+
+def cpu_baseline(threads, min_seconds=8.0):
+    """The CPU oracle (C restatement of the reference arithmetic: scores and
+    the softmax in bf16 as softmax(precise: false) computes them, fp64
+    accumulation elsewhere) on one layer of the same workload: the 64
+    config-3 sequences (same lengths as the GPU scene), 8 KV / 32 query
+    heads, 4-bit g64.  Timed twice, single-threaded and on `threads` OpenMP
+    threads, each repeated until at least `min_seconds` of wall time."""
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -294,21 +496,34 @@ def cpu_baseline(threads, min_seconds=10.0):
     kq, vq = tile(kq0), tile(vq0)
     ks, kb, vs, vb = tile(f(ks0)), tile(f(kb0)), tile(f(vs0)), tile(f(vb0))
     q = f(O.from_f32(rng.standard_normal((len(lens), Hq, D)).astype(np.float32), O.BF16))
-    passes = 0
-    t0 = time.perf_counter()
-    while True:
-        O.quantized_decode_batch(q, O.BF16, kq, ks, kb, vq, vs, vb, lens, tok_off, H, D ** -0.5,
-                                 64, 4, threads=threads)
-        passes += 1
-        dt = time.perf_counter() - t0
-        if dt >= min_seconds:
-            break
-    byts = passes * int(lens.sum()) * H * BYTES_PER_TOKEN_HEAD
-    return {"value": round(byts / dt / 1e9, 4), "unit": "GB/s", "cores": threads,
+    layer_bytes = int(lens.sum()) * H * BYTES_PER_TOKEN_HEAD
+
+    def run(n_threads):
+        passes = 0
+        t0 = time.perf_counter()
+        while True:
+            O.quantized_decode_batch(q, O.BF16, kq, ks, kb, vq, vs, vb, lens, tok_off, H,
+                                     D ** -0.5, 64, 4, threads=n_threads,
+                                     rounding=O.REF_DECODE)
+            passes += 1
+            dt = time.perf_counter() - t0
+            if dt >= min_seconds:
+                return passes * layer_bytes / dt / 1e9, passes, dt
+
+    one, p1, t1 = run(1)
+    many, pn, tn = run(threads)
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return {"value": round(many, 4), "unit": "GB/s", "cores": threads,
             "kind": "port",
+            "single_thread": {"value": round(one, 4), "unit": "GB/s", "cores": 1},
+            "host_cpus": {"nproc": avail, "os_cpu_count": os.cpu_count()},
             "sample": f"one config-3 layer: 64 sequences ({int(lens.sum())} tokens) x 8 KV / 32 "
-                      f"query heads, 4-bit g64; {passes} passes in {dt:.1f} s; C oracle (fp64 "
-                      f"restatement of the reference arithmetic, OpenMP, {threads} threads)"}
+                      f"query heads, 4-bit g64; C oracle (restatement of the reference "
+                      f"arithmetic, fp64 accumulation); {threads} OpenMP threads: {pn} passes "
+                      f"in {tn:.1f} s; 1 thread: {p1} passes in {t1:.1f} s"}
 
 
 def main():
@@ -325,6 +540,17 @@ def main():
     torch.cuda.set_device(0)
     if args.calibrate_copy:
         calibrate_copy(torch, vkv)
+        return
+    legs = {
+        "config1": lambda: config1_measure(torch, vkv, args.steps, args.warmup),
+        "config2": lambda: {f"bits{b}": config2_measure(torch, vkv, args.steps, args.warmup, b)
+                            for b in (4, 8)},
+        "config4": lambda: config4_measure(torch, vkv, args.steps, args.warmup),
+        "mla": lambda: mla_measure(torch, vkv, args.steps, args.warmup),
+        "prefill": lambda: prefill_measure(torch, vkv, args.steps, args.warmup),
+    }
+    if args.only in legs:
+        print(json.dumps({args.only: legs[args.only]()}), flush=True)
         return
     layers = args.layers
     pool, sc = build_scene(torch, vkv, layers)
@@ -388,11 +614,19 @@ def main():
     att_gbs = logical / (att_avg_ms * 1e-3) / 1e9
     dec_gbs = logical / (dec_avg_ms * 1e-3) / 1e9
     append_tokens = sc["n_seqs"] + sc["prefill"]
-    mla = None if args.no_mla else mla_measure(torch, vkv, args.steps, args.warmup)
-    prefill = None if args.no_mla else prefill_measure(torch, vkv, args.steps, args.warmup)
+    others = args.only == "all" and not args.no_mla
+    mla = legs["mla"]() if others else None
+    prefill = legs["prefill"]() if others else None
+    configs = {k: legs[k]() for k in ("config1", "config2", "config4")} if others else None
     cpu = None
-    if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    if not args.no_cpu_baseline and args.only == "all":
+        # all the host CPUs this process may use, at most 16 (a GPU box's
+        # share of its host)
+        try:
+            avail = len(os.sched_getaffinity(0))
+        except AttributeError:
+            avail = os.cpu_count() or 1
+        threads = args.cpu_threads or min(16, avail)
         cpu = cpu_baseline(threads)
     rec = {
         "metric": "KV-read GB/s (% HBM peak) in paged quant decode attn; KV append tokens/s",
@@ -427,6 +661,7 @@ def main():
         "cpu_baseline": cpu,
         "mla": mla,
         "prefill": prefill,
+        "configs": configs,
     }
     print(json.dumps(rec), flush=True)
 

@@ -955,7 +955,8 @@ qdecode_kernel(DecodeArgs a) {
 // dims of one head.  The pair's partial count, its length and its first
 // kFirst partials load together (the partial slots past the count hold
 // stale data, which the merge masks), so a pair of up to kFirst partials
-// costs one round trip to memory.
+// costs one round trip to memory.  (Loading 16 at once measured slower:
+// most pairs have few partials, and the stale slots cost traffic.)
 template <int HP>
 __global__ void __launch_bounds__(512) qdecode_combine_kernel(DecodeArgs a, int D) {
   constexpr int kFirst = 4;

@@ -27,6 +27,7 @@
 #include <algorithm>
 
 #include "vkv_device.h"
+#include <hip/hip_ext.h>
 #include "vkv_internal.h"
 
 namespace vkv {
@@ -241,11 +242,17 @@ void launch_d(const AttnArgs& a, int64_t rows, hipStream_t st) {
   const int R = rep <= 1 ? 1 : rep <= 2 ? 2 : rep <= 4 ? 4 : 8;
   const int n_hg = (rep + R - 1) / R;
   const dim3 grid(a.n_parts, a.Hkv * n_hg, static_cast<unsigned>(rows));
-  if (R == 1) hipLaunchKernelGGL((fdecode_kernel<DT, D, 1>), grid, dim3(64), 0, st, a, rep);
-  else if (R == 2) hipLaunchKernelGGL((fdecode_kernel<DT, D, 2>), grid, dim3(64), 0, st, a, rep);
-  else if (R == 4) hipLaunchKernelGGL((fdecode_kernel<DT, D, 4>), grid, dim3(64), 0, st, a, rep);
-  else hipLaunchKernelGGL((fdecode_kernel<DT, D, 8>), grid, dim3(64), 0, st, a, rep);
+  const TimedLaunch tl = timing_prepare(kTimeFDecode);
+  if (R == 1)
+    hipExtLaunchKernelGGL((fdecode_kernel<DT, D, 1>), grid, dim3(64), 0, st, tl.start, tl.stop, 0, a, rep);
+  else if (R == 2)
+    hipExtLaunchKernelGGL((fdecode_kernel<DT, D, 2>), grid, dim3(64), 0, st, tl.start, tl.stop, 0, a, rep);
+  else if (R == 4)
+    hipExtLaunchKernelGGL((fdecode_kernel<DT, D, 4>), grid, dim3(64), 0, st, tl.start, tl.stop, 0, a, rep);
+  else
+    hipExtLaunchKernelGGL((fdecode_kernel<DT, D, 8>), grid, dim3(64), 0, st, tl.start, tl.stop, 0, a, rep);
   VKV_HIP(hipGetLastError());
+  timing_commit(tl);
 }
 
 template <int DT>

@@ -248,7 +248,7 @@ void launch_roll_mask(int64_t size, int64_t window, int64_t shift, uint8_t* mask
 // Kernel timing (a measurement aid): while enabled, launchers start their
 // main kernel with hipExtLaunchKernelGGL and a start/stop event pair, which
 // the runtime records at the kernel's own start and end.
-enum { kTimeDecode = 0, kTimeMla = 1, kTimeKinds = 2 };
+enum { kTimeDecode = 0, kTimeMla = 1, kTimeFDecode = 2, kTimeKinds = 3 };
 struct TimedLaunch {
   int kind = 0;
   hipEvent_t start = nullptr, stop = nullptr;  // null when timing is off

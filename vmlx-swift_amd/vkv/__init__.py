@@ -84,7 +84,7 @@ EXPORTS = (
     "vkv_dynamic_slice_update", "vkv_dynamic_slice", "vkv_cache_set_offset",
     "vkv_attention_with_cache_update", "vkv_paged_sdpa_noalloc", "vkv_workspace_release",
 )
-TIME_DECODE, TIME_MLA = 0, 1
+TIME_DECODE, TIME_MLA, TIME_FDECODE = 0, 1, 2
 
 _lib = None
 
