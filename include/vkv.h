@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define VKV_ABI_VERSION 1
+#define VKV_ABI_VERSION 2
 
 /* ------------------------------------------------------------------ types */
 
@@ -140,11 +140,17 @@ enum { VKV_MASK_NONE = 0, VKV_MASK_CAUSAL = 1, VKV_MASK_ARRAY = 2 };
  * by MLXFast.scaledDotProductAttention (MLX/MLXFast.swift:203-218):
  * q [B,Hq,L,D], k [B,Hkv,T,D], v [B,Hkv,T,Dv] (strided, same float dtype),
  * Hq % Hkv == 0 (GQA without tiling).  fp32 softmax and accumulation.
- * mask_mode VKV_MASK_ARRAY takes a bool or float (additive) mask array
- * broadcastable to [B,Hq,L,T] (stride 0 on broadcast dims).  out [B,Hq,L,Dv]
- * in q's dtype.  A row with no visible key yields zeros. */
+ * mask_mode VKV_MASK_ARRAY takes a bool mask, or an additive mask in f32 or
+ * q's dtype, broadcastable to [B,Hq,L,T] (stride 0 on broadcast dims); an
+ * additive mask is read as q's dtype and keys whose mask is below that
+ * dtype's lowest finite value are skipped (sdpa_vector.h:15-38, :105-121).
+ * sinks (NULL = none): [Hq] logits (f32 or a 16-bit float, read as q's
+ * dtype), one per query head, each an extra softmax term with a zero value
+ * row (sdpa_vector.h:93-96, :257-260).  out [B,Hq,L,Dv] in q's dtype.  A
+ * row with no visible key yields zeros. */
 int vkv_sdpa(const vkv_array *q, const vkv_array *k, const vkv_array *v, float scale,
-             int32_t mask_mode, const vkv_array *mask, vkv_array *out, void *stream);
+             int32_t mask_mode, const vkv_array *mask, const vkv_array *sinks,
+             vkv_array *out, void *stream);
 
 /* quantizedScaledDotProductAttention (MLXLMCommon/KVCache.swift:1909-1997)
  * over quantized tuples in the reference layout: k_wq [B,Hkv,T,D*bits/32]
@@ -200,11 +206,14 @@ int vkv_mla_decode(const vkv_array *q, const vkv_paged_view *kv, float scale,
  * keys/values, where a VKV_MASK_NONE mask is replaced by the cache's own
  * array mask if makeMask(n:windowSize:nil:returnArray:true) gives one
  * (called after the update, as the reference does).  q [B,Hq,L,D],
- * keys/values [B,Hkv,L,D] (the new tokens), out [B,Hq,L,Dv]. */
+ * keys/values [B,Hkv,L,D] (the new tokens), out [B,Hq,L,Dv].  sinks as in
+ * vkv_sdpa, for the float caches only (a quantized cache refuses them, as
+ * the models that pass sinks do, Libraries/MLXLLM/Models/GPTOSS.swift:
+ * 223-235). */
 int vkv_attention_with_cache_update(const vkv_array *q, const vkv_array *keys,
                                     const vkv_array *values, vkv_cache cache, float scale,
-                                    int32_t mask_mode, const vkv_array *mask, vkv_array *out,
-                                    void *stream);
+                                    int32_t mask_mode, const vkv_array *mask,
+                                    const vkv_array *sinks, vkv_array *out, void *stream);
 
 /* ------------------------------------------------------- per-layer caches */
 

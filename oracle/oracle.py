@@ -63,7 +63,7 @@ def _declare(L):
     L.vkvo_dequantize.argtypes = [vp, vp, vp, i32, i64, i32, i32, i32, i32, vp]
     L.vkvo_dequantize_rule_split.restype = i64
     L.vkvo_dequantize_rule_split.argtypes = [vp, vp, vp, i32, i64, i32, i32, i32]
-    L.vkvo_sdpa.argtypes = [vp, vp, vp] + [i32] * 7 + [f32, i32, vp, vp] + [i64] * 4 + [vp]
+    L.vkvo_sdpa.argtypes = [vp, vp, vp] + [i32] * 7 + [f32, i32, vp, vp] + [i64] * 4 + [i32, vp, vp]
     L.vkvo_quantized_sdpa.argtypes = (
         [vp, i32] + [vp] * 6 + [i32] * 8 + [f32, i32, vp, vp] + [i64] * 4 + [i32, vp, vp]
     )
@@ -151,15 +151,19 @@ def _mask_args(mask, B, H, L, T):
     return 3, None, mf, st, mf
 
 
-def sdpa(q, k, v, scale, mask=None):
-    """q [B,Hq,L,D], k [B,Hkv,T,D], v [B,Hkv,T,Dv] as f32 values -> f64 out."""
+def sdpa(q, k, v, scale, mask=None, q_dtype=F32, sinks=None):
+    """q [B,Hq,L,D], k [B,Hkv,T,D], v [B,Hkv,T,Dv] as f32 values -> f64 out.
+    An additive mask is read in q_dtype (rounded to it, keys below its
+    lowest finite value skipped); sinks: optional [Hq] logits (values of
+    q_dtype)."""
     q, k, v = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v))
     B, Hq, L, D = q.shape
     Hkv, T, Dv = k.shape[1], k.shape[2], v.shape[3]
     mode, mb, mf, st, keep = _mask_args(mask, B, Hq, L, T)
+    sk = None if sinks is None else np.ascontiguousarray(sinks, dtype=np.float32)
     out = np.empty((B, Hq, L, Dv), np.float64)
     lib().vkvo_sdpa(_p(q), _p(k), _p(v), B, Hq, Hkv, L, T, D, Dv, scale, mode, _p(mb),
-                    _p(mf), *st, _p(out))
+                    _p(mf), *st, q_dtype, _p(sk), _p(out))
     return out
 
 

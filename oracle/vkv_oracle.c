@@ -254,11 +254,17 @@ static inline int mask_visible(int mask_mode, const uint8_t *bmask, const float 
 }
 
 /* MLXFast.swift:173-218 semantics as computed by sdpa_vector.h:15-177:
- * q scaled in fp32, softmax over visible keys, zero output for an empty row. */
+ * q scaled in fp32, softmax over visible keys, zero output for an empty row.
+ * An additive mask is read in the query dtype q_dtype (the kernel's `const
+ * device T* fmask`, :15-38): each value is rounded to it, and a key whose
+ * rounded mask is below the dtype's lowest finite value is skipped
+ * (:105-121).  sinks (NULL = none): per query head logit [Hq] that starts
+ * the running max with sum 1 (:93-96), i.e. one more softmax term whose
+ * value row is zero. */
 void vkvo_sdpa(const float *q, const float *k, const float *v, int B, int Hq,
                int Hkv, int L, int T, int D, int Dv, float scale, int mask_mode,
                const uint8_t *bmask, const float *fmask, int64_t msb, int64_t msh,
-               int64_t msl, int64_t mst, double *out) {
+               int64_t msl, int64_t mst, int q_dtype, const float *sinks, double *out) {
   const int rep = Hq / Hkv;
   double *sc = (double *)malloc(sizeof(double) * (size_t)(T > 0 ? T : 1));
   unsigned char *vis = (unsigned char *)malloc((size_t)(T > 0 ? T : 1));
@@ -267,19 +273,24 @@ void vkvo_sdpa(const float *q, const float *k, const float *v, int B, int Hq,
       for (int l = 0; l < L; l++) {
         const float *qr = q + (((int64_t)b * Hq + h) * L + l) * D;
         const int hk = h / rep;
-        double mx = -INFINITY;
+        double mx = sinks ? (double)sinks[h] : -INFINITY;
         for (int t = 0; t < T; t++) {
           double add;
           int64_t mo = b * msb + h * msh + l * msl + t * mst;
           vis[t] = (unsigned char)mask_visible(mask_mode, bmask, fmask, mo, l, L, t, T, &add);
+          if (mask_mode == 3) {
+            add = (double)round_to((float)add, q_dtype);
+            vis[t] = add >= -(double)type_max(q_dtype);
+          }
           if (!vis[t]) continue;
           const float *kr = k + (((int64_t)b * Hkv + hk) * T + t) * D;
           double s = 0.0;
           for (int d = 0; d < D; d++) s += (double)(scale * qr[d]) * (double)kr[d];
-          sc[t] = s + add;
+          /* the kernel adds the mask to its fp32 score (U = float) */
+          sc[t] = mask_mode == 3 ? (double)((float)s + (float)add) : s;
           if (sc[t] > mx) mx = sc[t];
         }
-        double den = 0.0;
+        double den = sinks ? exp((double)sinks[h] - mx) : 0.0;
         double *o = out + (((int64_t)b * Hq + h) * L + l) * Dv;
         for (int d = 0; d < Dv; d++) o[d] = 0.0;
         for (int t = 0; t < T; t++) {

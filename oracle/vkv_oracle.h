@@ -52,12 +52,16 @@ int64_t vkvo_dequantize_rule_split(const uint32_t *wq, const void *scales,
  * the stored dtype); q is scaled in f32 (sdpa_vector.h:78).  Accumulation is
  * f64.  mask_mode: 0 none, 1 causal (key i visible to query row l when
  * i <= T - L + l), 2 bool, 3 additive.  Mask element (b,h,l,t) lives at
- * mask[b*msb + h*msh + l*msl + t*mst].  Masked keys are skipped; a row with
- * no visible key returns zeros (sdpa_vector.h:160-166). out [B,Hq,L,Dv] f64. */
+ * mask[b*msb + h*msh + l*msl + t*mst].  An additive mask is rounded to the
+ * query dtype q_dtype and keys below its lowest finite value are skipped
+ * (sdpa_vector.h:15-38, :105-121); masked keys are skipped; a row with no
+ * visible key (and no sink) returns zeros (sdpa_vector.h:160-166).  sinks
+ * (NULL = none): [Hq] logits, one extra softmax term per query head with a
+ * zero value row (:93-96).  out [B,Hq,L,Dv] f64. */
 void vkvo_sdpa(const float *q, const float *k, const float *v, int B, int Hq,
                int Hkv, int L, int T, int D, int Dv, float scale, int mask_mode,
                const uint8_t *bmask, const float *fmask, int64_t msb, int64_t msh,
-               int64_t msl, int64_t mst, double *out);
+               int64_t msl, int64_t mst, int q_dtype, const float *sinks, double *out);
 
 /* ---- quantized SDPA (KVCache.swift:1909-1997) ----
  * q [B,Hq,L,D] f32 values of dtype q_dtype; the queries are first scaled in

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     missing = [s for s in decl if not hasattr(L, s)]
     assert not missing
     assert sorted(vkv.EXPORTS) == decl
-    assert L.vkv_abi_version() == 1
+    assert L.vkv_abi_version() == 2
 
 
 def test_errors_are_reported_not_thrown():
@@ -47,7 +47,7 @@ def test_errors_are_reported_not_thrown():
     with pytest.raises(vkv.VKVError, match="updateQuantized"):  # KVCache.swift:1126-1130
         vkv._chk(L.vkv_cache_update(q._h, None, None, None, None, None))
     # the last error is per thread and cleared by the next success
-    assert L.vkv_abi_version() == 1
+    assert L.vkv_abi_version() == 2
 
 
 def test_meta_state_roundtrip_and_validation():

@@ -119,7 +119,7 @@ def test_sdpa_decode_one_token(dtype, Hq, Hkv, D, mask, monkeypatch):
     scale = D ** -0.5
     out = vkv.scaled_dot_product_attention(dev(q, dtype), k_dev, v_dev, scale, mask=m_dev)
     f = lambda a: O.to_f32(a, dtype) if dtype != O.F32 else a
-    ref = O.sdpa(f(q), f(k), f(v), scale, mask=m_ref)
+    ref = O.sdpa(f(q), f(k), f(v), scale, mask=m_ref, q_dtype=dtype)
     got = values(out, dtype)
     assert (np.abs(got - ref) <= attn_tol(dtype, ref)).all()
     if mask == "bool":
@@ -150,7 +150,7 @@ def test_sdpa_masks(mask):
     out = vkv.scaled_dot_product_attention(dev(q, dtype), dev(k, dtype), dev(v, dtype), 0.1,
                                            mask=m_dev)
     f = lambda a: O.to_f32(a, dtype)
-    ref = O.sdpa(f(q), f(k), f(v), 0.1, mask=m_ref)
+    ref = O.sdpa(f(q), f(k), f(v), 0.1, mask=m_ref, q_dtype=dtype)
     got = values(out, dtype)
     assert (np.abs(got - ref) <= attn_tol(dtype, ref)).all()
     if mask == "bool_empty_row":
@@ -184,3 +184,89 @@ def test_quantized_sdpa_matches_oracle(dtype, bits, mask):
                    mask=m_ref)
     got = values(out, dtype)
     assert_qclose(got, ref, wb, dtype, f"{dtype} {bits} {mask}")
+
+
+@pytest.mark.parametrize("path", ["decode", "generic", "prefill", "router"])
+@pytest.mark.parametrize("dtype", [O.BF16, O.F16])
+def test_sdpa_sinks(path, dtype, monkeypatch):
+    """Attention sinks (MLXFast.scaledDotProductAttention(..., sinks:),
+    sdpa_vector.h:93-96, :257-260) on every float path: the dense decode
+    kernel (one token, a fully masked row keeps only its sink and yields
+    zeros), the generic kernel, the multi-query prefill kernel (causal), and
+    the router over a KVCacheSimple; against the oracle."""
+    rng = np.random.default_rng(60 + dtype + len(path))
+    B, Hq, Hkv, D = 2, 16, 4, 128
+    L, T = (1, 700) if path in ("decode", "generic") else (40, 40)
+    q = rand_bits(rng, (B, Hq, L, D), dtype)
+    k = rand_bits(rng, (B, Hkv, T, D), dtype)
+    v = rand_bits(rng, (B, Hkv, T, D), dtype)
+    sk = O.from_f32((rng.standard_normal(Hq) * 2 + 5).astype(np.float32), dtype)
+    f = lambda a: O.to_f32(a, dtype)
+    scale = D ** -0.5
+    if L == 1:
+        m = rng.random((B, Hq, 1, T)) > 0.3
+        m[1, 3, 0] = False
+        m_dev, m_ref = torch.from_numpy(m).cuda(), m
+    else:
+        m_dev = m_ref = "causal"
+    if path == "generic":
+        monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
+    if path == "router":
+        c = vkv.KVCacheSimple()
+        out = vkv.attention_with_cache_update(dev(q, dtype), dev(k, dtype), dev(v, dtype), c, scale,
+                                              mask=m_dev, sinks=dev(sk, dtype))
+        assert c.offset == T
+    else:
+        out = vkv.scaled_dot_product_attention(dev(q, dtype), dev(k, dtype), dev(v, dtype), scale,
+                                               mask=m_dev, sinks=dev(sk, dtype))
+    ref = O.sdpa(f(q), f(k), f(v), scale, mask=m_ref, q_dtype=dtype, sinks=f(sk))
+    got = values(out, dtype)
+    assert_within(got, ref, attn_tol(dtype, ref), path)
+    if L == 1:
+        assert (got[1, 3, 0] == 0).all()
+    # the sinks change the result (they are not ignored)
+    plain = O.sdpa(f(q), f(k), f(v), scale, mask=m_ref, q_dtype=dtype)
+    assert np.abs(plain - ref).max() > 0.1 * np.abs(plain).max()
+
+
+def test_quantized_cache_refuses_sinks():
+    c = vkv.QuantizedKVCache(64, 4)
+    x = torch.zeros((1, 2, 1, 64), dtype=torch.bfloat16, device="cuda")
+    q = torch.zeros((1, 4, 1, 64), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(vkv.VKVError, match="sinks"):
+        vkv.attention_with_cache_update(q, x, x, c, 0.125,
+                                        sinks=torch.zeros(4, dtype=torch.bfloat16, device="cuda"))
+    assert c.offset == 0
+
+
+@pytest.mark.parametrize("generic", [False, True])
+def test_sdpa_additive_mask_in_query_dtype(generic, monkeypatch):
+    """Additive masks are read in the query dtype (sdpa_vector.h:15-38,
+    :105-121): with f16 queries an f32 mask of -1e9 rounds to -inf and
+    empties the row (zeros); with bf16 queries a bf16 mask of -1e9 stays
+    finite, the fp32 scores collapse to -1e9 and the row averages V."""
+    if generic:
+        monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
+    rng = np.random.default_rng(70)
+    B, Hq, Hkv, T, D = 1, 4, 2, 300, 64
+    for dtype, mdt in ((O.F16, np.float32), (O.BF16, None)):
+        q = rand_bits(rng, (B, Hq, 1, D), dtype)
+        k = rand_bits(rng, (B, Hkv, T, D), dtype)
+        v = rand_bits(rng, (B, Hkv, T, D), dtype)
+        m = (rng.standard_normal((B, Hq, 1, T)) * 2).astype(np.float32)
+        m[0, 1] = -1e9
+        if mdt is None:
+            mb = O.from_f32(m, dtype)
+            m_dev, m_ref = dev(mb, dtype), O.to_f32(mb, dtype)
+        else:
+            m_dev, m_ref = torch.from_numpy(m).cuda(), m
+        f = lambda a: O.to_f32(a, dtype)
+        out = values(vkv.scaled_dot_product_attention(dev(q, dtype), dev(k, dtype), dev(v, dtype),
+                                                      0.125, mask=m_dev), dtype)
+        ref = O.sdpa(f(q), f(k), f(v), 0.125, mask=m_ref, q_dtype=dtype)
+        assert_within(out, ref, attn_tol(dtype, ref), f"dtype {dtype}")
+        if dtype == O.F16:
+            assert (out[0, 1] == 0).all()
+        else:
+            mean_v = f(v)[0, 0].mean(0)  # head 1 reads kv head 0
+            assert np.abs(out[0, 1, 0] - mean_v).max() < 2e-2

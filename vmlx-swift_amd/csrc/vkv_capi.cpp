@@ -241,10 +241,10 @@ int vkv_dequantize_affine(const vkv_array* wq, const vkv_array* scales, const vk
 // ---------------------------------------------------------------- attention
 
 namespace {
-// The attention mask arguments: none, causal, or a bool / additive f32
-// array broadcast to [B, Hq, L, T].
+// The attention mask arguments: none, causal, or a bool / additive array
+// (f32 or the query dtype) broadcast to [B, Hq, L, T].
 void set_mask(AttnArgs& a, int32_t mask_mode, const vkv_array* mask, int64_t B, int64_t Hq,
-              int64_t L, int64_t T) {
+              int64_t L, int64_t T, int q_dtype) {
   if (mask_mode == VKV_MASK_CAUSAL) {
     a.mask_mode = 1;
   } else if (mask_mode == VKV_MASK_ARRAY) {
@@ -252,9 +252,14 @@ void set_mask(AttnArgs& a, int32_t mask_mode, const vkv_array* mask, int64_t B, 
     const int64_t target[4] = {B, Hq, L, T};
     int64_t ms[4];
     mask_strides(*mask, target, ms);
-    if (mask->dtype == VKV_BOOL || mask->dtype == VKV_U8) a.mask_mode = 2;
-    else if (mask->dtype == VKV_F32) a.mask_mode = 3;
-    else throw Error("mask must be bool or f32 (additive)");
+    if (mask->dtype == VKV_BOOL || mask->dtype == VKV_U8) {
+      a.mask_mode = 2;
+    } else if (mask->dtype == VKV_F32 || mask->dtype == q_dtype) {
+      a.mask_mode = 3;
+      a.mask_dtype = mask->dtype;
+    } else {
+      throw Error("mask must be bool, or additive in f32 or the query dtype");
+    }
     a.mask = mask->data;
     a.m_sb = ms[0];
     a.m_sh = ms[1];
@@ -264,12 +269,25 @@ void set_mask(AttnArgs& a, int32_t mask_mode, const vkv_array* mask, int64_t B, 
     throw Error("unknown mask mode");
   }
 }
+
+// Attention sinks: one logit per query head, f32 or the query dtype.
+void set_sinks(AttnArgs& a, const vkv_array* sinks, int64_t Hq) {
+  if (!sinks) return;
+  if (sinks->ndim != 1 || sinks->shape[0] != Hq || (Hq > 1 && sinks->strides[0] != 1))
+    throw Error("sinks must be a contiguous [Hq] array");
+  if (sinks->dtype != VKV_F32 && sinks->dtype != VKV_F16 && sinks->dtype != VKV_BF16)
+    throw Error("sinks must be f32, f16 or bf16");
+  if (!sinks->data) throw Error("sinks has no data");
+  a.sinks = sinks->data;
+  a.sinks_dtype = sinks->dtype;
+}
 }  // namespace
 
 extern "C" {
 
 int vkv_sdpa(const vkv_array* q, const vkv_array* k, const vkv_array* v, float scale,
-             int32_t mask_mode, const vkv_array* mask, vkv_array* out, void* stream) {
+             int32_t mask_mode, const vkv_array* mask, const vkv_array* sinks, vkv_array* out,
+             void* stream) {
   return guard([&] {
     need(q, "q");
     need(k, "k");
@@ -309,7 +327,8 @@ int vkv_sdpa(const vkv_array* q, const vkv_array* k, const vkv_array* v, float s
     a.o_sb = out->strides[0];
     a.o_sh = out->strides[1];
     a.o_sl = out->strides[2];
-    set_mask(a, mask_mode, mask, B, Hq, L, T);
+    set_mask(a, mask_mode, mask, B, Hq, L, T, q->dtype);
+    set_sinks(a, sinks, Hq);
     run_attention(q->dtype, 0, 64, false, a, B * L, T, S(stream));
   });
 }
@@ -381,7 +400,7 @@ int vkv_quantized_sdpa(const vkv_array* q, const vkv_array* k_wq, const vkv_arra
     a.o_sb = out->strides[0];
     a.o_sh = out->strides[1];
     a.o_sl = out->strides[2];
-    set_mask(a, mask_mode, mask, B, Hq, L, T);
+    set_mask(a, mask_mode, mask, B, Hq, L, T, q->dtype);
     run_attention(q->dtype, bits, group_size, true, a, B * L, T, S(stream));
   });
 }
@@ -495,7 +514,8 @@ int vkv_workspace_release(void* stream, int64_t* bytes) {
 
 int vkv_attention_with_cache_update(const vkv_array* q, const vkv_array* keys, const vkv_array* values,
                                     vkv_cache cache, float scale, int32_t mask_mode,
-                                    const vkv_array* mask, vkv_array* out, void* stream) {
+                                    const vkv_array* mask, const vkv_array* sinks, vkv_array* out,
+                                    void* stream) {
   return guard([&] {
     need(q, "q");
     need(keys, "keys");
@@ -505,11 +525,14 @@ int vkv_attention_with_cache_update(const vkv_array* q, const vkv_array* keys, c
       if (rc != 0) throw Error(g_error);
     };
     if (!cache) {  // AttentionUtils.swift:85-93
-      call(vkv_sdpa(q, keys, values, scale, mask_mode, mask, out, stream));
+      call(vkv_sdpa(q, keys, values, scale, mask_mode, mask, sinks, out, stream));
       return;
     }
     if (q->ndim != 4 || out->ndim != 4) throw Error("q and out must be 4-D");
     if (cache->impl->kind() == VKV_CACHE_QUANTIZED) {  // :94-105
+      // the quantized path has no sinks (the models refuse them,
+      // Libraries/MLXLLM/Models/GPTOSS.swift:223-235)
+      if (sinks) throw Error("quantized attention does not support sinks");
       vkv_paged_view view{};
       call(vkv_cache_update_quantized(cache, keys, values, stream, &view));
       const int64_t B = q->shape[0], Hq = q->shape[1], L = q->shape[2];
@@ -546,7 +569,7 @@ int vkv_attention_with_cache_update(const vkv_array* q, const vkv_array* keys, c
       a.o_sb = out->strides[0];
       a.o_sh = out->strides[1];
       a.o_sl = out->strides[2];
-      set_mask(a, mask_mode, mask, B, Hq, L, view.max_len);
+      set_mask(a, mask_mode, mask, B, Hq, L, view.max_len, view.dtype);
       run_attention(view.dtype, view.bits, view.group_size, true, a, B * L, view.max_len, S(stream));
       return;
     }
@@ -563,7 +586,7 @@ int vkv_attention_with_cache_update(const vkv_array* q, const vkv_array* keys, c
         m = &cm;
       }
     }
-    call(vkv_sdpa(q, &ck, &cv, scale, mode, m, out, stream));
+    call(vkv_sdpa(q, &ck, &cv, scale, mode, m, sinks, out, stream));
   });
 }
 

@@ -60,6 +60,20 @@ __device__ __forceinline__ float round_to(float f) {
   return Elem<DT>::to_f32(Elem<DT>::from_f32(f));
 }
 
+// Element i of a float array of dtype `dt` (kF32, kF16 or kBF16) as fp32,
+// rounded to the dtype DT of the attention (the reference kernels read
+// masks and sinks as the query dtype T, sdpa_vector.h:15-38).
+__device__ __forceinline__ float load_f32(const void* p, int dt, int64_t i) {
+  if (dt == kF16) return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  if (dt == kBF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  return static_cast<const float*>(p)[i];
+}
+template <int DT>
+__device__ __forceinline__ float load_as(const void* p, int dt, int64_t i) {
+  const float v = load_f32(p, dt, i);
+  return dt == DT ? v : round_to<DT>(v);
+}
+
 // ---------------------------------------------------------------------------
 // Affine paged chunk format (block_size % 32 == 0, head_dim % 32 == 0).
 // One (block, kv head) chunk holds K codes, V codes, then the scale/bias

@@ -127,6 +127,13 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
   for (int r = 0; r < REP; r++) {
     m[r] = -INFINITY;
     l[r] = 0.0f;
+    // an attention sink is one more logit with a zero value row, counted
+    // once per row: the running max starts at it with sum 1
+    // (sdpa_vector.h:93-96, :257-260)
+    if (a.sinks && part == 0 && r < nh) {
+      m[r] = load_as<DT>(a.sinks, a.sinks_dtype, h0 + r);
+      l[r] = 1.0f;
+    }
 #pragma unroll
     for (int e = 0; e < VEC; e++) o[r][e] = 0.0f;
   }
@@ -162,8 +169,10 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
         if (a.mask_mode == 2) {
           vis = static_cast<const uint8_t*>(a.mask)[mo] != 0;
         } else {
-          const float add = static_cast<const float*>(a.mask)[mo];
-          vis = add >= -3.402823466e38f;
+          // the mask in the query dtype; keys below its lowest finite
+          // value are skipped (sdpa_vector.h:105-121)
+          const float add = load_as<DT>(a.mask, a.mask_dtype, mo);
+          vis = add >= -E::kMax;
           s[r] += add;
         }
       }

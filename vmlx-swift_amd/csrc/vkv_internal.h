@@ -90,6 +90,9 @@ struct AttnArgs {
   float scale;
   KVSrc kv;
   int32_t mask_mode;       // 0 none, 1 causal, 2 bool array, 3 additive array
+  int32_t mask_dtype;      // additive mask element type (0 f32, 1 f16, 2 bf16)
+  const void* sinks;       // per query head attention sink logits [Hq], or null
+  int32_t sinks_dtype;     // (0 f32, 1 f16, 2 bf16)
   const void* mask;
   int64_t m_sb, m_sh, m_sl, m_st;
   void* out;

@@ -752,6 +752,12 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(AttnArgs a, int h_off
 #pragma unroll
   for (int r = 0; r < REP; r++) o[r] = 0.0f;
   float m_run = -3.402823466e38f, l_run = 0.0f;  // lanes r < REP of wave 0 own head r
+  // an attention sink (MLXFast semantics only) is one more logit with a
+  // zero value row, counted once per row (sdpa_vector.h:93-96, :257-260)
+  if (!QSEM && a.sinks && part == 0 && tid < REP) {
+    m_run = load_as<DT>(a.sinks, a.sinks_dtype, hk * rep_total + h_off + tid);
+    l_run = 1.0f;
+  }
   __syncthreads();
 
   for (int64_t t0 = t_begin; t0 < t_end; t0 += kTile) {
@@ -787,14 +793,17 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(AttnArgs a, int h_off
               const int64_t mo = b * a.m_sb + h * a.m_sh + l * a.m_sl + t * a.m_st;
               if (a.mask_mode == 2) {
                 vis = static_cast<const uint8_t*>(a.mask)[mo] != 0;
+              } else if (QSEM) {
+                // scores (T) + mask: a T mask keeps the sum in T, an f32
+                // mask promotes it to f32 (KVCache.swift:1963-1969)
+                const float add = load_f32(a.mask, a.mask_dtype, mo);
+                s = a.mask_dtype == DT ? round_to<DT>(s + add) : s + add;
               } else {
-                const float add = static_cast<const float*>(a.mask)[mo];
-                if (QSEM) {
-                  s += add;
-                } else {
-                  vis = add >= -3.402823466e38f;
-                  s += add;
-                }
+                // the mask in the query dtype; keys below its lowest finite
+                // value are skipped (sdpa_vector.h:105-121)
+                const float add = load_as<DT>(a.mask, a.mask_dtype, mo);
+                vis = add >= -E::kMax;
+                s += add;
               }
             }
             if (QSEM && !vis && t < t_end) {

@@ -191,6 +191,14 @@ prefill_kernel(const AttnArgs a, int rep) {
   for (int rb = 0; rb < 2; rb++) {
     m_run[rb] = -1e30f;  // finite: a masked score (-inf) gives p = 0
     l_run[rb] = 0.f;
+    // an attention sink (MLXFast semantics only) is one more logit with a
+    // zero value row, counted once per row (sdpa_vector.h:93-96): the
+    // running max (log2 units) starts at it with sum 1
+    if (!QSEM && a.sinks && part == 0) {
+      const int64_t qr = min<int64_t>(qrow[rb], nrows - 1);
+      m_run[rb] = load_as<DT>(a.sinks, a.sinks_dtype, hk * rep + static_cast<int>(qr % rep)) * kLog2e;
+      l_run[rb] = kg == 0 ? 1.f : 0.f;  // the two lane halves' sums are added at the end
+    }
 #pragma unroll
     for (int db = 0; db < kDB; db++) o[rb][db] = f32x16_t{};
   }

@@ -192,6 +192,10 @@ def _as_array(x):
     return x if isinstance(x, Array) else arr(x)
 
 
+def _sinks_arg(sinks):
+    return None if sinks is None else C.byref(arr(sinks))
+
+
 def _mask_args(mask):
     if mask is None:
         return MASK_NONE, None
@@ -202,11 +206,12 @@ def _mask_args(mask):
 
 
 def scaled_dot_product_attention(queries, keys, values, scale: float, mask=None, stream=None,
-                                 out=None):
+                                 out=None, sinks=None):
     """MLXFast.scaledDotProductAttention (Source/MLX/MLXFast.swift:203-218).
     keys, values and an array mask may be tensors or library-owned Arrays
     (the views a cache returns); `out` may be given (nothing is allocated
-    then, as a captured HIP graph needs)."""
+    then, as a captured HIP graph needs); `sinks` is an optional [Hq]
+    tensor of attention-sink logits."""
     torch = _torch()
     B, Hq, L, _ = queries.shape
     a_k, a_v = _as_array(keys), _as_array(values)
@@ -215,12 +220,13 @@ def scaled_dot_product_attention(queries, keys, values, scale: float, mask=None,
     mode, m = _mask_args(mask)
     a_out = arr(out)
     _chk(lib().vkv_sdpa(C.byref(arr(queries)), C.byref(a_k), C.byref(a_v),
-                        C.c_float(scale), mode, m, C.byref(a_out), stream_ptr(stream)))
+                        C.c_float(scale), mode, m, _sinks_arg(sinks), C.byref(a_out),
+                        stream_ptr(stream)))
     return out
 
 
 def attention_with_cache_update(queries, keys, values, cache, scale: float, mask=None,
-                                stream=None, out=None):
+                                stream=None, out=None, sinks=None):
     """attentionWithCacheUpdate (MLXLMCommon/AttentionUtils.swift:77-143):
     updates `cache` (None: no cache) with the new keys/values and attends the
     queries [B, Hq, L, D] over the cached K/V; see
@@ -234,8 +240,8 @@ def attention_with_cache_update(queries, keys, values, cache, scale: float, mask
     a_out = arr(out)
     _chk(lib().vkv_attention_with_cache_update(
         C.byref(arr(queries)), C.byref(arr(keys)), C.byref(arr(values)),
-        cache._h if cache is not None else None, C.c_float(scale), mode, m, C.byref(a_out),
-        stream_ptr(stream)))
+        cache._h if cache is not None else None, C.c_float(scale), mode, m, _sinks_arg(sinks),
+        C.byref(a_out), stream_ptr(stream)))
     return out
 
 
