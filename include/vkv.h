@@ -198,6 +198,19 @@ int vkv_paged_sdpa_noalloc(const vkv_array *q, const vkv_paged_view *kv, float s
 int vkv_mla_decode(const vkv_array *q, const vkv_paged_view *kv, float scale,
                    vkv_array *out, void *stream);
 
+/* quantizedScaledDotProductAttention(queries:quantizedKeys:quantizedValues:
+ * scale:mask:groupSize:bits:) (KVCache.swift:1909-1997) over the paged view
+ * that vkv_cache_update_quantized returns (or a pool view of affine
+ * blocks), for any number of query tokens: the binding for a model that
+ * calls updateQuantized and then quantizedScaledDotProductAttention itself
+ * (GPTOSS.swift:239-248, MiMoV2Flash.swift:36-45) without materializing the
+ * tuples.  q [n_seqs,Hq,L,D], out [n_seqs,Hq,L,Dv] in the view's dtype;
+ * masks as in vkv_quantized_sdpa (causal: query l of a sequence of length
+ * T sees keys t <= T - L + l).  Same arithmetic as vkv_quantized_sdpa. */
+int vkv_quantized_paged_sdpa(const vkv_array *q, const vkv_paged_view *kv, float scale,
+                             int32_t mask_mode, const vkv_array *mask, vkv_array *out,
+                             void *stream);
+
 /* attentionWithCacheUpdate(queries:keys:values:cache:scale:mask:)
  * (AttentionUtils.swift:77-143), one call: with cache == NULL, SDPA over
  * keys/values; with a QuantizedKVCache, updateQuantized then quantized SDPA
@@ -260,9 +273,11 @@ int vkv_cache_update(vkv_cache cache, const vkv_array *keys, const vkv_array *va
 
 /* updateQuantized(keys:values:) (KVCache.swift:1049-1122): quantizes the new
  * tokens (affine, bit-exact with quantized.h:2393-2497) into the cache and
- * returns the whole cache as a paged view for vkv_paged_sdpa (queries
- * [B,Hq,D] for one decode token).  The reference-layout tuples are available
- * from vkv_cache_state(). */
+ * returns the whole cache as a paged view: the updated tuples in the paged
+ * block format, which vkv_quantized_paged_sdpa (any query length, masks)
+ * and vkv_paged_sdpa (one decode token) attend over directly.  The
+ * reference-layout tuples themselves come from vkv_cache_state() (a
+ * gather). */
 int vkv_cache_update_quantized(vkv_cache cache, const vkv_array *keys,
                                const vkv_array *values, void *stream,
                                vkv_paged_view *out);

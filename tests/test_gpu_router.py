@@ -6,6 +6,7 @@ through the generic kernel), RotatingKVCache, and CompilableKVCache, whose
 array mask the router takes after the update as the reference does."""
 import numpy as np
 import pytest
+import torch
 
 import kvcache_ref as R
 import oracle as O
@@ -102,3 +103,71 @@ def test_router_compilable_cache_takes_cache_mask():
         ref = O.sdpa(f(q), f(rk), f(rv), D ** -0.5, r.make_mask(L))
         assert c.offset == r.offset
         assert close(out, ref, dtype), step
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_update_quantized_then_quantized_attention(bits):
+    """A model that calls updateQuantized and then
+    quantizedScaledDotProductAttention itself (GPTOSS.swift:239-248,
+    MiMoV2Flash.swift:36-45): the paged view updateQuantized returns is
+    attended over directly for any query length and mask, without a state
+    gather; against the reference-arithmetic oracle."""
+    dtype, D, Hkv, Hq = O.BF16, 128, 2, 8
+    rng = np.random.default_rng(30 + bits)
+    c, r = vkv.QuantizedKVCache(64, bits), R.QuantizedKVCacheRef(64, bits)
+    f = lambda a: O.to_f32(a, dtype)
+    for L, mask in [(20, "causal"), (1, None), (5, "causal"), (1, "bool"), (3, None)]:
+        q = rand_bits(rng, (2, Hq, L, D), dtype)
+        k = rand_bits(rng, (2, Hkv, L, D), dtype)
+        v = rand_bits(rng, (2, Hkv, L, D), dtype)
+        view = c.update_quantized(dev(k, dtype), dev(v, dtype))
+        r.update_quantized(k, v, dtype)
+        T = r.offset
+        m_dev = m_ref = mask
+        if mask == "bool":
+            m = rng.random((2, Hq, L, T)) > 0.3
+            m_dev, m_ref = torch.from_numpy(m).cuda(), m
+        out = vkv.quantized_paged_attention(dev(q, dtype), view, D ** -0.5, mask=m_dev)
+        kq, ks, kb, vq, vs, vb = r.state
+        ref, wb = qref(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64,
+                       bits, mask=m_ref, rounding=O.REF_CHUNK if L >= 16 else O.REF_DECODE)
+        assert_qclose(values(out, dtype), ref, wb, dtype, f"L {L} mask {mask}")
+
+
+def test_quantized_attention_over_pool_view_chunks():
+    """A chunk of 4 query tokens per sequence over a paged pool with mixed
+    lengths (continuous batching): causal per sequence (query l of a
+    sequence of T tokens sees keys t <= T - 4 + l)."""
+    dtype, bits, D, Hkv, Hq, bs, L = O.BF16, 4, 128, 2, 8, 32, 4
+    rng = np.random.default_rng(40)
+    lens = [37, 300, 4, 129]
+    nb = sum((n + bs - 1) // bs for n in lens) + 1
+    pool = vkv.PagedPool(nb, bs, 1, Hkv, D, dtype=vkv.BF16, bits=bits)
+    perm = rng.permutation(np.arange(1, nb))
+    tables, slots, keys, vals, i = [], [], [], [], 0
+    for n in lens:
+        t = [int(x) for x in perm[i:i + (n + bs - 1) // bs]]
+        i += len(t)
+        tables.append(t)
+        slots += [t[p // bs] * bs + p % bs for p in range(n)]
+        keys.append(rand_bits(rng, (n, Hkv, D), dtype))
+        vals.append(rand_bits(rng, (n, Hkv, D), dtype))
+    pool.append(0, dev(np.concatenate(keys), dtype), dev(np.concatenate(vals), dtype),
+                torch.tensor(slots, dtype=torch.int32, device="cuda"))
+    tab = np.zeros((len(lens), max(len(t) for t in tables)), np.int32)
+    for s, t in enumerate(tables):
+        tab[s, :len(t)] = t
+    tab_d = torch.from_numpy(tab).cuda()
+    len_d = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    view = pool.view(0, tab_d, len_d, max(lens))
+    q = rand_bits(rng, (len(lens), Hq, L, D), dtype)
+    out = values(vkv.quantized_paged_attention(dev(q, dtype), view, D ** -0.5, mask="causal"),
+                 dtype)
+    f = lambda a: O.to_f32(a, dtype)
+    for s, n in enumerate(lens):
+        rk = O.quantize(np.ascontiguousarray(keys[s].transpose(1, 0, 2)), dtype, 64, bits)
+        rv = O.quantize(np.ascontiguousarray(vals[s].transpose(1, 0, 2)), dtype, 64, bits)
+        ref, wb = (x[0] for x in qref(f(q[s])[None], dtype, rk[0][None], f(rk[1])[None],
+                                      f(rk[2])[None], rv[0][None], f(rv[1])[None], f(rv[2])[None],
+                                      D ** -0.5, 64, bits, mask="causal"))
+        assert_qclose(out[s], ref, wb, dtype, f"sequence {s} (length {n})")

@@ -512,6 +512,59 @@ int vkv_workspace_release(void* stream, int64_t* bytes) {
   });
 }
 
+int vkv_quantized_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale,
+                             int32_t mask_mode, const vkv_array* mask, vkv_array* out,
+                             void* stream) {
+  return guard([&] {
+    need(q, "q");
+    need(kv, "kv");
+    need(out, "out");
+    auto call = [](int rc) {
+      if (rc != 0) throw Error(g_error);
+    };
+    const vkv_paged_view& view = *kv;
+    if (view.bits != 4 && view.bits != 8) throw Error("the view must hold affine 4- or 8-bit blocks");
+    if (view.flags & VKV_VIEW_KEYS_ONLY) throw Error("a keys-only view has no values");
+    if (q->ndim != 4 || out->ndim != 4) throw Error("q and out must be 4-D");
+    const int64_t B = q->shape[0], Hq = q->shape[1], L = q->shape[2];
+    if (q->dtype != view.dtype || out->dtype != view.dtype) throw Error("q/out dtype must match the view");
+    if (q->shape[3] != view.head_dim || out->shape[0] != B || out->shape[1] != Hq ||
+        out->shape[2] != L || out->shape[3] != view.v_head_dim || B != view.n_seqs ||
+        view.n_kv_heads < 1 || Hq % view.n_kv_heads)
+      throw Error("q/out shapes do not match the view");
+    if (L == 1 && mask_mode == VKV_MASK_NONE) {
+      // one decode token: the paged decode path over [B, Hq, D] views
+      vkv_array q3 = *q, o3 = *out;
+      q3.ndim = o3.ndim = 3;
+      q3.shape[2] = q->shape[3];
+      q3.strides[2] = q->strides[3];
+      o3.shape[2] = out->shape[3];
+      o3.strides[2] = out->strides[3];
+      call(vkv_paged_sdpa(&q3, &view, scale, &o3, stream));
+      return;
+    }
+    if (q->strides[3] != 1 || out->strides[3] != 1) throw Error("last dims must be contiguous");
+    AttnArgs a{};
+    a.q = q->data;
+    a.q_sb = q->strides[0];
+    a.q_sh = q->strides[1];
+    a.q_sl = q->strides[2];
+    a.L = static_cast<int32_t>(L);
+    a.Hq = static_cast<int32_t>(Hq);
+    a.Hkv = view.n_kv_heads;
+    a.D = view.head_dim;
+    a.Dv = view.v_head_dim;
+    a.scale = scale;
+    a.kv = kvsrc_from_view(view);
+    a.out = out->data;
+    a.o_sb = out->strides[0];
+    a.o_sh = out->strides[1];
+    a.o_sl = out->strides[2];
+    set_mask(a, mask_mode, mask, B, Hq, L, view.max_len, view.dtype);
+    run_attention(view.dtype, view.bits, view.group_size, true, a, B * L, view.max_len, S(stream));
+  });
+}
+
 int vkv_attention_with_cache_update(const vkv_array* q, const vkv_array* keys, const vkv_array* values,
                                     vkv_cache cache, float scale, int32_t mask_mode,
                                     const vkv_array* mask, const vkv_array* sinks, vkv_array* out,
@@ -535,42 +588,7 @@ int vkv_attention_with_cache_update(const vkv_array* q, const vkv_array* keys, c
       if (sinks) throw Error("quantized attention does not support sinks");
       vkv_paged_view view{};
       call(vkv_cache_update_quantized(cache, keys, values, stream, &view));
-      const int64_t B = q->shape[0], Hq = q->shape[1], L = q->shape[2];
-      if (q->dtype != view.dtype || out->dtype != view.dtype) throw Error("q/out dtype must match the cache");
-      if (q->shape[3] != view.head_dim || out->shape[0] != B || out->shape[1] != Hq ||
-          out->shape[2] != L || out->shape[3] != view.v_head_dim || B != view.n_seqs ||
-          Hq % view.n_kv_heads)
-        throw Error("q/out shapes do not match the cache");
-      if (L == 1 && mask_mode == VKV_MASK_NONE) {
-        // one decode token: the paged decode path over [B, Hq, D] views
-        vkv_array q3 = *q, o3 = *out;
-        q3.ndim = o3.ndim = 3;
-        q3.shape[2] = q->shape[3];
-        q3.strides[2] = q->strides[3];
-        o3.shape[2] = out->shape[3];
-        o3.strides[2] = out->strides[3];
-        call(vkv_paged_sdpa(&q3, &view, scale, &o3, stream));
-        return;
-      }
-      if (q->strides[3] != 1 || out->strides[3] != 1) throw Error("last dims must be contiguous");
-      AttnArgs a{};
-      a.q = q->data;
-      a.q_sb = q->strides[0];
-      a.q_sh = q->strides[1];
-      a.q_sl = q->strides[2];
-      a.L = static_cast<int32_t>(L);
-      a.Hq = static_cast<int32_t>(Hq);
-      a.Hkv = view.n_kv_heads;
-      a.D = view.head_dim;
-      a.Dv = view.v_head_dim;
-      a.scale = scale;
-      a.kv = kvsrc_from_view(view);
-      a.out = out->data;
-      a.o_sb = out->strides[0];
-      a.o_sh = out->strides[1];
-      a.o_sl = out->strides[2];
-      set_mask(a, mask_mode, mask, B, Hq, L, view.max_len, view.dtype);
-      run_attention(view.dtype, view.bits, view.group_size, true, a, B * L, view.max_len, S(stream));
+      call(vkv_quantized_paged_sdpa(q, &view, scale, mask_mode, mask, out, stream));
       return;
     }
     // :106-142: update, then the cache's array mask when none was given

@@ -83,6 +83,7 @@ EXPORTS = (
     "vkv_cache_to_compilable", "vkv_cache_to_compilable_rotating", "vkv_cache_inner_state",
     "vkv_dynamic_slice_update", "vkv_dynamic_slice", "vkv_cache_set_offset",
     "vkv_attention_with_cache_update", "vkv_paged_sdpa_noalloc", "vkv_workspace_release",
+    "vkv_quantized_paged_sdpa",
 )
 TIME_DECODE, TIME_MLA, TIME_FDECODE = 0, 1, 2
 
@@ -276,6 +277,21 @@ def paged_attention(queries, view: PagedView, scale: float, stream=None, out=Non
     fn = lib().vkv_paged_sdpa_noalloc if noalloc else lib().vkv_paged_sdpa
     _chk(fn(C.byref(arr(queries)), C.byref(view), C.c_float(scale), C.byref(a_out),
             stream_ptr(stream)))
+    return out
+
+
+def quantized_paged_attention(queries, view: PagedView, scale: float, mask=None, stream=None,
+                              out=None):
+    """quantizedScaledDotProductAttention (KVCache.swift:1909-1997) over the
+    paged view updateQuantized returned: queries [n_seqs, Hq, L, D], any L."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty(tuple(queries.shape[:3]) + (view.v_head_dim,), dtype=queries.dtype,
+                          device=queries.device)
+    mode, m = _mask_args(mask)
+    a_out = arr(out)
+    _chk(lib().vkv_quantized_paged_sdpa(C.byref(arr(queries)), C.byref(view), C.c_float(scale),
+                                        mode, m, C.byref(a_out), stream_ptr(stream)))
     return out
 
 
