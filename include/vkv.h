@@ -448,6 +448,20 @@ int vkv_prefix_fetch(vkv_prefix mgr, const int64_t *tokens, int64_t n_tokens,
                      const char *media_salt, int32_t *blocks, int32_t capacity,
                      int32_t *n_blocks, int64_t *matched_tokens);
 
+/* Copy-on-write before writing into `block` (the partially filled last block
+ * of a fetched prefix, PagedCacheManager.swift:351-361, or a block forked to
+ * several sequences with vkv_prefix_incref).  *out_block = block when the
+ * caller holds the only reference and no cache entry names it; otherwise a
+ * fresh block (allocated from the LRU head, evicting as allocateBlock does)
+ * receives a device copy of every layer of `block` on `stream`, the
+ * caller's reference moves to it (`block` keeps its cache entry and its
+ * other holders), and *out_block is the fresh block (refcount 1, no cache
+ * entry); -1 when no block is free.  The caller then points its block
+ * table at *out_block.  Replaces the copy of every restored block the
+ * reference makes (Cache/CacheHelpers.swift:431-552): only the block that
+ * is written into is copied. */
+int vkv_prefix_writable(vkv_prefix mgr, int32_t block, void *stream, int32_t *out_block);
+
 /* CacheStats (PagedCacheManager.swift:10-17). */
 typedef struct vkv_prefix_stats {
   int64_t total_blocks, allocated_blocks, free_blocks, cache_hits, cache_misses, evictions;

@@ -456,6 +456,22 @@ class PagedCacheManagerRef:
                 self.stats["allocated_blocks"] -= 1
                 self.stats["free_blocks"] += 1
 
+    def writable(self, bid):
+        """Copy-on-write before writing into block bid (the library's
+        vkv_prefix_writable; no reference counterpart): the block itself
+        when the caller holds the only reference and no cache entry names
+        it, else a freshly allocated block (None if none is free) that
+        takes over the caller's reference."""
+        b = self.blocks[bid]
+        assert b.ref >= 1
+        if b.ref == 1 and b.hash is None:
+            return bid
+        nb = self.allocate_block()
+        if nb is None:
+            return None
+        self.free_block(bid)
+        return nb
+
     def _pin(self, b):
         if b.ref == 0 and b.id in self.queue:
             self.queue.remove(b.id)

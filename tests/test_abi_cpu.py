@@ -207,11 +207,20 @@ def test_prefix_manager_matches_restatement_randomized():
                 assert ra == (None if rb is None else (rb[0], rb[1], rb[2]))
                 if ra:
                     held.extend(ra[2])
-            elif held:
+            elif held and op < 0.9:
                 x = held.pop(rng.randrange(len(held)))
                 a.free_block(x)
                 b.free_block(x)
+            elif held:
+                # copy-on-write of a held block, as before a write into it
+                i = rng.randrange(len(held))
+                wa, wb = a.writable(held[i]), b.writable(held[i])
+                assert wa == wb, (trial, step)
+                if wa is not None:
+                    held[i] = wa
             assert a.stats == b.stats, (trial, step)
+            for x in set(held):
+                assert a.ref_count(x) == b.blocks[x].ref
 
 
 def _desc(shape, dtype, addr=0x1000):
@@ -288,3 +297,31 @@ def test_noalloc_scratch_limit_is_checked_on_the_host():
     out = _desc((1, 8, 128), 2)
     assert L.vkv_paged_sdpa_noalloc(C.byref(q), None, C.c_float(0.1), C.byref(out), None) == 1
     assert b"kv is NULL" in L.vkv_last_error()
+
+
+def test_prefix_writable_copy_on_write_rules():
+    """vkv_prefix_writable: a block held once and uncached is written in
+    place; a forked block (refcount 2) or a cached block (a fetched prefix
+    leaf) moves the caller to a fresh block; an exhausted pool gives None."""
+    m = vkv.PagedCacheManager(4, 6)
+    b = m.allocate_block()
+    assert m.writable(b) == b and m.ref_count(b) == 1
+    m.incref(b)  # forked to a second sequence
+    c = m.writable(b)
+    assert c not in (None, b) and m.ref_count(b) == 1 and m.ref_count(c) == 1
+    # a stored and fetched sequence: its partial leaf is cached
+    m2 = vkv.PagedCacheManager(4, 6)
+    m2.store_token_sequence([1, 2, 3, 4, 5, 6], 2)
+    matched, rest, blocks = m2.fetch_prefix([1, 2, 3, 4, 5, 6, 7])
+    assert matched == 6 and len(blocks) == 2 and m2.ref_count(blocks[1]) == 1
+    leaf = blocks[1]
+    w = m2.writable(leaf)
+    assert w != leaf and m2.ref_count(leaf) == 0 and m2.token_count(leaf) == 2
+    # the cached leaf is still found by a later fetch
+    again = m2.fetch_prefix([1, 2, 3, 4, 5, 6])
+    assert again[0] == 6 and again[2][1] == leaf
+    # exhaust the pool: no copy possible
+    m3 = vkv.PagedCacheManager(4, 3)
+    x, y = m3.allocate_block(), m3.allocate_block()
+    m3.incref(x)
+    assert m3.allocate_block() is None and m3.writable(x) is None and m3.ref_count(x) == 2

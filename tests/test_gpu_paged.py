@@ -306,3 +306,92 @@ def test_append_aligned_groups_ragged_and_scattered_slots():
         rq, rs, rb, _ = O.quantize(np.ascontiguousarray(x.transpose(1, 0, 2)), dtype, 64, bits)
         assert np.array_equal(host(got[0][2, :, :8]), rq)
         assert np.array_equal(host(got[1][2, :, :8]).view(rs.dtype), rs)
+
+
+def test_prefix_copy_on_write_and_lru_eviction_on_device():
+    """The prefix manager wired to a device pool (PagedCacheManager.swift:
+    104-376): a 72-token sequence (two full 32-token blocks and an 8-token
+    partial leaf) is stored (device block copies) and fetched by two
+    sequences; the one that appends copies the shared leaf first
+    (vkv_prefix_writable), so the cached leaf and the other sequence keep
+    their bytes.  Then, with everything released, allocation under a small
+    pool evicts cached blocks leaf first.  Block ids and stats follow the
+    restatement step by step; the device bytes are checked through gathers
+    against the oracle quantizer."""
+    import kvcache_ref as R
+
+    rng = np.random.default_rng(91)
+    dtype, bits, bs, Hkv, D, nblk = O.BF16, 4, 32, 2, 64, 12
+    pool = vkv.PagedPool(nblk, bs, 1, Hkv, D, dtype=dtype, bits=bits)
+    mgr = vkv.PagedCacheManager(bs, nblk, pool=pool)
+    ref = R.PagedCacheManagerRef(bs, nblk)
+    toks = [int(x) for x in rng.integers(0, 1000, 72)]
+    kx = rand_bits(rng, (73, Hkv, D), dtype)  # 72 prompt tokens + 1 generated
+    vx = rand_bits(rng, (73, Hkv, D), dtype)
+
+    def both(fa, fb):
+        a, b = fa(mgr), fb(ref)
+        assert a == b and mgr.stats == ref.stats, (a, b)
+        return a
+
+    def append(blocks, positions, rows):
+        slots = [blocks[p // bs] * bs + p % bs for p in positions]
+        pool.append(0, dev(kx[rows], dtype), dev(vx[rows], dtype),
+                    torch.tensor(slots, dtype=torch.int32, device="cuda"))
+
+    def gather(blocks, n):
+        tab = torch.tensor([blocks], dtype=torch.int32, device="cuda")
+        view = pool.view(0, tab, torch.tensor([n], dtype=torch.int32, device="cuda"), n)
+        (kq, ks, kb), (vq, vs, vb) = vkv.paged_gather_quantized(view)
+        torch.cuda.synchronize()
+        return [host(x[0]) for x in (kq, ks, kb, vq, vs, vb)]
+
+    def expect(rows):
+        out = []
+        for x in (kx, vx):
+            rq, rs, rb, _ = O.quantize(np.ascontiguousarray(x[rows].transpose(1, 0, 2)), dtype, 64, bits)
+            out += [rq, rs.view(np.uint16), rb.view(np.uint16)]
+        return out
+
+    # sequence A computes its prompt into three private blocks, stores it
+    a_blocks = [both(lambda m: m.allocate_block(), lambda r: r.allocate_block()) for _ in range(3)]
+    append(a_blocks, range(72), list(range(72)))
+    mgr.store_token_sequence(toks, 3, src_blocks=a_blocks)
+    ref.store_token_sequence(toks, 3)
+    assert mgr.stats == ref.stats
+    for b in reversed(a_blocks):
+        both(lambda m: m.free_block(b), lambda r: r.free_block(b))
+    # sequences B and C fetch it: the same three cached blocks, the last partial
+    fb = both(lambda m: m.fetch_prefix(toks + [7]), lambda r: r.fetch_prefix(toks + [7]))
+    fc = both(lambda m: m.fetch_prefix(toks), lambda r: r.fetch_prefix(toks))
+    assert fb[0] == fc[0] == 72 and fb[2] == fc[2]
+    cached = fb[2]
+    assert mgr.ref_count(cached[2]) == 2 and mgr.token_count(cached[2]) == 8
+    # B appends its generated token: copy-on-write of the shared leaf
+    leaf_b = both(lambda m: m.writable(cached[2]), lambda r: r.writable(cached[2]))
+    assert leaf_b not in cached and mgr.ref_count(cached[2]) == 1
+    b_blocks = cached[:2] + [leaf_b]
+    append(b_blocks, [72], [72])
+    for got, want in zip(gather(b_blocks, 73), expect(list(range(73)))):
+        assert np.array_equal(got.view(want.dtype), want)
+    for got, want in zip(gather(cached, 72), expect(list(range(72)))):
+        assert np.array_equal(got.view(want.dtype), want)  # the cache entry kept its bytes
+    # a private, uncached block is written in place
+    assert both(lambda m: m.writable(leaf_b), lambda r: r.writable(leaf_b)) == leaf_b
+    # release everything (leaves first), then allocate until the first
+    # cached block is evicted: it is the partial leaf
+    def ref_release(r, blocks):
+        for x in reversed(blocks):
+            r.free_block(x)
+
+    for blocks in (b_blocks, cached):
+        both(lambda m: m.release(blocks), lambda r: ref_release(r, blocks))
+    taken = []
+    while ref.stats["evictions"] == 0:
+        taken.append(both(lambda m: m.allocate_block(), lambda r: r.allocate_block()))
+        assert taken[-1] is not None
+    assert taken[-1] == cached[2]
+    hit = both(lambda m: m.fetch_prefix(toks), lambda r: r.fetch_prefix(toks))
+    assert hit[0] == 64 and hit[2] == cached[:2]
+    for got, want in zip(gather(cached[:2], 64), expect(list(range(64)))):
+        assert np.array_equal(got.view(want.dtype), want)

@@ -1201,6 +1201,14 @@ int vkv_prefix_fetch(vkv_prefix mgr, const int64_t* tokens, int64_t n_tokens, co
   });
 }
 
+int vkv_prefix_writable(vkv_prefix mgr, int32_t block, void* stream, int32_t* out_block) {
+  return guard([&] {
+    need(mgr, "mgr");
+    need(out_block, "out_block");
+    *out_block = mgr->impl->writable(block, S(stream));
+  });
+}
+
 int vkv_prefix_stats_get(vkv_prefix mgr, vkv_prefix_stats* out) {
   return guard([&] {
     need(mgr, "mgr");

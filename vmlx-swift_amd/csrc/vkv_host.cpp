@@ -1397,6 +1397,32 @@ int32_t PrefixManager::block_tokens(int32_t b) {
   return blocks_[b].has_hash ? static_cast<int32_t>(blocks_[b].tokens.size()) : -1;
 }
 
+// Copy-on-write of a block about to be written (the partially filled last
+// block of a fetched prefix, or any block another sequence also holds): a
+// block the caller alone references and no cache entry names is returned as
+// it is; otherwise a fresh block (from the LRU head, which may evict) gets
+// a device copy of every layer of b on `st`, the caller's reference moves
+// from b to it (b keeps its cache entry and its other holders), and the
+// fresh block is returned, unregistered with refcount 1.  -1 when no block
+// is free.  Replaces the copy the reference makes of every restored block
+// (CacheHelpers.swift:431-552): here only the block written into is copied.
+int32_t PrefixManager::writable(int32_t b, hipStream_t st) {
+  std::lock_guard<std::mutex> g(mu_);
+  check_block(b, max_blocks_);
+  Block& x = blocks_[b];
+  if (x.ref < 1) throw Error("copy-on-write needs a block the caller references");
+  if (x.ref == 1 && !x.has_hash) return b;
+  const int32_t nb = alloc_locked();  // b is referenced, so never on the free queue
+  if (nb < 0) return -1;
+  if (pool_) {
+    const int32_t src = b, dst = nb;
+    launch_copy_blocks(pool_->mem.bytes(), pool_->layer_bytes, pool_->p.n_layers,
+                       pool_->block_bytes, &src, &dst, 1, st);
+  }
+  free_locked(b);
+  return nb;
+}
+
 // findCachedBlock (PagedCacheManager.swift:164-180)
 int32_t PrefixManager::find(const std::string& hash) {
   std::lock_guard<std::mutex> g(mu_);

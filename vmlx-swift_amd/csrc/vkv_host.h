@@ -314,6 +314,8 @@ class PrefixManager {
              int32_t* n_blocks, int64_t* matched);
   vkv_prefix_stats stats();
   int32_t block_tokens(int32_t b);
+  // Copy-on-write before a caller writes into block b (see vkv_prefix_writable).
+  int32_t writable(int32_t b, hipStream_t st);
   static std::string block_hash(const std::string* parent, const int64_t* tokens, int64_t n,
                                 const std::string* model_key, const std::string* salt);
 

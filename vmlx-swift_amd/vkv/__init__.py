@@ -83,7 +83,7 @@ EXPORTS = (
     "vkv_cache_to_compilable", "vkv_cache_to_compilable_rotating", "vkv_cache_inner_state",
     "vkv_dynamic_slice_update", "vkv_dynamic_slice", "vkv_cache_set_offset",
     "vkv_attention_with_cache_update", "vkv_paged_sdpa_noalloc", "vkv_workspace_release",
-    "vkv_quantized_paged_sdpa",
+    "vkv_quantized_paged_sdpa", "vkv_prefix_writable",
 )
 TIME_DECODE, TIME_MLA, TIME_FDECODE = 0, 1, 2
 
@@ -726,6 +726,15 @@ class PagedCacheManager:
         if nb.value == 0:
             return None
         return matched.value, list(tokens[matched.value:]), [blocks[i] for i in range(nb.value)]
+
+    def writable(self, block: int, stream=None) -> Optional[int]:
+        """Copy-on-write before writing into `block` (vkv_prefix_writable):
+        the block to write into, or None when the pool has no free block."""
+        b = C.c_int32()
+        _chk(lib().vkv_prefix_writable(self._h, block,
+                                       stream_ptr(stream) if self._pool is not None else None,
+                                       C.byref(b)))
+        return None if b.value < 0 else b.value
 
     @property
     def stats(self) -> dict:
