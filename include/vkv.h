@@ -282,6 +282,10 @@ int vkv_cache_update_quantized(vkv_cache cache, const vkv_array *keys,
                                const vkv_array *values, void *stream,
                                vkv_paged_view *out);
 
+/* The cache's class (VKV_CACHE_*): the dynamic type the reference's
+ * savePromptCache switches on (KVCache.swift:1627-1646). */
+int vkv_cache_kind(vkv_cache cache, int32_t *kind);
+
 /* offset / maxSize / isTrimmable / trim(n) (KVCache.swift:38-77). */
 int vkv_cache_offset(vkv_cache cache, int64_t *offset);
 /* offset setter (BaseKVCache.offset, KVCache.swift:256-262; the device
@@ -475,6 +479,66 @@ int vkv_prefix_block_tokens(vkv_prefix mgr, int32_t block, int32_t *n_tokens);
  * raw little-endian Int64 bytes; 64 lowercase hex chars + NUL into out[65]. */
 int vkv_block_hash(const char *parent_hash, const int64_t *tokens, int64_t n_tokens,
                    const char *model_key, const char *media_salt, char *out);
+
+/* ------------------------------------------------------ on-disk formats */
+
+/* savePromptCache(url:cache:metadata:) (MLXLMCommon/KVCache.swift:1620-1680):
+ * a safetensors file with each cache's state arrays as "i.j", its metaState
+ * strings as metadata "0.i.j", the user metadata as "1.<key>" and the class
+ * names ("KVCache", "RotatingKVCache", "QuantizedKVCache") as "2.i", the
+ * Python mlx-lm layout.  The states are copied to the host on `stream`. */
+int vkv_prompt_cache_save(const char *path, const vkv_cache *caches, int32_t n_caches,
+                          const char *const *meta_keys, const char *const *meta_values,
+                          int32_t n_meta, void *stream);
+/* loadPromptCache(url:) (:1687-1780): new cache handles into caches[0..n),
+ * *n_caches = n (with caches == NULL only counts); user metadata as
+ * NUL-separated key, value pairs in meta_buf (*n_meta pairs; NULL buf only
+ * counts).  Errors as the reference throws them ("Unknown cache class",
+ * "Mismatch in cache counts", RotatingKVCache maxSize None); the whole file
+ * is validated before any cache is built.  Quantized layers keep the group
+ * size and bits their metaState records (the reference rebuilds them as
+ * QuantizedKVCache() and sets only the offset). */
+int vkv_prompt_cache_load(const char *path, void *stream, vkv_cache *caches, int32_t capacity,
+                          int32_t *n_caches, char *meta_buf, int64_t meta_buf_len,
+                          int32_t *n_meta);
+/* The same file written from one sequence's pool blocks (host block ids,
+ * tokens 0 .. n_tokens-1 at blocks[t / block_size]): per pool layer, an
+ * affine pool gives the QuantizedKVCache arrays (the stored codes, no
+ * requantization), a float pool KVCacheSimple's keys and values. */
+int vkv_prompt_cache_save_paged(const char *path, vkv_pool pool, const int32_t *blocks,
+                                int32_t n_blocks, int64_t n_tokens,
+                                const char *const *meta_keys, const char *const *meta_values,
+                                int32_t n_meta, void *stream);
+/* ... and read back into one sequence's pool blocks (restoreLayerData,
+ * Cache/CacheHelpers.swift:431-552, without the concatenated copy): float
+ * layers are appended (quantized for an affine pool), quantized layers with
+ * the pool's group size and bits are written as they are, others are
+ * dequantized and appended.  *n_tokens receives the token count. */
+int vkv_prompt_cache_load_paged(const char *path, vkv_pool pool, const int32_t *blocks,
+                                int32_t n_blocks, int64_t *n_tokens, char *meta_buf,
+                                int64_t meta_buf_len, int32_t *n_meta, void *stream);
+
+/* DiskCache.hashTokens (Cache/DiskCache.swift:659-682): the first 32 hex
+ * digits of SHA-256(model key, "|media:" + salt, tokens as little-endian
+ * Int64), the disk tier's file name; 32 chars + NUL into out[33]. */
+int vkv_disk_hash_tokens(const int64_t *tokens, int64_t n_tokens, const char *model_key,
+                         const char *media_salt, char *out);
+/* TQDiskSerializer.serialize, format version 2 (Cache/TQDiskSerializer.swift:
+ * 240-330): __jang_cache_format_version__ = [2], __layer_kind_i__ per layer
+ * (2 kv: kv_i_keys/values; 6 rotating: rot_i_keys/values + __rot_i_meta__
+ * [keep, maxSize, step, offset, idx]; 5 quantized: qkv_i_k +
+ * __qkv_i_count__/_offset__/_group_size__/_bits__; 4 skip for an empty
+ * cache), scalars as 1-element int32 arrays, file metadata {"format": "mlx"}
+ * (DiskCache.swift:315). */
+int vkv_disk_cache_save(const char *path, const vkv_cache *caches, int32_t n_caches,
+                        void *stream);
+/* deserializeV2 (:1023-1170) for those kinds: caches[i] = layer i's new
+ * cache, NULL for a skipped layer; *n_layers = the layer count (caches ==
+ * NULL only counts).  A gap in the kind tags, an incomplete payload or a
+ * kind this library does not hold (TurboQuant, Mamba, composite) fails the
+ * whole record, the reference's required miss. */
+int vkv_disk_cache_load(const char *path, void *stream, vkv_cache *caches, int32_t capacity,
+                        int32_t *n_layers);
 
 /* Strided copy between two arrays of the same shape and element size
  * (materializes a view returned by a cache into caller memory).  Replaces

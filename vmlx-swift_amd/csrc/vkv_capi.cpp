@@ -166,6 +166,10 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
 
 }  // namespace
 
+namespace vkv {
+int guarded_call(const std::function<void()>& f) { return guard(f); }
+}  // namespace vkv
+
 extern "C" {
 
 const char* vkv_last_error(void) { return g_error.c_str(); }
@@ -714,6 +718,14 @@ int vkv_cache_update_quantized(vkv_cache cache, const vkv_array* keys, const vkv
     need(values, "values");
     need(out, "out");
     cache->impl->update_quantized(*keys, *values, S(stream), out);
+  });
+}
+
+int vkv_cache_kind(vkv_cache cache, int32_t* kind) {
+  return guard([&] {
+    need(cache, "cache");
+    need(kind, "kind");
+    *kind = cache->impl->kind();
   });
 }
 

@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <functional>
 #include <list>
 #include <map>
 #include <memory>
@@ -355,6 +356,10 @@ class PrefixManager {
 // bytes released.  Growth during graph capture on `st` is an error.
 float* attention_workspace(hipStream_t st, size_t floats);
 size_t workspace_release(hipStream_t st);
+
+// Runs f under the C ABI's error convention (vkv_capi.cpp): returns 0, or 1
+// with the exception's message kept for vkv_last_error().
+int guarded_call(const std::function<void()>& f);
 
 }  // namespace vkv
 

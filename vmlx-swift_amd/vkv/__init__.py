@@ -83,7 +83,9 @@ EXPORTS = (
     "vkv_cache_to_compilable", "vkv_cache_to_compilable_rotating", "vkv_cache_inner_state",
     "vkv_dynamic_slice_update", "vkv_dynamic_slice", "vkv_cache_set_offset",
     "vkv_attention_with_cache_update", "vkv_paged_sdpa_noalloc", "vkv_workspace_release",
-    "vkv_quantized_paged_sdpa", "vkv_prefix_writable",
+    "vkv_quantized_paged_sdpa", "vkv_prefix_writable", "vkv_prompt_cache_save",
+    "vkv_prompt_cache_load", "vkv_prompt_cache_save_paged", "vkv_prompt_cache_load_paged",
+    "vkv_disk_hash_tokens", "vkv_disk_cache_save", "vkv_disk_cache_load", "vkv_cache_kind",
 )
 TIME_DECODE, TIME_MLA, TIME_FDECODE = 0, 1, 2
 
@@ -741,3 +743,109 @@ class PagedCacheManager:
         s = PrefixStats()
         _chk(lib().vkv_prefix_stats_get(self._h, C.byref(s)))
         return {f: getattr(s, f) for f, _ in PrefixStats._fields_}
+
+
+# ----------------------------------------------------------- on-disk formats
+def _wrap_handle(h):
+    """A library cache handle as the Python class of its kind."""
+    k = C.c_int32()
+    _chk(lib().vkv_cache_kind(h, C.byref(k)))
+    cls = {CACHE_SIMPLE: KVCacheSimple, CACHE_ROTATING: RotatingKVCache,
+           CACHE_QUANTIZED: QuantizedKVCache}.get(k.value, _Cache)
+    obj = object.__new__(cls)
+    _Cache.__init__(obj, None, handle=h)
+    return obj
+
+
+def _meta_args(metadata):
+    items = list((metadata or {}).items())
+    keys = (C.c_char_p * max(1, len(items)))(*[k.encode() for k, _ in items])
+    vals = (C.c_char_p * max(1, len(items)))(*[v.encode() for _, v in items])
+    return keys, vals, len(items)
+
+
+def _meta_out(call):
+    """Runs call(buf, len, n_ptr) twice (count, then fill) -> dict."""
+    n = C.c_int32()
+    call(None, C.c_int64(0), C.byref(n))
+    buf = C.create_string_buffer(1 << 16)
+    while True:
+        try:
+            call(buf, C.c_int64(len(buf)), C.byref(n))
+            break
+        except VKVError as e:
+            if "too small" not in str(e):
+                raise
+            buf = C.create_string_buffer(2 * len(buf))
+    parts = buf.raw.split(b"\0")[: 2 * n.value]
+    return {parts[i].decode(): parts[i + 1].decode() for i in range(0, len(parts), 2)}
+
+
+def save_prompt_cache(path: str, caches, metadata=None, stream=None):
+    """savePromptCache(url:cache:metadata:) (KVCache.swift:1620-1680)."""
+    hs = (C.c_void_p * max(1, len(caches)))(*[c._h.value for c in caches])
+    keys, vals, n = _meta_args(metadata)
+    _chk(lib().vkv_prompt_cache_save(path.encode(), hs, len(caches), keys, vals, n,
+                                     stream_ptr(stream)))
+
+
+def load_prompt_cache(path: str, stream=None):
+    """loadPromptCache(url:) (KVCache.swift:1687-1780) -> (caches, metadata)."""
+    n = C.c_int32()
+    sp = stream_ptr(stream)
+    _chk(lib().vkv_prompt_cache_load(path.encode(), sp, None, 0, C.byref(n), None, C.c_int64(0),
+                                     None))
+    count = C.c_int32()
+    meta = _meta_out(lambda buf, ln, nm: _chk(lib().vkv_prompt_cache_load(
+        path.encode(), sp, None, 0, C.byref(count), buf, ln, nm)))
+    hs = (C.c_void_p * max(1, n.value))()
+    _chk(lib().vkv_prompt_cache_load(path.encode(), sp, hs, n.value, C.byref(n), None,
+                                     C.c_int64(0), None))
+    return [_wrap_handle(C.c_void_p(hs[i])) for i in range(n.value)], meta
+
+
+def save_prompt_cache_paged(path: str, pool, blocks, n_tokens: int, metadata=None, stream=None):
+    """savePromptCache's file from one sequence's pool blocks (host ids)."""
+    b = (C.c_int32 * max(1, len(blocks)))(*blocks)
+    keys, vals, n = _meta_args(metadata)
+    _chk(lib().vkv_prompt_cache_save_paged(path.encode(), pool._h, b, len(blocks),
+                                           C.c_int64(n_tokens), keys, vals, n,
+                                           stream_ptr(stream)))
+
+
+def load_prompt_cache_paged(path: str, pool, blocks, stream=None):
+    """A prompt-cache file into one sequence's pool blocks -> (n_tokens, metadata)."""
+    b = (C.c_int32 * max(1, len(blocks)))(*blocks)
+    nt = C.c_int64()
+
+    def call(buf, ln, nm):
+        _chk(lib().vkv_prompt_cache_load_paged(path.encode(), pool._h, b, len(blocks),
+                                               C.byref(nt), buf, ln, nm, stream_ptr(stream)))
+
+    meta = _meta_out(call)
+    return nt.value, meta
+
+
+def disk_hash_tokens(tokens, model_key=None, media_salt=None) -> str:
+    """DiskCache.hashTokens (Cache/DiskCache.swift:659-682)."""
+    t = (C.c_int64 * max(1, len(tokens)))(*tokens)
+    out = C.create_string_buffer(33)
+    _chk(lib().vkv_disk_hash_tokens(t, len(tokens),
+                                    model_key.encode() if model_key is not None else None,
+                                    media_salt.encode() if media_salt is not None else None, out))
+    return out.value.decode()
+
+
+def disk_cache_save(path: str, caches, stream=None):
+    """TQDiskSerializer.serialize, format version 2."""
+    hs = (C.c_void_p * max(1, len(caches)))(*[c._h.value for c in caches])
+    _chk(lib().vkv_disk_cache_save(path.encode(), hs, len(caches), stream_ptr(stream)))
+
+
+def disk_cache_load(path: str, stream=None):
+    """TQDiskSerializer.deserializeV2 -> caches (None for a skipped layer)."""
+    n = C.c_int32()
+    _chk(lib().vkv_disk_cache_load(path.encode(), stream_ptr(stream), None, 0, C.byref(n)))
+    hs = (C.c_void_p * max(1, n.value))()
+    _chk(lib().vkv_disk_cache_load(path.encode(), stream_ptr(stream), hs, n.value, C.byref(n)))
+    return [None if not hs[i] else _wrap_handle(C.c_void_p(hs[i])) for i in range(n.value)]
