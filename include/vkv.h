@@ -320,6 +320,22 @@ int vkv_cache_set_meta_state(vkv_cache cache, const char *const *strings, int32_
 int vkv_cache_make_mask(vkv_cache cache, int32_t n, int32_t window, int32_t return_array,
                         void *stream, int32_t *mode, vkv_array *mask);
 
+/* createBatchCausalMask(queryLen:offsets:effectiveKeyLens:windowSize:)
+ * (BatchEngine/BatchMask.swift:44-115): the bool mask [batch, 1, n,
+ * max_total] of a batched step in which slot b held offsets[b] tokens
+ * before the step.  key_lens (NULL: offsets[b] + n) are the keys each
+ * slot's update returns; a slot whose key length is below offsets[b] + n
+ * has wrapped its ring and sees every key below its length.  window < 0
+ * means no window (windowSize nil); window >= 0 also requires key j >=
+ * query position - (window - 1).  *max_total receives the last dimension
+ * (the largest key length).  With out == NULL nothing is launched (a size
+ * query); otherwise out is a caller-owned, 16-byte aligned device buffer
+ * of out_bytes >= batch * n * max_total.  The per-slot values are read on
+ * the host and travel as kernel arguments (no allocation, no copy). */
+int vkv_batch_causal_mask(int32_t n, const int32_t *offsets, const int32_t *key_lens,
+                          int32_t batch, int32_t window, void *out, int64_t out_bytes,
+                          void *stream, int32_t *max_total);
+
 /* KVCacheSimple.toQuantized (KVCache.swift:561-581) and
  * QuantizedKVCache.toUnquantized (:1199-1220); new handles. */
 int vkv_cache_to_quantized(vkv_cache simple, int32_t group_size, int32_t bits,

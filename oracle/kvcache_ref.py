@@ -335,6 +335,30 @@ def causal_mask(n, offset, window=None):
     return m
 
 
+def batch_causal_mask(n, offsets, key_lens=None, window=None):
+    """createBatchCausalMask (BatchEngine/BatchMask.swift:44-115): bool
+    [B, 1, n, maxTotal]; a slot whose key length is below offset + n has
+    wrapped and sees every key below its length (:80-94), otherwise the
+    causal (+ window) test on positions offset + i, cut at the key length
+    (:95-111)."""
+    assert len(offsets) > 0
+    kls = list(key_lens) if key_lens is not None else [o + n for o in offsets]
+    total = max(kls)
+    r = np.arange(total)[None]
+    out = np.zeros((len(offsets), 1, n, total), bool)
+    for b, (off, kl) in enumerate(zip(offsets, kls)):
+        if kl < off + n:
+            m = np.broadcast_to(r < kl, (n, total))
+        else:
+            l = (np.arange(n) + off)[:, None]
+            m = l >= r
+            if window is not None:
+                m = m & (r >= l - (window - 1))
+            m = m & (r < kl)
+        out[b, 0] = m
+    return out
+
+
 def base_make_mask(offset, n, window=None, return_array=False):
     """BaseKVCache.makeMask (KVCache.swift:287-311)."""
     if n == 1:

@@ -834,6 +834,32 @@ int vkv_cache_make_mask(vkv_cache cache, int32_t n, int32_t window, int32_t retu
   });
 }
 
+int vkv_batch_causal_mask(int32_t n, const int32_t* offsets, const int32_t* key_lens, int32_t batch,
+                          int32_t window, void* out, int64_t out_bytes, void* stream,
+                          int32_t* max_total) {
+  return guard([&] {
+    if (batch <= 0) throw Error("createBatchCausalMask requires at least one sequence");
+    if (n < 0) throw Error("queryLen must be >= 0");
+    need(offsets, "offsets");
+    need(max_total, "max_total");
+    std::vector<int32_t> kl(batch);
+    int64_t mx = 0;
+    for (int b = 0; b < batch; ++b) {
+      if (offsets[b] < 0) throw Error("offsets must be >= 0");
+      const int64_t len = key_lens ? key_lens[b] : static_cast<int64_t>(offsets[b]) + n;
+      if (len < 0 || len > INT32_MAX) throw Error("key lengths must be in [0, 2^31)");
+      kl[b] = static_cast<int32_t>(len);
+      mx = std::max(mx, len);
+    }
+    *max_total = static_cast<int32_t>(mx);
+    if (!out) return;
+    const int64_t bytes = static_cast<int64_t>(batch) * n * mx;
+    if (out_bytes < bytes) throw Error("the mask buffer holds fewer than batch * n * max_total bytes");
+    launch_batch_mask(n, static_cast<int>(mx), window, offsets, kl.data(), batch,
+                      static_cast<uint8_t*>(out), S(stream));
+  });
+}
+
 int vkv_cache_to_quantized(vkv_cache simple, int32_t group_size, int32_t bits, void* stream,
                            vkv_cache* out) {
   return guard([&] {

@@ -10,7 +10,10 @@
 //     157-207);
 //   * the full-buffer attention mask computed from the device offset
 //     (CompilableKVCache.swift:167-193, CompilableRotatingKVCache.swift:
-//     233-260).
+//     233-260);
+//   * the host-offset masks: createCausalMask, the rotating cache's rolled
+//     row and the batch mask of createBatchCausalMask
+//     (BatchEngine/BatchMask.swift:44-115).
 //
 // No host read of the offset is needed between steps, so a decode step
 // built from these launches can be captured once in a HIP graph and
@@ -139,6 +142,58 @@ __global__ void __launch_bounds__(256) roll_mask_kernel(int64_t size, int64_t wi
   }
 }
 
+// createBatchCausalMask (BatchEngine/BatchMask.swift:44-115) for up to
+// kBatchMaskSlots slots per launch: mask [B, 1, n, cols] as bytes, slot b
+// row i column j.  A slot whose key length is below offset + n has wrapped
+// its ring: every key below the key length is visible.  Otherwise key j is
+// visible to the query at l = offset + i when j <= l, j < keyLen and, with
+// a window (window >= 0), j >= l - (window - 1).  Each thread writes 16
+// consecutive bytes of the launch's range [slot0 * n * cols, slot1 * n *
+// cols) with one vector store when they are aligned and in range.
+struct BatchMaskArgs {
+  int32_t n, cols, window, slot0, slots;
+  int32_t offset[kBatchMaskSlots];
+  int32_t key_len[kBatchMaskSlots];
+};
+
+__global__ void __launch_bounds__(256) batch_mask_kernel(BatchMaskArgs a, uint8_t* mask) {
+  const int64_t row = static_cast<int64_t>(a.n) * a.cols;
+  const int64_t lo = a.slot0 * row, hi = (a.slot0 + static_cast<int64_t>(a.slots)) * row;
+  const int64_t first = lo & ~static_cast<int64_t>(15);
+  for (int64_t c = first + (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 16;
+       c < hi; c += static_cast<int64_t>(gridDim.x) * blockDim.x * 16) {
+    uint32_t w[4] = {0, 0, 0, 0};
+    const int64_t e0 = c < lo ? lo : c;
+    int64_t b = e0 / row, r = e0 - b * row;
+    int64_t i = r / a.cols, j = r - i * a.cols;
+    for (int t = static_cast<int>(e0 - c); t < 16 && c + t < hi; ++t) {
+      const int64_t off = a.offset[b - a.slot0], kl = a.key_len[b - a.slot0];
+      bool m;
+      if (kl < off + a.n) {
+        m = j < kl;
+      } else {
+        const int64_t l = off + i;
+        m = l >= j && j < kl;
+        if (a.window >= 0) m = m && j >= l - (a.window - 1);
+      }
+      w[t >> 2] |= static_cast<uint32_t>(m) << (8 * (t & 3));
+      if (++j == a.cols) {
+        j = 0;
+        if (++i == a.n) {
+          i = 0;
+          ++b;
+        }
+      }
+    }
+    if (c >= lo && c + 16 <= hi) {
+      *reinterpret_cast<uint4*>(mask + c) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+      for (int t = 0; t < 16; ++t)
+        if (c + t >= lo && c + t < hi) mask[c + t] = static_cast<uint8_t>(w[t >> 2] >> (8 * (t & 3)));
+    }
+  }
+}
+
 int blocks_for(int64_t n) {
   return static_cast<int>(std::min<int64_t>((n + 255) / 256, 4096));
 }
@@ -194,6 +249,28 @@ void launch_roll_mask(int64_t size, int64_t window, int64_t shift, uint8_t* mask
   hipLaunchKernelGGL(roll_mask_kernel, dim3(blocks_for(size)), dim3(256), 0, st, size, window,
                      shift, mask);
   VKV_HIP(hipGetLastError());
+}
+
+void launch_batch_mask(int n, int cols, int window, const int32_t* offsets, const int32_t* key_lens,
+                       int batch, uint8_t* mask, hipStream_t st) {
+  VKV_CHECK(reinterpret_cast<uintptr_t>(mask) % 16 == 0, "the batch mask must be 16-byte aligned");
+  for (int s0 = 0; s0 < batch; s0 += kBatchMaskSlots) {
+    BatchMaskArgs a{};
+    a.n = n;
+    a.cols = cols;
+    a.window = window;
+    a.slot0 = s0;
+    a.slots = std::min(kBatchMaskSlots, batch - s0);
+    for (int b = 0; b < a.slots; ++b) {
+      a.offset[b] = offsets[s0 + b];
+      a.key_len[b] = key_lens[s0 + b];
+    }
+    const int64_t bytes = static_cast<int64_t>(a.slots) * n * cols;
+    if (bytes <= 0) continue;
+    hipLaunchKernelGGL(batch_mask_kernel, dim3(blocks_for((bytes + 31) / 16)), dim3(256), 0, st, a,
+                       mask);
+    VKV_HIP(hipGetLastError());
+  }
 }
 
 }  // namespace vkv

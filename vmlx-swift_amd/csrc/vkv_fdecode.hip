@@ -61,17 +61,6 @@ __device__ __forceinline__ void unpack16(const u32x4_t& w, float* out) {
   }
 }
 
-// Maximum / sum over the 64 lanes (every lane gets the result).
-__device__ __forceinline__ float wave_maxf(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
-}
-__device__ __forceinline__ float wave_sumf(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  return x;
-}
 // Maximum / sum within each half-wave of 32 lanes.
 __device__ __forceinline__ float half_maxf(float x) {
 #pragma unroll

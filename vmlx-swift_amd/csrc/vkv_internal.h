@@ -247,6 +247,11 @@ void launch_offset_mask(const int32_t* ctr, int n, int cols, int window, int rin
 void launch_causal_mask(int n, int64_t off, int window, uint8_t* mask, hipStream_t st);
 // [size] bool: roll(arange(size) >= size - window, shift).
 void launch_roll_mask(int64_t size, int64_t window, int64_t shift, uint8_t* mask, hipStream_t st);
+// createBatchCausalMask: [batch, 1, n, cols] bytes from host per-slot
+// offsets and key lengths; window < 0 means none.
+constexpr int kBatchMaskSlots = 240;
+void launch_batch_mask(int n, int cols, int window, const int32_t* offsets, const int32_t* key_lens,
+                       int batch, uint8_t* mask, hipStream_t st);
 
 // Kernel timing (a measurement aid): while enabled, launchers start their
 // main kernel with hipExtLaunchKernelGGL and a start/stop event pair, which

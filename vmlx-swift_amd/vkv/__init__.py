@@ -86,6 +86,7 @@ EXPORTS = (
     "vkv_quantized_paged_sdpa", "vkv_prefix_writable", "vkv_prompt_cache_save",
     "vkv_prompt_cache_load", "vkv_prompt_cache_save_paged", "vkv_prompt_cache_load_paged",
     "vkv_disk_hash_tokens", "vkv_disk_cache_save", "vkv_disk_cache_load", "vkv_cache_kind",
+    "vkv_batch_causal_mask",
 )
 TIME_DECODE, TIME_MLA, TIME_FDECODE = 0, 1, 2
 
@@ -164,6 +165,29 @@ def to_torch(a: Array, stream=None):
 
 
 # ------------------------------------------------------------------- ops
+def batch_causal_mask(n: int, offsets, effective_key_lens=None, window_size=None, stream=None):
+    """createBatchCausalMask(queryLen:offsets:effectiveKeyLens:windowSize:)
+    (BatchEngine/BatchMask.swift:44-115): a bool tensor [B, 1, n, maxTotal]."""
+    torch = _torch()
+    B = len(offsets)
+    offs = (C.c_int32 * max(1, B))(*offsets)
+    kls = None
+    if effective_key_lens is not None:
+        if len(effective_key_lens) != B:
+            raise VKVError(f"effectiveKeyLens.count {len(effective_key_lens)} must equal "
+                           f"offsets.count {B}")
+        kls = (C.c_int32 * max(1, B))(*effective_key_lens)
+    win = -1 if window_size is None else int(window_size)
+    mt = C.c_int32()
+    _chk(lib().vkv_batch_causal_mask(n, offs, kls, B, win, None, C.c_int64(0), None, C.byref(mt)))
+    out = torch.empty((B, 1, n, mt.value), dtype=torch.bool, device="cuda")
+    if out.numel():
+        _chk(lib().vkv_batch_causal_mask(n, offs, kls, B, win, C.c_void_p(out.data_ptr()),
+                                         C.c_int64(out.numel()), stream_ptr(stream),
+                                         C.byref(mt)))
+    return out
+
+
 def quantized(w, group_size: int = 64, bits: int = 4, stream=None):
     """mlx `quantized(_:groupSize:bits:)` (Source/MLX/Ops.swift:2368-2391),
     affine mode: returns (wq int32-as-u32, scales, biases)."""
