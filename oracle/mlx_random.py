@@ -93,14 +93,20 @@ class KeySequence:
         return sub
 
 
-def uniform(seq: KeySequence, shape, low: float = 0.0, high: float = 1.0) -> np.ndarray:
+def uniform_from_key(key_: tuple[int, int], shape, low: float = 0.0,
+                     high: float = 1.0) -> np.ndarray:
+    """`uniform` drawing from an explicit key (MLXRandom.uniform(key:))."""
     n = int(np.prod(shape)) if len(shape) else 1
-    w = bits(seq.next(), n)
+    w = bits(key_, n)
     lo = np.float32(low)
     rng = np.float32(np.float32(high) - lo)
     u = w.astype(np.float32) / np.float32(4294967296.0)
     u = np.minimum(u, np.nextafter(np.float32(1.0), np.float32(0.0)))
     return (rng * u + lo).astype(np.float32).reshape(shape)
+
+
+def uniform(seq: KeySequence, shape, low: float = 0.0, high: float = 1.0) -> np.ndarray:
+    return uniform_from_key(seq.next(), shape, low, high)
 
 
 def normal(seq: KeySequence, shape) -> np.ndarray:
@@ -111,3 +117,10 @@ def normal(seq: KeySequence, shape) -> np.ndarray:
     return (np.float32(np.sqrt(2.0)) * erfinv(u.astype(np.float64)).astype(np.float32)).astype(
         np.float32
     )
+
+
+def normal_uniforms(key_: tuple[int, int], shape) -> np.ndarray:
+    """The uniform(-1 + ulp, 1) draws MLXRandom.normal(key:) maps through
+    sqrt(2) * erfinv."""
+    lo = float(np.nextafter(np.float32(-1.0), np.float32(0.0)))
+    return uniform_from_key(key_, shape, lo, 1.0)

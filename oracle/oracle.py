@@ -71,6 +71,16 @@ def _declare(L):
     L.vkvo_quantized_decode_batch.argtypes = (
         [vp, i32] + [vp] * 6 + [i32, vp, vp, i32, i32, i32, i32, i32, f32, i32, i32, vp]
     )
+    L.tqo_codebook.argtypes = [i32, i32, i32, vp]
+    L.tqo_random_signs.argtypes = [i32, C.c_long, vp]
+    L.tqo_erfinv.restype = f32
+    L.tqo_erfinv.argtypes = [f32]
+    L.tqo_normal_from_uniform.argtypes = [vp, i64, vp]
+    L.tqo_hadamard.argtypes = [vp, i64, i32, vp, i32]
+    L.tqo_pow2_blocks.restype = i32
+    L.tqo_pow2_blocks.argtypes = [i32, vp]
+    L.tqo_encode.argtypes = [vp, i32, i64, i32, vp, vp, i32] + [vp] * 7
+    L.tqo_decode.argtypes = [vp, vp, vp, vp, i64, i32, vp, vp, vp, vp]
 
 
 def np_dtype(code):
@@ -214,3 +224,164 @@ def quantized_decode_batch(q, q_dtype, kq, ks, kb, vq, vs, vb, lens, tok_off, Hk
         _p(np.ascontiguousarray(tok_off, dtype=np.int64)), Hq, Hkv, D, group, bits, scale,
         rounding, threads, _p(out))
     return out
+
+
+# ---------------------------------------------------------------- TurboQuant
+# TurboQuant KV codec (Libraries/MLXLMCommon/TurboQuant/): tq_oracle.c plus
+# the bit packing of TQBitPack.swift and the encoded-record layout of
+# TQEncodedData.swift.
+def tq_codebook(dim: int, bits: int, iterations: int = 200) -> np.ndarray:
+    """TQCodebook.computeCodebook (TQCodebook.swift:103-160)."""
+    out = np.empty(1 << bits, np.float32)
+    lib().tqo_codebook(dim, bits, iterations, _p(out))
+    return out
+
+
+def tq_random_signs(dim: int, seed: int) -> np.ndarray:
+    """TQHadamard.generateRandomSigns (TQHadamard.swift:52-62)."""
+    out = np.empty(dim, np.float32)
+    lib().tqo_random_signs(dim, C.c_long(seed), _p(out))
+    return out
+
+
+def tq_erfinv(a) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty_like(a)
+    f = lib().tqo_erfinv
+    flat_in, flat_out = a.reshape(-1), out.reshape(-1)
+    for i in range(flat_in.size):
+        flat_out[i] = f(float(flat_in[i]))
+    return out
+
+
+def tq_qjl_matrix(dim: int, seed: int) -> np.ndarray:
+    """TQQJL.generateProjection (TQQJL.swift:55-58): MLXRandom.normal([dim,
+    dim], key(seed)) -- MLX's uniform draws mapped through its f32 erfinv."""
+    import mlx_random as mr
+
+    u = mr.normal_uniforms(mr.key(seed), (dim, dim))
+    out = np.empty_like(u)
+    lib().tqo_normal_from_uniform(_p(u), u.size, _p(out))
+    return out
+
+
+def tq_hadamard(x, signs, inverse=False) -> np.ndarray:
+    """hadamardRotate / hadamardInverse (TQHadamard.swift:117-153) on rows."""
+    y = np.array(x, dtype=np.float32, order="C", copy=True)
+    dim = y.shape[-1]
+    lib().tqo_hadamard(_p(y), y.size // dim, dim, _p(np.ascontiguousarray(signs, np.float32)),
+                       int(inverse))
+    return y
+
+
+def tq_pack_bits(values, bits: int) -> np.ndarray:
+    """TQBitPack.packBits (TQBitPack.swift:47-65): flat, 32 // bits values
+    per u32 little-end first, zero-padded."""
+    vpw = 32 // bits
+    flat = np.asarray(values, np.uint32).reshape(-1)
+    pad = (vpw - flat.size % vpw) % vpw
+    flat = np.concatenate([flat, np.zeros(pad, np.uint32)]).reshape(-1, vpw)
+    out = np.zeros(flat.shape[0], np.uint32)
+    for i in range(vpw):
+        out |= flat[:, i] << np.uint32(i * bits)
+    return out
+
+
+def tq_unpack_bits(packed, bits: int, n: int) -> np.ndarray:
+    """TQBitPack.unpackBits (TQBitPack.swift:77-88)."""
+    vpw = 32 // bits
+    p = np.asarray(packed, np.uint32)
+    cols = [(p >> np.uint32(i * bits)) & np.uint32((1 << bits) - 1) for i in range(vpw)]
+    return np.stack(cols, -1).reshape(-1)[:n].astype(np.uint8)
+
+
+def tq_pack_signs(bits01) -> np.ndarray:
+    """TQBitPack.packSigns (TQBitPack.swift:95-112): bit 1 for +1."""
+    return tq_pack_bits(bits01, 1)
+
+
+class TQState:
+    """TQEncoder.EncoderState (TQEncoder.swift:88-107)."""
+
+    def __init__(self, dim: int, key_bits: int = 3, value_bits: int = 3, seed: int = 42):
+        self.dim, self.key_bits, self.value_bits, self.seed = dim, key_bits, value_bits, seed
+        self.signs = tq_random_signs(dim, seed)
+        self.key_index_bits = max(key_bits - 1, 1)
+        self.key_codebook = tq_codebook(dim, self.key_index_bits)
+        self.value_index_bits = value_bits
+        self.value_codebook = tq_codebook(dim, value_bits)
+        self.S = tq_qjl_matrix(dim, seed + 1000)
+
+
+def _promote(a: int, b: int) -> int:
+    """MLX's type promotion among f32 / f16 / bf16: f16 with bf16 is f32."""
+    return a if a == b else F32
+
+
+def tq_encode(x, dtype: int, state: TQState, keys: bool, sink: int = 4, tail: int = 0) -> dict:
+    """TQEncoder.encodeKeys / encodeValues (TQEncoder.swift:135-206,
+    :262-312).  x: [B, H, T, D] values of `dtype` as f32.  Returns the
+    EncodedKeys / EncodedValues fields (norms as f16 bit patterns, sink /
+    tail as `dtype` values) plus the unpacked codes, signs, projections and
+    rotated vectors for the tests."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    B, H, T, D = x.shape
+    pre = min(max(sink, 0), T)
+    tl = min(max(tail, 0), max(0, T - pre))
+    mid = x[:, :, pre:T - tl]
+    assert mid.shape[2] > 0, "TurboQuant encode requires at least one compressible token"
+    rows = B * H * mid.shape[2]
+    flat = np.ascontiguousarray(mid).reshape(rows, D)
+    cb = state.key_codebook if keys else state.value_codebook
+    ib = state.key_index_bits if keys else state.value_index_bits
+    idx = np.empty((rows, D), np.uint8)
+    sgn = np.empty((rows, D), np.uint8)
+    vn = np.empty(rows, np.float32)
+    rn = np.empty(rows, np.float32)
+    proj = np.empty((rows, D), np.float32)
+    rot = np.empty((rows, D), np.float32)
+    S = state.S if keys else None
+    lib().tqo_encode(_p(flat), dtype, rows, D, _p(state.signs), _p(cb), ib,
+                     _p(S) if keys else None, _p(idx), _p(sgn), _p(vn), _p(rn), _p(proj), _p(rot))
+    ms = mid.shape
+    enc = {
+        "indices": tq_pack_bits(idx, ib), "vec_norms": from_f32(vn, F16).reshape(ms[:3] + (1,)),
+        "shape": list(ms), "index_bits": ib, "seed": state.seed,
+        "sink": x[:, :, :pre] if pre else None, "tail": x[:, :, T - tl:] if tl else None,
+        "dtype": dtype, "idx": idx, "rot": rot,
+    }
+    if keys:
+        enc.update(qjl=tq_pack_signs(sgn), res_norms=from_f32(rn, F16).reshape(ms[:3] + (1,)),
+                   sgn=sgn, proj=proj)
+    return enc
+
+
+def tq_decode(enc: dict, state: TQState, keys: bool):
+    """TQEncoder.decodeKeys / decodeValues (TQEncoder.swift:214-255,
+    :315-345) with the sink / tail concatenation; returns (values as f32,
+    result dtype code)."""
+    B, H, Tc, D = enc["shape"]
+    rows = B * H * Tc
+    idx = tq_unpack_bits(enc["indices"], enc["index_bits"], rows * D)
+    cb = state.key_codebook if keys else state.value_codebook
+    vn = to_f32(np.ascontiguousarray(enc["vec_norms"]).reshape(-1), F16)
+    out = np.empty((rows, D), np.float32)
+    if keys:
+        sg = tq_unpack_bits(enc["qjl"], 1, rows * D)
+        rn = to_f32(np.ascontiguousarray(enc["res_norms"]).reshape(-1), F16)
+        lib().tqo_decode(_p(idx), _p(sg), _p(vn), _p(rn), rows, D, _p(state.signs), _p(cb),
+                         _p(state.S), _p(out))
+    else:
+        lib().tqo_decode(_p(idx), None, _p(vn), None, rows, D, _p(state.signs), _p(cb), None,
+                         _p(out))
+    dec = out.reshape(B, H, Tc, D)
+    dt = F16
+    parts = [dec]
+    if enc["sink"] is not None:
+        parts.insert(0, enc["sink"])
+        dt = _promote(enc["dtype"], dt)
+    if enc["tail"] is not None:
+        parts.append(enc["tail"])
+        dt = _promote(enc["dtype"], dt)
+    return np.concatenate(parts, axis=2).astype(np.float32), dt
+
