@@ -242,7 +242,13 @@ enum {
   /* CompilableRotatingKVCache (BatchEngine/CompilableRotatingKVCache.swift:
    * 1-265): a RotatingKVCache whose buffers are allocated at maxSize once and
    * whose ring index and offset live in device memory. */
-  VKV_CACHE_COMPILABLE_ROTATING = 4
+  VKV_CACHE_COMPILABLE_ROTATING = 4,
+  /* TurboQuantKVCache (TurboQuant/TurboQuantKVCache.swift:70-671): float
+   * KV while filling, then a TurboQuant-encoded prefix decoded once into a
+   * float buffer followed by a float window.  vkv_cache_create gives the
+   * reference's defaults (keyBits 3, valueBits 3, 4 sink tokens, 64
+   * residual tokens; params.bits > 0 sets both bit widths). */
+  VKV_CACHE_TURBOQUANT = 5
 };
 
 typedef struct vkv_cache_params {
@@ -319,6 +325,81 @@ int vkv_cache_set_meta_state(vkv_cache cache, const char *const *strings, int32_
  * rolled [maskSize] row of the rotating single-token case). */
 int vkv_cache_make_mask(vkv_cache cache, int32_t n, int32_t window, int32_t return_array,
                         void *stream, int32_t *mode, vkv_array *mask);
+
+/* ---- TurboQuant KV codec (Libraries/MLXLMCommon/TurboQuant/) ----
+ * EncodedKeys / EncodedValues (TQEncodedData.swift:38-170) as device
+ * arrays, in the layouts TQDiskSerializer writes: codes of index_bits each
+ * and QJL signs packed flat into u32 words (TQBitPack.swift: value e of the
+ * [B, H, Tc, D] tensor in word e / (32 / bits) at bit (e % (32 / bits)) *
+ * bits), f16 norms [B, H, Tc, 1], and the exact sink / tail tokens
+ * [B, H, n, D] in the input dtype (ndim 0 when absent).  Values have no
+ * qjl / res_norms (ndim 0). */
+typedef struct vkv_tq_encoded {
+  vkv_array indices;
+  vkv_array qjl;
+  vkv_array res_norms;
+  vkv_array vec_norms;
+  vkv_array sink;
+  vkv_array tail;
+  int32_t shape[4];    /* the compressed [B, H, Tc, D] */
+  int32_t index_bits;  /* keys: keyBits - 1 (at least 1); values: valueBits */
+  int32_t seed;        /* EncoderState seed (42) */
+} vkv_tq_encoded;
+
+typedef struct vkv_tq_info {
+  int32_t phase;          /* TQPhase: 0 fill, 1 compressed */
+  int32_t has_encoded;    /* compressedKeys / compressedValues are present */
+  int64_t prefix_tokens;  /* prefixTokenCount */
+  int64_t window_tokens;  /* windowOffset */
+  int32_t key_bits, value_bits, sink_tokens, residual_tokens;
+} vkv_tq_info;
+
+/* TurboQuantKVCache(keyBits:valueBits:sinkTokens:residualTokens:)
+ * (TurboQuantKVCache.swift:139-150).  keyBits in [1, 9] (codes of
+ * max(keyBits - 1, 1) bits plus one QJL bit), valueBits in [1, 8]. */
+int vkv_turboquant_create(int32_t key_bits, int32_t value_bits, int32_t sink_tokens,
+                          int32_t residual_tokens, vkv_cache *out);
+/* TurboQuantKVCache.fromSimpleCache(_:keyBits:valueBits:sinkTokens:
+ * residualTokens:) (:326-356): encodes the simple cache's K/V (sink tokens
+ * and the last residual tokens kept exact), decodes them once into the
+ * unified buffer and returns a compressed-phase cache at the source's
+ * offset; an empty fill-phase cache when the source has no compressible
+ * middle of at least 8 tokens. */
+int vkv_turboquant_from_simple(vkv_cache simple, int32_t key_bits, int32_t value_bits,
+                               int32_t sink_tokens, int32_t residual_tokens, void *stream,
+                               vkv_cache *out);
+/* TurboQuantKVCache.hasCompressibleMiddle (:152-162). */
+int vkv_turboquant_has_compressible_middle(int64_t token_count, int32_t sink_tokens,
+                                           int32_t residual_tokens, int32_t minimum,
+                                           int32_t *out);
+int vkv_turboquant_info(vkv_cache cache, vkv_tq_info *info);
+/* compressedKeys / compressedValues (:94-95) as views owned by the cache;
+ * fails when the cache holds none (fill phase, or restored from decoded
+ * K/V). */
+int vkv_turboquant_encoded(vkv_cache cache, vkv_tq_encoded *keys, vkv_tq_encoded *values);
+/* serializedWindowState (:254-263): the exact tokens appended after the
+ * compression, *present = 0 when there are none. */
+int vkv_turboquant_window(vkv_cache cache, vkv_array *keys, vkv_array *values, int32_t *present);
+/* restoreCompressed(encodedKeys:encodedValues:sourceOffset:windowKeys:
+ * windowValues:) (:180-252): copies the records, decodes them with
+ * EncoderState(dim, index_bits + 1 | index_bits, seed), then appends the
+ * window, which must hold exactly sourceOffset - (encoded tokens) tokens
+ * (NULL when none); a mismatch leaves the cache empty (offset 0), as in
+ * the reference. */
+int vkv_turboquant_restore_compressed(vkv_cache cache, const vkv_tq_encoded *keys,
+                                      const vkv_tq_encoded *values, int64_t source_offset,
+                                      const vkv_array *window_keys, const vkv_array *window_values,
+                                      void *stream);
+/* restoreFromDecodedKV(keys:values:sourceOffset:) (:281-322). */
+int vkv_turboquant_restore_decoded(vkv_cache cache, const vkv_array *keys, const vkv_array *values,
+                                   int64_t source_offset, void *stream);
+/* The codec's host tables (EncoderState, TQEncoder.swift:88-107): the
+ * rotation signs of (dim, seed) (TQHadamard.generateRandomSigns), the
+ * Lloyd-Max codebook of (dim, bits) (TQCodebook.computeCodebook, 2^bits
+ * floats) and the QJL matrix [dim, dim] (TQQJL.generateProjection with
+ * seed + 1000).  Any output may be NULL.  Host only. */
+int vkv_tq_tables(int32_t dim, int32_t bits, int32_t seed, float *signs, float *codebook,
+                  float *qjl);
 
 /* createBatchCausalMask(queryLen:offsets:effectiveKeyLens:windowSize:)
  * (BatchEngine/BatchMask.swift:44-115): the bool mask [batch, 1, n,

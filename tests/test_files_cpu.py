@@ -177,3 +177,56 @@ def test_disk_record_reader_counts_and_required_miss(tmp_path):
             assert all(h is None for h in hs), name
         else:
             assert rc == 1 and want[name] in vkv.lib().vkv_last_error().decode(), name
+
+
+def _tq_record(window_values=True, offset=100):
+    """A kind-1 layer in serializeTQLayer's layout (TQDiskSerializer.swift:
+    368-429) with 28 encoded + 4 sink + 64 tail tokens and a 4-token
+    window (zeros: only the structure is read before the check fails)."""
+    i32 = lambda *v: np.array(v, np.int32)
+    f16 = lambda *s: np.zeros(s, np.float16)
+    words = lambda n, bits: np.zeros(-(-n // (32 // bits)), np.uint32)
+    n = 4 * 28 * 16
+    rec = {"__jang_cache_format_version__": i32(2), "__layer_kind_0__": i32(1),
+           "tq_0_ck_indices": words(n, 3), "tq_0_ck_qjl": words(n, 1),
+           "tq_0_ck_res_norms": f16(1, 4, 28, 1), "tq_0_ck_vec_norms": f16(1, 4, 28, 1),
+           "tq_0_ck_sink": f16(1, 4, 4, 16), "tq_0_ck_tail": f16(1, 4, 64, 16),
+           "__tq_0_ck_shape__": i32(1, 4, 28, 16), "__tq_0_ck_index_bits__": i32(3),
+           "__tq_0_ck_seed__": i32(42), "tq_0_cv_indices": words(n, 4),
+           "tq_0_cv_norms": f16(1, 4, 28, 1), "tq_0_cv_sink": f16(1, 4, 4, 16),
+           "tq_0_cv_tail": f16(1, 4, 64, 16), "__tq_0_cv_shape__": i32(1, 4, 28, 16),
+           "__tq_0_cv_index_bits__": i32(4), "__tq_0_cv_seed__": i32(42),
+           "__tq_0_offset__": i32(offset), "tq_0_window_keys": f16(1, 4, offset - 96, 16)}
+    if window_values:
+        rec["tq_0_window_values"] = f16(1, 4, offset - 96, 16)
+    return rec
+
+
+@pytest.mark.parametrize("case,message", [
+    ("missing_window_values", "missing TurboQuant window"),
+    ("short_offset", "inconsistent TurboQuant token counts"),
+    ("no_qjl", "incomplete TurboQuant payload"),
+    ("unexpected_window", "unexpected TurboQuant window"),
+])
+def test_disk_record_turboquant_required_misses(tmp_path, case, message):
+    """deserializeTQLayer's refusals (TQDiskSerializer.swift:1244-1346) and
+    the reference test that drops tq_0_window_values
+    (TQDiskSerializerTests.swift:221-239): the whole record is refused
+    before any layer is built."""
+    rec = _tq_record()
+    if case == "missing_window_values":
+        rec = _tq_record(window_values=False)
+    elif case == "short_offset":
+        rec["__tq_0_offset__"] = np.array([90], np.int32)
+    elif case == "no_qjl":
+        del rec["tq_0_ck_qjl"]
+    elif case == "unexpected_window":
+        rec["__tq_0_offset__"] = np.array([96], np.int32)
+    p = str(tmp_path / f"{case}.safetensors")
+    save_file(rec, p, metadata={"format": "mlx"})
+    n = C.c_int32()
+    hs = (C.c_void_p * 4)()
+    assert vkv.lib().vkv_disk_cache_load(p.encode(), None, hs, 4, C.byref(n)) == 1
+    err = vkv.lib().vkv_last_error().decode()
+    assert message in err and "required miss" in err, err
+    assert all(h is None for h in hs)

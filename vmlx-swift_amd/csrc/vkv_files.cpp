@@ -506,6 +506,7 @@ const char* class_name(int kind) {
     case VKV_CACHE_ROTATING:
     case VKV_CACHE_COMPILABLE_ROTATING: return "RotatingKVCache";
     case VKV_CACHE_QUANTIZED: return "QuantizedKVCache";
+    case VKV_CACHE_TURBOQUANT: return "TurboQuantKVCache";  // not loadable, as in the reference
     default: return "KVCache";  // KVCacheSimple and the fixed-buffer cache
   }
 }
@@ -723,12 +724,158 @@ int vkv_disk_hash_tokens(const int64_t* tokens, int64_t n_tokens, const char* mo
   });
 }
 
+namespace {
+
+// serializeTQLayer (TQDiskSerializer.swift:368-429): the encoded records
+// (tq_i_ck_* / tq_i_cv_*, shapes, index bits, seeds), the offset and, when
+// tokens follow the encoded ones, the exact window (tq_i_window_*).
+void save_tq_layer(TurboQuantCache& t, const std::string& I, TensorMap& ts, hipStream_t st) {
+  vkv_tq_encoded ek, ev;
+  t.encoded(&ek, &ev);
+  const std::string k = "tq_" + I + "_ck_", v = "tq_" + I + "_cv_";
+  ts[k + "indices"] = to_host(ek.indices, st);
+  ts[k + "qjl"] = to_host(ek.qjl, st);
+  ts[k + "res_norms"] = to_host(ek.res_norms, st);
+  ts[k + "vec_norms"] = to_host(ek.vec_norms, st);
+  if (ek.sink.ndim) ts[k + "sink"] = to_host(ek.sink, st);
+  if (ek.tail.ndim) ts[k + "tail"] = to_host(ek.tail, st);
+  ts["__tq_" + I + "_ck_shape__"] = int32_vec({ek.shape[0], ek.shape[1], ek.shape[2], ek.shape[3]});
+  ts["__tq_" + I + "_ck_index_bits__"] = int32_vec({ek.index_bits});
+  ts["__tq_" + I + "_ck_seed__"] = int32_vec({ek.seed});
+  ts[v + "indices"] = to_host(ev.indices, st);
+  ts[v + "norms"] = to_host(ev.vec_norms, st);
+  if (ev.sink.ndim) ts[v + "sink"] = to_host(ev.sink, st);
+  if (ev.tail.ndim) ts[v + "tail"] = to_host(ev.tail, st);
+  ts["__tq_" + I + "_cv_shape__"] = int32_vec({ev.shape[0], ev.shape[1], ev.shape[2], ev.shape[3]});
+  ts["__tq_" + I + "_cv_index_bits__"] = int32_vec({ev.index_bits});
+  ts["__tq_" + I + "_cv_seed__"] = int32_vec({ev.seed});
+  ts["__tq_" + I + "_offset__"] = int32_vec({static_cast<int32_t>(t.offset)});
+  const int64_t encoded = static_cast<int64_t>(ek.shape[2]) + (ek.sink.ndim ? ek.sink.shape[2] : 0) +
+                          (ek.tail.ndim ? ek.tail.shape[2] : 0);
+  const int64_t live = t.offset - encoded;
+  vkv_array wk{}, wv{};
+  if (live > 0 && t.window_state(&wk, &wv)) {
+    if (wk.shape[2] != live || wv.shape[2] != live) return;
+    ts["tq_" + I + "_window_keys"] = to_host(wk, st);
+    ts["tq_" + I + "_window_values"] = to_host(wv, st);
+  }
+}
+
+// deserializeTQLayer (TQDiskSerializer.swift:1244-1346) checks: every
+// record field present, the counts of encoded key and value tokens equal
+// and positive, the offset (default: the key shape's token count) not below
+// them, and exactly offset - count window tokens when that is positive.
+// Returns the offset.
+int64_t check_tq_layer(const StFile& f, const std::string& I) {
+  auto has = [&](const std::string& k) { return f.tensors.count(k) > 0; };
+  const std::string k = "tq_" + I + "_ck_", v = "tq_" + I + "_cv_";
+  int32_t x = 0;
+  for (const char* n : {"indices", "qjl", "res_norms", "vec_norms"})
+    if (!has(k + n)) throw Error("layer " + I + ": incomplete TurboQuant payload: required miss");
+  if (!has(v + "indices") || !has(v + "norms"))
+    throw Error("layer " + I + ": incomplete TurboQuant payload: required miss");
+  for (const char* n : {"ck", "cv"}) {
+    const std::string p = "__tq_" + I + "_" + n;
+    if (!has(p + "_shape__") || !meta_int32(f, p + "_index_bits__", &x) ||
+        !meta_int32(f, p + "_seed__", &x))
+      throw Error("layer " + I + ": incomplete TurboQuant payload: required miss");
+  }
+  auto shape = [&](const std::string& key) {
+    HostTensor t = read_tensor(f, key);
+    if (t.dtype != VKV_I32 || t.shape.size() != 1) throw Error("layer " + I + ": bad TurboQuant shape");
+    std::vector<int32_t> out(t.shape[0]);
+    memcpy(out.data(), t.data.data(), out.size() * 4);
+    return out;
+  };
+  auto count = [&](const std::vector<int32_t>& sh, const std::string& pre) {
+    if (sh.size() < 3) return int64_t{0};
+    int64_t n = sh[2];
+    for (const char* part : {"sink", "tail"}) {
+      auto it = f.tensors.find(pre + part);
+      if (it != f.tensors.end() && it->second.shape.size() == 4) n += it->second.shape[2];
+    }
+    return n;
+  };
+  const auto ks = shape("__tq_" + I + "_ck_shape__"), vs = shape("__tq_" + I + "_cv_shape__");
+  const int64_t nk = count(ks, k), nv = count(vs, v);
+  int64_t offset = ks.size() >= 3 ? ks[2] : 0;
+  if (has("__tq_" + I + "_offset__")) {
+    if (!meta_int32(f, "__tq_" + I + "_offset__", &x)) throw Error("layer " + I + ": bad TurboQuant offset");
+    offset = x;
+  }
+  if (nk <= 0 || nk != nv || offset < nk)
+    throw Error("layer " + I + ": inconsistent TurboQuant token counts: required miss");
+  const int64_t window = offset - nk;
+  const bool wk = has("tq_" + I + "_window_keys"), wv = has("tq_" + I + "_window_values");
+  if (window == 0 && (wk || wv))
+    throw Error("layer " + I + ": unexpected TurboQuant window: required miss");
+  if (window > 0) {
+    if (!wk || !wv) throw Error("layer " + I + ": missing TurboQuant window: required miss");
+    const auto& a = f.tensors.at("tq_" + I + "_window_keys");
+    const auto& b = f.tensors.at("tq_" + I + "_window_values");
+    if (a.shape.size() != 4 || b.shape.size() != 4 || a.shape[2] != window || b.shape[2] != window)
+      throw Error("layer " + I + ": TurboQuant window length mismatch: required miss");
+  }
+  return offset;
+}
+
+// restoreTQLayer into a fresh layer (CacheHelpers.swift:1248-1320):
+// TurboQuantKVCache(keyBits: ck bits + 1, valueBits: cv bits, sinkTokens:
+// max(sinks, 4), residualTokens: max(tails, 64)), then restoreCompressed.
+std::unique_ptr<Cache> load_tq_layer(const StFile& f, const std::string& I, int64_t offset,
+                                     hipStream_t st) {
+  std::vector<DevBuf> keep;
+  auto dev = [&](const std::string& key, vkv_array* a) {
+    if (!f.tensors.count(key)) {
+      *a = vkv_array{};
+      return;
+    }
+    keep.push_back(to_device(read_tensor(f, key), st, a));
+  };
+  auto record = [&](const std::string& pre, const std::string& meta, bool keys) {
+    vkv_tq_encoded e{};
+    dev(pre + "indices", &e.indices);
+    if (keys) {
+      dev(pre + "qjl", &e.qjl);
+      dev(pre + "res_norms", &e.res_norms);
+      dev(pre + "vec_norms", &e.vec_norms);
+    } else {
+      dev(pre + "norms", &e.vec_norms);
+    }
+    dev(pre + "sink", &e.sink);
+    dev(pre + "tail", &e.tail);
+    HostTensor sh = read_tensor(f, meta + "_shape__");
+    if (sh.shape.size() != 1 || sh.shape[0] != 4) throw Error("layer " + I + ": bad TurboQuant shape");
+    memcpy(e.shape, sh.data.data(), 16);
+    meta_int32(f, meta + "_index_bits__", &e.index_bits);
+    meta_int32(f, meta + "_seed__", &e.seed);
+    return e;
+  };
+  vkv_tq_encoded ek = record("tq_" + I + "_ck_", "__tq_" + I + "_ck", true);
+  vkv_tq_encoded ev = record("tq_" + I + "_cv_", "__tq_" + I + "_cv", false);
+  vkv_array wk{}, wv{};
+  dev("tq_" + I + "_window_keys", &wk);
+  dev("tq_" + I + "_window_values", &wv);
+  auto cnt = [](const vkv_array& a) { return a.ndim == 4 ? a.shape[2] : 0; };
+  const int sink = static_cast<int>(std::max<int64_t>({cnt(ek.sink), cnt(ev.sink), 4}));
+  const int res = static_cast<int>(std::max<int64_t>({cnt(ek.tail), cnt(ev.tail), 64}));
+  auto c = std::make_unique<TurboQuantCache>(ek.index_bits + 1, ev.index_bits, sink, res);
+  c->restore_compressed(ek, ev, offset, wk.ndim ? &wk : nullptr, wv.ndim ? &wv : nullptr, st);
+  VKV_HIP(hipStreamSynchronize(st));
+  if (c->offset <= 0) throw Error("layer " + I + ": the TurboQuant layer did not restore: required miss");
+  return c;
+}
+
+}  // namespace
+
 // TQDiskSerializer.serialize (version 2) for the attention layers this
 // library holds: KVCacheSimple -> kind 2 (kv_i_keys / kv_i_values),
 // RotatingKVCache -> kind 6 (rot_i_keys / rot_i_values + __rot_i_meta__
 // [keep, maxSize, step, offset, idx]), QuantizedKVCache -> kind 5
-// (qkv_i_k + __qkv_i_count__ / _offset__ / _group_size__ / _bits__); an
-// empty cache -> kind 4 (skip).  Scalars are 1-element int32 arrays.
+// (qkv_i_k + __qkv_i_count__ / _offset__ / _group_size__ / _bits__), a
+// compressed TurboQuantKVCache holding its encoded records -> kind 1, any
+// other TurboQuantKVCache -> kind 2 from its state; an empty cache -> kind
+// 4 (skip).  Scalars are 1-element int32 arrays.
 int vkv_disk_cache_save(const char* path, const vkv_cache* caches, int32_t n_caches, void* stream) {
   return guarded([&] {
     if (!path) throw Error("path is NULL");
@@ -742,8 +889,16 @@ int vkv_disk_cache_save(const char* path, const vkv_cache* caches, int32_t n_cac
       Cache& c = *caches[i]->impl;
       const std::string I = std::to_string(i);
       const std::string kind_key = "__layer_kind_" + I + "__";
-      auto arrays = state_to_host(c, st);
       const int kind = c.kind();
+      if (kind == VKV_CACHE_TURBOQUANT) {
+        auto* t = static_cast<TurboQuantCache*>(&c);
+        if (t->phase_ == 1 && t->ck_ && t->cv_) {
+          save_tq_layer(*t, I, ts, st);
+          ts[kind_key] = int32_vec({1});
+          continue;
+        }
+      }
+      auto arrays = state_to_host(c, st);
       if (kind == VKV_CACHE_QUANTIZED) {
         if (arrays.size() != 4 && arrays.size() != 6) {
           ts[kind_key] = int32_vec({4});
@@ -787,11 +942,12 @@ int vkv_disk_cache_save(const char* path, const vkv_cache* caches, int32_t n_cac
   });
 }
 
-// TQDiskSerializer.deserializeV2 (:1023-1170) for kinds 2, 5, 6 and 4:
+// TQDiskSerializer.deserializeV2 (:1023-1170) for kinds 1, 2, 5, 6 and 4:
 // caches[i] receives the restored layer i, or NULL for a skipped layer.  A
-// missing kind tag inside the layer range, an incomplete payload or an
-// unsupported kind (TurboQuant, Mamba, composite) fails the whole record,
-// as the reference turns them into a required miss.
+// missing kind tag inside the layer range, an incomplete payload, a
+// TurboQuant layer that does not restore or an unsupported kind (Mamba,
+// composite) fails the whole record, as the reference turns them into a
+// required miss.
 int vkv_disk_cache_load(const char* path, void* stream, vkv_cache* caches, int32_t capacity,
                         int32_t* n_layers) {
   return guarded([&] {
@@ -837,9 +993,10 @@ int vkv_disk_cache_load(const char* path, void* stream, vkv_cache* caches, int32
           if (!has("qkv_" + I + "_" + std::to_string(k)))
             throw Error("layer " + I + ": incomplete quantized payload");
       }
-      if (kind != 2 && kind != 4 && kind != 5 && kind != 6)
+      if (kind == 1) check_tq_layer(f, I);
+      if (kind != 1 && kind != 2 && kind != 4 && kind != 5 && kind != 6)
         throw Error("layer " + I + ": kind " + std::to_string(kind) +
-                    " (TurboQuant, Mamba or composite) is not restored here: required miss");
+                    " (Mamba or composite) is not restored here: required miss");
     }
     std::vector<std::unique_ptr<Cache>> built(n);
     for (int i = 0; i < n; i++) {
@@ -847,7 +1004,9 @@ int vkv_disk_cache_load(const char* path, void* stream, vkv_cache* caches, int32
       const int32_t kind = kinds[i];
       vkv_cache_params p{};
       if (kind == 4) continue;  // skip
-      if (kind == 2) {
+      if (kind == 1) {
+        built[i] = load_tq_layer(f, I, check_tq_layer(f, I), st);
+      } else if (kind == 2) {
         if (!f.tensors.count("kv_" + I + "_keys") || !f.tensors.count("kv_" + I + "_values"))
           throw Error("layer " + I + ": incomplete kv payload");
         p.kind = VKV_CACHE_SIMPLE;
@@ -895,7 +1054,7 @@ int vkv_disk_cache_load(const char* path, void* stream, vkv_cache* caches, int32
         built[i] = std::move(c);
       } else {
         throw Error("layer " + I + ": kind " + std::to_string(kind) +
-                    " (TurboQuant, Mamba or composite) is not restored here: required miss");
+                    " (Mamba or composite) is not restored here: required miss");
       }
     }
     for (int i = 0; i < n; i++) {

@@ -16,7 +16,7 @@ namespace vkv {
 
 // ----------------------------------------------------------------- helpers
 
-static void check4(const vkv_array& a, const char* name) {
+void check4(const vkv_array& a, const char* name) {
   if (a.ndim != 4) throw Error(std::string(name) + " must be a 4-D array [B, H, S, D]");
   if (a.strides[3] != 1) throw Error(std::string(name) + " last dim must be contiguous");
   if (a.dtype != VKV_F32 && a.dtype != VKV_F16 && a.dtype != VKV_BF16)
@@ -41,7 +41,7 @@ vkv_array Dense4::view(int64_t len) const {
   return a;
 }
 
-static Dense4 alloc_dense(int64_t B, int64_t H, int64_t cap, int64_t D, int dtype, bool zero,
+Dense4 alloc_dense(int64_t B, int64_t H, int64_t cap, int64_t D, int dtype, bool zero,
                           hipStream_t st) {
   Dense4 d;
   d.dtype = dtype;
@@ -55,7 +55,7 @@ static Dense4 alloc_dense(int64_t B, int64_t H, int64_t cap, int64_t D, int dtyp
 }
 
 // dst[:, :, dt0:dt0+len, :] = src[:, :, st0:st0+len, :]  (src any strided 4-D array)
-static void copy_tokens(const Dense4& dst, int64_t dt0, const vkv_array& src, int64_t st0,
+void copy_tokens(const Dense4& dst, int64_t dt0, const vkv_array& src, int64_t st0,
                         int64_t len, hipStream_t st) {
   if (len <= 0) return;
   const int es = elem_bytes(src.dtype);
@@ -67,12 +67,12 @@ static void copy_tokens(const Dense4& dst, int64_t dt0, const vkv_array& src, in
   launch_copy4d(es, sp, shape, sstr, dp, dstr, st);
 }
 
-static void copy_dense(const Dense4& dst, int64_t dt0, const Dense4& src, int64_t st0, int64_t len,
+void copy_dense(const Dense4& dst, int64_t dt0, const Dense4& src, int64_t st0, int64_t len,
                        hipStream_t st) {
   copy_tokens(dst, dt0, src.view(src.cap), st0, len, st);
 }
 
-static Dense4 dense_from_array(const vkv_array& a, hipStream_t st) {
+Dense4 dense_from_array(const vkv_array& a, hipStream_t st) {
   Dense4 d = alloc_dense(a.shape[0], a.shape[1], a.shape[2], a.shape[3], a.dtype, false, st);
   copy_tokens(d, 0, a, 0, a.shape[2], st);
   return d;
@@ -130,6 +130,9 @@ std::unique_ptr<Cache> make_cache(const vkv_cache_params& p) {
       if (p.max_size <= 0) throw Error("CompilableRotatingKVCache requires maxSize > 0");
       if (p.keep < 0 || p.keep >= p.max_size) throw Error("keep must be in [0, maxSize)");
       return std::make_unique<CompilableRotatingCache>(p.max_size, p.keep, step);
+    case VKV_CACHE_TURBOQUANT:
+      return std::make_unique<TurboQuantCache>(p.bits > 0 ? p.bits : 3, p.bits > 0 ? p.bits : 3, 4,
+                                               64);
     default: throw Error("unknown cache kind");
   }
 }

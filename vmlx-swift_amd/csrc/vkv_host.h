@@ -76,6 +76,17 @@ struct Dense4 {
   vkv_array view(int64_t len) const;  // [B,H,len,D] over [.., cap, ..]
 };
 
+// Dense helpers shared by the caches (vkv_host.cpp).
+void check4(const vkv_array& a, const char* name);
+Dense4 alloc_dense(int64_t B, int64_t H, int64_t cap, int64_t D, int dtype, bool zero,
+                   hipStream_t st);
+// dst[:, :, dt0:dt0+len, :] = src[:, :, st0:st0+len, :] (same dtype)
+void copy_tokens(const Dense4& dst, int64_t dt0, const vkv_array& src, int64_t st0, int64_t len,
+                 hipStream_t st);
+void copy_dense(const Dense4& dst, int64_t dt0, const Dense4& src, int64_t st0, int64_t len,
+                hipStream_t st);
+Dense4 dense_from_array(const vkv_array& a, hipStream_t st);
+
 // Chunk layout shared by the pool and the quantized cache: byte sizes of one
 // matrix's codes (or float values) and of the scale/bias area, the chunk
 // size, and the offsets of K, V and the scale/bias area.
@@ -356,6 +367,55 @@ class PrefixManager {
 // bytes released.  Growth during graph capture on `st` is an error.
 float* attention_workspace(hipStream_t st, size_t floats);
 size_t workspace_release(hipStream_t st);
+
+// TurboQuantKVCache (TurboQuant/TurboQuantKVCache.swift:70-671), in
+// vkv_tq_host.cpp.  Fill phase: float K/V appended as KVCacheSimple would
+// return them.  Compressed phase: the encoded records of the prefix
+// (sink + middle + tail tokens), decoded once into a unified float buffer
+// [decoded prefix | window], new tokens written into the window.
+struct TqEncoded;
+class TurboQuantCache : public Cache {
+ public:
+  static constexpr int64_t kWindowStep = 256;      // windowStep (:106)
+  static constexpr int64_t kMinimumCompressed = 8;  // minimumCompressedTokens (:79)
+  TurboQuantCache(int key_bits, int value_bits, int sink, int residual);
+  int kind() const override { return VKV_CACHE_TURBOQUANT; }
+  bool trimmable() const override { return true; }
+  int64_t trim(int64_t n) override;
+  int64_t capacity() const override;
+  void update(const vkv_array& k, const vkv_array& v, hipStream_t st, vkv_array* ok,
+              vkv_array* ov) override;
+  int state(hipStream_t, vkv_array* out) override;
+  void set_state(const vkv_array* a, int count, hipStream_t st) override;
+  void set_meta_state(const std::vector<std::string>&) override {}  // the setter ignores
+  std::unique_ptr<Cache> copy(hipStream_t st) override;
+  void read_kv(hipStream_t st, vkv_array* k, vkv_array* v) override;
+
+  static bool has_compressible_middle(int64_t tokens, int64_t sink, int64_t residual,
+                                      int64_t minimum);
+  static std::unique_ptr<TurboQuantCache> from_simple(Cache& src, int key_bits, int value_bits,
+                                                      int sink, int residual, hipStream_t st);
+  void compress(const vkv_array& k, const vkv_array& v, int64_t source_offset, hipStream_t st);
+  void restore_compressed(const vkv_tq_encoded& k, const vkv_tq_encoded& v, int64_t source_offset,
+                          const vkv_array* wk, const vkv_array* wv, hipStream_t st);
+  void restore_decoded(const vkv_array& k, const vkv_array& v, int64_t source_offset,
+                       hipStream_t st);
+  bool window_state(vkv_array* k, vkv_array* v) const;
+  void encoded(vkv_tq_encoded* k, vkv_tq_encoded* v) const;
+
+  int key_bits_, value_bits_, sink_, residual_;
+  int phase_ = 0;  // 0 fill, 1 compressed
+  Dense4 fk_, fv_;
+  std::shared_ptr<TqEncoded> ck_, cv_;
+  Dense4 uk_, uv_;
+  int64_t prefix_ = 0, window_ = 0;
+
+ private:
+  void reset();
+  void seat(std::shared_ptr<TqEncoded> ek, std::shared_ptr<TqEncoded> ev, hipStream_t st);
+  void append_window(const vkv_array& k, const vkv_array& v, hipStream_t st);
+};
+void tq_host_tables(int dim, int bits, int seed, float* signs, float* codebook, float* qjl);
 
 // Runs f under the C ABI's error convention (vkv_capi.cpp): returns 0, or 1
 // with the exception's message kept for vkv_last_error().

@@ -247,6 +247,52 @@ void launch_offset_mask(const int32_t* ctr, int n, int cols, int window, int rin
 void launch_causal_mask(int n, int64_t off, int window, uint8_t* mask, hipStream_t st);
 // [size] bool: roll(arange(size) >= size - window, shift).
 void launch_roll_mask(int64_t size, int64_t window, int64_t shift, uint8_t* mask, hipStream_t st);
+// ---- TurboQuant codec (vkv_tq.hip) ----
+constexpr int kTqTileRows = 32;  // vectors per workgroup tile
+// The power-of-two blocks of TQHadamard.decomposePow2Blocks and their f32
+// 1 / sqrt(n) scales.
+struct TqBlocks {
+  int32_t n;
+  int32_t size[16], off[16];
+  float scale[16];
+};
+struct TqEncodeArgs {
+  const void* x;             // [B, H, T, D] strided source, element strides
+  int32_t dtype;
+  int64_t sb, sh, st;
+  int32_t B, H, Tc, t0, D;   // encodes tokens [t0, t0 + Tc)
+  const float* signs;        // [D] rotation signs
+  const float* codebook;     // [nc] levels
+  const float* bounds;       // [nc - 1] midpoints
+  int32_t nc, bits;          // levels, index bits
+  const float* St;           // keys: S transposed [D][D]; null for values
+  TqBlocks blocks;
+  uint32_t* indices;         // packed codes (zeroed first)
+  uint32_t* qjl;             // packed signs (keys, zeroed first)
+  uint16_t* vec_norms;       // f16 [rows]
+  uint16_t* res_norms;       // f16 [rows] (keys)
+};
+struct TqDecodeArgs {
+  const uint32_t* indices;
+  const uint32_t* qjl;       // keys; null for values
+  const uint16_t* vec_norms;
+  const uint16_t* res_norms;
+  int32_t B, H, Tc, D, bits;
+  const float* codebook;
+  const float* signs;
+  const float* S;            // keys: [D][D]; null for values
+  float qs;                  // f32(sqrt(pi / 2)) / f32(D)
+  TqBlocks blocks;
+  void* out;                 // f16 or f32, element strides, tokens from t0
+  int32_t out_dtype, t0;
+  int64_t osb, osh, ost;
+};
+void launch_tq_encode(const TqEncodeArgs& a, hipStream_t st);
+void launch_tq_decode(const TqDecodeArgs& a, hipStream_t st);
+// dst = src with a dtype conversion (4-D, element strides).
+void launch_cast4d(const void* src, int sdt, const int64_t* shape, const int64_t* sstr, void* dst,
+                   int ddt, const int64_t* dstr, hipStream_t st);
+
 // createBatchCausalMask: [batch, 1, n, cols] bytes from host per-slot
 // offsets and key lengths; window < 0 means none.
 constexpr int kBatchMaskSlots = 240;

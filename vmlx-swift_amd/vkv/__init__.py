@@ -25,6 +25,7 @@ F32, F16, BF16, U32, I32, U8, BOOL = 0, 1, 2, 3, 4, 5, 6
 MASK_NONE, MASK_CAUSAL, MASK_ARRAY = 0, 1, 2
 CACHE_SIMPLE, CACHE_ROTATING, CACHE_QUANTIZED = 0, 1, 2
 CACHE_COMPILABLE, CACHE_COMPILABLE_ROTATING = 3, 4
+CACHE_TURBOQUANT = 5
 VIEW_KEYS_ONLY = 1
 
 
@@ -44,6 +45,19 @@ class PagedView(C.Structure):
                 ("block_bytes", C.c_int64), ("head_bytes", C.c_int64),
                 ("block_table", C.c_void_p), ("table_stride", C.c_int32),
                 ("seq_lens", C.c_void_p), ("n_seqs", C.c_int32), ("max_len", C.c_int32)]
+
+
+class TQEncoded(C.Structure):
+    """vkv_tq_encoded: EncodedKeys / EncodedValues as device arrays."""
+    _fields_ = [("indices", Array), ("qjl", Array), ("res_norms", Array), ("vec_norms", Array),
+                ("sink", Array), ("tail", Array), ("shape", C.c_int32 * 4),
+                ("index_bits", C.c_int32), ("seed", C.c_int32)]
+
+
+class TQInfo(C.Structure):
+    _fields_ = [("phase", C.c_int32), ("has_encoded", C.c_int32), ("prefix_tokens", C.c_int64),
+                ("window_tokens", C.c_int64), ("key_bits", C.c_int32), ("value_bits", C.c_int32),
+                ("sink_tokens", C.c_int32), ("residual_tokens", C.c_int32)]
 
 
 class CacheParams(C.Structure):
@@ -86,7 +100,10 @@ EXPORTS = (
     "vkv_quantized_paged_sdpa", "vkv_prefix_writable", "vkv_prompt_cache_save",
     "vkv_prompt_cache_load", "vkv_prompt_cache_save_paged", "vkv_prompt_cache_load_paged",
     "vkv_disk_hash_tokens", "vkv_disk_cache_save", "vkv_disk_cache_load", "vkv_cache_kind",
-    "vkv_batch_causal_mask",
+    "vkv_batch_causal_mask", "vkv_turboquant_create", "vkv_turboquant_from_simple",
+    "vkv_turboquant_has_compressible_middle", "vkv_turboquant_info", "vkv_turboquant_encoded",
+    "vkv_turboquant_window", "vkv_turboquant_restore_compressed",
+    "vkv_turboquant_restore_decoded", "vkv_tq_tables",
 )
 TIME_DECODE, TIME_MLA, TIME_FDECODE = 0, 1, 2
 
@@ -599,6 +616,114 @@ class QuantizedKVCache(_Cache):
         return s
 
 
+class TurboQuantKVCache(_Cache):
+    """TurboQuantKVCache (TurboQuant/TurboQuantKVCache.swift:70-671)."""
+    DEFAULT_RESIDUAL_TOKENS = 64
+    MINIMUM_COMPRESSED_TOKENS = 8
+
+    def __init__(self, key_bits: int = 3, value_bits: int = 3, sink_tokens: int = 4,
+                 residual_tokens: int = 64, handle=None):
+        self._h = C.c_void_p()
+        if handle is not None:
+            self._h = handle
+        else:
+            _chk(lib().vkv_turboquant_create(key_bits, value_bits, sink_tokens, residual_tokens,
+                                             C.byref(self._h)))
+
+    @staticmethod
+    def from_simple_cache(source: "KVCacheSimple", key_bits: int, value_bits: int,
+                          sink_tokens: int = 4, residual_tokens: int = 64, stream=None):
+        h = C.c_void_p()
+        _chk(lib().vkv_turboquant_from_simple(source._h, key_bits, value_bits, sink_tokens,
+                                              residual_tokens, stream_ptr(stream), C.byref(h)))
+        return TurboQuantKVCache(handle=h)
+
+    @staticmethod
+    def has_compressible_middle(token_count: int, sink_tokens: int = 4,
+                                residual_tokens: int = 64, minimum: int = 8) -> bool:
+        out = C.c_int32()
+        _chk(lib().vkv_turboquant_has_compressible_middle(C.c_int64(token_count), sink_tokens,
+                                                          residual_tokens, minimum, C.byref(out)))
+        return bool(out.value)
+
+    @property
+    def info(self) -> dict:
+        i = TQInfo()
+        _chk(lib().vkv_turboquant_info(self._h, C.byref(i)))
+        return {f: getattr(i, f) for f, _ in TQInfo._fields_}
+
+    @property
+    def phase(self) -> str:
+        return "compressed" if self.info["phase"] else "fill"
+
+    def encoded_views(self):
+        k, v = TQEncoded(), TQEncoded()
+        _chk(lib().vkv_turboquant_encoded(self._h, C.byref(k), C.byref(v)))
+        return k, v
+
+    def encoded(self):
+        """(compressedKeys, compressedValues) as dicts of fresh tensors."""
+        def rec(e):
+            get = lambda a: to_torch(a) if a.ndim else None
+            return {"indices": get(e.indices), "qjl": get(e.qjl), "res_norms": get(e.res_norms),
+                    "vec_norms": get(e.vec_norms), "sink": get(e.sink), "tail": get(e.tail),
+                    "shape": list(e.shape), "index_bits": e.index_bits, "seed": e.seed}
+        k, v = self.encoded_views()
+        return rec(k), rec(v)
+
+    def window_state(self):
+        k, v, p = Array(), Array(), C.c_int32()
+        _chk(lib().vkv_turboquant_window(self._h, C.byref(k), C.byref(v), C.byref(p)))
+        return (to_torch(k), to_torch(v)) if p.value else None
+
+    @staticmethod
+    def _record(r: dict) -> TQEncoded:
+        e = TQEncoded()
+        e.indices = arr(r["indices"], U32)
+        if r.get("qjl") is not None:
+            e.qjl = arr(r["qjl"], U32)
+        if r.get("res_norms") is not None:
+            e.res_norms = arr(r["res_norms"])
+        e.vec_norms = arr(r["vec_norms"])
+        if r.get("sink") is not None:
+            e.sink = arr(r["sink"])
+        if r.get("tail") is not None:
+            e.tail = arr(r["tail"])
+        for i in range(4):
+            e.shape[i] = r["shape"][i]
+        e.index_bits = r["index_bits"]
+        e.seed = r.get("seed", 42)
+        return e
+
+    def restore_compressed(self, keys: dict, values: dict, source_offset: int,
+                           window_keys=None, window_values=None, stream=None):
+        """restoreCompressed(encodedKeys:encodedValues:sourceOffset:windowKeys:
+        windowValues:); records as returned by encoded()."""
+        ek, ev = self._record(keys), self._record(values)
+        wk = C.byref(arr(window_keys)) if window_keys is not None else None
+        wv = C.byref(arr(window_values)) if window_values is not None else None
+        _chk(lib().vkv_turboquant_restore_compressed(self._h, C.byref(ek), C.byref(ev),
+                                                     C.c_int64(source_offset), wk, wv,
+                                                     stream_ptr(stream)))
+
+    def restore_from_decoded(self, keys, values, source_offset: int, stream=None):
+        _chk(lib().vkv_turboquant_restore_decoded(self._h, C.byref(arr(keys)),
+                                                  C.byref(arr(values)), C.c_int64(source_offset),
+                                                  stream_ptr(stream)))
+
+
+def tq_tables(dim: int, bits: int, seed: int = 42):
+    """(rotation signs, Lloyd-Max codebook, QJL matrix) of the codec's
+    EncoderState, from the library's host code (no device needed)."""
+    import numpy as np
+    signs = np.empty(dim, np.float32)
+    cb = np.empty(1 << bits, np.float32)
+    S = np.empty((dim, dim), np.float32)
+    f = lambda a: a.ctypes.data_as(C.c_void_p)
+    _chk(lib().vkv_tq_tables(dim, bits, seed, f(signs), f(cb), f(S)))
+    return signs, cb, S
+
+
 # -------------------------------------------------------------------- pool
 class PagedPool:
     """Device block pool: [layer][block][kv head] chunks."""
@@ -775,7 +900,8 @@ def _wrap_handle(h):
     k = C.c_int32()
     _chk(lib().vkv_cache_kind(h, C.byref(k)))
     cls = {CACHE_SIMPLE: KVCacheSimple, CACHE_ROTATING: RotatingKVCache,
-           CACHE_QUANTIZED: QuantizedKVCache}.get(k.value, _Cache)
+           CACHE_QUANTIZED: QuantizedKVCache, CACHE_TURBOQUANT: TurboQuantKVCache}.get(k.value,
+                                                                                     _Cache)
     obj = object.__new__(cls)
     _Cache.__init__(obj, None, handle=h)
     return obj
