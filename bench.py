@@ -49,7 +49,8 @@ def parse():
     p.add_argument("--no-mla", action="store_true",
                    help="skip the MLA latent decode measurement (config 5)")
     p.add_argument("--only", default="all",
-                   choices=["all", "config3", "config1", "config2", "config4", "mla", "prefill"],
+                   choices=["all", "config3", "config1", "config2", "config4", "mla", "prefill",
+                            "turboquant"],
                    help="run one workload only (profiling); the JSON line needs 'all'")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 1 GiB device copy (vkv_array_copy) 5 times: the "
@@ -526,6 +527,59 @@ def cpu_baseline(threads, min_seconds=8.0):
                       f"in {tn:.1f} s; 1 thread: {p1} passes in {t1:.1f} s"}
 
 
+F32_VALU_PEAK_TFLOPS = 157.3  # MI355X dense fp32 (vector and matrix)
+
+
+def turboquant_measure(torch, vkv, steps, warmup):
+    """TurboQuantKVCache.fromSimpleCache at a Llama-3-8B layer's shape
+    (config 2: B 8, 8 KV heads x 128, 4096 bf16 tokens) with the reference's
+    defaults (keyBits 3, valueBits 3, 4 sink and 64 residual tokens): encode
+    K and V, decode both once into the unified buffer.  The key kernels
+    dominate: each vector's QJL projection (encode) and sign product
+    (decode) is a 128 x 128 f32 matrix-vector product, 2 * 128^2 flops."""
+    B, H, T, D = 8, 8, 4096, 128
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    k = vkv.fill_normal(torch.empty((B, H, T, D), **bf), 61)
+    v = vkv.fill_normal(torch.empty((B, H, T, D), **bf), 62)
+    simple = vkv.KVCacheSimple()
+    simple.update(k, v)
+    keep = []
+
+    def compress():
+        keep.append(vkv.TurboQuantKVCache.from_simple_cache(simple, 3, 3))
+        if len(keep) > 2:
+            keep.pop(0)
+
+    ms, enc_ms, enc_n = _time_calls(torch, vkv, compress, steps, warmup, vkv.TIME_TQ_ENCODE)
+    vkv.kernel_timing(True)
+    for _ in range(steps):
+        compress()
+    dec_ms, dec_n = vkv.kernel_timing_read(vkv.TIME_TQ_DECODE)
+    vkv.kernel_timing(False)
+    dec_ms /= max(dec_n, 1)
+    rows = B * H * (T - 4 - 64)
+    flops = rows * 2 * D * D
+    enc_tf = flops / (enc_ms * 1e-3) / 1e12
+    dec_tf = flops / (dec_ms * 1e-3) / 1e12
+    sk, _ = keep[-1].state
+    if not bool(torch.isfinite(sk.float()).all()):
+        raise RuntimeError("the decoded TurboQuant keys hold non-finite values")
+    return {
+        "workload": "TurboQuantKVCache.fromSimpleCache, bf16 [8, 8, 4096, 128] K and V, keyBits 3, "
+                    "valueBits 3, 4 sink + 64 residual tokens (encode + one decode, per layer)",
+        "compress_ms_per_layer": round(ms, 4),
+        "tokens_per_s": round(B * T / (ms * 1e-3), 1),
+        "key_encode_kernel_us": round(enc_ms * 1e3, 2),
+        "key_decode_kernel_us": round(dec_ms * 1e3, 2),
+        "roofline": {"bound": "valu", "achieved": round(enc_tf, 2), "peak": F32_VALU_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(enc_tf / F32_VALU_PEAK_TFLOPS, 4),
+                     "kernel": "tq_encode_kernel<128> (keys)", "flops_per_launch": flops},
+        "decode_roofline": {"achieved": round(dec_tf, 2), "peak": F32_VALU_PEAK_TFLOPS,
+                            "unit": "TFLOP/s", "frac": round(dec_tf / F32_VALU_PEAK_TFLOPS, 4),
+                            "kernel": "tq_decode_kernel<128> (keys)"},
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -548,6 +602,7 @@ def main():
         "config4": lambda: config4_measure(torch, vkv, args.steps, args.warmup),
         "mla": lambda: mla_measure(torch, vkv, args.steps, args.warmup),
         "prefill": lambda: prefill_measure(torch, vkv, args.steps, args.warmup),
+        "turboquant": lambda: turboquant_measure(torch, vkv, args.steps, args.warmup),
     }
     if args.only in legs:
         print(json.dumps({args.only: legs[args.only]()}), flush=True)
@@ -617,7 +672,8 @@ def main():
     others = args.only == "all" and not args.no_mla
     mla = legs["mla"]() if others else None
     prefill = legs["prefill"]() if others else None
-    configs = {k: legs[k]() for k in ("config1", "config2", "config4")} if others else None
+    configs = ({k: legs[k]() for k in ("config1", "config2", "config4", "turboquant")}
+               if others else None)
     cpu = None
     if not args.no_cpu_baseline and args.only == "all":
         # all the host CPUs this process may use, at most 16 (a GPU box's

@@ -105,7 +105,7 @@ EXPORTS = (
     "vkv_turboquant_window", "vkv_turboquant_restore_compressed",
     "vkv_turboquant_restore_decoded", "vkv_tq_tables",
 )
-TIME_DECODE, TIME_MLA, TIME_FDECODE = 0, 1, 2
+TIME_DECODE, TIME_MLA, TIME_FDECODE, TIME_TQ_ENCODE, TIME_TQ_DECODE = 0, 1, 2, 3, 4
 
 _lib = None
 
