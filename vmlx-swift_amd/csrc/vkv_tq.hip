@@ -33,6 +33,7 @@ namespace {
 
 constexpr int kRows = kTqTileRows;
 constexpr int kThreads = 256;
+static_assert(kRows * 8 == kThreads, "row sums use eight lanes per row");
 
 // f16 of an f32 value that is first rounded to f32: the barrier keeps the
 // compiler from folding the product or sum that made v into a mixed
@@ -48,9 +49,11 @@ __device__ __forceinline__ float round_dt(float v, int dt) {
   return v;
 }
 
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+// Sum over the 8 lanes of an aligned lane group (every lane gets it).
+__device__ __forceinline__ double group8_sum_d(double v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
   return v;
 }
 
@@ -195,13 +198,15 @@ __device__ void load_tables(TqLds& t, const float* signs, const float* cb, const
 
 // Element offset of row r0 + r of a [B, H, Tc] row space inside a strided
 // [B, H, T, D] array whose token axis starts at t0, for the tile's rows.
+// The host keeps B * H * Tc below 2^31, so the row split is 32-bit.
 __device__ void row_offsets(int64_t* off, int64_t r0, int nr, int H, int Tc, int t0, int64_t sb,
                             int64_t sh, int64_t st) {
   const int r = threadIdx.x;
   if (r < nr) {
-    const int64_t row = r0 + r;
-    const int64_t t = row % Tc, bh = row / Tc, h = bh % H, b = bh / H;
-    off[r] = b * sb + h * sh + (t0 + t) * st;
+    const uint32_t row = static_cast<uint32_t>(r0 + r);
+    const uint32_t bh = row / static_cast<uint32_t>(Tc), t = row - bh * static_cast<uint32_t>(Tc);
+    const uint32_t b = bh / static_cast<uint32_t>(H), h = bh - b * static_cast<uint32_t>(H);
+    off[r] = static_cast<int64_t>(b) * sb + static_cast<int64_t>(h) * sh + (t0 + static_cast<int64_t>(t)) * st;
   }
 }
 
@@ -215,7 +220,7 @@ __global__ void __launch_bounds__(kThreads) tq_encode_kernel(TqEncodeArgs a) {
   __shared__ float den_s[kRows];
   __shared__ int64_t roff[kRows];
   __shared__ TqLds tb;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int64_t rows = static_cast<int64_t>(a.B) * a.H * a.Tc, total = rows * D;
   const bool keys = a.St != nullptr;
   const int nb = a.nc - 1;
@@ -231,16 +236,18 @@ __global__ void __launch_bounds__(kThreads) tq_encode_kernel(TqEncodeArgs a) {
       y[e] = r < nr ? load_f32(a.x, a.dtype, roff[r] + i) : 0.0f;
     }
     __syncthreads();
-    // 2. norm in T: T(sqrt(T(sum T(x_i^2)))), the divisor T(norm + T(1e-8))
-    for (int r = wave; r < kRows; r += kThreads / 64) {
+    // 2. norm in T: T(sqrt(T(sum T(x_i^2)))), the divisor T(norm + T(1e-8));
+    //    eight lanes per row, double sums
+    {
+      const int r = tid >> 3, part = tid & 7;
       double s = 0.0;
-      for (int i = lane; i < D; i += 64) {
+      for (int i = part; i < D; i += 8) {
         const float v = y[r * D + i];
         s += static_cast<double>(round_dt(v * v, a.dtype));
       }
-      s = wave_sum_d(s);
+      s = group8_sum_d(s);
       const float nrm = round_dt(sqrtf(round_dt(static_cast<float>(s), a.dtype)), a.dtype);
-      if (lane == 0) {
+      if (part == 0) {
         den_s[r] = round_dt(nrm + round_dt(1e-8f, a.dtype), a.dtype);
         if (r < nr) a.vec_norms[r0 + r] = f16_of(nrm);
       }
@@ -263,14 +270,15 @@ __global__ void __launch_bounds__(kThreads) tq_encode_kernel(TqEncodeArgs a) {
     __syncthreads();
     if (keys) {
       // 5. residual norm: f32(sum f32(r_i^2)) -> sqrt -> f16
-      for (int r = wave; r < nr; r += kThreads / 64) {
+      {
+        const int r = tid >> 3, part = tid & 7;
         double s = 0.0;
-        for (int i = lane; i < D; i += 64) {
+        for (int i = part; i < D; i += 8) {
           const float v = y[r * D + i];
           s += static_cast<double>(v * v);
         }
-        s = wave_sum_d(s);
-        if (lane == 0) a.res_norms[r0 + r] = f16_of(sqrtf(static_cast<float>(s)));
+        s = group8_sum_d(s);
+        if (part == 0 && r < nr) a.res_norms[r0 + r] = f16_of(sqrtf(static_cast<float>(s)));
       }
       // 6. projection through S (S^T as the right operand), signs p >= 0
       tile_matmul<DT, false>(y, nullptr, nr, D, a.St,
@@ -389,6 +397,7 @@ int grid_for(int64_t rows) {
 void launch_tq_encode(const TqEncodeArgs& a, hipStream_t st) {
   const int64_t rows = static_cast<int64_t>(a.B) * a.H * a.Tc;
   if (rows <= 0) return;
+  VKV_CHECK(rows < (int64_t{1} << 31), "TurboQuant encodes fewer than 2^31 vectors per call");
   VKV_CHECK(a.D >= 2 && a.D <= 256, "TurboQuant head dims must be in [2, 256]");
   VKV_CHECK(a.bits >= 1 && a.bits <= 8, "TurboQuant index bits must be in [1, 8]");
   const size_t lds = static_cast<size_t>(kRows) * a.D * (4 + 1 + 1);
@@ -408,6 +417,7 @@ void launch_tq_encode(const TqEncodeArgs& a, hipStream_t st) {
 void launch_tq_decode(const TqDecodeArgs& a, hipStream_t st) {
   const int64_t rows = static_cast<int64_t>(a.B) * a.H * a.Tc;
   if (rows <= 0) return;
+  VKV_CHECK(rows < (int64_t{1} << 31), "TurboQuant decodes fewer than 2^31 vectors per call");
   VKV_CHECK(a.D >= 2 && a.D <= 256, "TurboQuant head dims must be in [2, 256]");
   VKV_CHECK(a.bits >= 1 && a.bits <= 8, "TurboQuant index bits must be in [1, 8]");
   const size_t lds = static_cast<size_t>(kRows) * a.D * (4 + 1 + 1);
