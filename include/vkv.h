@@ -652,6 +652,24 @@ int vkv_array_copy(const vkv_array *src, vkv_array *dst, void *stream);
  * when no captured graph that used the stream will be replayed again. */
 int vkv_workspace_release(void *stream, int64_t *bytes);
 
+/* ------------------------------------------------------- dispatch options */
+
+/* Process-wide dispatch options, with no counterpart in the reference (a
+ * tuning and testing aid): GENERIC_ATTENTION (0/1) sends every attention
+ * call to the generic VALU kernel; DECODE_WAVES (0 = choose per launch)
+ * sets the paged decode kernel's wave count; MLA_SPLITS (0 = choose) sets
+ * the MLA kernel's token splits.  Initial values come from the environment
+ * variables VKV_GENERIC_ATTENTION, VKV_DECODE_WAVES and VKV_MLA_SPLITS,
+ * read once; calls read the options, never the environment. */
+enum {
+  VKV_OPTION_GENERIC_ATTENTION = 0,
+  VKV_OPTION_DECODE_WAVES = 1,
+  VKV_OPTION_MLA_SPLITS = 2,
+  VKV_OPTION_COUNT = 3
+};
+int vkv_set_option(int32_t which, int64_t value);
+int vkv_get_option(int32_t which, int64_t *value);
+
 /* ------------------------------------------------------- kernel timing */
 
 /* Kernel timing, a measurement aid with no counterpart in the reference:

@@ -4,6 +4,7 @@ import numpy as np
 import torch
 
 import oracle as O
+import vkv
 
 TORCH = {O.F32: torch.float32, O.F16: torch.float16, O.BF16: torch.bfloat16}
 
@@ -88,3 +89,19 @@ def assert_within(got, ref, tol, ctx="", wb=None):
 def assert_qclose(got, ref, wb, dtype, ctx=""):
     """assert_within against the reference-rounded oracle (qattn_tol)."""
     assert_within(got, ref, qattn_tol(dtype, ref, wb), ctx, wb)
+
+
+class _Options:
+    """The library's dispatch options as attributes, so that
+    monkeypatch.setattr(OPTIONS, "generic_attention", 1) sets one for a
+    test and restores it at teardown."""
+
+    def __getattr__(self, name):
+        return vkv.get_option(name)
+
+    def __setattr__(self, name, value):
+        vkv.set_option(name, value)
+
+
+OPTIONS = _Options()
+

@@ -5,7 +5,6 @@ the paged append: mixed lengths, ragged last tiles, empty sequences, head
 counts that are not multiples of 16, forced single and many token splits,
 and the restart taken when a later score exceeds the running max by more
 than the kernel's headroom."""
-import os
 
 import numpy as np
 import pytest
@@ -63,18 +62,14 @@ class Latent:
 
 
 def run(L, q, scale, splits=None, with_lens=True):
-    old = os.environ.get("VKV_MLA_SPLITS")
+    old = vkv.get_option("mla_splits")
     try:
         if splits is not None:
-            os.environ["VKV_MLA_SPLITS"] = str(splits)
+            vkv.set_option("mla_splits", splits)
         out = vkv.mla_decode(dev(q, O.BF16), L.view(with_lens), scale)
         torch.cuda.synchronize()
     finally:
-        if splits is not None:
-            if old is None:
-                del os.environ["VKV_MLA_SPLITS"]
-            else:
-                os.environ["VKV_MLA_SPLITS"] = old
+        vkv.set_option("mla_splits", old)
     return values(out, O.BF16)
 
 

@@ -9,7 +9,7 @@ import torch
 import mlx_random as mr
 import oracle as O
 import vkv
-from gpu_util import assert_qclose, assert_within, qattn_tol, qref, attn_tol, dev, host, rand_bits, values
+from gpu_util import OPTIONS, assert_qclose, assert_within, qattn_tol, qref, attn_tol, dev, host, rand_bits, values
 
 pytestmark = pytest.mark.gpu
 
@@ -124,7 +124,7 @@ def test_sdpa_decode_one_token(dtype, Hq, Hkv, D, mask, monkeypatch):
     assert (np.abs(got - ref) <= attn_tol(dtype, ref)).all()
     if mask == "bool":
         assert (got[1, 2, 0] == 0).all()
-    monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
+    monkeypatch.setattr(OPTIONS, "generic_attention", 1)
     gen = values(vkv.scaled_dot_product_attention(dev(q, dtype), k_dev, v_dev, scale, mask=m_dev),
                  dtype)
     assert (np.abs(got - gen) <= attn_tol(dtype, ref)).all()
@@ -210,7 +210,7 @@ def test_sdpa_sinks(path, dtype, monkeypatch):
     else:
         m_dev = m_ref = "causal"
     if path == "generic":
-        monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
+        monkeypatch.setattr(OPTIONS, "generic_attention", 1)
     if path == "router":
         c = vkv.KVCacheSimple()
         out = vkv.attention_with_cache_update(dev(q, dtype), dev(k, dtype), dev(v, dtype), c, scale,
@@ -246,7 +246,7 @@ def test_sdpa_additive_mask_in_query_dtype(generic, monkeypatch):
     empties the row (zeros); with bf16 queries a bf16 mask of -1e9 stays
     finite, the fp32 scores collapse to -1e9 and the row averages V."""
     if generic:
-        monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
+        monkeypatch.setattr(OPTIONS, "generic_attention", 1)
     rng = np.random.default_rng(70)
     B, Hq, Hkv, T, D = 1, 4, 2, 300, 64
     for dtype, mdt in ((O.F16, np.float32), (O.BF16, None)):

@@ -10,7 +10,7 @@ import torch
 
 import oracle as O
 import vkv
-from gpu_util import assert_qclose, assert_within, qattn_tol, qref, attn_tol, dev, host, rand_bits, values
+from gpu_util import OPTIONS, assert_qclose, assert_within, qattn_tol, qref, attn_tol, dev, host, rand_bits, values
 
 pytestmark = pytest.mark.gpu
 
@@ -220,7 +220,7 @@ def test_generic_and_matrix_core_paths_agree(monkeypatch):
     view = P.view()
     q = dev(rand_bits(rng, (len(P.lens), 32, 128), dtype), dtype)
     fast = values(vkv.paged_attention(q, view, 0.088), dtype)
-    monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
+    monkeypatch.setattr(OPTIONS, "generic_attention", 1)
     slow = values(vkv.paged_attention(q, view, 0.088), dtype)
     assert np.abs(fast - slow).max() <= 2e-2
 
@@ -238,7 +238,7 @@ def test_decode_wave_counts_agree(monkeypatch, waves):
     view = P.view()
     q = dev(rand_bits(rng, (len(P.lens), 32, 128), dtype), dtype)
     base = values(vkv.paged_attention(q, view, 0.088), dtype)
-    monkeypatch.setenv("VKV_DECODE_WAVES", waves)
+    monkeypatch.setattr(OPTIONS, "decode_waves", int(waves))
     got = values(vkv.paged_attention(q, view, 0.088), dtype)
     for _ in range(2):
         again = values(vkv.paged_attention(q, view, 0.088), dtype)

@@ -1,7 +1,7 @@
 """GPU parity of multi-query attention (L >= 2 query tokens: chunked prefill)
 over dense bf16 / f16 K/V with no or a causal mask, the matrix-core path of
 vkv_sdpa (vkv_prefill.hip), against the oracle's SDPA and against the
-generic kernel (VKV_GENERIC_ATTENTION=1): GQA groups of 1, 4 and 8, key
+generic kernel (the generic_attention option): GQA groups of 1, 4 and 8, key
 counts that are not multiples of the 32-token tile, query counts that are
 not multiples of the 256-row block, several key splits, strided slices of
 cache buffers and two batch rows.  Quantized K/V (a QuantizedKVCache's
@@ -13,7 +13,7 @@ import torch
 
 import oracle as O
 import vkv
-from gpu_util import assert_qclose, assert_within, qattn_tol, qref, attn_tol, dev, rand_bits, values
+from gpu_util import OPTIONS, assert_qclose, assert_within, qattn_tol, qref, attn_tol, dev, rand_bits, values
 
 pytestmark = pytest.mark.gpu
 
@@ -38,10 +38,10 @@ def run_case(rng, dtype, B, Hq, Hkv, L, T, mask, cap=None, monkeypatch=None, sca
     bad = np.abs(got - ref) > attn_tol(dtype, ref)
     assert not bad.any(), (np.abs(got - ref).max(), np.argwhere(bad)[:4])
     if monkeypatch is not None:
-        monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
+        monkeypatch.setattr(OPTIONS, "generic_attention", 1)
         gen = values(vkv.scaled_dot_product_attention(dev(q, dtype), kd, vd, scale, mask=mask),
                      dtype)
-        monkeypatch.delenv("VKV_GENERIC_ATTENTION")
+        monkeypatch.setattr(OPTIONS, "generic_attention", 0)
         assert (np.abs(got - gen) <= attn_tol(dtype, ref)).all()
 
 
@@ -112,7 +112,7 @@ def test_quantized_cache_chunk(bits, monkeypatch):
                    mask="causal", rounding=O.REF_CHUNK)
     tol = qattn_tol(dtype, ref, wb)
     assert_within(got, ref, tol, "oracle", wb)
-    monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
+    monkeypatch.setattr(OPTIONS, "generic_attention", 1)
     gen = step()
     assert_within(got, gen, attn_tol(dtype, ref) + 2 * wb, "generic", wb)
 
@@ -159,5 +159,5 @@ def test_quantized_sdpa_reference_layout_chunk(bits, L, mask, monkeypatch):
                    mask=mask, rounding=O.REF_CHUNK)
     tol = qattn_tol(dtype, ref, wb)
     assert_within(got, ref, tol, "oracle", wb)
-    monkeypatch.setenv("VKV_GENERIC_ATTENTION", "1")
+    monkeypatch.setattr(OPTIONS, "generic_attention", 1)
     assert_within(got, run(), attn_tol(dtype, ref) + 2 * wb, "generic", wb)

@@ -5,6 +5,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <string>
 #include <vector>
@@ -76,6 +77,28 @@ int32_t choose_parts(int64_t rows_x_heads, int64_t max_len, int32_t* part_tokens
 
 constexpr int kGatherPrefillMinL = 16;
 
+// Dispatch options (vkv_set_option): process-wide, read with relaxed loads on
+// the hot path.  The environment variables of the same names give their
+// initial values, read once.
+struct Options {
+  std::atomic<int64_t> v[VKV_OPTION_COUNT];
+  Options() {
+    const char* names[VKV_OPTION_COUNT] = {"VKV_GENERIC_ATTENTION", "VKV_DECODE_WAVES",
+                                           "VKV_MLA_SPLITS"};
+    for (int i = 0; i < VKV_OPTION_COUNT; i++) {
+      const char* e = getenv(names[i]);
+      int64_t x = 0;
+      if (e) x = i == VKV_OPTION_GENERIC_ATTENTION ? 1 : std::max(1, atoi(e));
+      v[i].store(x, std::memory_order_relaxed);
+    }
+  }
+};
+Options& options() {
+  static Options o;
+  return o;
+}
+int64_t option(int which) { return options().v[which].load(std::memory_order_relaxed); }
+
 // Split-K scratch: the per-stream workspace, or (noalloc) the fixed device
 // array of the no-allocation entry point.
 float* workspace(hipStream_t st, size_t floats, bool noalloc) {
@@ -84,7 +107,7 @@ float* workspace(hipStream_t st, size_t floats, bool noalloc) {
 
 void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64_t rows,
                    int64_t max_len, hipStream_t st, bool noalloc = false) {
-  if (fdecode_supported(dtype, bits, qsem, a) && !getenv("VKV_GENERIC_ATTENTION")) {
+  if (fdecode_supported(dtype, bits, qsem, a) && !option(VKV_OPTION_GENERIC_ATTENTION)) {
     a.n_parts = fdecode_parts(rows * a.Hkv, max_len, &a.part_tokens);
     if (a.n_parts > 1) {
       const size_t per = static_cast<size_t>(rows) * a.Hq * a.n_parts;
@@ -102,7 +125,7 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
   // which keeps the dequantized values unrounded (fp32) as the quantized
   // matmul of the oracle does.
   if ((bits > 0 || a.kv.table) && !a.kv.seq_lens && a.L >= kGatherPrefillMinL && a.kv.T > 0 &&
-      !getenv("VKV_GENERIC_ATTENTION")) {
+      !option(VKV_OPTION_GENERIC_ATTENTION)) {
     AttnArgs d = a;
     const int64_t batch = rows / a.L, T = a.kv.T;
     const int64_t es = elem_bytes(dtype);
@@ -142,7 +165,7 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
       return;
     }
   }
-  if (prefill_supported(dtype, bits, a) && !getenv("VKV_GENERIC_ATTENTION")) {
+  if (prefill_supported(dtype, bits, a) && !option(VKV_OPTION_GENERIC_ATTENTION)) {
     const int64_t batch = rows / a.L;
     a.n_parts = prefill_parts(batch, a.Hkv, a.L, a.Hq / a.Hkv, a.kv.T, &a.part_tokens);
     if (a.n_parts > 1) {
@@ -437,7 +460,7 @@ void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_a
                          (reinterpret_cast<uintptr_t>(out->data) % 8 == 0) &&
                          out->strides[0] % 4 == 0 && out->strides[1] % 4 == 0;
     if (kv->bits > 0 && !keys_only && aligned && kv->max_len <= qdecode_max_len() &&
-        !getenv("VKV_GENERIC_ATTENTION") &&
+        !option(VKV_OPTION_GENERIC_ATTENTION) &&
         qdecode_supported(kv->dtype, kv->bits, kv->head_dim, kv->block_size, rep, kv->group_size)) {
       // matrix-core path (vkv_decode.hip)
       KVSrc src = kvsrc_from_view(*kv);
@@ -464,8 +487,7 @@ void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_a
       d.Hkv = kv->n_kv_heads;
       d.rep = rep;
       d.n_seqs = kv->n_seqs;
-      int want = 0;
-      if (const char* e = getenv("VKV_DECODE_WAVES")) want = std::max(1, atoi(e));
+      const int want = static_cast<int>(option(VKV_OPTION_DECODE_WAVES));
       d.n_waves = want;  // 0 = choose per launch
       const int chunk = std::min(kv->n_seqs, qdecode_max_seqs());
       const int w_max = qdecode_waves(chunk, kv->n_kv_heads, rep, kv->max_len, want);
@@ -630,7 +652,7 @@ int vkv_mla_decode(const vkv_array* q, const vkv_paged_view* kv, float scale, vk
     const bool aligned = (reinterpret_cast<uintptr_t>(q->data) % 16 == 0) &&
                          q->strides[0] % 8 == 0 && q->strides[1] % 8 == 0;
     // (the matrix-core kernel takes the max of the raw scores, so scale > 0)
-    if (!aligned || !(scale > 0.0f) || getenv("VKV_GENERIC_ATTENTION") ||
+    if (!aligned || !(scale > 0.0f) || option(VKV_OPTION_GENERIC_ATTENTION) ||
         !mla_supported(kv->dtype, kv->bits, kv->group_size, kv->head_dim, kv->v_head_dim,
                        kv->n_kv_heads, kv->block_size)) {
       // other latent geometries run on the generic paged kernel
@@ -662,8 +684,7 @@ int vkv_mla_decode(const vkv_array* q, const vkv_paged_view* kv, float scale, vk
     m.H = static_cast<int32_t>(q->shape[1]);
     m.n_seqs = kv->n_seqs;
     if (m.H < 1 || m.n_seqs < 1) return;
-    int want = 0;
-    if (const char* e = getenv("VKV_MLA_SPLITS")) want = std::max(1, atoi(e));
+    const int want = static_cast<int>(option(VKV_OPTION_MLA_SPLITS));
     const size_t ws = mla_plan(m, want);
     if (ws) m.ws_o = reinterpret_cast<uint16_t*>(attention_workspace(S(stream), ws));
     launch_mla(m, S(stream));
@@ -831,6 +852,22 @@ int vkv_cache_make_mask(vkv_cache cache, int32_t n, int32_t window, int32_t retu
     vkv_array m{};
     *mode = cache->impl->make_mask(n, window, return_array != 0, S(stream), &m);
     if (mask) *mask = m;
+  });
+}
+
+int vkv_set_option(int32_t which, int64_t value) {
+  return guard([&] {
+    if (which < 0 || which >= VKV_OPTION_COUNT) throw Error("unknown option");
+    if (value < 0) throw Error("option values must be >= 0");
+    options().v[which].store(value, std::memory_order_relaxed);
+  });
+}
+
+int vkv_get_option(int32_t which, int64_t* value) {
+  return guard([&] {
+    if (which < 0 || which >= VKV_OPTION_COUNT) throw Error("unknown option");
+    need(value, "value");
+    *value = option(which);
   });
 }
 

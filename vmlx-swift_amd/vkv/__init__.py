@@ -103,7 +103,7 @@ EXPORTS = (
     "vkv_batch_causal_mask", "vkv_turboquant_create", "vkv_turboquant_from_simple",
     "vkv_turboquant_has_compressible_middle", "vkv_turboquant_info", "vkv_turboquant_encoded",
     "vkv_turboquant_window", "vkv_turboquant_restore_compressed",
-    "vkv_turboquant_restore_decoded", "vkv_tq_tables",
+    "vkv_turboquant_restore_decoded", "vkv_tq_tables", "vkv_set_option", "vkv_get_option",
 )
 TIME_DECODE, TIME_MLA, TIME_FDECODE, TIME_TQ_ENCODE, TIME_TQ_DECODE = 0, 1, 2, 3, 4
 
@@ -182,6 +182,21 @@ def to_torch(a: Array, stream=None):
 
 
 # ------------------------------------------------------------------- ops
+OPTIONS = {"generic_attention": 0, "decode_waves": 1, "mla_splits": 2}
+
+
+def set_option(name: str, value: int):
+    """vkv_set_option: process-wide dispatch options (generic_attention,
+    decode_waves, mla_splits)."""
+    _chk(lib().vkv_set_option(OPTIONS[name], C.c_int64(int(value))))
+
+
+def get_option(name: str) -> int:
+    v = C.c_int64()
+    _chk(lib().vkv_get_option(OPTIONS[name], C.byref(v)))
+    return v.value
+
+
 def batch_causal_mask(n: int, offsets, effective_key_lens=None, window_size=None, stream=None):
     """createBatchCausalMask(queryLen:offsets:effectiveKeyLens:windowSize:)
     (BatchEngine/BatchMask.swift:44-115): a bool tensor [B, 1, n, maxTotal]."""
