@@ -11,7 +11,7 @@ import torch
 import kvcache_ref as R
 import oracle as O
 import vkv
-from gpu_util import assert_qclose, assert_within, qattn_tol, qref, attn_tol, dev, host, rand_bits, values
+from gpu_util import OPTIONS, assert_qclose, assert_within, qattn_tol, qref, attn_tol, dev, host, rand_bits, values
 
 pytestmark = pytest.mark.gpu
 
@@ -171,3 +171,50 @@ def test_quantized_attention_over_pool_view_chunks():
                                       f(rk[2])[None], rv[0][None], f(rv[1])[None], f(rv[2])[None],
                                       D ** -0.5, 64, bits, mask="causal"))
         assert_qclose(out[s], ref, wb, dtype, f"sequence {s} (length {n})")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantized_chunk_over_ragged_pool_view_on_matrix_cores(bits, monkeypatch):
+    """A 20-token chunk per sequence over a paged pool with ragged lengths
+    (the continuous-batching prefill step): 16 or more query tokens take the
+    gather + matrix-core path with per-sequence lengths.  A sequence shorter
+    than the chunk leaves its first queries without a visible key, which the
+    reference's where(mask, s, finfo.min) turns into uniform weights (the
+    mean of V); against the oracle with the multi-token arithmetic
+    (REF_CHUNK) and against the generic kernel."""
+    dtype, D, Hkv, Hq, bs, L = O.BF16, 128, 2, 8, 32, 20
+    rng = np.random.default_rng(41 + bits)
+    lens = [300, 37, 5, 129, 20, 1000]
+    nb = sum((n + bs - 1) // bs for n in lens) + 1
+    pool = vkv.PagedPool(nb, bs, 1, Hkv, D, dtype=vkv.BF16, bits=bits)
+    perm = rng.permutation(np.arange(1, nb))
+    tables, slots, keys, vals, i = [], [], [], [], 0
+    for n in lens:
+        t = [int(x) for x in perm[i:i + (n + bs - 1) // bs]]
+        i += len(t)
+        tables.append(t)
+        slots += [t[p // bs] * bs + p % bs for p in range(n)]
+        keys.append(rand_bits(rng, (n, Hkv, D), dtype))
+        vals.append(rand_bits(rng, (n, Hkv, D), dtype))
+    pool.append(0, dev(np.concatenate(keys), dtype), dev(np.concatenate(vals), dtype),
+                torch.tensor(slots, dtype=torch.int32, device="cuda"))
+    tab = np.zeros((len(lens), max(len(t) for t in tables)), np.int32)
+    for s, t in enumerate(tables):
+        tab[s, :len(t)] = t
+    view = pool.view(0, torch.from_numpy(tab).cuda(),
+                     torch.tensor(lens, dtype=torch.int32, device="cuda"), max(lens))
+    q = rand_bits(rng, (len(lens), Hq, L, D), dtype)
+    run = lambda: values(vkv.quantized_paged_attention(dev(q, dtype), view, D ** -0.5,
+                                                       mask="causal"), dtype)
+    out = run()
+    monkeypatch.setattr(OPTIONS, "generic_attention", 1)
+    gen = run()
+    f = lambda a: O.to_f32(a, dtype)
+    for s, n in enumerate(lens):
+        rk = O.quantize(np.ascontiguousarray(keys[s].transpose(1, 0, 2)), dtype, 64, bits)
+        rv = O.quantize(np.ascontiguousarray(vals[s].transpose(1, 0, 2)), dtype, 64, bits)
+        ref, wb = (x[0] for x in qref(f(q[s])[None], dtype, rk[0][None], f(rk[1])[None],
+                                      f(rk[2])[None], rv[0][None], f(rv[1])[None], f(rv[2])[None],
+                                      D ** -0.5, 64, bits, mask="causal", rounding=O.REF_CHUNK))
+        assert_within(out[s], ref, qattn_tol(dtype, ref, wb), f"sequence {s} (length {n})", wb)
+        assert_within(out[s], gen[s], attn_tol(dtype, ref) + 2 * wb, f"generic, sequence {s}", wb)

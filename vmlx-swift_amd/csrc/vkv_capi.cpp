@@ -118,13 +118,13 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
     launch_fdecode(dtype, a, rows, st);
     return;
   }
-  // Quantized or paged K/V (a uniform length per row) with a chunk of query
-  // tokens: gather them to dense rows of the dtype (the dequantized values
-  // the reference's dequantize produces), then the matrix-core multi-query
-  // kernel on the copy.  Fewer query tokens stay on the generic kernel,
-  // which keeps the dequantized values unrounded (fp32) as the quantized
-  // matmul of the oracle does.
-  if ((bits > 0 || a.kv.table) && !a.kv.seq_lens && a.L >= kGatherPrefillMinL && a.kv.T > 0 &&
+  // Quantized or paged K/V with a chunk of query tokens (uniform or ragged
+  // lengths): gather them to dense rows of the dtype (the dequantized values
+  // the reference's dequantize produces; a ragged row fills its own length),
+  // then the matrix-core multi-query kernel on the copy.  Fewer query tokens
+  // stay on the generic kernel, which keeps the dequantized values
+  // unrounded (fp32) as the quantized matmul of the oracle does.
+  if ((bits > 0 || a.kv.table) && a.L >= kGatherPrefillMinL && a.kv.T > 0 &&
       !option(VKV_OPTION_GENERIC_ATTENTION)) {
     AttnArgs d = a;
     const int64_t batch = rows / a.L, T = a.kv.T;
@@ -132,6 +132,7 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
     const int64_t per_head = T * a.D * es, kv_bytes = batch * a.Hkv * per_head;
     d.kv = KVSrc{};
     d.kv.T = a.kv.T;
+    d.kv.seq_lens = a.kv.seq_lens;
     d.kv.kc = Comp{nullptr, a.Hkv * per_head, per_head, a.D * es};
     d.kv.vc = d.kv.kc;
     // a stand-in base with the copy's alignment decides support first

@@ -2,7 +2,9 @@
 // chunked prefill) over dense float K/V on gfx950 matrix cores.
 //
 // Semantics: MLXFast.scaledDotProductAttention with a causal or no mask
-// (MLXFast.swift:173-218; causal = query l of L sees keys 0 .. T - L + l),
+// (MLXFast.swift:173-218; causal = query l of L sees keys 0 .. T - L + l,
+// with T each row's own length when the rows are ragged: the chunk of a
+// continuous batch over a paged pool),
 // and quantizedScaledDotProductAttention (KVCache.swift:1909-1997) of the
 // quantized caches after their pages are gathered to bf16 (the dequantized
 // values the reference's dequantize produces).  Scores and the weighted sum
@@ -138,14 +140,21 @@ prefill_kernel(const AttnArgs a, int rep) {
   const int hk = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int L = a.L;
-  const int64_t T = a.kv.T;
+  // keys of this row of the batch: its own length when the rows are ragged
+  // (query l of a row of length T sees keys up to T - L + l when causal)
+  const int64_t T = a.kv.seq_lens ? min<int64_t>(a.kv.seq_lens[b], a.kv.T) : a.kv.T;
   const int64_t nrows = static_cast<int64_t>(L) * rep;  // query rows of (b, hk)
   const int64_t row0 = static_cast<int64_t>(rblk) * kRows;
   // keys of this workgroup: the part's range, and for a causal mask the
   // range its last position can see
   const int64_t rlast = min<int64_t>(nrows, row0 + kRows) - 1;
   int64_t k_end = min<int64_t>(T, static_cast<int64_t>(part + 1) * a.part_tokens);
-  if (a.mask_mode == 1) k_end = min<int64_t>(k_end, T - L + rlast / rep + 1);
+  // QSEM: a query that sees no key (a ragged row shorter than the chunk)
+  // has every score at T's lowest value in the reference (where(mask, s,
+  // finfo.min)), i.e. uniform weights over all of the row's keys; a
+  // workgroup holding such a query scans them all
+  const bool some_none = QSEM && a.mask_mode == 1 && T - L + row0 / rep < 0;
+  if (a.mask_mode == 1 && !some_none) k_end = min<int64_t>(k_end, T - L + rlast / rep + 1);
   const int64_t k_begin = static_cast<int64_t>(part) * a.part_tokens;
   const int ntiles = k_end > k_begin ? static_cast<int>((k_end - k_begin + kTok - 1) / kTok) : 0;
 
@@ -225,7 +234,7 @@ prefill_kernel(const AttnArgs a, int rep) {
       const uint32_t kdst = lds_addr(&kv[s][0][0]), vdst = lds_addr(&kv[s][1][0]);
 #pragma unroll
       for (int x = 0; x < 2; x++) {
-        // rows past the end repeat the last row (masked)
+        // rows past the end repeat the last row (masked); t0 < T here
         const int64_t t = min<int64_t>(t0 + lrow[x], T - 1) - t0;
         const uint32_t koff = static_cast<uint32_t>(t * kst) + 16 * kpiece[x];
         const uint32_t voff = static_cast<uint32_t>(t * vst) + 16 * vpiece[x];
@@ -300,7 +309,16 @@ prefill_kernel(const AttnArgs a, int rep) {
 #pragma unroll
           for (int j = 0; j < 16; j++) x[j] = round_to<DT>(x[j]);
         }
-        if (__builtin_amdgcn_ballot_w64(edge)) {
+        if (QSEM && some_none && __builtin_amdgcn_ballot_w64(kmax[rb] < 0)) {
+          // rows that see no key: equal scores (0) on the row's keys
+          const bool none = kmax[rb] < 0;
+          const int64_t lim = (none ? k_end - 1 : min<int64_t>(kmax[rb], k_end - 1)) - t0;
+#pragma unroll
+          for (int j = 0; j < 16; j++) {
+            if (none) x[j] = 0.0f;
+            if (8 * (j >> 2) + 4 * kg + (j & 3) > lim) x[j] = -INFINITY;
+          }
+        } else if (__builtin_amdgcn_ballot_w64(edge)) {
           const int64_t lim = min<int64_t>(kmax[rb], k_end - 1) - t0;
 #pragma unroll
           for (int j = 0; j < 16; j++)
@@ -396,11 +414,14 @@ prefill_kernel(const AttnArgs a, int rep) {
 }  // namespace
 
 bool prefill_supported(int dtype, int bits, const AttnArgs& a) {
-  if (bits != 0 || a.kv.table || a.kv.qfmt || a.kv.seq_lens) return false;
+  if (bits != 0 || a.kv.table || a.kv.qfmt) return false;
   if (dtype != kBF16 && dtype != kF16) return false;
   if (a.L < 2 || a.D != kD || a.Dv != kD || a.Hq % a.Hkv) return false;
   if (a.mask_mode != 0 && a.mask_mode != 1) return false;
-  if (a.mask_mode == 1 && a.L > a.kv.T) return false;
+  // uniform rows: a causal chunk longer than the keys is the generic
+  // kernel's; ragged rows (seq_lens) shorter than the chunk see no keys for
+  // their first queries, as there
+  if (a.mask_mode == 1 && !a.kv.seq_lens && a.L > a.kv.T) return false;
   // 16-byte loads of query rows and of K / V rows
   auto al = [](const void* p, int64_t s0, int64_t s1, int64_t s2) {
     return reinterpret_cast<uintptr_t>(p) % 16 == 0 && s0 % 16 == 0 && s1 % 16 == 0 && s2 % 16 == 0;
