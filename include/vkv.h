@@ -658,14 +658,17 @@ int vkv_workspace_release(void *stream, int64_t *bytes);
  * tuning and testing aid): GENERIC_ATTENTION (0/1) sends every attention
  * call to the generic VALU kernel; DECODE_WAVES (0 = choose per launch)
  * sets the paged decode kernel's wave count; MLA_SPLITS (0 = choose) sets
- * the MLA kernel's token splits.  Initial values come from the environment
- * variables VKV_GENERIC_ATTENTION, VKV_DECODE_WAVES and VKV_MLA_SPLITS,
- * read once; calls read the options, never the environment. */
+ * the MLA kernel's token splits; FDECODE_WAVES (0 = choose) the float
+ * decode kernel's target wave count.  Initial values come from the
+ * environment variables VKV_GENERIC_ATTENTION, VKV_DECODE_WAVES,
+ * VKV_MLA_SPLITS and VKV_FDECODE_WAVES, read once; calls read the options,
+ * never the environment. */
 enum {
   VKV_OPTION_GENERIC_ATTENTION = 0,
   VKV_OPTION_DECODE_WAVES = 1,
   VKV_OPTION_MLA_SPLITS = 2,
-  VKV_OPTION_COUNT = 3
+  VKV_OPTION_FDECODE_WAVES = 3, /* 0 = 2048: waves the float decode kernel aims for */
+  VKV_OPTION_COUNT = 4
 };
 int vkv_set_option(int32_t which, int64_t value);
 int vkv_get_option(int32_t which, int64_t *value);

@@ -84,7 +84,7 @@ struct Options {
   std::atomic<int64_t> v[VKV_OPTION_COUNT];
   Options() {
     const char* names[VKV_OPTION_COUNT] = {"VKV_GENERIC_ATTENTION", "VKV_DECODE_WAVES",
-                                           "VKV_MLA_SPLITS"};
+                                           "VKV_MLA_SPLITS", "VKV_FDECODE_WAVES"};
     for (int i = 0; i < VKV_OPTION_COUNT; i++) {
       const char* e = getenv(names[i]);
       int64_t x = 0;
@@ -108,7 +108,8 @@ float* workspace(hipStream_t st, size_t floats, bool noalloc) {
 void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64_t rows,
                    int64_t max_len, hipStream_t st, bool noalloc = false) {
   if (fdecode_supported(dtype, bits, qsem, a) && !option(VKV_OPTION_GENERIC_ATTENTION)) {
-    a.n_parts = fdecode_parts(rows * a.Hkv, max_len, &a.part_tokens);
+    a.n_parts = fdecode_parts(rows * a.Hkv, max_len, &a.part_tokens,
+                              static_cast<int>(option(VKV_OPTION_FDECODE_WAVES)));
     if (a.n_parts > 1) {
       const size_t per = static_cast<size_t>(rows) * a.Hq * a.n_parts;
       float* ws = workspace(st, per * (a.Dv + 2), noalloc);

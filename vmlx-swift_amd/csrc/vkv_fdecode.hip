@@ -277,9 +277,10 @@ bool fdecode_supported(int dtype, int bits, bool qsem, const AttnArgs& a) {
          al(a.kv.vc.ptr, a.kv.vc.sb, a.kv.vc.sh, a.kv.vc.st);
 }
 
-int fdecode_parts(int64_t rows_x_heads, int64_t T, int32_t* part_tokens) {
-  // about 2048 waves, kStep-token steps
-  int64_t parts = std::max<int64_t>(1, 2048 / std::max<int64_t>(1, rows_x_heads));
+int fdecode_parts(int64_t rows_x_heads, int64_t T, int32_t* part_tokens, int waves) {
+  // about `waves` (default 2048) waves, kStep-token steps
+  if (waves <= 0) waves = 2048;
+  int64_t parts = std::max<int64_t>(1, waves / std::max<int64_t>(1, rows_x_heads));
   parts = std::min<int64_t>(parts, std::max<int64_t>(1, (T + kStep - 1) / kStep));
   int64_t pt = (T + parts - 1) / parts;
   pt = std::max<int64_t>(kStep, (pt + kStep - 1) / kStep * kStep);

@@ -147,7 +147,7 @@ bool prefill_supported(int dtype, int bits, const AttnArgs& a);
 int prefill_parts(int64_t batch, int Hkv, int64_t L, int rep, int64_t T, int32_t* part_tokens);
 void launch_prefill(int dtype, bool qsem, const AttnArgs& a, int64_t batch, hipStream_t st);
 bool fdecode_supported(int dtype, int bits, bool qsem, const AttnArgs& a);
-int fdecode_parts(int64_t rows_x_heads, int64_t T, int32_t* part_tokens);
+int fdecode_parts(int64_t rows_x_heads, int64_t T, int32_t* part_tokens, int waves);
 void launch_fdecode(int dtype, const AttnArgs& a, int64_t rows, hipStream_t st);
 // MFMA decode attention over paged affine bf16 KV (vkv_decode.hip).
 struct DecodeArgs {
