@@ -13,18 +13,21 @@
 // attn_combine_kernel as sdpa_vector_2pass_2 merges them
 // (sdpa_vector.h:320-394).
 //
-// Work layout.  A workgroup of 4 waves (one per SIMD) owns a block of 128
-// query rows of one (row of the batch, kv head) and one key range; a query
-// row is one (query head of the group, position), position-major.  Wave w
-// owns rows 32w .. 32w + 31.  Two workgroups share a CU, so each SIMD runs
-// two waves of different workgroups, whose barriers are independent: one
-// wave's softmax overlaps the other's matrix-core work.  Per 32-token key
-// tile:
+// Work layout.  A workgroup of 8 waves (two per SIMD, one workgroup per
+// CU) owns a block of 256 query rows of one (row of the batch, kv head) and
+// one key range; a query row is one (query head of the group, position),
+// position-major.  Wave w owns rows 32w .. 32w + 31.  Each 32-token key tile
+// takes two phases separated by workgroup barriers: a matrix phase (the
+// scores of the tile, the P.V of the tile before) and a softmax phase.
+// Waves 4..7 run one phase behind waves 0..3, so the two waves of a SIMD are
+// always in different phases: one wave's MFMAs overlap the other's softmax
+// (ping-pong), and the wave in its matrix phase issues at the higher
+// priority.  Per tile:
 //   * K and V tiles (32 rows of D elements each) go HBM -> LDS with
-//     global_load_lds_dwordx4 two tiles ahead (each wave loads two 1 KB
-//     pieces of each); the per-lane source offsets
-//     place each 16-byte piece at its swizzled slot, so the tiles are
-//     bank-conflict free with no register staging;
+//     global_load_lds_dwordx4 two tiles ahead into four stages (each wave
+//     loads one 1 KB piece of each); the per-lane source offsets place each
+//     16-byte piece at its swizzled slot, so the tiles are bank-conflict
+//     free with no register staging;
 //   * scores S^T = K Q^T on v_mfma_f32_32x32x16 (A = key rows from LDS,
 //     B = the wave's queries, in registers): lane l holds query row l % 32
 //     of its block for tokens 8 (j / 4) + 4 (l / 32) + j % 4, j = 0..15;
@@ -68,16 +71,16 @@ constexpr int kD = 128;                // head dim (keys and values)
 constexpr int kTok = 32;               // tokens per key tile
 constexpr int kRowB = kD * 2;          // bytes per K / V row
 constexpr int kTileB = kTok * kRowB;   // bytes per K (or V) tile
-constexpr int kStages = 3;             // K+V tiles in LDS (two in flight); the tile loop is unrolled by it
-constexpr int kRows = 128;             // query rows per workgroup
-constexpr int kWaves = kRows / 32;     // one 32-row block per wave, one wave per SIMD;
-constexpr int kThreads = 64 * kWaves;  // two workgroups per CU
+constexpr int kStages = 4;             // K+V tiles in LDS; the tile loop is unrolled by it
+constexpr int kRows = 256;             // query rows per workgroup
+constexpr int kWaves = kRows / 32;     // one 32-row block per wave, two waves per SIMD
+constexpr int kThreads = 64 * kWaves;  // one workgroup per CU
 constexpr int kChunks = kD / 16;       // K steps of the score MFMA
 constexpr int kDB = kD / 32;           // 32-dim blocks of the output
 constexpr int kLoadsPerWave = 2 * kTileB / 1024 / kWaves;  // 16-byte-per-lane loads per wave per tile
 constexpr float kTau = 8.0f;           // rescale threshold (log2)
 constexpr float kLog2e = 1.4426950408889634f;
-static_assert(kLoadsPerWave == 4, "a wave loads two 1 KB pieces of the K tile and two of the V tile");
+static_assert(kLoadsPerWave == 2, "a wave loads one 1 KB piece of the K tile and one of the V tile");
 
 template <int... Is, class F>
 __device__ __forceinline__ void sfor_impl(std::integer_sequence<int, Is...>, F&& f) {
@@ -123,12 +126,39 @@ __device__ __forceinline__ void dma16(const uint8_t* base, uint32_t voff, uint32
                "s"(base)
                : "memory", "m0");
 }
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+// Before every barrier a wave waits for all of its tile loads but the last
+// tile's (kLoadsPerWave), and for its LDS reads.  The scheduling barriers
+// keep the compiler from moving any instruction from one phase into the
+// other.
+// A wave enters a matrix phase at issue priority 1 and a softmax phase at
+// 0, so that on a SIMD the MFMAs of the one wave issue back to back and the
+// softmax of the other fills the cycles between them.
+template <int PRIO>
+__device__ __forceinline__ void phase_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt vmcnt(2)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_s_setprio(PRIO);
+  __builtin_amdgcn_sched_barrier(0);
 }
-// At most one tile's loads (kLoadsPerWave) in flight.
-__device__ __forceinline__ void tile_wait_one() { asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); }
 __device__ __forceinline__ void tile_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// A value a phase produces is complete before the phase's closing barrier:
+// the compiler may otherwise move pure arithmetic (the exponentials, the
+// MFMAs) across the barrier into the other phase.
+__device__ __forceinline__ void pin(float v) { asm volatile("" ::"v"(v)); }
+__device__ __forceinline__ void pin(const u32x4_t& v) { asm volatile("" ::"v"(v)); }
+__device__ __forceinline__ void pin(const f32x16_t& v) { asm volatile("" ::"v"(v)); }
+// last visible key of a tile relative to its first, clamped to -1 .. kTok
+__device__ __forceinline__ int tile_limit(int64_t last) {
+  return static_cast<int>(last < -1 ? -1 : (last > kTok ? kTok : last));
+}
+// max of a value over the two 32-lane halves of the wave
+__device__ __forceinline__ float halves_max(float v) {
+  float lo = v, hi = v;
+  // lo's upper half <- hi's lower half: lo = the lower half's values in both
+  // halves, hi = the upper half's
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(lo), "+v"(hi));
+  return fmaxf(lo, hi);
+}
 
 // QSEM: the quantized-SDPA arithmetic (KVCache.swift:1909-1997): queries
 // times the scale rounded to the dtype, rounded again, instead of fp32 scores
@@ -140,6 +170,8 @@ prefill_kernel(const AttnArgs a, int rep) {
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // waves w and w + 4 share a SIMD; group 1 runs one phase behind group 0
+  const int grp = wave >> 2;
   const int lane = tid & 63, l32 = lane & 31, kg = lane >> 5;
   // workgroup id -> (kv head, part, row block, row of the batch), kv head
   // fastest: workgroups are dealt to the 8 XCDs in id order, so with 8 kv
@@ -171,6 +203,13 @@ prefill_kernel(const AttnArgs a, int rep) {
   if (a.mask_mode == 1 && !some_none) k_end = min<int64_t>(k_end, T - L + rlast / rep + 1);
   const int64_t k_begin = static_cast<int64_t>(part) * a.part_tokens;
   const int ntiles = k_end > k_begin ? static_cast<int>((k_end - k_begin + kTok - 1) / kTok) : 0;
+  // tiles that every row of the workgroup sees whole (no mask work)
+  int n_open = 0;
+  if (!some_none) {
+    const int64_t kmin = a.mask_mode == 1 ? T - L + row0 / rep : T - 1;
+    const int64_t open = min<int64_t>(kmin, k_end - 1) - k_begin + 1;
+    n_open = open > 0 ? static_cast<int>(min<int64_t>(open / kTok, ntiles)) : 0;
+  }
 
   // ---- this lane's query row and its queries: B operand of score step c
   // = dims 16c + 8 kg .. +8
@@ -220,34 +259,31 @@ prefill_kernel(const AttnArgs a, int rep) {
 
   if (ntiles > 0) {
     // ---- tile loads.  Load n (0..7) of a K or V tile fills its rows
-    // 4n .. 4n + 3; wave w issues loads w and w + 4 of each.  Lane lam of a load
-    // fills LDS slot lam % 16 of row 4n + lam / 16 with the row's piece
+    // 4n .. 4n + 3; wave w issues load w of each.  Lane lam of a load fills
+    // LDS slot lam % 16 of row 4n + lam / 16 with the row's piece
     // (lam % 16) ^ swizzle(row).
     const uint8_t* kbase = a.kv.kc.ptr + b * a.kv.kc.sb + hk * a.kv.kc.sh;
     const uint8_t* vbase = a.kv.vc.ptr + b * a.kv.vc.sb + hk * a.kv.vc.sh;
     const int64_t kst = a.kv.kc.st, vst = a.kv.vc.st;
-    // per-lane row and slot of this wave's loads (n = wave + kWaves x)
-    constexpr int kLx = kLoadsPerWave / 2;
-    int lrow[kLx], kpiece[kLx], vpiece[kLx];
-#pragma unroll
-    for (int x = 0; x < kLx; x++) {
-      lrow[x] = 4 * (wave + kWaves * x) + (lane >> 4);
-      kpiece[x] = (lane & 15) ^ (lrow[x] & 15);
-      vpiece[x] = (lane & 15) ^ (4 * (lrow[x] & 3));
-    }
+    const int lrow = 4 * wave + (lane >> 4);
+    const int kpiece = (lane & 15) ^ (lrow & 15), vpiece = (lane & 15) ^ (4 * (lrow & 3));
+    // offsets within a whole tile (T * stride < 2^31 is checked on the host)
+    const uint32_t koff_w = static_cast<uint32_t>(lrow * kst) + 16 * kpiece;
+    const uint32_t voff_w = static_cast<uint32_t>(lrow * vst) + 16 * vpiece;
     auto load_tile = [&](int i, int s) __attribute__((always_inline)) {
       const int ti = min(i, ntiles - 1);  // clamped: every wave issues the same loads
       const int64_t t0 = k_begin + static_cast<int64_t>(kTok) * ti;
-      const uint32_t kdst = lds_addr(&kv[s][0][0]), vdst = lds_addr(&kv[s][1][0]);
-#pragma unroll
-      for (int x = 0; x < kLx; x++) {
+      const uint32_t kdst = lds_addr(&kv[s][0][0]) + 1024 * wave;
+      const uint32_t vdst = lds_addr(&kv[s][1][0]) + 1024 * wave;
+      uint32_t koff = koff_w, voff = voff_w;
+      if (t0 + kTok > T) {
         // rows past the end repeat the last row (masked); t0 < T here
-        const int64_t t = min<int64_t>(t0 + lrow[x], T - 1) - t0;
-        const uint32_t koff = static_cast<uint32_t>(t * kst) + 16 * kpiece[x];
-        const uint32_t voff = static_cast<uint32_t>(t * vst) + 16 * vpiece[x];
-        dma16(kbase + t0 * kst, koff, kdst + 1024 * (wave + kWaves * x));
-        dma16(vbase + t0 * vst, voff, vdst + 1024 * (wave + kWaves * x));
+        const int t = min<int64_t>(lrow, T - 1 - t0);
+        koff = static_cast<uint32_t>(t * kst) + 16 * kpiece;
+        voff = static_cast<uint32_t>(t * vst) + 16 * vpiece;
       }
+      dma16(kbase + t0 * kst, koff, kdst);
+      dma16(vbase + t0 * vst, voff, vdst);
     };
 
     // ---- per-lane LDS addresses
@@ -262,52 +298,76 @@ prefill_kernel(const AttnArgs a, int rep) {
     const int vpc = 2 * (a4 & 1) + (jj >> 1);  // piece within the 4-piece group
     const int vx = 4 * (e4 & 3);               // swizzle of rows 4 (a4 / 2) + e (+ 8 hf + 16 ks)
 
-    load_tile(0, 0);
-    load_tile(1, 1);
-    // the loop is unrolled by the stage count, so every LDS address of a
-    // tile is a per-lane base plus an immediate offset
-    auto step = [&](int i, auto S_) __attribute__((always_inline)) {
-      constexpr int S = decltype(S_)::value;
-      tile_wait_one();  // tile i (this wave's loads)
-      lds_barrier();    // every wave's loads of tile i; stage (i + 2) % 3 free
-      load_tile(i + 2, (S + 2) % kStages);
-      const int64_t t0 = k_begin + static_cast<int64_t>(kTok) * i;
-      const uint32_t kb = ka + S * 2 * kTileB, vb = va + S * 2 * kTileB;
-
-      // -- scores
-      f32x16_t x = f32x16_t{};
-      u32x4_t kf[2];
-      kf[0] = *lds_ptr<const u32x4_t>(kb + 16 * ((kg) ^ kx));
-      sfor<kChunks>([&](auto C) {
-        constexpr int c = decltype(C)::value;
-        if constexpr (c + 1 < kChunks)
-          kf[(c + 1) & 1] = *lds_ptr<const u32x4_t>(kb + 16 * ((2 * (c + 1) + kg) ^ kx));
-        x = mfma<DT>(kf[c & 1], qf[c], x);
-      });
-
-      // -- value operands (independent of the softmax)
+    // QSEM: P carried as hi + lo (two operands of the dtype, ~16
+    // significant bits), so the weighted sum keeps fp32-like accuracy on
+    // large value channels; otherwise one operand
+    u32x4_t pb[2], pl[2];
+    f32x16_t x;
+    // the matrix phase: scores of the tile at LDS base kb (K rows) into x
+    // and, with PV, O^T += V^T P^T for the tile at LDS base vb (V rows).
+    // Every LDS read is issued before the first MFMA, so the MFMAs run
+    // back to back instead of each waiting for its operand's read.
+    auto matrix = [&](uint32_t kb, uint32_t vb, auto PV_) __attribute__((always_inline)) {
+      constexpr bool PV = decltype(PV_)::value;
+      u32x4_t kf[kChunks];
+#pragma unroll
+      for (int c = 0; c < kChunks; c++)
+        kf[c] = *lds_ptr<const u32x4_t>(kb + 16 * ((2 * c + kg) ^ kx));
       u32x4_t vf[kDB][2];
+      if constexpr (PV) {
 #pragma unroll
-      for (int db = 0; db < kDB; db++)
+        for (int db = 0; db < kDB; db++)
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-          // rows 16 ks + 8 hf + 4 (a4 / 2) + e (row & 3 = e): piece
-          // 4 db + vpc at slot (4 db + vpc) ^ 4e
-          const uint32_t slot = 16 * ((4 * db + vpc) ^ vx);
-          const uint32_t off0 = (16 * ks) * kRowB + slot;
-          const uint32_t off1 = (16 * ks + 8) * kRowB + slot;
-          const i16x4_t x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr<i16x4_t>(vb + off0));
-          const i16x4_t x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr<i16x4_t>(vb + off1));
-          const u32x2_t w0 = __builtin_bit_cast(u32x2_t, x0), w1 = __builtin_bit_cast(u32x2_t, x1);
-          vf[db][ks] = u32x4_t{w0[0], w0[1], w1[0], w1[1]};
-        }
-
-      // -- softmax of the row (keys past the range / causal limit masked)
-      const bool edge = t0 + kTok - 1 > kmax || t0 + kTok > k_end;
-      // QSEM: P carried as hi + lo (two operands of the dtype, ~16
-      // significant bits), so the weighted sum keeps fp32-like accuracy on
-      // large value channels; otherwise one operand
-      u32x4_t pb[2], pl[2];
+          for (int ks = 0; ks < 2; ks++) {
+            // rows 16 ks + 8 hf + 4 (a4 / 2) + e (row & 3 = e): piece
+            // 4 db + vpc at slot (4 db + vpc) ^ 4e
+            const uint32_t slot = 16 * ((4 * db + vpc) ^ vx);
+            const uint32_t off0 = (16 * ks) * kRowB + slot;
+            const uint32_t off1 = (16 * ks + 8) * kRowB + slot;
+            const i16x4_t x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr<i16x4_t>(vb + off0));
+            const i16x4_t x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr<i16x4_t>(vb + off1));
+            const u32x2_t w0 = __builtin_bit_cast(u32x2_t, x0), w1 = __builtin_bit_cast(u32x2_t, x1);
+            vf[db][ks] = u32x4_t{w0[0], w0[1], w1[0], w1[1]};
+          }
+      }
+      x = f32x16_t{};
+      if constexpr (PV) {
+        // the score chain (8 dependent MFMAs) interleaved with the P.V
+        // MFMAs (one chain per 32-dim block)
+        constexpr int kPv = (QSEM ? 4 : 2) * kDB;  // P.V MFMAs
+        constexpr int kPer = kPv / kChunks;       // per score MFMA
+        sfor<kChunks>([&](auto C) {
+          constexpr int c = decltype(C)::value;
+          x = mfma<DT>(kf[c], qf[c], x);
+          sfor<kPer>([&](auto J) {
+            constexpr int n = c * kPer + decltype(J)::value;  // n-th P.V MFMA
+            constexpr int db = n % kDB;
+            constexpr int q = n / kDB;  // QSEM: ks hi, ks lo; else ks
+            constexpr int ks = QSEM ? q / 2 : q;
+            if constexpr (QSEM && q % 2 == 1)
+              o[db] = mfma<DT>(vf[db][ks], pl[ks], o[db]);
+            else
+              o[db] = mfma<DT>(vf[db][ks], pb[ks], o[db]);
+          });
+        });
+        __builtin_amdgcn_sched_group_barrier(0x100, kChunks + 4 * kDB, 0);  // LDS reads
+        __builtin_amdgcn_sched_group_barrier(0x008, kChunks + kPv, 0);      // MFMAs
+#pragma unroll
+        for (int db = 0; db < kDB; db++) pin(o[db]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < kChunks; c++) x = mfma<DT>(kf[c], qf[c], x);
+        __builtin_amdgcn_sched_group_barrier(0x100, kChunks, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kChunks, 0);
+      }
+      pin(x);
+    };
+    // softmax of the row over tile i's scores x: the running max and sum,
+    // the rescale of o, and the P operands.  EDGE: keys past the range or
+    // the causal limit of some row are masked
+    auto softmax = [&](int i, auto EDGE_) __attribute__((always_inline)) {
+      constexpr bool EDGE = decltype(EDGE_)::value;
+      const int64_t t0 = k_begin + static_cast<int64_t>(kTok) * i;
       if constexpr (QSEM) {
         // the scores are stored in the dtype (quantizedMM returns T,
         // KVCache.swift:1945-1949) before the mask and the softmax: the
@@ -319,25 +379,27 @@ prefill_kernel(const AttnArgs a, int rep) {
           x[j + 1] = E::to_f32(static_cast<typename E::T>(w >> 16));
         }
       }
-      if (QSEM && some_none && __builtin_amdgcn_ballot_w64(kmax < 0)) {
-        // rows that see no key: equal scores (0) on the row's keys
-        const bool none = kmax < 0;
-        const int64_t lim = (none ? k_end - 1 : min<int64_t>(kmax, k_end - 1)) - t0;
+      if constexpr (EDGE) {
+        if (QSEM && some_none && __builtin_amdgcn_ballot_w64(kmax < 0)) {
+          // rows that see no key: equal scores (0) on the row's keys
+          const bool none = kmax < 0;
+          const int lim = tile_limit((none ? k_end - 1 : min<int64_t>(kmax, k_end - 1)) - t0);
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-          if (none) x[j] = 0.0f;
-          if (8 * (j >> 2) + 4 * kg + (j & 3) > lim) x[j] = -INFINITY;
+          for (int j = 0; j < 16; j++) {
+            if (none) x[j] = 0.0f;
+            if (8 * (j >> 2) + 4 * kg + (j & 3) > lim) x[j] = -INFINITY;
+          }
+        } else {
+          const int lim = tile_limit(min<int64_t>(kmax, k_end - 1) - t0);
+#pragma unroll
+          for (int j = 0; j < 16; j++)
+            if (8 * (j >> 2) + 4 * kg + (j & 3) > lim) x[j] = -INFINITY;
         }
-      } else if (__builtin_amdgcn_ballot_w64(edge)) {
-        const int64_t lim = min<int64_t>(kmax, k_end - 1) - t0;
-#pragma unroll
-        for (int j = 0; j < 16; j++)
-          if (8 * (j >> 2) + 4 * kg + (j & 3) > lim) x[j] = -INFINITY;
       }
       float mx = x[0];
 #pragma unroll
       for (int j = 1; j < 16; j++) mx = fmaxf(mx, x[j]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32)) * cl;  // scale > 0
+      mx = halves_max(mx) * cl;  // scale > 0
       if (__builtin_amdgcn_ballot_w64(mx > m_run + kTau)) {
         const float mn = fmaxf(m_run, mx);
         const float al = fast_exp2f(m_run - mn);
@@ -365,22 +427,62 @@ prefill_kernel(const AttnArgs a, int rep) {
           }
           pl[ks] = u32x4_t{pack2<DT>(r[0], r[1]), pack2<DT>(r[2], r[3]), pack2<DT>(r[4], r[5]),
                            pack2<DT>(r[6], r[7])};
+          pin(pl[ks]);
         }
+        pin(pb[ks]);
       }
-      // -- O^T += V^T P^T
-#pragma unroll
-      for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-        for (int db = 0; db < kDB; db++) {
-          o[db] = mfma<DT>(vf[db][ks], pb[ks], o[db]);
-          if constexpr (QSEM) o[db] = mfma<DT>(vf[db][ks], pl[ks], o[db]);
-        }
+      pin(l_run);
     };
-    for (int i = 0; i < ntiles; i += kStages) {
-      step(i, std::integral_constant<int, 0>{});
-      if (i + 1 < ntiles) step(i + 1, std::integral_constant<int, 1>{});
-      if (i + 2 < ntiles) step(i + 2, std::integral_constant<int, 2>{});
+
+    // ---- the tile loop, in two phases per tile separated by workgroup
+    // barriers: a matrix phase (loads of tile i + 2, scores of tile i,
+    // O += V P of tile i - 1) and a softmax phase (tile i).  Group 1 runs
+    // one phase behind group 0, so on each SIMD one wave's MFMAs overlap the
+    // other wave's softmax.  Tile i lives in stage i % 4: its K is read in
+    // the matrix phases of i, its V in those of i + 1 (the last read, by
+    // group 1, ends before the phase in which tile i + 4 is loaded over it).
+    // Tiles that every row sees whole run unrolled by the stage count, so
+    // every LDS address is a per-lane base plus an immediate offset; the
+    // rest (masked) run with the stage computed.
+    const uint32_t stage_b = 2 * kTileB;
+    load_tile(0, 0);
+    load_tile(1, 1);
+    phase_barrier<1>();
+    if (grp) phase_barrier<1>();
+    load_tile(2, 2);
+    matrix(ka, 0, std::false_type{});
+    phase_barrier<0>();
+    // softmax of tile i, then the matrix phase of tile i + 1
+    auto open_tile = [&](int i, auto S_) __attribute__((always_inline)) {
+      constexpr int S = decltype(S_)::value;
+      softmax(i, std::false_type{});
+      phase_barrier<1>();
+      load_tile(i + 3, (S + 3) % kStages);
+      // past the last tile this scores the clamped copy of the last tile
+      // (loaded and complete like any other): unused, but no branch
+      matrix(ka + ((S + 1) % kStages) * stage_b, va + S * stage_b, std::true_type{});
+      phase_barrier<0>();
+    };
+    int i = 0;
+    for (; i + kStages <= n_open; i += kStages) {
+      open_tile(i, std::integral_constant<int, 0>{});
+      open_tile(i + 1, std::integral_constant<int, 1>{});
+      open_tile(i + 2, std::integral_constant<int, 2>{});
+      open_tile(i + 3, std::integral_constant<int, 3>{});
     }
+    for (; i < ntiles; i++) {
+      const int s = i % kStages;
+      if (i < n_open)
+        softmax(i, std::false_type{});
+      else
+        softmax(i, std::true_type{});
+      phase_barrier<1>();
+      load_tile(i + 3, (s + 3) % kStages);
+      matrix(ka + ((s + 1) % kStages) * stage_b, va + s * stage_b, std::true_type{});
+      phase_barrier<0>();
+    }
+    // group 0 has one barrier fewer: it meets group 1's last one here
+    if (!grp) phase_barrier<0>();
     tile_wait_all();  // the clamped loads issued past the end
   }
 
@@ -453,8 +555,8 @@ bool prefill_supported(int dtype, int bits, const AttnArgs& a) {
 int prefill_parts(int64_t rows, int Hkv, int64_t L, int rep, int64_t T, int32_t* part_tokens) {
   const int64_t rblocks = (L * rep + kRows - 1) / kRows;
   const int64_t wgs = rows * Hkv * rblocks;  // rows = batch rows here
-  // two workgroups per CU
-  int64_t parts = std::max<int64_t>(1, 512 / std::max<int64_t>(1, wgs));
+  // one workgroup per CU
+  int64_t parts = std::max<int64_t>(1, 256 / std::max<int64_t>(1, wgs));
   parts = std::min<int64_t>(parts, std::max<int64_t>(1, (T + 255) / 256));
   int64_t pt = (T + parts - 1) / parts;
   pt = (pt + kTok - 1) / kTok * kTok;
