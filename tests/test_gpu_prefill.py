@@ -4,7 +4,8 @@ vkv_sdpa (vkv_prefill.hip), against the oracle's SDPA and against the
 generic kernel (the generic_attention option): GQA groups of 1, 4 and 8, key
 counts that are not multiples of the 32-token tile, query counts that are
 not multiples of the 256-row block, several key splits, strided slices of
-cache buffers and two batch rows.  Quantized K/V (a QuantizedKVCache's
+cache buffers and two batch rows; head dims 64, 128 and 256 (at 256 the two
+waves of a SIMD split the output dims).  Quantized K/V (a QuantizedKVCache's
 paged chunks, or reference-layout code/scale/bias arrays) with 16+ query
 tokens take the same kernel after a gather to bf16 rows."""
 import numpy as np
@@ -18,8 +19,7 @@ from gpu_util import OPTIONS, assert_qclose, assert_within, qattn_tol, qref, att
 pytestmark = pytest.mark.gpu
 
 
-def run_case(rng, dtype, B, Hq, Hkv, L, T, mask, cap=None, monkeypatch=None, scale=None):
-    D = 128
+def run_case(rng, dtype, B, Hq, Hkv, L, T, mask, cap=None, monkeypatch=None, scale=None, D=128):
     scale = D ** -0.5 if scale is None else scale
     q = rand_bits(rng, (B, Hq, L, D), dtype)
     k = rand_bits(rng, (B, Hkv, T, D), dtype)
@@ -78,11 +78,33 @@ def test_prefill_large_scores_rescale():
     run_case(rng, O.BF16, 1, 16, 4, 40, 600, "causal", scale=0.5)
 
 
-def quantized_chunk(rng, bits, outliers, T0=300, L=64, Hkv=8):
+@pytest.mark.parametrize("dtype", [O.BF16, O.F16])
+@pytest.mark.parametrize("mask", [None, "causal"])
+@pytest.mark.parametrize("D", [64, 256])
+def test_prefill_head_dims(dtype, mask, D, monkeypatch):
+    # Gemma-style 16 / 8 heads at 256 dims; 64 dims
+    rng = np.random.default_rng(dtype * 10 + D + (mask == "causal"))
+    run_case(rng, dtype, 1, 16, 8, 70, 301, mask, monkeypatch=monkeypatch, D=D)
+
+
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("L,T", [(2, 33), (300, 700)])
+def test_prefill_head_dims_lengths(D, L, T):
+    # two batch rows of cache-buffer slices; short and long chunks
+    rng = np.random.default_rng(D + L + T)
+    run_case(rng, O.BF16, 2, 8, 2, L, T, "causal", cap=T + 40, D=D)
+
+
+def test_prefill_256_long_keys_many_splits():
+    rng = np.random.default_rng(17)
+    run_case(rng, O.BF16, 1, 16, 8, 6, 3000, None, D=256)
+
+
+def quantized_chunk(rng, bits, outliers, T0=300, L=64, Hkv=8, D=128, rep=4):
     """An L-token causal chunk through the router over a QuantizedKVCache
-    holding a T0-token prefix (GQA 4): returns the output, the chunk's
+    holding a T0-token prefix (GQA rep): returns the output, the chunk's
     inputs and the whole (prefix + chunk) K/V."""
-    dtype, Hq, D = O.BF16, 4 * Hkv, 128
+    dtype, Hq = O.BF16, rep * Hkv
     k0, v0 = (rand_bits(rng, (1, Hkv, T0, D), dtype, outliers=outliers) for _ in range(2))
     k1, v1 = (rand_bits(rng, (1, Hkv, L, D), dtype, outliers=outliers) for _ in range(2))
     q = rand_bits(rng, (1, Hq, L, D), dtype)
@@ -112,6 +134,26 @@ def test_quantized_cache_chunk(bits, monkeypatch):
                    mask="causal", rounding=O.REF_CHUNK)
     tol = qattn_tol(dtype, ref, wb)
     assert_within(got, ref, tol, "oracle", wb)
+    monkeypatch.setattr(OPTIONS, "generic_attention", 1)
+    gen = step()
+    assert_within(got, gen, attn_tol(dtype, ref) + 2 * wb, "generic", wb)
+
+
+@pytest.mark.parametrize("D,bits,rep", [(256, 8, 2), (64, 4, 4)])
+def test_quantized_cache_chunk_head_dims(D, bits, rep, monkeypatch):
+    """A chunk over a QuantizedKVCache at 256 dims (config 4's 8-bit global
+    layer, 16 / 8 heads) and at 64 dims, against the oracle and the generic
+    path."""
+    dtype = O.BF16
+    step, q, kx, vx = quantized_chunk(np.random.default_rng(D + bits), bits, 0, T0=500, L=96,
+                                      Hkv=8, D=D, rep=rep)
+    got = step()
+    kq, ks, kb, _ = O.quantize(kx, dtype, 64, bits)
+    vq, vs, vb, _ = O.quantize(vx, dtype, 64, bits)
+    f = lambda a: O.to_f32(a, dtype)
+    ref, wb = qref(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64, bits,
+                   mask="causal", rounding=O.REF_CHUNK)
+    assert_qclose(got, ref, wb, dtype, f"D {D}")
     monkeypatch.setattr(OPTIONS, "generic_attention", 1)
     gen = step()
     assert_within(got, gen, attn_tol(dtype, ref) + 2 * wb, "generic", wb)

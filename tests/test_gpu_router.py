@@ -173,8 +173,8 @@ def test_quantized_attention_over_pool_view_chunks():
         assert_qclose(out[s], ref, wb, dtype, f"sequence {s} (length {n})")
 
 
-@pytest.mark.parametrize("bits", [4, 8])
-def test_quantized_chunk_over_ragged_pool_view_on_matrix_cores(bits, monkeypatch):
+@pytest.mark.parametrize("bits,D", [(4, 128), (8, 128), (8, 256)])
+def test_quantized_chunk_over_ragged_pool_view_on_matrix_cores(bits, D, monkeypatch):
     """A 20-token chunk per sequence over a paged pool with ragged lengths
     (the continuous-batching prefill step): 16 or more query tokens take the
     gather + matrix-core path with per-sequence lengths.  A sequence shorter
@@ -182,8 +182,8 @@ def test_quantized_chunk_over_ragged_pool_view_on_matrix_cores(bits, monkeypatch
     reference's where(mask, s, finfo.min) turns into uniform weights (the
     mean of V); against the oracle with the multi-token arithmetic
     (REF_CHUNK) and against the generic kernel."""
-    dtype, D, Hkv, Hq, bs, L = O.BF16, 128, 2, 8, 32, 20
-    rng = np.random.default_rng(41 + bits)
+    dtype, Hkv, Hq, bs, L = O.BF16, 2, 8, 32, 20
+    rng = np.random.default_rng(41 + bits + D)
     lens = [300, 37, 5, 129, 20, 1000]
     nb = sum((n + bs - 1) // bs for n in lens) + 1
     pool = vkv.PagedPool(nb, bs, 1, Hkv, D, dtype=vkv.BF16, bits=bits)

@@ -139,7 +139,7 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
     // a stand-in base with the copy's alignment decides support first
     d.kv.kc.ptr = d.kv.vc.ptr = reinterpret_cast<const uint8_t*>(uintptr_t{256});
     if (a.D == a.Dv && prefill_supported(dtype, 0, d)) {
-      d.n_parts = prefill_parts(batch, a.Hkv, a.L, a.Hq / a.Hkv, T, &d.part_tokens);
+      d.n_parts = prefill_parts(batch, a.Hkv, a.L, a.Hq / a.Hkv, T, a.D, &d.part_tokens);
       const size_t copy_floats = static_cast<size_t>((2 * kv_bytes + 255) / 256 * 64);
       const size_t per = static_cast<size_t>(rows) * a.Hq * d.n_parts;
       float* ws = workspace(st, copy_floats + (d.n_parts > 1 ? per * (a.Dv + 2) : 0), noalloc);
@@ -169,7 +169,7 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
   }
   if (prefill_supported(dtype, bits, a) && !option(VKV_OPTION_GENERIC_ATTENTION)) {
     const int64_t batch = rows / a.L;
-    a.n_parts = prefill_parts(batch, a.Hkv, a.L, a.Hq / a.Hkv, a.kv.T, &a.part_tokens);
+    a.n_parts = prefill_parts(batch, a.Hkv, a.L, a.Hq / a.Hkv, a.kv.T, a.D, &a.part_tokens);
     if (a.n_parts > 1) {
       const size_t per = static_cast<size_t>(rows) * a.Hq * a.n_parts;
       float* ws = workspace(st, per * (a.Dv + 2), noalloc);

@@ -144,7 +144,7 @@ void launch_attn_combine(int dtype, const AttnArgs& a, int64_t rows, hipStream_t
 // Multi-query attention (L >= 2) over dense bf16 / f16 K/V, D = 128, no or
 // causal mask, on matrix cores (vkv_prefill.hip).
 bool prefill_supported(int dtype, int bits, const AttnArgs& a);
-int prefill_parts(int64_t batch, int Hkv, int64_t L, int rep, int64_t T, int32_t* part_tokens);
+int prefill_parts(int64_t batch, int Hkv, int64_t L, int rep, int64_t T, int D, int32_t* part_tokens);
 void launch_prefill(int dtype, bool qsem, const AttnArgs& a, int64_t batch, hipStream_t st);
 bool fdecode_supported(int dtype, int bits, bool qsem, const AttnArgs& a);
 int fdecode_parts(int64_t rows_x_heads, int64_t T, int32_t* part_tokens, int waves);

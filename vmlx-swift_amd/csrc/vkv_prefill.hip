@@ -67,20 +67,47 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;
 
-constexpr int kD = 128;                // head dim (keys and values)
-constexpr int kTok = 32;               // tokens per key tile
-constexpr int kRowB = kD * 2;          // bytes per K / V row
-constexpr int kTileB = kTok * kRowB;   // bytes per K (or V) tile
-constexpr int kStages = 4;             // K+V tiles in LDS; the tile loop is unrolled by it
-constexpr int kRows = 256;             // query rows per workgroup
-constexpr int kWaves = kRows / 32;     // one 32-row block per wave, two waves per SIMD
-constexpr int kThreads = 64 * kWaves;  // one workgroup per CU
-constexpr int kChunks = kD / 16;       // K steps of the score MFMA
-constexpr int kDB = kD / 32;           // 32-dim blocks of the output
-constexpr int kLoadsPerWave = 2 * kTileB / 1024 / kWaves;  // 16-byte-per-lane loads per wave per tile
-constexpr float kTau = 8.0f;           // rescale threshold (log2)
+constexpr int kTok = 32;      // tokens per key tile
+constexpr int kStages = 4;    // K+V tiles in LDS; the open-tile loop is unrolled by it
+constexpr int kWaves = 8;     // two per SIMD, one workgroup per CU
+constexpr int kThreads = 64 * kWaves;
+constexpr float kTau = 8.0f;  // rescale threshold (log2)
 constexpr float kLog2e = 1.4426950408889634f;
-static_assert(kLoadsPerWave == 2, "a wave loads one 1 KB piece of the K tile and one of the V tile");
+
+// Layout for head dim D (keys and values).  Every wave owns 32 query rows.
+// Up to 128 dims a wave holds all D output dims, so a workgroup covers 8
+// row blocks; at 256 dims the two waves of a SIMD own the same 32 rows and
+// split the output dims (each computes the full scores), so a workgroup
+// covers 4 row blocks.
+template <int D>
+struct PfCfg {
+  static constexpr int kChunks = D / 16;            // K steps of the score MFMA
+  static constexpr int kSplit = D == 256 ? 2 : 1;   // waves sharing a row block
+  static constexpr int kDBw = D / 32 / kSplit;      // 32-dim output blocks per wave
+  static constexpr int kRB = kWaves / kSplit;       // row blocks per workgroup
+  static constexpr int kRows = 32 * kRB;            // query rows per workgroup
+  static constexpr int kRowB = 2 * D;               // bytes per K / V row
+  static constexpr int kTileB = kTok * kRowB;       // bytes per K (or V) tile
+  static constexpr int kSlots = D / 8;              // 16-byte pieces per row
+  static constexpr int kKLoads = kTileB / 1024;     // 1 KB loads of a K (or V) tile
+  static constexpr int kLoads = 2 * kKLoads / kWaves;  // 1 KB loads per wave per tile
+  static_assert(D == 64 || D == 128 || D == 256, "head dims 64, 128, 256");
+  static_assert(kLoads >= 1 && kLoads * kWaves == 2 * kKLoads, "loads split evenly");
+};
+// LDS slot of piece p of key row t is p ^ kswz(t): a score read of 16
+// consecutive rows at one piece hits 16 distinct 16-byte bank groups (rows
+// of 256 or 512 bytes: t & 15; of 128 bytes, where rows t and t + 1 already
+// differ by half the banks: (t / 2) & 7).
+template <int D>
+__device__ __forceinline__ int kswz(int t) {
+  return D == 64 ? (t >> 1) & 7 : t & 15;
+}
+// value rows: piece p at slot p ^ vswz(t & 3), for the transposing reads
+// (4 rows x 32 bytes per 16 lanes)
+template <int D>
+__device__ __forceinline__ int vswz(int t) {
+  return D == 64 ? 2 * ((t >> 1) & 1) : 4 * (t & 3);
+}
 
 template <int... Is, class F>
 __device__ __forceinline__ void sfor_impl(std::integer_sequence<int, Is...>, F&& f) {
@@ -127,16 +154,16 @@ __device__ __forceinline__ void dma16(const uint8_t* base, uint32_t voff, uint32
                : "memory", "m0");
 }
 // Before every barrier a wave waits for all of its tile loads but the last
-// tile's (kLoadsPerWave), and for its LDS reads.  The scheduling barriers
+// tile's (LOADS), and for its LDS reads.  The scheduling barriers
 // keep the compiler from moving any instruction from one phase into the
 // other.
 // A wave enters a matrix phase at issue priority 1 and a softmax phase at
 // 0, so that on a SIMD the MFMAs of the one wave issue back to back and the
 // softmax of the other fills the cycles between them.
-template <int PRIO>
+template <int PRIO, int LOADS>
 __device__ __forceinline__ void phase_barrier() {
   __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_waitcnt vmcnt(2)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(LOADS) : "memory");
   __builtin_amdgcn_s_setprio(PRIO);
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -163,15 +190,20 @@ __device__ __forceinline__ float halves_max(float v) {
 // QSEM: the quantized-SDPA arithmetic (KVCache.swift:1909-1997): queries
 // times the scale rounded to the dtype, rounded again, instead of fp32 scores
 // times the scale; scores rounded to the dtype before the softmax.
-template <int DT, bool QSEM>
+template <int DT, bool QSEM, int D>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 prefill_kernel(const AttnArgs a, int rep) {
+  using Cfg = PfCfg<D>;
+  constexpr int kChunks = Cfg::kChunks, kDBw = Cfg::kDBw, kRows = Cfg::kRows;
+  constexpr int kRowB = Cfg::kRowB, kTileB = Cfg::kTileB, kLoads = Cfg::kLoads;
   __shared__ __attribute__((aligned(16))) uint8_t kv[kStages][2][kTileB];  // [stage][K/V]
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // waves w and w + 4 share a SIMD; group 1 runs one phase behind group 0
   const int grp = wave >> 2;
+  // the wave's 32-row block and (at 256 dims) half of the output dims
+  const int rb = wave % Cfg::kRB, dh = wave / Cfg::kRB;
   const int lane = tid & 63, l32 = lane & 31, kg = lane >> 5;
   // workgroup id -> (kv head, part, row block, row of the batch), kv head
   // fastest: workgroups are dealt to the 8 XCDs in id order, so with 8 kv
@@ -214,7 +246,7 @@ prefill_kernel(const AttnArgs a, int rep) {
   // ---- this lane's query row and its queries: B operand of score step c
   // = dims 16c + 8 kg .. +8
   using E = Elem<DT>;
-  const int64_t qrow = row0 + 32 * wave + l32;
+  const int64_t qrow = row0 + 32 * rb + l32;
   int64_t kmax;  // last key the row may see
   u32x4_t qf[kChunks];
   {
@@ -243,7 +275,7 @@ prefill_kernel(const AttnArgs a, int rep) {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   const float cl = QSEM ? kLog2e : a.scale * kLog2e;
 
-  f32x16_t o[kDB];
+  f32x16_t o[kDBw];  // output dims 32 (dh kDBw + db) ..
   float m_run = -1e30f;  // finite: a masked score (-inf) gives p = 0
   float l_run = 0.f;
   // an attention sink (MLXFast semantics only) is one more logit with a
@@ -255,48 +287,62 @@ prefill_kernel(const AttnArgs a, int rep) {
     l_run = kg == 0 ? 1.f : 0.f;  // the two lane halves' sums are added at the end
   }
 #pragma unroll
-  for (int db = 0; db < kDB; db++) o[db] = f32x16_t{};
+  for (int db = 0; db < kDBw; db++) o[db] = f32x16_t{};
 
   if (ntiles > 0) {
-    // ---- tile loads.  Load n (0..7) of a K or V tile fills its rows
-    // 4n .. 4n + 3; wave w issues load w of each.  Lane lam of a load fills
-    // LDS slot lam % 16 of row 4n + lam / 16 with the row's piece
-    // (lam % 16) ^ swizzle(row).
+    // ---- tile loads.  A tile is 2 kKLoads loads of 1 KB (the K tile's,
+    // then the V tile's); wave w issues loads w + 8 x.  Lane lam of a load
+    // fills LDS slot lam % kSlots of its row (the load covers 1024 / kRowB
+    // consecutive rows) with the row's piece (lam % kSlots) ^ swizzle(row).
     const uint8_t* kbase = a.kv.kc.ptr + b * a.kv.kc.sb + hk * a.kv.kc.sh;
     const uint8_t* vbase = a.kv.vc.ptr + b * a.kv.vc.sb + hk * a.kv.vc.sh;
     const int64_t kst = a.kv.kc.st, vst = a.kv.vc.st;
-    const int lrow = 4 * wave + (lane >> 4);
-    const int kpiece = (lane & 15) ^ (lrow & 15), vpiece = (lane & 15) ^ (4 * (lrow & 3));
-    // offsets within a whole tile (T * stride < 2^31 is checked on the host)
-    const uint32_t koff_w = static_cast<uint32_t>(lrow * kst) + 16 * kpiece;
-    const uint32_t voff_w = static_cast<uint32_t>(lrow * vst) + 16 * vpiece;
+    // the lane's row and piece in load x (recomputed where needed: at 256
+    // dims four loads' worth would hold registers through the loop)
+    auto lrow = [&](int x) __attribute__((always_inline)) {
+      return ((wave + kWaves * x) % Cfg::kKLoads) * (1024 / kRowB) + lane / Cfg::kSlots;
+    };
+    auto lpiece = [&](int x) __attribute__((always_inline)) {
+      const int slot = lane % Cfg::kSlots, r = lrow(x);
+      return wave + kWaves * x >= Cfg::kKLoads ? slot ^ vswz<D>(r & 3) : slot ^ kswz<D>(r);
+    };
+    uint32_t loff[kLoads];  // offsets within a whole tile (T * stride < 2^31, host-checked)
+#pragma unroll
+    for (int x = 0; x < kLoads; x++) {
+      const bool is_v = wave + kWaves * x >= Cfg::kKLoads;  // wave-uniform
+      loff[x] = static_cast<uint32_t>(lrow(x) * (is_v ? vst : kst)) + 16 * lpiece(x);
+    }
     auto load_tile = [&](int i, int s) __attribute__((always_inline)) {
       const int ti = min(i, ntiles - 1);  // clamped: every wave issues the same loads
       const int64_t t0 = k_begin + static_cast<int64_t>(kTok) * ti;
-      const uint32_t kdst = lds_addr(&kv[s][0][0]) + 1024 * wave;
-      const uint32_t vdst = lds_addr(&kv[s][1][0]) + 1024 * wave;
-      uint32_t koff = koff_w, voff = voff_w;
-      if (t0 + kTok > T) {
-        // rows past the end repeat the last row (masked); t0 < T here
-        const int t = min<int64_t>(lrow, T - 1 - t0);
-        koff = static_cast<uint32_t>(t * kst) + 16 * kpiece;
-        voff = static_cast<uint32_t>(t * vst) + 16 * vpiece;
+#pragma unroll
+      for (int x = 0; x < kLoads; x++) {
+        const int n = wave + kWaves * x, pn = n % Cfg::kKLoads;
+        const bool is_v = n >= Cfg::kKLoads;
+        const int64_t st = is_v ? vst : kst;
+        uint32_t off = loff[x];
+        if (t0 + kTok > T) {
+          // rows past the end repeat the last row (masked); t0 < T here
+          const int t = min<int64_t>(lrow(x), T - 1 - t0);
+          off = static_cast<uint32_t>(t * st) + 16 * lpiece(x);
+        }
+        // wave-uniform (M0), which the compiler does not see through the select
+        const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_addr(&kv[s][is_v][0]) + 1024 * pn);
+        dma16((is_v ? vbase : kbase) + t0 * st, off, dst);
       }
-      dma16(kbase + t0 * kst, koff, kdst);
-      dma16(vbase + t0 * vst, voff, vdst);
     };
 
     // ---- per-lane LDS addresses
-    // score A operand, step c: K row l32, piece 2c + kg at slot (2c + kg) ^ (l32 & 15)
+    // score A operand, step c: K row l32, piece 2c + kg at slot (2c + kg) ^ kswz(l32)
     const uint32_t ka = lds_addr(&kv[0][0][0]) + l32 * kRowB;
-    const int kx = l32 & 15;
+    const int kx = kswz<D>(l32);
     // value A operand (dim block db, k-step ks, token half hf): lane
     // 16 a4 + 4 e + jj reads V row 16 ks + 8 hf + 4 (a4 / 2) + e, dims
     // 32 db + 16 (a4 % 2) + 4 jj .. +4 = piece 4 db + 2 (a4 % 2) + jj / 2
     const int a4 = lane >> 4, e4 = (lane >> 2) & 3, jj = lane & 3;
     const uint32_t va = lds_addr(&kv[0][1][0]) + (4 * (a4 >> 1) + e4) * kRowB + 8 * (jj & 1);
     const int vpc = 2 * (a4 & 1) + (jj >> 1);  // piece within the 4-piece group
-    const int vx = 4 * (e4 & 3);               // swizzle of rows 4 (a4 / 2) + e (+ 8 hf + 16 ks)
+    const int vx = vswz<D>(e4);                // swizzle of rows 4 (a4 / 2) + e (+ 8 hf + 16 ks)
 
     // QSEM: P carried as hi + lo (two operands of the dtype, ~16
     // significant bits), so the weighted sum keeps fp32-like accuracy on
@@ -313,15 +359,15 @@ prefill_kernel(const AttnArgs a, int rep) {
 #pragma unroll
       for (int c = 0; c < kChunks; c++)
         kf[c] = *lds_ptr<const u32x4_t>(kb + 16 * ((2 * c + kg) ^ kx));
-      u32x4_t vf[kDB][2];
+      u32x4_t vf[kDBw][2];
       if constexpr (PV) {
 #pragma unroll
-        for (int db = 0; db < kDB; db++)
+        for (int db = 0; db < kDBw; db++)
 #pragma unroll
           for (int ks = 0; ks < 2; ks++) {
             // rows 16 ks + 8 hf + 4 (a4 / 2) + e (row & 3 = e): piece
-            // 4 db + vpc at slot (4 db + vpc) ^ 4e
-            const uint32_t slot = 16 * ((4 * db + vpc) ^ vx);
+            // 4 gdb + vpc (gdb = the global dim block) at slot (4 gdb + vpc) ^ vswz(e)
+            const uint32_t slot = 16 * ((4 * (dh * kDBw + db) + vpc) ^ vx);
             const uint32_t off0 = (16 * ks) * kRowB + slot;
             const uint32_t off1 = (16 * ks + 8) * kRowB + slot;
             const i16x4_t x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_ptr<i16x4_t>(vb + off0));
@@ -334,31 +380,49 @@ prefill_kernel(const AttnArgs a, int rep) {
       if constexpr (PV) {
         // the score chain (8 dependent MFMAs) interleaved with the P.V
         // MFMAs (one chain per 32-dim block)
-        constexpr int kPv = (QSEM ? 4 : 2) * kDB;  // P.V MFMAs
-        constexpr int kPer = kPv / kChunks;       // per score MFMA
+        constexpr int kPv = (QSEM ? 4 : 2) * kDBw;  // P.V MFMAs
         sfor<kChunks>([&](auto C) {
           constexpr int c = decltype(C)::value;
           x = mfma<DT>(kf[c], qf[c], x);
-          sfor<kPer>([&](auto J) {
-            constexpr int n = c * kPer + decltype(J)::value;  // n-th P.V MFMA
-            constexpr int db = n % kDB;
-            constexpr int q = n / kDB;  // QSEM: ks hi, ks lo; else ks
-            constexpr int ks = QSEM ? q / 2 : q;
-            if constexpr (QSEM && q % 2 == 1)
-              o[db] = mfma<DT>(vf[db][ks], pl[ks], o[db]);
-            else
-              o[db] = mfma<DT>(vf[db][ks], pb[ks], o[db]);
+          // the P.V MFMAs spread evenly over the score steps
+          sfor<kPv>([&](auto J) {
+            constexpr int n = decltype(J)::value;  // n-th P.V MFMA
+            if constexpr (n >= c * kPv / kChunks && n < (c + 1) * kPv / kChunks) {
+              constexpr int db = n % kDBw;
+              constexpr int q = n / kDBw;  // QSEM: ks hi, ks lo; else ks
+              constexpr int ks = QSEM ? q / 2 : q;
+              if constexpr (QSEM && q % 2 == 1)
+                o[db] = mfma<DT>(vf[db][ks], pl[ks], o[db]);
+              else
+                o[db] = mfma<DT>(vf[db][ks], pb[ks], o[db]);
+            }
           });
         });
-        __builtin_amdgcn_sched_group_barrier(0x100, kChunks + 4 * kDB, 0);  // LDS reads
-        __builtin_amdgcn_sched_group_barrier(0x008, kChunks + kPv, 0);      // MFMAs
+        if constexpr (D <= 128) {
+          __builtin_amdgcn_sched_group_barrier(0x100, kChunks + 4 * kDBw, 0);  // LDS reads
+          __builtin_amdgcn_sched_group_barrier(0x008, kChunks + kPv, 0);       // MFMAs
+        } else {
+          // at 256 dims every read at once would not fit the registers:
+          // eight rounds of reads, each followed by its share of MFMAs
+          sfor<8>([&](auto) {
+            __builtin_amdgcn_sched_group_barrier(0x100, (kChunks + 4 * kDBw) / 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, (kChunks + kPv) / 8, 0);
+          });
+        }
 #pragma unroll
-        for (int db = 0; db < kDB; db++) pin(o[db]);
+        for (int db = 0; db < kDBw; db++) pin(o[db]);
       } else {
 #pragma unroll
         for (int c = 0; c < kChunks; c++) x = mfma<DT>(kf[c], qf[c], x);
-        __builtin_amdgcn_sched_group_barrier(0x100, kChunks, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, kChunks, 0);
+        if constexpr (D <= 128) {
+          __builtin_amdgcn_sched_group_barrier(0x100, kChunks, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, kChunks, 0);
+        } else {
+          sfor<4>([&](auto) {
+            __builtin_amdgcn_sched_group_barrier(0x100, kChunks / 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, kChunks / 4, 0);
+          });
+        }
       }
       pin(x);
     };
@@ -405,7 +469,7 @@ prefill_kernel(const AttnArgs a, int rep) {
         const float al = fast_exp2f(m_run - mn);
         l_run *= al;
 #pragma unroll
-        for (int db = 0; db < kDB; db++) o[db] *= al;
+        for (int db = 0; db < kDBw; db++) o[db] *= al;
         m_run = mn;
       }
 #pragma unroll
@@ -447,21 +511,21 @@ prefill_kernel(const AttnArgs a, int rep) {
     const uint32_t stage_b = 2 * kTileB;
     load_tile(0, 0);
     load_tile(1, 1);
-    phase_barrier<1>();
-    if (grp) phase_barrier<1>();
+    phase_barrier<1, kLoads>();
+    if (grp) phase_barrier<1, kLoads>();
     load_tile(2, 2);
     matrix(ka, 0, std::false_type{});
-    phase_barrier<0>();
+    phase_barrier<0, kLoads>();
     // softmax of tile i, then the matrix phase of tile i + 1
     auto open_tile = [&](int i, auto S_) __attribute__((always_inline)) {
       constexpr int S = decltype(S_)::value;
       softmax(i, std::false_type{});
-      phase_barrier<1>();
+      phase_barrier<1, kLoads>();
       load_tile(i + 3, (S + 3) % kStages);
       // past the last tile this scores the clamped copy of the last tile
       // (loaded and complete like any other): unused, but no branch
       matrix(ka + ((S + 1) % kStages) * stage_b, va + S * stage_b, std::true_type{});
-      phase_barrier<0>();
+      phase_barrier<0, kLoads>();
     };
     int i = 0;
     for (; i + kStages <= n_open; i += kStages) {
@@ -476,13 +540,13 @@ prefill_kernel(const AttnArgs a, int rep) {
         softmax(i, std::false_type{});
       else
         softmax(i, std::true_type{});
-      phase_barrier<1>();
+      phase_barrier<1, kLoads>();
       load_tile(i + 3, (s + 3) % kStages);
       matrix(ka + ((s + 1) % kStages) * stage_b, va + s * stage_b, std::true_type{});
-      phase_barrier<0>();
+      phase_barrier<0, kLoads>();
     }
     // group 0 has one barrier fewer: it meets group 1's last one here
-    if (!grp) phase_barrier<0>();
+    if (!grp) phase_barrier<0, kLoads>();
     tile_wait_all();  // the clamped loads issued past the end
   }
 
@@ -497,10 +561,10 @@ prefill_kernel(const AttnArgs a, int rep) {
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     typename E::T* op = static_cast<typename E::T*>(a.out) + b * a.o_sb + h * a.o_sh + pos * a.o_sl;
 #pragma unroll
-    for (int db = 0; db < kDB; db++)
+    for (int db = 0; db < kDBw; db++)
 #pragma unroll
       for (int m = 0; m < 4; m++) {
-        const int d = 32 * db + 8 * m + 4 * kg;
+        const int d = 32 * (dh * kDBw + db) + 8 * m + 4 * kg;
         u32x2_t w;
         w[0] = pack2<DT>(o[db][4 * m] * inv, o[db][4 * m + 1] * inv);
         w[1] = pack2<DT>(o[db][4 * m + 2] * inv, o[db][4 * m + 3] * inv);
@@ -509,12 +573,12 @@ prefill_kernel(const AttnArgs a, int rep) {
   } else {
     // unnormalized partial; (max, sum) with the max in natural-log units
     const int64_t base = (grow * a.Hq + h) * a.n_parts + part;
-    float* wo = a.ws_o + base * kD;
+    float* wo = a.ws_o + base * D + 32 * dh * kDBw;
 #pragma unroll
-    for (int db = 0; db < kDB; db++)
+    for (int db = 0; db < kDBw; db++)
 #pragma unroll
       for (int j = 0; j < 16; j++) wo[32 * db + 8 * (j >> 2) + 4 * kg + (j & 3)] = o[db][j];
-    if (kg == 0) {
+    if (kg == 0 && dh == 0) {  // the two dim halves hold the same (max, sum)
       a.ws_ml[base * 2] = lt > 0.f ? m_run * (1.0f / kLog2e) : -INFINITY;
       a.ws_ml[base * 2 + 1] = lt;
     }
@@ -526,7 +590,8 @@ prefill_kernel(const AttnArgs a, int rep) {
 bool prefill_supported(int dtype, int bits, const AttnArgs& a) {
   if (bits != 0 || a.kv.table || a.kv.qfmt) return false;
   if (dtype != kBF16 && dtype != kF16) return false;
-  if (a.L < 2 || a.D != kD || a.Dv != kD || a.Hq % a.Hkv) return false;
+  if (a.L < 2 || a.Dv != a.D || a.Hq % a.Hkv) return false;
+  if (a.D != 64 && a.D != 128 && a.D != 256) return false;
   if (a.mask_mode != 0 && a.mask_mode != 1) return false;
   // uniform rows: a causal chunk longer than the keys is the generic
   // kernel's; ragged rows (seq_lens) shorter than the chunk see no keys for
@@ -552,8 +617,11 @@ bool prefill_supported(int dtype, int bits, const AttnArgs& a) {
   return true;
 }
 
-int prefill_parts(int64_t rows, int Hkv, int64_t L, int rep, int64_t T, int32_t* part_tokens) {
-  const int64_t rblocks = (L * rep + kRows - 1) / kRows;
+static int prefill_rows_per_wg(int D) { return D == 256 ? PfCfg<256>::kRows : PfCfg<128>::kRows; }
+
+int prefill_parts(int64_t rows, int Hkv, int64_t L, int rep, int64_t T, int D, int32_t* part_tokens) {
+  const int64_t rpw = prefill_rows_per_wg(D);
+  const int64_t rblocks = (L * rep + rpw - 1) / rpw;
   const int64_t wgs = rows * Hkv * rblocks;  // rows = batch rows here
   // one workgroup per CU
   int64_t parts = std::max<int64_t>(1, 256 / std::max<int64_t>(1, wgs));
@@ -564,21 +632,34 @@ int prefill_parts(int64_t rows, int Hkv, int64_t L, int rep, int64_t T, int32_t*
   return static_cast<int>((T + *part_tokens - 1) / *part_tokens);
 }
 
+template <int D>
+static void launch_prefill_d(int dtype, bool qsem, const AttnArgs& a, const dim3& grid, int rep,
+                             hipStream_t st) {
+  if (dtype == kBF16 && qsem)
+    hipLaunchKernelGGL((prefill_kernel<kBF16, true, D>), grid, dim3(kThreads), 0, st, a, rep);
+  else if (dtype == kBF16)
+    hipLaunchKernelGGL((prefill_kernel<kBF16, false, D>), grid, dim3(kThreads), 0, st, a, rep);
+  else if (qsem)
+    hipLaunchKernelGGL((prefill_kernel<kF16, true, D>), grid, dim3(kThreads), 0, st, a, rep);
+  else
+    hipLaunchKernelGGL((prefill_kernel<kF16, false, D>), grid, dim3(kThreads), 0, st, a, rep);
+}
+
 void launch_prefill(int dtype, bool qsem, const AttnArgs& a, int64_t batch, hipStream_t st) {
   if (batch <= 0 || a.L <= 0) return;
+  VKV_CHECK(a.D == 64 || a.D == 128 || a.D == 256, "prefill kernel head dim");
   const int rep = a.Hq / a.Hkv;
-  const int64_t rblocks = (static_cast<int64_t>(a.L) * rep + kRows - 1) / kRows;
+  const int64_t rpw = prefill_rows_per_wg(a.D);
+  const int64_t rblocks = (static_cast<int64_t>(a.L) * rep + rpw - 1) / rpw;
   const int64_t wgs = rblocks * a.n_parts * a.Hkv * batch;
   VKV_CHECK(wgs < (int64_t{1} << 31), "too many prefill workgroups for one launch");
   const dim3 grid(static_cast<unsigned>(wgs));
-  if (dtype == kBF16 && qsem)
-    hipLaunchKernelGGL((prefill_kernel<kBF16, true>), grid, dim3(kThreads), 0, st, a, rep);
-  else if (dtype == kBF16)
-    hipLaunchKernelGGL((prefill_kernel<kBF16, false>), grid, dim3(kThreads), 0, st, a, rep);
-  else if (qsem)
-    hipLaunchKernelGGL((prefill_kernel<kF16, true>), grid, dim3(kThreads), 0, st, a, rep);
+  if (a.D == 64)
+    launch_prefill_d<64>(dtype, qsem, a, grid, rep, st);
+  else if (a.D == 128)
+    launch_prefill_d<128>(dtype, qsem, a, grid, rep, st);
   else
-    hipLaunchKernelGGL((prefill_kernel<kF16, false>), grid, dim3(kThreads), 0, st, a, rep);
+    launch_prefill_d<256>(dtype, qsem, a, grid, rep, st);
   VKV_HIP(hipGetLastError());
   if (a.n_parts > 1) launch_attn_combine(dtype, a, batch * a.L, st);
 }
