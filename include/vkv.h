@@ -659,16 +659,20 @@ int vkv_workspace_release(void *stream, int64_t *bytes);
  * call to the generic VALU kernel; DECODE_WAVES (0 = choose per launch)
  * sets the paged decode kernel's wave count; MLA_SPLITS (0 = choose) sets
  * the MLA kernel's token splits; FDECODE_WAVES (0 = choose) the float
- * decode kernel's target wave count.  Initial values come from the
- * environment variables VKV_GENERIC_ATTENTION, VKV_DECODE_WAVES,
- * VKV_MLA_SPLITS and VKV_FDECODE_WAVES, read once; calls read the options,
- * never the environment. */
+ * decode kernel's target wave count; GATHER_TOKENS (0 = choose) the key
+ * window of a multi-token chunk over a quantized or paged cache (its K/V are
+ * gathered to the dtype one window at a time; by default a window's copy
+ * stays within 256 MiB).  Initial values come from the environment
+ * variables VKV_GENERIC_ATTENTION, VKV_DECODE_WAVES, VKV_MLA_SPLITS,
+ * VKV_FDECODE_WAVES and VKV_GATHER_TOKENS, read once; calls read the
+ * options, never the environment. */
 enum {
   VKV_OPTION_GENERIC_ATTENTION = 0,
   VKV_OPTION_DECODE_WAVES = 1,
   VKV_OPTION_MLA_SPLITS = 2,
   VKV_OPTION_FDECODE_WAVES = 3, /* 0 = 2048: waves the float decode kernel aims for */
-  VKV_OPTION_COUNT = 4
+  VKV_OPTION_GATHER_TOKENS = 4, /* 0 = a 256 MiB copy: key window of a gathered chunk */
+  VKV_OPTION_COUNT = 5
 };
 int vkv_set_option(int32_t which, int64_t value);
 int vkv_get_option(int32_t which, int64_t *value);

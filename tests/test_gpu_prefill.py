@@ -139,6 +139,27 @@ def test_quantized_cache_chunk(bits, monkeypatch):
     assert_within(got, gen, attn_tol(dtype, ref) + 2 * wb, "generic", wb)
 
 
+@pytest.mark.parametrize("bits,window", [(4, 96), (8, 32), (4, 160)])
+def test_quantized_cache_chunk_key_windows(bits, window, monkeypatch):
+    """The chunk's K/V gathered one key window at a time (the gather_tokens
+    option; by default a window's copy is at most 256 MiB): against the
+    oracle and against the single-window result (the same arithmetic, only
+    the split merge groups differently)."""
+    dtype, D = O.BF16, 128
+    step, q, kx, vx = quantized_chunk(np.random.default_rng(70 + bits + window), bits, 0, T0=500,
+                                      L=64)
+    whole = step()
+    monkeypatch.setattr(OPTIONS, "gather_tokens", window)
+    got = step()
+    kq, ks, kb, _ = O.quantize(kx, dtype, 64, bits)
+    vq, vs, vb, _ = O.quantize(vx, dtype, 64, bits)
+    f = lambda a: O.to_f32(a, dtype)
+    ref, wb = qref(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64, bits,
+                   mask="causal", rounding=O.REF_CHUNK)
+    assert_qclose(got, ref, wb, dtype, f"window {window}")
+    assert_within(got, whole, attn_tol(dtype, ref), "one window")
+
+
 @pytest.mark.parametrize("D,bits,rep", [(256, 8, 2), (64, 4, 4)])
 def test_quantized_cache_chunk_head_dims(D, bits, rep, monkeypatch):
     """A chunk over a QuantizedKVCache at 256 dims (config 4's 8-bit global

@@ -173,8 +173,8 @@ def test_quantized_attention_over_pool_view_chunks():
         assert_qclose(out[s], ref, wb, dtype, f"sequence {s} (length {n})")
 
 
-@pytest.mark.parametrize("bits,D", [(4, 128), (8, 128), (8, 256)])
-def test_quantized_chunk_over_ragged_pool_view_on_matrix_cores(bits, D, monkeypatch):
+@pytest.mark.parametrize("bits,D,window", [(4, 128, 0), (8, 128, 0), (8, 256, 0), (4, 128, 64)])
+def test_quantized_chunk_over_ragged_pool_view_on_matrix_cores(bits, D, window, monkeypatch):
     """A 20-token chunk per sequence over a paged pool with ragged lengths
     (the continuous-batching prefill step): 16 or more query tokens take the
     gather + matrix-core path with per-sequence lengths.  A sequence shorter
@@ -206,6 +206,9 @@ def test_quantized_chunk_over_ragged_pool_view_on_matrix_cores(bits, D, monkeypa
     q = rand_bits(rng, (len(lens), Hq, L, D), dtype)
     run = lambda: values(vkv.quantized_paged_attention(dev(q, dtype), view, D ** -0.5,
                                                        mask="causal"), dtype)
+    # window > 0: K/V gathered 64 tokens at a time, so the shorter rows have
+    # windows past their end
+    monkeypatch.setattr(OPTIONS, "gather_tokens", window)
     out = run()
     monkeypatch.setattr(OPTIONS, "generic_attention", 1)
     gen = run()

@@ -76,6 +76,9 @@ int32_t choose_parts(int64_t rows_x_heads, int64_t max_len, int32_t* part_tokens
 }
 
 constexpr int kGatherPrefillMinL = 16;
+// Bytes of the K/V copy of one key window of a gathered chunk (the whole
+// context in one window up to this size).
+constexpr int64_t kGatherCopyBytes = int64_t{256} << 20;
 
 // Dispatch options (vkv_set_option): process-wide, read with relaxed loads on
 // the hot path.  The environment variables of the same names give their
@@ -84,7 +87,8 @@ struct Options {
   std::atomic<int64_t> v[VKV_OPTION_COUNT];
   Options() {
     const char* names[VKV_OPTION_COUNT] = {"VKV_GENERIC_ATTENTION", "VKV_DECODE_WAVES",
-                                           "VKV_MLA_SPLITS", "VKV_FDECODE_WAVES"};
+                                           "VKV_MLA_SPLITS", "VKV_FDECODE_WAVES",
+                                           "VKV_GATHER_TOKENS"};
     for (int i = 0; i < VKV_OPTION_COUNT; i++) {
       const char* e = getenv(names[i]);
       int64_t x = 0;
@@ -130,7 +134,7 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
     AttnArgs d = a;
     const int64_t batch = rows / a.L, T = a.kv.T;
     const int64_t es = elem_bytes(dtype);
-    const int64_t per_head = T * a.D * es, kv_bytes = batch * a.Hkv * per_head;
+    const int64_t per_head = T * a.D * es;
     d.kv = KVSrc{};
     d.kv.T = a.kv.T;
     d.kv.seq_lens = a.kv.seq_lens;
@@ -140,30 +144,53 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
     d.kv.kc.ptr = d.kv.vc.ptr = reinterpret_cast<const uint8_t*>(uintptr_t{256});
     if (a.D == a.Dv && prefill_supported(dtype, 0, d)) {
       d.n_parts = prefill_parts(batch, a.Hkv, a.L, a.Hq / a.Hkv, T, a.D, &d.part_tokens);
-      const size_t copy_floats = static_cast<size_t>((2 * kv_bytes + 255) / 256 * 64);
+      // key windows of whole parts, each gathered to a copy of at most
+      // kGatherCopyBytes (or the gather_tokens option) before its parts run
+      const int64_t tok_bytes = 2 * batch * a.Hkv * a.D * es;  // K + V per token
+      int64_t win = option(VKV_OPTION_GATHER_TOKENS);
+      if (win <= 0) win = kGatherCopyBytes / tok_bytes;
+      win = std::max<int64_t>(32, win / 32 * 32);
+      if (win < T && d.part_tokens > win) {
+        d.part_tokens = static_cast<int32_t>(win);
+        d.n_parts = static_cast<int32_t>((T + win - 1) / win);
+      }
+      const int ppw = static_cast<int>(std::max<int64_t>(1, win / d.part_tokens));
+      const int64_t wtok = std::min<int64_t>(T, static_cast<int64_t>(ppw) * d.part_tokens);
+      const int64_t wbytes = batch * a.Hkv * wtok * a.D * es;  // one matrix of a window
+      const size_t copy_floats = static_cast<size_t>((2 * wbytes + 255) / 256 * 64);
       const size_t per = static_cast<size_t>(rows) * a.Hq * d.n_parts;
       float* ws = workspace(st, copy_floats + (d.n_parts > 1 ? per * (a.Dv + 2) : 0), noalloc);
       uint8_t* kd = reinterpret_cast<uint8_t*>(ws);
-      uint8_t* vd = kd + kv_bytes;
-      GatherArgs g{};
-      g.kv = a.kv;
-      g.n_seqs = static_cast<int32_t>(batch);
-      g.H = a.Hkv;
-      g.T = static_cast<int32_t>(T);
-      g.D = a.D;
-      g.bits = bits;
-      g.group = group;
-      g.dtype = dtype;
-      g.out = kd;
-      g.out_v = vd;
-      launch_gather(g, 0, st);
-      d.kv.kc.ptr = kd;
-      d.kv.vc.ptr = vd;
+      uint8_t* vd = kd + wbytes;
+      const int64_t wph = wtok * a.D * es;  // copy bytes per (row, kv head)
+      d.kv.kc = Comp{kd, a.Hkv * wph, wph, a.D * es};
+      d.kv.vc = Comp{vd, a.Hkv * wph, wph, a.D * es};
       if (d.n_parts > 1) {
         d.ws_o = ws + copy_floats;
         d.ws_ml = d.ws_o + per * a.Dv;
       }
-      launch_prefill(dtype, qsem, d, batch, st);
+      for (int p0 = 0; p0 < d.n_parts; p0 += ppw) {
+        GatherArgs g{};
+        g.kv = a.kv;
+        g.n_seqs = static_cast<int32_t>(batch);
+        g.H = a.Hkv;
+        g.t_begin = static_cast<int32_t>(static_cast<int64_t>(p0) * d.part_tokens);
+        // the copy's layout holds wtok tokens per (row, head); the gather
+        // fills each row's tokens of the window (fewer in the last one)
+        g.T = static_cast<int32_t>(wtok);
+        g.D = a.D;
+        g.bits = bits;
+        g.group = group;
+        g.dtype = dtype;
+        g.out = kd;
+        g.out_v = vd;
+        launch_gather(g, 0, st);
+        d.part0 = p0;
+        d.parts_run = std::min(ppw, d.n_parts - p0);
+        d.t_base = g.t_begin;
+        launch_prefill(dtype, qsem, d, batch, st, /*combine=*/false);
+      }
+      if (d.n_parts > 1) launch_attn_combine(dtype, d, rows, st);
       return;
     }
   }

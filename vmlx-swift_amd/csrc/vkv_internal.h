@@ -98,6 +98,10 @@ struct AttnArgs {
   void* out;
   int64_t o_sb, o_sh, o_sl;
   int32_t part_tokens, n_parts;
+  // prefill over a window of the keys (0, 0 = all parts): this launch runs
+  // parts part0 .. part0 + parts_run - 1 of n_parts, over K/V whose first row
+  // is token t_base
+  int32_t part0, parts_run, t_base;
   float* ws_o;             // [rows][Hq][n_parts][Dv]
   float* ws_ml;            // [rows][Hq][n_parts][2] (max, sum)
 };
@@ -121,6 +125,7 @@ void launch_dequantize(int dtype, int bits, int group, const uint32_t* wq, const
 struct GatherArgs {
   KVSrc kv;
   int32_t n_seqs, H, T, D, which, bits, group, dtype;
+  int32_t t_begin;  // first token gathered: output token t is token t_begin + t
   void* out;        // [n,H,T,D] values, or [n,H,T,D*bits/32] u32 codes
   void* out_s;      // [n,H,T,D/group]
   void* out_b;
@@ -145,7 +150,9 @@ void launch_attn_combine(int dtype, const AttnArgs& a, int64_t rows, hipStream_t
 // causal mask, on matrix cores (vkv_prefill.hip).
 bool prefill_supported(int dtype, int bits, const AttnArgs& a);
 int prefill_parts(int64_t batch, int Hkv, int64_t L, int rep, int64_t T, int D, int32_t* part_tokens);
-void launch_prefill(int dtype, bool qsem, const AttnArgs& a, int64_t batch, hipStream_t st);
+// combine = false leaves the split merge to the caller (a window of parts)
+void launch_prefill(int dtype, bool qsem, const AttnArgs& a, int64_t batch, hipStream_t st,
+                    bool combine = true);
 bool fdecode_supported(int dtype, int bits, bool qsem, const AttnArgs& a);
 int fdecode_parts(int64_t rows_x_heads, int64_t T, int32_t* part_tokens, int waves);
 void launch_fdecode(int dtype, const AttnArgs& a, int64_t rows, hipStream_t st);

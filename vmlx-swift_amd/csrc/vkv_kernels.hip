@@ -444,8 +444,8 @@ __global__ void __launch_bounds__(256) gather_kernel(GatherArgs g) {
   const int64_t h = (row / g.T) % g.H;
   const int64_t s = row / (static_cast<int64_t>(g.T) * g.H);
   const int64_t len = g.kv.seq_lens ? g.kv.seq_lens[s] : g.kv.T;
-  if (t >= len) return;
-  const TokLoc l = locate(g.kv, s, t);
+  if (t + g.t_begin >= len) return;
+  const TokLoc l = locate(g.kv, s, t + g.t_begin);
   const int d0 = j * 8;
   const int cnt = min(8, g.D - d0);
   if constexpr (KIND == 0) {
@@ -493,7 +493,9 @@ __global__ void __launch_bounds__(256) gather_dequant8_kernel(GatherArgs g) {
   constexpr uint32_t kMask = (1u << BITS) - 1u;
   const int tpr = g.D >> 3;
   const int plane = blockIdx.y, s = plane / g.H, h = plane - s * g.H;
-  const int len = min(g.T, static_cast<int>(g.kv.seq_lens ? g.kv.seq_lens[s] : g.kv.T));
+  // tokens of this row in the window [t_begin, t_begin + T)
+  const int len =
+      min(g.T, static_cast<int>(g.kv.seq_lens ? g.kv.seq_lens[s] : g.kv.T) - g.t_begin);
   if (len <= 0) return;  // an empty sequence may own no block
   const KVSrc& kv = g.kv;
   const bool ko = kv.keys_only != 0;
@@ -510,7 +512,8 @@ __global__ void __launch_bounds__(256) gather_dequant8_kernel(GatherArgs g) {
     ti[k] = idx / tpr;
     d0[k] = (idx - ti[k] * tpr) * 8;
     live[k] = ti[k] < len;
-    const int t = live[k] ? ti[k] : 0;  // dead pieces load token 0 (in bounds) and store nothing
+    // dead pieces load the window's first token (in bounds) and store nothing
+    const int t = g.t_begin + (live[k] ? ti[k] : 0);
     TokLoc l;
     if (kv.table) {
       const int b = t / kv.block_size;

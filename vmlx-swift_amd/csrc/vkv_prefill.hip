@@ -211,11 +211,13 @@ prefill_kernel(const AttnArgs a, int rep) {
   // row block and part, stays in the XCD's L2
   const int L = a.L;
   const int rblocks = static_cast<int>((static_cast<int64_t>(L) * rep + kRows - 1) / kRows);
+  // parts of this launch: all, or a window part0 .. part0 + parts_run - 1
+  const int prun = a.parts_run > 0 ? a.parts_run : a.n_parts;
   int id = blockIdx.x;
   const int hk = id % a.Hkv;
   id /= a.Hkv;
-  const int part = id % a.n_parts;
-  id /= a.n_parts;
+  const int part = a.part0 + id % prun;
+  id /= prun;
   const int rblk = id % rblocks;
   const int64_t b = id / rblocks;
   // keys of this row of the batch: its own length when the rows are ragged
@@ -294,8 +296,9 @@ prefill_kernel(const AttnArgs a, int rep) {
     // then the V tile's); wave w issues loads w + 8 x.  Lane lam of a load
     // fills LDS slot lam % kSlots of its row (the load covers 1024 / kRowB
     // consecutive rows) with the row's piece (lam % kSlots) ^ swizzle(row).
-    const uint8_t* kbase = a.kv.kc.ptr + b * a.kv.kc.sb + hk * a.kv.kc.sh;
-    const uint8_t* vbase = a.kv.vc.ptr + b * a.kv.vc.sb + hk * a.kv.vc.sh;
+    // row 0 of the K / V views is token t_base (a window of the keys)
+    const uint8_t* kbase = a.kv.kc.ptr + b * a.kv.kc.sb + hk * a.kv.kc.sh - a.t_base * a.kv.kc.st;
+    const uint8_t* vbase = a.kv.vc.ptr + b * a.kv.vc.sb + hk * a.kv.vc.sh - a.t_base * a.kv.vc.st;
     const int64_t kst = a.kv.kc.st, vst = a.kv.vc.st;
     // the lane's row and piece in load x (recomputed where needed: at 256
     // dims four loads' worth would hold registers through the loop)
@@ -645,13 +648,16 @@ static void launch_prefill_d(int dtype, bool qsem, const AttnArgs& a, const dim3
     hipLaunchKernelGGL((prefill_kernel<kF16, false, D>), grid, dim3(kThreads), 0, st, a, rep);
 }
 
-void launch_prefill(int dtype, bool qsem, const AttnArgs& a, int64_t batch, hipStream_t st) {
+void launch_prefill(int dtype, bool qsem, const AttnArgs& a, int64_t batch, hipStream_t st,
+                    bool combine) {
   if (batch <= 0 || a.L <= 0) return;
   VKV_CHECK(a.D == 64 || a.D == 128 || a.D == 256, "prefill kernel head dim");
+  const int prun = a.parts_run > 0 ? a.parts_run : a.n_parts;
+  VKV_CHECK(a.part0 >= 0 && a.part0 + prun <= a.n_parts, "prefill part window");
   const int rep = a.Hq / a.Hkv;
   const int64_t rpw = prefill_rows_per_wg(a.D);
   const int64_t rblocks = (static_cast<int64_t>(a.L) * rep + rpw - 1) / rpw;
-  const int64_t wgs = rblocks * a.n_parts * a.Hkv * batch;
+  const int64_t wgs = rblocks * prun * a.Hkv * batch;
   VKV_CHECK(wgs < (int64_t{1} << 31), "too many prefill workgroups for one launch");
   const dim3 grid(static_cast<unsigned>(wgs));
   if (a.D == 64)
@@ -661,7 +667,7 @@ void launch_prefill(int dtype, bool qsem, const AttnArgs& a, int64_t batch, hipS
   else
     launch_prefill_d<256>(dtype, qsem, a, grid, rep, st);
   VKV_HIP(hipGetLastError());
-  if (a.n_parts > 1) launch_attn_combine(dtype, a, batch * a.L, st);
+  if (combine && a.n_parts > 1) launch_attn_combine(dtype, a, batch * a.L, st);
 }
 
 }  // namespace vkv

@@ -182,7 +182,8 @@ def to_torch(a: Array, stream=None):
 
 
 # ------------------------------------------------------------------- ops
-OPTIONS = {"generic_attention": 0, "decode_waves": 1, "mla_splits": 2, "fdecode_waves": 3}
+OPTIONS = {"generic_attention": 0, "decode_waves": 1, "mla_splits": 2, "fdecode_waves": 3,
+           "gather_tokens": 4}
 
 
 def set_option(name: str, value: int):
