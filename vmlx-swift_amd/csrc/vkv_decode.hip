@@ -321,6 +321,11 @@ struct QD {
   // per-step operand registers; steps are double buffered when they fit
   static constexpr int BUF = D * UW / 4 + HP * D / 32;
   static constexpr bool kPrefetch = BUF <= 48;
+  // one wave per SIMD (D = 256): the next step's key words and scales load
+  // while a step computes, its value words at the step's start (behind the
+  // scores); whole double buffers would not fit beside the rest, and with 8
+  // heads per part neither does this (it spills)
+  static constexpr bool kPrefetchK = !kPrefetch && D >= 256 && HP == 4;
 
   struct Buf {
     uint32_t kw[TT][PP][RUN];    // key words of this lane's token, per tile
@@ -565,9 +570,8 @@ qdecode_kernel(DecodeArgs a) {
     sb_lane[tau] = a.sb_off + (8 * lg + tok_off<BITS>(c2 & 1, 0)) * SBW * 4;
   }
   const int32_t v_lane = a.vc_off + (lg * 16 + n) * VW * 4;
-  auto load_step = [&](int ui, Buf& b) __attribute__((always_inline)) {
-    const uint8_t* bc[2];  // codes base of each sub-block
-    const uint8_t* bs[2];  // scale/bias base
+  // code and scale/bias bases of unit ui's two 32-token sub-blocks
+  auto step_bases = [&](int ui, const uint8_t** bc, const uint8_t** bs) __attribute__((always_inline)) {
 #pragma unroll
     for (int s = 0; s < 2; s++) {
       const uint8_t* cb = a.base + __builtin_amdgcn_readfirstlane(sub_off[2 * ui + s]);
@@ -575,6 +579,12 @@ qdecode_kernel(DecodeArgs a) {
       bc[s] = cb + t0 * ROW;
       bs[s] = cb + t0 * SBW * 4;
     }
+  };
+  // key words and scales / biases of unit ui
+  auto load_k = [&](int ui, Buf& b) __attribute__((always_inline)) {
+    const uint8_t* bc[2];
+    const uint8_t* bs[2];
+    step_bases(ui, bc, bs);
 #pragma unroll
     for (int tau = 0; tau < TT; tau++) {
       const uint8_t* row = (ks_sub[tau] ? bc[1] : bc[0]) + k_lane[tau];
@@ -585,12 +595,26 @@ qdecode_kernel(DecodeArgs a) {
       for (int i = 0; i < 4; i++)
         load_words<SBW>(sbp + (tok_off<BITS>(0, i) - tok_off<BITS>(0, 0)) * SBW * 4, b.sb[tau][i]);
     }
+  };
+  // value words of unit ui
+  auto load_v = [&](int ui, uint32_t (&vw)[2][VW]) __attribute__((always_inline)) {
+    const uint8_t* bc[2];
+    const uint8_t* bs[2];
+    step_bases(ui, bc, bs);
 #pragma unroll
-    for (int s = 0; s < 2; s++) load_words<VW>(bc[s] + v_lane, b.vw[s]);
+    for (int s = 0; s < 2; s++) load_words<VW>(bc[s] + v_lane, vw[s]);
+  };
+  auto load_step = [&](int ui, Buf& b) __attribute__((always_inline)) {
+    load_k(ui, b);
+    load_v(ui, b.vw);
   };
 
   Buf bufA, bufB;
-  load_step(0, bufA);
+  uint32_t vcur[2][VW];  // kPrefetchK: the current unit's value words
+  if constexpr (C::kPrefetchK)
+    load_k(0, bufA);
+  else
+    load_step(0, bufA);
   const Magic mg;
   const float scale_t = round_to<kBF16>(a.scale);
 
@@ -668,7 +692,7 @@ qdecode_kernel(DecodeArgs a) {
   for (int g = 0; g < G; g++) corr[g] = 0.0f;
   const u32x4_t* qlane = qtab + ((pA == p) ? n * SPW + wA : 16 * SPW);
 
-  auto compute_step = [&](int stp, const Buf& b) __attribute__((always_inline)) {
+  auto compute_step = [&](int stp, const Buf& b, const uint32_t (&vw)[2][VW]) __attribute__((always_inline)) {
     const int len = seg_len;
     // ---- scores: acc[tau][g] = q . (KMAG + c) over group g's dims
     f32x4_t acc[TT][G];
@@ -816,12 +840,12 @@ qdecode_kernel(DecodeArgs a) {
       for (int t = 0; t < NT; t++) {
         const int g = t / (NT / G);
         if constexpr (BITS == 4) {
-          const u32x4_t av = nib_magic(b.vw[s][t], mg);
+          const u32x4_t av = nib_magic(vw[s][t], mg);
           oacc[t] = mfma(av, bpv[g][0], oacc[t]);
           oacc[t] = mfma(av, bpv[g][1], oacc[t]);
         } else {
           u32x4_t lo, hi;
-          byte_magic(b.vw[s][2 * t], b.vw[s][2 * t + 1], mg, lo, hi);
+          byte_magic(vw[s][2 * t], vw[s][2 * t + 1], mg, lo, hi);
           oacc[t] = mfma(lo, bpv[g][0], oacc[t]);
           oacc[t] = mfma(lo, bpv[g][1], oacc[t]);
           oacc[t] = mfma(hi, bpv[g][0], oacc[t]);
@@ -916,7 +940,7 @@ qdecode_kernel(DecodeArgs a) {
         else if (other < ui) __builtin_amdgcn_s_setprio(0);  // ahead: yield
       }
     }
-    compute_step(seg_t + (ui - seg_first), cur);
+    compute_step(seg_t + (ui - seg_first), cur, cur.vw);
     if (ui == seg_first + seg_take - 1) {  // last unit of the segment
       finalize();
       if (k + 1 < nseg) {
@@ -935,9 +959,33 @@ qdecode_kernel(DecodeArgs a) {
       unit(ui + 1, bufB, bufA, std::true_type{});
     }
     if (ui < nunits) unit(ui, bufA, bufB, std::false_type{});
+  } else if constexpr (C::kPrefetchK) {
+    // unit ui: its value words, then unit ui + 1's key words (clamped,
+    // unconditional), issued before it computes; the value words' latency
+    // hides behind the scores
+    auto unit_k = [&](int ui, const Buf& cur, Buf& nxt) __attribute__((always_inline)) {
+      load_v(ui, vcur);
+      load_k(min(ui + 1, nunits - 1), nxt);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_step(seg_t + (ui - seg_first), cur, vcur);
+      if (ui == seg_first + seg_take - 1) {
+        finalize();
+        if (k + 1 < nseg) {
+          k++;
+          setup_segment(k, qpre);
+          load_q(min(k + 1, nseg - 1), qpre);
+        }
+      }
+    };
+    int ui = 0;
+    for (; ui + 1 < nunits; ui += 2) {
+      unit_k(ui, bufA, bufB);
+      unit_k(ui + 1, bufB, bufA);
+    }
+    if (ui < nunits) unit_k(ui, bufA, bufB);
   } else {
     for (int ui = 0;; ui++) {
-      compute_step(seg_t + (ui - seg_first), bufA);
+      compute_step(seg_t + (ui - seg_first), bufA, bufA.vw);
       if (ui == seg_first + seg_take - 1) {
         finalize();
         if (ui + 1 == nunits) break;
