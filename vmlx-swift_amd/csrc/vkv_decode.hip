@@ -321,10 +321,12 @@ struct QD {
   // per-step operand registers; steps are double buffered when they fit
   static constexpr int BUF = D * UW / 4 + HP * D / 32;
   static constexpr bool kPrefetch = BUF <= 48;
-  // one wave per SIMD (D = 256): the next step's key words and scales load
-  // while a step computes, its value words at the step's start (behind the
-  // scores); whole double buffers would not fit beside the rest, and with 8
-  // heads per part neither does this (it spills)
+  // one wave per SIMD (D = 256) with 4 heads per part: the next step's key
+  // words and scales load while a step computes, its value words at the
+  // step's start (behind the scores); whole double buffers would not fit
+  // beside the rest, and with 8 heads per part neither does this (it
+  // spills).  (At D 128, 8-bit, where two waves share a SIMD, it fits but
+  // measured no faster: the partner wave already covers the loads.)
   static constexpr bool kPrefetchK = !kPrefetch && D >= 256 && HP == 4;
 
   struct Buf {
