@@ -297,8 +297,8 @@ prefill_kernel(const AttnArgs a, int rep) {
     // fills LDS slot lam % kSlots of its row (the load covers 1024 / kRowB
     // consecutive rows) with the row's piece (lam % kSlots) ^ swizzle(row).
     // row 0 of the K / V views is token t_base (a window of the keys)
-    const uint8_t* kbase = a.kv.kc.ptr + b * a.kv.kc.sb + hk * a.kv.kc.sh - a.t_base * a.kv.kc.st;
-    const uint8_t* vbase = a.kv.vc.ptr + b * a.kv.vc.sb + hk * a.kv.vc.sh - a.t_base * a.kv.vc.st;
+    const uint8_t* kbase = a.kv.kc.ptr + b * a.kv.kc.sb + hk * a.kv.kc.sh;
+    const uint8_t* vbase = a.kv.vc.ptr + b * a.kv.vc.sb + hk * a.kv.vc.sh;
     const int64_t kst = a.kv.kc.st, vst = a.kv.vc.st;
     // the lane's row and piece in load x (recomputed where needed: at 256
     // dims four loads' worth would hold registers through the loop)
@@ -331,7 +331,7 @@ prefill_kernel(const AttnArgs a, int rep) {
         }
         // wave-uniform (M0), which the compiler does not see through the select
         const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_addr(&kv[s][is_v][0]) + 1024 * pn);
-        dma16((is_v ? vbase : kbase) + t0 * st, off, dst);
+        dma16((is_v ? vbase : kbase) + (t0 - a.t_base) * st, off, dst);
       }
     };
 
