@@ -573,10 +573,10 @@ def turboquant_measure(torch, vkv, steps, warmup):
         "key_decode_kernel_us": round(dec_ms * 1e3, 2),
         "roofline": {"bound": "valu", "achieved": round(enc_tf, 2), "peak": F32_VALU_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(enc_tf / F32_VALU_PEAK_TFLOPS, 4),
-                     "kernel": "tq_encode_kernel<128> (keys)", "flops_per_launch": flops},
+                     "kernel": "tq_encode_rows<128, keys>", "flops_per_launch": flops},
         "decode_roofline": {"achieved": round(dec_tf, 2), "peak": F32_VALU_PEAK_TFLOPS,
                             "unit": "TFLOP/s", "frac": round(dec_tf / F32_VALU_PEAK_TFLOPS, 4),
-                            "kernel": "tq_decode_kernel<128> (keys)"},
+                            "kernel": "tq_decode_rows<128, keys>"},
     }
 
 

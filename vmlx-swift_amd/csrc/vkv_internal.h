@@ -296,6 +296,9 @@ struct TqDecodeArgs {
 };
 void launch_tq_encode(const TqEncodeArgs& a, hipStream_t st);
 void launch_tq_decode(const TqDecodeArgs& a, hipStream_t st);
+// Zeros in `rows` runs of run_bytes, pitch_bytes apart (2-byte units).
+void launch_zero_runs(void* base, int64_t pitch_bytes, int64_t run_bytes, int64_t rows,
+                      hipStream_t st);
 // dst = src with a dtype conversion (4-D, element strides).
 void launch_cast4d(const void* src, int sdt, const int64_t* shape, const int64_t* sstr, void* dst,
                    int ddt, const int64_t* dstr, hipStream_t st);

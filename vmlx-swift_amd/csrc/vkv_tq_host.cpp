@@ -501,13 +501,22 @@ void TurboQuantCache::compress(const vkv_array& k, const vkv_array& v, int64_t s
   offset = source_offset;
 }
 
+// Zeros in tokens [t0, t0 + len) of every (b, h) row of d (the rest of the
+// buffer is written by the caller).
+static void zero_token_range(const Dense4& d, int64_t t0, int64_t len, hipStream_t st) {
+  const int64_t es = elem_bytes(d.dtype);
+  launch_zero_runs(d.buf->bytes() + t0 * d.D * es, d.cap * d.D * es, len * d.D * es, d.B * d.H, st);
+}
+
 // The decoded prefix plus windowStep zero slots, as restoreCompressed and
 // compressFloatKV build it.
 void TurboQuantCache::seat(std::shared_ptr<TqEncoded> ek, std::shared_ptr<TqEncoded> ev,
                            hipStream_t st) {
   const int64_t n = ek->tokens();
-  Dense4 uk = alloc_dense(ek->B, ek->H, n + kWindowStep, ek->D, ek->decoded_dtype(), true, st);
-  Dense4 uv = alloc_dense(ev->B, ev->H, n + kWindowStep, ev->D, ev->decoded_dtype(), true, st);
+  Dense4 uk = alloc_dense(ek->B, ek->H, n + kWindowStep, ek->D, ek->decoded_dtype(), false, st);
+  Dense4 uv = alloc_dense(ev->B, ev->H, n + kWindowStep, ev->D, ev->decoded_dtype(), false, st);
+  zero_token_range(uk, n, kWindowStep, st);
+  zero_token_range(uv, n, kWindowStep, st);
   decode_into(*ek, uk, st);
   decode_into(*ev, uv, st);
   reset();
@@ -693,8 +702,10 @@ void TurboQuantCache::restore_decoded(const vkv_array& k, const vkv_array& v, in
   check4(v, "values");
   if (source_offset <= 0) return;
   const int64_t n = k.shape[2];
-  Dense4 uk = alloc_dense(k.shape[0], k.shape[1], n + kWindowStep, k.shape[3], k.dtype, true, st);
-  Dense4 uv = alloc_dense(v.shape[0], v.shape[1], n + kWindowStep, v.shape[3], v.dtype, true, st);
+  Dense4 uk = alloc_dense(k.shape[0], k.shape[1], n + kWindowStep, k.shape[3], k.dtype, false, st);
+  Dense4 uv = alloc_dense(v.shape[0], v.shape[1], n + kWindowStep, v.shape[3], v.dtype, false, st);
+  zero_token_range(uk, n, kWindowStep, st);
+  zero_token_range(uv, n, kWindowStep, st);
   copy_tokens(uk, 0, k, 0, n, st);
   copy_tokens(uv, 0, v, 0, n, st);
   reset();
