@@ -61,16 +61,43 @@ __device__ __forceinline__ void unpack16(const u32x4_t& w, float* out) {
   }
 }
 
-// Maximum / sum within each half-wave of 32 lanes.
+// Cross-lane moves without an LDS round trip where one exists: DPP inside
+// rows of 16 lanes, the swizzle for partners 8 and 16 lanes away (within
+// 32), the half swap for partners 32 lanes away.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+template <int M>  // the value of lane (lane ^ M), M = 8 or 16
+__device__ __forceinline__ float swz_xor(float x) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1F | (M << 10)));
+}
+// v + the value of lane (lane ^ 32), added in that order
+__device__ __forceinline__ float add_xor32(float v) {
+  float lo = v, hi = v;
+  // lo's upper half <- hi's lower half: lo = the lower half's values in both
+  // halves, hi = the upper half's
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(lo), "+v"(hi));
+  return lo + hi;
+}
+
+// Maximum / sum within each half-wave of 32 lanes: pairs 1 and 2 apart
+// (quad permutes), then each lane with its mirror in 8 and in 16 lanes (the
+// partners hold equal values by then, so the mirror acts as a butterfly),
+// then 16 apart.
 __device__ __forceinline__ float half_maxf(float x) {
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
+  x = fmaxf(x, dpp_mov<0xB1>(x));
+  x = fmaxf(x, dpp_mov<0x4E>(x));
+  x = fmaxf(x, dpp_mov<0x141>(x));
+  x = fmaxf(x, dpp_mov<0x140>(x));
+  return fmaxf(x, swz_xor<16>(x));
 }
 __device__ __forceinline__ float half_sumf(float x) {
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  return x;
+  x += dpp_mov<0xB1>(x);
+  x += dpp_mov<0x4E>(x);
+  x += dpp_mov<0x141>(x);
+  x += dpp_mov<0x140>(x);
+  return x + swz_xor<16>(x);
 }
 
 template <int DT, int D, int REP>
@@ -96,21 +123,57 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
   const int64_t t_begin = static_cast<int64_t>(part) * a.part_tokens;
   const int64_t t_end = min<int64_t>(T, t_begin + a.part_tokens);
 
-  for (int i = lane; i < REP * D; i += 64) {
-    const int r = i / D, d = i % D;
-    float qv = 0.0f;
-    if (r < nh)
-      qv = E::load(static_cast<const typename E::T*>(a.q) + b * a.q_sb + (h0 + r) * a.q_sh + d) *
-           a.scale;
-    qs[r][d] = qv;
-  }
-  __syncthreads();
-
   const uint8_t* kbase = a.kv.kc.ptr + b * a.kv.kc.sb + hk * a.kv.kc.sh;
   const uint8_t* vbase = a.kv.vc.ptr + b * a.kv.vc.sb + hk * a.kv.vc.sh;
   const int64_t kst = a.kv.kc.st, vst = a.kv.vc.st;
   const int rs = lane / LPR, dg = lane % LPR;  // value phase: row slot, 16-byte run
+  const int tok = lane & (kStep - 1), half = lane / kStep;
+  // Loads of a step (t0): lanes tok and tok + 32 read half of key row
+  // t0 + tok each; value row slot rs takes tokens t0 + rs, t0 + rs + RPI, ...
+  // (rows past the end read the range's first row; their scores are masked
+  // and their probabilities are 0).  All of a step's loads go out before
+  // its first use, so a step waits for one memory round trip, not one per
+  // group of loads; f32 at 256 dims would need more than 160 registers for
+  // both sets, so there the value loads go out after the scores.  (Loading
+  // the next step during this one's arithmetic keeps both sets live across
+  // the loop: measured slower, fewer waves fit.)
+  constexpr int NV = kStep / RPI;
+  constexpr bool kVEarly = (KL / 2 + NV) * 4 <= 160;
+  u32x4_t kw[KL / 2], vw[NV];
+  auto load_k = [&](int64_t t0) __attribute__((always_inline)) {
+    const int64_t t = t0 + tok;
+    const uint8_t* krow = kbase + (t < t_end ? t : t_begin) * kst + 16 * (KL / 2) * half;
+#pragma unroll
+    for (int c = 0; c < KL / 2; c++) kw[c] = *(g_u32x4_t*)(krow + 16 * c);
+  };
+  auto load_v = [&](int64_t t0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+      const int64_t tv = t0 + rs + RPI * k;
+      vw[k] = *(g_u32x4_t*)(vbase + (tv < t_end ? tv : t_begin) * vst + 16 * dg);
+    }
+  };
 
+  // the queries (times the scale) go to LDS; their loads go out first,
+  // then the first step's key and value loads, so both latencies overlap
+  constexpr int NQ = REP * D / 64;
+  float qv[NQ];
+#pragma unroll
+  for (int j = 0; j < NQ; j++) {
+    const int i = lane + 64 * j, r = i / D, d = i % D;
+    qv[j] = r < nh ? E::load(static_cast<const typename E::T*>(a.q) + b * a.q_sb + (h0 + r) * a.q_sh + d)
+                   : 0.0f;
+  }
+  if (t_begin < t_end) {
+    load_k(t_begin);
+    if constexpr (kVEarly) load_v(t_begin);
+  }
+#pragma unroll
+  for (int j = 0; j < NQ; j++) {
+    const int i = lane + 64 * j;
+    qs[i / D][i % D] = qv[j] * a.scale;
+  }
+  __syncthreads();
   float m[REP], l[REP], o[REP][VEC];
 #pragma unroll
   for (int r = 0; r < REP; r++) {
@@ -127,29 +190,32 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
     for (int e = 0; e < VEC; e++) o[r][e] = 0.0f;
   }
 
-  const int tok = lane & (kStep - 1), half = lane / kStep;
   for (int64_t t0 = t_begin; t0 < t_end; t0 += kStep) {
     // ---- scores: lanes tok and tok + 32 own token t0 + tok, each half of
-    // its dims (rows past the end read the range's first row and are masked)
+    // its dims
     const int64_t t = t0 + tok;
     const bool valid = t < t_end;
-    const uint8_t* krow = kbase + (valid ? t : t_begin) * kst + 16 * (KL / 2) * half;
+    if (t0 != t_begin) {
+      load_k(t0);
+      if constexpr (kVEarly) load_v(t0);
+    }
     float s[REP];
 #pragma unroll
     for (int r = 0; r < REP; r++) s[r] = 0.0f;
-#pragma unroll 4
+#pragma unroll
     for (int c = 0; c < KL / 2; c++) {
-      const u32x4_t w = *(g_u32x4_t*)(krow + 16 * c);
       float kv[VEC];
-      unpack16<DT>(w, kv);
+      unpack16<DT>(kw[c], kv);
       const int q0 = VEC * (c + (KL / 2) * half);
 #pragma unroll
       for (int r = 0; r < REP; r++)
 #pragma unroll
         for (int e = 0; e < VEC; e++) s[r] = fmaf(qs[r][q0 + e], kv[e], s[r]);
     }
+    if constexpr (!kVEarly) load_v(t0);
+
 #pragma unroll
-    for (int r = 0; r < REP; r++) s[r] += __shfl_xor(s[r], kStep);
+    for (int r = 0; r < REP; r++) s[r] = add_xor32(s[r]);
 #pragma unroll
     for (int r = 0; r < REP; r++) {
       bool vis = valid && r < nh;
@@ -183,16 +249,11 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
       for (int e = 0; e < VEC; e++) o[r][e] *= alpha;
     }
     __syncthreads();
-    // ---- values: row slot rs takes tokens t0 + rs, t0 + rs + RPI, ...
-    // (probability 0 past the end, where the row read is clamped)
-#pragma unroll 4
-    for (int k = 0; k < kStep / RPI; k++) {
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
       const int tt = rs + RPI * k;
-      const int64_t tv = t0 + tt;
-      const uint8_t* vrow = vbase + (tv < t_end ? tv : t_begin) * vst + 16 * dg;
-      const u32x4_t w = *(g_u32x4_t*)(vrow);
       float vv[VEC];
-      unpack16<DT>(w, vv);
+      unpack16<DT>(vw[k], vv);
 #pragma unroll
       for (int r = 0; r < REP; r++) {
         const float p = ps[r][tt];
@@ -207,9 +268,11 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
 #pragma unroll
   for (int r = 0; r < REP; r++)
 #pragma unroll
-    for (int e = 0; e < VEC; e++)
-#pragma unroll
-      for (int off = LPR; off < 64; off <<= 1) o[r][e] += __shfl_xor(o[r][e], off);
+    for (int e = 0; e < VEC; e++) {
+      if constexpr (LPR <= 8) o[r][e] += swz_xor<8>(o[r][e]);
+      if constexpr (LPR <= 16) o[r][e] += swz_xor<16>(o[r][e]);
+      if constexpr (LPR <= 32) o[r][e] = add_xor32(o[r][e]);
+    }
   if (rs != 0) return;
 #pragma unroll
   for (int r = 0; r < REP; r++) {
