@@ -945,6 +945,59 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int64_t n
   }
 }
 
+// The same merge for launches with few (row, head)s: one wave per (row,
+// head, 64 dims), lane l merging dim 64 c + l, the (max, sum) pairs and
+// partials of up to 32 parts loaded before any is used (the pairs are the
+// same for the whole wave, so they load through the scalar path): four
+// times the waves and one memory round trip per 32 parts.
+template <int DT>
+__global__ void __launch_bounds__(64) attn_combine_narrow_kernel(AttnArgs a, int64_t n_rh) {
+  using E = Elem<DT>;
+  const int nch = (a.Dv + 63) / 64;
+  const int64_t rh = blockIdx.x / nch;  // row * Hq + h
+  if (rh >= n_rh) return;
+  const int d = 64 * static_cast<int>(blockIdx.x % nch) + threadIdx.x;
+  const bool dv = d < a.Dv;
+  const int64_t row = rh / a.Hq;
+  const int h = static_cast<int>(rh % a.Hq);
+  const int64_t b = row / a.L;
+  const int l = static_cast<int>(row % a.L);
+  const float* ml = a.ws_ml + rh * a.n_parts * 2;
+  const float* wo = a.ws_o + rh * a.n_parts * a.Dv + (dv ? d : 0);
+  float M = -3.402823466e38f, den = 0.0f, acc = 0.0f;
+  for (int c = 0; c < a.n_parts; c += 32) {
+    float m[32], ls[32], v[32];
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      const int p = min(c + j, a.n_parts - 1);  // (clamped slots are selected away)
+      m[j] = ml[2 * p];
+      ls[j] = ml[2 * p + 1];
+      v[j] = wo[static_cast<int64_t>(p) * a.Dv];
+    }
+    float Mc = M;
+#pragma unroll
+    for (int j = 0; j < 32; j++)
+      if (c + j < a.n_parts) Mc = fmaxf(Mc, m[j]);
+    const float r = __expf(M - Mc);
+    den *= r;
+    acc *= r;
+    M = Mc;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      if (c + j < a.n_parts) {
+        const float w = __expf(m[j] - M);
+        den += w * ls[j];
+        acc = fmaf(w, v[j], acc);
+      }
+    }
+  }
+  if (dv) {
+    typename E::T* out = static_cast<typename E::T*>(a.out) + b * a.o_sb + h * a.o_sh +
+                         static_cast<int64_t>(l) * a.o_sl;
+    out[d] = E::from_f32(den > 0.0f ? acc / den : 0.0f);
+  }
+}
+
 // ------------------------------------------------------------ launchers
 
 static inline unsigned blocks_for(int64_t threads) {
@@ -1244,6 +1297,19 @@ static void attn_dispatch(int bits, bool qsem, const AttnArgs& a, int64_t rows, 
 void launch_attn_combine(int dtype, const AttnArgs& a, int64_t rows, hipStream_t st) {
   if (a.Dv > 256) throw Error("attention merge supports value dims up to 256");
   const int64_t n_rh = rows * a.Hq;
+  const int64_t nch = (a.Dv + 63) / 64;
+  if (n_rh * nch <= 2048) {
+    // few (row, head)s: the narrow merge's waves fit the chip at once
+    const dim3 g(static_cast<unsigned>(n_rh * nch));
+    switch (dtype) {
+      case kF32: hipLaunchKernelGGL((attn_combine_narrow_kernel<kF32>), g, dim3(64), 0, st, a, n_rh); break;
+      case kF16: hipLaunchKernelGGL((attn_combine_narrow_kernel<kF16>), g, dim3(64), 0, st, a, n_rh); break;
+      case kBF16: hipLaunchKernelGGL((attn_combine_narrow_kernel<kBF16>), g, dim3(64), 0, st, a, n_rh); break;
+      default: throw Error("unsupported dtype");
+    }
+    VKV_HIP(hipGetLastError());
+    return;
+  }
   const dim3 grid(static_cast<unsigned>((n_rh + 3) / 4));
   switch (dtype) {
     case kF32: hipLaunchKernelGGL((attn_combine_kernel<kF32>), grid, dim3(256), 0, st, a, n_rh); break;
