@@ -1005,8 +1005,10 @@ qdecode_kernel(DecodeArgs a) {
 // dims of one head.  The pair's partial count, its length and its first
 // kFirst partials load together (the partial slots past the count hold
 // stale data, which the merge masks), so a pair of up to kFirst partials
-// costs one round trip to memory.  (Loading 16 at once measured slower:
-// most pairs have few partials, and the stale slots cost traffic.)
+// costs one round trip to memory; the rest of a pair's partials (at most
+// kMaxParts - kFirst, only those below the count) then load together, a
+// second round trip.  (Loading 16 with the count measured slower: most
+// pairs have few partials, and the stale slots cost traffic.)
 template <int HP>
 __global__ void __launch_bounds__(512) qdecode_combine_kernel(DecodeArgs a, int D) {
   constexpr int kFirst = 4;
@@ -1021,12 +1023,13 @@ __global__ void __launch_bounds__(512) qdecode_combine_kernel(DecodeArgs a, int 
   if (r >= HP) return;
   float M = -INFINITY, L = 0.0f;
   f32x4_t o = {0.f, 0.f, 0.f, 0.f};
-  auto merge = [&](int k0, int cnt, const f32x2_t* ml, const f32x4_t* oo) __attribute__((always_inline)) {
-    float mm[kFirst];
+  auto merge = [&](int k0, auto N_, const f32x2_t* ml, const f32x4_t* oo) __attribute__((always_inline)) {
+    constexpr int N = decltype(N_)::value;
+    float mm[N];
     float Mn = M;
 #pragma unroll
-    for (int q = 0; q < kFirst; q++) {
-      mm[q] = (q < cnt && k0 + q < K) ? ml[q][0] : -INFINITY;
+    for (int q = 0; q < N; q++) {
+      mm[q] = k0 + q < K ? ml[q][0] : -INFINITY;
       Mn = fmaxf(Mn, mm[q]);
     }
     const float f = M == -INFINITY ? 0.0f : exp2f((M - Mn) * kLog2e);
@@ -1034,7 +1037,7 @@ __global__ void __launch_bounds__(512) qdecode_combine_kernel(DecodeArgs a, int 
 #pragma unroll
     for (int e = 0; e < 4; e++) o[e] *= f;
 #pragma unroll
-    for (int q = 0; q < kFirst; q++) {
+    for (int q = 0; q < N; q++) {
       // stale slots: weight 0, and their (possibly non-finite) values are
       // selected away rather than multiplied by it
       const bool live = mm[q] != -INFINITY;
@@ -1055,18 +1058,24 @@ __global__ void __launch_bounds__(512) qdecode_combine_kernel(DecodeArgs a, int 
       oo[q] = *reinterpret_cast<const f32x4_t*>(a.ws_o + slot * D + d);
     }
     if (len == 0 || K <= 1 || r >= nh) return;  // written by the decode kernel itself
-    merge(0, kFirst, ml, oo);
+    merge(0, std::integral_constant<int, kFirst>{}, ml, oo);
   }
-  for (int k0 = kFirst; k0 < K; k0 += kFirst) {
-    f32x2_t ml[kFirst];
-    f32x4_t oo[kFirst];
+  if (K > kFirst) {
+    constexpr int kRest = kMaxParts - kFirst;
+    f32x2_t ml[kRest];
+    f32x4_t oo[kRest];
 #pragma unroll
-    for (int q = 0; q < kFirst; q++) {
-      const int64_t slot = (slot0 + min(k0 + q, K - 1)) * HP + r;
-      ml[q] = *reinterpret_cast<const f32x2_t*>(a.ws_ml + slot * 2);
-      oo[q] = *reinterpret_cast<const f32x4_t*>(a.ws_o + slot * D + d);
+    for (int q = 0; q < kRest; q++) {
+      if (kFirst + q < K) {
+        const int64_t slot = (slot0 + kFirst + q) * HP + r;
+        ml[q] = *reinterpret_cast<const f32x2_t*>(a.ws_ml + slot * 2);
+        oo[q] = *reinterpret_cast<const f32x4_t*>(a.ws_o + slot * D + d);
+      } else {
+        ml[q] = f32x2_t{-INFINITY, 0.0f};
+        oo[q] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
     }
-    merge(k0, kFirst, ml, oo);
+    merge(kFirst, std::integral_constant<int, kRest>{}, ml, oo);
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
   u32x2_t v;
