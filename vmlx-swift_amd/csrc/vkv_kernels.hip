@@ -201,6 +201,8 @@ __global__ void __launch_bounds__(256) append_affine_kernel(RowSrc sk, RowSrc sv
   const int64_t n = static_cast<int64_t>(blockIdx.x) * 8 + i;
   const int h = blockIdx.y * hb + hl;
   const bool active = n < ntok && h < H;
+  // the token's slot (a block-table read) goes out with the row's load
+  const int64_t slot = active ? token_slot(dst, n) : -1;
 
   float v[8];
   if (active) {
@@ -231,7 +233,6 @@ __global__ void __launch_bounds__(256) append_affine_kernel(RowSrc sk, RowSrc sv
     const float x = fminf(roundf((v[e] - bias) / scale), n_bins);
     code[e] = x > 0.0f ? static_cast<uint32_t>(x) : 0u;
   }
-  const int64_t slot = active ? token_slot(dst, n) : -1;
   const int g = (j * 8) / GROUP;
   if (slot >= 0 && (j % TEAM) == 0) {
     uint8_t* chunk = dst.base + (slot / dst.block_size) * dst.block_bytes + h * dst.head_bytes;
@@ -250,7 +251,7 @@ __global__ void __launch_bounds__(256) append_affine_kernel(RowSrc sk, RowSrc sv
   // ---- 4-bit V
   __shared__ int64_t tok_slot[8];
   __shared__ uint8_t vcode[8][256];  // [token][head * D + dim], hb * D = 256
-  if (hl == 0 && j == 0) tok_slot[i] = (n < ntok) ? token_slot(dst, n) : -1;
+  if (hl == 0 && j == 0) tok_slot[i] = slot;  // hl 0: a head below H, so slot is n's
   __syncthreads();
   const int64_t s0 = tok_slot[0];
   bool aligned = s0 >= 0 && s0 % 8 == 0;
