@@ -67,6 +67,33 @@ void copy_tokens(const Dense4& dst, int64_t dt0, const vkv_array& src, int64_t s
   launch_copy4d(es, sp, shape, sstr, dp, dstr, st);
 }
 
+// copy_tokens of K and V (tokens [st0, st0 + len) of each into [dt0, ..)),
+// in one launch when they share an element size.
+void copy_tokens_kv(const Dense4& dk, const Dense4& dv, int64_t dt0, const vkv_array& k,
+                    const vkv_array& v, int64_t st0, int64_t len, hipStream_t st) {
+  if (len <= 0) return;
+  const int es = elem_bytes(k.dtype);
+  if (elem_bytes(v.dtype) != es) {
+    copy_tokens(dk, dt0, k, st0, len, st);
+    copy_tokens(dv, dt0, v, st0, len, st);
+    return;
+  }
+  auto desc = [&](const Dense4& d, const vkv_array& a) {
+    Copy4D c;
+    c.src = static_cast<const uint8_t*>(a.data) + st0 * a.strides[2] * es;
+    c.dst = d.buf->bytes() + dt0 * d.D * es;
+    const int64_t n[4] = {a.shape[0], a.shape[1], len, a.shape[3]};
+    const int64_t dd[4] = {d.H * d.cap * d.D, d.cap * d.D, d.D, 1};
+    for (int i = 0; i < 4; i++) {
+      c.n[i] = n[i];
+      c.s[i] = a.strides[i];
+      c.d[i] = dd[i];
+    }
+    return c;
+  };
+  launch_copy4d_pair(es, desc(dk, k), desc(dv, v), st);
+}
+
 void copy_dense(const Dense4& dst, int64_t dt0, const Dense4& src, int64_t st0, int64_t len,
                        hipStream_t st) {
   copy_tokens(dst, dt0, src.view(src.cap), st0, len, st);
@@ -167,8 +194,7 @@ void SimpleCache::update(const vkv_array& k, const vkv_array& v, hipStream_t st,
     }
   }
   offset += Sn;
-  copy_tokens(k_, prev, k, 0, Sn, st);
-  copy_tokens(v_, prev, v, 0, Sn, st);
+  copy_tokens_kv(k_, v_, prev, k, v, 0, Sn, st);
   *ok = k_.view(offset);
   *ov = v_.view(offset);
 }
@@ -329,8 +355,7 @@ bool RotatingCache::update_in_place(const vkv_array& k, const vkv_array& v, hipS
     update_concat(k, v, st);
     return false;
   }
-  copy_tokens(k_, idx_, k, 0, Sn, st);
-  copy_tokens(v_, idx_, v, 0, Sn, st);
+  copy_tokens_kv(k_, v_, idx_, k, v, 0, Sn, st);
   offset += Sn;
   idx_ += Sn;
   return true;

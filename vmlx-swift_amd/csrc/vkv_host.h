@@ -83,6 +83,8 @@ Dense4 alloc_dense(int64_t B, int64_t H, int64_t cap, int64_t D, int dtype, bool
 // dst[:, :, dt0:dt0+len, :] = src[:, :, st0:st0+len, :] (same dtype)
 void copy_tokens(const Dense4& dst, int64_t dt0, const vkv_array& src, int64_t st0, int64_t len,
                  hipStream_t st);
+void copy_tokens_kv(const Dense4& dk, const Dense4& dv, int64_t dt0, const vkv_array& k,
+                    const vkv_array& v, int64_t st0, int64_t len, hipStream_t st);
 void copy_dense(const Dense4& dst, int64_t dt0, const Dense4& src, int64_t st0, int64_t len,
                 hipStream_t st);
 Dense4 dense_from_array(const vkv_array& a, hipStream_t st);

@@ -136,6 +136,14 @@ void launch_gather(const GatherArgs& g, int out_kind, hipStream_t st);
 // Strided 4-D copy (element size 2 or 4): dst[i] = src[i].
 void launch_copy4d(int esize, const void* src, const int64_t* shape, const int64_t* sstr,
                    void* dst, const int64_t* dstr, hipStream_t st);
+// One strided 4-D copy (element strides) for launch_copy4d_pair.
+struct Copy4D {
+  const void* src;
+  void* dst;
+  int64_t n[4], s[4], d[4];
+};
+// Two copies of one element size in one launch.
+void launch_copy4d_pair(int esize, const Copy4D& c0, const Copy4D& c1, hipStream_t st);
 void launch_fill_normal(int dtype, void* data, int64_t n, uint64_t seed, float std,
                         hipStream_t st);
 void launch_attention(int dtype, int bits, int group, bool quant_semantics,

@@ -652,6 +652,27 @@ __global__ void __launch_bounds__(256) copy4d_kernel(const U* src, U* dst, int64
   }
 }
 
+// Two strided 4-D copies of one element size in one launch (blockIdx.y
+// picks the copy): a cache update writes its K and V tokens with one launch.
+template <typename U>
+__global__ void __launch_bounds__(256) copy4d_pair_kernel(Copy4D c0, Copy4D c1) {
+  const Copy4D& c = blockIdx.y ? c1 : c0;
+  const int64_t total = c.n[0] * c.n[1] * c.n[2] * c.n[3];
+  const U* src = static_cast<const U*>(c.src);
+  U* dst = static_cast<U*>(c.dst);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    int64_t i3 = i % c.n[3];
+    int64_t r = i / c.n[3];
+    int64_t i2 = r % c.n[2];
+    r /= c.n[2];
+    int64_t i1 = r % c.n[1];
+    int64_t i0 = r / c.n[1];
+    dst[i0 * c.d[0] + i1 * c.d[1] + i2 * c.d[2] + i3 * c.d[3]] =
+        src[i0 * c.s[0] + i1 * c.s[1] + i2 * c.s[2] + i3 * c.s[3]];
+  }
+}
+
 // Whole-block copy across all layers (copy-on-write, prefix store).  The
 // (src, dst) pairs travel in the kernel arguments, so no device staging
 // buffer has to outlive the launch.
@@ -1218,6 +1239,23 @@ void launch_copy4d(int esize, const void* src, const int64_t* n, const int64_t* 
   } else {
     throw Error("copy4d: element size must be 1, 2 or 4");
   }
+  VKV_HIP(hipGetLastError());
+}
+
+void launch_copy4d_pair(int esize, const Copy4D& c0, const Copy4D& c1, hipStream_t st) {
+  const int64_t t0 = c0.n[0] * c0.n[1] * c0.n[2] * c0.n[3];
+  const int64_t t1 = c1.n[0] * c1.n[1] * c1.n[2] * c1.n[3];
+  const int64_t total = std::max(t0, t1);
+  if (total <= 0) return;
+  const dim3 grid(static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 65536)), 2);
+  if (esize == 2)
+    hipLaunchKernelGGL((copy4d_pair_kernel<uint16_t>), grid, dim3(256), 0, st, c0, c1);
+  else if (esize == 4)
+    hipLaunchKernelGGL((copy4d_pair_kernel<uint32_t>), grid, dim3(256), 0, st, c0, c1);
+  else if (esize == 1)
+    hipLaunchKernelGGL((copy4d_pair_kernel<uint8_t>), grid, dim3(256), 0, st, c0, c1);
+  else
+    throw Error("copy4d: element size must be 1, 2 or 4");
   VKV_HIP(hipGetLastError());
 }
 
