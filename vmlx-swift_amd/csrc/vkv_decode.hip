@@ -377,12 +377,7 @@ qdecode_kernel(DecodeArgs a) {
   int32_t(*seg_tab)[7] = seg_tab_g[wv];
 
   const int lane = threadIdx.x & 63, n = lane & 15, lg = lane >> 4;
-  // Workgroups go to the 8 XCDs in id order (id % 8); XCD x takes the x-th
-  // eighth of the ranges, so the sequences that share prefix blocks meet
-  // in few XCDs' L2 caches instead of every one.
-  const int nwg = gridDim.x;
-  const int wg = (nwg % 8 == 0) ? (blockIdx.x % 8) * (nwg / 8) + blockIdx.x / 8 : blockIdx.x;
-  const int w = wg * WPG + wv, W = nwg * WPG;
+  const int w = blockIdx.x * WPG + wv, W = gridDim.x * WPG;
   const int ns = a.n_seqs;
 
   // ---- sequence lengths first (the set-up is a chain of dependent loads):
