@@ -1005,11 +1005,14 @@ qdecode_kernel(DecodeArgs a) {
 // dims of one head.  The pair's partial count, its length and its first
 // kFirst partials load together (the partial slots past the count hold
 // stale data, which the merge masks), so a pair of up to kFirst partials
-// costs one round trip to memory; the rest of a pair's partials (at most
-// kMaxParts - kFirst, only those below the count) then load together, a
-// second round trip.  (Loading 16 with the count measured slower: most
-// pairs have few partials, and the stale slots cost traffic.)
-template <int HP>
+// costs one round trip to memory.  With REST the rest of a pair's partials
+// (at most kMaxParts - kFirst, only those below the count) then load
+// together, a second round trip; without it they load kFirst at a time (the
+// host picks REST when launches average more than kFirst waves per pair:
+// the larger kernel measured slower where pairs have few partials).
+// (Loading 16 with the count measured slower: most pairs have few
+// partials, and the stale slots cost traffic.)
+template <int HP, bool REST>
 __global__ void __launch_bounds__(512) qdecode_combine_kernel(DecodeArgs a, int D) {
   constexpr int kFirst = 4;
   const int rep = a.rep, n_hg = (rep + HP - 1) / HP, HG = a.Hkv * n_hg;
@@ -1060,7 +1063,19 @@ __global__ void __launch_bounds__(512) qdecode_combine_kernel(DecodeArgs a, int 
     if (len == 0 || K <= 1 || r >= nh) return;  // written by the decode kernel itself
     merge(0, std::integral_constant<int, kFirst>{}, ml, oo);
   }
-  if (K > kFirst) {
+  if (!REST) {
+    for (int k0 = kFirst; k0 < K; k0 += kFirst) {
+      f32x2_t ml[kFirst];
+      f32x4_t oo[kFirst];
+#pragma unroll
+      for (int q = 0; q < kFirst; q++) {
+        const int64_t slot = (slot0 + min(k0 + q, K - 1)) * HP + r;
+        ml[q] = *reinterpret_cast<const f32x2_t*>(a.ws_ml + slot * 2);
+        oo[q] = *reinterpret_cast<const f32x4_t*>(a.ws_o + slot * D + d);
+      }
+      merge(k0, std::integral_constant<int, kFirst>{}, ml, oo);
+    }
+  } else if (K > kFirst) {
     constexpr int kRest = kMaxParts - kFirst;
     f32x2_t ml[kRest];
     f32x4_t oo[kRest];
@@ -1158,17 +1173,24 @@ static void launch_d(const DecodeArgs& a, hipStream_t st) {
   constexpr int wpg = qd_waves<D>();
   const dim3 grid((a.n_waves + wpg - 1) / wpg), block(64 * wpg);
   const int pairs = a.n_seqs * a.Hkv * qdecode_head_groups(a.rep);
+  const bool rest = a.n_waves > 4 * pairs;  // more than kFirst partials per pair on average
   const TimedLaunch tl = timing_prepare(kTimeDecode);
   if (heads_per_part(a.rep) == 4) {
     hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, 4>), grid, block, 0, st, tl.start, tl.stop, 0, a);
     VKV_HIP(hipGetLastError());
     timing_commit(tl);
-    hipLaunchKernelGGL(qdecode_combine_kernel<4>, dim3(pairs), dim3(D), 0, st, a, D);
+    if (rest)
+      hipLaunchKernelGGL((qdecode_combine_kernel<4, true>), dim3(pairs), dim3(D), 0, st, a, D);
+    else
+      hipLaunchKernelGGL((qdecode_combine_kernel<4, false>), dim3(pairs), dim3(D), 0, st, a, D);
   } else {
     hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, 8>), grid, block, 0, st, tl.start, tl.stop, 0, a);
     VKV_HIP(hipGetLastError());
     timing_commit(tl);
-    hipLaunchKernelGGL(qdecode_combine_kernel<8>, dim3(pairs), dim3(2 * D), 0, st, a, D);
+    if (rest)
+      hipLaunchKernelGGL((qdecode_combine_kernel<8, true>), dim3(pairs), dim3(2 * D), 0, st, a, D);
+    else
+      hipLaunchKernelGGL((qdecode_combine_kernel<8, false>), dim3(pairs), dim3(2 * D), 0, st, a, D);
   }
   VKV_HIP(hipGetLastError());
 }
