@@ -910,9 +910,11 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(AttnArgs a, int h_off
 }
 
 // One wave per (row, head): lane l merges dims l, l + 64, .. (Dv <= 256).
-// The (max, sum) pairs and partial rows of up to 8 parts are loaded before
-// any is used, so a merge costs one memory round trip per 8 parts.
-template <int DT>
+// The (max, sum) pairs and partial rows of up to NP parts are loaded before
+// any is used, so a merge costs one memory round trip per NP parts (NP = 2,
+// 4 or 8, the smallest that holds the launch's parts, so few parts load no
+// clamped duplicates).
+template <int DT, int NP = 8>
 __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int64_t n_rh) {
   using E = Elem<DT>;
   const int64_t rh = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // row * Hq + h
@@ -926,10 +928,10 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int64_t n
   const float* wo = a.ws_o + rh * a.n_parts * a.Dv;
   float M = -3.402823466e38f, den = 0.0f;
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int c = 0; c < a.n_parts; c += 8) {
-    float m[8], ls[8], v[8][4];
+  for (int c = 0; c < a.n_parts; c += NP) {
+    float m[NP], ls[NP], v[NP][4];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
+    for (int j = 0; j < NP; j++) {
       const int p = min(c + j, a.n_parts - 1);  // (clamped slots are selected away)
       m[j] = ml[2 * p];
       ls[j] = ml[2 * p + 1];
@@ -941,7 +943,7 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int64_t n
     }
     float Mc = M;
 #pragma unroll
-    for (int j = 0; j < 8; j++)
+    for (int j = 0; j < NP; j++)
       if (c + j < a.n_parts) Mc = fmaxf(Mc, m[j]);
     const float r = __expf(M - Mc);
     den *= r;
@@ -949,7 +951,7 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int64_t n
     for (int i = 0; i < 4; i++) acc[i] *= r;
     M = Mc;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
+    for (int j = 0; j < NP; j++) {
       if (c + j < a.n_parts) {
         const float w = __expf(m[j] - M);
         den += w * ls[j];
@@ -1350,12 +1352,22 @@ void launch_attn_combine(int dtype, const AttnArgs& a, int64_t rows, hipStream_t
     return;
   }
   const dim3 grid(static_cast<unsigned>((n_rh + 3) / 4));
+  const int np = a.n_parts <= 2 ? 2 : a.n_parts <= 4 ? 4 : 8;
+#define VKV_C(T, N) hipLaunchKernelGGL((attn_combine_kernel<T, N>), grid, dim3(256), 0, st, a, n_rh)
+#define VKV_CD(T)                   \
+  do {                              \
+    if (np == 2) VKV_C(T, 2);       \
+    else if (np == 4) VKV_C(T, 4);  \
+    else VKV_C(T, 8);               \
+  } while (0)
   switch (dtype) {
-    case kF32: hipLaunchKernelGGL((attn_combine_kernel<kF32>), grid, dim3(256), 0, st, a, n_rh); break;
-    case kF16: hipLaunchKernelGGL((attn_combine_kernel<kF16>), grid, dim3(256), 0, st, a, n_rh); break;
-    case kBF16: hipLaunchKernelGGL((attn_combine_kernel<kBF16>), grid, dim3(256), 0, st, a, n_rh); break;
+    case kF32: VKV_CD(kF32); break;
+    case kF16: VKV_CD(kF16); break;
+    case kBF16: VKV_CD(kBF16); break;
     default: throw Error("unsupported dtype");
   }
+#undef VKV_CD
+#undef VKV_C
   VKV_HIP(hipGetLastError());
 }
 
