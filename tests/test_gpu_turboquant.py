@@ -3,7 +3,7 @@ TQEncoder.swift) against the TurboQuant restatement (oracle.tq_*), which
 tests/test_oracle_turboquant.py pins:
 
   * fromSimpleCache on f16 / bf16 / f32 K/V at D 64, 80 (blockwise
-    rotation), 128 and 256 with several bit widths: the encoded records (the
+    rotation), 128 and 256 with 1- to 8-bit codes: the encoded records (the
     packed codes and QJL signs, both norms, the exact sink and tail tokens)
     and the decoded unified buffer (its values and its promoted dtype) are
     bit-exact;
@@ -74,6 +74,7 @@ CASES = [  # dtype, B, H, T, D, key bits, value bits, sink, residual
     (O.F32, 2, 2, 90, 64, 2, 4, 0, 0),
     (O.BF16, 1, 2, 300, 256, 3, 3, 4, 16),
     (O.F16, 2, 3, 77, 80, 3, 5, 2, 7),
+    (O.BF16, 1, 2, 120, 128, 9, 8, 4, 8),  # 8-bit codes: four to a word
 ]
 
 
