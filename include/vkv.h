@@ -248,7 +248,12 @@ enum {
    * float buffer followed by a float window.  vkv_cache_create gives the
    * reference's defaults (keyBits 3, valueBits 3, 4 sink tokens, 64
    * residual tokens; params.bits > 0 sets both bit widths). */
-  VKV_CACHE_TURBOQUANT = 5
+  VKV_CACHE_TURBOQUANT = 5,
+  /* CompilableTurboQuantKVCache (BatchEngine/CompilableTurboQuantKVCache.swift:
+   * 57-294): a compressed TurboQuantKVCache whose window writes go to the
+   * offset held in device memory (update returns the whole unified buffers,
+   * makeMask an array mask over them); made by vkv_turboquant_to_compilable. */
+  VKV_CACHE_COMPILABLE_TURBOQUANT = 6
 };
 
 typedef struct vkv_cache_params {
@@ -442,10 +447,21 @@ int vkv_cache_to_compilable(vkv_cache src, int64_t max_length, void *stream, vkv
  * a new cache with src's keep/maxSize/step, ring index and offset, and its
  * buffers extended with zeros to maxSize. */
 int vkv_cache_to_compilable_rotating(vkv_cache rotating, void *stream, vkv_cache *out);
+/* CompilableTurboQuantKVCache(from:) (CompilableTurboQuantKVCache.swift:
+ * 110-160): a new cache restored from tq's encoded records and window
+ * (restoreCompressed), its window write position and offset copied to
+ * device counters.  tq must be in the compressed phase.  In that phase
+ * update writes the new tokens (cast to the unified buffers' dtype, as the
+ * reference's dynamicSliceUpdate does) at the device offset, clamped so
+ * they fit, advances both counters and the host offset, and returns the
+ * whole unified buffers; fill-phase updates are TurboQuantKVCache's. */
+int vkv_turboquant_to_compilable(vkv_cache tq, void *stream, vkv_cache *out);
 /* innerState: the arrays a captured step reads and writes in place —
  * keys and values [B,H,max,D], then the counters as int32 [1] device arrays:
- * the offset (CompilableKVCache.swift:108-113), or the ring index then the
- * offset (CompilableRotatingKVCache.swift:255-264).  `arrays` has room for 4. */
+ * the offset (CompilableKVCache.swift:108-113), the ring index then the
+ * offset (CompilableRotatingKVCache.swift:255-264), or the window write
+ * position then the offset (CompilableTurboQuantKVCache.swift:286-293, the
+ * unified buffers first).  `arrays` has room for 4. */
 int vkv_cache_inner_state(vkv_cache cache, vkv_array *arrays, int32_t *count);
 
 /* dynamicSliceUpdate(src, update:, start:, axes: [axis])

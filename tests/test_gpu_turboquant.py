@@ -293,3 +293,92 @@ def test_disk_record_with_turboquant_layers(tmp_path):
         assert isinstance(got, vkv.KVCacheSimple) and got.offset == src.offset
         for a, b in zip(src.state, got.state):
             assert torch.equal(a.cpu(), b.cpu())
+
+
+def _compressed(rng, dtype, B=1, H=2, T=120, D=64):
+    k = rand_bits(rng, (B, H, T, D), dtype)
+    v = rand_bits(rng, (B, H, T, D), dtype)
+    return vkv.TurboQuantKVCache.from_simple_cache(_simple(k, v, dtype), 3, 3, 4, 16)
+
+
+@pytest.mark.parametrize("dtype", [O.BF16, O.F16])
+def test_compilable_turboquant_follows_the_parent(dtype):
+    """CompilableTurboQuantKVCache(from:) then decode steps: the whole unified
+    buffers it returns hold, at [0, offset), exactly what the parent cache
+    returns for the same steps (bf16 tokens are cast into the f32 unified
+    buffer, f16 ones written as they are); the device counters are the
+    window position and the offset; attention over the whole buffers with
+    its array mask equals attention over the parent's views."""
+    rng = np.random.default_rng(7 + dtype)
+    D = 64
+    tq = _compressed(rng, dtype, D=D)
+    c = vkv.CompilableTurboQuantKVCache.from_turboquant(tq)
+    assert c.kind == vkv.CACHE_COMPILABLE_TURBOQUANT and c.offset == tq.offset == 120
+    win0 = tq.info["window_tokens"]
+    for step in range(5):
+        k1 = dev(rand_bits(rng, (1, 2, 1, D), dtype), dtype)
+        v1 = dev(rand_bits(rng, (1, 2, 1, D), dtype), dtype)
+        q = dev(rand_bits(rng, (1, 8, 1, D), dtype), dtype)
+        mask = c.make_mask(1)
+        ck, cv = (vkv.to_torch(x) for x in c.update(k1, v1))
+        tk, tv = (vkv.to_torch(x) for x in tq.update(k1, v1))
+        n = tq.offset
+        assert c.offset == n == 121 + step
+        assert ck.shape[2] >= n and ck.dtype == tk.dtype
+        assert torch.equal(ck[:, :, :n], tk) and torch.equal(cv[:, :, :n], tv), step
+        m = host(mask)
+        assert m.shape == (1, ck.shape[2]) and m[0, :n].all() and not m[0, n:].any()
+        inner = c.inner_state()
+        assert len(inner) == 4 and inner[0].shape[2] == ck.shape[2]
+        assert int(host(vkv.to_torch(inner[2]))[0]) == win0 + step + 1
+        assert int(host(vkv.to_torch(inner[3]))[0]) == n
+        a = vkv.scaled_dot_product_attention(q, ck.to(q.dtype), cv.to(q.dtype), D ** -0.5,
+                                             mask=mask)
+        b = vkv.scaled_dot_product_attention(q, tk.to(q.dtype), tv.to(q.dtype), D ** -0.5)
+        assert torch.allclose(a.float(), b.float(), atol=2e-2, rtol=2e-2), step
+
+
+def test_compilable_turboquant_graph_replay():
+    """make_mask + update + attention on the compilable cache captured once
+    in a HIP graph and replayed with new tokens copied in between: every
+    replay equals the same step run eagerly on a twin, and the offset the
+    device holds advances by one per replay."""
+    dtype, D = O.F16, 64
+    rng = np.random.default_rng(77)
+    src = _compressed(rng, dtype, D=D)
+    cap = vkv.CompilableTurboQuantKVCache.from_turboquant(src)
+    twin = vkv.CompilableTurboQuantKVCache.from_turboquant(src)
+    kin = torch.zeros((1, 2, 1, D), dtype=torch.float16, device="cuda")
+    vin = torch.zeros_like(kin)
+    qin = torch.zeros((1, 8, 1, D), dtype=torch.float16, device="cuda")
+    out = torch.empty((1, 8, 1, D), dtype=torch.float16, device="cuda")
+
+    def step(cache, o):
+        mask = cache.make_mask(1)
+        ck, cv = cache.update(kin, vin)
+        vkv.scaled_dot_product_attention(qin, ck, cv, D ** -0.5, mask=mask, out=o)
+
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        warm = vkv.CompilableTurboQuantKVCache.from_turboquant(src)
+        step(warm, torch.empty_like(out))
+        cap.make_mask(1)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            step(cap, out)
+    torch.cuda.synchronize()
+    for r in range(4):
+        kin.copy_(dev(rand_bits(rng, (1, 2, 1, D), dtype), dtype))
+        vin.copy_(dev(rand_bits(rng, (1, 2, 1, D), dtype), dtype))
+        qin.copy_(dev(rand_bits(rng, (1, 8, 1, D), dtype), dtype))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        eager = torch.empty_like(out)
+        step(twin, eager)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), r
+        assert int(host(vkv.to_torch(cap.inner_state()[3]))[0]) == 121 + r

@@ -984,6 +984,8 @@ int vkv_cache_inner_state(vkv_cache cache, vkv_array* arrays, int32_t* count) {
       *count = c->inner_state(arrays);
     else if (auto* r = dynamic_cast<CompilableRotatingCache*>(cache->impl.get()))
       *count = r->inner_state(arrays);
+    else if (auto* t = dynamic_cast<CompilableTurboQuantCache*>(cache->impl.get()))
+      *count = t->inner_state(arrays);
     else
       throw Error("innerState is exposed for the fixed-buffer (compilable) caches only");
   });

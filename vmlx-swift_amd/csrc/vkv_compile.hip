@@ -90,6 +90,13 @@ __global__ void counter_advance_kernel(int32_t* ctr, int32_t n, int32_t ring, in
   }
 }
 
+__global__ void counter_advance_both_kernel(int32_t* ctr, int32_t n) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    ctr[0] += n;
+    ctr[1] += n;
+  }
+}
+
 __global__ void counter_set_kernel(int32_t* ctr, int32_t offset, int32_t idx) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
     ctr[0] = offset;
@@ -219,6 +226,11 @@ void launch_dyn_copy(int esize, const DynCopy& c, hipStream_t st) {
 
 void launch_counter_advance(int32_t* ctr, int n, int ring, int max_size, int keep, hipStream_t st) {
   hipLaunchKernelGGL(counter_advance_kernel, dim3(1), dim3(64), 0, st, ctr, n, ring, max_size, keep);
+  VKV_HIP(hipGetLastError());
+}
+
+void launch_counter_advance_both(int32_t* ctr, int n, hipStream_t st) {
+  hipLaunchKernelGGL(counter_advance_both_kernel, dim3(1), dim3(64), 0, st, ctr, n);
   VKV_HIP(hipGetLastError());
 }
 

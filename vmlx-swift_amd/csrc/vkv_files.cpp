@@ -506,7 +506,8 @@ const char* class_name(int kind) {
     case VKV_CACHE_ROTATING:
     case VKV_CACHE_COMPILABLE_ROTATING: return "RotatingKVCache";
     case VKV_CACHE_QUANTIZED: return "QuantizedKVCache";
-    case VKV_CACHE_TURBOQUANT: return "TurboQuantKVCache";  // not loadable, as in the reference
+    case VKV_CACHE_TURBOQUANT:
+    case VKV_CACHE_COMPILABLE_TURBOQUANT: return "TurboQuantKVCache";  // not loadable, as in the reference
     default: return "KVCache";  // KVCacheSimple and the fixed-buffer cache
   }
 }
@@ -890,7 +891,7 @@ int vkv_disk_cache_save(const char* path, const vkv_cache* caches, int32_t n_cac
       const std::string I = std::to_string(i);
       const std::string kind_key = "__layer_kind_" + I + "__";
       const int kind = c.kind();
-      if (kind == VKV_CACHE_TURBOQUANT) {
+      if (kind == VKV_CACHE_TURBOQUANT || kind == VKV_CACHE_COMPILABLE_TURBOQUANT) {
         auto* t = static_cast<TurboQuantCache*>(&c);
         if (t->phase_ == 1 && t->ck_ && t->cv_) {
           save_tq_layer(*t, I, ts, st);

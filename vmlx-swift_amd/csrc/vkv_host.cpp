@@ -160,6 +160,9 @@ std::unique_ptr<Cache> make_cache(const vkv_cache_params& p) {
     case VKV_CACHE_TURBOQUANT:
       return std::make_unique<TurboQuantCache>(p.bits > 0 ? p.bits : 3, p.bits > 0 ? p.bits : 3, 4,
                                                64);
+    case VKV_CACHE_COMPILABLE_TURBOQUANT:  // the direct init (:89-108): the parent's fill phase
+      return std::make_unique<CompilableTurboQuantCache>(p.bits > 0 ? p.bits : 3,
+                                                         p.bits > 0 ? p.bits : 3, 4, 64);
     default: throw Error("unknown cache kind");
   }
 }
@@ -690,6 +693,96 @@ int CompilableCache::inner_state(vkv_array* out) {
     out[c++] = k_.view(k_.cap);
     out[c++] = v_.view(v_.cap);
   }
+  out[c++] = counter_array(ctr_, 0);
+  return c;
+}
+
+// ------------------------------------------ CompilableTurboQuantKVCache
+
+CompilableTurboQuantCache::CompilableTurboQuantCache(int key_bits, int value_bits, int sink,
+                                                     int residual)
+    : TurboQuantCache(key_bits, value_bits, sink, residual), ctr_(make_counters()) {}
+
+// init(from:) (CompilableTurboQuantKVCache.swift:110-160): restoreCompressed
+// from the source's records and window, then the counters from its window
+// position and offset
+std::unique_ptr<CompilableTurboQuantCache> CompilableTurboQuantCache::from(TurboQuantCache& src,
+                                                                           hipStream_t st) {
+  if (src.phase_ != 1 || !src.ck_ || !src.cv_)
+    throw Error("CompilableTurboQuantKVCache(from:) requires a cache in the compressed phase");
+  auto c = std::make_unique<CompilableTurboQuantCache>(src.key_bits_, src.value_bits_, src.sink_,
+                                                       src.residual_);
+  vkv_tq_encoded ek{}, ev{};
+  src.encoded(&ek, &ev);
+  vkv_array wk{}, wv{};
+  const bool window = src.window_state(&wk, &wv);
+  c->restore_compressed(ek, ev, src.offset, window ? &wk : nullptr, window ? &wv : nullptr, st);
+  launch_counter_set(static_cast<int32_t*>(c->ctr_.get()), static_cast<int32_t>(c->offset),
+                     static_cast<int32_t>(c->window_), st);
+  c->last_ = st;
+  return c;
+}
+
+// update (:168-224): the fill phase is the parent's; compressed, the new
+// tokens go to the unified buffers at the device offset (dynamicSliceUpdate:
+// cast to the buffers' dtype, start clamped so they fit), both counters and
+// the host offset and window position advance, and the whole buffers return
+void CompilableTurboQuantCache::update(const vkv_array& k, const vkv_array& v, hipStream_t st,
+                                       vkv_array* ok, vkv_array* ov) {
+  if (phase_ != 1 || uk_.empty()) {
+    TurboQuantCache::update(k, v, st, ok, ov);
+    return;
+  }
+  check_kv_pair(k, v);
+  if (k.shape[0] != uk_.B || k.shape[1] != uk_.H || k.shape[3] != uk_.D || v.shape[3] != uv_.D)
+    throw Error("keys and values do not match the cache's unified buffers");
+  const int64_t S = k.shape[2];
+  if (S > uk_.cap) throw Error("update is longer than the unified buffers");
+  int32_t* ctr = static_cast<int32_t*>(ctr_.get());
+  auto put = [&](const Dense4& d, const vkv_array& a, DevBuf& tmp) {
+    if (a.dtype == d.dtype) {
+      write_at_device_offset(d, a, ctr, st);
+      return;
+    }
+    const int64_t shape[4] = {a.shape[0], a.shape[1], S, a.shape[3]};
+    const int64_t dstr[4] = {a.shape[1] * S * a.shape[3], S * a.shape[3], a.shape[3], 1};
+    tmp.ensure(static_cast<size_t>(shape[0] * dstr[0]) * elem_bytes(d.dtype));
+    launch_cast4d(a.data, a.dtype, shape, a.strides, tmp.get(), d.dtype, dstr, st);
+    vkv_array c{};
+    c.data = tmp.get();
+    c.dtype = d.dtype;
+    c.ndim = 4;
+    for (int i = 0; i < 4; i++) {
+      c.shape[i] = shape[i];
+      c.strides[i] = dstr[i];
+    }
+    write_at_device_offset(d, c, ctr, st);
+  };
+  put(uk_, k, cast_k_);
+  put(uv_, v, cast_v_);
+  launch_counter_advance_both(ctr, static_cast<int>(S), st);
+  last_ = st;
+  offset += S;
+  window_ += S;
+  *ok = uk_.view(uk_.cap);
+  *ov = uv_.view(uv_.cap);
+}
+
+// makeMask (:226-284): an array mask [n, buffer length] from the device
+// offset, row i seeing positions <= offset + i (within the window if given)
+int CompilableTurboQuantCache::make_mask(int n, int window, bool return_array, hipStream_t st,
+                                         vkv_array* mask) {
+  if (phase_ != 1 || uk_.empty()) return TurboQuantCache::make_mask(n, window, return_array, st, mask);
+  return full_mask(masks_, ctr_, n, uk_.cap, window, 0, st, mask);
+}
+
+int CompilableTurboQuantCache::inner_state(vkv_array* out) {
+  int c = 0;
+  if (!uk_.empty()) {
+    out[c++] = uk_.view(uk_.cap);
+    out[c++] = uv_.view(uv_.cap);
+  }
+  out[c++] = counter_array(ctr_, 1);
   out[c++] = counter_array(ctr_, 0);
   return c;
 }

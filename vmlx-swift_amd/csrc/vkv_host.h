@@ -417,6 +417,27 @@ class TurboQuantCache : public Cache {
   void seat(std::shared_ptr<TqEncoded> ek, std::shared_ptr<TqEncoded> ev, hipStream_t st);
   void append_window(const vkv_array& k, const vkv_array& v, hipStream_t st);
 };
+// CompilableTurboQuantKVCache (BatchEngine/CompilableTurboQuantKVCache.swift:
+// 57-294): compressed-phase window writes at the offset held in device
+// memory (ctr[0] = offset, ctr[1] = window write position).
+class CompilableTurboQuantCache : public TurboQuantCache {
+ public:
+  CompilableTurboQuantCache(int key_bits, int value_bits, int sink, int residual);
+  int kind() const override { return VKV_CACHE_COMPILABLE_TURBOQUANT; }
+  void update(const vkv_array& k, const vkv_array& v, hipStream_t st, vkv_array* ok,
+              vkv_array* ov) override;
+  int make_mask(int n, int window, bool return_array, hipStream_t st, vkv_array* mask) override;
+  // innerState (:286-293): unified keys and values, window position, offset
+  int inner_state(vkv_array* out);
+  // init(from:) (:110-160)
+  static std::unique_ptr<CompilableTurboQuantCache> from(TurboQuantCache& src, hipStream_t st);
+  DevBuf ctr_;
+  hipStream_t last_ = nullptr;
+
+ private:
+  std::map<int, DevBuf> masks_;  // one mask buffer per row count, never moved
+  DevBuf cast_k_, cast_v_;       // the update cast to the buffers' dtype
+};
 void tq_host_tables(int dim, int bits, int seed, float* signs, float* codebook, float* qjl);
 
 // Runs f under the C ABI's error convention (vkv_capi.cpp): returns 0, or 1

@@ -255,6 +255,8 @@ void launch_dyn_copy(int esize, const DynCopy& c, hipStream_t st);
 // write index.  Advance by n (with the ring wrap when ring != 0), or set.
 void launch_counter_advance(int32_t* ctr, int n, int ring, int max_size, int keep, hipStream_t st);
 void launch_counter_set(int32_t* ctr, int32_t offset, int32_t idx, hipStream_t st);
+// ctr[0] += n and ctr[1] += n (offset and window write position).
+void launch_counter_advance_both(int32_t* ctr, int n, hipStream_t st);
 // [n, cols] bool mask from the device offset (see vkv_compile.hip).
 void launch_offset_mask(const int32_t* ctr, int n, int cols, int window, int ring, uint8_t* mask,
                         hipStream_t st);

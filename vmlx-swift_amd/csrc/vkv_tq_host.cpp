@@ -890,6 +890,13 @@ int vkv_turboquant_create(int32_t key_bits, int32_t value_bits, int32_t sink_tok
   });
 }
 
+int vkv_turboquant_to_compilable(vkv_cache tq, void* stream, vkv_cache* out) {
+  return guarded([&] {
+    need_ptr(out, "out");
+    *out = wrap(CompilableTurboQuantCache::from(*as_tq(tq), S(stream)));
+  });
+}
+
 int vkv_turboquant_from_simple(vkv_cache simple, int32_t key_bits, int32_t value_bits,
                                int32_t sink_tokens, int32_t residual_tokens, void* stream,
                                vkv_cache* out) {

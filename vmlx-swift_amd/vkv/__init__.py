@@ -26,6 +26,7 @@ MASK_NONE, MASK_CAUSAL, MASK_ARRAY = 0, 1, 2
 CACHE_SIMPLE, CACHE_ROTATING, CACHE_QUANTIZED = 0, 1, 2
 CACHE_COMPILABLE, CACHE_COMPILABLE_ROTATING = 3, 4
 CACHE_TURBOQUANT = 5
+CACHE_COMPILABLE_TURBOQUANT = 6
 VIEW_KEYS_ONLY = 1
 
 
@@ -95,6 +96,7 @@ EXPORTS = (
     "vkv_prefix_stats_get", "vkv_prefix_block_tokens", "vkv_block_hash", "vkv_array_copy",
     "vkv_kernel_timing", "vkv_kernel_timing_read", "vkv_fill_normal",
     "vkv_cache_to_compilable", "vkv_cache_to_compilable_rotating", "vkv_cache_inner_state",
+    "vkv_turboquant_to_compilable",
     "vkv_dynamic_slice_update", "vkv_dynamic_slice", "vkv_cache_set_offset",
     "vkv_attention_with_cache_update", "vkv_paged_sdpa_noalloc", "vkv_workspace_release",
     "vkv_quantized_paged_sdpa", "vkv_prefix_writable", "vkv_prompt_cache_save",
@@ -421,6 +423,13 @@ class _Cache:
             self._h = None
 
     @property
+    def kind(self) -> int:
+        """The cache's class (CACHE_*), vkv_cache_kind."""
+        v = C.c_int32()
+        _chk(lib().vkv_cache_kind(self._h, C.byref(v)))
+        return v.value
+
+    @property
     def offset(self) -> int:
         v = C.c_int64()
         _chk(lib().vkv_cache_offset(self._h, C.byref(v)))
@@ -728,6 +737,29 @@ class TurboQuantKVCache(_Cache):
                                                   stream_ptr(stream)))
 
 
+class CompilableTurboQuantKVCache(TurboQuantKVCache):
+    """CompilableTurboQuantKVCache (BatchEngine/CompilableTurboQuantKVCache.
+    swift:57-294): a compressed TurboQuantKVCache whose window writes go to
+    the offset in device memory; update returns the whole unified buffers and
+    make_mask an array mask over them, so a decode step can be captured in a
+    HIP graph."""
+
+    @classmethod
+    def from_turboquant(cls, tq: TurboQuantKVCache, stream=None):
+        """CompilableTurboQuantKVCache(from:) (:110-160); tq must be compressed."""
+        h = C.c_void_p()
+        _chk(lib().vkv_turboquant_to_compilable(tq._h, stream_ptr(stream), C.byref(h)))
+        return cls(handle=h)
+
+    def inner_state(self):
+        """innerState (:286-293): the unified keys and values, then the int32
+        [1] device counters (window write position, offset)."""
+        arrs = (Array * 4)()
+        n = C.c_int32()
+        _chk(lib().vkv_cache_inner_state(self._h, arrs, C.byref(n)))
+        return [arrs[i] for i in range(n.value)]
+
+
 def tq_tables(dim: int, bits: int, seed: int = 42):
     """(rotation signs, Lloyd-Max codebook, QJL matrix) of the codec's
     EncoderState, from the library's host code (no device needed)."""
@@ -916,7 +948,8 @@ def _wrap_handle(h):
     k = C.c_int32()
     _chk(lib().vkv_cache_kind(h, C.byref(k)))
     cls = {CACHE_SIMPLE: KVCacheSimple, CACHE_ROTATING: RotatingKVCache,
-           CACHE_QUANTIZED: QuantizedKVCache, CACHE_TURBOQUANT: TurboQuantKVCache}.get(k.value,
+           CACHE_QUANTIZED: QuantizedKVCache, CACHE_TURBOQUANT: TurboQuantKVCache,
+           CACHE_COMPILABLE_TURBOQUANT: CompilableTurboQuantKVCache}.get(k.value,
                                                                                      _Cache)
     obj = object.__new__(cls)
     _Cache.__init__(obj, None, handle=h)
