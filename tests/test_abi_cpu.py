@@ -46,6 +46,11 @@ def test_errors_are_reported_not_thrown():
     q = vkv.QuantizedKVCache(64, 4)
     with pytest.raises(vkv.VKVError, match="updateQuantized"):  # KVCache.swift:1126-1130
         vkv._chk(L.vkv_cache_update(q._h, None, None, None, None, None))
+    # CompilableTurboQuantKVCache(from:) needs a compressed source
+    # (CompilableTurboQuantKVCache.swift:111-112)
+    tq = vkv.TurboQuantKVCache()
+    assert L.vkv_turboquant_to_compilable(tq._h, None, C.byref(h)) == 1
+    assert b"compressed phase" in L.vkv_last_error()
     # the last error is per thread and cleared by the next success
     assert L.vkv_abi_version() == 2
 
