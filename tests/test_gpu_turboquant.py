@@ -382,3 +382,22 @@ def test_compilable_turboquant_graph_replay():
         torch.cuda.synchronize()
         assert torch.equal(out, eager), r
         assert int(host(vkv.to_torch(cap.inner_state()[3]))[0]) == 121 + r
+
+
+def test_compilable_turboquant_promotion_sanity():
+    """CompilableTurboQuantKVCacheTests.swift:108-126: 16 tokens of ones in a
+    KVCacheSimple [1, 4, *, 64], fromSimpleCache(keyBits 3, valueBits 3,
+    residualTokens 0), then CompilableTurboQuantKVCache(from:): compressed,
+    offset 16, and two [1] counters beside the unified buffers."""
+    simple = vkv.KVCacheSimple()
+    one = torch.ones((1, 4, 1, 64), dtype=torch.float32, device="cuda")
+    for _ in range(16):
+        simple.update(one, one)
+    tq = vkv.TurboQuantKVCache.from_simple_cache(simple, 3, 3, 4, 0)
+    assert tq.info["phase"] == 1
+    c = vkv.CompilableTurboQuantKVCache.from_turboquant(tq)
+    assert c.info["phase"] == 1 and c.offset == 16
+    inner = c.inner_state()
+    assert len(inner) == 4 and inner[2].shape[0] == 1 and inner[3].shape[0] == 1
+    assert int(host(vkv.to_torch(inner[2]))[0]) == 0
+    assert int(host(vkv.to_torch(inner[3]))[0]) == 16
