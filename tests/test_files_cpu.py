@@ -115,6 +115,8 @@ def _raw_file(path, header: dict, data: bytes, pad=True):
     ("not_json", "safetensors header"),
     ("float_offset", "non-integer"),
     ("missing_file", "cannot open"),
+    # dims each within bounds whose product wraps int64 to 0 (2^32 * 2^32)
+    ("shape_overflow", "too large"),
 ])
 def test_safetensors_container_validation(tmp_path, case, message):
     p = str(tmp_path / f"{case}.safetensors")
@@ -137,6 +139,9 @@ def test_safetensors_container_validation(tmp_path, case, message):
     elif case == "float_offset":
         h = {**meta, "0.0": {"dtype": "F32", "shape": [1, 2, 3, 8], "data_offsets": [0.0, 192]}}
         _raw_file(p, h, data)
+    elif case == "shape_overflow":
+        _raw_file(p, {**meta, "0.0": ent((0, 0), shape=(1, 1, 2 ** 32, 2 ** 32)),
+                      "0.1": ent((0, 192))}, data)
     if case != "missing_file":
         assert os.path.exists(p)
     rc, n, nm, err = _load_count(p)

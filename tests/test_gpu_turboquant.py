@@ -401,3 +401,70 @@ def test_compilable_turboquant_promotion_sanity():
     assert len(inner) == 4 and inner[2].shape[0] == 1 and inner[3].shape[0] == 1
     assert int(host(vkv.to_torch(inner[2]))[0]) == 0
     assert int(host(vkv.to_torch(inner[3]))[0]) == 16
+
+
+def test_compilable_turboquant_past_the_buffers(tmp_path):
+    """A compiled decode that runs past the unified buffers: the device
+    writes clamp to the buffers (dynamicSliceUpdate), so state is the whole
+    buffers (MLX slicing clamps [..<total]), the window is absent
+    (serializedWindowState needs the buffers to hold it,
+    TurboQuantKVCache.swift:254-258), and a disk save writes the encoded
+    record without a window, readable by the safetensors package."""
+    from safetensors import safe_open
+    rng = np.random.default_rng(91)
+    D = 64
+    src = _compressed(rng, O.BF16, D=D)
+    c = vkv.CompilableTurboQuantKVCache.from_turboquant(src)
+    cap = c.inner_state()[0].shape[2]
+    steps = cap - c.offset + 1
+    k1 = dev(rand_bits(rng, (1, 2, 1, D), O.BF16), O.BF16)
+    for _ in range(steps):
+        c.update(k1, k1)
+    torch.cuda.synchronize()
+    assert c.offset == cap + 1
+    sk, sv = c.state
+    assert sk.shape == (1, 2, cap, D) and sv.shape == (1, 2, cap, D)
+    assert c.window_state() is None
+    path = str(tmp_path / "past.safetensors")
+    vkv.disk_cache_save(path, [c])
+    with safe_open(path, framework="pt") as f:
+        names = set(f.keys())
+        assert f.get_tensor("__tq_0_offset__").tolist() == [cap + 1]
+    assert "tq_0_ck_indices" in names and "tq_0_window_keys" not in names
+
+
+def test_compilable_turboquant_bf16_graph_replay():
+    """bf16 tokens into the f32 unified buffers under HIP-graph capture: the
+    cast scratch is reserved when the compilable cache is made, so the
+    captured update allocates nothing and every replay equals the eager step
+    on a twin."""
+    dtype, D = O.BF16, 64
+    rng = np.random.default_rng(78)
+    src = _compressed(rng, dtype, D=D)
+    cap = vkv.CompilableTurboQuantKVCache.from_turboquant(src)
+    twin = vkv.CompilableTurboQuantKVCache.from_turboquant(src)
+    assert cap.inner_state()[0].dtype == torch.float32
+    kin = torch.zeros((1, 2, 1, D), dtype=torch.bfloat16, device="cuda")
+    vin = torch.zeros_like(kin)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            cap.update(kin, vin)  # the first compressed update, under capture
+    torch.cuda.synchronize()
+    for r in range(3):
+        kin.copy_(dev(rand_bits(rng, (1, 2, 1, D), dtype), dtype))
+        vin.copy_(dev(rand_bits(rng, (1, 2, 1, D), dtype), dtype))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        ck, _ = twin.update(kin, vin)
+        torch.cuda.synchronize()
+        n = twin.offset
+        want = vkv.to_torch(ck)[:, :, n - 1:n]
+        full = vkv.to_torch(cap.inner_state()[0])
+        assert torch.equal(full[:, :, n - 1:n], want), r
+        assert torch.equal(want, kin.float()), r
+        assert int(host(vkv.to_torch(cap.inner_state()[3]))[0]) == n

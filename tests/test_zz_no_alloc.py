@@ -96,3 +96,37 @@ def test_noalloc_rejects_calls_beyond_the_scratch():
     with pytest.raises(vkv.VKVError, match="scratch"):
         vkv.paged_attention(q, view, 128 ** -0.5, out=torch.empty_like(q), noalloc=True)
     torch.cuda.synchronize()
+
+
+def test_noalloc_under_graph_capture():
+    """The use the entry point is for: a decode call captured in a HIP graph
+    (after one eager call, which resolves the scratch on the device) and
+    replayed with new queries copied in between; every replay equals the
+    eager call of the allocating entry point on the same queries."""
+    rng = np.random.default_rng(730)
+    dtype, Hkv, D, Hq, bits = O.BF16, 8, 128, 32, 4
+    lens = [1200, 31, 4000, 700]
+    print(f"noalloc capture: lens {lens}", flush=True)
+    pool, view, keys, vals, keep = scene(rng, bits, lens, Hkv, D)
+    qin = dev(rand_bits(rng, (len(lens), Hq, D), dtype), dtype)
+    out = torch.empty_like(qin)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        vkv.paged_attention(qin, view, D ** -0.5, out=out, noalloc=True)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            vkv.paged_attention(qin, view, D ** -0.5, out=out, noalloc=True)
+    torch.cuda.synchronize()
+    for r in range(4):
+        q = rand_bits(rng, (len(lens), Hq, D), dtype)
+        qin.copy_(dev(q, dtype))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        want = vkv.paged_attention(qin, view, D ** -0.5)
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out), host(want)), r
+        check_against_oracle(values(out, dtype), q, keys, vals, bits, dtype, D)

@@ -382,8 +382,11 @@ StFile read_safetensors_header(const std::string& path) {
       if (d.kind != JVal::Int || d.i < 0 || d.i > (int64_t{1} << 40))
         throw Error(path + ": bad shape for tensor " + kv.first);
       e.shape.push_back(d.i);
+      // the element count stays below 2^42, checked before the product
+      // could overflow
+      constexpr int64_t kMaxElems = int64_t{1} << 42;
+      if (d.i != 0 && n > kMaxElems / d.i) throw Error(path + ": tensor " + kv.first + " is too large");
       n *= d.i;
-      if (n > (int64_t{1} << 42)) throw Error(path + ": tensor " + kv.first + " is too large");
     }
     if (of->arr[0].kind != JVal::Int || of->arr[1].kind != JVal::Int)
       throw Error(path + ": bad data_offsets for tensor " + kv.first);

@@ -26,6 +26,8 @@ void check4(const vkv_array& a, const char* name) {
 }
 
 vkv_array Dense4::view(int64_t len) const {
+  if (len < 0 || len > cap) throw Error("view of " + std::to_string(len) + " tokens over a buffer of " +
+                                        std::to_string(cap));
   vkv_array a{};
   a.data = buf ? buf->get() : nullptr;
   a.dtype = dtype;
@@ -212,8 +214,9 @@ int64_t SimpleCache::trim(int64_t n) {
 // KVCacheSimple.state getter (KVCache.swift:527-537)
 int SimpleCache::state(hipStream_t, vkv_array* out) {
   if (k_.empty()) return 0;
-  out[0] = k_.view(offset);
-  out[1] = v_.view(offset);
+  // [..<offset] clamps to the buffers' length, as MLX slicing does
+  out[0] = k_.view(std::min(offset, k_.cap));
+  out[1] = v_.view(std::min(offset, v_.cap));
   return 2;
 }
 
@@ -255,6 +258,7 @@ std::unique_ptr<Cache> SimpleCache::to_quantized(int group, int bits, hipStream_
   if (!k_.empty() && offset > 0) {
     q->reserve(k_.B, k_.H, k_.D, offset, k_.dtype, st);
     if (v_.D != k_.D) throw Error("toQuantized needs equal key and value head dims");
+    if (offset > k_.cap) throw Error("toQuantized: offset is past the cached tokens");
     vkv_array kv[2] = {k_.view(offset), v_.view(offset)};
     for (int which = 0; which < 2; which++) {
       const vkv_array& a = kv[which];
@@ -720,7 +724,19 @@ std::unique_ptr<CompilableTurboQuantCache> CompilableTurboQuantCache::from(Turbo
   launch_counter_set(static_cast<int32_t*>(c->ctr_.get()), static_cast<int32_t>(c->offset),
                      static_cast<int32_t>(c->window_), st);
   c->last_ = st;
+  c->reserve_casts();
   return c;
+}
+
+// The cast scratch of a compressed-phase update (tokens of another dtype
+// than the unified buffers'), sized once for the longest update the buffers
+// take, when the buffers are made: an update under HIP-graph capture then
+// neither allocates nor frees, and a captured graph's scratch address stays
+// valid.
+void CompilableTurboQuantCache::reserve_casts() {
+  if (phase_ != 1 || uk_.empty()) return;
+  cast_k_.ensure(static_cast<size_t>(uk_.B * uk_.H * uk_.cap * uk_.D) * elem_bytes(uk_.dtype));
+  cast_v_.ensure(static_cast<size_t>(uv_.B * uv_.H * uv_.cap * uv_.D) * elem_bytes(uv_.dtype));
 }
 
 // update (:168-224): the fill phase is the parent's; compressed, the new
@@ -731,6 +747,7 @@ void CompilableTurboQuantCache::update(const vkv_array& k, const vkv_array& v, h
                                        vkv_array* ok, vkv_array* ov) {
   if (phase_ != 1 || uk_.empty()) {
     TurboQuantCache::update(k, v, st, ok, ov);
+    reserve_casts();  // the update that promotes the cache makes its buffers
     return;
   }
   check_kv_pair(k, v);
@@ -739,6 +756,13 @@ void CompilableTurboQuantCache::update(const vkv_array& k, const vkv_array& v, h
   const int64_t S = k.shape[2];
   if (S > uk_.cap) throw Error("update is longer than the unified buffers");
   int32_t* ctr = static_cast<int32_t*>(ctr_.get());
+  if (k.dtype != uk_.dtype || v.dtype != uv_.dtype) {
+    // buffers restored another way than from() or a promotion get their
+    // cast scratch here, outside a capture (a no-op once it exists)
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    VKV_HIP(hipStreamIsCapturing(st, &cs));
+    if (cs == hipStreamCaptureStatusNone) reserve_casts();
+  }
   auto put = [&](const Dense4& d, const vkv_array& a, DevBuf& tmp) {
     if (a.dtype == d.dtype) {
       write_at_device_offset(d, a, ctr, st);
@@ -746,7 +770,9 @@ void CompilableTurboQuantCache::update(const vkv_array& k, const vkv_array& v, h
     }
     const int64_t shape[4] = {a.shape[0], a.shape[1], S, a.shape[3]};
     const int64_t dstr[4] = {a.shape[1] * S * a.shape[3], S * a.shape[3], a.shape[3], 1};
-    tmp.ensure(static_cast<size_t>(shape[0] * dstr[0]) * elem_bytes(d.dtype));
+    // S <= cap, so the scratch reserved with the buffers holds it
+    if (static_cast<size_t>(shape[0] * dstr[0]) * elem_bytes(d.dtype) > tmp.size())
+      throw Error("the cast scratch does not hold the update (run one update before capturing)");
     launch_cast4d(a.data, a.dtype, shape, a.strides, tmp.get(), d.dtype, dstr, st);
     vkv_array c{};
     c.data = tmp.get();

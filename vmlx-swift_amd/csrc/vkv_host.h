@@ -435,8 +435,9 @@ class CompilableTurboQuantCache : public TurboQuantCache {
   hipStream_t last_ = nullptr;
 
  private:
+  void reserve_casts();
   std::map<int, DevBuf> masks_;  // one mask buffer per row count, never moved
-  DevBuf cast_k_, cast_v_;       // the update cast to the buffers' dtype
+  DevBuf cast_k_, cast_v_;       // the update cast to the buffers' dtype (cap tokens)
 };
 void tq_host_tables(int dim, int bits, int seed, float* signs, float* codebook, float* qjl);
 

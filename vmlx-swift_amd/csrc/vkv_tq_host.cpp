@@ -600,7 +600,9 @@ int TurboQuantCache::state(hipStream_t, vkv_array* out) {
     out[1] = fv_.view(offset);
     return 2;
   }
-  const int64_t total = prefix_ + window_;
+  // MLX slicing clamps [..<total] to the buffers' length: a compiled cache
+  // whose counters ran past the unified buffers returns the whole buffers
+  const int64_t total = std::min(prefix_ + window_, std::min(uk_.cap, uv_.cap));
   if (uk_.empty() || total <= 0) return 0;
   out[0] = uk_.view(total);
   out[1] = uv_.view(total);
@@ -811,7 +813,9 @@ void TurboQuantCache::restore_compressed(const vkv_tq_encoded& rk, const vkv_tq_
 bool TurboQuantCache::window_state(vkv_array* k, vkv_array* v) const {
   if (phase_ != 1 || window_ <= 0 || uk_.empty()) return false;
   const int64_t end = prefix_ + window_;
-  if (end != offset) return false;
+  // the window must end at offset and lie inside the unified buffers
+  // (:254-258); a compiled cache's counters can run past them
+  if (end != offset || uk_.cap < end || uv_.cap < end) return false;
   vkv_array a = uk_.view(end), b = uv_.view(end);
   const int64_t ek = prefix_ * a.strides[2] * elem_bytes(a.dtype);
   const int64_t ev = prefix_ * b.strides[2] * elem_bytes(b.dtype);
