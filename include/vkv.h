@@ -678,17 +678,24 @@ int vkv_workspace_release(void *stream, int64_t *bytes);
  * decode kernel's target wave count; GATHER_TOKENS (0 = choose) the key
  * window of a multi-token chunk over a quantized or paged cache (its K/V are
  * gathered to the dtype one window at a time; by default a window's copy
- * stays within 256 MiB).  Initial values come from the environment
- * variables VKV_GENERIC_ATTENTION, VKV_DECODE_WAVES, VKV_MLA_SPLITS,
- * VKV_FDECODE_WAVES and VKV_GATHER_TOKENS, read once; calls read the
- * options, never the environment. */
+ * stays within 256 MiB); REFERENCE_SOFTMAX (0/1) computes quantized
+ * attention with the reference's own roundings: scores stored in the query
+ * dtype, softmax(precise: false) with its AccT = T arithmetic in a pass of
+ * its own (KVCache.swift:1982, mlx-generated/metal/softmax.h:10-190),
+ * weights stored in the dtype, then P.V (with it off, the softmax of the
+ * stored scores runs in fp32 inside one pass).  Initial values come from
+ * the environment variables VKV_GENERIC_ATTENTION, VKV_DECODE_WAVES,
+ * VKV_MLA_SPLITS, VKV_FDECODE_WAVES, VKV_GATHER_TOKENS and
+ * VKV_REFERENCE_SOFTMAX, read once; calls read the options, never the
+ * environment. */
 enum {
   VKV_OPTION_GENERIC_ATTENTION = 0,
   VKV_OPTION_DECODE_WAVES = 1,
   VKV_OPTION_MLA_SPLITS = 2,
   VKV_OPTION_FDECODE_WAVES = 3, /* 0 = 2048: waves the float decode kernel aims for */
   VKV_OPTION_GATHER_TOKENS = 4, /* 0 = a 256 MiB copy: key window of a gathered chunk */
-  VKV_OPTION_COUNT = 5
+  VKV_OPTION_REFERENCE_SOFTMAX = 5, /* quantized attention with the reference's arithmetic */
+  VKV_OPTION_COUNT = 6
 };
 int vkv_set_option(int32_t which, int64_t value);
 int vkv_get_option(int32_t which, int64_t *value);

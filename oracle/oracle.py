@@ -65,7 +65,7 @@ def _declare(L):
     L.vkvo_dequantize_rule_split.argtypes = [vp, vp, vp, i32, i64, i32, i32, i32]
     L.vkvo_sdpa.argtypes = [vp, vp, vp] + [i32] * 7 + [f32, i32, vp, vp] + [i64] * 4 + [i32, vp, vp]
     L.vkvo_quantized_sdpa.argtypes = (
-        [vp, i32] + [vp] * 6 + [i32] * 8 + [f32, i32, vp, vp] + [i64] * 4 + [i32, vp, vp]
+        [vp, i32] + [vp] * 6 + [i32] * 8 + [f32, i32, vp, vp] + [i64] * 4 + [i32, vp, vp, vp]
     )
     L.vkvo_mla_decode.argtypes = [vp, vp, vp, vp, i32, i32, i32, vp, i32, i32, i32, i32, f32, vp]
     L.vkvo_quantized_decode_batch.argtypes = (
@@ -178,12 +178,14 @@ def sdpa(q, k, v, scale, mask=None, q_dtype=F32, sinks=None):
 
 
 def quantized_sdpa(q, q_dtype, kq, ks, kb, vq, vs, vb, scale, group=64, bits=4, mask=None,
-                   rounding=QMV, bound=False):
+                   rounding=QMV, bound=False, flip=False):
     """Reference-layout quantized cache; scales/biases as f32 values.
 
     rounding: EXACT, QMV (default: the reference's decode arithmetic), QMM
     or QMV_ACC_T (see vkvo_quantized_sdpa).  With bound=True also returns
-    the per-output weight-rounding bound sum_t |w_t - p_t| |v_t|."""
+    the per-output rounding bound (the weight term sum_t |w_t - p_t| |v_t|
+    plus the score-boundary term); with flip=True instead the
+    score-boundary term alone."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     B, Hq, L, D = q.shape
     Hkv, T = kq.shape[1], kq.shape[2]
@@ -193,10 +195,13 @@ def quantized_sdpa(q, q_dtype, kq, ks, kb, vq, vs, vb, scale, group=64, bits=4, 
     mode, mb, mf, st, keep = _mask_args(mask, B, Hq, L, T)
     out = np.empty((B, Hq, L, D), np.float64)
     wb = np.empty((B, Hq, L, D), np.float64) if bound else None
+    fb = np.empty((B, Hq, L, D), np.float64) if flip else None
     lib().vkvo_quantized_sdpa(_p(q), q_dtype, *[_p(a) for a in arrs], B, Hq, Hkv, L, T, D,
                               group, bits, scale, mode, _p(mb), _p(mf), *st, rounding,
-                              _p(out), _p(wb))
-    return (out, wb) if bound else out
+                              _p(out), _p(wb), _p(fb))
+    if bound and flip:
+        return out, wb, fb
+    return (out, wb) if bound else (out, fb) if flip else out
 
 
 def mla_decode(q, cq, cs, cb, lens, scale, Dv=512, group=64, bits=8):

@@ -472,13 +472,15 @@ static void qsdpa_row(const float *qs, const uint32_t *kq, const float *ks,
                       const float *vb, int T, int D, int group, int bits,
                       const double *add, const unsigned char *vis, double fill,
                       int rnd, int sdt, double *sc, double *pw, double *pe, double *o,
-                      double *wb) {
+                      double *wb, double *fb) {
   const int wpr = D * bits / 32;
   const int G = D / group;
   const int deq_dt = (rnd == 2 || rnd == 4) ? sdt : -1;
   const int wdt = add ? 0 : sdt;
-  /* flip factors exp(n_t - r_t) for scores near a rounding boundary (0: none) */
-  double *flip = (wb && rnd) ? (double *)calloc((size_t)(T > 0 ? T : 1), sizeof(double)) : NULL;
+  /* flip factors exp(n_t - r_t) for scores near a rounding boundary (0: none),
+   * and the flipped score itself (the other neighbour, mask added) */
+  double *flip = ((wb || fb) && rnd) ? (double *)calloc((size_t)(T > 0 ? T : 1), sizeof(double)) : NULL;
+  double *alt = (fb && rnd) ? (double *)calloc((size_t)(T > 0 ? T : 1), sizeof(double)) : NULL;
   const int acc_t = ((rnd == 3 || rnd == 4) && !add) ? sdt : -1;
   for (int t = 0; t < T; t++) {
     double s = fill;
@@ -498,8 +500,14 @@ static void qsdpa_row(const float *qs, const uint32_t *kq, const float *ks,
           double below, above;
           t_neighbours(r, sdt, &below, &above);
           const double eps = ldexp(mag, -17);
-          if (fabs(s - 0.5 * (r + above)) < eps) flip[t] = exp(above - r);
-          if (fabs(s - 0.5 * (r + below)) < eps) flip[t] = exp(below - r);
+          if (fabs(s - 0.5 * (r + above)) < eps) {
+            flip[t] = exp(above - r);
+            if (alt) alt[t] = add ? (double)(float)(above + add[t]) : above;
+          }
+          if (fabs(s - 0.5 * (r + below)) < eps) {
+            flip[t] = exp(below - r);
+            if (alt) alt[t] = add ? (double)(float)(below + add[t]) : below;
+          }
         }
         s = r;
       }
@@ -508,23 +516,23 @@ static void qsdpa_row(const float *qs, const uint32_t *kq, const float *ks,
     sc[t] = s;
   }
   softmax_row(sc, T, rnd, acc_t, wdt, pw, pe);
-  double *o1 = wb ? (double *)calloc((size_t)D, sizeof(double)) : NULL;
+  double *o1 = (wb || fb) ? (double *)calloc((size_t)D, sizeof(double)) : NULL;
   for (int d = 0; d < D; d++) o[d] = 0.0;
   if (wb)
     for (int d = 0; d < D; d++) wb[d] = 0.0;
+  if (fb)
+    for (int d = 0; d < D; d++) fb[d] = 0.0;
   for (int t = 0; t < T; t++) {
     const uint32_t *vr = vq + (int64_t)t * wpr;
     for (int d = 0; d < D; d++) {
       const double vv = deq_at(vr, vs + (int64_t)t * G, vb + (int64_t)t * G, d, group, bits,
                                deq_dt);
       o[d] += pw[t] * vv;
-      if (wb) {
-        wb[d] += fabs(pw[t] - pe[t]) * fabs(vv);
-        o1[d] += pe[t] * vv;
-      }
+      if (wb) wb[d] += fabs(pw[t] - pe[t]) * fabs(vv);
+      if (o1) o1[d] += pe[t] * vv;
     }
   }
-  if (flip) {
+  if (flip && wb) {
     /* a flipped score t scales its exponential by f: the output becomes
      * (o1 + (f - 1) pe_t v_t) / (1 + (f - 1) pe_t) */
     for (int t = 0; t < T; t++) {
@@ -538,7 +546,38 @@ static void qsdpa_row(const float *qs, const uint32_t *kq, const float *ks,
       }
     }
   }
+  if (flip && fb) {
+    /* fb: the move of the output, in this mode's own arithmetic (the same
+     * rounded softmax, weights and P.V), when one flipped score t is
+     * stored the other way: a flip can move the rounded normaliser and so
+     * every weight, which the exact-softmax formula above does not see.
+     * Flips of one row are added. */
+    double *sc2 = (double *)malloc(sizeof(double) * (size_t)T);
+    double *pw2 = (double *)malloc(sizeof(double) * (size_t)T);
+    double *pe2 = (double *)malloc(sizeof(double) * (size_t)T);
+    double *o2 = (double *)malloc(sizeof(double) * (size_t)D);
+    for (int t = 0; t < T; t++) {
+      if (flip[t] == 0.0) continue;
+      memcpy(sc2, sc, sizeof(double) * (size_t)T);
+      sc2[t] = alt[t];
+      softmax_row(sc2, T, rnd, acc_t, wdt, pw2, pe2);
+      for (int d = 0; d < D; d++) o2[d] = 0.0;
+      for (int u = 0; u < T; u++) {
+        if (pw2[u] == pw[u]) continue;
+        const uint32_t *vr = vq + (int64_t)u * wpr;
+        for (int d = 0; d < D; d++)
+          o2[d] += (pw2[u] - pw[u]) * deq_at(vr, vs + (int64_t)u * G, vb + (int64_t)u * G, d,
+                                             group, bits, deq_dt);
+      }
+      for (int d = 0; d < D; d++) fb[d] += fabs(o2[d]);
+    }
+    free(sc2);
+    free(pw2);
+    free(pe2);
+    free(o2);
+  }
   free(flip);
+  free(alt);
   free(o1);
 }
 
@@ -549,7 +588,7 @@ void vkvo_quantized_sdpa(const float *q, int q_dtype, const uint32_t *kq,
                          int L, int T, int D, int group, int bits, float scale,
                          int mask_mode, const uint8_t *bmask, const float *fmask,
                          int64_t msb, int64_t msh, int64_t msl, int64_t mst,
-                         int rounding, double *out, double *wbound) {
+                         int rounding, double *out, double *wbound, double *fbound) {
   const int rep = Hq / Hkv;
   const int wpr = D * bits / 32;
   const int G = D / group;
@@ -587,12 +626,14 @@ void vkvo_quantized_sdpa(const float *q, int q_dtype, const uint32_t *kq,
           for (int d = 0; d < D; d++) out[orow + d] = 0.0;
           if (wbound)
             for (int d = 0; d < D; d++) wbound[orow + d] = 0.0;
+          if (fbound)
+            for (int d = 0; d < D; d++) fbound[orow + d] = 0.0;
           continue;
         }
         qsdpa_row(qs, kq + kv_row0 * wpr, ks + kv_row0 * G, kb + kv_row0 * G,
                   vq + kv_row0 * wpr, vs + kv_row0 * G, vb + kv_row0 * G, T, D, group,
                   bits, mask_mode == 3 ? add : NULL, vis, fill, rounding, q_dtype, sc, pw, pe,
-                  out + orow, wbound ? wbound + orow : NULL);
+                  out + orow, wbound ? wbound + orow : NULL, fbound ? fbound + orow : NULL);
       }
   free(qs);
   free(sc);
@@ -635,7 +676,7 @@ void vkvo_quantized_decode_batch(const float *q, int q_dtype, const uint32_t *kq
         const int64_t row0 = tok_off[s] + (int64_t)(h / rep) * T;
         qsdpa_row(qs, kq + row0 * wpr, ks + row0 * G, kb + row0 * G, vq + row0 * wpr,
                   vs + row0 * G, vb + row0 * G, (int)T, D, group, bits, NULL, NULL, 0.0,
-                  rounding, q_dtype, sc, pw, pe, out + ((int64_t)s * Hq + h) * D, NULL);
+                  rounding, q_dtype, sc, pw, pe, out + ((int64_t)s * Hq + h) * D, NULL, NULL);
       }
     free(qs);
     free(sc);

@@ -93,14 +93,19 @@ void vkvo_sdpa(const float *q, const float *k, const float *v, int B, int Hq,
  * the rounded scores: sum_t |w_t - pe_t| |v_t| for the weights stored in T,
  * plus, for each score within 2^-17 sum_d |q_d k_td| of a T rounding
  * boundary (where any fp32 accumulation may land on either side), the exact
- * output change of rounding it the other way. */
+ * output change of rounding it the other way.  fbound (optional, same
+ * shape): the score-boundary term alone, for a kernel that reproduces the
+ * reference's weights from the same stored scores: for each such score,
+ * the move of the output when it is stored the other way, computed in the
+ * mode's own arithmetic (the rounded softmax can move its normaliser, and
+ * with it every weight); the flips of a row are added. */
 void vkvo_quantized_sdpa(const float *q, int q_dtype, const uint32_t *kq,
                          const float *ks, const float *kb, const uint32_t *vq,
                          const float *vs, const float *vb, int B, int Hq, int Hkv,
                          int L, int T, int D, int group, int bits, float scale,
                          int mask_mode, const uint8_t *bmask, const float *fmask,
                          int64_t msb, int64_t msh, int64_t msl, int64_t mst,
-                         int rounding, double *out, double *wbound);
+                         int rounding, double *out, double *wbound, double *fbound);
 
 /* ---- MLA absorbed-latent decode (GLM4MOELite.swift:233-290,
  * AttentionUtils.swift:43-75) ----

@@ -70,6 +70,21 @@ def qattn_tol(dtype: int, ref: np.ndarray, wb: np.ndarray) -> np.ndarray:
     return attn_tol(dtype, ref) + wb
 
 
+def qref_flip(*args, rounding=O.REF_DECODE, **kw):
+    """The oracle's quantized SDPA with the reference's arithmetic and its
+    score-boundary term alone: the bound for the reference-softmax path,
+    which reproduces the reference's weights from the stored scores, so that
+    only a score that an fp32 accumulation rounds to the other side of a
+    dtype rounding boundary (either side is as right as the other) moves it."""
+    return O.quantized_sdpa(*args, rounding=rounding, flip=True, **kw)
+
+
+def assert_refclose(got, ref, fb, dtype, ctx=""):
+    """Reference-softmax path against the oracle: 2e-2 (1e-4 for f32) + 1 ulp
+    + the score-boundary term fb."""
+    assert_within(got, ref, attn_tol(dtype, ref) + fb, ctx, fb)
+
+
 def assert_within(got, ref, tol, ctx="", wb=None):
     """Element-wise |got - ref| <= tol, reporting the worst element (index,
     values, tolerance, the rounding bound there) instead of whole arrays."""

@@ -180,22 +180,30 @@ def test_quantized_cache_chunk_head_dims(D, bits, rep, monkeypatch):
     assert_within(got, gen, attn_tol(dtype, ref) + 2 * wb, "generic", wb)
 
 
+@pytest.mark.parametrize("ref_mode", [1, 0], ids=["reference_softmax", "fp32_softmax"])
 @pytest.mark.parametrize("bits", [4, 8])
-def test_quantized_cache_chunk_outlier_channels(bits):
+def test_quantized_cache_chunk_outlier_channels(bits, ref_mode, monkeypatch):
     """Config-2 data (4 channels per head scaled x20), a 512-token chunk
     over a 4096-token cache: against the reference's matrix-path rounding
     (affine_qmm dequantizes K/V tiles to bf16, quantized.h:568-576,
-    :686-713; scores and weights stored in bf16, KVCache.swift:1945-1982)."""
+    :686-713; scores and weights stored in bf16, KVCache.swift:1945-1982).
+    With the reference softmax the bar holds the score-boundary term alone;
+    the single-pass matrix-core kernel (fp32 softmax) adds the weight term."""
     dtype, D = O.BF16, 128
+    monkeypatch.setattr(OPTIONS, "reference_softmax", ref_mode)
     step, q, kx, vx = quantized_chunk(np.random.default_rng(10 + bits), bits, 4, T0=3584,
                                       L=512, Hkv=2)
     got = step()
     kq, ks, kb, _ = O.quantize(kx, dtype, 64, bits)
     vq, vs, vb, _ = O.quantize(vx, dtype, 64, bits)
     f = lambda a: O.to_f32(a, dtype)
-    ref, wb = qref(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5, 64, bits,
-                   mask="causal", rounding=O.REF_CHUNK)
-    assert_qclose(got, ref, wb, dtype, f"bits {bits}")
+    ref, wb, fb = O.quantized_sdpa(f(q), dtype, kq, f(ks), f(kb), vq, f(vs), f(vb), D ** -0.5,
+                                   64, bits, mask="causal", rounding=O.REF_CHUNK, bound=True,
+                                   flip=True)
+    if ref_mode:
+        assert_within(got, ref, attn_tol(dtype, ref) + fb, f"bits {bits} reference softmax", fb)
+    else:
+        assert_qclose(got, ref, wb, dtype, f"bits {bits}")
 
 
 @pytest.mark.parametrize("bits", [4, 8])

@@ -443,7 +443,7 @@ def test_compilable_turboquant_bf16_graph_replay():
     src = _compressed(rng, dtype, D=D)
     cap = vkv.CompilableTurboQuantKVCache.from_turboquant(src)
     twin = vkv.CompilableTurboQuantKVCache.from_turboquant(src)
-    assert cap.inner_state()[0].dtype == torch.float32
+    assert vkv.to_torch(cap.inner_state()[0]).dtype == torch.float32
     kin = torch.zeros((1, 2, 1, D), dtype=torch.bfloat16, device="cuda")
     vin = torch.zeros_like(kin)
     g = torch.cuda.CUDAGraph()

@@ -88,11 +88,12 @@ struct Options {
   Options() {
     const char* names[VKV_OPTION_COUNT] = {"VKV_GENERIC_ATTENTION", "VKV_DECODE_WAVES",
                                            "VKV_MLA_SPLITS", "VKV_FDECODE_WAVES",
-                                           "VKV_GATHER_TOKENS"};
+                                           "VKV_GATHER_TOKENS", "VKV_REFERENCE_SOFTMAX"};
     for (int i = 0; i < VKV_OPTION_COUNT; i++) {
       const char* e = getenv(names[i]);
       int64_t x = 0;
-      if (e) x = i == VKV_OPTION_GENERIC_ATTENTION ? 1 : std::max(1, atoi(e));
+      const bool flag = i == VKV_OPTION_GENERIC_ATTENTION || i == VKV_OPTION_REFERENCE_SOFTMAX;
+      if (e) x = flag ? (atoi(e) != 0) : std::max(1, atoi(e));
       v[i].store(x, std::memory_order_relaxed);
     }
   }
@@ -109,8 +110,44 @@ float* workspace(hipStream_t st, size_t floats, bool noalloc) {
   return noalloc ? decode_scratch(floats) : attention_workspace(st, floats);
 }
 
+// Quantized attention with the reference's arithmetic (vkv_refattn.hip):
+// the query positions go in batches whose score rows fit 256 MiB.
+constexpr int64_t kRefScoreBytes = int64_t{256} << 20;
+void run_ref_attention(int dtype, int bits, int group, const AttnArgs& a, int64_t rows,
+                       hipStream_t st, bool noalloc) {
+  const int64_t B = rows / a.L, T = a.kv.T;
+  RefArgs r{};
+  r.a = a;
+  r.group = group;
+  r.bits = bits;
+  r.deq_round = a.L >= kGatherPrefillMinL;  // the quantized matmul's tiled path
+  r.score_f32 = a.mask_mode == 3 && a.mask_dtype == VKV_F32;  // an f32 additive mask
+  r.tpad = (std::max<int64_t>(T, 1) + 63) / 64 * 64;
+  const int rep = a.Hq / a.Hkv;
+  const int64_t per_l = B * a.Hq * r.tpad;  // score floats per query position
+  const int64_t nl = std::max<int64_t>(1, std::min<int64_t>(a.L, kRefScoreBytes / 4 / per_l));
+  for (int64_t l0 = 0; l0 < a.L; l0 += nl) {
+    r.l0 = static_cast<int32_t>(l0);
+    r.nl = static_cast<int32_t>(std::min<int64_t>(nl, a.L - l0));
+    r.n_rows = B * a.Hq * r.nl;
+    r.part_tokens = ref_part_tokens(B, a.Hkv, rep * r.nl, T, &r.n_parts);
+    const size_t sc_floats = static_cast<size_t>(r.n_rows * r.tpad);
+    const size_t pv_floats = r.n_parts > 1 ? static_cast<size_t>(r.n_parts * r.n_rows * a.Dv) : 0;
+    float* ws = workspace(st, sc_floats + pv_floats, noalloc);
+    r.sc = ws;
+    r.ws = ws + sc_floats;
+    launch_ref_attention(dtype, r, B, st);
+  }
+}
+
 void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64_t rows,
                    int64_t max_len, hipStream_t st, bool noalloc = false) {
+  a.group = group;
+  if (qsem && bits > 0 && option(VKV_OPTION_REFERENCE_SOFTMAX)) {
+    if (a.D > kMaxRefD || a.Dv > kMaxRefD) throw Error("head dims above 256 are not supported here");
+    if (rows > 0) run_ref_attention(dtype, bits, group, a, rows, st, noalloc);
+    return;
+  }
   if (fdecode_supported(dtype, bits, qsem, a) && !option(VKV_OPTION_GENERIC_ATTENTION)) {
     a.n_parts = fdecode_parts(rows * a.Hkv, max_len, &a.part_tokens,
                               static_cast<int>(option(VKV_OPTION_FDECODE_WAVES)));
@@ -401,7 +438,8 @@ int vkv_quantized_sdpa(const vkv_array* q, const vkv_array* k_wq, const vkv_arra
       need(x, "quantized tuple array");
       if (x->ndim != 4 || x->strides[3] != 1) throw Error("quantized tuples must be 4-D, last dim contiguous");
     }
-    if (group_size != 64) throw Error("quantized attention supports group_size 64");
+    if (group_size != 32 && group_size != 64 && group_size != 128)
+      throw Error("quantized attention supports group_size 32, 64 or 128");
     if (bits != 4 && bits != 8) throw Error("bits must be 4 or 8");
     if (q->ndim != 4 || out->ndim != 4 || q->strides[3] != 1 || out->strides[3] != 1)
       throw Error("q and out must be 4-D with a contiguous last dim");
@@ -489,7 +527,7 @@ void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_a
                          (reinterpret_cast<uintptr_t>(out->data) % 8 == 0) &&
                          out->strides[0] % 4 == 0 && out->strides[1] % 4 == 0;
     if (kv->bits > 0 && !keys_only && aligned && kv->max_len <= qdecode_max_len() &&
-        !option(VKV_OPTION_GENERIC_ATTENTION) &&
+        !option(VKV_OPTION_GENERIC_ATTENTION) && !option(VKV_OPTION_REFERENCE_SOFTMAX) &&
         qdecode_supported(kv->dtype, kv->bits, kv->head_dim, kv->block_size, rep, kv->group_size)) {
       // matrix-core path (vkv_decode.hip)
       KVSrc src = kvsrc_from_view(*kv);

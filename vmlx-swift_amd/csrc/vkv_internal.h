@@ -104,7 +104,35 @@ struct AttnArgs {
   int32_t part0, parts_run, t_base;
   float* ws_o;             // [rows][Hq][n_parts][Dv]
   float* ws_ml;            // [rows][Hq][n_parts][2] (max, sum)
+  int32_t group;           // affine quantization group (0 = 64)
 };
+
+// Quantized attention with the reference's arithmetic (vkv_refattn.hip):
+// scores stored in the query dtype, the reference softmax (AccT = T) in its
+// own pass, then P.V.  One launch covers the query positions
+// [l0, l0 + nl) of every batch row.
+constexpr int kMaxRefD = 256;
+struct RefArgs {
+  AttnArgs a;
+  int32_t group, bits;
+  int32_t deq_round;       // K/V dequantized to the dtype first (the tiled matmul path)
+  int32_t score_f32;       // an f32 additive mask: f32 scores, fp32 softmax, f32 weights
+  int32_t l0, nl;
+  float* sc;               // scores, then weights: [B][Hq][nl][tpad]
+  int64_t tpad;
+  int32_t n_parts, part_tokens;
+  float* ws;               // P.V partials [n_parts][n_rows][Dv] (n_parts > 1)
+  int64_t n_rows;          // B * Hq * nl
+};
+size_t ref_scores_lds(int D);
+size_t ref_pv_lds(int Dv);
+// P.V token split for a launch; returns the part length (a multiple of 64)
+int ref_part_tokens(int64_t B, int Hkv, int nrows, int64_t T, int* n_parts);
+void launch_ref_attention(int dtype, const RefArgs& r, int64_t B, hipStream_t st);
+// The reference softmax in place over bf16 score rows (row r holds
+// seq_lens[r / per_b] scores, or T when seq_lens is null).
+void launch_ref_softmax_bf16(uint16_t* sc, int64_t rows, int64_t tpad, const int32_t* seq_lens,
+                             int32_t T, int64_t per_b, hipStream_t st);
 
 // ---- launchers (vkv_kernels.hip) ----
 void launch_quantize_rows(int dtype, int bits, int group, int mode, const RowSrc& src,

@@ -9,6 +9,7 @@
 // (quantized SDPA semantics).
 #include "vkv_device.h"
 #include "vkv_internal.h"
+#include "vkv_kvread.h"
 
 #include <algorithm>
 
@@ -348,86 +349,6 @@ __global__ void __launch_bounds__(256) dequantize_kernel(const uint32_t* wq, con
   }
 }
 
-// ---------------------------------------------------------------- KV access
-
-struct TokLoc {
-  int64_t blk;  // block id (paged) or sequence index (dense)
-  int64_t tib;  // token index inside the block (or sequence)
-};
-
-__device__ __forceinline__ TokLoc locate(const KVSrc& kv, int64_t s, int64_t t) {
-  TokLoc r;
-  if (kv.table) {
-    r.blk = kv.table[s * kv.table_stride + t / kv.block_size];
-    r.tib = t % kv.block_size;
-  } else {
-    r.blk = s;
-    r.tib = t;
-  }
-  return r;
-}
-
-__device__ __forceinline__ const uint8_t* at(const Comp& c, const TokLoc& l, int64_t h) {
-  return c.ptr + l.blk * c.sb + h * c.sh + l.tib * c.st;
-}
-
-// code of element d of a token-major codes row
-template <int BITS>
-__device__ __forceinline__ uint32_t code_tm(const uint8_t* row, int d) {
-  if constexpr (BITS == 8) return row[d];
-  return (row[d >> 1] >> (4 * (d & 1))) & 15u;
-}
-
-// Raw affine code of element d of the token at `l` (which: 0 = K, 1 = V)
-// with its stored scale and bias, for either the paged chunk format or the
-// reference layout.  Values of a keys-only (MLA) chunk are its key entries.
-template <int DT, int BITS>
-__device__ __forceinline__ uint32_t qcode(const KVSrc& kv, const TokLoc& l, int64_t h, int d,
-                                          int which, int group, float* s, float* b) {
-  using E = Elem<DT>;
-  const int g = d / group;
-  if (kv.qfmt) {
-    const uint8_t* chunk = kv.base + l.blk * kv.block_bytes + h * kv.head_bytes;
-    const typename E::T* sb = reinterpret_cast<const typename E::T*>(chunk + kv.sb_off);
-    const bool ko = kv.keys_only != 0;
-    const int w = (which && !ko) ? 1 : 0;
-    *s = E::load(sb + qsb_index(l.tib, w, g, 0, kv.G, ko));
-    *b = E::load(sb + qsb_index(l.tib, w, g, 1, kv.G, ko));
-    if (w == 0) {
-      constexpr int per = 32 / BITS;
-      const uint32_t word = *reinterpret_cast<const uint32_t*>(
-          chunk + kv.kc_off + qk_word_off(l.tib, d / per, kv.D, BITS));
-      return (word >> (BITS * (d % per))) & ((1u << BITS) - 1u);
-    }
-    int sh;
-    const uint32_t word =
-        *reinterpret_cast<const uint32_t*>(chunk + kv.vc_off + qv_word_off(l.tib, d, kv.D, BITS, &sh));
-    return (word >> sh) & ((1u << BITS) - 1u);
-  }
-  const Comp& cc = which ? kv.vc : kv.kc;
-  const Comp& sc = which ? kv.vs : kv.ks;
-  const Comp& bc = which ? kv.vb : kv.kb;
-  *s = E::load(reinterpret_cast<const typename E::T*>(at(sc, l, h)) + g);
-  *b = E::load(reinterpret_cast<const typename E::T*>(at(bc, l, h)) + g);
-  return code_tm<BITS>(at(cc, l, h), d);
-}
-
-// K (which 0) or V (which 1) element as float: float blocks load it,
-// affine blocks dequantize it as fp32 scale * code + bias.
-template <int DT, int BITS>
-__device__ __forceinline__ float kv_at(const KVSrc& kv, const TokLoc& l, int64_t h, int d, int which,
-                                       int group) {
-  using E = Elem<DT>;
-  if constexpr (BITS == 0) {
-    const Comp& c = which ? kv.vc : kv.kc;
-    return E::load(reinterpret_cast<const typename E::T*>(at(c, l, h)) + d);
-  } else {
-    float s, b;
-    const uint32_t c = qcode<DT, BITS>(kv, l, h, d, which, group, &s, &b);
-    return fmaf(s, static_cast<float>(c), b);
-  }
-}
-
 // --------------------------------------------------------------- gather
 //
 // Thread per (seq, head, token, 8 dims).  out_kind 0: values (dequantized
@@ -736,7 +657,6 @@ __global__ void __launch_bounds__(256) fill_normal_kernel(void* data, int64_t n,
 // fp32, masked keys skipped, an empty row yields zeros.
 constexpr int kTile = 32;
 constexpr int kMaxD = 256;
-constexpr int kGroup = 64;  // affine attention group size
 
 template <int DT, int BITS, int REP, bool QSEM>
 __global__ void __launch_bounds__(256) attn_partial_kernel(AttnArgs a, int h_off, int rep_total) {
@@ -757,6 +677,7 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(AttnArgs a, int h_off
   const int64_t t_begin = static_cast<int64_t>(part) * a.part_tokens;
   const int64_t t_end = min<int64_t>(T, t_begin + a.part_tokens);
   const float lowest = -E::kMax;
+  const int group = a.group > 0 ? a.group : 64;
 
   // queries of the REP heads sharing kv head hk
   const float scale_t = QSEM ? round_to<DT>(a.scale) : a.scale;
@@ -796,7 +717,7 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(AttnArgs a, int h_off
       if (t < t_end) {
         const TokLoc loc = locate(a.kv, b, t);
         for (int d = lane; d < D; d += 8) {
-          const float kv = kv_at<DT, BITS>(a.kv, loc, hk, d, 0, kGroup);
+          const float kv = kv_at<DT, BITS>(a.kv, loc, hk, d, 0, group);
 #pragma unroll
           for (int r = 0; r < REP; r++) acc[r] = fmaf(qs[r][d], kv, acc[r]);
         }
@@ -870,7 +791,7 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(AttnArgs a, int h_off
         const int64_t t = t0 + tt;
         if (t >= t_end) break;
         const TokLoc loc = locate(a.kv, b, t);
-        const float vv = kv_at<DT, BITS>(a.kv, loc, hk, vd, 1, kGroup);
+        const float vv = kv_at<DT, BITS>(a.kv, loc, hk, vd, 1, group);
 #pragma unroll
         for (int r = 0; r < REP; r++) o[r] = fmaf(sc[r][tt], vv, o[r]);
       }
@@ -1376,7 +1297,9 @@ void launch_attention(int dtype, int bits, int group, bool quant_semantics,
   if (rows <= 0) return;
   VKV_CHECK(a.D <= kMaxD && a.Dv <= kMaxD, "head dims above 256 are not supported here");
   VKV_CHECK(a.Hq % a.Hkv == 0, "query heads must be a multiple of kv heads");
-  VKV_CHECK(bits == 0 || group == 64, "affine attention supports group_size 64");
+  VKV_CHECK(bits == 0 || group == 32 || group == 64 || group == 128,
+            "affine attention supports group_size 32, 64 or 128");
+  VKV_CHECK(bits == 0 || a.group == group, "the attention arguments carry another group size");
   switch (dtype) {
     case kF32: attn_dispatch<kF32>(bits, quant_semantics, a, rows, st); break;
     case kF16: attn_dispatch<kF16>(bits, quant_semantics, a, rows, st); break;

@@ -1,0 +1,459 @@
+// vkv_refattn.hip -- quantized attention with the reference's own
+// arithmetic, in three passes over any query length, mask, group size and
+// float dtype:
+//
+//   1. scores:  q (times the dtype-rounded scale, rounded to the dtype) .
+//      dequant(K), accumulated in fp32 and stored in the query dtype, as
+//      quantizedMM returns T (Libraries/MLXLMCommon/KVCache.swift:1945-1949);
+//      the mask as :1951-1975 applies it (causal / bool: where(mask, s,
+//      finfo.min); additive: s + mask, in T for a mask of T, promoted to
+//      f32 for an f32 mask);
+//   2. softmax(scores, axis: -1) with precise: false (:1982,
+//      Source/MLX/Ops.swift:2702-2710): the Metal kernels' default
+//      AccT = T (Source/Cmlx/mlx-generated/metal/softmax.h:10, :100), i.e.
+//      exponentials, partial sums and the normaliser rounded to T, with the
+//      grouping of softmax_single_row (:10-98: 4 consecutive keys per
+//      thread, 32-thread simd sums, then their sum) for rows of up to 4096
+//      keys and of softmax_looped (:100-190: 1024 threads, each a running
+//      (max, sum) rescaled at every round) above; weights stored in T.  An
+//      f32 additive mask keeps the row in f32 (fp32 softmax, f32 weights);
+//   3. P.V: the stored weights times dequant(V), fp32 accumulation, the
+//      output rounded to T.
+// With 16 or more query tokens the reference's quantized matmul runs its
+// tiled path, which dequantizes K and V tiles to T first
+// (quantized.h:568-576, :686-713): deq_round rounds them the same way.
+//
+// The softmax pass mirrors that grouping exactly and does its sums in
+// fp64 (each partial sum rounded as the AccT arithmetic rounds it), so
+// from the same stored scores it produces the same weights bit for bit as
+// the oracle's restatement.  The order of the fp32 additions inside one
+// Metal simd_sum is the hardware's and not in the tree; fp64 sums of at
+// most 32 dtype-rounded terms are exact in practice, so any order agrees.
+//
+// This path trades speed for the reference's rounding: the score buffer is
+// written and read back, and the softmax is its own pass.  One-token decode
+// over paged bf16 4/8-bit views runs passes 1 and 3 on matrix cores
+// instead (qdecode_kernel's score and weight modes, vkv_decode.hip).
+#include "vkv_device.h"
+#include "vkv_internal.h"
+#include "vkv_kvread.h"
+
+#include <algorithm>
+
+namespace vkv {
+
+namespace {
+
+constexpr int kRefTile = 64;    // tokens per score / P.V tile
+constexpr int kRefRows = 16;    // query rows per block of the score and P.V passes
+constexpr int kSoftmaxThreads = 1024;
+constexpr int kSoftmaxReads = 4;
+constexpr int kSoftmaxLoopedLimit = 4096;
+
+__device__ __forceinline__ int64_t row_len(const KVSrc& kv, int64_t b) {
+  return kv.seq_lens ? kv.seq_lens[b] : kv.T;
+}
+
+// x rounded to float, then to dtype dt (0 f32, 1 f16, 2 bf16): the AccT
+// arithmetic's rounding of an fp64 value.
+__device__ __forceinline__ double rnd_d(double x, int dt) {
+  const float f = static_cast<float>(x);
+  if (dt == kF16) return static_cast<double>(round_to<kF16>(f));
+  if (dt == kBF16) return static_cast<double>(round_to<kBF16>(f));
+  return static_cast<double>(f);
+}
+__device__ __forceinline__ double t_exp(double x, int dt) { return rnd_d(exp(x), dt); }
+
+__device__ __forceinline__ double type_max_d(int dt) {
+  return dt == kF16 ? 65504.0 : dt == kBF16 ? 3.38953139e38 : 3.402823466e38;
+}
+
+// Score / weight storage: float, or bf16 bit patterns (the matrix-core
+// decode path's bf16 rows).
+template <typename S> struct Store;
+template <> struct Store<float> {
+  __device__ __forceinline__ static double get(const float* p, int64_t i) { return p[i]; }
+  __device__ __forceinline__ static void put(float* p, int64_t i, double v) { p[i] = static_cast<float>(v); }
+};
+template <> struct Store<uint16_t> {
+  __device__ __forceinline__ static double get(const uint16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+  __device__ __forceinline__ static void put(uint16_t* p, int64_t i, double v) {
+    p[i] = f32_to_bf16(static_cast<float>(v));
+  }
+};
+
+}  // namespace
+
+// ---- pass 1: scores.  Workgroup = one (64-token tile, kv head, batch
+// row); the tile's keys are dequantized into LDS once, then every query row
+// of the kv head (rep heads x the batch of query positions) is scored
+// against them, 16 rows at a time.
+template <int DT, int BITS>
+__global__ void __launch_bounds__(256) ref_scores_kernel(RefArgs r) {
+  using E = Elem<DT>;
+  const AttnArgs& a = r.a;
+  extern __shared__ float smem[];
+  __shared__ TokLoc loc[kRefTile];
+  const int D = a.D, tid = threadIdx.x;
+  const int hk = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int64_t T = row_len(a.kv, b);
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kRefTile;
+  if (t0 >= T) return;
+  const int nt = static_cast<int>(min<int64_t>(kRefTile, T - t0));
+  float* kt = smem;                         // [kRefTile][D + 1]
+  float* qs = smem + kRefTile * (D + 1);    // [kRefRows][D]
+  if (tid < nt) loc[tid] = locate(a.kv, b, t0 + tid);
+  __syncthreads();
+  for (int i = tid; i < nt * D; i += 256) {
+    const int t = i / D, d = i % D;
+    const float v = kv_at<DT, BITS>(a.kv, loc[t], hk, d, 0, r.group);
+    kt[t * (D + 1) + d] = r.deq_round ? round_to<DT>(v) : v;
+  }
+  const int rep = a.Hq / a.Hkv, nl = r.nl, nrows = rep * nl;
+  const float scale_t = round_to<DT>(a.scale);
+  const int tt = tid & 63, rg = tid >> 6;
+  const float lowest = -E::kMax;
+  for (int rb = 0; rb < nrows; rb += kRefRows) {
+    __syncthreads();  // the key tile is complete; the previous rows are done
+    for (int i = tid; i < kRefRows * D; i += 256) {
+      const int ri = rb + i / D, d = i % D;
+      float v = 0.0f;
+      if (ri < nrows) {
+        const int h = hk * rep + ri / nl, l = r.l0 + ri % nl;
+        const float qv = E::load(static_cast<const typename E::T*>(a.q) + b * a.q_sb + h * a.q_sh +
+                                 static_cast<int64_t>(l) * a.q_sl + d);
+        v = round_to<DT>(qv * scale_t);
+      }
+      qs[i] = v;
+    }
+    __syncthreads();
+    if (tt >= nt) continue;
+    const float* kr = kt + tt * (D + 1);
+    const int64_t t = t0 + tt;
+    for (int k = rg; k < kRefRows; k += 4) {
+      const int ri = rb + k;
+      if (ri >= nrows) break;
+      const float* qr = qs + k * D;
+      float acc = 0.0f;
+      for (int d = 0; d < D; d++) acc = fmaf(qr[d], kr[d], acc);
+      const int h = hk * rep + ri / nl, li = ri % nl, l = r.l0 + li;
+      float s = round_to<DT>(acc);
+      bool vis = true;
+      if (a.mask_mode == 1) {
+        vis = t <= T - a.L + l;
+      } else if (a.mask_mode >= 2) {
+        const int64_t mo = b * a.m_sb + h * a.m_sh + static_cast<int64_t>(l) * a.m_sl + t * a.m_st;
+        if (a.mask_mode == 2) {
+          vis = static_cast<const uint8_t*>(a.mask)[mo] != 0;
+        } else {
+          const float add = load_f32(a.mask, a.mask_dtype, mo);
+          s = a.mask_dtype == DT ? round_to<DT>(s + add) : s + add;
+        }
+      }
+      if (!vis) s = lowest;
+      r.sc[((b * a.Hq + h) * nl + li) * r.tpad + t] = s;
+    }
+  }
+}
+
+// ---- pass 2: the reference softmax of one row (workgroup of 1024
+// threads), in place over the stored scores.  acc_dt: the AccT dtype, or -1
+// for the fp32 arithmetic of an f32-promoted row; w_dt: the weights' dtype.
+template <typename S>
+__global__ void __launch_bounds__(kSoftmaxThreads) ref_softmax_kernel(S* sc, int64_t tpad,
+                                                                      const int32_t* seq_lens,
+                                                                      int32_t T_all, int64_t per_b,
+                                                                      int acc_dt, int w_dt) {
+  using St = Store<S>;
+  __shared__ double red[kSoftmaxThreads];
+  __shared__ double red_m[kSoftmaxThreads];
+  __shared__ double simd_s[kSoftmaxThreads / 32], simd_m[kSoftmaxThreads / 32];
+  __shared__ double bcast[2];
+  const int64_t row = blockIdx.x;
+  const int64_t T = seq_lens ? seq_lens[row / per_b] : T_all;
+  if (T <= 0) return;
+  S* p = sc + row * tpad;
+  const int lid = threadIdx.x;
+
+  // row max (of stored values: exact in any order)
+  double mx = -INFINITY;
+  for (int64_t t = lid; t < T; t += kSoftmaxThreads) mx = fmax(mx, St::get(p, t));
+  red_m[lid] = mx;
+  __syncthreads();
+  for (int o = kSoftmaxThreads / 2; o > 0; o >>= 1) {
+    if (lid < o) red_m[lid] = fmax(red_m[lid], red_m[lid + o]);
+    __syncthreads();
+  }
+  mx = red_m[0];
+  __syncthreads();
+
+  if (acc_dt < 0) {
+    // fp32 arithmetic: exp of the f32 difference, summed, one reciprocal
+    double sum = 0.0;
+    for (int64_t t = lid; t < T; t += kSoftmaxThreads)
+      sum += static_cast<double>(static_cast<float>(exp(static_cast<double>(static_cast<float>(St::get(p, t) - mx)))));
+    red[lid] = sum;
+    __syncthreads();
+    for (int o = kSoftmaxThreads / 2; o > 0; o >>= 1) {
+      if (lid < o) red[lid] += red[lid + o];
+      __syncthreads();
+    }
+    const float rr = static_cast<float>(1.0 / static_cast<double>(static_cast<float>(red[0])));
+    for (int64_t t = lid; t < T; t += kSoftmaxThreads) {
+      const float e = static_cast<float>(exp(static_cast<double>(static_cast<float>(St::get(p, t) - mx))));
+      St::put(p, t, rnd_d(static_cast<double>(e * rr), w_dt));
+    }
+    return;
+  }
+  const int dt = acc_dt;
+  if (T <= kSoftmaxLoopedLimit) {
+    // softmax_single_row: thread lid owns keys 4 lid .. 4 lid + 3
+    double e[kSoftmaxReads];
+    double thr = 0.0;
+#pragma unroll
+    for (int i = 0; i < kSoftmaxReads; i++) {
+      const int64_t t = static_cast<int64_t>(kSoftmaxReads) * lid + i;
+      e[i] = t < T ? t_exp(rnd_d(St::get(p, t) - mx, dt), dt) : 0.0;
+      if (t < T) thr = rnd_d(thr + e[i], dt);
+    }
+    red[lid] = thr;
+    __syncthreads();
+    const int nsimd = static_cast<int>((T + 127) / 128);
+    if (lid < nsimd) {  // the simd sum of threads 32 lid .. 32 lid + 31, in their order
+      double s = 0.0;
+      for (int k = 0; k < 32; k++) s += red[32 * lid + k];
+      simd_s[lid] = rnd_d(s, dt);
+    }
+    __syncthreads();
+    if (lid == 0) {
+      double total = 0.0;
+      for (int g = 0; g < nsimd; g++) total += simd_s[g];
+      bcast[0] = rnd_d(1.0 / rnd_d(total, dt), dt);
+    }
+    __syncthreads();
+    const double rr = bcast[0];
+#pragma unroll
+    for (int i = 0; i < kSoftmaxReads; i++) {
+      const int64_t t = static_cast<int64_t>(kSoftmaxReads) * lid + i;
+      if (t < T) St::put(p, t, rnd_d(e[i] * rr, dt));
+    }
+    return;
+  }
+  // softmax_looped: each thread a running (max, sum) over keys
+  // lid * 4 + 4096 r + i, rescaled at every round
+  const double fmin = -type_max_d(dt);
+  const int64_t stride = static_cast<int64_t>(kSoftmaxReads) * kSoftmaxThreads;
+  const int64_t rounds = (T + stride - 1) / stride;
+  double m = fmin, n = 0.0;
+  for (int64_t rd = 0; rd < rounds; rd++) {
+    const int64_t off = rd * stride + static_cast<int64_t>(lid) * kSoftmaxReads;
+    double v[kSoftmaxReads];
+    const double prev = m;
+#pragma unroll
+    for (int i = 0; i < kSoftmaxReads; i++) {
+      v[i] = off + i < T ? St::get(p, off + i) : -INFINITY;
+      m = v[i] > m ? v[i] : m;
+    }
+    n = rnd_d(n * t_exp(rnd_d(prev - m, dt), dt), dt);
+#pragma unroll
+    for (int i = 0; i < kSoftmaxReads; i++) n = rnd_d(n + t_exp(rnd_d(v[i] - m, dt), dt), dt);
+  }
+  red_m[lid] = m;
+  red[lid] = n;
+  __syncthreads();
+  if (lid < kSoftmaxThreads / 32) {  // simdgroup lid: max, then the rescaled sums in order
+    double mg = fmin, acc = 0.0;
+    for (int k = 0; k < 32; k++) mg = red_m[32 * lid + k] > mg ? red_m[32 * lid + k] : mg;
+    for (int k = 0; k < 32; k++)
+      acc += rnd_d(red[32 * lid + k] * t_exp(rnd_d(red_m[32 * lid + k] - mg, dt), dt), dt);
+    simd_m[lid] = mg;
+    simd_s[lid] = rnd_d(acc, dt);
+  }
+  __syncthreads();
+  if (lid == 0) {
+    double gmax = fmin;
+    for (int g = 0; g < kSoftmaxThreads / 32; g++) gmax = simd_m[g] > gmax ? simd_m[g] : gmax;
+    double total = 0.0;
+    for (int g = 0; g < kSoftmaxThreads / 32; g++)
+      total += rnd_d(simd_s[g] * t_exp(rnd_d(simd_m[g] - gmax, dt), dt), dt);
+    bcast[0] = gmax;
+    bcast[1] = rnd_d(1.0 / rnd_d(total, dt), dt);
+  }
+  __syncthreads();
+  const double gmax = bcast[0], rr = bcast[1];
+  for (int64_t t = lid; t < T; t += kSoftmaxThreads)
+    St::put(p, t, rnd_d(t_exp(rnd_d(St::get(p, t) - gmax, dt), dt) * rr, dt));
+}
+
+// ---- pass 3: out = sum_t w_t dequant(v_t).  Workgroup = (token part, kv
+// head x 16-row block, batch row); value tiles dequantized into LDS, each
+// thread owns up to 16 (row, dim) outputs; parts are summed in order by
+// ref_merge_kernel.
+template <int DT, int BITS>
+__global__ void __launch_bounds__(256) ref_pv_kernel(RefArgs r) {
+  using E = Elem<DT>;
+  const AttnArgs& a = r.a;
+  extern __shared__ float smem[];
+  __shared__ TokLoc loc[kRefTile];
+  __shared__ float wt[kRefRows][kRefTile];
+  const int Dv = a.Dv, tid = threadIdx.x;
+  const int rep = a.Hq / a.Hkv, nl = r.nl, nrows = rep * nl;
+  const int nrb = (nrows + kRefRows - 1) / kRefRows;
+  const int hk = blockIdx.y / nrb, rb = (blockIdx.y % nrb) * kRefRows;
+  const int64_t b = blockIdx.z;
+  const int part = blockIdx.x;
+  const int64_t T = row_len(a.kv, b);
+  const int64_t tb = static_cast<int64_t>(part) * r.part_tokens;
+  const int64_t te = min<int64_t>(T, tb + r.part_tokens);
+  float* vt = smem;  // [kRefTile][Dv]
+  constexpr int kOut = kRefRows * 256 / 256;  // outputs per thread at Dv <= 256
+  float acc[kOut];
+#pragma unroll
+  for (int k = 0; k < kOut; k++) acc[k] = 0.0f;
+  const int nout = kRefRows * Dv;
+  for (int64_t t0 = tb; t0 < te; t0 += kRefTile) {
+    const int nt = static_cast<int>(min<int64_t>(kRefTile, te - t0));
+    __syncthreads();  // the previous tile is consumed
+    if (tid < nt) loc[tid] = locate(a.kv, b, t0 + tid);
+    for (int i = tid; i < kRefRows * kRefTile; i += 256) {
+      const int k = i / kRefTile, t = i % kRefTile;
+      const int ri = rb + k;
+      float w = 0.0f;
+      if (ri < nrows && t < nt) {
+        const int h = hk * rep + ri / nl, li = ri % nl;
+        w = r.sc[((b * a.Hq + h) * nl + li) * r.tpad + t0 + t];
+      }
+      wt[k][t] = w;
+    }
+    __syncthreads();
+    for (int i = tid; i < nt * Dv; i += 256) {
+      const int t = i / Dv, d = i % Dv;
+      const float v = kv_at<DT, BITS>(a.kv, loc[t], hk, d, 1, r.group);
+      vt[t * Dv + d] = r.deq_round ? round_to<DT>(v) : v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kOut; k++) {
+      const int o = tid + 256 * k;
+      if (o >= nout) break;
+      const int row = o / Dv, d = o % Dv;
+      float s = acc[k];
+      for (int t = 0; t < nt; t++) s = fmaf(wt[row][t], vt[t * Dv + d], s);
+      acc[k] = s;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kOut; k++) {
+    const int o = tid + 256 * k;
+    if (o >= nout) break;
+    const int row = o / Dv, d = o % Dv;
+    const int ri = rb + row;
+    if (ri >= nrows) continue;
+    const int h = hk * rep + ri / nl, li = ri % nl;
+    const int64_t ridx = (b * a.Hq + h) * nl + li;
+    if (r.n_parts == 1) {
+      static_cast<typename E::T*>(a.out)[b * a.o_sb + h * a.o_sh +
+                                         static_cast<int64_t>(r.l0 + li) * a.o_sl + d] = E::from_f32(acc[k]);
+    } else {
+      r.ws[(static_cast<int64_t>(part) * r.n_rows + ridx) * Dv + d] = acc[k];
+    }
+  }
+}
+
+// The parts' sums, added in part order.
+template <int DT>
+__global__ void __launch_bounds__(256) ref_merge_kernel(RefArgs r) {
+  using E = Elem<DT>;
+  const AttnArgs& a = r.a;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= r.n_rows * a.Dv) return;
+  const int64_t ridx = i / a.Dv;
+  const int d = static_cast<int>(i % a.Dv);
+  float s = 0.0f;
+  for (int p = 0; p < r.n_parts; p++) s += r.ws[(static_cast<int64_t>(p) * r.n_rows + ridx) * a.Dv + d];
+  const int nl = r.nl;
+  const int64_t li = ridx % nl, bh = ridx / nl, h = bh % a.Hq, b = bh / a.Hq;
+  static_cast<typename E::T*>(a.out)[b * a.o_sb + h * a.o_sh + (r.l0 + li) * a.o_sl + d] = E::from_f32(s);
+}
+
+// ---------------------------------------------------------------- host
+
+size_t ref_scores_lds(int D) { return sizeof(float) * (kRefTile * (D + 1) + kRefRows * D); }
+size_t ref_pv_lds(int Dv) { return sizeof(float) * kRefTile * Dv; }
+
+int ref_part_tokens(int64_t B, int Hkv, int nrows, int64_t T, int* n_parts) {
+  const int64_t nrb = (nrows + kRefRows - 1) / kRefRows;
+  const int64_t groups = std::max<int64_t>(1, B * Hkv * nrb);
+  int64_t parts = std::max<int64_t>(1, (2048 + groups - 1) / groups);
+  parts = std::min<int64_t>(parts, std::max<int64_t>(1, (T + kRefTile - 1) / kRefTile));
+  int64_t pt = (std::max<int64_t>(T, 1) + parts - 1) / parts;
+  pt = (pt + kRefTile - 1) / kRefTile * kRefTile;
+  *n_parts = static_cast<int>(std::max<int64_t>(1, (T + pt - 1) / pt));
+  return static_cast<int>(pt);
+}
+
+template <int DT, int BITS>
+static void ref_launch_dt(const RefArgs& r, int64_t B, hipStream_t st) {
+  const AttnArgs& a = r.a;
+  const int rep = a.Hq / a.Hkv, nrows = rep * r.nl;
+  const int64_t T = a.kv.T;
+  const dim3 gs(static_cast<unsigned>((std::max<int64_t>(T, 1) + kRefTile - 1) / kRefTile),
+                static_cast<unsigned>(a.Hkv), static_cast<unsigned>(B));
+  // above 64 KB of dynamic LDS (head dims over ~200) the kernel must ask
+  static const bool lds_ok = [] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&ref_scores_kernel<DT, BITS>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               static_cast<int>(ref_scores_lds(kMaxRefD))) == hipSuccess;
+  }();
+  VKV_CHECK(lds_ok, "cannot raise the score kernel's LDS limit");
+  hipLaunchKernelGGL((ref_scores_kernel<DT, BITS>), gs, dim3(256), ref_scores_lds(a.D), st, r);
+  VKV_HIP(hipGetLastError());
+  const int acc_dt = r.score_f32 ? -1 : DT;
+  const int w_dt = r.score_f32 ? kF32 : DT;
+  hipLaunchKernelGGL((ref_softmax_kernel<float>), dim3(static_cast<unsigned>(B * a.Hq * r.nl)),
+                     dim3(kSoftmaxThreads), 0, st, r.sc, r.tpad, a.kv.seq_lens, a.kv.T,
+                     static_cast<int64_t>(a.Hq) * r.nl, acc_dt, w_dt);
+  VKV_HIP(hipGetLastError());
+  const int nrb = (nrows + kRefRows - 1) / kRefRows;
+  const dim3 gp(static_cast<unsigned>(r.n_parts), static_cast<unsigned>(a.Hkv * nrb),
+                static_cast<unsigned>(B));
+  hipLaunchKernelGGL((ref_pv_kernel<DT, BITS>), gp, dim3(256), ref_pv_lds(a.Dv), st, r);
+  VKV_HIP(hipGetLastError());
+  if (r.n_parts > 1) {
+    const int64_t n = r.n_rows * a.Dv;
+    hipLaunchKernelGGL((ref_merge_kernel<DT>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                       st, r);
+    VKV_HIP(hipGetLastError());
+  }
+}
+
+template <int DT>
+static void ref_launch_bits(const RefArgs& r, int64_t B, hipStream_t st) {
+  if (r.bits == 4) ref_launch_dt<DT, 4>(r, B, st);
+  else if (r.bits == 8) ref_launch_dt<DT, 8>(r, B, st);
+  else throw Error("reference-arithmetic attention needs an affine 4- or 8-bit cache");
+}
+
+void launch_ref_attention(int dtype, const RefArgs& r, int64_t B, hipStream_t st) {
+  VKV_CHECK(r.a.D <= kMaxRefD && r.a.Dv <= kMaxRefD, "head dims above 256 are not supported here");
+  VKV_CHECK(r.a.Hq % r.a.Hkv == 0, "query heads must be a multiple of kv heads");
+  switch (dtype) {
+    case kF32: ref_launch_bits<kF32>(r, B, st); break;
+    case kF16: ref_launch_bits<kF16>(r, B, st); break;
+    case kBF16: ref_launch_bits<kBF16>(r, B, st); break;
+    default: throw Error("unsupported dtype");
+  }
+}
+
+// The reference softmax over bf16 score rows (the matrix-core decode
+// path): rows of seq_lens[row / per_b] (or T) scores, tpad apart.
+void launch_ref_softmax_bf16(uint16_t* sc, int64_t rows, int64_t tpad, const int32_t* seq_lens,
+                             int32_t T, int64_t per_b, hipStream_t st) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL((ref_softmax_kernel<uint16_t>), dim3(static_cast<unsigned>(rows)),
+                     dim3(kSoftmaxThreads), 0, st, sc, tpad, seq_lens, T, per_b, kBF16, kBF16);
+  VKV_HIP(hipGetLastError());
+}
+
+}  // namespace vkv
