@@ -318,6 +318,16 @@ static inline double deq_at(const uint32_t *row, const float *s, const float *b,
   return round_dt >= 0 ? (double)round_to((float)x, round_dt) : x;
 }
 
+/* K or V element (t, d) of one (batch row, kv head): from the
+ * pre-dequantized [T][D] values when given, else dequantized in place. */
+static inline double kv_val(const double *pre, const uint32_t *codes, const float *s,
+                            const float *b, int64_t t, int d, int D, int group, int bits,
+                            int deq_dt) {
+  if (pre) return pre[t * D + d];
+  const int wpr = D * bits / 32, G = D / group;
+  return deq_at(codes + t * wpr, s + t * G, b + t * G, d, group, bits, deq_dt);
+}
+
 static inline double round_d(double x, int dtype) {
   return (double)round_to((float)x, dtype);
 }
@@ -472,10 +482,8 @@ static void qsdpa_row(const float *qs, const uint32_t *kq, const float *ks,
                       const float *vb, int T, int D, int group, int bits,
                       const double *add, const unsigned char *vis, double fill,
                       int rnd, int sdt, double *sc, double *pw, double *pe, double *o,
-                      double *wb, double *fb) {
-  const int wpr = D * bits / 32;
-  const int G = D / group;
-  const int deq_dt = (rnd == 2 || rnd == 4) ? sdt : -1;
+                      double *wb, double *fb, const double *kd, const double *vd) {
+    const int deq_dt = (rnd == 2 || rnd == 4) ? sdt : -1;
   const int wdt = add ? 0 : sdt;
   /* flip factors exp(n_t - r_t) for scores near a rounding boundary (0: none),
    * and the flipped score itself (the other neighbour, mask added) */
@@ -485,12 +493,10 @@ static void qsdpa_row(const float *qs, const uint32_t *kq, const float *ks,
   for (int t = 0; t < T; t++) {
     double s = fill;
     if (!vis || vis[t]) {
-      const uint32_t *kr = kq + (int64_t)t * wpr;
       s = 0.0;
       double mag = 0.0;
       for (int d = 0; d < D; d++) {
-        const double kv = deq_at(kr, ks + (int64_t)t * G, kb + (int64_t)t * G, d, group, bits,
-                                 deq_dt);
+        const double kv = kv_val(kd, kq, ks, kb, t, d, D, group, bits, deq_dt);
         s += (double)qs[d] * kv;
         mag += fabs((double)qs[d] * kv);
       }
@@ -523,10 +529,8 @@ static void qsdpa_row(const float *qs, const uint32_t *kq, const float *ks,
   if (fb)
     for (int d = 0; d < D; d++) fb[d] = 0.0;
   for (int t = 0; t < T; t++) {
-    const uint32_t *vr = vq + (int64_t)t * wpr;
     for (int d = 0; d < D; d++) {
-      const double vv = deq_at(vr, vs + (int64_t)t * G, vb + (int64_t)t * G, d, group, bits,
-                               deq_dt);
+      const double vv = kv_val(vd, vq, vs, vb, t, d, D, group, bits, deq_dt);
       o[d] += pw[t] * vv;
       if (wb) wb[d] += fabs(pw[t] - pe[t]) * fabs(vv);
       if (o1) o1[d] += pe[t] * vv;
@@ -538,10 +542,8 @@ static void qsdpa_row(const float *qs, const uint32_t *kq, const float *ks,
     for (int t = 0; t < T; t++) {
       if (flip[t] == 0.0) continue;
       const double a = (flip[t] - 1.0) * pe[t];
-      const uint32_t *vr = vq + (int64_t)t * wpr;
       for (int d = 0; d < D; d++) {
-        const double vv = deq_at(vr, vs + (int64_t)t * G, vb + (int64_t)t * G, d, group, bits,
-                                 deq_dt);
+        const double vv = kv_val(vd, vq, vs, vb, t, d, D, group, bits, deq_dt);
         wb[d] += fabs((o1[d] + a * vv) / (1.0 + a) - o1[d]);
       }
     }
@@ -564,10 +566,8 @@ static void qsdpa_row(const float *qs, const uint32_t *kq, const float *ks,
       for (int d = 0; d < D; d++) o2[d] = 0.0;
       for (int u = 0; u < T; u++) {
         if (pw2[u] == pw[u]) continue;
-        const uint32_t *vr = vq + (int64_t)u * wpr;
         for (int d = 0; d < D; d++)
-          o2[d] += (pw2[u] - pw[u]) * deq_at(vr, vs + (int64_t)u * G, vb + (int64_t)u * G, d,
-                                             group, bits, deq_dt);
+          o2[d] += (pw2[u] - pw[u]) * kv_val(vd, vq, vs, vb, u, d, D, group, bits, deq_dt);
       }
       for (int d = 0; d < D; d++) fb[d] += fabs(o2[d]);
     }
@@ -581,7 +581,10 @@ static void qsdpa_row(const float *qs, const uint32_t *kq, const float *ks,
   free(o1);
 }
 
-/* KVCache.swift:1909-1997 (quantizedScaledDotProductAttention). */
+/* KVCache.swift:1909-1997 (quantizedScaledDotProductAttention).  Each
+ * (batch row, kv head)'s K and V are dequantized once (as the rounding mode
+ * rounds them); its query rows run in parallel (OpenMP), each on its own
+ * scratch, so the result does not depend on the thread count. */
 void vkvo_quantized_sdpa(const float *q, int q_dtype, const uint32_t *kq,
                          const float *ks, const float *kb, const uint32_t *vq,
                          const float *vs, const float *vb, int B, int Hq, int Hkv,
@@ -595,52 +598,73 @@ void vkvo_quantized_sdpa(const float *q, int q_dtype, const uint32_t *kq,
   const float scale_t = round_to(scale, q_dtype);
   const double fill = type_lowest(q_dtype);
   const size_t nT = (size_t)(T > 0 ? T : 1);
-  float *qs = (float *)malloc(sizeof(float) * (size_t)D);
-  double *sc = (double *)malloc(sizeof(double) * nT);
-  double *pw = (double *)malloc(sizeof(double) * nT);
-  double *pe = (double *)malloc(sizeof(double) * nT);
-  double *add = (double *)malloc(sizeof(double) * nT);
-  unsigned char *vis = (unsigned char *)malloc(nT);
+  const int deq_dt = (rounding == 2 || rounding == 4) ? q_dtype : -1;
+  double *kd = (double *)malloc(sizeof(double) * nT * (size_t)D);
+  double *vd = (double *)malloc(sizeof(double) * nT * (size_t)D);
   for (int b = 0; b < B; b++)
-    for (int h = 0; h < Hq; h++)
-      for (int l = 0; l < L; l++) {
-        const float *qr = q + (((int64_t)b * Hq + h) * L + l) * D;
-        for (int d = 0; d < D; d++) qs[d] = round_to(qr[d] * scale_t, q_dtype);
-        const int hk = h / rep;
-        const int64_t kv_row0 = ((int64_t)b * Hkv + hk) * T;
-        const int64_t orow = (((int64_t)b * Hq + h) * L + l) * D;
-        for (int t = 0; t < T; t++) {
-          double a;
-          int64_t mo = b * msb + h * msh + l * msl + t * mst;
-          if (mask_mode == 1) {
-            /* causal: query row l sits at key position l + (T - L) */
-            vis[t] = (unsigned char)(l + (T - L) >= t);
-            add[t] = 0.0;
-          } else {
-            vis[t] = (unsigned char)mask_visible(mask_mode == 3 ? 0 : mask_mode, bmask, fmask,
-                                                 mo, l, L, t, T, &a);
-            add[t] = mask_mode == 3 ? (double)fmask[mo] : 0.0;
+    for (int hk = 0; hk < Hkv; hk++) {
+      const int64_t kv_row0 = ((int64_t)b * Hkv + hk) * T;
+      for (int t = 0; t < T; t++)
+        for (int d = 0; d < D; d++) {
+          const int64_t r = kv_row0 + t;
+          kd[(int64_t)t * D + d] = deq_at(kq + r * wpr, ks + r * G, kb + r * G, d, group, bits, deq_dt);
+          vd[(int64_t)t * D + d] = deq_at(vq + r * wpr, vs + r * G, vb + r * G, d, group, bits, deq_dt);
+        }
+#ifdef _OPENMP
+#pragma omp parallel
+#endif
+      {
+        float *qs = (float *)malloc(sizeof(float) * (size_t)D);
+        double *sc = (double *)malloc(sizeof(double) * nT);
+        double *pw = (double *)malloc(sizeof(double) * nT);
+        double *pe = (double *)malloc(sizeof(double) * nT);
+        double *add = (double *)malloc(sizeof(double) * nT);
+        unsigned char *vis = (unsigned char *)malloc(nT);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (int rl = 0; rl < rep * L; rl++) {
+          const int h = hk * rep + rl / L, l = rl % L;
+          const float *qr = q + (((int64_t)b * Hq + h) * L + l) * D;
+          for (int d = 0; d < D; d++) qs[d] = round_to(qr[d] * scale_t, q_dtype);
+          const int64_t orow = (((int64_t)b * Hq + h) * L + l) * D;
+          for (int t = 0; t < T; t++) {
+            double a;
+            int64_t mo = b * msb + h * msh + l * msl + t * mst;
+            if (mask_mode == 1) {
+              /* causal: query row l sits at key position l + (T - L) */
+              vis[t] = (unsigned char)(l + (T - L) >= t);
+              add[t] = 0.0;
+            } else {
+              vis[t] = (unsigned char)mask_visible(mask_mode == 3 ? 0 : mask_mode, bmask, fmask,
+                                                   mo, l, L, t, T, &a);
+              add[t] = mask_mode == 3 ? (double)fmask[mo] : 0.0;
+            }
           }
+          if (T == 0) {
+            for (int d = 0; d < D; d++) out[orow + d] = 0.0;
+            if (wbound)
+              for (int d = 0; d < D; d++) wbound[orow + d] = 0.0;
+            if (fbound)
+              for (int d = 0; d < D; d++) fbound[orow + d] = 0.0;
+            continue;
+          }
+          qsdpa_row(qs, kq + kv_row0 * wpr, ks + kv_row0 * G, kb + kv_row0 * G,
+                    vq + kv_row0 * wpr, vs + kv_row0 * G, vb + kv_row0 * G, T, D, group,
+                    bits, mask_mode == 3 ? add : NULL, vis, fill, rounding, q_dtype, sc, pw, pe,
+                    out + orow, wbound ? wbound + orow : NULL, fbound ? fbound + orow : NULL, kd,
+                    vd);
         }
-        if (T == 0) {
-          for (int d = 0; d < D; d++) out[orow + d] = 0.0;
-          if (wbound)
-            for (int d = 0; d < D; d++) wbound[orow + d] = 0.0;
-          if (fbound)
-            for (int d = 0; d < D; d++) fbound[orow + d] = 0.0;
-          continue;
-        }
-        qsdpa_row(qs, kq + kv_row0 * wpr, ks + kv_row0 * G, kb + kv_row0 * G,
-                  vq + kv_row0 * wpr, vs + kv_row0 * G, vb + kv_row0 * G, T, D, group,
-                  bits, mask_mode == 3 ? add : NULL, vis, fill, rounding, q_dtype, sc, pw, pe,
-                  out + orow, wbound ? wbound + orow : NULL, fbound ? fbound + orow : NULL);
+        free(qs);
+        free(sc);
+        free(pw);
+        free(pe);
+        free(add);
+        free(vis);
       }
-  free(qs);
-  free(sc);
-  free(pw);
-  free(pe);
-  free(add);
-  free(vis);
+    }
+  free(kd);
+  free(vd);
 }
 
 void vkvo_quantized_decode_batch(const float *q, int q_dtype, const uint32_t *kq,
@@ -676,7 +700,8 @@ void vkvo_quantized_decode_batch(const float *q, int q_dtype, const uint32_t *kq
         const int64_t row0 = tok_off[s] + (int64_t)(h / rep) * T;
         qsdpa_row(qs, kq + row0 * wpr, ks + row0 * G, kb + row0 * G, vq + row0 * wpr,
                   vs + row0 * G, vb + row0 * G, (int)T, D, group, bits, NULL, NULL, 0.0,
-                  rounding, q_dtype, sc, pw, pe, out + ((int64_t)s * Hq + h) * D, NULL, NULL);
+                  rounding, q_dtype, sc, pw, pe, out + ((int64_t)s * Hq + h) * D, NULL, NULL, NULL,
+                  NULL);
       }
     free(qs);
     free(sc);

@@ -242,3 +242,63 @@ def test_reference_case_additive_mask(ref_mode, monkeypatch):
     out = q_attention(q, kt, vt, dtype, mask)
     ref = float_attention(q, k, v, dtype, mask)
     assert all_close(out, ref)
+
+
+def paged_scene(rng, bits, lens, Hkv, D, outliers, bs=32, dtype=O.BF16):
+    nblocks = sum((L + bs - 1) // bs for L in lens) + 2
+    pool = vkv.PagedPool(nblocks, bs, 1, Hkv, D, dtype=dtype, bits=bits)
+    perm = rng.permutation(np.arange(1, nblocks))
+    tables, slots, keys, vals, i = [], [], [], [], 0
+    for L in lens:
+        nb = (L + bs - 1) // bs
+        t = [int(b) for b in perm[i:i + nb]]
+        i += nb
+        tables.append(t)
+        slots += [t[p // bs] * bs + p % bs for p in range(L)]
+        keys.append(rand_bits(rng, (L, Hkv, D), dtype, outliers=outliers))
+        vals.append(rand_bits(rng, (L, Hkv, D), dtype, outliers=outliers))
+    pool.append(0, dev(np.concatenate(keys), dtype), dev(np.concatenate(vals), dtype),
+                torch.tensor(slots, dtype=torch.int32, device="cuda"))
+    width = max(1, max(len(t) for t in tables))
+    tab = np.zeros((len(lens), width), np.int32)
+    for s, t in enumerate(tables):
+        tab[s, :len(t)] = t
+    keep = (torch.from_numpy(tab).cuda(), torch.tensor(lens, dtype=torch.int32, device="cuda"))
+    view = pool.view(0, keep[0], keep[1], max(lens))
+    return pool, view, keys, vals, keep
+
+
+@pytest.mark.parametrize("bits,D,rep,lens", [
+    (4, 128, 4, [4100, 1, 0, 900, 33, 2048, 64, 4097]),
+    (8, 128, 4, [6000, 70, 3000]),
+    (4, 64, 8, [1500, 31, 250]),
+    (8, 256, 2, [2500, 100]),
+    (4, 128, 12, [700, 5]),
+])
+def test_paged_decode_reference_softmax_on_matrix_cores(bits, D, rep, lens, monkeypatch):
+    """The reference path of one-token paged decode on matrix cores (bf16
+    score rows from the decode kernel, the reference softmax over them, P.V
+    from the stored weights, partials summed): mixed lengths across the
+    4096-key switch to softmax_looped, empty and one-token sequences, 4 / 8
+    query heads per part and head groups, x20 outlier channels; against the
+    oracle's REF_DECODE at 2e-2 + 1 ulp + the score-boundary term."""
+    dtype, Hkv = O.BF16, 2
+    rng = np.random.default_rng(bits * 100 + D + rep)
+    print(f"paged reference decode: bits {bits} D {D} rep {rep} lens {lens}", flush=True)
+    pool, view, keys, vals, keep = paged_scene(rng, bits, lens, Hkv, D, outliers=4)
+    q = rand_bits(rng, (len(lens), Hkv * rep, D), dtype)
+    monkeypatch.setattr(OPTIONS, "reference_softmax", 1)
+    out = vkv.paged_attention(dev(q, dtype), view, D ** -0.5)
+    torch.cuda.synchronize()
+    got = values(out, dtype)
+    f = lambda a: O.to_f32(a, dtype)
+    for s, L in enumerate(lens):
+        if L == 0:
+            assert (got[s] == 0).all()
+            continue
+        rk = O.quantize(np.ascontiguousarray(keys[s].transpose(1, 0, 2)), dtype, 64, bits)
+        rv = O.quantize(np.ascontiguousarray(vals[s].transpose(1, 0, 2)), dtype, 64, bits)
+        ref, fb = (x[0, :, 0] for x in qref_flip(
+            f(q[s])[None, :, None], dtype, rk[0][None], f(rk[1])[None], f(rk[2])[None],
+            rv[0][None], f(rv[1])[None], f(rv[2])[None], D ** -0.5, 64, bits))
+        assert_refclose(got[s], ref, fb, dtype, f"seq {s} len {L}")

@@ -527,7 +527,7 @@ void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_a
                          (reinterpret_cast<uintptr_t>(out->data) % 8 == 0) &&
                          out->strides[0] % 4 == 0 && out->strides[1] % 4 == 0;
     if (kv->bits > 0 && !keys_only && aligned && kv->max_len <= qdecode_max_len() &&
-        !option(VKV_OPTION_GENERIC_ATTENTION) && !option(VKV_OPTION_REFERENCE_SOFTMAX) &&
+        !option(VKV_OPTION_GENERIC_ATTENTION) &&
         qdecode_supported(kv->dtype, kv->bits, kv->head_dim, kv->block_size, rep, kv->group_size)) {
       // matrix-core path (vkv_decode.hip)
       KVSrc src = kvsrc_from_view(*kv);
@@ -558,10 +558,15 @@ void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_a
       d.n_waves = want;  // 0 = choose per launch
       const int chunk = std::min(kv->n_seqs, qdecode_max_seqs());
       const int w_max = qdecode_waves(chunk, kv->n_kv_heads, rep, kv->max_len, want);
-      d.ws = workspace(S(stream),
-                       qdecode_workspace_floats(chunk, kv->n_kv_heads, rep, kv->head_dim, w_max),
-                       noalloc);
-      launch_qdecode(d, kv->bits, kv->head_dim, S(stream));
+      const size_t part_floats =
+          qdecode_workspace_floats(chunk, kv->n_kv_heads, rep, kv->head_dim, w_max);
+      const bool ref = option(VKV_OPTION_REFERENCE_SOFTMAX) != 0;
+      // the reference path's bf16 score rows follow the partials
+      d.sc_stride = (std::max<int64_t>(kv->max_len, 1) + 63) / 64 * 64;
+      const size_t sc_floats = ref ? static_cast<size_t>(chunk) * d.Hq * d.sc_stride / 2 : 0;
+      d.ws = workspace(S(stream), (part_floats + 63) / 64 * 64 + sc_floats, noalloc);
+      d.sc = ref ? reinterpret_cast<uint16_t*>(d.ws + (part_floats + 63) / 64 * 64) : nullptr;
+      launch_qdecode(d, kv->bits, kv->head_dim, S(stream), ref);
       return;
     }
     AttnArgs a{};

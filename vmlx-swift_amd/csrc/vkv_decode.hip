@@ -333,6 +333,7 @@ struct QD {
     uint32_t kw[TT][PP][RUN];    // key words of this lane's token, per tile
     uint32_t sb[TT][4][SBW];     // scale/bias of the 4 scored tokens, per tile
     uint32_t vw[2][VW];          // value words, per 32-token sub-block
+    uint32_t wt[TT][2];          // stored bf16 weights of the 4 tokens (weights mode)
   };
 };
 
@@ -342,10 +343,19 @@ struct QD {
 template <int D>
 constexpr int qd_waves() { return D >= 256 ? 1 : 8; }
 
+// Kernel modes: the fused single pass (scores, online fp32 softmax, P.V),
+// or the two matrix-core passes of the reference-arithmetic path: the
+// bf16 scores written to score rows (kModeScores), and, after the
+// reference softmax has turned them into bf16 weights in place, P.V from
+// the stored weights (kModeWeights: no key loads, no score MFMAs, no max;
+// the partials are plain sums, merged with max 0 and the pair's first
+// partial carrying sum 1).
+constexpr int kModeFused = 0, kModeScores = 1, kModeWeights = 2;
+
 // See the header comment for the work split.  Every wave works on its own
 // range with its own LDS tables; the waves of a workgroup only share their
 // SIMD placement and unit counters.
-template <int BITS, int D, int HP>
+template <int BITS, int D, int HP, int MODE>
 __global__ void __launch_bounds__(64 * qd_waves<D>())
 __attribute__((amdgpu_waves_per_eu((D >= 256) ? 1 : 2)))
 qdecode_kernel(DecodeArgs a) {
@@ -370,6 +380,11 @@ qdecode_kernel(DecodeArgs a) {
   __shared__ int32_t seg_tab_g[WPG][kMaxRange][7];
   __shared__ int32_t simd_of[WPG];  // SIMD of each wave of the workgroup
   __shared__ int32_t done_of[WPG];  // units each wave has started
+  // score / weight rows (score and weights modes): per unit, the element
+  // offset of its head group's first row at the unit's first token, and the
+  // group's live heads
+  __shared__ int64_t u_woff_g[MODE != kModeFused ? WPG : 1][MODE != kModeFused ? kMaxRange : 1];
+  __shared__ int32_t u_nh_g[MODE != kModeFused ? WPG : 1][MODE != kModeFused ? kMaxRange : 1];
   const int wv = WPG > 1 ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6) : 0;
   u32x4_t* qtab = qtab_g[wv];
   int64_t* sub_off = sub_off_g[wv];
@@ -437,7 +452,7 @@ qdecode_kernel(DecodeArgs a) {
   }
   max_nst = wave_max(max_nst);
   const int U = __builtin_amdgcn_readfirstlane(carry);
-  if (w == 0) {  // empty sequences: zero output
+  if (MODE != kModeScores && w == 0) {  // empty sequences: zero output
 #pragma unroll
     for (int r = 0; r < SR; r++) {
       uint64_t empty = __builtin_amdgcn_ballot_w64(64 * r + lane < ns && nst_r[r] == 0);
@@ -544,13 +559,22 @@ qdecode_kernel(DecodeArgs a) {
     load_q_sj(__builtin_amdgcn_readfirstlane(seg_tab[k][0]), __builtin_amdgcn_readfirstlane(seg_tab[k][1]), qr);
   };
   u32x4_t qpre[QPL];
-  load_q_sj(seq0, j0, qpre);
+  if constexpr (MODE != kModeWeights) load_q_sj(seq0, j0, qpre);
 #pragma unroll
   for (int r = 0; r < 2; r++) {
     const int e = lane + 64 * r;
     if (e < 2 * kMaxRange) {
       sub_off[e] = my_off[r];
       sub_t0[e] = my_t0[r];
+    }
+    if constexpr (MODE != kModeFused) {
+      if ((e & 1) == 0 && e < 2 * kMaxRange) {
+        const int j = sel_j[r];
+        const int64_t hq0 = static_cast<int64_t>(j / n_hg) * rep + (j % n_hg) * HP;
+        u_woff_g[wv][e >> 1] = (static_cast<int64_t>(sel_seq[r]) * a.Hq + hq0) * a.sc_stride +
+                               static_cast<int64_t>(sel_step[r]) * 64;
+        u_nh_g[wv][e >> 1] = min(HP, rep - (j % n_hg) * HP);
+      }
     }
   }
   // the zero entry of every query-table slice (lanes outside a column's part)
@@ -582,29 +606,61 @@ qdecode_kernel(DecodeArgs a) {
       bs[s] = cb + t0 * SBW * 4;
     }
   };
-  // key words and scales / biases of unit ui
+  // the first of a lane's 4 tokens within a step, per tile (its pairs are
+  // t, t + 1 and t + 4, t + 5 at 4 bits; t .. t + 3 at 8 bits)
+  int32_t w_tok[TT];
+#pragma unroll
+  for (int tau = 0; tau < TT; tau++) {
+    const int c = tau * PP + p;
+    w_tok[tau] = 32 * (c >> 1) + 8 * lg + tok_off<BITS>(c & 1, 0);
+  }
+  // this lane's score / weight row offset within its unit's head group (a
+  // head past the group's live heads reads the last live one)
+  auto w_row = [&](int nh_u) __attribute__((always_inline)) {
+    return static_cast<int64_t>(min(h, nh_u - 1)) * a.sc_stride;
+  };
+  // key words (stored weights in the weights mode) and scales / biases of unit ui
   auto load_k = [&](int ui, Buf& b) __attribute__((always_inline)) {
     const uint8_t* bc[2];
     const uint8_t* bs[2];
     step_bases(ui, bc, bs);
+    if constexpr (MODE == kModeWeights) {
+      const int64_t wo = u_woff_g[wv][ui] + w_row(u_nh_g[wv][ui]);
+#pragma unroll
+      for (int tau = 0; tau < TT; tau++) {
+        const uint16_t* wp = a.sc + wo + w_tok[tau];
+        if constexpr (BITS == 4) {
+          b.wt[tau][0] = *(g_u32_t*)wp;
+          b.wt[tau][1] = *(g_u32_t*)(wp + 4);
+        } else {
+          const u32x2_t x = *(g_u32x2_t*)wp;
+          b.wt[tau][0] = x[0];
+          b.wt[tau][1] = x[1];
+        }
+      }
+    }
 #pragma unroll
     for (int tau = 0; tau < TT; tau++) {
-      const uint8_t* row = (ks_sub[tau] ? bc[1] : bc[0]) + k_lane[tau];
+      if constexpr (MODE != kModeWeights) {
+        const uint8_t* row = (ks_sub[tau] ? bc[1] : bc[0]) + k_lane[tau];
 #pragma unroll
-      for (int rho = 0; rho < PP; rho++) load_words<RUN>(row + rho * SPW * RUN * 4, b.kw[tau][rho]);
+        for (int rho = 0; rho < PP; rho++) load_words<RUN>(row + rho * SPW * RUN * 4, b.kw[tau][rho]);
+      }
       const uint8_t* sbp = (ss_sub[tau] ? bs[1] : bs[0]) + sb_lane[tau];
 #pragma unroll
       for (int i = 0; i < 4; i++)
         load_words<SBW>(sbp + (tok_off<BITS>(0, i) - tok_off<BITS>(0, 0)) * SBW * 4, b.sb[tau][i]);
     }
   };
-  // value words of unit ui
+  // value words of unit ui (none in the score mode)
   auto load_v = [&](int ui, uint32_t (&vw)[2][VW]) __attribute__((always_inline)) {
-    const uint8_t* bc[2];
-    const uint8_t* bs[2];
-    step_bases(ui, bc, bs);
+    if constexpr (MODE != kModeScores) {
+      const uint8_t* bc[2];
+      const uint8_t* bs[2];
+      step_bases(ui, bc, bs);
 #pragma unroll
-    for (int s = 0; s < 2; s++) load_words<VW>(bc[s] + v_lane, vw[s]);
+      for (int s = 0; s < 2; s++) load_words<VW>(bc[s] + v_lane, vw[s]);
+    }
   };
   auto load_step = [&](int ui, Buf& b) __attribute__((always_inline)) {
     load_k(ui, b);
@@ -636,6 +692,7 @@ qdecode_kernel(DecodeArgs a) {
     seg_first = __builtin_amdgcn_readfirstlane(seg_tab[kk][5]);
     seg_pa = __builtin_amdgcn_readfirstlane(seg_tab[kk][6]);
     nh = min(HP, rep - (seg_j % n_hg) * HP);
+    if constexpr (MODE == kModeWeights) return;  // no queries: the weights are stored
     float part[QPL][G];
 #pragma unroll
     for (int c = 0; c < QPL; c++) {
@@ -684,7 +741,7 @@ qdecode_kernel(DecodeArgs a) {
   };
   setup_segment(0, qpre);
   // the next segment's queries load while this segment's units compute
-  load_q(min(1, nseg - 1), qpre);
+  if constexpr (MODE != kModeWeights) load_q(min(1, nseg - 1), qpre);
 
   f32x4_t oacc[NT];
 #pragma unroll
@@ -712,7 +769,7 @@ qdecode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int jj = 0; jj < kQA; jj++) qring[jj] = qlane[slice(jj) * QROW];
 #pragma unroll
-    for (int o = 0; o < SL; o++) {
+    for (int o = 0; o < (MODE == kModeWeights ? 0 : SL); o++) {
       const int sg = slice(o);
       const u32x4_t qb = qring[o % kQA];
       if (o + kQA < SL) qring[o % kQA] = qlane[slice(o + kQA) * QROW];
@@ -739,15 +796,23 @@ qdecode_kernel(DecodeArgs a) {
 #pragma unroll
         for (int g = 0; g < G; g++) {
           const uint32_t kwd = b.sb[tau][i][g], vwd = b.sb[tau][i][G + g];
-          const float ks = bf_lo(kwd);
-          s = fmaf(fmaf(-KMAG, ks, bf_hi(kwd)), sq[g], s);
-          s = fmaf(ks, acc[tau][g][i], s);
+          if constexpr (MODE != kModeWeights) {
+            const float ks = bf_lo(kwd);
+            s = fmaf(fmaf(-KMAG, ks, bf_hi(kwd)), sq[g], s);
+            s = fmaf(ks, acc[tau][g][i], s);
+          }
           vs[tau][i][g] = bf_lo(vwd);
           vb[tau][i][g] = bf_hi(vwd);
         }
-        // the reference stores the scores in the query dtype before the
-        // softmax (quantizedMM returns T, KVCache.swift:1945-1949)
-        sc[tau][i] = round_to<kBF16>(s);
+        if constexpr (MODE == kModeWeights) {
+          // the stored weight of token i: pairs (i0, i2) and (i1, i3) share a word
+          const uint32_t wd = b.wt[tau][i & 1];
+          sc[tau][i] = (i >> 1) ? bf_hi(wd) : bf_lo(wd);
+        } else {
+          // the reference stores the scores in the query dtype before the
+          // softmax (quantizedMM returns T, KVCache.swift:1945-1949)
+          sc[tau][i] = round_to<kBF16>(s);
+        }
       }
     if (stp * 64 + 64 > len) {  // the sequence ends inside this step
       asm volatile("");  // a real branch: keeps the masking off the common path
@@ -757,7 +822,7 @@ qdecode_kernel(DecodeArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const bool ok = stp * 64 + 32 * s + 8 * lg + tok_off<BITS>(q, i) < len;
-          sc[tau][i] = ok ? sc[tau][i] : -INFINITY;
+          sc[tau][i] = ok ? sc[tau][i] : (MODE == kModeWeights ? 0.0f : -INFINITY);
 #pragma unroll
           for (int g = 0; g < G; g++) {
             vs[tau][i][g] = ok ? vs[tau][i][g] : 0.0f;
@@ -767,6 +832,34 @@ qdecode_kernel(DecodeArgs a) {
       }
     }
 
+    if constexpr (MODE == kModeScores) {
+      // the bf16 scores of head h's row at this lane's 4 tokens (past the
+      // sequence -inf, inside the row's padding)
+      if (h < nh) {
+        uint16_t* row = a.sc + (static_cast<int64_t>(seg_seq) * a.Hq +
+                                static_cast<int64_t>(seg_j / n_hg) * rep + (seg_j % n_hg) * HP + h) *
+                                   a.sc_stride + stp * 64;
+#pragma unroll
+        for (int tau = 0; tau < TT; tau++) {
+          const uint32_t w0 = pack_bf16(sc[tau][0], sc[tau][2]);
+          const uint32_t w1 = pack_bf16(sc[tau][1], sc[tau][3]);
+          if constexpr (BITS == 4) {
+            *reinterpret_cast<uint32_t*>(row + w_tok[tau]) = w0;
+            *reinterpret_cast<uint32_t*>(row + w_tok[tau] + 4) = w1;
+          } else {
+            *reinterpret_cast<u32x2_t*>(row + w_tok[tau]) = u32x2_t{w0, w1};
+          }
+        }
+      }
+      return;
+    }
+    float pr[TT][4];
+    if constexpr (MODE == kModeWeights) {
+#pragma unroll
+      for (int tau = 0; tau < TT; tau++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) pr[tau][i] = sc[tau][i];
+    } else {
     // ---- online softmax with a lazily refreshed max
     float mx = -INFINITY;
 #pragma unroll
@@ -791,7 +884,6 @@ qdecode_kernel(DecodeArgs a) {
       for (int t = 0; t < NT; t++) scale_inplace(oacc[t], alpha);
     }
     const float m2 = fmaxf(m_run * kLog2e, -3.402823466e38f);
-    float pr[TT][4];
 #pragma unroll
     for (int tau = 0; tau < TT; tau++)
 #pragma unroll
@@ -799,6 +891,7 @@ qdecode_kernel(DecodeArgs a) {
         pr[tau][i] = fast_exp2(fmaf(sc[tau][i], kLog2e, -m2));
         l_run += pr[tau][i];
       }
+    }
 
     // ---- P = p * s_v as bf16 hi + lo pairs, in value-operand register order
     uint32_t pk[TT][2][G][2];  // [tile][pair][group][hi, lo]
@@ -860,6 +953,7 @@ qdecode_kernel(DecodeArgs a) {
 
   // ---- end of a segment: the output itself, or this wave's partial
   auto finalize = [&]() __attribute__((always_inline)) {
+    if constexpr (MODE == kModeScores) return;  // the scores are written per step
     float lsum = l_run, csum[G];
 #pragma unroll
     for (int g = 0; g < G; g++) csum[g] = corr[g];
@@ -890,7 +984,8 @@ qdecode_kernel(DecodeArgs a) {
     const int64_t hq0 = static_cast<int64_t>(seg_j / n_hg) * rep + (seg_j % n_hg) * HP;
     if (n < nh) {
       if (whole) {
-        const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+        // (the stored weights are final: no normalisation)
+        const float inv = MODE == kModeWeights ? 1.0f : lsum > 0.0f ? 1.0f / lsum : 0.0f;
         uint16_t* o = a.out + seg_seq * a.o_ss + (hq0 + n) * a.o_sh + 4 * lg;
 #pragma unroll
         for (int t = 0; t < NT; t++) {
@@ -910,14 +1005,23 @@ qdecode_kernel(DecodeArgs a) {
               f32x4_t{oacc[t][0] + cg, oacc[t][1] + cg, oacc[t][2] + cg, oacc[t][3] + cg};
         }
         if (lg == 0) {
-          a.ws_ml[(slot * HP + n) * 2] = m_run;
-          a.ws_ml[(slot * HP + n) * 2 + 1] = lsum;
+          // weights mode: plain sums, merged with max 0 and the pair's
+          // first partial carrying the sum 1
+          a.ws_ml[(slot * HP + n) * 2] = MODE == kModeWeights ? 0.0f : m_run;
+          a.ws_ml[(slot * HP + n) * 2 + 1] = MODE == kModeWeights ? (w == wa ? 1.0f : 0.0f) : lsum;
         }
       }
     }
     // the next segment's first step refreshes the max from -inf, which
-    // scales the accumulators, l_run and corr by zero
+    // scales the accumulators, l_run and corr by zero; the weights mode has
+    // no max, so it clears them here
     m_run = -INFINITY;
+    if constexpr (MODE == kModeWeights) {
+#pragma unroll
+      for (int t = 0; t < NT; t++) oacc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int g = 0; g < G; g++) corr[g] = 0.0f;
+    }
   };
 
   // ---- the range: unit ui computes while unit ui + 1 loads, and the next
@@ -948,7 +1052,7 @@ qdecode_kernel(DecodeArgs a) {
       if (k + 1 < nseg) {
         k++;
         setup_segment(k, qpre);
-        load_q(min(k + 1, nseg - 1), qpre);
+        if constexpr (MODE != kModeWeights) load_q(min(k + 1, nseg - 1), qpre);
       }
     }
   };
@@ -975,7 +1079,7 @@ qdecode_kernel(DecodeArgs a) {
         if (k + 1 < nseg) {
           k++;
           setup_segment(k, qpre);
-          load_q(min(k + 1, nseg - 1), qpre);
+          if constexpr (MODE != kModeWeights) load_q(min(k + 1, nseg - 1), qpre);
         }
       }
     };
@@ -993,7 +1097,7 @@ qdecode_kernel(DecodeArgs a) {
         if (ui + 1 == nunits) break;
         k++;
         setup_segment(k, qpre);
-        load_q(min(k + 1, nseg - 1), qpre);
+        if constexpr (MODE != kModeWeights) load_q(min(k + 1, nseg - 1), qpre);
       }
       load_step(ui + 1, bufA);
     }
@@ -1168,34 +1272,46 @@ float* decode_scratch(size_t floats) {
 // units with at most kMaxParts partials per pair.
 int qdecode_max_len() { return kMaxRange * (kMaxParts - 1) * 64; }
 
-template <int BITS, int D>
-static void launch_d(const DecodeArgs& a, hipStream_t st) {
+template <int BITS, int D, int HP>
+static void launch_hp(const DecodeArgs& a, bool ref, hipStream_t st) {
   constexpr int wpg = qd_waves<D>();
   const dim3 grid((a.n_waves + wpg - 1) / wpg), block(64 * wpg);
   const int pairs = a.n_seqs * a.Hkv * qdecode_head_groups(a.rep);
   const bool rest = a.n_waves > 4 * pairs;  // more than kFirst partials per pair on average
-  const TimedLaunch tl = timing_prepare(kTimeDecode);
-  if (heads_per_part(a.rep) == 4) {
-    hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, 4>), grid, block, 0, st, tl.start, tl.stop, 0, a);
+  if (ref) {
+    // the reference-arithmetic path: bf16 score rows, the reference softmax
+    // over them in place, then P.V from the stored weights
+    hipLaunchKernelGGL((qdecode_kernel<BITS, D, HP, kModeScores>), grid, block, 0, st, a);
+    VKV_HIP(hipGetLastError());
+    launch_ref_softmax_bf16(a.sc, static_cast<int64_t>(a.n_seqs) * a.Hq, a.sc_stride, a.seq_lens,
+                            a.max_len, a.Hq, st);
+    const TimedLaunch tl = timing_prepare(kTimeDecode);
+    hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, HP, kModeWeights>), grid, block, 0, st, tl.start,
+                          tl.stop, 0, a);
     VKV_HIP(hipGetLastError());
     timing_commit(tl);
-    if (rest)
-      hipLaunchKernelGGL((qdecode_combine_kernel<4, true>), dim3(pairs), dim3(D), 0, st, a, D);
-    else
-      hipLaunchKernelGGL((qdecode_combine_kernel<4, false>), dim3(pairs), dim3(D), 0, st, a, D);
   } else {
-    hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, 8>), grid, block, 0, st, tl.start, tl.stop, 0, a);
+    const TimedLaunch tl = timing_prepare(kTimeDecode);
+    hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, HP, kModeFused>), grid, block, 0, st, tl.start,
+                          tl.stop, 0, a);
     VKV_HIP(hipGetLastError());
     timing_commit(tl);
-    if (rest)
-      hipLaunchKernelGGL((qdecode_combine_kernel<8, true>), dim3(pairs), dim3(2 * D), 0, st, a, D);
-    else
-      hipLaunchKernelGGL((qdecode_combine_kernel<8, false>), dim3(pairs), dim3(2 * D), 0, st, a, D);
   }
+  const dim3 cb(HP == 4 ? D : 2 * D);
+  if (rest)
+    hipLaunchKernelGGL((qdecode_combine_kernel<HP, true>), dim3(pairs), cb, 0, st, a, D);
+  else
+    hipLaunchKernelGGL((qdecode_combine_kernel<HP, false>), dim3(pairs), cb, 0, st, a, D);
   VKV_HIP(hipGetLastError());
 }
 
-void launch_qdecode(const DecodeArgs& a0, int bits, int D, hipStream_t st) {
+template <int BITS, int D>
+static void launch_d(const DecodeArgs& a, bool ref, hipStream_t st) {
+  if (heads_per_part(a.rep) == 4) launch_hp<BITS, D, 4>(a, ref, st);
+  else launch_hp<BITS, D, 8>(a, ref, st);
+}
+
+void launch_qdecode(const DecodeArgs& a0, int bits, int D, hipStream_t st, bool ref) {
   // at most kMaxSeqs sequences per launch
   for (int s0 = 0; s0 < a0.n_seqs; s0 += kMaxSeqs) {
     DecodeArgs a = a0;
@@ -1210,13 +1326,13 @@ void launch_qdecode(const DecodeArgs& a0, int bits, int D, hipStream_t st) {
     a.table += static_cast<int64_t>(s0) * a0.table_stride;
     if (a.seq_lens) a.seq_lens += s0;
     if (bits == 4) {
-      if (D == 64) launch_d<4, 64>(a, st);
-      else if (D == 128) launch_d<4, 128>(a, st);
-      else launch_d<4, 256>(a, st);
+      if (D == 64) launch_d<4, 64>(a, ref, st);
+      else if (D == 128) launch_d<4, 128>(a, ref, st);
+      else launch_d<4, 256>(a, ref, st);
     } else {
-      if (D == 64) launch_d<8, 64>(a, st);
-      else if (D == 128) launch_d<8, 128>(a, st);
-      else launch_d<8, 256>(a, st);
+      if (D == 64) launch_d<8, 64>(a, ref, st);
+      else if (D == 128) launch_d<8, 128>(a, ref, st);
+      else launch_d<8, 256>(a, ref, st);
     }
   }
 }

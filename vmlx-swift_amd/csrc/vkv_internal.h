@@ -215,6 +215,8 @@ struct DecodeArgs {
   float* ws_ml;              //                 partial (max, sum) [slot][head][2]
   int32_t ws_hdr;            //   then (as int32 at ws_ml + ws_hdr) the number
                              //   of partials of each (sequence, head pair)
+  uint16_t* sc;              // reference path: bf16 score / weight rows
+  int64_t sc_stride;         //   [n_seqs][Hq][sc_stride], sc_stride >= max_len, % 64 == 0
 };
 bool qdecode_supported(int dtype, int bits, int D, int block_size, int rep, int group);
 // (sequence, kv head) pairs are split into head groups of 4 or 8 query heads
@@ -226,7 +228,9 @@ int qdecode_max_len();
 // decode waves for a launch of n_seqs sequences (want > 0 overrides)
 int qdecode_waves(int n_seqs, int Hkv, int rep, int max_len, int want);
 size_t qdecode_workspace_floats(int n_seqs, int Hkv, int rep, int D, int n_waves);
-void launch_qdecode(const DecodeArgs& a, int bits, int D, hipStream_t st);
+// ref: the reference-arithmetic path (score rows, the reference softmax,
+// P.V from the stored weights) in place of the fused single pass
+void launch_qdecode(const DecodeArgs& a, int bits, int D, hipStream_t st, bool ref = false);
 // Scratch of the no-allocation decode entry point: a fixed device array in
 // vkv_decode.hip, of decode_scratch_bytes() bytes per device.  Returns its
 // device address on the current device (resolved once per device), or
