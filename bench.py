@@ -362,13 +362,15 @@ def _outlier_scale(torch, B, H, D, gen):
     return m
 
 
-def config2_measure(torch, vkv, steps, warmup, bits):
+def config2_measure(torch, vkv, steps, warmup, bits, ref=0):
     """Config 2: QuantizedKVCache at Llama-3-8B layer shapes -- 32 layers,
     batch 8, 8 KV / 32 query heads x 128, a 4096-token context, bf16 K/V
     ~ N(0,1) with 4 channels per head x20, affine g64 at `bits`.  One step =
     for each layer, updateQuantized of one token and quantized decode
     attention through attentionWithCacheUpdate; each cache is trimmed back by
-    the token after the step."""
+    the token after the step.  ref = 1: with the reference_softmax option
+    (the reference's bf16 softmax in a pass of its own; the roofline then
+    times the P.V pass)."""
     layers, B, H, Hq, D, T0 = 32, 8, 8, 32, 128, 4096
     gen = torch.Generator(device="cuda")
     gen.manual_seed(200 + bits)
@@ -393,14 +395,19 @@ def config2_measure(torch, vkv, steps, warmup, bits):
         for c in caches:
             c.trim(1)
 
-    ms, k_ms, k_n = _time_calls(torch, vkv, step, steps, warmup, vkv.TIME_DECODE)
+    vkv.set_option("reference_softmax", ref)
+    try:
+        ms, k_ms, k_n = _time_calls(torch, vkv, step, steps, warmup, vkv.TIME_DECODE)
+    finally:
+        vkv.set_option("reference_softmax", 0)
     per_tok = 2 * (D * bits // 8 + (D // 64) * 4)          # K + V codes + scale/bias
     layer_bytes = B * H * (T0 + 1) * per_tok
     finite = bool(torch.isfinite(out.float()).all())
     del caches
     return {
         "workload": f"QuantizedKVCache {bits}-bit g64, 32 layers, B8, 8/32 heads x 128, "
-                    f"context 4096 (+1 decode token), x20 outlier channels",
+                    f"context 4096 (+1 decode token), x20 outlier channels"
+                    + (", reference softmax" if ref else ""),
         "ms_per_step": round(ms, 4),
         "step_kv_gbs": round(layers * layer_bytes / (ms * 1e-3) / 1e9, 1),
         "roofline": _roofline(layer_bytes, k_ms, "qdecode_kernel"),
@@ -597,8 +604,9 @@ def main():
         return
     legs = {
         "config1": lambda: config1_measure(torch, vkv, args.steps, args.warmup),
-        "config2": lambda: {f"bits{b}": config2_measure(torch, vkv, args.steps, args.warmup, b)
-                            for b in (4, 8)},
+        "config2": lambda: {f"bits{b}{sfx}": config2_measure(torch, vkv, args.steps, args.warmup,
+                                                             b, ref)
+                            for b in (4, 8) for ref, sfx in ((0, ""), (1, "_reference_softmax"))},
         "config4": lambda: config4_measure(torch, vkv, args.steps, args.warmup),
         "mla": lambda: mla_measure(torch, vkv, args.steps, args.warmup),
         "prefill": lambda: prefill_measure(torch, vkv, args.steps, args.warmup),
@@ -657,6 +665,21 @@ def main():
     torch.cuda.synchronize()
     if not bool(torch.isfinite(sc["out"].float()).all()):
         raise RuntimeError("the decode attention output holds non-finite values")
+    # the attention calls alone with the reference softmax (score pass,
+    # softmax pass, P.V pass, merge), for its cost against the fused call
+    def att_only():
+        for l in range(layers):
+            vkv._chk(vkv.lib().vkv_paged_sdpa(
+                vkv.C.byref(vkv.arr(sc["q"][l])), vkv.C.byref(sc["views"][l]), vkv.C.c_float(scale),
+                vkv.C.byref(vkv.arr(sc["out"][l])), vkv.stream_ptr()))
+    att_fused_ms, _, _ = _time_calls(torch, vkv, att_only, args.steps, args.warmup)
+    vkv.set_option("reference_softmax", 1)
+    try:
+        att_ref_ms, _, _ = _time_calls(torch, vkv, att_only, args.steps, args.warmup)
+    finally:
+        vkv.set_option("reference_softmax", 0)
+    att_fused_ms /= layers
+    att_ref_ms /= layers
     n_att = args.steps * layers
     att_avg_ms = att_ms / n_att
     app_avg_ms = app_ms / n_att
@@ -707,7 +730,16 @@ def main():
         "attention": {"ms_per_layer": round(att_avg_ms, 5), "gbs_logical": round(att_gbs, 1),
                       "gbs_unique": round(unique / (att_avg_ms * 1e-3) / 1e9, 1),
                       "pct_hbm_peak": round(100 * att_gbs / HBM_PEAK_GBS, 2),
-                      "decode_kernel_ms": round(dec_avg_ms, 5)},
+                      "decode_kernel_ms": round(dec_avg_ms, 5),
+                      "calls_back_to_back_ms_per_layer": round(att_fused_ms, 5),
+                      "pct_hbm_peak_back_to_back": round(
+                          100 * logical / (att_fused_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)},
+        "attention_reference_softmax": {
+            "ms_per_layer": round(att_ref_ms, 5),
+            "gbs_logical": round(logical / (att_ref_ms * 1e-3) / 1e9, 1),
+            "pct_hbm_peak": round(100 * logical / (att_ref_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+            "note": "reference_softmax option: bf16 score rows, the reference's AccT = bf16 "
+                    "softmax pass, P.V from the stored weights (calls back to back)"},
         "append": {"tokens_per_layer_step": append_tokens,
                    "ms_per_layer": round(app_avg_ms, 5),
                    "tokens_per_s": round(append_tokens / (app_avg_ms * 1e-3), 1)},

@@ -157,50 +157,79 @@ __global__ void __launch_bounds__(256) ref_scores_kernel(RefArgs r) {
   }
 }
 
-// ---- pass 2: the reference softmax of one row (workgroup of 1024
-// threads), in place over the stored scores.  acc_dt: the AccT dtype, or -1
-// for the fp32 arithmetic of an f32-promoted row; w_dt: the weights' dtype.
+// ---- pass 2: the reference softmax of one row, in place over the stored
+// scores.  A workgroup of 256 threads plays the reference's 1024: thread
+// lid is threads lid + 256 k (k = 0..3), so the reference's grouping (4
+// keys per thread, simd groups of 32 threads) is kept; each simd group's
+// 32 threads are one half-wave of ours.  acc_dt: the AccT dtype, or -1 for
+// the fp32 arithmetic of an f32-promoted row; w_dt: the weights' dtype.
+// The fp64 sums of dtype-rounded terms are exact, so their order (here a
+// half-wave butterfly) does not change them.
+constexpr int kSmThreads = 256;
+constexpr int kSmVirtual = kSoftmaxThreads / kSmThreads;  // reference threads per thread
+
+// exp of a dtype value x, rounded as rnd_d rounds it (fp64 exp, to float,
+// to the dtype).  For bf16 the f32 exp decides it unless its result sits
+// within 16 float ulps of a bf16 rounding midpoint (or is tiny), where the
+// fp64 exp does.
+__device__ __forceinline__ double t_exp_fast(double x, int dt) {
+  if (dt == kBF16) {
+    const float e = expf(static_cast<float>(x));
+    const uint32_t lo = __float_as_uint(e) & 0xFFFFu;
+    if (e >= 1.0e-37f && (lo + 16u < 0x8000u || lo > 0x8000u + 16u))
+      return static_cast<double>(round_to<kBF16>(e));
+  }
+  return t_exp(x, dt);
+}
+
+__device__ __forceinline__ double half_sum(double x) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) x += __shfl_xor(x, o, 32);
+  return x;
+}
+__device__ __forceinline__ double half_max(double x) {
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) x = fmax(x, __shfl_xor(x, o, 32));
+  return x;
+}
+
 template <typename S>
-__global__ void __launch_bounds__(kSoftmaxThreads) ref_softmax_kernel(S* sc, int64_t tpad,
-                                                                      const int32_t* seq_lens,
-                                                                      int32_t T_all, int64_t per_b,
-                                                                      int acc_dt, int w_dt) {
+__global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t tpad,
+                                                                 const int32_t* seq_lens,
+                                                                 int32_t T_all, int64_t per_b,
+                                                                 int acc_dt, int w_dt) {
   using St = Store<S>;
-  __shared__ double red[kSoftmaxThreads];
-  __shared__ double red_m[kSoftmaxThreads];
+  __shared__ double red[kSmThreads / 64];
   __shared__ double simd_s[kSoftmaxThreads / 32], simd_m[kSoftmaxThreads / 32];
   __shared__ double bcast[2];
   const int64_t row = blockIdx.x;
   const int64_t T = seq_lens ? seq_lens[row / per_b] : T_all;
   if (T <= 0) return;
   S* p = sc + row * tpad;
-  const int lid = threadIdx.x;
+  const int lid = threadIdx.x, lane = lid & 63, wv = lid >> 6;
 
   // row max (of stored values: exact in any order)
   double mx = -INFINITY;
-  for (int64_t t = lid; t < T; t += kSoftmaxThreads) mx = fmax(mx, St::get(p, t));
-  red_m[lid] = mx;
+  for (int64_t t = lid; t < T; t += kSmThreads) mx = fmax(mx, St::get(p, t));
+  mx = half_max(mx);
+  mx = fmax(mx, __shfl_xor(mx, 32));
+  if (lane == 0) red[wv] = mx;
   __syncthreads();
-  for (int o = kSoftmaxThreads / 2; o > 0; o >>= 1) {
-    if (lid < o) red_m[lid] = fmax(red_m[lid], red_m[lid + o]);
-    __syncthreads();
-  }
-  mx = red_m[0];
+  mx = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
   __syncthreads();
 
   if (acc_dt < 0) {
     // fp32 arithmetic: exp of the f32 difference, summed, one reciprocal
     double sum = 0.0;
-    for (int64_t t = lid; t < T; t += kSoftmaxThreads)
+    for (int64_t t = lid; t < T; t += kSmThreads)
       sum += static_cast<double>(static_cast<float>(exp(static_cast<double>(static_cast<float>(St::get(p, t) - mx)))));
-    red[lid] = sum;
+    sum = half_sum(sum);
+    sum += __shfl_xor(sum, 32);
+    if (lane == 0) red[wv] = sum;
     __syncthreads();
-    for (int o = kSoftmaxThreads / 2; o > 0; o >>= 1) {
-      if (lid < o) red[lid] += red[lid + o];
-      __syncthreads();
-    }
-    const float rr = static_cast<float>(1.0 / static_cast<double>(static_cast<float>(red[0])));
-    for (int64_t t = lid; t < T; t += kSoftmaxThreads) {
+    const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float rr = static_cast<float>(1.0 / static_cast<double>(static_cast<float>(tot)));
+    for (int64_t t = lid; t < T; t += kSmThreads) {
       const float e = static_cast<float>(exp(static_cast<double>(static_cast<float>(St::get(p, t) - mx))));
       St::put(p, t, rnd_d(static_cast<double>(e * rr), w_dt));
     }
@@ -208,82 +237,83 @@ __global__ void __launch_bounds__(kSoftmaxThreads) ref_softmax_kernel(S* sc, int
   }
   const int dt = acc_dt;
   if (T <= kSoftmaxLoopedLimit) {
-    // softmax_single_row: thread lid owns keys 4 lid .. 4 lid + 3
-    double e[kSoftmaxReads];
-    double thr = 0.0;
+    // softmax_single_row: reference thread v = lid + 256 k owns keys 4v .. 4v + 3
+    double e[kSmVirtual][kSoftmaxReads];
 #pragma unroll
-    for (int i = 0; i < kSoftmaxReads; i++) {
-      const int64_t t = static_cast<int64_t>(kSoftmaxReads) * lid + i;
-      e[i] = t < T ? t_exp(rnd_d(St::get(p, t) - mx, dt), dt) : 0.0;
-      if (t < T) thr = rnd_d(thr + e[i], dt);
+    for (int k = 0; k < kSmVirtual; k++) {
+      double thr = 0.0;
+#pragma unroll
+      for (int i = 0; i < kSoftmaxReads; i++) {
+        const int64_t t = static_cast<int64_t>(kSoftmaxReads) * (lid + kSmThreads * k) + i;
+        e[k][i] = t < T ? t_exp_fast(rnd_d(St::get(p, t) - mx, dt), dt) : 0.0;
+        if (t < T) thr = rnd_d(thr + e[k][i], dt);
+      }
+      // simd group (lid + 256 k) / 32: this half-wave
+      const double sg = half_sum(thr);
+      if ((lid & 31) == 0) simd_s[(lid >> 5) + (kSmThreads / 32) * k] = rnd_d(sg, dt);
     }
-    red[lid] = thr;
     __syncthreads();
-    const int nsimd = static_cast<int>((T + 127) / 128);
-    if (lid < nsimd) {  // the simd sum of threads 32 lid .. 32 lid + 31, in their order
-      double s = 0.0;
-      for (int k = 0; k < 32; k++) s += red[32 * lid + k];
-      simd_s[lid] = rnd_d(s, dt);
-    }
-    __syncthreads();
-    if (lid == 0) {
-      double total = 0.0;
-      for (int g = 0; g < nsimd; g++) total += simd_s[g];
-      bcast[0] = rnd_d(1.0 / rnd_d(total, dt), dt);
+    if (wv == 0) {
+      const int nsimd = static_cast<int>((T + 127) / 128);
+      double tot = lane < 32 && lane < nsimd ? simd_s[lane] : 0.0;
+      tot = half_sum(tot);
+      if (lane == 0) bcast[0] = rnd_d(1.0 / rnd_d(tot, dt), dt);
     }
     __syncthreads();
     const double rr = bcast[0];
 #pragma unroll
-    for (int i = 0; i < kSoftmaxReads; i++) {
-      const int64_t t = static_cast<int64_t>(kSoftmaxReads) * lid + i;
-      if (t < T) St::put(p, t, rnd_d(e[i] * rr, dt));
-    }
+    for (int k = 0; k < kSmVirtual; k++)
+#pragma unroll
+      for (int i = 0; i < kSoftmaxReads; i++) {
+        const int64_t t = static_cast<int64_t>(kSoftmaxReads) * (lid + kSmThreads * k) + i;
+        if (t < T) St::put(p, t, rnd_d(e[k][i] * rr, dt));
+      }
     return;
   }
-  // softmax_looped: each thread a running (max, sum) over keys
-  // lid * 4 + 4096 r + i, rescaled at every round
+  // softmax_looped: reference thread v keeps a running (max, sum) over keys
+  // 4v + 4096 r + i, rescaled at every round
   const double fmin = -type_max_d(dt);
   const int64_t stride = static_cast<int64_t>(kSoftmaxReads) * kSoftmaxThreads;
   const int64_t rounds = (T + stride - 1) / stride;
-  double m = fmin, n = 0.0;
-  for (int64_t rd = 0; rd < rounds; rd++) {
-    const int64_t off = rd * stride + static_cast<int64_t>(lid) * kSoftmaxReads;
-    double v[kSoftmaxReads];
-    const double prev = m;
 #pragma unroll
-    for (int i = 0; i < kSoftmaxReads; i++) {
-      v[i] = off + i < T ? St::get(p, off + i) : -INFINITY;
-      m = v[i] > m ? v[i] : m;
+  for (int k = 0; k < kSmVirtual; k++) {
+    double m = fmin, n = 0.0;
+    for (int64_t rd = 0; rd < rounds; rd++) {
+      const int64_t off = rd * stride + static_cast<int64_t>(lid + kSmThreads * k) * kSoftmaxReads;
+      double v[kSoftmaxReads];
+      const double prev = m;
+#pragma unroll
+      for (int i = 0; i < kSoftmaxReads; i++) {
+        v[i] = off + i < T ? St::get(p, off + i) : -INFINITY;
+        m = v[i] > m ? v[i] : m;
+      }
+      n = rnd_d(n * t_exp_fast(rnd_d(prev - m, dt), dt), dt);
+#pragma unroll
+      for (int i = 0; i < kSoftmaxReads; i++) n = rnd_d(n + t_exp_fast(rnd_d(v[i] - m, dt), dt), dt);
     }
-    n = rnd_d(n * t_exp(rnd_d(prev - m, dt), dt), dt);
-#pragma unroll
-    for (int i = 0; i < kSoftmaxReads; i++) n = rnd_d(n + t_exp(rnd_d(v[i] - m, dt), dt), dt);
-  }
-  red_m[lid] = m;
-  red[lid] = n;
-  __syncthreads();
-  if (lid < kSoftmaxThreads / 32) {  // simdgroup lid: max, then the rescaled sums in order
-    double mg = fmin, acc = 0.0;
-    for (int k = 0; k < 32; k++) mg = red_m[32 * lid + k] > mg ? red_m[32 * lid + k] : mg;
-    for (int k = 0; k < 32; k++)
-      acc += rnd_d(red[32 * lid + k] * t_exp(rnd_d(red_m[32 * lid + k] - mg, dt), dt), dt);
-    simd_m[lid] = mg;
-    simd_s[lid] = rnd_d(acc, dt);
+    // simd group (lid + 256 k) / 32: its max, then the rescaled sums
+    const double mg = half_max(m);
+    const double acc = half_sum(rnd_d(n * t_exp_fast(rnd_d(m - mg, dt), dt), dt));
+    if ((lid & 31) == 0) {
+      simd_m[(lid >> 5) + (kSmThreads / 32) * k] = mg;
+      simd_s[(lid >> 5) + (kSmThreads / 32) * k] = rnd_d(acc, dt);
+    }
   }
   __syncthreads();
-  if (lid == 0) {
-    double gmax = fmin;
-    for (int g = 0; g < kSoftmaxThreads / 32; g++) gmax = simd_m[g] > gmax ? simd_m[g] : gmax;
-    double total = 0.0;
-    for (int g = 0; g < kSoftmaxThreads / 32; g++)
-      total += rnd_d(simd_s[g] * t_exp(rnd_d(simd_m[g] - gmax, dt), dt), dt);
-    bcast[0] = gmax;
-    bcast[1] = rnd_d(1.0 / rnd_d(total, dt), dt);
+  if (wv == 0) {
+    const double sm = lane < 32 ? simd_m[lane] : fmin;
+    const double gmax = half_max(sm);
+    double tot = lane < 32 ? rnd_d(simd_s[lane] * t_exp_fast(rnd_d(sm - gmax, dt), dt), dt) : 0.0;
+    tot = half_sum(tot);
+    if (lane == 0) {
+      bcast[0] = gmax;
+      bcast[1] = rnd_d(1.0 / rnd_d(tot, dt), dt);
+    }
   }
   __syncthreads();
   const double gmax = bcast[0], rr = bcast[1];
-  for (int64_t t = lid; t < T; t += kSoftmaxThreads)
-    St::put(p, t, rnd_d(t_exp(rnd_d(St::get(p, t) - gmax, dt), dt) * rr, dt));
+  for (int64_t t = lid; t < T; t += kSmThreads)
+    St::put(p, t, rnd_d(t_exp_fast(rnd_d(St::get(p, t) - gmax, dt), dt) * rr, dt));
 }
 
 // ---- pass 3: out = sum_t w_t dequant(v_t).  Workgroup = (token part, kv
@@ -412,7 +442,7 @@ static void ref_launch_dt(const RefArgs& r, int64_t B, hipStream_t st) {
   const int acc_dt = r.score_f32 ? -1 : DT;
   const int w_dt = r.score_f32 ? kF32 : DT;
   hipLaunchKernelGGL((ref_softmax_kernel<float>), dim3(static_cast<unsigned>(B * a.Hq * r.nl)),
-                     dim3(kSoftmaxThreads), 0, st, r.sc, r.tpad, a.kv.seq_lens, a.kv.T,
+                     dim3(kSmThreads), 0, st, r.sc, r.tpad, a.kv.seq_lens, a.kv.T,
                      static_cast<int64_t>(a.Hq) * r.nl, acc_dt, w_dt);
   VKV_HIP(hipGetLastError());
   const int nrb = (nrows + kRefRows - 1) / kRefRows;
@@ -452,7 +482,7 @@ void launch_ref_softmax_bf16(uint16_t* sc, int64_t rows, int64_t tpad, const int
                              int32_t T, int64_t per_b, hipStream_t st) {
   if (rows <= 0) return;
   hipLaunchKernelGGL((ref_softmax_kernel<uint16_t>), dim3(static_cast<unsigned>(rows)),
-                     dim3(kSoftmaxThreads), 0, st, sc, tpad, seq_lens, T, per_b, kBF16, kBF16);
+                     dim3(kSmThreads), 0, st, sc, tpad, seq_lens, T, per_b, kBF16, kBF16);
   VKV_HIP(hipGetLastError());
 }
 
