@@ -526,8 +526,11 @@ void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_a
                          q->strides[0] % 8 == 0 && q->strides[1] % 8 == 0 &&
                          (reinterpret_cast<uintptr_t>(out->data) % 8 == 0) &&
                          out->strides[0] % 4 == 0 && out->strides[1] % 4 == 0;
+    // (the matrix-core reference path stores bf16 score rows: an f16 cache
+    // with the reference softmax takes the generic reference path)
     if (kv->bits > 0 && !keys_only && aligned && kv->max_len <= qdecode_max_len() &&
         !option(VKV_OPTION_GENERIC_ATTENTION) &&
+        !(option(VKV_OPTION_REFERENCE_SOFTMAX) && kv->dtype != VKV_BF16) &&
         qdecode_supported(kv->dtype, kv->bits, kv->head_dim, kv->block_size, rep, kv->group_size)) {
       // matrix-core path (vkv_decode.hip)
       KVSrc src = kvsrc_from_view(*kv);
@@ -557,10 +560,10 @@ void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_a
       const int want = static_cast<int>(option(VKV_OPTION_DECODE_WAVES));
       d.n_waves = want;  // 0 = choose per launch
       const int chunk = std::min(kv->n_seqs, qdecode_max_seqs());
-      const int w_max = qdecode_waves(chunk, kv->n_kv_heads, rep, kv->max_len, want);
       const size_t part_floats =
-          qdecode_workspace_floats(chunk, kv->n_kv_heads, rep, kv->head_dim, w_max);
+          qdecode_workspace_floats(chunk, kv->n_kv_heads, rep, kv->head_dim, kv->max_len);
       const bool ref = option(VKV_OPTION_REFERENCE_SOFTMAX) != 0;
+      d.dtype = kv->dtype;
       // the reference path's bf16 score rows follow the partials
       d.sc_stride = (std::max<int64_t>(kv->max_len, 1) + 63) / 64 * 64;
       const size_t sc_floats = ref ? static_cast<size_t>(chunk) * d.Hq * d.sc_stride / 2 : 0;

@@ -76,6 +76,8 @@ namespace vkv {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -95,7 +97,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 constexpr int kMaxRange = 64;   // units (64-token steps) per wave, at most
 constexpr int kMaxSeqs = 256;   // sequences per launch (the host splits larger batches)
-constexpr int kMaxParts = 32;   // partials per (sequence, head pair), at most
+constexpr int kMaxParts = 32;   // partials per (sequence, head pair), at most, up to
+                                // kMaxRange * (kMaxParts - 1) * 64 tokens; longer
+                                // sequences raise the launch's limit (max_parts)
 // Work-split cost of a (sequence, head pair) beyond its 64-token steps: the
 // finalize and set-up at a segment boundary take about as long as a step
 // (0.7 steps measured at 128 dims, 4 bits), so the ranges count each pair
@@ -116,6 +120,17 @@ __device__ __forceinline__ void sfor(F&& f) {
 __device__ __forceinline__ f32x4_t mfma(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+// The score contraction in the cache's dtype: bf16 operands, or f16 ones for
+// an f16 cache (its queries keep their 11 bits).  The value contraction is
+// bf16 for both.
+template <int DT>
+__device__ __forceinline__ f32x4_t mfma_qk(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+  if constexpr (DT == kF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  else
+    return mfma(a, b, c);
 }
 
 // The bf16 exponent patterns OR-ed onto the codes, held in VGPRs the
@@ -169,6 +184,31 @@ __device__ __forceinline__ void byte_magic(uint32_t x, uint32_t y, const Magic& 
   hi[1] = ((x >> 12) & 0x000F000Fu) | mg.m2048;
   hi[2] = ((y >> 4) & 0x000F000Fu) | mg.m2048;
   hi[3] = ((y >> 12) & 0x000F000Fu) | mg.m2048;
+}
+
+// f16 key operands (an f16 cache): 8 nibbles -> f16 (16 + nibble), whose
+// mantissa unit is 1/64 (the nibble six bits up), KMAG = 16; 8 bytes ->
+// f16 (256 + byte), unit 1/4, KMAG = 256, one operand per 8 dims (bytes
+// (b0, b2), (b1, b3) of x, then of y, the order of byte_magic_k's lo).
+__device__ __forceinline__ u32x4_t nib_magic_k16(uint32_t w) {
+  uint32_t m = 0x4C004C00u;
+  asm volatile("" : "+v"(m));
+  u32x4_t r;
+  r[0] = ((w << 6) & 0x03C003C0u) | m;
+  r[1] = ((w << 2) & 0x03C003C0u) | m;
+  r[2] = ((w >> 2) & 0x03C003C0u) | m;
+  r[3] = ((w >> 6) & 0x03C003C0u) | m;
+  return r;
+}
+__device__ __forceinline__ u32x4_t byte_magic_k16(uint32_t x, uint32_t y) {
+  uint32_t m = 0x5C005C00u;
+  asm volatile("" : "+v"(m));
+  u32x4_t r;
+  r[0] = ((x << 2) & 0x03FC03FCu) | m;
+  r[1] = ((x >> 6) & 0x03FC03FCu) | m;
+  r[2] = ((y << 2) & 0x03FC03FCu) | m;
+  r[3] = ((y >> 6) & 0x03FC03FCu) | m;
+  return r;
 }
 
 // The same for key operands with small offsets: low nibbles as bf16
@@ -257,6 +297,30 @@ __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
+// The low / high element of a word of two values of the cache dtype, and a
+// pair packed into one (round to nearest even).
+template <int DT>
+__device__ __forceinline__ float el_lo(uint32_t w) {
+  if constexpr (DT == kF16) return f16_to_f32(static_cast<uint16_t>(w));
+  else return bf_lo(w);
+}
+template <int DT>
+__device__ __forceinline__ float el_hi(uint32_t w) {
+  if constexpr (DT == kF16) return f16_to_f32(static_cast<uint16_t>(w >> 16));
+  else return bf_hi(w);
+}
+template <int DT>
+__device__ __forceinline__ uint32_t pack_el(float a, float b) {
+  if constexpr (DT == kF16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
+  else
+    return pack_bf16(a, b);
+}
+template <int DT>
+__device__ __forceinline__ uint32_t out_el(float x) {
+  if constexpr (DT == kF16) return f32_to_f16(x);
+  else return f32_to_bf16(x);
+}
 
 // Orders one wave's LDS writes before its later LDS reads by other lanes
 // (no workgroup barrier: every workgroup is a single wave).
@@ -299,7 +363,7 @@ __device__ __forceinline__ int seq_at(const int (&t)[NR], int s) {
   return v;
 }
 
-template <int BITS, int D, int HP>
+template <int BITS, int D, int HP, int DT = kBF16>
 struct QD {
   static constexpr int G = D / 64;            // quantization groups per row
   static constexpr int PP = 16 / HP;          // token parts of a score tile
@@ -316,7 +380,7 @@ struct QD {
   static constexpr int QCH = HP * D / 8;      // 8-dim query chunks of a head group
   static constexpr int QPL = (QCH + 63) / 64; // query chunks per lane
   static constexpr float MAG = (BITS == 4) ? 128.0f : 2176.0f;   // value operands
-  static constexpr float KMAG = (BITS == 4) ? 16.0f : 272.0f;    // key operands
+  static constexpr float KMAG = (BITS == 4) ? 16.0f : (DT == kF16 ? 256.0f : 272.0f);  // key operands
   static constexpr float C0 = (BITS == 4) ? 8.0f : 128.0f;
   // per-step operand registers; steps are double buffered when they fit
   static constexpr int BUF = D * UW / 4 + HP * D / 32;
@@ -355,11 +419,12 @@ constexpr int kModeFused = 0, kModeScores = 1, kModeWeights = 2;
 // See the header comment for the work split.  Every wave works on its own
 // range with its own LDS tables; the waves of a workgroup only share their
 // SIMD placement and unit counters.
-template <int BITS, int D, int HP, int MODE>
+template <int BITS, int D, int HP, int MODE, int DT>
 __global__ void __launch_bounds__(64 * qd_waves<D>())
 __attribute__((amdgpu_waves_per_eu((D >= 256) ? 1 : 2)))
 qdecode_kernel(DecodeArgs a) {
-  using C = QD<BITS, D, HP>;
+  static_assert(DT == kBF16 || MODE == kModeFused, "the reference modes store bf16 rows");
+  using C = QD<BITS, D, HP, DT>;
   constexpr int WPG = qd_waves<D>();
   constexpr int G = C::G, PP = C::PP, TT = C::TT, SPW = C::SPW, SL = C::SL;
   constexpr int RUN = C::RUN, NT = C::NT, VW = C::VW, ROW = C::ROW, SBW = C::SBW;
@@ -465,9 +530,13 @@ qdecode_kernel(DecodeArgs a) {
     }
   }
   // cost units per wave: W ranges (<= kMaxRange units, by the host's
-  // choice of W), and at least max_nst / (kMaxParts - 1) so that no pair is
-  // split into more than kMaxParts partials
-  const int cper = max((U + W - 1) / W, (max_nst + kMaxParts - 2) / (kMaxParts - 1));
+  // choice of W), and at least max_nst / (max_parts - 1) so that no pair is
+  // split into more than max_parts partials (the host's choice of max_parts
+  // keeps that within kMaxRange)
+  const int cper = max((U + W - 1) / W, (max_nst + a.max_parts - 2) / (a.max_parts - 1));
+  // sequence lengths past the view's max_len (a broken call) would need
+  // longer ranges than the LDS tables hold: write nothing rather than past them
+  if (cper > kMaxRange) return;
   const int u0 = w * cper;
   if (u0 >= U) return;
   const int u1 = min(U, u0 + cper);
@@ -674,7 +743,7 @@ qdecode_kernel(DecodeArgs a) {
   else
     load_step(0, bufA);
   const Magic mg;
-  const float scale_t = round_to<kBF16>(a.scale);
+  const float scale_t = round_to<DT>(a.scale);
 
   // ---- segment state
   int k = 0;             // current segment
@@ -701,8 +770,8 @@ qdecode_kernel(DecodeArgs a) {
       float v[8];
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        v[2 * e] = round_to<kBF16>(bf_lo(qr[c][e]) * scale_t);
-        v[2 * e + 1] = round_to<kBF16>(bf_hi(qr[c][e]) * scale_t);
+        v[2 * e] = round_to<DT>(el_lo<DT>(qr[c][e]) * scale_t);
+        v[2 * e + 1] = round_to<DT>(el_hi<DT>(qr[c][e]) * scale_t);
       }
       const bool live = ci < QCH && r < nh;
       float sum = 0.0f;
@@ -714,7 +783,7 @@ qdecode_kernel(DecodeArgs a) {
       u32x4_t ent;
 #pragma unroll
       for (int pr = 0; pr < 4; pr++)
-        ent[pr] = pack_bf16(v[kslot<BITS>(2 * pr)], v[kslot<BITS>(2 * pr + 1)]);
+        ent[pr] = pack_el<DT>(v[kslot<BITS>(2 * pr)], v[kslot<BITS>(2 * pr + 1)]);
       if (ci < QCH) {
         const int sg = unit / SPW, ws = unit % SPW;
 #pragma unroll
@@ -776,7 +845,12 @@ qdecode_kernel(DecodeArgs a) {
       const int g = sg / (SL / G), rho = sg % PP, kq = sg / PP;
 #pragma unroll
       for (int tau = 0; tau < TT; tau++) {
-        if constexpr (BITS == 4) {
+        if constexpr (DT == kF16 && BITS == 4) {
+          acc[tau][g] = mfma_qk<DT>(nib_magic_k16(b.kw[tau][rho][kq]), qb, acc[tau][g]);
+        } else if constexpr (DT == kF16) {
+          acc[tau][g] = mfma_qk<DT>(byte_magic_k16(b.kw[tau][rho][2 * kq], b.kw[tau][rho][2 * kq + 1]),
+                                    qb, acc[tau][g]);
+        } else if constexpr (BITS == 4) {
           acc[tau][g] = mfma(nib_magic_k(b.kw[tau][rho][kq], mg), qb, acc[tau][g]);
         } else {
           u32x4_t lo, hi;
@@ -797,12 +871,12 @@ qdecode_kernel(DecodeArgs a) {
         for (int g = 0; g < G; g++) {
           const uint32_t kwd = b.sb[tau][i][g], vwd = b.sb[tau][i][G + g];
           if constexpr (MODE != kModeWeights) {
-            const float ks = bf_lo(kwd);
-            s = fmaf(fmaf(-KMAG, ks, bf_hi(kwd)), sq[g], s);
+            const float ks = el_lo<DT>(kwd);
+            s = fmaf(fmaf(-KMAG, ks, el_hi<DT>(kwd)), sq[g], s);
             s = fmaf(ks, acc[tau][g][i], s);
           }
-          vs[tau][i][g] = bf_lo(vwd);
-          vb[tau][i][g] = bf_hi(vwd);
+          vs[tau][i][g] = el_lo<DT>(vwd);
+          vb[tau][i][g] = el_hi<DT>(vwd);
         }
         if constexpr (MODE == kModeWeights) {
           // the stored weight of token i: pairs (i0, i2) and (i1, i3) share a word
@@ -811,7 +885,7 @@ qdecode_kernel(DecodeArgs a) {
         } else {
           // the reference stores the scores in the query dtype before the
           // softmax (quantizedMM returns T, KVCache.swift:1945-1949)
-          sc[tau][i] = round_to<kBF16>(s);
+          sc[tau][i] = round_to<DT>(s);
         }
       }
     if (stp * 64 + 64 > len) {  // the sequence ends inside this step
@@ -991,12 +1065,12 @@ qdecode_kernel(DecodeArgs a) {
         for (int t = 0; t < NT; t++) {
           const float cg = csum[t / (NT / G)];
           u32x2_t v;
-          v[0] = f32_to_bf16((oacc[t][0] + cg) * inv) | (uint32_t(f32_to_bf16((oacc[t][1] + cg) * inv)) << 16);
-          v[1] = f32_to_bf16((oacc[t][2] + cg) * inv) | (uint32_t(f32_to_bf16((oacc[t][3] + cg) * inv)) << 16);
+          v[0] = out_el<DT>((oacc[t][0] + cg) * inv) | (out_el<DT>((oacc[t][1] + cg) * inv) << 16);
+          v[1] = out_el<DT>((oacc[t][2] + cg) * inv) | (out_el<DT>((oacc[t][3] + cg) * inv) << 16);
           *reinterpret_cast<u32x2_t*>(o + 16 * t) = v;
         }
       } else {
-        const int64_t slot = pair * kMaxParts + (w - wa);
+        const int64_t slot = pair * a.max_parts + (w - wa);
         float* o = a.ws_o + (slot * HP + n) * D + 4 * lg;
 #pragma unroll
         for (int t = 0; t < NT; t++) {
@@ -1116,16 +1190,17 @@ qdecode_kernel(DecodeArgs a) {
 // the larger kernel measured slower where pairs have few partials).
 // (Loading 16 with the count measured slower: most pairs have few
 // partials, and the stale slots cost traffic.)
-template <int HP, bool REST>
+template <int HP, bool REST, int DT>
 __global__ void __launch_bounds__(512) qdecode_combine_kernel(DecodeArgs a, int D) {
   constexpr int kFirst = 4;
   const int rep = a.rep, n_hg = (rep + HP - 1) / HP, HG = a.Hkv * n_hg;
   const int P = blockIdx.x, seq = P / HG, j = P % HG;
   const int len = a.seq_lens ? a.seq_lens[seq] : a.max_len;
-  const int K = reinterpret_cast<const int32_t*>(a.ws_ml + a.ws_hdr)[P];
+  // (clamped: a count the decode kernel did not write stays within the slots)
+  const int K = min(reinterpret_cast<const int32_t*>(a.ws_ml + a.ws_hdr)[P], a.max_parts);
   const int64_t hq0 = static_cast<int64_t>(j / n_hg) * rep + (j % n_hg) * HP;
   const int nh = min(HP, rep - (j % n_hg) * HP);
-  const int64_t slot0 = static_cast<int64_t>(P) * kMaxParts;
+  const int64_t slot0 = static_cast<int64_t>(P) * a.max_parts;
   const int r = threadIdx.x / (D / 4), d = 4 * (threadIdx.x % (D / 4));
   if (r >= HP) return;
   float M = -INFINITY, L = 0.0f;
@@ -1195,11 +1270,23 @@ __global__ void __launch_bounds__(512) qdecode_combine_kernel(DecodeArgs a, int 
       }
     }
     merge(kFirst, std::integral_constant<int, kRest>{}, ml, oo);
+    // a long sequence's partials past kMaxParts, kFirst a round trip
+    for (int k0 = kMaxParts; k0 < K; k0 += kFirst) {
+      f32x2_t ml2[kFirst];
+      f32x4_t oo2[kFirst];
+#pragma unroll
+      for (int q = 0; q < kFirst; q++) {
+        const int64_t slot = (slot0 + min(k0 + q, K - 1)) * HP + r;
+        ml2[q] = *reinterpret_cast<const f32x2_t*>(a.ws_ml + slot * 2);
+        oo2[q] = *reinterpret_cast<const f32x4_t*>(a.ws_o + slot * D + d);
+      }
+      merge(k0, std::integral_constant<int, kFirst>{}, ml2, oo2);
+    }
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
   u32x2_t v;
-  v[0] = f32_to_bf16(o[0] * inv) | (uint32_t(f32_to_bf16(o[1] * inv)) << 16);
-  v[1] = f32_to_bf16(o[2] * inv) | (uint32_t(f32_to_bf16(o[3] * inv)) << 16);
+  v[0] = out_el<DT>(o[0] * inv) | (out_el<DT>(o[1] * inv) << 16);
+  v[1] = out_el<DT>(o[2] * inv) | (out_el<DT>(o[3] * inv) << 16);
   *reinterpret_cast<u32x2_t*>(a.out + seq * a.o_ss + (hq0 + r) * a.o_sh + d) = v;
 }
 
@@ -1208,8 +1295,9 @@ static int heads_per_part(int rep) { return rep <= 4 ? 4 : 8; }
 int qdecode_head_groups(int rep) { return (rep + heads_per_part(rep) - 1) / heads_per_part(rep); }
 
 bool qdecode_supported(int dtype, int bits, int D, int block_size, int rep, int group) {
-  return dtype == kBF16 && (bits == 4 || bits == 8) && (D == 64 || D == 128 || D == 256) &&
-         block_size % 32 == 0 && rep >= 1 && rep <= 16 && group == 64;
+  return (dtype == kBF16 || dtype == kF16) && (bits == 4 || bits == 8) &&
+         (D == 64 || D == 128 || D == 256) && block_size % 32 == 0 && rep >= 1 && rep <= 16 &&
+         group == 64;
 }
 
 int qdecode_waves(int n_seqs, int Hkv, int rep, int max_len, int want) {
@@ -1225,10 +1313,19 @@ int qdecode_waves(int n_seqs, int Hkv, int rep, int max_len, int want) {
   return static_cast<int>(waves);
 }
 
-size_t qdecode_workspace_floats(int n_seqs, int Hkv, int rep, int D, int) {
+// Partials per (sequence, head pair) a launch allows: kMaxParts, or as many
+// as keep every wave's range within kMaxRange units for the longest
+// sequence.
+int qdecode_max_parts(int max_len) {
+  const int max_nst = (std::max(max_len, 1) + 63) / 64;
+  return std::max(kMaxParts, (max_nst + kMaxRange - 1) / kMaxRange + 2);
+}
+
+size_t qdecode_workspace_floats(int n_seqs, int Hkv, int rep, int D, int max_len) {
   const int hp = heads_per_part(rep);
   const size_t pairs = static_cast<size_t>(n_seqs) * Hkv * qdecode_head_groups(rep);
-  return pairs * kMaxParts * hp * (D + 2) + pairs;  // + one partial count (int32) per pair
+  // + one partial count (int32) per pair
+  return pairs * qdecode_max_parts(max_len) * hp * (D + 2) + pairs;
 }
 
 int qdecode_max_seqs() { return kMaxSeqs; }
@@ -1268,56 +1365,76 @@ float* decode_scratch(size_t floats) {
   return static_cast<float*>(addr[dev]);
 }
 
-// Longest sequence the decode kernel takes: ranges of at most kMaxRange
-// units with at most kMaxParts partials per pair.
-int qdecode_max_len() { return kMaxRange * (kMaxParts - 1) * 64; }
+// Longest sequence the decode kernel takes (its cost units stay in int32
+// for a launch of kMaxSeqs sequences).
+int qdecode_max_len() { return 1 << 24; }
 
-template <int BITS, int D, int HP>
+template <int BITS, int D, int HP, int DT>
 static void launch_hp(const DecodeArgs& a, bool ref, hipStream_t st) {
   constexpr int wpg = qd_waves<D>();
   const dim3 grid((a.n_waves + wpg - 1) / wpg), block(64 * wpg);
   const int pairs = a.n_seqs * a.Hkv * qdecode_head_groups(a.rep);
   const bool rest = a.n_waves > 4 * pairs;  // more than kFirst partials per pair on average
-  if (ref) {
-    // the reference-arithmetic path: bf16 score rows, the reference softmax
-    // over them in place, then P.V from the stored weights
-    hipLaunchKernelGGL((qdecode_kernel<BITS, D, HP, kModeScores>), grid, block, 0, st, a);
-    VKV_HIP(hipGetLastError());
-    launch_ref_softmax_bf16(a.sc, static_cast<int64_t>(a.n_seqs) * a.Hq, a.sc_stride, a.seq_lens,
-                            a.max_len, a.Hq, st);
-    const TimedLaunch tl = timing_prepare(kTimeDecode);
-    hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, HP, kModeWeights>), grid, block, 0, st, tl.start,
-                          tl.stop, 0, a);
-    VKV_HIP(hipGetLastError());
-    timing_commit(tl);
+  if constexpr (DT == kBF16) {
+    if (ref) {
+      // the reference-arithmetic path: bf16 score rows, the reference
+      // softmax over them in place, then P.V from the stored weights
+      hipLaunchKernelGGL((qdecode_kernel<BITS, D, HP, kModeScores, DT>), grid, block, 0, st, a);
+      VKV_HIP(hipGetLastError());
+      launch_ref_softmax_bf16(a.sc, static_cast<int64_t>(a.n_seqs) * a.Hq, a.sc_stride,
+                              a.seq_lens, a.max_len, a.Hq, st);
+      const TimedLaunch tl = timing_prepare(kTimeDecode);
+      hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, HP, kModeWeights, DT>), grid, block, 0, st,
+                            tl.start, tl.stop, 0, a);
+      VKV_HIP(hipGetLastError());
+      timing_commit(tl);
+    }
   } else {
+    if (ref) throw Error("the matrix-core reference path takes bf16 caches");
+  }
+  if (!ref) {
     const TimedLaunch tl = timing_prepare(kTimeDecode);
-    hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, HP, kModeFused>), grid, block, 0, st, tl.start,
-                          tl.stop, 0, a);
+    hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, HP, kModeFused, DT>), grid, block, 0, st,
+                          tl.start, tl.stop, 0, a);
     VKV_HIP(hipGetLastError());
     timing_commit(tl);
   }
   const dim3 cb(HP == 4 ? D : 2 * D);
   if (rest)
-    hipLaunchKernelGGL((qdecode_combine_kernel<HP, true>), dim3(pairs), cb, 0, st, a, D);
+    hipLaunchKernelGGL((qdecode_combine_kernel<HP, true, DT>), dim3(pairs), cb, 0, st, a, D);
   else
-    hipLaunchKernelGGL((qdecode_combine_kernel<HP, false>), dim3(pairs), cb, 0, st, a, D);
+    hipLaunchKernelGGL((qdecode_combine_kernel<HP, false, DT>), dim3(pairs), cb, 0, st, a, D);
   VKV_HIP(hipGetLastError());
 }
 
-template <int BITS, int D>
+template <int BITS, int D, int DT>
 static void launch_d(const DecodeArgs& a, bool ref, hipStream_t st) {
-  if (heads_per_part(a.rep) == 4) launch_hp<BITS, D, 4>(a, ref, st);
-  else launch_hp<BITS, D, 8>(a, ref, st);
+  if (heads_per_part(a.rep) == 4) launch_hp<BITS, D, 4, DT>(a, ref, st);
+  else launch_hp<BITS, D, 8, DT>(a, ref, st);
+}
+
+template <int DT>
+static void launch_dt(const DecodeArgs& a, int bits, int D, bool ref, hipStream_t st) {
+  if (bits == 4) {
+    if (D == 64) launch_d<4, 64, DT>(a, ref, st);
+    else if (D == 128) launch_d<4, 128, DT>(a, ref, st);
+    else launch_d<4, 256, DT>(a, ref, st);
+  } else {
+    if (D == 64) launch_d<8, 64, DT>(a, ref, st);
+    else if (D == 128) launch_d<8, 128, DT>(a, ref, st);
+    else launch_d<8, 256, DT>(a, ref, st);
+  }
 }
 
 void launch_qdecode(const DecodeArgs& a0, int bits, int D, hipStream_t st, bool ref) {
+  VKV_CHECK(a0.dtype == kBF16 || a0.dtype == kF16, "the matrix-core decode takes bf16 or f16 caches");
   // at most kMaxSeqs sequences per launch
   for (int s0 = 0; s0 < a0.n_seqs; s0 += kMaxSeqs) {
     DecodeArgs a = a0;
     a.n_seqs = std::min(kMaxSeqs, a0.n_seqs - s0);
     a.n_waves = qdecode_waves(a.n_seqs, a.Hkv, a.rep, a.max_len, a0.n_waves);
-    const size_t slots = static_cast<size_t>(a.n_seqs) * a.Hkv * qdecode_head_groups(a.rep) * kMaxParts;
+    a.max_parts = qdecode_max_parts(a.max_len);
+    const size_t slots = static_cast<size_t>(a.n_seqs) * a.Hkv * qdecode_head_groups(a.rep) * a.max_parts;
     a.ws_o = a0.ws;
     a.ws_ml = a0.ws + slots * heads_per_part(a.rep) * D;
     a.ws_hdr = static_cast<int32_t>(slots * heads_per_part(a.rep) * 2);
@@ -1325,15 +1442,8 @@ void launch_qdecode(const DecodeArgs& a0, int bits, int D, hipStream_t st, bool 
     a.out += s0 * a0.o_ss;
     a.table += static_cast<int64_t>(s0) * a0.table_stride;
     if (a.seq_lens) a.seq_lens += s0;
-    if (bits == 4) {
-      if (D == 64) launch_d<4, 64>(a, ref, st);
-      else if (D == 128) launch_d<4, 128>(a, ref, st);
-      else launch_d<4, 256>(a, ref, st);
-    } else {
-      if (D == 64) launch_d<8, 64>(a, ref, st);
-      else if (D == 128) launch_d<8, 128>(a, ref, st);
-      else launch_d<8, 256>(a, ref, st);
-    }
+    if (a.dtype == kF16) launch_dt<kF16>(a, bits, D, ref, st);
+    else launch_dt<kBF16>(a, bits, D, ref, st);
   }
 }
 

@@ -194,9 +194,9 @@ int fdecode_parts(int64_t rows_x_heads, int64_t T, int32_t* part_tokens, int wav
 void launch_fdecode(int dtype, const AttnArgs& a, int64_t rows, hipStream_t st);
 // MFMA decode attention over paged affine bf16 KV (vkv_decode.hip).
 struct DecodeArgs {
-  const uint16_t* q;         // [n_seqs][Hq][D] bf16
+  const uint16_t* q;         // [n_seqs][Hq][D] bf16 / f16
   int64_t q_ss, q_sh;        // element strides
-  uint16_t* out;             // [n_seqs][Hq][D] bf16
+  uint16_t* out;             // [n_seqs][Hq][D] bf16 / f16
   int64_t o_ss, o_sh;
   float scale;
   const uint8_t* base;       // layer base of the chunk pool
@@ -215,6 +215,8 @@ struct DecodeArgs {
   float* ws_ml;              //                 partial (max, sum) [slot][head][2]
   int32_t ws_hdr;            //   then (as int32 at ws_ml + ws_hdr) the number
                              //   of partials of each (sequence, head pair)
+  int32_t max_parts;         // set per launch: partials per (sequence, head pair), at most
+  int32_t dtype;             // kBF16 or kF16: queries, scales / biases and output
   uint16_t* sc;              // reference path: bf16 score / weight rows
   int64_t sc_stride;         //   [n_seqs][Hq][sc_stride], sc_stride >= max_len, % 64 == 0
 };
@@ -227,7 +229,7 @@ int qdecode_max_seqs();
 int qdecode_max_len();
 // decode waves for a launch of n_seqs sequences (want > 0 overrides)
 int qdecode_waves(int n_seqs, int Hkv, int rep, int max_len, int want);
-size_t qdecode_workspace_floats(int n_seqs, int Hkv, int rep, int D, int n_waves);
+size_t qdecode_workspace_floats(int n_seqs, int Hkv, int rep, int D, int max_len);
 // ref: the reference-arithmetic path (score rows, the reference softmax,
 // P.V from the stored weights) in place of the fused single pass
 void launch_qdecode(const DecodeArgs& a, int bits, int D, hipStream_t st, bool ref = false);
