@@ -1180,19 +1180,20 @@ qdecode_kernel(DecodeArgs a) {
 
 // Merge of the partials of (sequence, head pair)s that several waves
 // share (sdpa_vector.h:320-394).  Block = one (sequence, pair), thread = 4
-// dims of one head.  The pair's partial count, its length and its first
-// kFirst partials load together (the partial slots past the count hold
-// stale data, which the merge masks), so a pair of up to kFirst partials
-// costs one round trip to memory.  With REST the rest of a pair's partials
-// (at most kMaxParts - kFirst, only those below the count) then load
-// together, a second round trip; without it they load kFirst at a time (the
-// host picks REST when launches average more than kFirst waves per pair:
-// the larger kernel measured slower where pairs have few partials).
-// (Loading 16 with the count measured slower: most pairs have few
-// partials, and the stale slots cost traffic.)
-template <int HP, bool REST, int DT>
+// dims of one head.  The pair's partial count, its length and its first NF
+// partials load together (the partial slots past the count hold stale
+// data, which the merge masks), so a pair of up to NF partials costs one
+// round trip to memory.  With REST the rest of a pair's first kMaxParts
+// partials (only those below the count) then load together, a second round
+// trip; without it they load 4 at a time (the host picks REST when launches
+// average more than 4 waves per pair).  Partials past kMaxParts (long
+// sequences) load 4 a round trip.  (Loading 16 with the count measured
+// slower where most pairs have few partials, the stale slots costing
+// traffic; loading all 32 with the count for config 2's 32 partials a pair
+// took the merge from 4.7 to 10.4 us.)
+template <int HP, int NF, bool REST, int DT>
 __global__ void __launch_bounds__(512) qdecode_combine_kernel(DecodeArgs a, int D) {
-  constexpr int kFirst = 4;
+  constexpr int kQuad = 4;
   const int rep = a.rep, n_hg = (rep + HP - 1) / HP, HG = a.Hkv * n_hg;
   const int P = blockIdx.x, seq = P / HG, j = P % HG;
   const int len = a.seq_lens ? a.seq_lens[seq] : a.max_len;
@@ -1230,38 +1231,37 @@ __global__ void __launch_bounds__(512) qdecode_combine_kernel(DecodeArgs a, int 
     }
     M = Mn;
   };
-  {
-    f32x2_t ml[kFirst];
-    f32x4_t oo[kFirst];
+  // slots k0 .. k0 + N - 1 (clamped to the last live one), loaded together
+  auto load = [&](int k0, auto N_, f32x2_t* ml, f32x4_t* oo) __attribute__((always_inline)) {
+    constexpr int N = decltype(N_)::value;
 #pragma unroll
-    for (int q = 0; q < kFirst; q++) {
+    for (int q = 0; q < N; q++) {
+      const int64_t slot = (slot0 + min(k0 + q, max(K - 1, 0))) * HP + r;
+      ml[q] = *reinterpret_cast<const f32x2_t*>(a.ws_ml + slot * 2);
+      oo[q] = *reinterpret_cast<const f32x4_t*>(a.ws_o + slot * D + d);
+    }
+  };
+  {
+    f32x2_t ml[NF];
+    f32x4_t oo[NF];
+#pragma unroll
+    for (int q = 0; q < NF; q++) {  // unclamped: issued beside the count's load
       const int64_t slot = (slot0 + q) * HP + r;
       ml[q] = *reinterpret_cast<const f32x2_t*>(a.ws_ml + slot * 2);
       oo[q] = *reinterpret_cast<const f32x4_t*>(a.ws_o + slot * D + d);
     }
     if (len == 0 || K <= 1 || r >= nh) return;  // written by the decode kernel itself
-    merge(0, std::integral_constant<int, kFirst>{}, ml, oo);
+    merge(0, std::integral_constant<int, NF>{}, ml, oo);
   }
-  if (!REST) {
-    for (int k0 = kFirst; k0 < K; k0 += kFirst) {
-      f32x2_t ml[kFirst];
-      f32x4_t oo[kFirst];
-#pragma unroll
-      for (int q = 0; q < kFirst; q++) {
-        const int64_t slot = (slot0 + min(k0 + q, K - 1)) * HP + r;
-        ml[q] = *reinterpret_cast<const f32x2_t*>(a.ws_ml + slot * 2);
-        oo[q] = *reinterpret_cast<const f32x4_t*>(a.ws_o + slot * D + d);
-      }
-      merge(k0, std::integral_constant<int, kFirst>{}, ml, oo);
-    }
-  } else if (K > kFirst) {
-    constexpr int kRest = kMaxParts - kFirst;
+  int k0 = NF;
+  if (REST && NF < kMaxParts && K > NF) {
+    constexpr int kRest = kMaxParts - NF > 0 ? kMaxParts - NF : 1;
     f32x2_t ml[kRest];
     f32x4_t oo[kRest];
 #pragma unroll
     for (int q = 0; q < kRest; q++) {
-      if (kFirst + q < K) {
-        const int64_t slot = (slot0 + kFirst + q) * HP + r;
+      if (NF + q < K) {
+        const int64_t slot = (slot0 + NF + q) * HP + r;
         ml[q] = *reinterpret_cast<const f32x2_t*>(a.ws_ml + slot * 2);
         oo[q] = *reinterpret_cast<const f32x4_t*>(a.ws_o + slot * D + d);
       } else {
@@ -1269,19 +1269,14 @@ __global__ void __launch_bounds__(512) qdecode_combine_kernel(DecodeArgs a, int 
         oo[q] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
       }
     }
-    merge(kFirst, std::integral_constant<int, kRest>{}, ml, oo);
-    // a long sequence's partials past kMaxParts, kFirst a round trip
-    for (int k0 = kMaxParts; k0 < K; k0 += kFirst) {
-      f32x2_t ml2[kFirst];
-      f32x4_t oo2[kFirst];
-#pragma unroll
-      for (int q = 0; q < kFirst; q++) {
-        const int64_t slot = (slot0 + min(k0 + q, K - 1)) * HP + r;
-        ml2[q] = *reinterpret_cast<const f32x2_t*>(a.ws_ml + slot * 2);
-        oo2[q] = *reinterpret_cast<const f32x4_t*>(a.ws_o + slot * D + d);
-      }
-      merge(k0, std::integral_constant<int, kFirst>{}, ml2, oo2);
-    }
+    merge(NF, std::integral_constant<int, kRest>{}, ml, oo);
+    k0 = kMaxParts;
+  }
+  for (; k0 < K; k0 += kQuad) {
+    f32x2_t ml[kQuad];
+    f32x4_t oo[kQuad];
+    load(k0, std::integral_constant<int, kQuad>{}, ml, oo);
+    merge(k0, std::integral_constant<int, kQuad>{}, ml, oo);
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
   u32x2_t v;
@@ -1401,9 +1396,9 @@ static void launch_hp(const DecodeArgs& a, bool ref, hipStream_t st) {
   }
   const dim3 cb(HP == 4 ? D : 2 * D);
   if (rest)
-    hipLaunchKernelGGL((qdecode_combine_kernel<HP, true, DT>), dim3(pairs), cb, 0, st, a, D);
+    hipLaunchKernelGGL((qdecode_combine_kernel<HP, 4, true, DT>), dim3(pairs), cb, 0, st, a, D);
   else
-    hipLaunchKernelGGL((qdecode_combine_kernel<HP, false, DT>), dim3(pairs), cb, 0, st, a, D);
+    hipLaunchKernelGGL((qdecode_combine_kernel<HP, 4, false, DT>), dim3(pairs), cb, 0, st, a, D);
   VKV_HIP(hipGetLastError());
 }
 

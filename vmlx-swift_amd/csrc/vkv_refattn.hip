@@ -54,18 +54,23 @@ __device__ __forceinline__ int64_t row_len(const KVSrc& kv, int64_t b) {
   return kv.seq_lens ? kv.seq_lens[b] : kv.T;
 }
 
-// x rounded to float, then to dtype dt (0 f32, 1 f16, 2 bf16): the AccT
+// x rounded to float, then to dtype DT (0 f32, 1 f16, 2 bf16): the AccT
 // arithmetic's rounding of an fp64 value.
-__device__ __forceinline__ double rnd_d(double x, int dt) {
+template <int DT>
+__device__ __forceinline__ double rnd_d(double x) {
   const float f = static_cast<float>(x);
-  if (dt == kF16) return static_cast<double>(round_to<kF16>(f));
-  if (dt == kBF16) return static_cast<double>(round_to<kBF16>(f));
-  return static_cast<double>(f);
+  if constexpr (DT == kF16) return static_cast<double>(round_to<kF16>(f));
+  else if constexpr (DT == kBF16) return static_cast<double>(round_to<kBF16>(f));
+  else return static_cast<double>(f);
 }
-__device__ __forceinline__ double t_exp(double x, int dt) { return rnd_d(exp(x), dt); }
+// (not inlined: the fp64 exp is the rare path of t_exp_fast, and inlined
+// at every call it grew the softmax kernel past the instruction cache)
+template <int DT>
+__device__ __attribute__((noinline)) double t_exp(double x) { return rnd_d<DT>(exp(x)); }
 
-__device__ __forceinline__ double type_max_d(int dt) {
-  return dt == kF16 ? 65504.0 : dt == kBF16 ? 3.38953139e38 : 3.402823466e38;
+template <int DT>
+__device__ __forceinline__ double type_max_d() {
+  return DT == kF16 ? 65504.0 : DT == kBF16 ? 3.38953139e38 : 3.402823466e38;
 }
 
 // Score / weight storage: float, or bf16 bit patterns (the matrix-core
@@ -169,17 +174,27 @@ constexpr int kSmThreads = 256;
 constexpr int kSmVirtual = kSoftmaxThreads / kSmThreads;  // reference threads per thread
 
 // exp of a dtype value x, rounded as rnd_d rounds it (fp64 exp, to float,
-// to the dtype).  For bf16 the f32 exp decides it unless its result sits
-// within 16 float ulps of a bf16 rounding midpoint (or is tiny), where the
-// fp64 exp does.
-__device__ __forceinline__ double t_exp_fast(double x, int dt) {
-  if (dt == kBF16) {
+// to the dtype).  Below the dtype's underflow (exp(x) under half its
+// smallest subnormal: x < -25 ln 2 for f16, x < -134 ln 2 for bf16) that is
+// 0.  Otherwise the f32 exp decides it unless its result sits within 16
+// float ulps of a dtype rounding midpoint (or under the dtype's normal
+// range), where the fp64 exp does.
+template <int DT>
+__device__ __forceinline__ double t_exp_fast(double x) {
+  if constexpr (DT == kBF16) {
+    if (x < -93.0) return 0.0;
     const float e = expf(static_cast<float>(x));
     const uint32_t lo = __float_as_uint(e) & 0xFFFFu;
-    if (e >= 1.0e-37f && (lo + 16u < 0x8000u || lo > 0x8000u + 16u))
+    if (e >= 1.2e-38f && (lo + 16u < 0x8000u || lo > 0x8000u + 16u))
       return static_cast<double>(round_to<kBF16>(e));
+  } else if constexpr (DT == kF16) {
+    if (x < -17.5) return 0.0;
+    const float e = expf(static_cast<float>(x));
+    const uint32_t lo = __float_as_uint(e) & 0x1FFFu;
+    if (e >= 6.2e-5f && (lo + 16u < 0x1000u || lo > 0x1000u + 16u))
+      return static_cast<double>(round_to<kF16>(e));
   }
-  return t_exp(x, dt);
+  return t_exp<DT>(x);
 }
 
 __device__ __forceinline__ double half_sum(double x) {
@@ -193,12 +208,39 @@ __device__ __forceinline__ double half_max(double x) {
   return x;
 }
 
+// Rows are staged through LDS in windows of kSmWindow scores (all of a
+// window's loads in flight at once); a row that fits one window stays there
+// for the final pass.
+constexpr int kSmWindow = 16384;
+
 template <typename S>
+__device__ __forceinline__ void sm_stage(const S* p, int64_t w0, int wlen, float* buf, int lid) {
+  using St = Store<S>;
+  constexpr int U = 16;
+  for (int i0 = 0; i0 < wlen; i0 += U * kSmThreads) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int i = i0 + u * kSmThreads + lid;
+      v[u] = i < wlen ? static_cast<float>(St::get(p, w0 + i)) : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int i = i0 + u * kSmThreads + lid;
+      if (i < wlen) buf[i] = v[u];
+    }
+  }
+}
+
+template <typename S, int ACC>
 __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t tpad,
                                                                  const int32_t* seq_lens,
-                                                                 int32_t T_all, int64_t per_b,
-                                                                 int acc_dt, int w_dt) {
+                                                                 int32_t T_all, int64_t per_b) {
+  // ACC: the AccT dtype, or -1 for an f32-promoted row (fp32 arithmetic,
+  // f32 weights)
+  constexpr int dt = ACC < 0 ? kF32 : ACC;
   using St = Store<S>;
+  __shared__ float buf[kSmWindow];
   __shared__ double red[kSmThreads / 64];
   __shared__ double simd_s[kSoftmaxThreads / 32], simd_m[kSoftmaxThreads / 32];
   __shared__ double bcast[2];
@@ -207,10 +249,21 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
   if (T <= 0) return;
   S* p = sc + row * tpad;
   const int lid = threadIdx.x, lane = lid & 63, wv = lid >> 6;
+  const bool resident = T <= kSmWindow;  // the whole row stays in LDS
+  // score t: from LDS when the row is resident
+  auto score = [&](int64_t t) __attribute__((always_inline)) {
+    return resident ? static_cast<double>(buf[t]) : St::get(p, t);
+  };
 
-  // row max (of stored values: exact in any order)
+  // row max (of stored values: exact in any order), window by window
   double mx = -INFINITY;
-  for (int64_t t = lid; t < T; t += kSmThreads) mx = fmax(mx, St::get(p, t));
+  for (int64_t w0 = 0; w0 < T; w0 += kSmWindow) {
+    const int wlen = static_cast<int>(min<int64_t>(kSmWindow, T - w0));
+    if (w0 > 0) __syncthreads();
+    sm_stage(p, w0, wlen, buf, lid);
+    __syncthreads();
+    for (int i = lid; i < wlen; i += kSmThreads) mx = fmax(mx, static_cast<double>(buf[i]));
+  }
   mx = half_max(mx);
   mx = fmax(mx, __shfl_xor(mx, 32));
   if (lane == 0) red[wv] = mx;
@@ -218,11 +271,11 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
   mx = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
   __syncthreads();
 
-  if (acc_dt < 0) {
+  if constexpr (ACC < 0) {
     // fp32 arithmetic: exp of the f32 difference, summed, one reciprocal
     double sum = 0.0;
     for (int64_t t = lid; t < T; t += kSmThreads)
-      sum += static_cast<double>(static_cast<float>(exp(static_cast<double>(static_cast<float>(St::get(p, t) - mx)))));
+      sum += static_cast<double>(static_cast<float>(exp(static_cast<double>(static_cast<float>(score(t) - mx)))));
     sum = half_sum(sum);
     sum += __shfl_xor(sum, 32);
     if (lane == 0) red[wv] = sum;
@@ -230,12 +283,11 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
     const double tot = (red[0] + red[1]) + (red[2] + red[3]);
     const float rr = static_cast<float>(1.0 / static_cast<double>(static_cast<float>(tot)));
     for (int64_t t = lid; t < T; t += kSmThreads) {
-      const float e = static_cast<float>(exp(static_cast<double>(static_cast<float>(St::get(p, t) - mx))));
-      St::put(p, t, rnd_d(static_cast<double>(e * rr), w_dt));
+      const float e = static_cast<float>(exp(static_cast<double>(static_cast<float>(score(t) - mx))));
+      St::put(p, t, rnd_d<kF32>(static_cast<double>(e * rr)));
     }
     return;
   }
-  const int dt = acc_dt;
   if (T <= kSoftmaxLoopedLimit) {
     // softmax_single_row: reference thread v = lid + 256 k owns keys 4v .. 4v + 3
     double e[kSmVirtual][kSoftmaxReads];
@@ -245,19 +297,19 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
 #pragma unroll
       for (int i = 0; i < kSoftmaxReads; i++) {
         const int64_t t = static_cast<int64_t>(kSoftmaxReads) * (lid + kSmThreads * k) + i;
-        e[k][i] = t < T ? t_exp_fast(rnd_d(St::get(p, t) - mx, dt), dt) : 0.0;
-        if (t < T) thr = rnd_d(thr + e[k][i], dt);
+        e[k][i] = t < T ? t_exp_fast<dt>(rnd_d<dt>(static_cast<double>(buf[t]) - mx)) : 0.0;
+        if (t < T) thr = rnd_d<dt>(thr + e[k][i]);
       }
       // simd group (lid + 256 k) / 32: this half-wave
       const double sg = half_sum(thr);
-      if ((lid & 31) == 0) simd_s[(lid >> 5) + (kSmThreads / 32) * k] = rnd_d(sg, dt);
+      if ((lid & 31) == 0) simd_s[(lid >> 5) + (kSmThreads / 32) * k] = rnd_d<dt>(sg);
     }
     __syncthreads();
     if (wv == 0) {
       const int nsimd = static_cast<int>((T + 127) / 128);
       double tot = lane < 32 && lane < nsimd ? simd_s[lane] : 0.0;
       tot = half_sum(tot);
-      if (lane == 0) bcast[0] = rnd_d(1.0 / rnd_d(tot, dt), dt);
+      if (lane == 0) bcast[0] = rnd_d<dt>(1.0 / rnd_d<dt>(tot));
     }
     __syncthreads();
     const double rr = bcast[0];
@@ -266,54 +318,84 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
 #pragma unroll
       for (int i = 0; i < kSoftmaxReads; i++) {
         const int64_t t = static_cast<int64_t>(kSoftmaxReads) * (lid + kSmThreads * k) + i;
-        if (t < T) St::put(p, t, rnd_d(e[k][i] * rr, dt));
+        if (t < T) St::put(p, t, rnd_d<dt>(e[k][i] * rr));
       }
     return;
   }
   // softmax_looped: reference thread v keeps a running (max, sum) over keys
-  // 4v + 4096 r + i, rescaled at every round
-  const double fmin = -type_max_d(dt);
+  // 4v + 4096 r + i, rescaled at every round; the rounds go window by window
+  const double fmin = -type_max_d<dt>();
   const int64_t stride = static_cast<int64_t>(kSoftmaxReads) * kSoftmaxThreads;
   const int64_t rounds = (T + stride - 1) / stride;
+  constexpr int kRoundsPerWindow = kSmWindow / (kSoftmaxReads * kSoftmaxThreads);
+  double m[kSmVirtual], n[kSmVirtual];
 #pragma unroll
   for (int k = 0; k < kSmVirtual; k++) {
-    double m = fmin, n = 0.0;
-    for (int64_t rd = 0; rd < rounds; rd++) {
-      const int64_t off = rd * stride + static_cast<int64_t>(lid + kSmThreads * k) * kSoftmaxReads;
-      double v[kSoftmaxReads];
-      const double prev = m;
-#pragma unroll
-      for (int i = 0; i < kSoftmaxReads; i++) {
-        v[i] = off + i < T ? St::get(p, off + i) : -INFINITY;
-        m = v[i] > m ? v[i] : m;
-      }
-      n = rnd_d(n * t_exp_fast(rnd_d(prev - m, dt), dt), dt);
-#pragma unroll
-      for (int i = 0; i < kSoftmaxReads; i++) n = rnd_d(n + t_exp_fast(rnd_d(v[i] - m, dt), dt), dt);
+    m[k] = fmin;
+    n[k] = 0.0;
+  }
+  for (int64_t rd0 = 0; rd0 < rounds; rd0 += kRoundsPerWindow) {
+    const int64_t w0 = rd0 * stride;
+    const int wlen = static_cast<int>(min<int64_t>(kSmWindow, T - w0));
+    if (!resident) {
+      __syncthreads();
+      sm_stage(p, w0, wlen, buf, lid);
+      __syncthreads();
     }
+    const int64_t rd1 = min<int64_t>(rounds, rd0 + kRoundsPerWindow);
+    for (int64_t rd = rd0; rd < rd1; rd++) {
+#pragma unroll
+      for (int k = 0; k < kSmVirtual; k++) {
+        const int64_t off = rd * stride + static_cast<int64_t>(lid + kSmThreads * k) * kSoftmaxReads;
+        double v[kSoftmaxReads];
+        const double prev = m[k];
+#pragma unroll
+        for (int i = 0; i < kSoftmaxReads; i++) {
+          v[i] = off + i < T ? static_cast<double>(buf[off + i - w0]) : -INFINITY;
+          m[k] = v[i] > m[k] ? v[i] : m[k];
+        }
+        n[k] = rnd_d<dt>(n[k] * t_exp_fast<dt>(rnd_d<dt>(prev - m[k])));
+#pragma unroll
+        for (int i = 0; i < kSoftmaxReads; i++) n[k] = rnd_d<dt>(n[k] + t_exp_fast<dt>(rnd_d<dt>(v[i] - m[k])));
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kSmVirtual; k++) {
     // simd group (lid + 256 k) / 32: its max, then the rescaled sums
-    const double mg = half_max(m);
-    const double acc = half_sum(rnd_d(n * t_exp_fast(rnd_d(m - mg, dt), dt), dt));
+    const double mg = half_max(m[k]);
+    const double acc = half_sum(rnd_d<dt>(n[k] * t_exp_fast<dt>(rnd_d<dt>(m[k] - mg))));
     if ((lid & 31) == 0) {
       simd_m[(lid >> 5) + (kSmThreads / 32) * k] = mg;
-      simd_s[(lid >> 5) + (kSmThreads / 32) * k] = rnd_d(acc, dt);
+      simd_s[(lid >> 5) + (kSmThreads / 32) * k] = rnd_d<dt>(acc);
     }
   }
   __syncthreads();
   if (wv == 0) {
     const double sm = lane < 32 ? simd_m[lane] : fmin;
     const double gmax = half_max(sm);
-    double tot = lane < 32 ? rnd_d(simd_s[lane] * t_exp_fast(rnd_d(sm - gmax, dt), dt), dt) : 0.0;
+    double tot = lane < 32 ? rnd_d<dt>(simd_s[lane] * t_exp_fast<dt>(rnd_d<dt>(sm - gmax))) : 0.0;
     tot = half_sum(tot);
     if (lane == 0) {
       bcast[0] = gmax;
-      bcast[1] = rnd_d(1.0 / rnd_d(tot, dt), dt);
+      bcast[1] = rnd_d<dt>(1.0 / rnd_d<dt>(tot));
     }
   }
   __syncthreads();
   const double gmax = bcast[0], rr = bcast[1];
-  for (int64_t t = lid; t < T; t += kSmThreads)
-    St::put(p, t, rnd_d(t_exp_fast(rnd_d(St::get(p, t) - gmax, dt), dt) * rr, dt));
+  if (resident) {
+    for (int64_t t = lid; t < T; t += kSmThreads)
+      St::put(p, t, rnd_d<dt>(t_exp_fast<dt>(rnd_d<dt>(static_cast<double>(buf[t]) - gmax)) * rr));
+    return;
+  }
+  for (int64_t w0 = 0; w0 < T; w0 += kSmWindow) {
+    const int wlen = static_cast<int>(min<int64_t>(kSmWindow, T - w0));
+    __syncthreads();
+    sm_stage(p, w0, wlen, buf, lid);
+    __syncthreads();
+    for (int i = lid; i < wlen; i += kSmThreads)
+      St::put(p, w0 + i, rnd_d<dt>(t_exp_fast<dt>(rnd_d<dt>(static_cast<double>(buf[i]) - gmax)) * rr));
+  }
 }
 
 // ---- pass 3: out = sum_t w_t dequant(v_t).  Workgroup = (token part, kv
@@ -439,11 +521,14 @@ static void ref_launch_dt(const RefArgs& r, int64_t B, hipStream_t st) {
   VKV_CHECK(lds_ok, "cannot raise the score kernel's LDS limit");
   hipLaunchKernelGGL((ref_scores_kernel<DT, BITS>), gs, dim3(256), ref_scores_lds(a.D), st, r);
   VKV_HIP(hipGetLastError());
-  const int acc_dt = r.score_f32 ? -1 : DT;
-  const int w_dt = r.score_f32 ? kF32 : DT;
-  hipLaunchKernelGGL((ref_softmax_kernel<float>), dim3(static_cast<unsigned>(B * a.Hq * r.nl)),
-                     dim3(kSmThreads), 0, st, r.sc, r.tpad, a.kv.seq_lens, a.kv.T,
-                     static_cast<int64_t>(a.Hq) * r.nl, acc_dt, w_dt);
+  const dim3 rows(static_cast<unsigned>(B * a.Hq * r.nl));
+  const int64_t per_b = static_cast<int64_t>(a.Hq) * r.nl;
+  if (r.score_f32)
+    hipLaunchKernelGGL((ref_softmax_kernel<float, -1>), rows, dim3(kSmThreads), 0, st, r.sc, r.tpad,
+                       a.kv.seq_lens, a.kv.T, per_b);
+  else
+    hipLaunchKernelGGL((ref_softmax_kernel<float, DT>), rows, dim3(kSmThreads), 0, st, r.sc, r.tpad,
+                       a.kv.seq_lens, a.kv.T, per_b);
   VKV_HIP(hipGetLastError());
   const int nrb = (nrows + kRefRows - 1) / kRefRows;
   const dim3 gp(static_cast<unsigned>(r.n_parts), static_cast<unsigned>(a.Hkv * nrb),
@@ -481,8 +566,8 @@ void launch_ref_attention(int dtype, const RefArgs& r, int64_t B, hipStream_t st
 void launch_ref_softmax_bf16(uint16_t* sc, int64_t rows, int64_t tpad, const int32_t* seq_lens,
                              int32_t T, int64_t per_b, hipStream_t st) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL((ref_softmax_kernel<uint16_t>), dim3(static_cast<unsigned>(rows)),
-                     dim3(kSmThreads), 0, st, sc, tpad, seq_lens, T, per_b, kBF16, kBF16);
+  hipLaunchKernelGGL((ref_softmax_kernel<uint16_t, kBF16>), dim3(static_cast<unsigned>(rows)),
+                     dim3(kSmThreads), 0, st, sc, tpad, seq_lens, T, per_b);
   VKV_HIP(hipGetLastError());
 }
 
