@@ -374,6 +374,80 @@ void set_sinks(AttnArgs& a, const vkv_array* sinks, int64_t Hq) {
   a.sinks = sinks->data;
   a.sinks_dtype = sinks->dtype;
 }
+// MLXFast SDPA (vkv_sdpa); pt: a cache update's deferred one-token write,
+// which the float decode kernel performs as it reads the token (or, where
+// that kernel does not run, a copy launched first).
+void sdpa_impl(const vkv_array* q, const vkv_array* k, const vkv_array* v, float scale,
+             int32_t mask_mode, const vkv_array* mask, const vkv_array* sinks, vkv_array* out,
+             void* stream, Cache* pt) {
+  need(q, "q");
+  need(k, "k");
+  need(v, "v");
+  need(out, "out");
+  if (q->ndim != 4 || k->ndim != 4 || v->ndim != 4 || out->ndim != 4)
+    throw Error("q, k, v and out must be 4-D");
+  if (q->dtype != k->dtype || q->dtype != v->dtype || q->dtype != out->dtype || !is_float(q->dtype))
+    throw Error("q, k, v and out must share a float dtype");
+  if (q->strides[3] != 1 || k->strides[3] != 1 || v->strides[3] != 1 || out->strides[3] != 1)
+    throw Error("last dims must be contiguous");
+  const int64_t B = q->shape[0], Hq = q->shape[1], L = q->shape[2], D = q->shape[3];
+  const int64_t Hkv = k->shape[1], T = k->shape[2], Dv = v->shape[3];
+  if (k->shape[0] != B || v->shape[0] != B || v->shape[1] != Hkv || v->shape[2] != T ||
+      k->shape[3] != D || Hq % Hkv)
+    throw Error("q/k/v shapes are inconsistent");
+  if (out->shape[0] != B || out->shape[1] != Hq || out->shape[2] != L || out->shape[3] != Dv)
+    throw Error("out must be [B, Hq, L, Dv]");
+  const int es = elem_bytes(q->dtype);
+  AttnArgs a{};
+  a.q = q->data;
+  a.q_sb = q->strides[0];
+  a.q_sh = q->strides[1];
+  a.q_sl = q->strides[2];
+  a.L = static_cast<int32_t>(L);
+  a.Hq = static_cast<int32_t>(Hq);
+  a.Hkv = static_cast<int32_t>(Hkv);
+  a.D = static_cast<int32_t>(D);
+  a.Dv = static_cast<int32_t>(Dv);
+  a.scale = scale;
+  a.kv.kc = Comp{static_cast<const uint8_t*>(k->data), k->strides[0] * es, k->strides[1] * es,
+                 k->strides[2] * es};
+  a.kv.vc = Comp{static_cast<const uint8_t*>(v->data), v->strides[0] * es, v->strides[1] * es,
+                 v->strides[2] * es};
+  a.kv.T = static_cast<int32_t>(T);
+  a.out = out->data;
+  a.o_sb = out->strides[0];
+  a.o_sh = out->strides[1];
+  a.o_sl = out->strides[2];
+  set_mask(a, mask_mode, mask, B, Hq, L, T, q->dtype);
+  set_sinks(a, sinks, Hq);
+  if (pt && pt->pending.set) {
+    const Cache::PendingToken& p = pt->pending;
+    const vkv_array& nk = p.k;
+    const vkv_array& nv = p.v;
+    const bool al = reinterpret_cast<uintptr_t>(nk.data) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(nv.data) % 16 == 0 &&
+                    (nk.strides[0] * es) % 16 == 0 && (nk.strides[1] * es) % 16 == 0 &&
+                    (nv.strides[0] * es) % 16 == 0 && (nv.strides[1] * es) % 16 == 0;
+    const bool same = k->data == p.dk->buf->get() && v->data == p.dv->buf->get() &&
+                      nk.dtype == q->dtype && nv.dtype == q->dtype;
+    if (al && same && p.pos < T && fdecode_supported(q->dtype, 0, false, a) &&
+        !option(VKV_OPTION_GENERIC_ATTENTION)) {
+      a.has_new = 1;
+      a.new_t = p.pos;
+      a.nk_ptr = static_cast<const uint8_t*>(nk.data);
+      a.nv_ptr = static_cast<const uint8_t*>(nv.data);
+      a.nk_sb = nk.strides[0] * es;
+      a.nk_sh = nk.strides[1] * es;
+      a.nv_sb = nv.strides[0] * es;
+      a.nv_sh = nv.strides[1] * es;
+      pt->pending.set = false;  // the decode kernel writes it
+    } else {
+      pt->flush_pending(S(stream));
+    }
+  }
+  run_attention(q->dtype, 0, 64, false, a, B * L, T, S(stream));
+}
+
 }  // namespace
 
 extern "C" {
@@ -381,51 +455,8 @@ extern "C" {
 int vkv_sdpa(const vkv_array* q, const vkv_array* k, const vkv_array* v, float scale,
              int32_t mask_mode, const vkv_array* mask, const vkv_array* sinks, vkv_array* out,
              void* stream) {
-  return guard([&] {
-    need(q, "q");
-    need(k, "k");
-    need(v, "v");
-    need(out, "out");
-    if (q->ndim != 4 || k->ndim != 4 || v->ndim != 4 || out->ndim != 4)
-      throw Error("q, k, v and out must be 4-D");
-    if (q->dtype != k->dtype || q->dtype != v->dtype || q->dtype != out->dtype || !is_float(q->dtype))
-      throw Error("q, k, v and out must share a float dtype");
-    if (q->strides[3] != 1 || k->strides[3] != 1 || v->strides[3] != 1 || out->strides[3] != 1)
-      throw Error("last dims must be contiguous");
-    const int64_t B = q->shape[0], Hq = q->shape[1], L = q->shape[2], D = q->shape[3];
-    const int64_t Hkv = k->shape[1], T = k->shape[2], Dv = v->shape[3];
-    if (k->shape[0] != B || v->shape[0] != B || v->shape[1] != Hkv || v->shape[2] != T ||
-        k->shape[3] != D || Hq % Hkv)
-      throw Error("q/k/v shapes are inconsistent");
-    if (out->shape[0] != B || out->shape[1] != Hq || out->shape[2] != L || out->shape[3] != Dv)
-      throw Error("out must be [B, Hq, L, Dv]");
-    const int es = elem_bytes(q->dtype);
-    AttnArgs a{};
-    a.q = q->data;
-    a.q_sb = q->strides[0];
-    a.q_sh = q->strides[1];
-    a.q_sl = q->strides[2];
-    a.L = static_cast<int32_t>(L);
-    a.Hq = static_cast<int32_t>(Hq);
-    a.Hkv = static_cast<int32_t>(Hkv);
-    a.D = static_cast<int32_t>(D);
-    a.Dv = static_cast<int32_t>(Dv);
-    a.scale = scale;
-    a.kv.kc = Comp{static_cast<const uint8_t*>(k->data), k->strides[0] * es, k->strides[1] * es,
-                   k->strides[2] * es};
-    a.kv.vc = Comp{static_cast<const uint8_t*>(v->data), v->strides[0] * es, v->strides[1] * es,
-                   v->strides[2] * es};
-    a.kv.T = static_cast<int32_t>(T);
-    a.out = out->data;
-    a.o_sb = out->strides[0];
-    a.o_sh = out->strides[1];
-    a.o_sl = out->strides[2];
-    set_mask(a, mask_mode, mask, B, Hq, L, T, q->dtype);
-    set_sinks(a, sinks, Hq);
-    run_attention(q->dtype, 0, 64, false, a, B * L, T, S(stream));
-  });
+  return guard([&] { sdpa_impl(q, k, v, scale, mask_mode, mask, sinks, out, stream, nullptr); });
 }
-
 int vkv_quantized_sdpa(const vkv_array* q, const vkv_array* k_wq, const vkv_array* k_scales,
                        const vkv_array* k_biases, const vkv_array* v_wq, const vkv_array* v_scales,
                        const vkv_array* v_biases, int32_t group_size, int32_t bits, float scale,
@@ -692,20 +723,36 @@ int vkv_attention_with_cache_update(const vkv_array* q, const vkv_array* keys, c
       call(vkv_quantized_paged_sdpa(q, &view, scale, mask_mode, mask, out, stream));
       return;
     }
-    // :106-142: update, then the cache's array mask when none was given
+    // :106-142: update, then the cache's array mask when none was given.
+    // A one-token update of a KVCacheSimple or RotatingKVCache leaves its
+    // copy to the float decode kernel that follows (it writes the token as
+    // it reads it); any other path flushes the copy first.
     vkv_array ck{}, cv{};
-    call(vkv_cache_update(cache, keys, values, stream, &ck, &cv));
-    int32_t mode = mask_mode;
-    const vkv_array* m = mask;
-    vkv_array cm{};
-    if (mask_mode == VKV_MASK_NONE) {
-      const int cmode = cache->impl->make_mask(static_cast<int>(q->shape[2]), 0, true, S(stream), &cm);
-      if (cmode == VKV_MASK_ARRAY) {
-        mode = VKV_MASK_ARRAY;
-        m = &cm;
-      }
+    Cache* c = cache->impl.get();
+    c->defer_token = true;
+    const int rc = vkv_cache_update(cache, keys, values, stream, &ck, &cv);
+    c->defer_token = false;
+    if (rc != 0) {
+      c->flush_pending(S(stream));
+      throw Error(g_error);
     }
-    call(vkv_sdpa(q, &ck, &cv, scale, mode, m, sinks, out, stream));
+    try {
+      int32_t mode = mask_mode;
+      const vkv_array* m = mask;
+      vkv_array cm{};
+      if (mask_mode == VKV_MASK_NONE) {
+        const int cmode = c->make_mask(static_cast<int>(q->shape[2]), 0, true, S(stream), &cm);
+        if (cmode == VKV_MASK_ARRAY) {
+          mode = VKV_MASK_ARRAY;
+          m = &cm;
+        }
+      }
+      sdpa_impl(q, &ck, &cv, scale, mode, m, sinks, out, stream, c);
+    } catch (...) {
+      c->flush_pending(S(stream));
+      throw;
+    }
+    c->flush_pending(S(stream));  // (nothing left once the kernel took it)
   });
 }
 

@@ -140,17 +140,23 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
   constexpr int NV = kStep / RPI;
   constexpr bool kVEarly = (KL / 2 + NV) * 4 <= 160;
   u32x4_t kw[KL / 2], vw[NV];
+  // a cache update's deferred token: row new_t comes from its source rows,
+  // and the range that holds it writes it into the cache (one head group)
+  const int64_t new_t = a.has_new ? a.new_t : -1;
+  const bool writes_new = new_t >= t_begin && new_t < t_end && hg == 0;
+  const uint8_t* nkrow = a.has_new ? a.nk_ptr + b * a.nk_sb + hk * a.nk_sh : kbase;
+  const uint8_t* nvrow = a.has_new ? a.nv_ptr + b * a.nv_sb + hk * a.nv_sh : vbase;
   auto load_k = [&](int64_t t0) __attribute__((always_inline)) {
-    const int64_t t = t0 + tok;
-    const uint8_t* krow = kbase + (t < t_end ? t : t_begin) * kst + 16 * (KL / 2) * half;
+    const int64_t t = t0 + tok < t_end ? t0 + tok : t_begin;
+    const uint8_t* krow = (t == new_t ? nkrow : kbase + t * kst) + 16 * (KL / 2) * half;
 #pragma unroll
     for (int c = 0; c < KL / 2; c++) kw[c] = *(g_u32x4_t*)(krow + 16 * c);
   };
   auto load_v = [&](int64_t t0) __attribute__((always_inline)) {
 #pragma unroll
     for (int k = 0; k < NV; k++) {
-      const int64_t tv = t0 + rs + RPI * k;
-      vw[k] = *(g_u32x4_t*)(vbase + (tv < t_end ? tv : t_begin) * vst + 16 * dg);
+      const int64_t tv = t0 + rs + RPI * k < t_end ? t0 + rs + RPI * k : t_begin;
+      vw[k] = *(g_u32x4_t*)((tv == new_t ? nvrow : vbase + tv * vst) + 16 * dg);
     }
   };
 
@@ -213,6 +219,11 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
         for (int e = 0; e < VEC; e++) s[r] = fmaf(qs[r][q0 + e], kv[e], s[r]);
     }
     if constexpr (!kVEarly) load_v(t0);
+    if (writes_new && t == new_t) {  // the new token's key row into the cache
+      uint8_t* dst = const_cast<uint8_t*>(kbase) + new_t * kst + 16 * (KL / 2) * half;
+#pragma unroll
+      for (int c = 0; c < KL / 2; c++) *reinterpret_cast<u32x4_t*>(dst + 16 * c) = kw[c];
+    }
 
 #pragma unroll
     for (int r = 0; r < REP; r++) s[r] = add_xor32(s[r]);
@@ -252,6 +263,8 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
 #pragma unroll
     for (int k = 0; k < NV; k++) {
       const int tt = rs + RPI * k;
+      if (writes_new && t0 + tt == new_t)  // the new token's value row into the cache
+        *reinterpret_cast<u32x4_t*>(const_cast<uint8_t*>(vbase) + new_t * vst + 16 * dg) = vw[k];
       float vv[VEC];
       unpack16<DT>(vw[k], vv);
 #pragma unroll

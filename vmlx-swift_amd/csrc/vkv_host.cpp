@@ -132,6 +132,26 @@ int Cache::make_mask(int n, int window, bool return_array, hipStream_t st, vkv_a
   return VKV_MASK_CAUSAL;
 }
 
+void Cache::write_tokens(const Dense4& dk, const Dense4& dv, int64_t dt0, const vkv_array& k,
+                         const vkv_array& v, int64_t len, hipStream_t st) {
+  if (defer_token && len == 1) {
+    pending.set = true;
+    pending.dk = &dk;
+    pending.dv = &dv;
+    pending.pos = dt0;
+    pending.k = k;
+    pending.v = v;
+    return;
+  }
+  copy_tokens_kv(dk, dv, dt0, k, v, 0, len, st);
+}
+
+void Cache::flush_pending(hipStream_t st) {
+  if (!pending.set) return;
+  pending.set = false;
+  copy_tokens_kv(*pending.dk, *pending.dv, pending.pos, pending.k, pending.v, 0, 1, st);
+}
+
 // BaseKVCache.metaState setter (KVCache.swift:268-276)
 void Cache::set_meta_state(const std::vector<std::string>& v) {
   if (!(v.size() == 1 && v[0].empty()))
@@ -199,7 +219,7 @@ void SimpleCache::update(const vkv_array& k, const vkv_array& v, hipStream_t st,
     }
   }
   offset += Sn;
-  copy_tokens_kv(k_, v_, prev, k, v, 0, Sn, st);
+  write_tokens(k_, v_, prev, k, v, Sn, st);
   *ok = k_.view(offset);
   *ov = v_.view(offset);
 }
@@ -362,7 +382,7 @@ bool RotatingCache::update_in_place(const vkv_array& k, const vkv_array& v, hipS
     update_concat(k, v, st);
     return false;
   }
-  copy_tokens_kv(k_, v_, idx_, k, v, 0, Sn, st);
+  write_tokens(k_, v_, idx_, k, v, Sn, st);
   offset += Sn;
   idx_ += Sn;
   return true;

@@ -130,7 +130,28 @@ class Cache {
   // BaseKVCache.makeMask (KVCache.swift:287-311)
   virtual int make_mask(int n, int window, bool return_array, hipStream_t st, vkv_array* mask);
 
+  // A one-token write an update may leave to the attention that follows
+  // it (the router's decode step): while armed, KVCacheSimple and
+  // RotatingKVCache record the new token's copy here instead of launching
+  // it, and the float decode kernel writes the token into the cache as it
+  // reads it.  Whoever arms it either hands the record to that kernel or
+  // calls flush_pending() before anything else reads the cache.
+  struct PendingToken {
+    bool set = false;
+    const Dense4* dk = nullptr;
+    const Dense4* dv = nullptr;
+    int64_t pos = 0;           // token position in the cache buffers
+    vkv_array k{}, v{};        // the new token's [B, H, 1, D] source rows
+  };
+  bool defer_token = false;
+  PendingToken pending;
+  void flush_pending(hipStream_t st);
+
  protected:
+  // the copy of an update's new tokens into the buffers (recorded instead
+  // when armed and the update is one token)
+  void write_tokens(const Dense4& dk, const Dense4& dv, int64_t dt0, const vkv_array& k,
+                    const vkv_array& v, int64_t len, hipStream_t st);
   DevBuf mask_buf_;
   int causal_array_mask(int n, int64_t off, int window, hipStream_t st, vkv_array* mask);
 };

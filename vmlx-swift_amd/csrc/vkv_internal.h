@@ -105,6 +105,14 @@ struct AttnArgs {
   float* ws_o;             // [rows][Hq][n_parts][Dv]
   float* ws_ml;            // [rows][Hq][n_parts][2] (max, sum)
   int32_t group;           // affine quantization group (0 = 64)
+  // float decode only: key/value row new_t of every (batch row, kv head)
+  // comes from these source rows (byte strides) instead of the cache, and
+  // the kernel writes it into the cache (a cache update's deferred token)
+  int32_t has_new;
+  int64_t new_t;
+  const uint8_t* nk_ptr;
+  const uint8_t* nv_ptr;
+  int64_t nk_sb, nk_sh, nv_sb, nv_sh;
 };
 
 // Quantized attention with the reference's arithmetic (vkv_refattn.hip):
