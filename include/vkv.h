@@ -398,6 +398,22 @@ int vkv_turboquant_restore_compressed(vkv_cache cache, const vkv_tq_encoded *key
 /* restoreFromDecodedKV(keys:values:sourceOffset:) (:281-322). */
 int vkv_turboquant_restore_decoded(vkv_cache cache, const vkv_array *keys, const vkv_array *values,
                                    int64_t source_offset, void *stream);
+/* A TurboQuant cache as pool pages, so that a compressed sequence joins a
+ * paged batched decode (vkv_paged_sdpa over the pool) beside float or
+ * affine sequences.  Under batching the reference compresses each slot's
+ * cache (BatchEngine/BatchQuantize.swift:115-125 -> maybeQuantizeKVCache)
+ * and BatchKVCache attends the plain K/V its update returns
+ * (TurboQuantKVCache.swift:428-500: the decoded prefix, then the exact
+ * window).  This writes tokens [first_token, first_token + n_tokens) of
+ * those K/V, every batch row, into pool slots: slot_mapping is device int32
+ * [B * n_tokens], row b's tokens at b * n_tokens (slot = block * block_size
+ * + position, -1 skips a token).  Rows are cast to the pool dtype (round to
+ * nearest even; an f32 pool holds them exactly) and quantized as any append
+ * when the pool is affine.  After the compression write [0, offset); after
+ * each later update write its new tokens (they sit in the window, exact). */
+int vkv_turboquant_write_pool(vkv_cache cache, vkv_pool pool, int32_t layer,
+                              const int32_t *slot_mapping, int64_t first_token, int64_t n_tokens,
+                              void *stream);
 /* The codec's host tables (EncoderState, TQEncoder.swift:88-107): the
  * rotation signs of (dim, seed) (TQHadamard.generateRandomSigns), the
  * Lloyd-Max codebook of (dim, bits) (TQCodebook.computeCodebook, 2^bits

@@ -979,6 +979,76 @@ int vkv_turboquant_restore_decoded(vkv_cache cache, const vkv_array* keys, const
   });
 }
 
+int vkv_turboquant_write_pool(vkv_cache cache, vkv_pool pool, int32_t layer,
+                              const int32_t* slot_mapping, int64_t first_token, int64_t n_tokens,
+                              void* stream) {
+  return guarded([&] {
+    need_ptr(pool, "pool");
+    TurboQuantCache* t = as_tq(cache);
+    const hipStream_t st = S(stream);
+    if (n_tokens < 0 || first_token < 0) throw Error("first_token and n_tokens must be >= 0");
+    if (n_tokens == 0) return;
+    if (!slot_mapping) throw Error("slot_mapping is required");
+    // the keys and values update() returns: [B, H, offset, D] views of the
+    // unified buffers (decoded prefix, then the exact window)
+    vkv_array s[2];
+    if (t->state(st, s) < 2) throw Error("the cache is empty");
+    if (first_token + n_tokens > s[0].shape[2])
+      throw Error("tokens [first_token, first_token + n_tokens) must lie within the cache's offset");
+    Pool& P = *pool->impl;
+    const bool keys_only = (P.p.flags & VKV_VIEW_KEYS_ONLY) != 0;
+    const int64_t B = s[0].shape[0], H = s[0].shape[1];
+    if (H != P.p.n_kv_heads || s[0].shape[3] != P.p.head_dim ||
+        (!keys_only && s[1].shape[3] != P.p.v_head_dim))
+      throw Error("the cache's heads and head dims must match the pool's");
+    const int passes = keys_only ? 1 : 2;
+    // rows in another dtype than the pool's are cast first (rounded to
+    // nearest even; an f32 pool keeps them exactly)
+    const bool cast = s[0].dtype != P.p.dtype || (!keys_only && s[1].dtype != P.p.dtype);
+    DevBuf tmp;
+    if (cast)
+      tmp.alloc(static_cast<size_t>(n_tokens * H * (P.p.head_dim + P.p.v_head_dim)) *
+                elem_bytes(P.p.dtype));
+    for (int64_t b = 0; b < B; b++) {
+      vkv_array rows[2]{};
+      int64_t off = 0;
+      for (int w = 0; w < passes; w++) {
+        const vkv_array& a = s[w];
+        const int64_t D = a.shape[3];
+        const void* src = static_cast<const uint8_t*>(a.data) +
+                          (b * a.strides[0] + first_token * a.strides[2]) * elem_bytes(a.dtype);
+        vkv_array& r = rows[w];
+        r.dtype = P.p.dtype;
+        r.ndim = 3;
+        r.shape[0] = n_tokens;
+        r.shape[1] = H;
+        r.shape[2] = D;
+        if (a.dtype == P.p.dtype) {
+          r.data = const_cast<void*>(src);
+          r.strides[0] = a.strides[2];
+          r.strides[1] = a.strides[1];
+          r.strides[2] = a.strides[3];
+        } else {
+          void* dst = tmp.bytes() + off * elem_bytes(P.p.dtype);
+          off += n_tokens * H * D;
+          const int64_t shape[4] = {1, n_tokens, H, D};
+          const int64_t sstr[4] = {0, a.strides[2], a.strides[1], a.strides[3]};
+          const int64_t dstr[4] = {0, H * D, D, 1};
+          launch_cast4d(src, a.dtype, shape, sstr, dst, P.p.dtype, dstr, st);
+          r.data = dst;
+          r.strides[0] = H * D;
+          r.strides[1] = D;
+          r.strides[2] = 1;
+        }
+      }
+      P.append(layer, rows[0], keys_only ? nullptr : &rows[1], slot_mapping + b * n_tokens,
+               n_tokens, st);
+    }
+    // the cast rows live until the appends have read them
+    if (cast) VKV_HIP(hipStreamSynchronize(st));
+  });
+}
+
 int vkv_tq_tables(int32_t dim, int32_t bits, int32_t seed, float* signs, float* codebook,
                   float* qjl) {
   return guarded([&] { tq_host_tables(dim, bits, seed, signs, codebook, qjl); });

@@ -106,6 +106,7 @@ EXPORTS = (
     "vkv_turboquant_has_compressible_middle", "vkv_turboquant_info", "vkv_turboquant_encoded",
     "vkv_turboquant_window", "vkv_turboquant_restore_compressed",
     "vkv_turboquant_restore_decoded", "vkv_tq_tables", "vkv_set_option", "vkv_get_option",
+    "vkv_turboquant_write_pool",
 )
 TIME_DECODE, TIME_MLA, TIME_FDECODE, TIME_TQ_ENCODE, TIME_TQ_DECODE = 0, 1, 2, 3, 4
 
@@ -695,6 +696,19 @@ class TurboQuantKVCache(_Cache):
                     "shape": list(e.shape), "index_bits": e.index_bits, "seed": e.seed}
         k, v = self.encoded_views()
         return rec(k), rec(v)
+
+    def write_pool(self, pool: "PagedPool", layer: int, slots, first: int = 0, n=None,
+                   stream=None):
+        """Write tokens [first, first + n) of the K/V update() returns (all of
+        them by default) into pool slots (device int32 [B * n]): the cache
+        as pool pages (vkv_turboquant_write_pool)."""
+        if n is None:
+            n = self.offset - first
+        if slots.dtype != _torch().int32 or not slots.is_contiguous() or slots.numel() < n:
+            raise VKVError("slots must be a contiguous int32 device tensor of B * n entries")
+        _chk(lib().vkv_turboquant_write_pool(self._h, pool._h, layer,
+                                             C.c_void_p(slots.data_ptr()), C.c_int64(first),
+                                             C.c_int64(n), stream_ptr(stream)))
 
     def window_state(self):
         k, v, p = Array(), Array(), C.c_int32()
