@@ -287,11 +287,27 @@ int vkv_cache_update(vkv_cache cache, const vkv_array *keys, const vkv_array *va
  * returns the whole cache as a paged view: the updated tuples in the paged
  * block format, which vkv_quantized_paged_sdpa (any query length, masks)
  * and vkv_paged_sdpa (one decode token) attend over directly.  The
- * reference-layout tuples themselves come from vkv_cache_state() (a
- * gather). */
+ * reference-layout tuples themselves come from
+ * vkv_cache_update_quantized_tuples (below). */
 int vkv_cache_update_quantized(vkv_cache cache, const vkv_array *keys,
                                const vkv_array *values, void *stream,
                                vkv_paged_view *out);
+
+/* updateQuantized(keys:values:) (KVCache.swift:1049-1122) with the
+ * reference's return value: out[6] receives the keys' (wq, scales, biases)
+ * then the values', each [B, Hkv, offset, *] in the reference layout
+ * (wq u32 [.., D * bits / 32], scales and biases in the K/V dtype [..,
+ * D / group]), views of cache-owned arrays whose dim(2) is the cache's
+ * capacity (the reference's keys.0.dim(2)).  The cache keeps them beside
+ * its paged store and brings them up to date from it for the tokens
+ * written since the previous call (a trim or a state setter included), so
+ * a decode step costs its new tokens, not the whole cache; when the
+ * capacity grows they are re-created and gathered whole, as the
+ * reference's arrays are.  The views stay valid until the next call that
+ * grows the cache.  The paged view (vkv_cache_update_quantized) is the
+ * same cache: both may be used on one cache. */
+int vkv_cache_update_quantized_tuples(vkv_cache cache, const vkv_array *keys,
+                                      const vkv_array *values, void *stream, vkv_array *out);
 
 /* The cache's class (VKV_CACHE_*): the dynamic type the reference's
  * savePromptCache switches on (KVCache.swift:1627-1646). */

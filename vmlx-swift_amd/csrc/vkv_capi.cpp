@@ -864,6 +864,21 @@ int vkv_cache_update_quantized(vkv_cache cache, const vkv_array* keys, const vkv
   });
 }
 
+int vkv_cache_update_quantized_tuples(vkv_cache cache, const vkv_array* keys,
+                                      const vkv_array* values, void* stream, vkv_array* out) {
+  return guard([&] {
+    need(cache, "cache");
+    need(keys, "keys");
+    need(values, "values");
+    need(out, "out");
+    auto* q = dynamic_cast<QuantizedCache*>(cache->impl.get());
+    if (!q) throw Error("updateQuantized needs a QuantizedKVCache");
+    vkv_paged_view view{};
+    q->update_quantized(*keys, *values, S(stream), &view);
+    q->tuples(S(stream), out);
+  });
+}
+
 int vkv_cache_kind(vkv_cache cache, int32_t* kind) {
   return guard([&] {
     need(cache, "cache");

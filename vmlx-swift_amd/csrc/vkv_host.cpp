@@ -1087,6 +1087,7 @@ void QuantizedCache::update_quantized(const vkv_array& k, const vkv_array& v, hi
   if (k.shape[3] != v.shape[3]) throw Error("QuantizedKVCache needs equal key and value head dims");
   const int64_t B = k.shape[0], H = k.shape[1], Sn = k.shape[2], D = k.shape[3];
   const int64_t prev = offset;
+  tup_valid_ = std::min(tup_valid_, prev);  // tokens from prev on are rewritten
   if (!store_.get() || prev + Sn > cap_) {
     const int64_t new_steps = ((step_ + Sn - 1) / step_) * step_;
     int64_t cap = new_steps;
@@ -1205,6 +1206,7 @@ void QuantizedCache::set_state(const vkv_array* a, int count, hipStream_t st) {
   const int64_t B = a[0].shape[0], H = a[0].shape[1], T = a[0].shape[2];
   const int64_t D = a[0].shape[3] * 32 / bits_;
   const int dtype = a[1].dtype;
+  tup_valid_ = 0;
   store_.release();
   table_.release();
   nblk_ = 0;
@@ -1229,6 +1231,68 @@ void QuantizedCache::set_state(const vkv_array* a, int count, hipStream_t st) {
     s.dst.table = static_cast<const int32_t*>(table_.get());
     s.dst.table_stride = static_cast<int32_t>(nblk_);
     launch_scatter_codes(s, st);
+  }
+}
+
+void QuantizedCache::tuples(hipStream_t st, vkv_array* out) {
+  if (!store_.get()) throw Error("nothing cached yet");
+  const int64_t T = std::min(offset, cap_);
+  const int64_t W = D_ * bits_ / 32, G = D_ / group_;
+  const int es = elem_bytes(dtype_);
+  const int64_t ws[3] = {W, G, G};
+  if (tup_B_ != B_ || tup_H_ != H_ || tup_D_ != D_ || tup_cap_ != cap_ || tup_dtype_ != dtype_) {
+    const int64_t eb[3] = {4, es, es};
+    for (int i = 0; i < 6; i++)
+      tup_[i].alloc(static_cast<size_t>(std::max<int64_t>(1, B_ * H_ * cap_ * ws[i % 3]) * eb[i % 3]));
+    tup_B_ = B_;
+    tup_H_ = H_;
+    tup_D_ = D_;
+    tup_cap_ = cap_;
+    tup_dtype_ = dtype_;
+    tup_valid_ = 0;
+  }
+  const int64_t t0 = std::min(tup_valid_, T);
+  if (T > t0) {
+    vkv_paged_view vw = view();
+    vw.max_len = static_cast<int32_t>(T);
+    const KVSrc kv = kvsrc_from_view(vw);
+    for (int which = 0; which < 2; which++) {
+      GatherArgs g{};
+      g.kv = kv;
+      g.n_seqs = static_cast<int32_t>(B_);
+      g.H = static_cast<int32_t>(H_);
+      g.T = static_cast<int32_t>(T - t0);
+      g.D = static_cast<int32_t>(D_);
+      g.which = which;
+      g.bits = bits_;
+      g.group = group_;
+      g.dtype = dtype_;
+      g.t_begin = static_cast<int32_t>(t0);
+      g.out_cap = static_cast<int32_t>(cap_);
+      g.out_t0 = static_cast<int32_t>(t0);
+      g.out = tup_[3 * which].get();
+      g.out_s = tup_[3 * which + 1].get();
+      g.out_b = tup_[3 * which + 2].get();
+      launch_gather(g, 1, st);
+    }
+  }
+  tup_valid_ = T;
+  const int dts[3] = {VKV_U32, dtype_, dtype_};
+  for (int i = 0; i < 6; i++) {
+    vkv_array& a = out[i];
+    const int64_t w = ws[i % 3];
+    a = vkv_array{};
+    a.data = tup_[i].get();
+    a.dtype = dts[i % 3];
+    a.ndim = 4;
+    a.shape[0] = B_;
+    a.shape[1] = H_;
+    a.shape[2] = T;
+    a.shape[3] = w;
+    a.strides[0] = H_ * cap_ * w;
+    a.strides[1] = cap_ * w;
+    a.strides[2] = w;
+    a.strides[3] = 1;
   }
 }
 

@@ -311,6 +311,17 @@ class QuantizedCache : public Cache {
   DevBuf table_;  // int32 [B][nblk_]
   DevBuf state_buf_[6];
   DevBuf kv_buf_[2];
+  // updateQuantized's return value (KVCache.swift:1049-1122): the keys'
+  // and values' (wq, scales, biases) in the reference layout, [B][H][cap]
+  // rows beside the paged store, brought up to date from the store for the
+  // tokens written since the last call (tup_valid_ tokens already match);
+  // out receives [B, H, offset, *] views of them.  They move (and are
+  // gathered whole once) when the capacity grows, as the reference's arrays
+  // are re-created then.
+  void tuples(hipStream_t st, vkv_array* out);
+  DevBuf tup_[6];
+  int64_t tup_B_ = 0, tup_H_ = 0, tup_D_ = 0, tup_cap_ = 0, tup_valid_ = 0;
+  int tup_dtype_ = -1;
 };
 
 class Pool {

@@ -167,6 +167,8 @@ struct GatherArgs {
   void* out_b;
   void* out_v;      // values (out_kind 0): non-null gathers K into out and V
                     //   into out_v in one call (which is then ignored)
+  int32_t out_cap;  // codes (out_kind 1): tokens per (seq, head) row of the
+  int32_t out_t0;   //   outputs (0 = T) and the output token of gathered token 0
 };
 void launch_gather(const GatherArgs& g, int out_kind, hipStream_t st);
 // Strided 4-D copy (element size 2 or 4): dst[i] = src[i].

@@ -378,7 +378,9 @@ __global__ void __launch_bounds__(256) gather_kernel(GatherArgs g) {
     uint32_t code[8];
     float s = 0.0f, b = 0.0f;
     for (int i = 0; i < 8; i++) code[i] = qcode<DT, BITS>(g.kv, l, h, d0 + i, g.which, g.group, &s, &b);
-    uint32_t* wq = static_cast<uint32_t*>(g.out) + row * (g.D * BITS / 32);
+    // (the output row: token out_t0 + t of rows out_cap tokens long)
+    const int64_t orow = (row / g.T) * (g.out_cap ? g.out_cap : g.T) + g.out_t0 + t;
+    uint32_t* wq = static_cast<uint32_t*>(g.out) + orow * (g.D * BITS / 32);
     if constexpr (BITS == 4) {
       uint32_t w = 0;
       for (int i = 0; i < 8; i++) w |= code[i] << (4 * i);
@@ -391,8 +393,8 @@ __global__ void __launch_bounds__(256) gather_kernel(GatherArgs g) {
       // s and b of the group holding dims [d0, d0+8) (exact stored values)
       const int G = g.D / g.group;
       const int gi = d0 / g.group;
-      static_cast<typename E::T*>(g.out_s)[row * G + gi] = E::from_f32(s);
-      static_cast<typename E::T*>(g.out_b)[row * G + gi] = E::from_f32(b);
+      static_cast<typename E::T*>(g.out_s)[orow * G + gi] = E::from_f32(s);
+      static_cast<typename E::T*>(g.out_b)[orow * G + gi] = E::from_f32(b);
     }
   }
 }

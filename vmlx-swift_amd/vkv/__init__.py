@@ -106,7 +106,7 @@ EXPORTS = (
     "vkv_turboquant_has_compressible_middle", "vkv_turboquant_info", "vkv_turboquant_encoded",
     "vkv_turboquant_window", "vkv_turboquant_restore_compressed",
     "vkv_turboquant_restore_decoded", "vkv_tq_tables", "vkv_set_option", "vkv_get_option",
-    "vkv_turboquant_write_pool",
+    "vkv_turboquant_write_pool", "vkv_cache_update_quantized_tuples",
 )
 TIME_DECODE, TIME_MLA, TIME_FDECODE, TIME_TQ_ENCODE, TIME_TQ_DECODE = 0, 1, 2, 3, 4
 
@@ -633,6 +633,16 @@ class QuantizedKVCache(_Cache):
         _chk(lib().vkv_cache_update_quantized(self._h, C.byref(arr(keys)), C.byref(arr(values)),
                                               stream_ptr(stream), C.byref(v)))
         return v
+
+    def update_quantized_tuples(self, keys, values, stream=None):
+        """updateQuantized(keys:values:) -> ((wq, scales, biases), (wq,
+        scales, biases)) as library-owned [B, H, offset, *] views
+        (vkv_cache_update_quantized_tuples; to_torch materializes one)."""
+        out = (Array * 6)()
+        _chk(lib().vkv_cache_update_quantized_tuples(self._h, C.byref(arr(keys)),
+                                                     C.byref(arr(values)), stream_ptr(stream),
+                                                     out))
+        return (out[0], out[1], out[2]), (out[3], out[4], out[5])
 
     def to_unquantized(self):
         h = C.c_void_p()
