@@ -316,6 +316,20 @@ __device__ __forceinline__ uint32_t pack_el(float a, float b) {
   else
     return pack_bf16(a, b);
 }
+// Two fp32 values rounded to the cache dtype (to nearest even): bf16
+// through one v_cvt_pk_bf16_f32 (the software rounding takes about six
+// instructions a value).
+template <int DT>
+__device__ __forceinline__ void round2(float& a, float& b) {
+  if constexpr (DT == kBF16) {
+    const uint32_t w = pack_bf16(a, b);
+    a = bf_lo(w);
+    b = bf_hi(w);
+  } else {
+    a = round_to<DT>(a);
+    b = round_to<DT>(b);
+  }
+}
 template <int DT>
 __device__ __forceinline__ uint32_t out_el(float x) {
   if constexpr (DT == kF16) return f32_to_f16(x);
@@ -770,8 +784,9 @@ qdecode_kernel(DecodeArgs a) {
       float v[8];
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        v[2 * e] = round_to<DT>(el_lo<DT>(qr[c][e]) * scale_t);
-        v[2 * e + 1] = round_to<DT>(el_hi<DT>(qr[c][e]) * scale_t);
+        v[2 * e] = el_lo<DT>(qr[c][e]) * scale_t;
+        v[2 * e + 1] = el_hi<DT>(qr[c][e]) * scale_t;
+        round2<DT>(v[2 * e], v[2 * e + 1]);
       }
       const bool live = ci < QCH && r < nh;
       float sum = 0.0f;
@@ -883,13 +898,21 @@ qdecode_kernel(DecodeArgs a) {
           const uint32_t wd = b.wt[tau][i & 1];
           sc[tau][i] = (i >> 1) ? bf_hi(wd) : bf_lo(wd);
         } else {
-          // the reference stores the scores in the query dtype before the
-          // softmax (quantizedMM returns T, KVCache.swift:1945-1949)
-          sc[tau][i] = round_to<DT>(s);
+          sc[tau][i] = s;
         }
       }
+    if constexpr (MODE != kModeWeights) {
+      // the reference stores the scores in the query dtype before the
+      // softmax (quantizedMM returns T, KVCache.swift:1945-1949)
+#pragma unroll
+      for (int tau = 0; tau < TT; tau++) {
+        round2<DT>(sc[tau][0], sc[tau][1]);
+        round2<DT>(sc[tau][2], sc[tau][3]);
+      }
+    }
     if (stp * 64 + 64 > len) {  // the sequence ends inside this step
-      asm volatile("");  // a real branch: keeps the masking off the common path
+      // a real branch: the masked values leave through the asm statements,
+      // so the selects cannot be hoisted onto the common path
 #pragma unroll
       for (int tau = 0; tau < TT; tau++) {
         const int c = tau * PP + p, s = c >> 1, q = c & 1;
@@ -897,10 +920,12 @@ qdecode_kernel(DecodeArgs a) {
         for (int i = 0; i < 4; i++) {
           const bool ok = stp * 64 + 32 * s + 8 * lg + tok_off<BITS>(q, i) < len;
           sc[tau][i] = ok ? sc[tau][i] : (MODE == kModeWeights ? 0.0f : -INFINITY);
+          asm volatile("" : "+v"(sc[tau][i]));
 #pragma unroll
           for (int g = 0; g < G; g++) {
             vs[tau][i][g] = ok ? vs[tau][i][g] : 0.0f;
             vb[tau][i][g] = ok ? vb[tau][i][g] : 0.0f;
+            asm volatile("" : "+v"(vs[tau][i][g]), "+v"(vb[tau][i][g]));
           }
         }
       }
