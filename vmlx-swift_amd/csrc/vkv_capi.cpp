@@ -156,6 +156,14 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
       float* ws = workspace(st, per * (a.Dv + 2), noalloc);
       a.ws_o = ws;
       a.ws_ml = ws + per * a.Dv;
+      // the merge inside the decode launch where the last part's merge is
+      // small (config 1, 18 parts x 128 dims x 4 heads: step 19.4 -> 17.8
+      // us); larger ones keep the separate merge (config 4's window layer,
+      // 32 parts x 256 dims x 2 heads: 19.9 us with it, 25.1 inside), as
+      // does the no-allocation path, which has no counters
+      if (!noalloc && fdecode_merge_here(a.n_parts, a.Dv, a.Hq, a.Hkv))
+        a.counters = attention_counters(st, static_cast<size_t>(rows) *
+                                                fdecode_counter_count(a.Hq, a.Hkv));
     }
     launch_fdecode(dtype, a, rows, st);
     return;

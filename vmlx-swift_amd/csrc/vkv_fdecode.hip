@@ -24,6 +24,17 @@
 // No matrix cores: at REP <= 8 query heads per kv head the contraction is
 // ~1 FMA per KV byte, well under the vector ALUs' rate, so the kernel runs
 // at the memory's pace.
+//
+// Split merge.  With counters (one per (row, kv head, head group)) the
+// parts merge inside the launch: each part stores its (o, max, sum)
+// partial with device-coherent stores (relaxed agent-scope atomics, which
+// write through to the level every XCD reads), waits for them to complete,
+// and counts itself in; the part that counts last reads every partial back
+// with device-coherent loads, merges them as sdpa_vector_2pass_2 does and
+// writes the output, then zeroes the counter for the next launch.  No
+// fence writes back or invalidates an L2, and a part has no loads in
+// flight when it waits for its stores.  Without counters the partials go
+// to attn_combine_kernel (a launch of its own).
 #include <algorithm>
 
 #include "vkv_device.h"
@@ -81,6 +92,11 @@ __device__ __forceinline__ float add_xor32(float v) {
   return lo + hi;
 }
 
+// Two floats as one 64-bit word (first in the low half).
+__device__ __forceinline__ uint64_t pack_f2(float lo, float hi) {
+  return static_cast<uint64_t>(__float_as_uint(lo)) | (static_cast<uint64_t>(__float_as_uint(hi)) << 32);
+}
+
 // Maximum / sum within each half-wave of 32 lanes: pairs 1 and 2 apart
 // (quad permutes), then each lane with its mirror in 8 and in 16 lanes (the
 // partners hold equal values by then, so the mirror acts as a butterfly),
@@ -98,6 +114,72 @@ __device__ __forceinline__ float half_sumf(float x) {
   x += dpp_mov<0x141>(x);
   x += dpp_mov<0x140>(x);
   return x + swz_xor<16>(x);
+}
+
+// The in-launch merge of a (row, kv head, head group)'s parts
+// (sdpa_vector.h:320-394), by the part that counted in last: the partials
+// come back through device-coherent loads; all 64 lanes take D / 64 dims of
+// a head each and issue every part's loads of the head together, one round
+// trip per head.
+template <int DT, int D, int REP>
+__device__ __forceinline__ void fdecode_merge_rows(const AttnArgs& a, int64_t b, int h0, int nh,
+                                                   int lane) {
+  using E = Elem<DT>;
+  constexpr int DPL = D / 64;  // dims per lane: 1, 2 or 4
+  constexpr int kMaxP = 32;    // parts per round trip
+  for (int r = 0; r < nh; r++) {
+    const int h = h0 + r;
+    const int64_t rh = b * a.Hq + h;
+    const float* mlp = a.ws_ml + rh * a.n_parts * 2;
+    const float* wo = a.ws_o + rh * a.n_parts * D + DPL * lane;
+    float M = -3.402823466e38f, den = 0.0f, acc[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; e++) acc[e] = 0.0f;
+    for (int c = 0; c < a.n_parts; c += kMaxP) {
+      float mj[kMaxP], lj[kMaxP], vj[kMaxP][DPL];
+#pragma unroll
+      for (int j = 0; j < kMaxP; j++) {
+        const int pp = min(c + j, a.n_parts - 1);  // (clamped slots are selected away)
+        const uint64_t w = __hip_atomic_load(reinterpret_cast<const uint64_t*>(mlp) + pp,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        mj[j] = __uint_as_float(static_cast<uint32_t>(w));
+        lj[j] = __uint_as_float(static_cast<uint32_t>(w >> 32));
+        const float* src = wo + static_cast<int64_t>(pp) * D;
+        if constexpr (DPL == 1) {
+          vj[j][0] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+#pragma unroll
+          for (int e = 0; e < DPL / 2; e++) {
+            const uint64_t x = __hip_atomic_load(reinterpret_cast<const uint64_t*>(src) + e,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            vj[j][2 * e] = __uint_as_float(static_cast<uint32_t>(x));
+            vj[j][2 * e + 1] = __uint_as_float(static_cast<uint32_t>(x >> 32));
+          }
+        }
+      }
+      float Mc = M;
+#pragma unroll
+      for (int j = 0; j < kMaxP; j++)
+        if (c + j < a.n_parts) Mc = fmaxf(Mc, mj[j]);
+      const float rsc = __expf(M - Mc);
+      den *= rsc;
+#pragma unroll
+      for (int e = 0; e < DPL; e++) acc[e] *= rsc;
+      M = Mc;
+#pragma unroll
+      for (int j = 0; j < kMaxP; j++) {
+        if (c + j < a.n_parts) {
+          const float w = __expf(mj[j] - M);
+          den += w * lj[j];
+#pragma unroll
+          for (int e = 0; e < DPL; e++) acc[e] = fmaf(w, vj[j][e], acc[e]);
+        }
+      }
+    }
+    typename E::T* out = static_cast<typename E::T*>(a.out) + b * a.o_sb + h * a.o_sh + DPL * lane;
+#pragma unroll
+    for (int e = 0; e < DPL; e++) out[e] = E::from_f32(den > 0.0f ? acc[e] / den : 0.0f);
+  }
 }
 
 template <int DT, int D, int REP>
@@ -286,28 +368,52 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
       if constexpr (LPR <= 16) o[r][e] += swz_xor<16>(o[r][e]);
       if constexpr (LPR <= 32) o[r][e] = add_xor32(o[r][e]);
     }
-  if (rs != 0) return;
+  const bool merge_here = a.n_parts > 1 && a.counters;
+  if (rs == 0) {
 #pragma unroll
-  for (int r = 0; r < REP; r++) {
-    if (r >= nh) break;
-    const int h = h0 + r;
-    const int d0 = VEC * dg;
-    if (a.n_parts == 1) {
-      const float inv = l[r] > 0.0f ? 1.0f / l[r] : 0.0f;
-      typename E::T* out = static_cast<typename E::T*>(a.out) + b * a.o_sb + h * a.o_sh + d0;
+    for (int r = 0; r < REP; r++) {
+      if (r >= nh) break;
+      const int h = h0 + r;
+      const int d0 = VEC * dg;
+      if (a.n_parts == 1) {
+        const float inv = l[r] > 0.0f ? 1.0f / l[r] : 0.0f;
+        typename E::T* out = static_cast<typename E::T*>(a.out) + b * a.o_sb + h * a.o_sh + d0;
 #pragma unroll
-      for (int e = 0; e < VEC; e++) out[e] = E::from_f32(o[r][e] * inv);
-    } else {
-      const int64_t base = (b * a.Hq + h) * a.n_parts + part;
-      float* wo = a.ws_o + base * D + d0;
+        for (int e = 0; e < VEC; e++) out[e] = E::from_f32(o[r][e] * inv);
+      } else if (merge_here) {
+        const int64_t base = (b * a.Hq + h) * a.n_parts + part;
+        uint64_t* wo = reinterpret_cast<uint64_t*>(a.ws_o + base * D + d0);
 #pragma unroll
-      for (int e = 0; e < VEC; e++) wo[e] = o[r][e];
-      if (dg == 0) {
-        a.ws_ml[base * 2] = m[r];
-        a.ws_ml[base * 2 + 1] = l[r];
+        for (int e = 0; e < VEC / 2; e++)
+          __hip_atomic_store(wo + e, pack_f2(o[r][2 * e], o[r][2 * e + 1]), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        if (dg == 0)
+          __hip_atomic_store(reinterpret_cast<uint64_t*>(a.ws_ml + base * 2), pack_f2(m[r], l[r]),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        const int64_t base = (b * a.Hq + h) * a.n_parts + part;
+        float* wo = a.ws_o + base * D + d0;
+#pragma unroll
+        for (int e = 0; e < VEC; e++) wo[e] = o[r][e];
+        if (dg == 0) {
+          a.ws_ml[base * 2] = m[r];
+          a.ws_ml[base * 2 + 1] = l[r];
+        }
       }
     }
   }
+  if (!merge_here) return;
+  // this part's partial stores are complete before it counts itself in
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  uint32_t* cnt = a.counters + (b * a.Hkv + hk) * n_hg + hg;
+  uint32_t before = 0;
+  if (lane == 0) before = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  before = __builtin_amdgcn_readfirstlane(before);
+  if (before != static_cast<uint32_t>(a.n_parts - 1)) return;
+  // the last part merges every part of the group's heads, then zeroes the
+  // counter for the next launch
+  if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  fdecode_merge_rows<DT, D, REP>(a, b, h0, nh, lane);
 }
 
 template <int DT, int D>
@@ -375,7 +481,23 @@ void launch_fdecode(int dtype, const AttnArgs& a, int64_t rows, hipStream_t st) 
     case kBF16: launch_dt<kBF16>(b, rows, st); break;
     default: throw Error("unsupported dtype");
   }
-  if (b.n_parts > 1) launch_attn_combine(dtype, b, rows, st);
+  if (b.n_parts > 1 && !b.counters) launch_attn_combine(dtype, b, rows, st);
+}
+
+static int fdecode_heads_per_group(int Hq, int Hkv) {
+  const int rep = Hq / Hkv;
+  return rep <= 1 ? 1 : rep <= 2 ? 2 : rep <= 4 ? 4 : 8;
+}
+
+int fdecode_counter_count(int Hq, int Hkv) {
+  const int rep = Hq / Hkv, R = fdecode_heads_per_group(Hq, Hkv);
+  return Hkv * ((rep + R - 1) / R);
+}
+
+bool fdecode_merge_here(int n_parts, int Dv, int Hq, int Hkv) {
+  // partial floats the last part of a head group reads back
+  constexpr int64_t kMaxMergeFloats = 12288;
+  return static_cast<int64_t>(n_parts) * Dv * fdecode_heads_per_group(Hq, Hkv) <= kMaxMergeFloats;
 }
 
 }  // namespace vkv

@@ -1919,6 +1919,7 @@ namespace {
 struct StreamWorkspace {
   DevBuf cur;
   std::vector<DevBuf> retired;
+  DevBuf counters;
 };
 std::mutex& ws_mutex() {
   static std::mutex mu;
@@ -1947,11 +1948,28 @@ float* attention_workspace(hipStream_t st, size_t floats) {
   return static_cast<float*>(w.cur.get());
 }
 
+uint32_t* attention_counters(hipStream_t st, size_t n) {
+  std::lock_guard<std::mutex> g(ws_mutex());
+  StreamWorkspace& w = ws_map()[st];
+  if (w.counters.size() < n * sizeof(uint32_t)) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    VKV_HIP(hipStreamIsCapturing(st, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+      throw Error("the attention counters of this stream must grow during HIP graph capture: "
+                  "run the same call once before capturing");
+    const size_t want = std::max(n * sizeof(uint32_t), std::max<size_t>(w.counters.size() * 2, 4096));
+    if (w.counters.size()) w.retired.push_back(std::move(w.counters));
+    w.counters.alloc(want);
+    VKV_HIP(hipMemsetAsync(w.counters.get(), 0, want, st));
+  }
+  return static_cast<uint32_t*>(w.counters.get());
+}
+
 size_t workspace_release(hipStream_t st) {
   std::lock_guard<std::mutex> g(ws_mutex());
   auto it = ws_map().find(st);
   if (it == ws_map().end()) return 0;
-  size_t n = it->second.cur.size();
+  size_t n = it->second.cur.size() + it->second.counters.size();
   for (auto& b : it->second.retired) n += b.size();
   ws_map().erase(it);  // hipFree waits for the device
   return n;

@@ -400,6 +400,11 @@ class PrefixManager {
 // them) until workspace_release(st), which frees them all and returns the
 // bytes released.  Growth during graph capture on `st` is an error.
 float* attention_workspace(hipStream_t st, size_t floats);
+// At least n zeroed uint32 counters of the stream, for kernels that count
+// arrivals and zero their counters again before they end (zeroed once, on
+// the stream, when the buffer is allocated or grown; growth during HIP
+// graph capture is refused like the workspace's).
+uint32_t* attention_counters(hipStream_t st, size_t n);
 size_t workspace_release(hipStream_t st);
 
 // TurboQuantKVCache (TurboQuant/TurboQuantKVCache.swift:70-671), in

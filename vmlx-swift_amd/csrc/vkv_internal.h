@@ -113,6 +113,10 @@ struct AttnArgs {
   const uint8_t* nk_ptr;
   const uint8_t* nv_ptr;
   int64_t nk_sb, nk_sh, nv_sb, nv_sh;
+  // float decode only: one zeroed counter per (batch row, kv head, head
+  // group); non-null merges the split partials inside the decode launch
+  // (the last part of a row merges, then zeroes its counter again)
+  uint32_t* counters;
 };
 
 // Quantized attention with the reference's arithmetic (vkv_refattn.hip):
@@ -202,6 +206,10 @@ void launch_prefill(int dtype, bool qsem, const AttnArgs& a, int64_t batch, hipS
 bool fdecode_supported(int dtype, int bits, bool qsem, const AttnArgs& a);
 int fdecode_parts(int64_t rows_x_heads, int64_t T, int32_t* part_tokens, int waves);
 void launch_fdecode(int dtype, const AttnArgs& a, int64_t rows, hipStream_t st);
+// counters per batch row the float decode's in-launch merge uses, and
+// whether a launch merges inside (a small merge) or in attn_combine_kernel
+int fdecode_counter_count(int Hq, int Hkv);
+bool fdecode_merge_here(int n_parts, int Dv, int Hq, int Hkv);
 // MFMA decode attention over paged affine bf16 KV (vkv_decode.hip).
 struct DecodeArgs {
   const uint16_t* q;         // [n_seqs][Hq][D] bf16 / f16
