@@ -1,6 +1,7 @@
 """Benchmark: paged 4-bit KV decode attention + KV append (config 3).
 
-Workload ("Paged continuous batching"): a pool of
+Workload ("Paged continuous batching", the configuration the headline metric is
+quoted on): a pool of
 16384 blocks x 32 tokens per layer, bf16 inputs stored affine 4-bit g64,
 8 KV heads x 128 dims; 64 sequences with lengths U[128, 8192] whose block
 tables are random permutations of pool ids; 32 sequences share one
@@ -18,7 +19,7 @@ its launch stream), "traffic" is the PMC-measured HBM bytes per decode launch,
 "cpu_baseline" times the C oracle, "prefill" times a 512-token chunked-prefill
 attention step over a 4-bit cache, and "mla" is the MLA latent decode workload
 (32 x 16384 tokens, 128 heads) with the MFMA roofline of its attention kernel.
-"configs" measures the other BASELINE workloads at their stated shapes, each
+"configs" measures the other benchmark workloads at their stated shapes, each
 with the roofline of its decode kernel: config 1 (KVCacheSimple fp16 decode
 steps), config 2 (QuantizedKVCache, 32 layers x batch 8 x 4096 tokens, 4 and
 8 bits) and config 4 (5 sliding-window + 1 global 8-bit layer at 32768).
