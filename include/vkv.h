@@ -536,7 +536,9 @@ int vkv_pool_view(vkv_pool pool, int32_t layer, const int32_t *block_table,
 /* Scatter new tokens into pool blocks (quantizing on the way for affine
  * pools).  keys [N,Hkv,D], values [N,Hkv,Dv] (strided; a [1,H,T,D] cache
  * array is passed as [T,H,D] with strides {D, T*D, 1}); slot_mapping
- * device int32 [N], slot = block_id * block_size + offset_in_block.  Replaces
+ * device int32 [N], slot = block_id * block_size + offset_in_block (a
+ * negative slot, or one at or past num_blocks * block_size, skips its token
+ * rather than writing outside the pool).  Replaces
  * the reference's per-sequence slice assignment (KVCache.swift:498-502,
  * :1105-1116) and block split (CacheCoordinator.swift:1238-1272).  Quantized
  * codes, scales and biases are bit-exact with the reference quantizer. */

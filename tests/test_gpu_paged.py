@@ -258,7 +258,8 @@ def test_decode_wave_counts_agree(monkeypatch, waves):
 def test_append_aligned_groups_ragged_and_scattered_slots():
     """One append call mixing an 8-aligned prefill run (V words assembled in
     LDS), a run starting mid-group, single tokens scattered over blocks
-    (nibbles merged atomically) and a skipped token (slot -1); the gathered
+    (nibbles merged atomically) and skipped tokens (slot -1, and slots past
+    the pool's last block, which must not be written); the gathered
     codes are bit-exact with the oracle quantizer, and tokens already in
     the touched words survive."""
     dtype, bits, bs, H, D = O.BF16, 4, 32, 4, 128
@@ -272,7 +273,7 @@ def test_append_aligned_groups_ragged_and_scattered_slots():
     slots = [ta[p // bs] * bs + p % bs for p in range(41)]
     slots += [tb[0] * bs + p for p in range(3, 22)]
     singles = [4 * bs + 5, 5 * bs + 5, 6 * bs + 5, 7 * bs + 5]
-    slots += singles + [-1]
+    slots += singles + [-1, nblocks * bs + 3, 2 ** 30]
     n = len(slots)
     k = rand_bits(rng, (n, H, D), dtype, outliers=2)
     v = rand_bits(rng, (n, H, D), dtype, outliers=2)

@@ -1443,6 +1443,7 @@ void Pool::append(int layer, const vkv_array& k, const vkv_array* v, const int32
     RowDst dv = keys_only ? dk : affine_dst(base, block_bytes, head_bytes, p.block_size, L, 1, G, false);
     dk.slots = slots;
     dv.slots = slots;
+    dk.slot_limit = dv.slot_limit = static_cast<int64_t>(p.num_blocks) * p.block_size;
     launch_append_affine(p.dtype, p.bits, p.group_size, sk, sv, dk, dv, n, p.n_kv_heads, p.head_dim,
                          !keys_only, st);
     return;
@@ -1454,6 +1455,7 @@ void Pool::append(int layer, const vkv_array& k, const vkv_array* v, const int32
     RowDst dst = affine_dst(base, block_bytes, head_bytes, p.block_size, L, which,
                             p.bits ? p.head_dim / p.group_size : 0, keys_only);
     dst.slots = slots;
+    dst.slot_limit = static_cast<int64_t>(p.num_blocks) * p.block_size;
     if (p.bits == 0) {
       launch_copy_rows(p.dtype, 1, src, dst, n * a.shape[1], static_cast<int>(a.shape[2]), st);
     } else {

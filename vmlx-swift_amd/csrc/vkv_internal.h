@@ -53,10 +53,12 @@ struct RowDst {
   int32_t G;                 // affine: groups per row
   int32_t keys_only;         // affine: chunk holds keys only (MLA latent)
   // slot of token n (n = row / e2 for paged rows ordered (token, head)):
-  const int32_t* slots;      // explicit [N] (slot = block*bs + offset), or
+  const int32_t* slots;      // explicit [N] (slot = block*bs + offset; slots at
+                             //   or past slot_limit, when set, are skipped), or
   const int32_t* table;      // block table [e0][table_stride] with
   int32_t table_stride;      //   token n -> (b = n / seq_S, pos = start + n % seq_S)
   int32_t seq_S, start;
+  int64_t slot_limit;        // explicit slots: the pool's slot count (0 = unchecked)
 };
 
 // One component (codes, scales, biases, or float values) of K or V.

@@ -25,9 +25,13 @@ __device__ __forceinline__ const uint8_t* row_ptr(const RowSrc& s, int64_t row, 
   return static_cast<const uint8_t*>(s.ptr) + (i0 * s.s0 + i1 * s.s1 + i2 * s.s2) * esize;
 }
 
-// Slot (block * block_size + offset) of paged token n; < 0 means skip.
+// Slot (block * block_size + offset) of paged token n; < 0 means skip (so
+// does an explicit slot past the pool, which would write outside it).
 __device__ __forceinline__ int64_t token_slot(const RowDst& d, int64_t n) {
-  if (d.slots) return d.slots[n];
+  if (d.slots) {
+    const int64_t s = d.slots[n];
+    return (d.slot_limit > 0 && s >= d.slot_limit) ? -1 : s;
+  }
   int64_t b = n / d.seq_S;
   int64_t pos = d.start + n % d.seq_S;
   int32_t blk = d.table[b * d.table_stride + pos / d.block_size];
