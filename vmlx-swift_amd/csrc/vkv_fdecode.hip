@@ -10,8 +10,17 @@
 //
 // Layout.  One wave per workgroup owns a (row, kv head, head group, token
 // range) and walks it 32 tokens at a time:
-//   * scores: lanes t and t + 32 own token t, each taking half of its key
-//     row with 16-byte loads (every byte of a row used), against the
+//   * scores, bf16 / f16 K/V: on matrix cores, S^T (16 tokens x 16 columns,
+//     the group's REP <= 8 heads) = K (A operands: lane (m, g) loads dims
+//     32 s + 8 g .. + 7 of token m of a 16-token tile, 16 bytes straight
+//     from memory) . Q^T (B operands: the raw queries in registers), one
+//     16x16x32 MFMA per tile and 32 dims; the fp32 scores are then scaled
+//     (the reference scales the queries first: the same fp32 arithmetic up
+//     to summation order).  The max and sum of a head reduce over the four
+//     lanes that hold it and reach every lane through readlane (config 4's
+//     window layer: 16.0 -> 12.1 us; config 1's step 17.8 -> 16.1 us);
+//   * scores, f32 K/V: lanes t and t + 32 own token t, each taking half of
+//     its key row with 16-byte loads (every byte of a row used), against the
 //     queries of the group's REP heads in LDS; one lane swap adds the
 //     halves.  Two lanes per token give a launch twice the waves of one
 //     lane per token for the same bytes (a 33.6 MB D = 256 decode: 14.9 ->
@@ -21,9 +30,9 @@
 //   * values: lanes own 16-byte runs of a value row, D/8 (bf16/f16) or D/4
 //     (f32) lanes per row, so every load instruction reads whole rows;
 //     the lanes that share a run sum their tokens at the end.
-// No matrix cores: at REP <= 8 query heads per kv head the contraction is
-// ~1 FMA per KV byte, well under the vector ALUs' rate, so the kernel runs
-// at the memory's pace.
+// The value contraction stays on the vector ALUs (at REP <= 8 query heads
+// per kv head about one FMA per KV byte); on matrix cores its value rows
+// would have to be transposed through LDS.
 //
 // Split merge.  With counters (one per (row, kv head, head group)) the
 // parts merge inside the launch: each part stores its (o, max, sum)
@@ -46,7 +55,21 @@ namespace vkv {
 namespace {
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(1))) const u32x4_t g_u32x4_t;
+
+// 16x16x32 MFMA on 16-bit operands of the cache dtype
+template <int DT>
+__device__ __forceinline__ f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+  if constexpr (DT == kF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
 
 // Tokens per step: two lanes per token, each scoring half of the dims.
 constexpr int kStep = 32;
@@ -191,7 +214,13 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
   constexpr int RPI = 64 / LPR;        // value rows per load instruction
   static_assert(LPR <= 64 && 64 % LPR == 0, "value rows must tile a wave");
   static_assert(KL % 2 == 0 && kStep % RPI == 0, "key rows split in two halves, value rows tile a step");
-  __shared__ float qs[REP][D];
+  // bf16 / f16 K/V: the scores on matrix cores (S^T = K . Q^T, 16 tokens x
+  // 16 columns of heads per MFMA, the raw queries as B operands, the scale
+  // applied to the fp32 scores); f32 K/V: on the vector ALUs
+  constexpr bool MF = DT != kF32;
+  constexpr int KS = D / 32;  // 32-dim K steps of a key row
+  static_assert(!MF || 2 * KS == KL / 2, "the key operands reuse the key-load registers");
+  __shared__ float qs[MF ? 1 : REP][MF ? 1 : D];
   __shared__ float ps[REP][kStep];
 
   const int lane = threadIdx.x;
@@ -228,11 +257,25 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
   const bool writes_new = new_t >= t_begin && new_t < t_end && hg == 0;
   const uint8_t* nkrow = a.has_new ? a.nk_ptr + b * a.nk_sb + hk * a.nk_sh : kbase;
   const uint8_t* nvrow = a.has_new ? a.nv_ptr + b * a.nv_sb + hk * a.nv_sh : vbase;
+  // matrix-core layout: lane (mrow, kgrp) loads dims 32 s + 8 kgrp .. + 7 of
+  // token t0 + 16 T + mrow into kw[T KS + s] (the A operand of step s, tile T)
+  const int mrow = lane & 15, kgrp = lane >> 4;
   auto load_k = [&](int64_t t0) __attribute__((always_inline)) {
-    const int64_t t = t0 + tok < t_end ? t0 + tok : t_begin;
-    const uint8_t* krow = (t == new_t ? nkrow : kbase + t * kst) + 16 * (KL / 2) * half;
+    if constexpr (MF) {
 #pragma unroll
-    for (int c = 0; c < KL / 2; c++) kw[c] = *(g_u32x4_t*)(krow + 16 * c);
+      for (int T = 0; T < 2; T++) {
+        const int64_t tt = t0 + 16 * T + mrow;
+        const int64_t t = tt < t_end ? tt : t_begin;
+        const uint8_t* krow = (t == new_t ? nkrow : kbase + t * kst) + 16 * kgrp;
+#pragma unroll
+        for (int st = 0; st < KS; st++) kw[T * KS + st] = *(g_u32x4_t*)(krow + 64 * st);
+      }
+    } else {
+      const int64_t t = t0 + tok < t_end ? t0 + tok : t_begin;
+      const uint8_t* krow = (t == new_t ? nkrow : kbase + t * kst) + 16 * (KL / 2) * half;
+#pragma unroll
+      for (int c = 0; c < KL / 2; c++) kw[c] = *(g_u32x4_t*)(krow + 16 * c);
+    }
   };
   auto load_v = [&](int64_t t0) __attribute__((always_inline)) {
 #pragma unroll
@@ -244,24 +287,40 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
 
   // the queries (times the scale) go to LDS; their loads go out first,
   // then the first step's key and value loads, so both latencies overlap
-  constexpr int NQ = REP * D / 64;
+  constexpr int NQ = MF ? 1 : REP * D / 64;
   float qv[NQ];
+  u32x4_t qb[MF ? KS : 1];  // matrix-core B operands: head mrow, dims 32 s + 8 kgrp .. + 7
+  if constexpr (MF) {
+    const uint16_t* qp = static_cast<const uint16_t*>(a.q) + b * a.q_sb +
+                         static_cast<int64_t>(h0 + min(mrow, nh - 1)) * a.q_sh + 8 * kgrp;
 #pragma unroll
-  for (int j = 0; j < NQ; j++) {
-    const int i = lane + 64 * j, r = i / D, d = i % D;
-    qv[j] = r < nh ? E::load(static_cast<const typename E::T*>(a.q) + b * a.q_sb + (h0 + r) * a.q_sh + d)
-                   : 0.0f;
+    for (int st = 0; st < KS; st++) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t lo = qp[32 * st + 2 * e], hi = qp[32 * st + 2 * e + 1];
+        qb[st][e] = mrow < nh ? (lo | (hi << 16)) : 0u;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NQ; j++) {
+      const int i = lane + 64 * j, r = i / D, d = i % D;
+      qv[j] = r < nh ? E::load(static_cast<const typename E::T*>(a.q) + b * a.q_sb + (h0 + r) * a.q_sh + d)
+                     : 0.0f;
+    }
   }
   if (t_begin < t_end) {
     load_k(t_begin);
     if constexpr (kVEarly) load_v(t_begin);
   }
+  if constexpr (!MF) {
 #pragma unroll
-  for (int j = 0; j < NQ; j++) {
-    const int i = lane + 64 * j;
-    qs[i / D][i % D] = qv[j] * a.scale;
+    for (int j = 0; j < NQ; j++) {
+      const int i = lane + 64 * j;
+      qs[i / D][i % D] = qv[j] * a.scale;
+    }
+    __syncthreads();
   }
-  __syncthreads();
   float m[REP], l[REP], o[REP][VEC];
 #pragma unroll
   for (int r = 0; r < REP; r++) {
@@ -287,6 +346,83 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
       load_k(t0);
       if constexpr (kVEarly) load_v(t0);
     }
+    if constexpr (MF) {
+      // ---- scores on matrix cores: lane (mrow, kgrp) ends with head mrow
+      // of tokens t0 + 16 T + 4 kgrp + i
+      f32x4_t acc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int st = 0; st < KS; st++)
+#pragma unroll
+        for (int T = 0; T < 2; T++) acc[T] = mfma16<DT>(kw[T * KS + st], qb[st], acc[T]);
+      if constexpr (!kVEarly) load_v(t0);
+      if (writes_new) {  // the new token's key row into the cache
+#pragma unroll
+        for (int T = 0; T < 2; T++) {
+          if (t0 + 16 * T + mrow == new_t) {
+            uint8_t* dst = const_cast<uint8_t*>(kbase) + new_t * kst + 16 * kgrp;
+#pragma unroll
+            for (int st = 0; st < KS; st++) *reinterpret_cast<u32x4_t*>(dst + 64 * st) = kw[T * KS + st];
+          }
+        }
+      }
+      float sc[2][4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int T = 0; T < 2; T++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int64_t t = t0 + 16 * T + 4 * kgrp + i;
+          float x = acc[T][i] * a.scale;
+          bool vis = t < t_end && mrow < nh;
+          if (vis && a.mask_mode >= 2) {
+            const int64_t mo = b * a.m_sb + (h0 + mrow) * a.m_sh + t * a.m_st;
+            if (a.mask_mode == 2) {
+              vis = static_cast<const uint8_t*>(a.mask)[mo] != 0;
+            } else {
+              // the mask in the query dtype; keys below its lowest finite
+              // value are skipped (sdpa_vector.h:105-121)
+              const float add = load_as<DT>(a.mask, a.mask_dtype, mo);
+              vis = add >= -E::kMax;
+              x += add;
+            }
+          }
+          sc[T][i] = vis ? x : -INFINITY;
+          mx = fmaxf(mx, sc[T][i]);
+        }
+      // the step's max of head mrow over its four lanes, then the new
+      // running max (this lane's head)
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      float m_own = m[0];
+#pragma unroll
+      for (int r = 1; r < REP; r++) m_own = mrow == r ? m[r] : m_own;
+      const float mn_own = fmaxf(m_own, mx);
+      float psum = 0.0f;
+#pragma unroll
+      for (int T = 0; T < 2; T++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float pr = (mn_own == -INFINITY || sc[T][i] == -INFINITY) ? 0.0f
+                                                                         : __expf(sc[T][i] - mn_own);
+          psum += pr;
+          if (mrow < REP) ps[mrow][16 * T + 4 * kgrp + i] = pr;
+        }
+      psum += __shfl_xor(psum, 16);
+      psum += __shfl_xor(psum, 32);
+      // ---- online softmax per head (sdpa_vector.h:116-131): lane r holds
+      // head r's new max and step sum
+#pragma unroll
+      for (int r = 0; r < REP; r++) {
+        const float mn = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mn_own), r));
+        const float ls = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, psum), r));
+        float alpha = 1.0f;
+        if (mn != -INFINITY) alpha = m[r] == -INFINITY ? 0.0f : __expf(m[r] - mn);
+        l[r] = l[r] * alpha + ls;
+        m[r] = mn;
+#pragma unroll
+        for (int e = 0; e < VEC; e++) o[r][e] *= alpha;
+      }
+    } else {
     float s[REP];
 #pragma unroll
     for (int r = 0; r < REP; r++) s[r] = 0.0f;
@@ -340,6 +476,7 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
       if (half == 0) ps[r][tok] = p;
 #pragma unroll
       for (int e = 0; e < VEC; e++) o[r][e] *= alpha;
+    }
     }
     __syncthreads();
 #pragma unroll
