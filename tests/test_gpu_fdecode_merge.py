@@ -1,10 +1,12 @@
 """The float decode's split merge (sdpa_vector_2pass_2, sdpa_vector.h:
-320-394) on both of its paths: inside the decode launch (the part that
-counts in last merges through device-coherent loads and zeroes its counter
-again) where the merge is small, and in attn_combine_kernel otherwise.
-Each path is checked against the oracle's float SDPA over several calls in
-a row (the counters must be back at zero after every launch) and under HIP
-graph replay (the counters reset inside the graph, no memset recorded)."""
+320-394) on its three paths: in LDS where one workgroup owns a whole (row,
+kv head, head group) (small bf16 / f16 launches), inside the decode launch
+(the part that counts in last merges through device-coherent loads and
+zeroes its counter again) where the merge is small, and in
+attn_combine_kernel otherwise.  Each path is checked against the oracle's
+float SDPA over several calls in a row (the counters must be back at zero
+after every launch) and under HIP graph replay (the counters reset inside
+the graph, no memset recorded)."""
 import numpy as np
 import pytest
 import torch
@@ -15,11 +17,16 @@ from gpu_util import assert_within, attn_tol, dev, rand_bits, values
 
 pytestmark = pytest.mark.gpu
 
-# (B, Hkv, Hq, T, D, dtype): 18 parts x 128 dims x 4 heads merges inside;
-# 32 parts x 256 dims x 2 heads in the merge launch; one head per group
-# (rep 1) and 8 heads per group (rep 8) inside
+# (B, Hkv, Hq, T, D, dtype): 8 waves of a workgroup (one query head each
+# at this size) merging in LDS; 32 parts x 256 dims x 2 heads in the merge
+# launch; 8 heads per group (no workgroup form at 128 dims) merging inside
+# the launch; the workgroup form at 64 dims, with parts fewer than waves;
+# f32 merging inside the launch; the workgroup form of larger launches,
+# which keeps the 8 / 4 heads of a kv head together
 SHAPES = [(2, 4, 16, 576, 128, O.BF16), (4, 8, 16, 1024, 256, O.BF16),
-          (1, 8, 8, 700, 64, O.F16), (2, 2, 16, 300, 128, O.F32)]
+          (2, 2, 16, 576, 128, O.BF16), (1, 8, 8, 100, 64, O.F16),
+          (2, 2, 16, 300, 128, O.F32), (24, 4, 32, 64, 64, O.BF16),
+          (40, 4, 16, 96, 128, O.F16)]
 
 
 def _ref(q, k, v, dtype, scale):
@@ -43,7 +50,7 @@ def test_decode_calls_in_a_row(shape):
         assert_within(values(out, dtype), ref, attn_tol(dtype, ref), f"call {call}")
 
 
-@pytest.mark.parametrize("shape", SHAPES[:2], ids=["merge_inside", "merge_launch"])
+@pytest.mark.parametrize("shape", SHAPES[:3], ids=["workgroup", "merge_launch", "merge_inside"])
 def test_decode_under_graph_replay(shape):
     B, Hkv, Hq, T, D, dtype = shape
     rng = np.random.default_rng(1600 + D)

@@ -149,6 +149,16 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
     return;
   }
   if (fdecode_supported(dtype, bits, qsem, a) && !option(VKV_OPTION_GENERIC_ATTENTION)) {
+    // a small launch: one workgroup per (row, head group), merged in LDS
+    // (the fdecode_waves option, a tuning override, keeps the split launch)
+    a.wg_parts = option(VKV_OPTION_FDECODE_WAVES)
+                     ? 0
+                     : fdecode_wg_parts(rows, a.Hq, a.Hkv, max_len, a.D, dtype, &a.part_tokens);
+    if (a.wg_parts > 0) {
+      a.n_parts = a.wg_parts;
+      launch_fdecode(dtype, a, rows, st);
+      return;
+    }
     a.n_parts = fdecode_parts(rows * a.Hkv, max_len, &a.part_tokens,
                               static_cast<int>(option(VKV_OPTION_FDECODE_WAVES)));
     if (a.n_parts > 1) {
@@ -157,7 +167,7 @@ void run_attention(int dtype, int bits, int group, bool qsem, AttnArgs& a, int64
       a.ws_o = ws;
       a.ws_ml = ws + per * a.Dv;
       // the merge inside the decode launch where the last part's merge is
-      // small (config 1, 18 parts x 128 dims x 4 heads: step 19.4 -> 17.8
+      // small (18 parts x 128 dims x 4 heads, one f16 row: step 19.4 -> 17.8
       // us); larger ones keep the separate merge (config 4's window layer,
       // 32 parts x 256 dims x 2 heads: 19.9 us with it, 25.1 inside), as
       // does the no-allocation path, which has no counters

@@ -139,6 +139,31 @@ __device__ __forceinline__ float half_sumf(float x) {
   return x + swz_xor<16>(x);
 }
 
+// Orders a wave's LDS writes before its other lanes' reads (the LDS data
+// of a workgroup of several waves is per wave, so no workgroup barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// Waves of a workgroup that owns a whole (row, kv head, head group) and
+// merges its parts in LDS: up to 8 (two per SIMD: the kernel needs ~240
+// registers a wave, and 16 waves would leave it 128, spilling), with the
+// partials (REP x D floats a wave) within 48 KB.
+template <int D, int REP>
+constexpr int fd_wg_waves() {
+  constexpr int n = 49152 / (REP * D * 4);
+  return n > 8 ? 8 : (n < 2 ? 2 : n);
+}
+// The shapes whose 8-wave workgroup fits its registers without spilling:
+// bf16 / f16 (matrix-core scores) at 64 dims, or 128 dims and at most 4
+// heads per group.
+template <int DT, int D, int REP>
+constexpr bool fd_wg_ok() {
+  return DT != kF32 && (D == 64 || (D == 128 && REP <= 4));
+}
+
 // The in-launch merge of a (row, kv head, head group)'s parts
 // (sdpa_vector.h:320-394), by the part that counted in last: the partials
 // come back through device-coherent loads; all 64 lanes take D / 64 dims of
@@ -205,8 +230,8 @@ __device__ __forceinline__ void fdecode_merge_rows(const AttnArgs& a, int64_t b,
   }
 }
 
-template <int DT, int D, int REP>
-__global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) {
+template <int DT, int D, int REP, int NW = 1>
+__global__ void __launch_bounds__(64 * NW) fdecode_kernel(AttnArgs a, int rep_total) {
   using E = Elem<DT>;
   constexpr int VEC = 16 / E::kBytes;  // elements per 16-byte load
   constexpr int KL = D / VEC;          // loads per key row
@@ -220,11 +245,20 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
   constexpr bool MF = DT != kF32;
   constexpr int KS = D / 32;  // 32-dim K steps of a key row
   static_assert(!MF || 2 * KS == KL / 2, "the key operands reuse the key-load registers");
-  __shared__ float qs[MF ? 1 : REP][MF ? 1 : D];
-  __shared__ float ps[REP][kStep];
+  // (NW > 1: a workgroup of NW waves owns the whole row, wave w its part
+  // w, and merges the parts in LDS at the end; each wave's LDS is its own)
+  __shared__ float qs_g[NW][MF ? 1 : REP][MF ? 1 : D];
+  __shared__ float ps_g[NW][REP][kStep];
+  const int wv = NW > 1 ? static_cast<int>(threadIdx.x >> 6) : 0;
+  float(*qs)[MF ? 1 : D] = qs_g[wv];
+  float(*ps)[kStep] = ps_g[wv];
+  auto step_sync = [&]() __attribute__((always_inline)) {
+    if constexpr (NW > 1) wave_lds_sync();
+    else __syncthreads();
+  };
 
-  const int lane = threadIdx.x;
-  const int part = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int part = static_cast<int>(blockIdx.x) * NW + wv;
   const int n_hg = (rep_total + REP - 1) / REP;
   const int hk = blockIdx.y / n_hg, hg = blockIdx.y % n_hg;
   const int64_t b = blockIdx.z;
@@ -319,7 +353,7 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
       const int i = lane + 64 * j;
       qs[i / D][i % D] = qv[j] * a.scale;
     }
-    __syncthreads();
+    step_sync();
   }
   float m[REP], l[REP], o[REP][VEC];
 #pragma unroll
@@ -478,7 +512,7 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
       for (int e = 0; e < VEC; e++) o[r][e] *= alpha;
     }
     }
-    __syncthreads();
+    step_sync();
 #pragma unroll
     for (int k = 0; k < NV; k++) {
       const int tt = rs + RPI * k;
@@ -493,7 +527,7 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
         for (int e = 0; e < VEC; e++) o[r][e] = fmaf(p, vv[e], o[r][e]);
       }
     }
-    __syncthreads();
+    step_sync();
   }
 
   // the row slots of a run hold disjoint tokens: sum them
@@ -505,6 +539,40 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
       if constexpr (LPR <= 16) o[r][e] += swz_xor<16>(o[r][e]);
       if constexpr (LPR <= 32) o[r][e] = add_xor32(o[r][e]);
     }
+  if constexpr (NW > 1) {
+    // ---- the workgroup's parts merge in LDS (sdpa_vector.h:320-394): each
+    // wave's (o, max, sum) per head, then every thread one (head, dim)
+    __shared__ float mo_g[NW][REP][D];
+    __shared__ float ml_g[NW][REP][2];
+    if (rs == 0) {
+#pragma unroll
+      for (int r = 0; r < REP; r++) {
+#pragma unroll
+        for (int e = 0; e < VEC; e++) mo_g[wv][r][VEC * dg + e] = o[r][e];
+        if (dg == 0) {
+          ml_g[wv][r][0] = m[r];
+          ml_g[wv][r][1] = l[r];
+        }
+      }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < nh * D; idx += 64 * NW) {
+      const int r = idx / D, d = idx % D;
+      float M = -3.402823466e38f;
+#pragma unroll
+      for (int w = 0; w < NW; w++) M = fmaxf(M, ml_g[w][r][0]);
+      float den = 0.0f, acc = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; w++) {
+        const float f = __expf(ml_g[w][r][0] - M);
+        den = fmaf(f, ml_g[w][r][1], den);
+        acc = fmaf(f, mo_g[w][r][d], acc);
+      }
+      typename E::T* out = static_cast<typename E::T*>(a.out) + b * a.o_sb + (h0 + r) * a.o_sh + d;
+      *out = E::from_f32(den > 0.0f ? acc / den : 0.0f);
+    }
+    return;
+  }
   const bool merge_here = a.n_parts > 1 && a.counters;
   if (rs == 0) {
 #pragma unroll
@@ -553,23 +621,48 @@ __global__ void __launch_bounds__(64) fdecode_kernel(AttnArgs a, int rep_total) 
   fdecode_merge_rows<DT, D, REP>(a, b, h0, nh, lane);
 }
 
+template <int DT, int D, int R>
+void launch_r(const AttnArgs& a, int64_t rows, int rep, int n_hg, hipStream_t st) {
+  const TimedLaunch tl = timing_prepare(kTimeFDecode);
+  if (a.wg_parts > 0) {
+    // one workgroup per (row, kv head, head group), its parts merged in LDS
+    if constexpr (fd_wg_ok<DT, D, R>()) {
+      constexpr int NW = fd_wg_waves<D, R>();
+      VKV_CHECK(a.wg_parts <= NW && a.n_parts == a.wg_parts, "workgroup parts");
+      const dim3 grid(1, a.Hkv * n_hg, static_cast<unsigned>(rows));
+      hipExtLaunchKernelGGL((fdecode_kernel<DT, D, R, NW>), grid, dim3(64 * NW), 0, st, tl.start,
+                            tl.stop, 0, a, rep);
+    } else {
+      throw Error("no workgroup float decode for this shape");
+    }
+  } else {
+    const dim3 grid(a.n_parts, a.Hkv * n_hg, static_cast<unsigned>(rows));
+    hipExtLaunchKernelGGL((fdecode_kernel<DT, D, R>), grid, dim3(64), 0, st, tl.start, tl.stop, 0,
+                          a, rep);
+  }
+  VKV_HIP(hipGetLastError());
+  timing_commit(tl);
+}
+
+// Query heads a wave takes (its head group): all of a kv head's, up to 8,
+// so that each key row is read once for them.  The workgroup form of a
+// launch of at most 512 (row, query head)s takes one head a workgroup: the
+// launch then has 4-8x the workgroups, each reading its K/V from L2 (config
+// 1, one row of 8 kv heads x 4: kernel 13.0 us at four heads, 10.2 at one).
+int fd_group_heads(int64_t rows, int Hkv, int rep, bool wg) {
+  if (wg && rows * Hkv * rep <= 512) return 1;
+  return rep <= 1 ? 1 : rep <= 2 ? 2 : rep <= 4 ? 4 : 8;
+}
+
 template <int DT, int D>
 void launch_d(const AttnArgs& a, int64_t rows, hipStream_t st) {
   const int rep = a.Hq / a.Hkv;
-  const int R = rep <= 1 ? 1 : rep <= 2 ? 2 : rep <= 4 ? 4 : 8;
+  const int R = fd_group_heads(rows, a.Hkv, rep, a.wg_parts > 0);
   const int n_hg = (rep + R - 1) / R;
-  const dim3 grid(a.n_parts, a.Hkv * n_hg, static_cast<unsigned>(rows));
-  const TimedLaunch tl = timing_prepare(kTimeFDecode);
-  if (R == 1)
-    hipExtLaunchKernelGGL((fdecode_kernel<DT, D, 1>), grid, dim3(64), 0, st, tl.start, tl.stop, 0, a, rep);
-  else if (R == 2)
-    hipExtLaunchKernelGGL((fdecode_kernel<DT, D, 2>), grid, dim3(64), 0, st, tl.start, tl.stop, 0, a, rep);
-  else if (R == 4)
-    hipExtLaunchKernelGGL((fdecode_kernel<DT, D, 4>), grid, dim3(64), 0, st, tl.start, tl.stop, 0, a, rep);
-  else
-    hipExtLaunchKernelGGL((fdecode_kernel<DT, D, 8>), grid, dim3(64), 0, st, tl.start, tl.stop, 0, a, rep);
-  VKV_HIP(hipGetLastError());
-  timing_commit(tl);
+  if (R == 1) launch_r<DT, D, 1>(a, rows, rep, n_hg, st);
+  else if (R == 2) launch_r<DT, D, 2>(a, rows, rep, n_hg, st);
+  else if (R == 4) launch_r<DT, D, 4>(a, rows, rep, n_hg, st);
+  else launch_r<DT, D, 8>(a, rows, rep, n_hg, st);
 }
 
 template <int DT>
@@ -607,6 +700,29 @@ int fdecode_parts(int64_t rows_x_heads, int64_t T, int32_t* part_tokens, int wav
   return static_cast<int>(std::max<int64_t>(1, (T + pt - 1) / pt));
 }
 
+int fdecode_wg_parts(int64_t rows, int Hq, int Hkv, int64_t T, int D, int dtype,
+                     int32_t* part_tokens) {
+  // launches of at most kWgBytes of K/V: few (row, head group)s whose parts
+  // the global merge would cost more than they save
+  constexpr int64_t kWgBytes = int64_t{8} << 20;
+  if (rows * Hkv * T * D * 2 * elem_bytes(dtype) > kWgBytes) return 0;
+  const int R = fd_group_heads(rows, Hkv, Hq / Hkv, true);
+  if (dtype == kF32 || !(D == 64 || (D == 128 && R <= 4))) return 0;  // fd_wg_ok
+  int nw = 8;
+  switch (D * 8 + R) {  // fd_wg_waves<D, R>()
+#define VKV_WG(DD, RR) case DD * 8 + RR: nw = fd_wg_waves<DD, RR>(); break;
+    VKV_WG(64, 1) VKV_WG(64, 2) VKV_WG(64, 4) VKV_WG(64, 8)
+    VKV_WG(128, 1) VKV_WG(128, 2) VKV_WG(128, 4)
+#undef VKV_WG
+    default: return 0;
+  }
+  const int64_t steps = std::max<int64_t>(1, (T + kStep - 1) / kStep);
+  const int64_t parts = std::min<int64_t>(nw, steps);
+  const int64_t pt = (steps + parts - 1) / parts * kStep;
+  *part_tokens = static_cast<int32_t>(pt);
+  return static_cast<int>((std::max<int64_t>(T, 1) + pt - 1) / pt);
+}
+
 void launch_fdecode(int dtype, const AttnArgs& a, int64_t rows, hipStream_t st) {
   if (rows <= 0) return;
   // a causal mask leaves one query token every key
@@ -618,7 +734,7 @@ void launch_fdecode(int dtype, const AttnArgs& a, int64_t rows, hipStream_t st) 
     case kBF16: launch_dt<kBF16>(b, rows, st); break;
     default: throw Error("unsupported dtype");
   }
-  if (b.n_parts > 1 && !b.counters) launch_attn_combine(dtype, b, rows, st);
+  if (b.n_parts > 1 && !b.counters && b.wg_parts == 0) launch_attn_combine(dtype, b, rows, st);
 }
 
 static int fdecode_heads_per_group(int Hq, int Hkv) {

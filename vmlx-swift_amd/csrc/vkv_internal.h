@@ -119,6 +119,9 @@ struct AttnArgs {
   // group); non-null merges the split partials inside the decode launch
   // (the last part of a row merges, then zeroes its counter again)
   uint32_t* counters;
+  // float decode only: > 0 = the launch is one workgroup of wg_parts waves
+  // per (row, kv head, head group) (n_parts == wg_parts), merged in LDS
+  int32_t wg_parts;
 };
 
 // Quantized attention with the reference's arithmetic (vkv_refattn.hip):
@@ -212,6 +215,9 @@ void launch_fdecode(int dtype, const AttnArgs& a, int64_t rows, hipStream_t st);
 // whether a launch merges inside (a small merge) or in attn_combine_kernel
 int fdecode_counter_count(int Hq, int Hkv);
 bool fdecode_merge_here(int n_parts, int Dv, int Hq, int Hkv);
+// parts of a workgroup-per-row launch (0: not a small launch), and their tokens
+int fdecode_wg_parts(int64_t rows, int Hq, int Hkv, int64_t T, int D, int dtype,
+                     int32_t* part_tokens);
 // MFMA decode attention over paged affine bf16 KV (vkv_decode.hip).
 struct DecodeArgs {
   const uint16_t* q;         // [n_seqs][Hq][D] bf16 / f16

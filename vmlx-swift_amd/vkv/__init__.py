@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import struct
 from typing import Optional, Sequence
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -37,6 +38,13 @@ class VKVError(RuntimeError):
 class Array(C.Structure):
     _fields_ = [("data", C.c_void_p), ("dtype", C.c_int32), ("ndim", C.c_int32),
                 ("shape", C.c_int64 * 4), ("strides", C.c_int64 * 4)]
+
+
+# the bytes of an Array (data, dtype, ndim, shape[4], strides[4]): one pack
+# and one copy build a descriptor about 3x faster than field assignments,
+# which dominate a decode step's host time at small shapes
+_ARRAY_BYTES = struct.Struct("<qii4q4q")
+assert _ARRAY_BYTES.size == C.sizeof(Array)
 
 
 class PagedView(C.Structure):
@@ -141,23 +149,26 @@ def _torch():
     return torch
 
 
+_DTYPE_CODES = {}
+
+
 def _dtype_code(t) -> int:
-    torch = _torch()
-    m = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.int32: I32,
-         torch.uint8: U8, torch.bool: BOOL}
-    return m[t.dtype]
+    if not _DTYPE_CODES:
+        torch = _torch()
+        _DTYPE_CODES.update({torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16,
+                             torch.int32: I32, torch.uint8: U8, torch.bool: BOOL})
+    return _DTYPE_CODES[t.dtype]
 
 
 def arr(t, dtype: Optional[int] = None) -> Array:
     """vkv_array describing a torch tensor (no copy)."""
-    a = Array()
-    a.data = t.data_ptr() if t.numel() else None
-    a.dtype = _dtype_code(t) if dtype is None else dtype
-    a.ndim = t.dim()
-    for i in range(t.dim()):
-        a.shape[i] = t.shape[i]
-        a.strides[i] = t.stride(i)
-    return a
+    nd = t.dim()
+    if nd > 4:
+        raise ValueError(f"arrays have at most 4 dims, got {nd}")
+    pad = (0,) * (4 - nd)
+    return Array.from_buffer_copy(_ARRAY_BYTES.pack(
+        t.data_ptr() if t.numel() else 0, _dtype_code(t) if dtype is None else dtype, nd,
+        *t.shape, *pad, *t.stride(), *pad))
 
 
 def _torch_dtype(code):
