@@ -618,6 +618,12 @@ void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_a
       const size_t sc_floats = ref ? static_cast<size_t>(chunk) * d.Hq * d.sc_stride / 2 : 0;
       d.ws = workspace(S(stream), (part_floats + 63) / 64 * 64 + sc_floats, noalloc);
       d.sc = ref ? reinterpret_cast<uint16_t*>(d.ws + (part_floats + 63) / 64 * 64) : nullptr;
+      // counters of the merge inside the launch, where the launch takes it
+      // (the no-allocation entry point has none: its partials merge in the
+      // separate launch, with the same arithmetic)
+      if (!noalloc && !ref && kv->head_dim <= 128)
+        d.counters = attention_counters(S(stream), static_cast<size_t>(chunk) * kv->n_kv_heads *
+                                                       qdecode_head_groups(rep));
       launch_qdecode(d, kv->bits, kv->head_dim, S(stream), ref);
       return;
     }

@@ -50,18 +50,22 @@
 // equal contiguous range of cost units, so mixed sequence lengths cost no
 // load imbalance.  A range crosses a few (sequence, head) segments; at each
 // boundary the wave finalizes the segment (the output itself when the
-// segment covers the whole sequence, else an (o, max, sum) partial that
-// qdecode_combine_kernel merges, as sdpa_vector_2pass_2 merges) and rebuilds
-// its wave-local query table.  The next unit's KV loads are in flight while
-// the current unit computes, and the next segment's queries while the
-// current segment does.  Up to 128 dims a workgroup is the 8 waves of one
-// CU (two per SIMD), and the two waves of a SIMD trade instruction-issue
-// priority so that neither finishes long before the other.  (Merging the
-// partials in the kernel, by the wave that counts a pair's last partial,
-// measured slower than the separate merge launch: with agent-coherent
-// stores the count must wait for every load in flight, and with
-// device-scope fences each partial writes back and invalidates the XCD's
-// L2.)
+// segment covers the whole sequence, else an (o, max, sum) partial, merged
+// as sdpa_vector_2pass_2 merges) and rebuilds its wave-local query table.
+// The next unit's KV loads are in flight while the current unit computes,
+// and the next segment's queries while the current segment does.  Up to 128
+// dims a workgroup is the 8 waves of one CU (two per SIMD), and the two
+// waves of a SIMD trade instruction-issue priority so that neither finishes
+// long before the other.
+//
+// Merge.  Where the host passes counters, the partials merge inside the
+// launch: a wave stores its partials with agent-coherent stores and counts
+// them in on per-pair counters only at its range's end (a count right after
+// the stores would wait for every prefetch in flight), and the wave that
+// counts a pair's last partial merges it (device-scope fences instead of
+// coherent stores would write back and invalidate the XCD's L2 per
+// partial).  Otherwise qdecode_combine_kernel merges, in a launch of its
+// own, through the same merge step.
 #include <algorithm>
 #include <mutex>
 #include <string>
@@ -334,6 +338,88 @@ template <int DT>
 __device__ __forceinline__ uint32_t out_el(float x) {
   if constexpr (DT == kF16) return f32_to_f16(x);
   else return f32_to_bf16(x);
+}
+
+// One step of the split-K merge (sdpa_vector.h:320-394) over N partials of
+// an element: the running (M, L, o) rescaled to the new max, then each live
+// partial added with its weight.  qdecode_combine_kernel and the in-launch
+// merge both take their partials through this in groups of 4, so the two
+// paths round alike (the no-allocation entry point, which has no counters,
+// merges in the separate launch and must equal the allocating one).
+template <int N, int E>
+__device__ __forceinline__ void qmerge_step(float& M, float& L, float (&o)[E], int k0, int K,
+                                            const float (&mlm)[N], const float (&mll)[N],
+                                            const float (&oo)[N][E]) {
+  float mm[N];
+  float Mn = M;
+#pragma unroll
+  for (int q = 0; q < N; q++) {
+    mm[q] = k0 + q < K ? mlm[q] : -INFINITY;
+    Mn = fmaxf(Mn, mm[q]);
+  }
+  const float f = M == -INFINITY ? 0.0f : exp2f((M - Mn) * kLog2e);
+  L *= f;
+#pragma unroll
+  for (int e = 0; e < E; e++) o[e] *= f;
+#pragma unroll
+  for (int q = 0; q < N; q++) {
+    // stale slots: weight 0, and their (possibly non-finite) values are
+    // selected away rather than multiplied by it
+    const bool live = mm[q] != -INFINITY;
+    const float w = live ? exp2f((mm[q] - Mn) * kLog2e) : 0.0f;
+    L = fmaf(w, live ? mll[q] : 0.0f, L);
+#pragma unroll
+    for (int e = 0; e < E; e++) o[e] = fmaf(w, live ? oo[q][e] : 0.0f, o[e]);
+  }
+  M = Mn;
+}
+
+// The in-launch merge of a (sequence, head pair)'s K partials by the wave
+// that counted in last: the partials come back through device-coherent
+// loads (they were stored the same way), 4 partials a round trip; lane l
+// takes head l / (64 / HP) and D * HP / 64 of its dims.
+template <int HP, int D, int DT>
+__device__ __forceinline__ void qdecode_merge_pair(const DecodeArgs& a, int pair, int K, int lane) {
+  constexpr int LPH = 64 / HP, EPL = D / LPH, kQuad = 4;
+  static_assert(EPL % 4 == 0, "4-element output stores");
+  const int rep = a.rep, n_hg = (rep + HP - 1) / HP, HG = a.Hkv * n_hg;
+  const int seq = pair / HG, j = pair % HG;
+  const int64_t hq0 = static_cast<int64_t>(j / n_hg) * rep + (j % n_hg) * HP;
+  const int nh = min(HP, rep - (j % n_hg) * HP);
+  const int r = lane / LPH, d0 = (lane % LPH) * EPL;
+  const int64_t slot0 = static_cast<int64_t>(pair) * a.max_parts;
+  float M = -INFINITY, L = 0.0f, o[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; e++) o[e] = 0.0f;
+  for (int k0 = 0; k0 < K; k0 += kQuad) {
+    float mlm[kQuad], mll[kQuad], oo[kQuad][EPL];
+#pragma unroll
+    for (int q = 0; q < kQuad; q++) {
+      const int64_t slot = (slot0 + min(k0 + q, K - 1)) * HP + r;
+      const uint64_t ml = __hip_atomic_load(reinterpret_cast<const uint64_t*>(a.ws_ml) + slot,
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      mlm[q] = __uint_as_float(static_cast<uint32_t>(ml));
+      mll[q] = __uint_as_float(static_cast<uint32_t>(ml >> 32));
+      const uint64_t* src = reinterpret_cast<const uint64_t*>(a.ws_o + slot * D + d0);
+#pragma unroll
+      for (int e = 0; e < EPL / 2; e++) {
+        const uint64_t x = __hip_atomic_load(src + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        oo[q][2 * e] = __uint_as_float(static_cast<uint32_t>(x));
+        oo[q][2 * e + 1] = __uint_as_float(static_cast<uint32_t>(x >> 32));
+      }
+    }
+    qmerge_step<kQuad, EPL>(M, L, o, k0, K, mlm, mll, oo);
+  }
+  if (r >= nh) return;
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  uint16_t* dst = a.out + seq * a.o_ss + (hq0 + r) * a.o_sh + d0;
+#pragma unroll
+  for (int e = 0; e < EPL; e += 4) {
+    u32x2_t v;
+    v[0] = out_el<DT>(o[e] * inv) | (out_el<DT>(o[e + 1] * inv) << 16);
+    v[1] = out_el<DT>(o[e + 2] * inv) | (out_el<DT>(o[e + 3] * inv) << 16);
+    *reinterpret_cast<u32x2_t*>(dst + e) = v;
+  }
 }
 
 // Orders one wave's LDS writes before its later LDS reads by other lanes
@@ -762,6 +848,11 @@ qdecode_kernel(DecodeArgs a) {
   // ---- segment state
   int k = 0;             // current segment
   int seg_seq = 0, seg_j = 0, seg_t = 0, seg_take = 0, seg_len = 0, seg_first = 0, seg_pa = 0, nh = 0;
+  // in-launch merge: the (pair, partial count) of the partials this wave
+  // counts in at its end, at most two (only a range's first and last
+  // segments can be parts of a pair)
+  int pend_pair0 = -1, pend_k0 = 0, pend_pair1 = -1, pend_k1 = 0;
+  const bool merge_here = MODE == kModeFused && D <= 128 && a.counters != nullptr;
   float sq[G];
   // query table of segment kk from its prefetched chunks: entry (slice sg,
   // column nn, unit slot ws) holds unit sg * SPW + ws of head nn % HP in the
@@ -1094,6 +1185,22 @@ qdecode_kernel(DecodeArgs a) {
           v[1] = out_el<DT>((oacc[t][2] + cg) * inv) | (out_el<DT>((oacc[t][3] + cg) * inv) << 16);
           *reinterpret_cast<u32x2_t*>(o + 16 * t) = v;
         }
+      } else if (merge_here) {
+        // device-coherent stores (written through to the level every XCD
+        // reads), for the wave that merges the pair
+        const int64_t slot = pair * a.max_parts + (w - wa);
+        uint64_t* o = reinterpret_cast<uint64_t*>(a.ws_o + (slot * HP + n) * D + 4 * lg);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+          const float cg = csum[t / (NT / G)];
+          __hip_atomic_store(o + 8 * t, pack_f2(oacc[t][0] + cg, oacc[t][1] + cg),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(o + 8 * t + 1, pack_f2(oacc[t][2] + cg, oacc[t][3] + cg),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (lg == 0)
+          __hip_atomic_store(reinterpret_cast<uint64_t*>(a.ws_ml) + slot * HP + n,
+                             pack_f2(m_run, lsum), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       } else {
         const int64_t slot = pair * a.max_parts + (w - wa);
         float* o = a.ws_o + (slot * HP + n) * D + 4 * lg;
@@ -1109,6 +1216,15 @@ qdecode_kernel(DecodeArgs a) {
           a.ws_ml[(slot * HP + n) * 2] = MODE == kModeWeights ? 0.0f : m_run;
           a.ws_ml[(slot * HP + n) * 2 + 1] = MODE == kModeWeights ? (w == wa ? 1.0f : 0.0f) : lsum;
         }
+      }
+    }
+    if (merge_here && !whole) {
+      if (pend_pair0 < 0) {
+        pend_pair0 = static_cast<int>(pair);
+        pend_k0 = wb - wa + 1;
+      } else {
+        pend_pair1 = static_cast<int>(pair);
+        pend_k1 = wb - wa + 1;
       }
     }
     // the next segment's first step refreshes the max from -inf, which
@@ -1201,6 +1317,25 @@ qdecode_kernel(DecodeArgs a) {
       load_step(ui + 1, bufA);
     }
   }
+  if (pend_pair0 >= 0) {
+    // Counted in at the range's end, where no loads are left to wait for:
+    // this wave's partial stores are complete first.  The wave that counts
+    // a pair's last partial zeroes the counter for the next launch and
+    // merges the pair.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    auto count_in = [&](int pair, int K) __attribute__((always_inline)) {
+      uint32_t before = 0;
+      if (lane == 0)
+        before = __hip_atomic_fetch_add(a.counters + pair, 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+      before = __builtin_amdgcn_readfirstlane(before);
+      if (before != static_cast<uint32_t>(K - 1)) return;
+      if (lane == 0) __hip_atomic_store(a.counters + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      qdecode_merge_pair<HP, D, DT>(a, pair, K, lane);
+    };
+    count_in(pend_pair0, pend_k0);
+    if (pend_pair1 >= 0) count_in(pend_pair1, pend_k1);
+  }
 }
 
 // Merge of the partials of (sequence, head pair)s that several waves
@@ -1229,32 +1364,18 @@ __global__ void __launch_bounds__(512) qdecode_combine_kernel(DecodeArgs a, int 
   const int64_t slot0 = static_cast<int64_t>(P) * a.max_parts;
   const int r = threadIdx.x / (D / 4), d = 4 * (threadIdx.x % (D / 4));
   if (r >= HP) return;
-  float M = -INFINITY, L = 0.0f;
-  f32x4_t o = {0.f, 0.f, 0.f, 0.f};
+  float M = -INFINITY, L = 0.0f, o[4] = {0.f, 0.f, 0.f, 0.f};
   auto merge = [&](int k0, auto N_, const f32x2_t* ml, const f32x4_t* oo) __attribute__((always_inline)) {
     constexpr int N = decltype(N_)::value;
-    float mm[N];
-    float Mn = M;
+    float mlm[N], mll[N], ov[N][4];
 #pragma unroll
     for (int q = 0; q < N; q++) {
-      mm[q] = k0 + q < K ? ml[q][0] : -INFINITY;
-      Mn = fmaxf(Mn, mm[q]);
+      mlm[q] = ml[q][0];
+      mll[q] = ml[q][1];
+#pragma unroll
+      for (int e = 0; e < 4; e++) ov[q][e] = oo[q][e];
     }
-    const float f = M == -INFINITY ? 0.0f : exp2f((M - Mn) * kLog2e);
-    L *= f;
-#pragma unroll
-    for (int e = 0; e < 4; e++) o[e] *= f;
-#pragma unroll
-    for (int q = 0; q < N; q++) {
-      // stale slots: weight 0, and their (possibly non-finite) values are
-      // selected away rather than multiplied by it
-      const bool live = mm[q] != -INFINITY;
-      const float w = live ? exp2f((mm[q] - Mn) * kLog2e) : 0.0f;
-      L = fmaf(w, live ? ml[q][1] : 0.0f, L);
-#pragma unroll
-      for (int e = 0; e < 4; e++) o[e] = fmaf(w, live ? oo[q][e] : 0.0f, o[e]);
-    }
-    M = Mn;
+    qmerge_step<N, 4>(M, L, o, k0, K, mlm, mll, ov);
   };
   // slots k0 .. k0 + N - 1 (clamped to the last live one), loaded together
   auto load = [&](int k0, auto N_, f32x2_t* ml, f32x4_t* oo) __attribute__((always_inline)) {
@@ -1390,11 +1511,17 @@ float* decode_scratch(size_t floats) {
 int qdecode_max_len() { return 1 << 24; }
 
 template <int BITS, int D, int HP, int DT>
-static void launch_hp(const DecodeArgs& a, bool ref, hipStream_t st) {
+static void launch_hp(const DecodeArgs& a0, bool ref, hipStream_t st) {
   constexpr int wpg = qd_waves<D>();
-  const dim3 grid((a.n_waves + wpg - 1) / wpg), block(64 * wpg);
-  const int pairs = a.n_seqs * a.Hkv * qdecode_head_groups(a.rep);
-  const bool rest = a.n_waves > 4 * pairs;  // more than kFirst partials per pair on average
+  const dim3 grid((a0.n_waves + wpg - 1) / wpg), block(64 * wpg);
+  const int pairs = a0.n_seqs * a0.Hkv * qdecode_head_groups(a0.rep);
+  const bool rest = a0.n_waves > 4 * pairs;  // more than kFirst partials per pair on average
+  // The partials merge inside the fused launch (each wave counts its
+  // partials in at its range's end; the last of a pair merges it) where
+  // pairs average at most 4 partials, at most 128 dims; longer merges
+  // (config 2: 32 partials a pair) and 256 dims keep the merge launch.
+  DecodeArgs a = a0;
+  if (ref || rest || D > 128) a.counters = nullptr;
   if constexpr (DT == kBF16) {
     if (ref) {
       // the reference-arithmetic path: bf16 score rows, the reference
@@ -1419,6 +1546,7 @@ static void launch_hp(const DecodeArgs& a, bool ref, hipStream_t st) {
     VKV_HIP(hipGetLastError());
     timing_commit(tl);
   }
+  if (a.counters) return;
   const dim3 cb(HP == 4 ? D : 2 * D);
   if (rest)
     hipLaunchKernelGGL((qdecode_combine_kernel<HP, 4, true, DT>), dim3(pairs), cb, 0, st, a, D);

@@ -127,6 +127,12 @@ __device__ __forceinline__ int64_t qsb_index(int64_t t, int which, int g, int se
   return t * (keys_only ? 2 * G : 4 * G) + which * 2 * G + g * 2 + sel;
 }
 
+// Two floats as one 64-bit word (first in the low half), for the
+// device-coherent 64-bit stores of split-K partials.
+__device__ __forceinline__ uint64_t pack_f2(float lo, float hi) {
+  return static_cast<uint64_t>(__float_as_uint(lo)) | (static_cast<uint64_t>(__float_as_uint(hi)) << 32);
+}
+
 __device__ __forceinline__ float wave_max(float v, int width) {
   for (int o = width / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, width));
   return v;

@@ -115,11 +115,6 @@ __device__ __forceinline__ float add_xor32(float v) {
   return lo + hi;
 }
 
-// Two floats as one 64-bit word (first in the low half).
-__device__ __forceinline__ uint64_t pack_f2(float lo, float hi) {
-  return static_cast<uint64_t>(__float_as_uint(lo)) | (static_cast<uint64_t>(__float_as_uint(hi)) << 32);
-}
-
 // Maximum / sum within each half-wave of 32 lanes: pairs 1 and 2 apart
 // (quad permutes), then each lane with its mirror in 8 and in 16 lanes (the
 // partners hold equal values by then, so the mirror acts as a butterfly),

@@ -245,6 +245,8 @@ struct DecodeArgs {
   int32_t dtype;             // kBF16 or kF16: queries, scales / biases and output
   uint16_t* sc;              // reference path: bf16 score / weight rows
   int64_t sc_stride;         //   [n_seqs][Hq][sc_stride], sc_stride >= max_len, % 64 == 0
+  uint32_t* counters;        // zeroed per-pair counters: the partials merge inside the
+                             //   decode launch (nullptr: in qdecode_combine_kernel)
 };
 bool qdecode_supported(int dtype, int bits, int D, int block_size, int rep, int group);
 // (sequence, kv head) pairs are split into head groups of 4 or 8 query heads
