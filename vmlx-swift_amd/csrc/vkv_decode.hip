@@ -377,11 +377,13 @@ __device__ __forceinline__ void qmerge_step(float& M, float& L, float (&o)[E], i
 // The in-launch merge of a (sequence, head pair)'s K partials by the wave
 // that counted in last: the partials come back through device-coherent
 // loads (they were stored the same way), 4 partials a round trip; lane l
-// takes head l / (64 / HP) and D * HP / 64 of its dims.
+// takes head l / (64 / HP) and D * HP / 64 consecutive floats of its row,
+// whose 8-byte word p holds dims 16 (p / 8) + 4 (p % 4) + 2 ((p / 4) % 2)
+// and the next (the order of the decode kernel's coherent stores).
 template <int HP, int D, int DT>
 __device__ __forceinline__ void qdecode_merge_pair(const DecodeArgs& a, int pair, int K, int lane) {
   constexpr int LPH = 64 / HP, EPL = D / LPH, kQuad = 4;
-  static_assert(EPL % 4 == 0, "4-element output stores");
+  static_assert(EPL % 2 == 0, "2-element output stores");
   const int rep = a.rep, n_hg = (rep + HP - 1) / HP, HG = a.Hkv * n_hg;
   const int seq = pair / HG, j = pair % HG;
   const int64_t hq0 = static_cast<int64_t>(j / n_hg) * rep + (j % n_hg) * HP;
@@ -412,13 +414,12 @@ __device__ __forceinline__ void qdecode_merge_pair(const DecodeArgs& a, int pair
   }
   if (r >= nh) return;
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  uint16_t* dst = a.out + seq * a.o_ss + (hq0 + r) * a.o_sh + d0;
+  uint16_t* dst = a.out + seq * a.o_ss + (hq0 + r) * a.o_sh;
 #pragma unroll
-  for (int e = 0; e < EPL; e += 4) {
-    u32x2_t v;
-    v[0] = out_el<DT>(o[e] * inv) | (out_el<DT>(o[e + 1] * inv) << 16);
-    v[1] = out_el<DT>(o[e + 2] * inv) | (out_el<DT>(o[e + 3] * inv) << 16);
-    *reinterpret_cast<u32x2_t*>(dst + e) = v;
+  for (int e = 0; e < EPL; e += 2) {
+    const int p = (d0 + e) / 2;
+    const int d = 16 * (p >> 3) + 4 * (p & 3) + 2 * ((p >> 2) & 1);
+    *reinterpret_cast<uint32_t*>(dst + d) = out_el<DT>(o[e] * inv) | (out_el<DT>(o[e + 1] * inv) << 16);
   }
 }
 
@@ -1187,15 +1188,18 @@ qdecode_kernel(DecodeArgs a) {
         }
       } else if (merge_here) {
         // device-coherent stores (written through to the level every XCD
-        // reads), for the wave that merges the pair
+        // reads), for the wave that merges the pair.  8 bytes a store: the
+        // row's 8-byte words are ordered (t, half e, lane group lg) so that
+        // each store instruction writes 32 contiguous bytes of a row (word
+        // 8 t + 4 e + lg holds dims 16 t + 4 lg + 2 e, + 1)
         const int64_t slot = pair * a.max_parts + (w - wa);
-        uint64_t* o = reinterpret_cast<uint64_t*>(a.ws_o + (slot * HP + n) * D + 4 * lg);
+        uint64_t* o = reinterpret_cast<uint64_t*>(a.ws_o + (slot * HP + n) * D) + lg;
 #pragma unroll
         for (int t = 0; t < NT; t++) {
           const float cg = csum[t / (NT / G)];
           __hip_atomic_store(o + 8 * t, pack_f2(oacc[t][0] + cg, oacc[t][1] + cg),
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(o + 8 * t + 1, pack_f2(oacc[t][2] + cg, oacc[t][3] + cg),
+          __hip_atomic_store(o + 8 * t + 4, pack_f2(oacc[t][2] + cg, oacc[t][3] + cg),
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         if (lg == 0)
