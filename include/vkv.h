@@ -741,13 +741,14 @@ int vkv_get_option(int32_t which, int64_t *value);
  * matrix-core decode kernel, without the split-K merge), the MLA launcher
  * (kind 1: its attention kernel) and the dense float decode launcher (kind
  * 2: its decode kernel, without the merge) and the TurboQuant launchers
- * (kind 3: the key encode kernel, kind 4: the key decode kernel) launch
+ * (kind 3: the key encode kernel, kind 4: the key decode kernel) and the
+ * affine pool append (kind 5: its quantize-and-store kernel) launch
  * that kernel with a start/stop HIP event pair (hipExtLaunchKernel),
  * recorded at the kernel's own start and end.  vkv_kernel_timing_read waits
  * for the launches of a kind recorded so far and returns their total
  * milliseconds and count, then forgets them. */
 enum { VKV_TIME_DECODE = 0, VKV_TIME_MLA = 1, VKV_TIME_FDECODE = 2, VKV_TIME_TQ_ENCODE = 3,
-       VKV_TIME_TQ_DECODE = 4 };
+       VKV_TIME_TQ_DECODE = 4, VKV_TIME_APPEND = 5 };
 int vkv_kernel_timing(int32_t enable);
 int vkv_kernel_timing_read(int32_t kind, double *total_ms, int32_t *count);
 

@@ -385,7 +385,7 @@ void launch_batch_mask(int n, int cols, int window, const int32_t* offsets, cons
 // main kernel with hipExtLaunchKernelGGL and a start/stop event pair, which
 // the runtime records at the kernel's own start and end.
 enum { kTimeDecode = 0, kTimeMla = 1, kTimeFDecode = 2, kTimeTqEncode = 3, kTimeTqDecode = 4,
-       kTimeKinds = 5 };
+       kTimeAppend = 5, kTimeKinds = 6 };
 struct TimedLaunch {
   int kind = 0;
   hipEvent_t start = nullptr, stop = nullptr;  // null when timing is off

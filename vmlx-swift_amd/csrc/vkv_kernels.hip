@@ -10,6 +10,7 @@
 #include "vkv_device.h"
 #include "vkv_internal.h"
 #include "vkv_kvread.h"
+#include <hip/hip_ext.h>
 
 #include <algorithm>
 
@@ -996,8 +997,10 @@ static void append_dispatch(int bits, int group, const RowSrc& sk, const RowSrc&
                             const RowDst& dv, int64_t ntok, int H, int D, bool with_v, hipStream_t st) {
   const int hb = 256 / D;
   const dim3 grid(static_cast<unsigned>((ntok + 7) / 8), (H + hb - 1) / hb, with_v ? 2 : 1);
-#define VKV_A(B, G) \
-  hipLaunchKernelGGL((append_affine_kernel<DT, B, G>), grid, dim3(256), 0, st, sk, sv, dk, dv, ntok, H, D)
+  const TimedLaunch tl = timing_prepare(kTimeAppend);
+#define VKV_A(B, G)                                                                            \
+  hipExtLaunchKernelGGL((append_affine_kernel<DT, B, G>), grid, dim3(256), 0, st, tl.start, tl.stop, \
+                        0, sk, sv, dk, dv, ntok, H, D)
 #define VKV_AG(B)                         \
   do {                                    \
     if (group == 32) VKV_A(B, 32);        \
@@ -1008,6 +1011,8 @@ static void append_dispatch(int bits, int group, const RowSrc& sk, const RowSrc&
   else VKV_AG(8);
 #undef VKV_AG
 #undef VKV_A
+  VKV_HIP(hipGetLastError());
+  timing_commit(tl);
 }
 
 bool append_affine_supported(int bits, int group, int D) {

@@ -116,7 +116,7 @@ EXPORTS = (
     "vkv_turboquant_restore_decoded", "vkv_tq_tables", "vkv_set_option", "vkv_get_option",
     "vkv_turboquant_write_pool", "vkv_cache_update_quantized_tuples",
 )
-TIME_DECODE, TIME_MLA, TIME_FDECODE, TIME_TQ_ENCODE, TIME_TQ_DECODE = 0, 1, 2, 3, 4
+TIME_DECODE, TIME_MLA, TIME_FDECODE, TIME_TQ_ENCODE, TIME_TQ_DECODE, TIME_APPEND = 0, 1, 2, 3, 4, 5
 
 _lib = None
 
@@ -388,14 +388,15 @@ def mla_decode(queries, view: PagedView, scale: float, stream=None):
 
 
 def kernel_timing(enable: bool):
-    """Start (True) or stop recording event pairs around the decode and MLA
-    kernels (a measurement aid; see vkv_kernel_timing)."""
+    """Start (True) or stop recording event pairs around the decode, MLA,
+    TurboQuant and pool-append kernels (a measurement aid; see
+    vkv_kernel_timing)."""
     _chk(lib().vkv_kernel_timing(C.c_int32(1 if enable else 0)))
 
 
 def kernel_timing_read(kind: int):
-    """(total milliseconds, launches) recorded for kind TIME_DECODE or
-    TIME_MLA since the last read; waits for those launches."""
+    """(total milliseconds, launches) recorded for a kind (TIME_DECODE,
+    TIME_MLA, ...) since the last read; waits for those launches."""
     ms = C.c_double()
     n = C.c_int32()
     _chk(lib().vkv_kernel_timing_read(C.c_int32(kind), C.byref(ms), C.byref(n)))
