@@ -96,6 +96,18 @@ def test_long_context_131072_tokens():
     run_and_check(rng, O.BF16, 4, [131072, 100], 8, 4, 128, outliers=0)
 
 
+def test_long_context_among_many_short_sequences():
+    """The merge inside the decode launch past 32 partials: 255 sequences of
+    40 tokens beside one of 131,072 give 2048 (sequence, head pair)s, so the
+    launch averages at most 4 partials a pair and merges inside, while the
+    long pair has about 33 partials (more than the 32 of one merge step);
+    the short pairs' few partials merge inside the same launch."""
+    rng = np.random.default_rng(9250)
+    lens = [40] * 120 + [131072] + [40] * 135
+    print(f"long context among {len(lens)} sequences", flush=True)
+    run_and_check(rng, O.BF16, 4, lens, 8, 4, 128, outliers=0)
+
+
 def test_long_context_reference_softmax(monkeypatch):
     """The reference-arithmetic decode (score rows, the looped reference
     softmax, P.V from stored weights) over 131,072 tokens: more than 32
