@@ -717,11 +717,15 @@ int vkv_workspace_release(void *stream, int64_t *bytes);
  * dtype, softmax(precise: false) with its AccT = T arithmetic in a pass of
  * its own (KVCache.swift:1982, mlx-generated/metal/softmax.h:10-190),
  * weights stored in the dtype, then P.V (with it off, the softmax of the
- * stored scores runs in fp32 inside one pass).  Initial values come from
+ * stored scores runs in fp32 inside one pass); SEPARATE_TOKEN_WRITE (0/1)
+ * makes vkv_attention_with_cache_update's one-token step over a
+ * QuantizedKVCache write the token in a launch of its own before the
+ * attention (by default the matrix-core decode launch quantizes and stores
+ * it as it starts; both give the same bits).  Initial values come from
  * the environment variables VKV_GENERIC_ATTENTION, VKV_DECODE_WAVES,
- * VKV_MLA_SPLITS, VKV_FDECODE_WAVES, VKV_GATHER_TOKENS and
- * VKV_REFERENCE_SOFTMAX, read once; calls read the options, never the
- * environment. */
+ * VKV_MLA_SPLITS, VKV_FDECODE_WAVES, VKV_GATHER_TOKENS,
+ * VKV_REFERENCE_SOFTMAX and VKV_SEPARATE_TOKEN_WRITE, read once; calls read
+ * the options, never the environment. */
 enum {
   VKV_OPTION_GENERIC_ATTENTION = 0,
   VKV_OPTION_DECODE_WAVES = 1,
@@ -729,7 +733,8 @@ enum {
   VKV_OPTION_FDECODE_WAVES = 3, /* 0 = 2048: waves the float decode kernel aims for */
   VKV_OPTION_GATHER_TOKENS = 4, /* 0 = a 256 MiB copy: key window of a gathered chunk */
   VKV_OPTION_REFERENCE_SOFTMAX = 5, /* quantized attention with the reference's arithmetic */
-  VKV_OPTION_COUNT = 6
+  VKV_OPTION_SEPARATE_TOKEN_WRITE = 6, /* the router's quantized decode token in its own launch */
+  VKV_OPTION_COUNT = 7
 };
 int vkv_set_option(int32_t which, int64_t value);
 int vkv_get_option(int32_t which, int64_t *value);

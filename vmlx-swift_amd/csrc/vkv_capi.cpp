@@ -88,11 +88,13 @@ struct Options {
   Options() {
     const char* names[VKV_OPTION_COUNT] = {"VKV_GENERIC_ATTENTION", "VKV_DECODE_WAVES",
                                            "VKV_MLA_SPLITS", "VKV_FDECODE_WAVES",
-                                           "VKV_GATHER_TOKENS", "VKV_REFERENCE_SOFTMAX"};
+                                           "VKV_GATHER_TOKENS", "VKV_REFERENCE_SOFTMAX",
+                                           "VKV_SEPARATE_TOKEN_WRITE"};
     for (int i = 0; i < VKV_OPTION_COUNT; i++) {
       const char* e = getenv(names[i]);
       int64_t x = 0;
-      const bool flag = i == VKV_OPTION_GENERIC_ATTENTION || i == VKV_OPTION_REFERENCE_SOFTMAX;
+      const bool flag = i == VKV_OPTION_GENERIC_ATTENTION || i == VKV_OPTION_REFERENCE_SOFTMAX ||
+                        i == VKV_OPTION_SEPARATE_TOKEN_WRITE;
       if (e) x = flag ? (atoi(e) != 0) : std::max(1, atoi(e));
       v[i].store(x, std::memory_order_relaxed);
     }
@@ -553,8 +555,37 @@ int vkv_quantized_sdpa(const vkv_array* q, const vkv_array* k_wq, const vkv_arra
 namespace {
 // vkv_paged_sdpa and its no-allocation variant (noalloc: split-K partials in
 // the fixed scratch array, nothing allocated).
+// The router's decode token over a QuantizedKVCache: its key / value rows
+// [B, Hkv, D] (element strides), which the matrix-core decode launch
+// quantizes and writes into the pool itself.
+struct DecodeToken {
+  const void* k;
+  const void* v;
+  int64_t k_ss, k_sh, v_ss, v_sh;
+};
+
+// Whether a paged decode call (3-D q / out checked by the caller) runs on
+// the matrix-core kernel (vkv_decode.hip).
+bool paged_decode_on_matrix_cores(const vkv_array* q, const vkv_array* out,
+                                  const vkv_paged_view* kv) {
+  const bool keys_only = (kv->flags & VKV_VIEW_KEYS_ONLY) != 0;
+  const int rep = static_cast<int>(q->shape[1] / kv->n_kv_heads);
+  // the matrix-core kernel loads queries 16 bytes and stores outputs 8
+  // bytes at a time
+  const bool aligned = (reinterpret_cast<uintptr_t>(q->data) % 16 == 0) &&
+                       q->strides[0] % 8 == 0 && q->strides[1] % 8 == 0 &&
+                       (reinterpret_cast<uintptr_t>(out->data) % 8 == 0) &&
+                       out->strides[0] % 4 == 0 && out->strides[1] % 4 == 0;
+  // (the matrix-core reference path stores bf16 score rows: an f16 cache
+  // with the reference softmax takes the generic reference path)
+  return kv->bits > 0 && !keys_only && aligned && kv->max_len <= qdecode_max_len() &&
+         !option(VKV_OPTION_GENERIC_ATTENTION) &&
+         !(option(VKV_OPTION_REFERENCE_SOFTMAX) && kv->dtype != VKV_BF16) &&
+         qdecode_supported(kv->dtype, kv->bits, kv->head_dim, kv->block_size, rep, kv->group_size);
+}
+
 void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_array* out,
-                void* stream, bool noalloc) {
+                void* stream, bool noalloc, const DecodeToken* tok = nullptr) {
   {
     need(q, "q");
     need(kv, "kv");
@@ -567,20 +598,8 @@ void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_a
       throw Error("q/out shapes do not match the view");
     if (q->shape[1] % kv->n_kv_heads) throw Error("query heads must be a multiple of kv heads");
     if (!kv->block_table) throw Error("view has no block table");
-    const bool keys_only = (kv->flags & VKV_VIEW_KEYS_ONLY) != 0;
     const int rep = static_cast<int>(q->shape[1] / kv->n_kv_heads);
-    // the matrix-core kernel loads queries 16 bytes and stores outputs 8
-    // bytes at a time
-    const bool aligned = (reinterpret_cast<uintptr_t>(q->data) % 16 == 0) &&
-                         q->strides[0] % 8 == 0 && q->strides[1] % 8 == 0 &&
-                         (reinterpret_cast<uintptr_t>(out->data) % 8 == 0) &&
-                         out->strides[0] % 4 == 0 && out->strides[1] % 4 == 0;
-    // (the matrix-core reference path stores bf16 score rows: an f16 cache
-    // with the reference softmax takes the generic reference path)
-    if (kv->bits > 0 && !keys_only && aligned && kv->max_len <= qdecode_max_len() &&
-        !option(VKV_OPTION_GENERIC_ATTENTION) &&
-        !(option(VKV_OPTION_REFERENCE_SOFTMAX) && kv->dtype != VKV_BF16) &&
-        qdecode_supported(kv->dtype, kv->bits, kv->head_dim, kv->block_size, rep, kv->group_size)) {
+    if (paged_decode_on_matrix_cores(q, out, kv)) {
       // matrix-core path (vkv_decode.hip)
       KVSrc src = kvsrc_from_view(*kv);
       DecodeArgs d{};
@@ -624,9 +643,19 @@ void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_a
       if (!noalloc && !ref && kv->head_dim <= 128)
         d.counters = attention_counters(S(stream), static_cast<size_t>(chunk) * kv->n_kv_heads *
                                                        qdecode_head_groups(rep));
+      if (tok) {
+        if (ref || kv->head_dim > 128) throw Error("the decode token needs the fused decode");
+        d.new_k = static_cast<const uint16_t*>(tok->k);
+        d.new_v = static_cast<const uint16_t*>(tok->v);
+        d.nk_ss = tok->k_ss;
+        d.nk_sh = tok->k_sh;
+        d.nv_ss = tok->v_ss;
+        d.nv_sh = tok->v_sh;
+      }
       launch_qdecode(d, kv->bits, kv->head_dim, S(stream), ref);
       return;
     }
+    if (tok) throw Error("the decode token needs the matrix-core decode");
     AttnArgs a{};
     a.q = q->data;
     a.q_sb = q->strides[0];
@@ -721,6 +750,64 @@ int vkv_quantized_paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float
   });
 }
 
+}  // extern "C"
+
+namespace {
+
+// The router's one-token decode step over a QuantizedKVCache in one launch:
+// updateQuantized's bookkeeping on the host, then the matrix-core decode,
+// which quantizes the token and stores it into its block before reading it
+// (the same bits as the append launch it replaces).  Returns false, having
+// done nothing, where that launch would not run (other shapes, options or
+// alignments take the two-call path).
+bool quantized_decode_step(const vkv_array* q, const vkv_array* keys, const vkv_array* values,
+                           vkv_cache cache, float scale, int32_t mask_mode, vkv_array* out,
+                           void* stream) {
+  auto* qc = dynamic_cast<QuantizedCache*>(cache->impl.get());
+  if (!qc || option(VKV_OPTION_SEPARATE_TOKEN_WRITE) || mask_mode != VKV_MASK_NONE) return false;
+  if (q->ndim != 4 || out->ndim != 4 || q->shape[2] != 1 || keys->ndim != 4 || values->ndim != 4 ||
+      keys->shape[2] != 1 || values->shape[2] != 1 || keys->dtype != values->dtype ||
+      q->strides[3] != 1 || out->strides[3] != 1)
+    return false;
+  // an existing store of the token's geometry (a first update takes the
+  // two-call path, which creates it), 4- or 8-bit g64 at 64 or 128 dims
+  if (!qc->store_.get() || keys->dtype != qc->dtype_ || keys->shape[0] != qc->B_ ||
+      keys->shape[1] != qc->H_ || keys->shape[3] != qc->D_ || values->shape[0] != qc->B_ ||
+      values->shape[1] != qc->H_ || values->shape[3] != qc->D_ || qc->group_ != 64 ||
+      (qc->bits_ != 4 && qc->bits_ != 8) || (qc->D_ != 64 && qc->D_ != 128) ||
+      option(VKV_OPTION_REFERENCE_SOFTMAX))
+    return false;
+  // 16-byte rows of 8 elements
+  for (const vkv_array* a : {keys, values})
+    if (reinterpret_cast<uintptr_t>(a->data) % 16 || a->strides[0] % 8 || a->strides[1] % 8 ||
+        a->strides[3] != 1)
+      return false;
+  // the view the step will attend: the current one, one token longer
+  vkv_paged_view next = qc->view();
+  next.max_len += 1;
+  vkv_array q3 = *q, o3 = *out;
+  q3.ndim = o3.ndim = 3;
+  q3.shape[2] = q->shape[3];
+  q3.strides[2] = q->strides[3];
+  o3.shape[2] = out->shape[3];
+  o3.strides[2] = out->strides[3];
+  if (q->dtype != next.dtype || out->dtype != next.dtype || q->shape[0] != next.n_seqs ||
+      q->shape[3] != next.head_dim || out->shape[0] != next.n_seqs || out->shape[1] != q->shape[1] ||
+      out->shape[3] != next.v_head_dim || q->shape[1] % next.n_kv_heads ||
+      !paged_decode_on_matrix_cores(&q3, &o3, &next))
+    return false;
+  qc->advance(*keys, *values, S(stream));
+  const vkv_paged_view view = qc->view();
+  const DecodeToken tok{keys->data,        values->data,      keys->strides[0],
+                        keys->strides[1], values->strides[0], values->strides[1]};
+  paged_sdpa(&q3, &view, scale, &o3, stream, false, &tok);
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
 int vkv_attention_with_cache_update(const vkv_array* q, const vkv_array* keys, const vkv_array* values,
                                     vkv_cache cache, float scale, int32_t mask_mode,
                                     const vkv_array* mask, const vkv_array* sinks, vkv_array* out,
@@ -742,6 +829,7 @@ int vkv_attention_with_cache_update(const vkv_array* q, const vkv_array* keys, c
       // the quantized path has no sinks (the models refuse them,
       // Libraries/MLXLLM/Models/GPTOSS.swift:223-235)
       if (sinks) throw Error("quantized attention does not support sinks");
+      if (quantized_decode_step(q, keys, values, cache, scale, mask_mode, out, stream)) return;
       vkv_paged_view view{};
       call(vkv_cache_update_quantized(cache, keys, values, stream, &view));
       call(vkv_quantized_paged_sdpa(q, &view, scale, mask_mode, mask, out, stream));

@@ -423,6 +423,78 @@ __device__ __forceinline__ void qdecode_merge_pair(const DecodeArgs& a, int pair
   }
 }
 
+// The decode token t of (sequence seq, kv head hk) -- the key and value
+// rows the router hands over with the attention, [seq][kv head][D] -- into
+// its pool block, quantized as the paged append quantizes it
+// (affine_quantize8, group 64; updateQuantized, KVCache.swift:1049-1122):
+// lanes 0 .. D/8 - 1 take 8 dims of the key row each, the next D/8 lanes
+// the value row's, 8 lanes a group.  Stores as the append's: key code
+// words, value code bytes (8-bit) or nibbles merged into their words with
+// atomics (4-bit: a word holds 8 tokens of a dim), scale and bias by a
+// group's first lane.
+template <int BITS, int D, int DT>
+__device__ __forceinline__ void qdecode_write_token(const DecodeArgs& a, int seq, int hk, int t,
+                                                    int lane) {
+  using E = Elem<DT>;
+  constexpr int LPR = D / 8, G = D / 64;
+  const bool active = lane < 2 * LPR;
+  const int which = lane / LPR, j8 = lane % LPR;
+  float v[8];
+  if (active) {
+    const uint16_t* src = which ? a.new_v + seq * a.nv_ss + hk * a.nv_sh
+                                : a.new_k + seq * a.nk_ss + hk * a.nk_sh;
+    const u32x4_t x = *(g_u32x4_t*)(src + 8 * j8);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      v[2 * e] = el_lo<DT>(x[e]);
+      v[2 * e + 1] = el_hi<DT>(x[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = 0.0f;
+  }
+  uint32_t code[8];
+  float scale, bias;
+  affine_quantize8<DT, BITS, 64>(v, code, scale, bias);  // (every lane: team shuffles)
+  if (!active) return;
+  const int64_t blk = a.table[static_cast<int64_t>(seq) * a.table_stride + t / a.block_size];
+  const int tib = t % a.block_size;
+  // (the pool is written through the view's base, which the decode only reads elsewhere)
+  uint8_t* chunk = const_cast<uint8_t*>(a.base) + blk * a.block_bytes + hk * a.head_bytes;
+  uint8_t* c = chunk + (which ? a.vc_off : a.kc_off);
+  if (!which) {
+    if constexpr (BITS == 4) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int i = 0; i < 8; i++) w |= code[i] << (4 * i);
+      *reinterpret_cast<uint32_t*>(c + qk_word_off(tib, j8, D, 4)) = w;
+    } else {
+      *reinterpret_cast<uint32_t*>(c + qk_word_off(tib, 2 * j8, D, 8)) =
+          code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
+      *reinterpret_cast<uint32_t*>(c + qk_word_off(tib, 2 * j8 + 1, D, 8)) =
+          code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      int sh;
+      const int64_t off = qv_word_off(tib, 8 * j8 + i, D, BITS, &sh);
+      if constexpr (BITS == 8) {
+        c[off + sh / 8] = static_cast<uint8_t>(code[i]);
+      } else {
+        uint32_t* word = reinterpret_cast<uint32_t*>(c + off);
+        atomicAnd(word, ~(0xFu << sh));
+        atomicOr(word, code[i] << sh);
+      }
+    }
+  }
+  if (j8 % 8 == 0) {
+    typename E::T* sbp = reinterpret_cast<typename E::T*>(chunk + a.sb_off);
+    sbp[qsb_index(tib, which, j8 / 8, 0, G, false)] = E::from_f32(scale);
+    sbp[qsb_index(tib, which, j8 / 8, 1, G, false)] = E::from_f32(bias);
+  }
+}
+
 // Orders one wave's LDS writes before its later LDS reads by other lanes
 // (no workgroup barrier: every workgroup is a single wave).
 __device__ __forceinline__ void wave_lds_sync() {
@@ -750,6 +822,28 @@ qdecode_kernel(DecodeArgs a) {
   // the zero entry of every query-table slice (lanes outside a column's part)
   for (int sg = lane; sg < SL; sg += 64) qtab[sg * QROW + 16 * SPW] = u32x4_t{0u, 0u, 0u, 0u};
   wave_lds_sync();
+
+  // ---- the router's decode step (updateQuantized, then the attention):
+  // the token of every pair whose last step this range holds goes into its
+  // block before any of the range's loads, and is complete (at the L2 this
+  // wave reads from) before they issue, so the unit holding it reads it back.
+  // The unit is this wave's alone, as are the blocks it reads.
+  if constexpr (MODE == kModeFused && D <= 128) {
+    if (a.new_k) {
+      bool wrote = false;
+      for (int kk = 0; kk < nseg; kk++) {
+        const int len = __builtin_amdgcn_readfirstlane(seg_tab[kk][4]);
+        const int t0 = __builtin_amdgcn_readfirstlane(seg_tab[kk][2]);
+        const int take = __builtin_amdgcn_readfirstlane(seg_tab[kk][3]);
+        if (len <= 0 || t0 + take != (len + 63) >> 6) continue;
+        qdecode_write_token<BITS, D, DT>(a, __builtin_amdgcn_readfirstlane(seg_tab[kk][0]),
+                                         __builtin_amdgcn_readfirstlane(seg_tab[kk][1]) / n_hg,
+                                         len - 1, lane);
+        wrote = true;
+      }
+      if (wrote) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+  }
 
   // ---- per-unit loads
   // This lane's byte offsets from a 32-token sub-block's two scalar bases
@@ -1594,6 +1688,10 @@ void launch_qdecode(const DecodeArgs& a0, int bits, int D, hipStream_t st, bool 
     a.out += s0 * a0.o_ss;
     a.table += static_cast<int64_t>(s0) * a0.table_stride;
     if (a.seq_lens) a.seq_lens += s0;
+    if (a.new_k) {
+      a.new_k += s0 * a0.nk_ss;
+      a.new_v += s0 * a0.nv_ss;
+    }
     if (a.dtype == kF16) launch_dt<kF16>(a, bits, D, ref, st);
     else launch_dt<kBF16>(a, bits, D, ref, st);
   }

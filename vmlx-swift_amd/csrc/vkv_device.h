@@ -146,4 +146,44 @@ __device__ __forceinline__ float wave_sum(float v, int width) {
   return v;
 }
 
+// The reference's affine quantization of a group (quantized.h:2422-2458),
+// 8 values of the group a lane, GROUP / 8 neighbouring lanes a group (every
+// lane of the team calls it), operation for operation in fp32 with IEEE
+// division and round-half-away-from-zero:
+//   running min starts at Limits<T>::max, running max at 0 (:2422-2431);
+//   scale = max((max - min) / n_bins, 1e-7), negated when max is the edge,
+//   q0 = round(edge / scale), scale = edge / q0, bias = edge unless q0 == 0
+//   (:2436-2443);
+//   code = min(round((w - bias) / scale), n_bins) with the unrounded scale
+//   (:2458); the caller stores scale and bias rounded to T (:2447-2450).
+template <int DT, int BITS, int GROUP>
+__device__ __forceinline__ void affine_quantize8(const float (&v)[8], uint32_t (&code)[8],
+                                                 float& scale_out, float& bias_out) {
+  constexpr int TEAM = GROUP / 8;
+  constexpr float n_bins = static_cast<float>((1 << BITS) - 1);
+  float w_min = Elem<DT>::kMax, w_max = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    w_min = fminf(w_min, v[e]);
+    w_max = fmaxf(w_max, v[e]);
+  }
+  w_min = wave_min(w_min, TEAM);
+  w_max = wave_max(w_max, TEAM);
+  float scale = fmaxf((w_max - w_min) / n_bins, 1e-7f);
+  const bool side = fabsf(w_min) > fabsf(w_max);
+  scale = side ? scale : -scale;
+  const float edge = side ? w_min : w_max;
+  const float q0 = roundf(edge / scale);
+  const bool at_zero = q0 == 0.0f;
+  scale = at_zero ? scale : edge / q0;
+  const float bias = at_zero ? 0.0f : edge;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const float x = fminf(roundf((v[e] - bias) / scale), n_bins);
+    code[e] = x > 0.0f ? static_cast<uint32_t>(x) : 0u;
+  }
+  scale_out = scale;
+  bias_out = bias;
+}
+
 }  // namespace vkv

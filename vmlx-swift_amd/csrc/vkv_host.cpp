@@ -1081,6 +1081,12 @@ vkv_paged_view QuantizedCache::view() const {
 // QuantizedKVCache.updateQuantized (KVCache.swift:1049-1122)
 void QuantizedCache::update_quantized(const vkv_array& k, const vkv_array& v, hipStream_t st,
                                       vkv_paged_view* out) {
+  const int64_t prev = advance(k, v, st);
+  write_tokens(k, v, prev, st);
+  *out = view();
+}
+
+int64_t QuantizedCache::advance(const vkv_array& k, const vkv_array& v, hipStream_t st) {
   check4(k, "keys");
   check4(v, "values");
   if (k.dtype != v.dtype) throw Error("keys and values must share a dtype");
@@ -1097,6 +1103,12 @@ void QuantizedCache::update_quantized(const vkv_array& k, const vkv_array& v, hi
     throw Error("keys do not match the cached [B, H, D] / dtype");
   }
   offset += Sn;
+  return prev;
+}
+
+void QuantizedCache::write_tokens(const vkv_array& k, const vkv_array& v, int64_t prev,
+                                  hipStream_t st) {
+  const int64_t B = k.shape[0], H = k.shape[1], Sn = k.shape[2], D = k.shape[3];
   const vkv_array* arr[2] = {&k, &v};
   ChunkLayout L = chunk_layout(bits_, dtype_, kBlock, static_cast<int>(D_), static_cast<int>(D_), group_,
                                false);
@@ -1116,7 +1128,6 @@ void QuantizedCache::update_quantized(const vkv_array& k, const vkv_array& v, hi
     }
     launch_append_affine(dtype_, bits_, group_, sk, sv, dk, dv, B * Sn, static_cast<int>(H),
                          static_cast<int>(D), true, st);
-    *out = view();
     return;
   }
   for (int which = 0; which < 2; which++) {
@@ -1130,7 +1141,6 @@ void QuantizedCache::update_quantized(const vkv_array& k, const vkv_array& v, hi
     dst.start = static_cast<int32_t>(prev);
     launch_quantize_rows(a.dtype, bits_, group_, 1, src, dst, B * H * Sn, static_cast<int>(D), st);
   }
-  *out = view();
 }
 
 int64_t QuantizedCache::trim(int64_t n) {

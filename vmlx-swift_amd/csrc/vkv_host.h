@@ -290,6 +290,11 @@ class QuantizedCache : public Cache {
   int64_t capacity() const override { return cap_; }
   void update_quantized(const vkv_array& k, const vkv_array& v, hipStream_t st,
                         vkv_paged_view* out) override;
+  // updateQuantized in two halves: the bookkeeping (growth, offset; returns
+  // the first new token's position), then the quantized write of the new
+  // tokens -- which a decode launch may do instead (vkv_decode.hip)
+  int64_t advance(const vkv_array& k, const vkv_array& v, hipStream_t st);
+  void write_tokens(const vkv_array& k, const vkv_array& v, int64_t prev, hipStream_t st);
   int state(hipStream_t st, vkv_array* out) override;
   void set_state(const vkv_array* a, int count, hipStream_t st) override;
   std::vector<std::string> meta_state() const override;

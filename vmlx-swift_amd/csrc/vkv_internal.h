@@ -247,6 +247,12 @@ struct DecodeArgs {
   int64_t sc_stride;         //   [n_seqs][Hq][sc_stride], sc_stride >= max_len, % 64 == 0
   uint32_t* counters;        // zeroed per-pair counters: the partials merge inside the
                              //   decode launch (nullptr: in qdecode_combine_kernel)
+  // the router's decode token (nullptr: none): the key / value rows
+  // [seq][kv head][D] of each sequence's last token, quantized and stored
+  // into its block by the launch itself (fused mode, D <= 128); element strides
+  const uint16_t* new_k;
+  const uint16_t* new_v;
+  int64_t nk_ss, nk_sh, nv_ss, nv_sh;
 };
 bool qdecode_supported(int dtype, int bits, int D, int block_size, int rep, int group);
 // (sequence, kv head) pairs are split into head groups of 4 or 8 query heads

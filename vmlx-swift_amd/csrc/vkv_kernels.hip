@@ -87,16 +87,9 @@ __device__ __forceinline__ void store_chunk_codes(uint8_t* chunk, const RowDst& 
 // ------------------------------------------------------- affine quantize
 //
 // One thread owns 8 consecutive values of a row; GROUP/8 neighbouring lanes
-// form one quantization group and reduce min/max with xor-shuffles.  The
-// arithmetic is the reference's, operation for operation, in fp32 with
-// IEEE division and round-half-away-from-zero:
-//   running min starts at Limits<T>::max, running max at 0
-//     (quantized.h:2422-2431);
-//   scale = max((max - min) / n_bins, 1e-7), negated when max is the edge,
-//   q0 = round(edge / scale), scale = edge / q0, bias = edge unless q0 == 0
-//     (:2436-2443);
-//   code = min(round((w - bias) / scale), n_bins) with the unrounded scale
-//     (:2458), scale/bias stored rounded to T (:2447-2450).
+// form one quantization group and reduce min/max with xor-shuffles; the
+// arithmetic is the reference's (affine_quantize8, quantized.h:2422-2458),
+// scale/bias stored rounded to T (:2447-2450).
 // mode 0 writes the reference layout; mode 1 writes a paged chunk (K rows
 // token-major, V rows dim-major).
 template <int DT, int BITS, int GROUP, int MODE>
@@ -104,7 +97,6 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(RowSrc src, RowDst d
                                                             int D) {
   using E = Elem<DT>;
   constexpr int TEAM = GROUP / 8;
-  constexpr float n_bins = static_cast<float>((1 << BITS) - 1);
   const int tpr = D / 8;
   const int64_t gtid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t row = gtid / tpr;
@@ -118,32 +110,10 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(RowSrc src, RowDst d
 #pragma unroll
     for (int i = 0; i < 8; i++) v[i] = 0.0f;
   }
-  float w_min = E::kMax;
-  float w_max = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    w_min = fminf(w_min, v[i]);
-    w_max = fmaxf(w_max, v[i]);
-  }
-  w_min = wave_min(w_min, TEAM);
-  w_max = wave_max(w_max, TEAM);
-  if (!active) return;
-
-  float scale = fmaxf((w_max - w_min) / n_bins, 1e-7f);
-  const bool side = fabsf(w_min) > fabsf(w_max);
-  scale = side ? scale : -scale;
-  const float edge = side ? w_min : w_max;
-  const float q0 = roundf(edge / scale);
-  const bool at_zero = q0 == 0.0f;
-  scale = at_zero ? scale : edge / q0;
-  const float bias = at_zero ? 0.0f : edge;
-
   uint32_t code[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    float x = fminf(roundf((v[i] - bias) / scale), n_bins);
-    code[i] = x > 0.0f ? static_cast<uint32_t>(x) : 0u;
-  }
+  float scale, bias;
+  affine_quantize8<DT, BITS, GROUP>(v, code, scale, bias);
+  if (!active) return;
   const int G = D / GROUP;
   const int g = (j * 8) / GROUP;
   const bool group_leader = (j % TEAM) == 0;
@@ -197,7 +167,6 @@ __global__ void __launch_bounds__(256) append_affine_kernel(RowSrc sk, RowSrc sv
                                                             int64_t ntok, int H, int D) {
   using E = Elem<DT>;
   constexpr int TEAM = GROUP / 8;
-  constexpr float n_bins = static_cast<float>((1 << BITS) - 1);
   const int which = blockIdx.z;
   const RowSrc src = which ? sv : sk;
   const RowDst dst = which ? dv : dk;
@@ -217,28 +186,9 @@ __global__ void __launch_bounds__(256) append_affine_kernel(RowSrc sk, RowSrc sv
 #pragma unroll
     for (int e = 0; e < 8; e++) v[e] = 0.0f;
   }
-  float w_min = E::kMax, w_max = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    w_min = fminf(w_min, v[e]);
-    w_max = fmaxf(w_max, v[e]);
-  }
-  w_min = wave_min(w_min, TEAM);
-  w_max = wave_max(w_max, TEAM);
-  float scale = fmaxf((w_max - w_min) / n_bins, 1e-7f);
-  const bool side = fabsf(w_min) > fabsf(w_max);
-  scale = side ? scale : -scale;
-  const float edge = side ? w_min : w_max;
-  const float q0 = roundf(edge / scale);
-  const bool at_zero = q0 == 0.0f;
-  scale = at_zero ? scale : edge / q0;
-  const float bias = at_zero ? 0.0f : edge;
   uint32_t code[8];
-#pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const float x = fminf(roundf((v[e] - bias) / scale), n_bins);
-    code[e] = x > 0.0f ? static_cast<uint32_t>(x) : 0u;
-  }
+  float scale, bias;
+  affine_quantize8<DT, BITS, GROUP>(v, code, scale, bias);
   const int g = (j * 8) / GROUP;
   if (slot >= 0 && (j % TEAM) == 0) {
     uint8_t* chunk = dst.base + (slot / dst.block_size) * dst.block_bytes + h * dst.head_bytes;

@@ -197,7 +197,7 @@ def to_torch(a: Array, stream=None):
 
 # ------------------------------------------------------------------- ops
 OPTIONS = {"generic_attention": 0, "decode_waves": 1, "mla_splits": 2, "fdecode_waves": 3,
-           "gather_tokens": 4, "reference_softmax": 5}
+           "gather_tokens": 4, "reference_softmax": 5, "separate_token_write": 6}
 
 
 def set_option(name: str, value: int):
