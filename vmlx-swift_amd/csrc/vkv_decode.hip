@@ -439,6 +439,8 @@ __device__ __forceinline__ void qdecode_write_token(const DecodeArgs& a, int seq
   constexpr int LPR = D / 8, G = D / 64;
   const bool active = lane < 2 * LPR;
   const int which = lane / LPR, j8 = lane % LPR;
+  // the token's block, read beside its rows (not after the quantization)
+  const int64_t blk = a.table[static_cast<int64_t>(seq) * a.table_stride + t / a.block_size];
   float v[8];
   if (active) {
     const uint16_t* src = which ? a.new_v + seq * a.nv_ss + hk * a.nv_sh
@@ -457,7 +459,6 @@ __device__ __forceinline__ void qdecode_write_token(const DecodeArgs& a, int seq
   float scale, bias;
   affine_quantize8<DT, BITS, 64>(v, code, scale, bias);  // (every lane: team shuffles)
   if (!active) return;
-  const int64_t blk = a.table[static_cast<int64_t>(seq) * a.table_stride + t / a.block_size];
   const int tib = t % a.block_size;
   // (the pool is written through the view's base, which the decode only reads elsewhere)
   uint8_t* chunk = const_cast<uint8_t*>(a.base) + blk * a.block_bytes + hk * a.head_bytes;
