@@ -12,8 +12,8 @@ restatement's (oracle/kvcache_ref.py, codes from the oracle quantizer) and
 the outputs are within the decode bar of the oracle's quantized SDPA.
 Covers capacity growth (the 256-token step), a trim whose next steps
 rewrite tokens (the 4-bit value nibbles are merged into words that already
-hold other tokens), both bit widths, 64 / 128 dims, bf16 / f16, and a batch
-past 256 rows (launched in slices)."""
+hold other tokens), both bit widths, 64 / 128 / 256 dims, bf16 / f16, and a
+batch past 256 rows (launched in slices)."""
 import numpy as np
 import pytest
 import torch
@@ -47,7 +47,7 @@ def _same_state(a, b, ref, ctx):
 
 
 @pytest.mark.parametrize("bits,D,dtype", [(4, 128, O.BF16), (8, 128, O.BF16), (4, 64, O.F16),
-                                          (8, 64, O.BF16)])
+                                          (8, 64, O.BF16), (8, 256, O.BF16), (4, 256, O.F16)])
 def test_one_launch_step_equals_two_launches(bits, D, dtype, monkeypatch):
     rng = np.random.default_rng(4100 + bits + D + dtype)
     B, Hkv, Hq = 3, 4, 16

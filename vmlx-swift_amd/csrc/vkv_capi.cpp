@@ -644,7 +644,7 @@ void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_a
         d.counters = attention_counters(S(stream), static_cast<size_t>(chunk) * kv->n_kv_heads *
                                                        qdecode_head_groups(rep));
       if (tok) {
-        if (ref || kv->head_dim > 128) throw Error("the decode token needs the fused decode");
+        if (ref) throw Error("the decode token needs the fused decode");
         d.new_k = static_cast<const uint16_t*>(tok->k);
         d.new_v = static_cast<const uint16_t*>(tok->v);
         d.nk_ss = tok->k_ss;
@@ -770,12 +770,11 @@ bool quantized_decode_step(const vkv_array* q, const vkv_array* keys, const vkv_
       q->strides[3] != 1 || out->strides[3] != 1)
     return false;
   // an existing store of the token's geometry (a first update takes the
-  // two-call path, which creates it), 4- or 8-bit g64 at 64 or 128 dims
+  // two-call path, which creates it), 4- or 8-bit g64
   if (!qc->store_.get() || keys->dtype != qc->dtype_ || keys->shape[0] != qc->B_ ||
       keys->shape[1] != qc->H_ || keys->shape[3] != qc->D_ || values->shape[0] != qc->B_ ||
       values->shape[1] != qc->H_ || values->shape[3] != qc->D_ || qc->group_ != 64 ||
-      (qc->bits_ != 4 && qc->bits_ != 8) || (qc->D_ != 64 && qc->D_ != 128) ||
-      option(VKV_OPTION_REFERENCE_SOFTMAX))
+      (qc->bits_ != 4 && qc->bits_ != 8) || option(VKV_OPTION_REFERENCE_SOFTMAX))
     return false;
   // 16-byte rows of 8 elements
   for (const vkv_array* a : {keys, values})

@@ -829,7 +829,7 @@ qdecode_kernel(DecodeArgs a) {
   // block before any of the range's loads, and is complete (at the L2 this
   // wave reads from) before they issue, so the unit holding it reads it back.
   // The unit is this wave's alone, as are the blocks it reads.
-  if constexpr (MODE == kModeFused && D <= 128) {
+  if constexpr (MODE == kModeFused) {
     if (a.new_k) {
       bool wrote = false;
       for (int kk = 0; kk < nseg; kk++) {

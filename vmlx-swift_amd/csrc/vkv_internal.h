@@ -249,7 +249,7 @@ struct DecodeArgs {
                              //   decode launch (nullptr: in qdecode_combine_kernel)
   // the router's decode token (nullptr: none): the key / value rows
   // [seq][kv head][D] of each sequence's last token, quantized and stored
-  // into its block by the launch itself (fused mode, D <= 128); element strides
+  // into its block by the launch itself (fused mode); element strides
   const uint16_t* new_k;
   const uint16_t* new_v;
   int64_t nk_ss, nk_sh, nv_ss, nv_sh;
