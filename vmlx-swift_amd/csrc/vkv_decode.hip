@@ -374,30 +374,28 @@ __device__ __forceinline__ void qmerge_step(float& M, float& L, float (&o)[E], i
   M = Mn;
 }
 
-// The in-launch merge of a (sequence, head pair)'s K partials by the wave
-// that counted in last: the partials come back through device-coherent
-// loads (they were stored the same way), 4 partials a round trip; lane l
+// The in-launch merge of NP (sequence, head pair)s' partials (K[p] of pair
+// p) by the wave that counted in last for each: the partials come back
+// through device-coherent loads (they were stored the same way), every
+// pair's first 4 in one round trip, then 4 a round trip; lane l
 // takes head l / (64 / HP) and D * HP / 64 consecutive floats of its row,
 // whose 8-byte word p holds dims 16 (p / 8) + 4 (p % 4) + 2 ((p / 4) % 2)
 // and the next (the order of the decode kernel's coherent stores).
-template <int HP, int D, int DT>
-__device__ __forceinline__ void qdecode_merge_pair(const DecodeArgs& a, int pair, int K, int lane) {
+template <int HP, int D, int DT, int NP>
+__device__ __forceinline__ void qdecode_merge_pairs(const DecodeArgs& a, const int (&pair)[NP],
+                                                    const int (&K)[NP], int lane) {
   constexpr int LPH = 64 / HP, EPL = D / LPH, kQuad = 4;
   static_assert(EPL % 2 == 0, "2-element output stores");
   const int rep = a.rep, n_hg = (rep + HP - 1) / HP, HG = a.Hkv * n_hg;
-  const int seq = pair / HG, j = pair % HG;
-  const int64_t hq0 = static_cast<int64_t>(j / n_hg) * rep + (j % n_hg) * HP;
-  const int nh = min(HP, rep - (j % n_hg) * HP);
   const int r = lane / LPH, d0 = (lane % LPH) * EPL;
-  const int64_t slot0 = static_cast<int64_t>(pair) * a.max_parts;
-  float M = -INFINITY, L = 0.0f, o[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; e++) o[e] = 0.0f;
-  for (int k0 = 0; k0 < K; k0 += kQuad) {
-    float mlm[kQuad], mll[kQuad], oo[kQuad][EPL];
+  // partials k0 .. k0 + 3 of pair p (slots past the count: the last one's,
+  // selected away by the merge)
+  auto load_quad = [&](int p, int k0, float (&mlm)[kQuad], float (&mll)[kQuad],
+                       float (&oo)[kQuad][EPL]) __attribute__((always_inline)) {
+    const int64_t slot0 = static_cast<int64_t>(pair[p]) * a.max_parts;
 #pragma unroll
     for (int q = 0; q < kQuad; q++) {
-      const int64_t slot = (slot0 + min(k0 + q, K - 1)) * HP + r;
+      const int64_t slot = (slot0 + min(k0 + q, K[p] - 1)) * HP + r;
       const uint64_t ml = __hip_atomic_load(reinterpret_cast<const uint64_t*>(a.ws_ml) + slot,
                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       mlm[q] = __uint_as_float(static_cast<uint32_t>(ml));
@@ -410,16 +408,43 @@ __device__ __forceinline__ void qdecode_merge_pair(const DecodeArgs& a, int pair
         oo[q][2 * e + 1] = __uint_as_float(static_cast<uint32_t>(x >> 32));
       }
     }
-    qmerge_step<kQuad, EPL>(M, L, o, k0, K, mlm, mll, oo);
-  }
-  if (r >= nh) return;
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  uint16_t* dst = a.out + seq * a.o_ss + (hq0 + r) * a.o_sh;
+  };
+  float M[NP], L[NP], o[NP][EPL];
+  {
+    // every pair's first 4 partials in one round trip
+    float mlm[NP][kQuad], mll[NP][kQuad], oo[NP][kQuad][EPL];
 #pragma unroll
-  for (int e = 0; e < EPL; e += 2) {
-    const int p = (d0 + e) / 2;
-    const int d = 16 * (p >> 3) + 4 * (p & 3) + 2 * ((p >> 2) & 1);
-    *reinterpret_cast<uint32_t*>(dst + d) = out_el<DT>(o[e] * inv) | (out_el<DT>(o[e + 1] * inv) << 16);
+    for (int p = 0; p < NP; p++) load_quad(p, 0, mlm[p], mll[p], oo[p]);
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+      M[p] = -INFINITY;
+      L[p] = 0.0f;
+#pragma unroll
+      for (int e = 0; e < EPL; e++) o[p][e] = 0.0f;
+      qmerge_step<kQuad, EPL>(M[p], L[p], o[p], 0, K[p], mlm[p], mll[p], oo[p]);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < NP; p++) {
+    for (int k0 = kQuad; k0 < K[p]; k0 += kQuad) {
+      float mlm[kQuad], mll[kQuad], oo[kQuad][EPL];
+      load_quad(p, k0, mlm, mll, oo);
+      qmerge_step<kQuad, EPL>(M[p], L[p], o[p], k0, K[p], mlm, mll, oo);
+    }
+    const int seq = pair[p] / HG, j = pair[p] % HG;
+    const int64_t hq0 = static_cast<int64_t>(j / n_hg) * rep + (j % n_hg) * HP;
+    const int nh = min(HP, rep - (j % n_hg) * HP);
+    if (r < nh) {
+      const float inv = L[p] > 0.0f ? 1.0f / L[p] : 0.0f;
+      uint16_t* dst = a.out + seq * a.o_ss + (hq0 + r) * a.o_sh;
+#pragma unroll
+      for (int e = 0; e < EPL; e += 2) {
+        const int w = (d0 + e) / 2;
+        const int d = 16 * (w >> 3) + 4 * (w & 3) + 2 * ((w >> 2) & 1);
+        *reinterpret_cast<uint32_t*>(dst + d) =
+            out_el<DT>(o[p][e] * inv) | (out_el<DT>(o[p][e + 1] * inv) << 16);
+      }
+    }
   }
 }
 
@@ -1422,18 +1447,29 @@ qdecode_kernel(DecodeArgs a) {
     // a pair's last partial zeroes the counter for the next launch and
     // merges the pair.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    auto count_in = [&](int pair, int K) __attribute__((always_inline)) {
-      uint32_t before = 0;
-      if (lane == 0)
-        before = __hip_atomic_fetch_add(a.counters + pair, 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-      before = __builtin_amdgcn_readfirstlane(before);
-      if (before != static_cast<uint32_t>(K - 1)) return;
-      if (lane == 0) __hip_atomic_store(a.counters + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      qdecode_merge_pair<HP, D, DT>(a, pair, K, lane);
-    };
-    count_in(pend_pair0, pend_k0);
-    if (pend_pair1 >= 0) count_in(pend_pair1, pend_k1);
+    // both counts in one round trip, then both merges' first loads together
+    uint32_t b0 = 0, b1 = 0;
+    if (lane == 0) {
+      b0 = __hip_atomic_fetch_add(a.counters + pend_pair0, 1u, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+      if (pend_pair1 >= 0)
+        b1 = __hip_atomic_fetch_add(a.counters + pend_pair1, 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const bool last0 = __builtin_amdgcn_readfirstlane(b0) == static_cast<uint32_t>(pend_k0 - 1);
+    const bool last1 =
+        pend_pair1 >= 0 && __builtin_amdgcn_readfirstlane(b1) == static_cast<uint32_t>(pend_k1 - 1);
+    if (lane == 0) {
+      if (last0) __hip_atomic_store(a.counters + pend_pair0, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (last1) __hip_atomic_store(a.counters + pend_pair1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (last0 && last1) {
+      const int pr[2] = {pend_pair0, pend_pair1}, kk[2] = {pend_k0, pend_k1};
+      qdecode_merge_pairs<HP, D, DT, 2>(a, pr, kk, lane);
+    } else if (last0 || last1) {
+      const int pr[1] = {last0 ? pend_pair0 : pend_pair1}, kk[1] = {last0 ? pend_k0 : pend_k1};
+      qdecode_merge_pairs<HP, D, DT, 1>(a, pr, kk, lane);
+    }
   }
 }
 
