@@ -117,3 +117,27 @@ def test_one_launch_step_past_256_rows(monkeypatch):
         assert torch.equal(got, want), f"step {i}"
         ref.update_quantized(k, v, dtype)
     _same_state(one, two, ref, "300 rows")
+
+
+def test_two_head_groups_keep_the_append_launch(monkeypatch):
+    """12 query heads a kv head (two head groups of the decode kernel): the
+    step keeps its append launch (two waves would write the token's value
+    nibbles) and equals the two-launch path."""
+    rng = np.random.default_rng(4300)
+    dtype, bits, D, B, Hkv, Hq = O.BF16, 4, 128, 2, 2, 24
+    one, two = vkv.QuantizedKVCache(64, bits), vkv.QuantizedKVCache(64, bits)
+    print("one-launch quantized decode: two head groups", flush=True)
+    q = rand_bits(rng, (B, Hq, 30, D), dtype)
+    k = rand_bits(rng, (B, Hkv, 30, D), dtype)
+    v = rand_bits(rng, (B, Hkv, 30, D), dtype)
+    for c in (one, two):
+        vkv.attention_with_cache_update(dev(q, dtype), dev(k, dtype), dev(v, dtype), c, D ** -0.5,
+                                        mask="causal")
+    for i in range(2):
+        q = rand_bits(rng, (B, Hq, 1, D), dtype)
+        k = rand_bits(rng, (B, Hkv, 1, D), dtype)
+        v = rand_bits(rng, (B, Hkv, 1, D), dtype)
+        got, n_app, n_dec = _step(one, q, k, v, dtype, D, False, monkeypatch)
+        want, _, _ = _step(two, q, k, v, dtype, D, True, monkeypatch)
+        assert (n_app, n_dec) == (1, 1), (n_app, n_dec)
+        assert torch.equal(got, want), f"step {i}"

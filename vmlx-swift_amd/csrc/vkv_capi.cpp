@@ -770,7 +770,11 @@ bool quantized_decode_step(const vkv_array* q, const vkv_array* keys, const vkv_
       q->strides[3] != 1 || out->strides[3] != 1)
     return false;
   // an existing store of the token's geometry (a first update takes the
-  // two-call path, which creates it), 4- or 8-bit g64
+  // two-call path, which creates it), 4- or 8-bit g64, and one head group
+  // per kv head (at most 8 query heads a kv head): with two, two waves
+  // would write the token's 4-bit value nibbles, whose clear-then-set
+  // atomics one could read between
+  if (q->shape[1] > 8 * keys->shape[1]) return false;
   if (!qc->store_.get() || keys->dtype != qc->dtype_ || keys->shape[0] != qc->B_ ||
       keys->shape[1] != qc->H_ || keys->shape[3] != qc->D_ || values->shape[0] != qc->B_ ||
       values->shape[1] != qc->H_ || values->shape[3] != qc->D_ || qc->group_ != 64 ||

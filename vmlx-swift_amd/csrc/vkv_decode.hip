@@ -853,7 +853,9 @@ qdecode_kernel(DecodeArgs a) {
   // the token of every pair whose last step this range holds goes into its
   // block before any of the range's loads, and is complete (at the L2 this
   // wave reads from) before they issue, so the unit holding it reads it back.
-  // The unit is this wave's alone, as are the blocks it reads.
+  // The unit is this wave's alone, as are the blocks it reads (the host
+  // passes the token only with one head group per kv head, so no other
+  // wave writes the same words).
   if constexpr (MODE == kModeFused) {
     if (a.new_k) {
       bool wrote = false;
