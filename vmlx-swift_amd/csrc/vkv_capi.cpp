@@ -553,8 +553,6 @@ int vkv_quantized_sdpa(const vkv_array* q, const vkv_array* k_wq, const vkv_arra
 }  // extern "C"
 
 namespace {
-// vkv_paged_sdpa and its no-allocation variant (noalloc: split-K partials in
-// the fixed scratch array, nothing allocated).
 // The router's decode token over a QuantizedKVCache: its key / value rows
 // [B, Hkv, D] (element strides), which the matrix-core decode launch
 // quantizes and writes into the pool itself.
@@ -584,6 +582,9 @@ bool paged_decode_on_matrix_cores(const vkv_array* q, const vkv_array* out,
          qdecode_supported(kv->dtype, kv->bits, kv->head_dim, kv->block_size, rep, kv->group_size);
 }
 
+// vkv_paged_sdpa and its no-allocation variant (noalloc: split-K partials in
+// the fixed scratch array, nothing allocated); tok: the router's decode
+// token, which the matrix-core launch writes.
 void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_array* out,
                 void* stream, bool noalloc, const DecodeToken* tok = nullptr) {
   {
