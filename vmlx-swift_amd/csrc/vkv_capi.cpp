@@ -800,11 +800,19 @@ bool quantized_decode_step(const vkv_array* q, const vkv_array* keys, const vkv_
       out->shape[3] != next.v_head_dim || q->shape[1] % next.n_kv_heads ||
       !paged_decode_on_matrix_cores(&q3, &o3, &next))
     return false;
-  qc->advance(*keys, *values, S(stream));
+  const int64_t prev = qc->advance(*keys, *values, S(stream));
   const vkv_paged_view view = qc->view();
   const DecodeToken tok{keys->data,        values->data,      keys->strides[0],
                         keys->strides[1], values->strides[0], values->strides[1]};
-  paged_sdpa(&q3, &view, scale, &o3, stream, false, &tok);
+  try {
+    paged_sdpa(&q3, &view, scale, &o3, stream, false, &tok);
+  } catch (...) {
+    // the update stands even where the attention failed (the two-call path
+    // writes the token first): the append launch stores it (the same bits
+    // the decode launch writes, should that have run)
+    qc->write_tokens(*keys, *values, prev, S(stream));
+    throw;
+  }
   return true;
 }
 
