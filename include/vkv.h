@@ -217,7 +217,7 @@ int vkv_quantized_paged_sdpa(const vkv_array *q, const vkv_paged_view *kv, float
  * over the whole cache (the matrix-core decode kernel for one query token
  * without a mask, which then also quantizes the new token into the cache
  * itself, in the same launch and with the same bits, where the cache has
- * at most 8 query heads a kv head); with any other cache, update then SDPA over the returned
+ * group 64 and at most 8 query heads a kv head); with any other cache, update then SDPA over the returned
  * keys/values, where a VKV_MASK_NONE mask is replaced by the cache's own
  * array mask if makeMask(n:windowSize:nil:returnArray:true) gives one
  * (called after the update, as the reference does).  q [B,Hq,L,D],

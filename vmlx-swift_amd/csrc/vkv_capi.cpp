@@ -574,11 +574,12 @@ bool paged_decode_on_matrix_cores(const vkv_array* q, const vkv_array* out,
                        q->strides[0] % 8 == 0 && q->strides[1] % 8 == 0 &&
                        (reinterpret_cast<uintptr_t>(out->data) % 8 == 0) &&
                        out->strides[0] % 4 == 0 && out->strides[1] % 4 == 0;
-  // (the matrix-core reference path stores bf16 score rows: an f16 cache
-  // with the reference softmax takes the generic reference path)
+  // (the matrix-core reference path stores bf16 score rows of group-64
+  // caches: an f16 or group-128 cache with the reference softmax takes the
+  // generic reference path)
   return kv->bits > 0 && !keys_only && aligned && kv->max_len <= qdecode_max_len() &&
          !option(VKV_OPTION_GENERIC_ATTENTION) &&
-         !(option(VKV_OPTION_REFERENCE_SOFTMAX) && kv->dtype != VKV_BF16) &&
+         !(option(VKV_OPTION_REFERENCE_SOFTMAX) && (kv->dtype != VKV_BF16 || kv->group_size != 64)) &&
          qdecode_supported(kv->dtype, kv->bits, kv->head_dim, kv->block_size, rep, kv->group_size);
 }
 
@@ -633,6 +634,7 @@ void paged_sdpa(const vkv_array* q, const vkv_paged_view* kv, float scale, vkv_a
           qdecode_workspace_floats(chunk, kv->n_kv_heads, rep, kv->head_dim, kv->max_len);
       const bool ref = option(VKV_OPTION_REFERENCE_SOFTMAX) != 0;
       d.dtype = kv->dtype;
+      d.group = kv->group_size;
       // the reference path's bf16 score rows follow the partials
       d.sc_stride = (std::max<int64_t>(kv->max_len, 1) + 63) / 64 * 64;
       const size_t sc_floats = ref ? static_cast<size_t>(chunk) * d.Hq * d.sc_stride / 2 : 0;

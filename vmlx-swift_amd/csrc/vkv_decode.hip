@@ -562,9 +562,11 @@ __device__ __forceinline__ int seq_at(const int (&t)[NR], int s) {
   return v;
 }
 
-template <int BITS, int D, int HP, int DT = kBF16>
+// GR: the quantization group in 64-dim units (1: group 64; 2: group 128,
+// whose scale and bias serve two consecutive 64-dim groups of the kernel)
+template <int BITS, int D, int HP, int DT = kBF16, int GR = 1>
 struct QD {
-  static constexpr int G = D / 64;            // quantization groups per row
+  static constexpr int G = D / 64;            // 64-dim groups per row
   static constexpr int PP = 16 / HP;          // token parts of a score tile
   static constexpr int TT = 4 / PP;           // score tiles per 64-token step
   static constexpr int SPW = 4 / PP;          // lane groups per part
@@ -574,7 +576,8 @@ struct QD {
   static constexpr int NT = D / 16;           // 16-dim output tiles
   static constexpr int VW = NT * UW;          // value words per lane per sub-block
   static constexpr int ROW = D * BITS / 8;    // key code bytes per token
-  static constexpr int SBW = 2 * G;           // scale/bias words per token (K, V)
+  static constexpr int SBW = 2 * G / GR;      // scale/bias words per token (K, V)
+  static_assert(G % GR == 0, "whole quantization groups per row");
   static constexpr int QROW = 16 * SPW + 1;   // query-table entries per slice
   static constexpr int QCH = HP * D / 8;      // 8-dim query chunks of a head group
   static constexpr int QPL = (QCH + 63) / 64; // query chunks per lane
@@ -612,8 +615,11 @@ constexpr int qd_waves() { return D >= 256 ? 1 : 8; }
 // reference softmax has turned them into bf16 weights in place, P.V from
 // the stored weights (kModeWeights: no key loads, no score MFMAs, no max;
 // the partials are plain sums, merged with max 0 and the pair's first
-// partial carrying sum 1).
-constexpr int kModeFused = 0, kModeScores = 1, kModeWeights = 2;
+// partial carrying sum 1).  kModeFusedG128 is the fused pass over caches
+// quantized with group 128 (GenerateParameters.kvGroupSize,
+// Evaluate.swift:109-112): each scale / bias pair is read once for two
+// 64-dim groups; the decode token is left to the append launch.
+constexpr int kModeFused = 0, kModeScores = 1, kModeWeights = 2, kModeFusedG128 = 3;
 
 // See the header comment for the work split.  Every wave works on its own
 // range with its own LDS tables; the waves of a workgroup only share their
@@ -622,8 +628,10 @@ template <int BITS, int D, int HP, int MODE, int DT>
 __global__ void __launch_bounds__(64 * qd_waves<D>())
 __attribute__((amdgpu_waves_per_eu((D >= 256) ? 1 : 2)))
 qdecode_kernel(DecodeArgs a) {
-  static_assert(DT == kBF16 || MODE == kModeFused, "the reference modes store bf16 rows");
-  using C = QD<BITS, D, HP, DT>;
+  constexpr bool kFused = MODE == kModeFused || MODE == kModeFusedG128;
+  constexpr int GR = MODE == kModeFusedG128 ? 2 : 1;
+  static_assert(DT == kBF16 || kFused, "the reference modes store bf16 rows");
+  using C = QD<BITS, D, HP, DT, GR>;
   constexpr int WPG = qd_waves<D>();
   constexpr int G = C::G, PP = C::PP, TT = C::TT, SPW = C::SPW, SL = C::SL;
   constexpr int RUN = C::RUN, NT = C::NT, VW = C::VW, ROW = C::ROW, SBW = C::SBW;
@@ -647,8 +655,8 @@ qdecode_kernel(DecodeArgs a) {
   // score / weight rows (score and weights modes): per unit, the element
   // offset of its head group's first row at the unit's first token, and the
   // group's live heads
-  __shared__ int64_t u_woff_g[MODE != kModeFused ? WPG : 1][MODE != kModeFused ? kMaxRange : 1];
-  __shared__ int32_t u_nh_g[MODE != kModeFused ? WPG : 1][MODE != kModeFused ? kMaxRange : 1];
+  __shared__ int64_t u_woff_g[!kFused ? WPG : 1][!kFused ? kMaxRange : 1];
+  __shared__ int32_t u_nh_g[!kFused ? WPG : 1][!kFused ? kMaxRange : 1];
   const int wv = WPG > 1 ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6) : 0;
   u32x4_t* qtab = qtab_g[wv];
   int64_t* sub_off = sub_off_g[wv];
@@ -835,7 +843,7 @@ qdecode_kernel(DecodeArgs a) {
       sub_off[e] = my_off[r];
       sub_t0[e] = my_t0[r];
     }
-    if constexpr (MODE != kModeFused) {
+    if constexpr (!kFused) {
       if ((e & 1) == 0 && e < 2 * kMaxRange) {
         const int j = sel_j[r];
         const int64_t hq0 = static_cast<int64_t>(j / n_hg) * rep + (j % n_hg) * HP;
@@ -975,7 +983,7 @@ qdecode_kernel(DecodeArgs a) {
   // counts in at its end, at most two (only a range's first and last
   // segments can be parts of a pair)
   int pend_pair0 = -1, pend_k0 = 0, pend_pair1 = -1, pend_k1 = 0;
-  const bool merge_here = MODE == kModeFused && D <= 128 && a.counters != nullptr;
+  const bool merge_here = kFused && D <= 128 && a.counters != nullptr;
   float sq[G];
   // query table of segment kk from its prefetched chunks: entry (slice sg,
   // column nn, unit slot ws) holds unit sg * SPW + ws of head nn % HP in the
@@ -1098,7 +1106,7 @@ qdecode_kernel(DecodeArgs a) {
         float s = 0.0f;
 #pragma unroll
         for (int g = 0; g < G; g++) {
-          const uint32_t kwd = b.sb[tau][i][g], vwd = b.sb[tau][i][G + g];
+          const uint32_t kwd = b.sb[tau][i][g / GR], vwd = b.sb[tau][i][(G + g) / GR];
           if constexpr (MODE != kModeWeights) {
             const float ks = el_lo<DT>(kwd);
             s = fmaf(fmaf(-KMAG, ks, el_hi<DT>(kwd)), sq[g], s);
@@ -1575,7 +1583,7 @@ int qdecode_head_groups(int rep) { return (rep + heads_per_part(rep) - 1) / head
 bool qdecode_supported(int dtype, int bits, int D, int block_size, int rep, int group) {
   return (dtype == kBF16 || dtype == kF16) && (bits == 4 || bits == 8) &&
          (D == 64 || D == 128 || D == 256) && block_size % 32 == 0 && rep >= 1 && rep <= 16 &&
-         group == 64;
+         (group == 64 || (group == 128 && D >= 128));
 }
 
 int qdecode_waves(int n_seqs, int Hkv, int rep, int max_len, int want) {
@@ -1659,6 +1667,7 @@ static void launch_hp(const DecodeArgs& a0, bool ref, hipStream_t st) {
   // (config 2: 32 partials a pair) and 256 dims keep the merge launch.
   DecodeArgs a = a0;
   if (ref || rest || D > 128) a.counters = nullptr;
+  if (ref) VKV_CHECK(a.group == 64, "the matrix-core reference path takes group 64");
   if constexpr (DT == kBF16) {
     if (ref) {
       // the reference-arithmetic path: bf16 score rows, the reference
@@ -1678,8 +1687,19 @@ static void launch_hp(const DecodeArgs& a0, bool ref, hipStream_t st) {
   }
   if (!ref) {
     const TimedLaunch tl = timing_prepare(kTimeDecode);
-    hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, HP, kModeFused, DT>), grid, block, 0, st,
-                          tl.start, tl.stop, 0, a);
+    if (a.group == 128) {
+      if constexpr (D >= 128) {
+        VKV_CHECK(a.new_k == nullptr, "a group-128 decode takes no decode token");
+        hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, HP, kModeFusedG128, DT>), grid, block, 0,
+                              st, tl.start, tl.stop, 0, a);
+      } else {
+        throw Error("group 128 needs head dims of at least 128");
+      }
+    } else {
+      VKV_CHECK(a.group == 64, "the matrix-core decode takes groups of 64 or 128");
+      hipExtLaunchKernelGGL((qdecode_kernel<BITS, D, HP, kModeFused, DT>), grid, block, 0, st,
+                            tl.start, tl.stop, 0, a);
+    }
     VKV_HIP(hipGetLastError());
     timing_commit(tl);
   }

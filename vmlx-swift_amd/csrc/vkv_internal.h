@@ -243,6 +243,7 @@ struct DecodeArgs {
                              //   of partials of each (sequence, head pair)
   int32_t max_parts;         // set per launch: partials per (sequence, head pair), at most
   int32_t dtype;             // kBF16 or kF16: queries, scales / biases and output
+  int32_t group;             // quantization group: 64, or 128 (fused mode, D >= 128)
   uint16_t* sc;              // reference path: bf16 score / weight rows
   int64_t sc_stride;         //   [n_seqs][Hq][sc_stride], sc_stride >= max_len, % 64 == 0
   uint32_t* counters;        // zeroed per-pair counters: the partials merge inside the
