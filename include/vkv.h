@@ -696,12 +696,13 @@ int vkv_array_copy(const vkv_array *src, vkv_array *dst, void *stream);
 
 /* Attention workspace of a stream (no reference counterpart; the reference
  * allocates per op through MLX's allocator).  The attention calls keep one
- * split-K workspace per stream that only grows; an outgrown buffer is kept,
- * not freed, because a HIP graph captured earlier on that stream still
- * points at it, and growth during capture is refused (run the call once
- * before capturing).  vkv_workspace_release frees the stream's workspace and
- * every outgrown buffer (*bytes, optional, receives the total); call it only
- * when no captured graph that used the stream will be replayed again. */
+ * split-K workspace per (device, stream) that only grows; an outgrown
+ * buffer is kept, not freed, because a HIP graph captured earlier on that
+ * stream still points at it, and growth during capture is refused (run the
+ * call once before capturing).  vkv_workspace_release frees the stream's
+ * workspace on the current device and every outgrown buffer (*bytes,
+ * optional, receives the total); call it only when no captured graph that
+ * used the stream will be replayed again. */
 int vkv_workspace_release(void *stream, int64_t *bytes);
 
 /* ------------------------------------------------------- dispatch options */

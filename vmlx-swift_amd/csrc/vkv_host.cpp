@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <map>
 
 #include "sha256.h"
 
@@ -1927,7 +1928,8 @@ namespace {
 // is outgrown is retired, not freed: it stays allocated until
 // vkv_workspace_release() for that stream (or the end of the process).
 // Growth inside a capture would record an allocation into the graph, so it
-// is refused there.
+// is refused there.  Keyed by (device, stream): the null stream has the same
+// handle on every device.
 struct StreamWorkspace {
   DevBuf cur;
   std::vector<DevBuf> retired;
@@ -1937,15 +1939,21 @@ std::mutex& ws_mutex() {
   static std::mutex mu;
   return mu;
 }
-std::unordered_map<hipStream_t, StreamWorkspace>& ws_map() {
-  static auto* m = new std::unordered_map<hipStream_t, StreamWorkspace>();
+using WsKey = std::pair<int, hipStream_t>;
+std::map<WsKey, StreamWorkspace>& ws_map() {
+  static auto* m = new std::map<WsKey, StreamWorkspace>();
   return *m;
+}
+WsKey ws_key(hipStream_t st) {
+  int dev = 0;
+  VKV_HIP(hipGetDevice(&dev));
+  return {dev, st};
 }
 }  // namespace
 
 float* attention_workspace(hipStream_t st, size_t floats) {
   std::lock_guard<std::mutex> g(ws_mutex());
-  StreamWorkspace& w = ws_map()[st];
+  StreamWorkspace& w = ws_map()[ws_key(st)];
   if (w.cur.size() < floats * sizeof(float)) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     VKV_HIP(hipStreamIsCapturing(st, &cs));
@@ -1962,7 +1970,7 @@ float* attention_workspace(hipStream_t st, size_t floats) {
 
 uint32_t* attention_counters(hipStream_t st, size_t n) {
   std::lock_guard<std::mutex> g(ws_mutex());
-  StreamWorkspace& w = ws_map()[st];
+  StreamWorkspace& w = ws_map()[ws_key(st)];
   if (w.counters.size() < n * sizeof(uint32_t)) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     VKV_HIP(hipStreamIsCapturing(st, &cs));
@@ -1979,7 +1987,7 @@ uint32_t* attention_counters(hipStream_t st, size_t n) {
 
 size_t workspace_release(hipStream_t st) {
   std::lock_guard<std::mutex> g(ws_mutex());
-  auto it = ws_map().find(st);
+  auto it = ws_map().find(ws_key(st));
   if (it == ws_map().end()) return 0;
   size_t n = it->second.cur.size() + it->second.counters.size();
   for (auto& b : it->second.retired) n += b.size();
