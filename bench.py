@@ -13,9 +13,9 @@ HBM before timing starts.  The step writes the decode token at the same
 position each step, so every step does identical work.
 
 Prints one JSON line: "value" is the whole-step KV-read rate (appends included),
-"attention" times the paged decode call (decode kernel + split-K merge),
-"roofline" the decode kernel alone (the library's event pair around it, on
-its launch stream), "traffic" is the PMC-measured HBM bytes per decode launch,
+"attention" times the paged decode call (one launch: the decode kernel
+merges its split-K partials itself), "roofline" that decode launch (the
+library's event pair around it, on its launch stream), "traffic" is the PMC-measured HBM bytes per decode launch,
 "cpu_baseline" times the C oracle, "prefill" times a 512-token chunked-prefill
 attention step over a 4-bit cache, and "mla" is the MLA latent decode workload
 (32 x 16384 tokens, 128 heads) with the MFMA roofline of its attention kernel.
@@ -752,7 +752,8 @@ def main():
                    "tokens_per_s_call": round(append_tokens / (app_avg_ms * 1e-3), 1)},
         "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": pmc_traffic(), "kernel": "qdecode_kernel"},
+                     "traffic": pmc_traffic(), "kernel": "qdecode_kernel",
+                     "scope": "one decode launch, its split-K merge included"},
         "cpu_baseline": cpu,
         "mla": mla,
         "prefill": prefill,
