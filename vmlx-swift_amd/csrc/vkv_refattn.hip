@@ -213,16 +213,39 @@ __device__ __forceinline__ double half_max(double x) {
 // for the final pass.
 constexpr int kSmWindow = 16384;
 
-template <typename S>
-__device__ __forceinline__ void sm_stage(const S* p, int64_t w0, int wlen, float* buf, int lid) {
-  using St = Store<S>;
+// The LDS copy of a window of a score row.  Scores stored in a 16-bit
+// dtype (bf16 rows, or f32 rows holding values rounded to bf16 / f16 for
+// that dtype's softmax) are kept as their 16-bit patterns: exact, and half
+// the LDS of floats, so twice the workgroups a CU.  Rows of f32 arithmetic
+// stay floats.
+template <typename S, int ACC> struct SmLds {
+  static constexpr bool kHalf = sizeof(S) == 2 || ACC == kF16 || ACC == kBF16;
+  static constexpr int kDt = sizeof(S) == 2 ? kBF16 : ACC;  // the 16-bit dtype
+  using T = typename std::conditional<kHalf, uint16_t, float>::type;
+  __device__ __forceinline__ static T put(S x) {
+    if constexpr (!kHalf) return x;
+    else if constexpr (sizeof(S) == 2) return x;
+    else if constexpr (kDt == kF16) return f32_to_f16(x);
+    else return f32_to_bf16(x);
+  }
+  __device__ __forceinline__ static double val(T x) {
+    if constexpr (!kHalf) return x;
+    else if constexpr (kDt == kF16) return f16_to_f32(x);
+    else return bf16_to_f32(x);
+  }
+};
+
+template <typename S, int ACC>
+__device__ __forceinline__ void sm_stage(const S* p, int64_t w0, int wlen,
+                                         typename SmLds<S, ACC>::T* buf, int lid) {
+  using L = SmLds<S, ACC>;
   constexpr int U = 16;
   for (int i0 = 0; i0 < wlen; i0 += U * kSmThreads) {
-    float v[U];
+    typename L::T v[U];
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int i = i0 + u * kSmThreads + lid;
-      v[u] = i < wlen ? static_cast<float>(St::get(p, w0 + i)) : 0.0f;
+      v[u] = i < wlen ? L::put(p[w0 + i]) : typename L::T{};
     }
 #pragma unroll
     for (int u = 0; u < U; u++) {
@@ -240,7 +263,8 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
   // f32 weights)
   constexpr int dt = ACC < 0 ? kF32 : ACC;
   using St = Store<S>;
-  __shared__ float buf[kSmWindow];
+  using L = SmLds<S, ACC>;
+  __shared__ typename L::T buf[kSmWindow];
   __shared__ double red[kSmThreads / 64];
   __shared__ double simd_s[kSoftmaxThreads / 32], simd_m[kSoftmaxThreads / 32];
   __shared__ double bcast[2];
@@ -252,7 +276,7 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
   const bool resident = T <= kSmWindow;  // the whole row stays in LDS
   // score t: from LDS when the row is resident
   auto score = [&](int64_t t) __attribute__((always_inline)) {
-    return resident ? static_cast<double>(buf[t]) : St::get(p, t);
+    return resident ? L::val(buf[t]) : St::get(p, t);
   };
 
   // row max (of stored values: exact in any order), window by window
@@ -260,9 +284,9 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
   for (int64_t w0 = 0; w0 < T; w0 += kSmWindow) {
     const int wlen = static_cast<int>(min<int64_t>(kSmWindow, T - w0));
     if (w0 > 0) __syncthreads();
-    sm_stage(p, w0, wlen, buf, lid);
+    sm_stage<S, ACC>(p, w0, wlen, buf, lid);
     __syncthreads();
-    for (int i = lid; i < wlen; i += kSmThreads) mx = fmax(mx, static_cast<double>(buf[i]));
+    for (int i = lid; i < wlen; i += kSmThreads) mx = fmax(mx, L::val(buf[i]));
   }
   mx = half_max(mx);
   mx = fmax(mx, __shfl_xor(mx, 32));
@@ -297,7 +321,7 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
 #pragma unroll
       for (int i = 0; i < kSoftmaxReads; i++) {
         const int64_t t = static_cast<int64_t>(kSoftmaxReads) * (lid + kSmThreads * k) + i;
-        e[k][i] = t < T ? t_exp_fast<dt>(rnd_d<dt>(static_cast<double>(buf[t]) - mx)) : 0.0;
+        e[k][i] = t < T ? t_exp_fast<dt>(rnd_d<dt>(L::val(buf[t]) - mx)) : 0.0;
         if (t < T) thr = rnd_d<dt>(thr + e[k][i]);
       }
       // simd group (lid + 256 k) / 32: this half-wave
@@ -339,7 +363,7 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
     const int wlen = static_cast<int>(min<int64_t>(kSmWindow, T - w0));
     if (!resident) {
       __syncthreads();
-      sm_stage(p, w0, wlen, buf, lid);
+      sm_stage<S, ACC>(p, w0, wlen, buf, lid);
       __syncthreads();
     }
     const int64_t rd1 = min<int64_t>(rounds, rd0 + kRoundsPerWindow);
@@ -351,7 +375,7 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
         const double prev = m[k];
 #pragma unroll
         for (int i = 0; i < kSoftmaxReads; i++) {
-          v[i] = off + i < T ? static_cast<double>(buf[off + i - w0]) : -INFINITY;
+          v[i] = off + i < T ? L::val(buf[off + i - w0]) : -INFINITY;
           m[k] = v[i] > m[k] ? v[i] : m[k];
         }
         n[k] = rnd_d<dt>(n[k] * t_exp_fast<dt>(rnd_d<dt>(prev - m[k])));
@@ -385,16 +409,16 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
   const double gmax = bcast[0], rr = bcast[1];
   if (resident) {
     for (int64_t t = lid; t < T; t += kSmThreads)
-      St::put(p, t, rnd_d<dt>(t_exp_fast<dt>(rnd_d<dt>(static_cast<double>(buf[t]) - gmax)) * rr));
+      St::put(p, t, rnd_d<dt>(t_exp_fast<dt>(rnd_d<dt>(L::val(buf[t]) - gmax)) * rr));
     return;
   }
   for (int64_t w0 = 0; w0 < T; w0 += kSmWindow) {
     const int wlen = static_cast<int>(min<int64_t>(kSmWindow, T - w0));
     __syncthreads();
-    sm_stage(p, w0, wlen, buf, lid);
+    sm_stage<S, ACC>(p, w0, wlen, buf, lid);
     __syncthreads();
     for (int i = lid; i < wlen; i += kSmThreads)
-      St::put(p, w0 + i, rnd_d<dt>(t_exp_fast<dt>(rnd_d<dt>(static_cast<double>(buf[i]) - gmax)) * rr));
+      St::put(p, w0 + i, rnd_d<dt>(t_exp_fast<dt>(rnd_d<dt>(L::val(buf[i]) - gmax)) * rr));
   }
 }
 
