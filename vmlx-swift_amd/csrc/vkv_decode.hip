@@ -592,8 +592,12 @@ struct QD {
   // step's start (behind the scores); whole double buffers would not fit
   // beside the rest, and with 8 heads per part neither does this (it
   // spills).  (At D 128, 8-bit, where two waves share a SIMD, it fits but
-  // measured no faster: the partner wave already covers the loads.)
-  static constexpr bool kPrefetchK = !kPrefetch && D >= 256 && HP == 4;
+  // measured no faster: the partner wave already covers the loads.)  f16
+  // caches at 8 bits hold more live registers here (their f16 query and
+  // key operands): with the prefetch they spill to scratch inside the loop,
+  // so they load then compute.
+  static constexpr bool kPrefetchK =
+      !kPrefetch && D >= 256 && HP == 4 && !(DT == kF16 && BITS == 8);
 
   struct Buf {
     uint32_t kw[TT][PP][RUN];    // key words of this lane's token, per tile
