@@ -25,7 +25,7 @@ pytestmark = pytest.mark.gpu
 # which keeps the 8 / 4 heads of a kv head together
 SHAPES = [(2, 4, 16, 576, 128, O.BF16), (4, 8, 16, 1024, 256, O.BF16),
           (2, 2, 16, 576, 128, O.BF16), (1, 8, 8, 100, 64, O.F16),
-          (2, 2, 16, 300, 128, O.F32), (24, 4, 32, 64, 64, O.BF16),
+          (2, 2, 8, 300, 128, O.F32), (24, 4, 32, 64, 64, O.BF16),
           (40, 4, 16, 96, 128, O.F16)]
 
 

@@ -674,6 +674,13 @@ bool fdecode_supported(int dtype, int bits, bool qsem, const AttnArgs& a) {
   if (a.D != a.Dv || (a.D != 64 && a.D != 128 && a.D != 256)) return false;
   if (a.Hq % a.Hkv) return false;
   if (a.mask_mode < 0 || a.mask_mode > 3) return false;
+  // f32 rows at 128 dims with more than 4 query heads a kv head, or at 256
+  // dims with more than 2, need more registers than a wave has (the step's
+  // f32 key and value rows beside the group's accumulators): those variants
+  // spill hundreds of registers to scratch and ran 1.9-4.7x slower than the
+  // generic kernel, which therefore takes them
+  const int rep = a.Hq / a.Hkv;
+  if (dtype == kF32 && ((a.D == 128 && rep > 4) || (a.D == 256 && rep > 2))) return false;
   const int es = elem_bytes(dtype);
   // 16-byte loads of key and value rows
   auto al = [](const void* p, int64_t s0, int64_t s1, int64_t s2) {
