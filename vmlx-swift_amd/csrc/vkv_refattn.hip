@@ -208,10 +208,18 @@ __device__ __forceinline__ double half_max(double x) {
   return x;
 }
 
-// Rows are staged through LDS in windows of kSmWindow scores (all of a
+// Rows are staged through LDS in windows of up to kSmWindow scores (all of a
 // window's loads in flight at once); a row that fits one window stays there
 // for the final pass.
 constexpr int kSmWindow = 16384;
+// The window of a launch: its longest row rounded up to whole rounds of the
+// looped softmax (4096 scores), at most kSmWindow, so short rows take less
+// LDS and more of them run on a CU.
+inline int sm_window(int64_t max_len) {
+  constexpr int kRound = kSoftmaxReads * kSoftmaxThreads;
+  const int64_t w = (std::max<int64_t>(max_len, 1) + kRound - 1) / kRound * kRound;
+  return static_cast<int>(std::min<int64_t>(w, kSmWindow));
+}
 
 // The LDS copy of a window of a score row.  Scores stored in a 16-bit
 // dtype (bf16 rows, or f32 rows holding values rounded to bf16 / f16 for
@@ -255,16 +263,20 @@ __device__ __forceinline__ void sm_stage(const S* p, int64_t w0, int wlen,
   }
 }
 
+// win: the LDS window (sm_window of the launch's longest row), in the
+// dynamic LDS the launch passes.
 template <typename S, int ACC>
 __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t tpad,
                                                                  const int32_t* seq_lens,
-                                                                 int32_t T_all, int64_t per_b) {
+                                                                 int32_t T_all, int64_t per_b,
+                                                                 int win) {
   // ACC: the AccT dtype, or -1 for an f32-promoted row (fp32 arithmetic,
   // f32 weights)
   constexpr int dt = ACC < 0 ? kF32 : ACC;
   using St = Store<S>;
   using L = SmLds<S, ACC>;
-  __shared__ typename L::T buf[kSmWindow];
+  extern __shared__ __attribute__((aligned(16))) unsigned char sm_win[];
+  typename L::T* buf = reinterpret_cast<typename L::T*>(sm_win);
   __shared__ double red[kSmThreads / 64];
   __shared__ double simd_s[kSoftmaxThreads / 32], simd_m[kSoftmaxThreads / 32];
   __shared__ double bcast[2];
@@ -273,7 +285,7 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
   if (T <= 0) return;
   S* p = sc + row * tpad;
   const int lid = threadIdx.x, lane = lid & 63, wv = lid >> 6;
-  const bool resident = T <= kSmWindow;  // the whole row stays in LDS
+  const bool resident = T <= win;  // the whole row stays in LDS
   // score t: from LDS when the row is resident
   auto score = [&](int64_t t) __attribute__((always_inline)) {
     return resident ? L::val(buf[t]) : St::get(p, t);
@@ -281,8 +293,8 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
 
   // row max (of stored values: exact in any order), window by window
   double mx = -INFINITY;
-  for (int64_t w0 = 0; w0 < T; w0 += kSmWindow) {
-    const int wlen = static_cast<int>(min<int64_t>(kSmWindow, T - w0));
+  for (int64_t w0 = 0; w0 < T; w0 += win) {
+    const int wlen = static_cast<int>(min<int64_t>(win, T - w0));
     if (w0 > 0) __syncthreads();
     sm_stage<S, ACC>(p, w0, wlen, buf, lid);
     __syncthreads();
@@ -351,22 +363,22 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
   const double fmin = -type_max_d<dt>();
   const int64_t stride = static_cast<int64_t>(kSoftmaxReads) * kSoftmaxThreads;
   const int64_t rounds = (T + stride - 1) / stride;
-  constexpr int kRoundsPerWindow = kSmWindow / (kSoftmaxReads * kSoftmaxThreads);
+  const int rounds_per_window = win / (kSoftmaxReads * kSoftmaxThreads);
   double m[kSmVirtual], n[kSmVirtual];
 #pragma unroll
   for (int k = 0; k < kSmVirtual; k++) {
     m[k] = fmin;
     n[k] = 0.0;
   }
-  for (int64_t rd0 = 0; rd0 < rounds; rd0 += kRoundsPerWindow) {
+  for (int64_t rd0 = 0; rd0 < rounds; rd0 += rounds_per_window) {
     const int64_t w0 = rd0 * stride;
-    const int wlen = static_cast<int>(min<int64_t>(kSmWindow, T - w0));
+    const int wlen = static_cast<int>(min<int64_t>(win, T - w0));
     if (!resident) {
       __syncthreads();
       sm_stage<S, ACC>(p, w0, wlen, buf, lid);
       __syncthreads();
     }
-    const int64_t rd1 = min<int64_t>(rounds, rd0 + kRoundsPerWindow);
+    const int64_t rd1 = min<int64_t>(rounds, rd0 + rounds_per_window);
     for (int64_t rd = rd0; rd < rd1; rd++) {
 #pragma unroll
       for (int k = 0; k < kSmVirtual; k++) {
@@ -412,8 +424,8 @@ __global__ void __launch_bounds__(kSmThreads) ref_softmax_kernel(S* sc, int64_t 
       St::put(p, t, rnd_d<dt>(t_exp_fast<dt>(rnd_d<dt>(L::val(buf[t]) - gmax)) * rr));
     return;
   }
-  for (int64_t w0 = 0; w0 < T; w0 += kSmWindow) {
-    const int wlen = static_cast<int>(min<int64_t>(kSmWindow, T - w0));
+  for (int64_t w0 = 0; w0 < T; w0 += win) {
+    const int wlen = static_cast<int>(min<int64_t>(win, T - w0));
     __syncthreads();
     sm_stage<S, ACC>(p, w0, wlen, buf, lid);
     __syncthreads();
@@ -529,6 +541,23 @@ int ref_part_tokens(int64_t B, int Hkv, int nrows, int64_t T, int* n_parts) {
   return static_cast<int>(pt);
 }
 
+// One workgroup a row; the LDS window sized to the launch's longest row
+// (max_len), in dynamic LDS.
+template <typename S, int ACC>
+static void launch_softmax(dim3 rows, S* sc, int64_t tpad, const int32_t* seq_lens,
+                           int32_t max_len, int64_t per_b, hipStream_t st) {
+  using T = typename SmLds<S, ACC>::T;
+  static const bool lds_ok = [] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&ref_softmax_kernel<S, ACC>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               static_cast<int>(kSmWindow * sizeof(T))) == hipSuccess;
+  }();
+  VKV_CHECK(lds_ok, "cannot raise the softmax kernel's LDS limit");
+  const int win = sm_window(max_len);
+  hipLaunchKernelGGL((ref_softmax_kernel<S, ACC>), rows, dim3(kSmThreads), win * sizeof(T), st, sc,
+                     tpad, seq_lens, max_len, per_b, win);
+}
+
 template <int DT, int BITS>
 static void ref_launch_dt(const RefArgs& r, int64_t B, hipStream_t st) {
   const AttnArgs& a = r.a;
@@ -548,11 +577,9 @@ static void ref_launch_dt(const RefArgs& r, int64_t B, hipStream_t st) {
   const dim3 rows(static_cast<unsigned>(B * a.Hq * r.nl));
   const int64_t per_b = static_cast<int64_t>(a.Hq) * r.nl;
   if (r.score_f32)
-    hipLaunchKernelGGL((ref_softmax_kernel<float, -1>), rows, dim3(kSmThreads), 0, st, r.sc, r.tpad,
-                       a.kv.seq_lens, a.kv.T, per_b);
+    launch_softmax<float, -1>(rows, r.sc, r.tpad, a.kv.seq_lens, a.kv.T, per_b, st);
   else
-    hipLaunchKernelGGL((ref_softmax_kernel<float, DT>), rows, dim3(kSmThreads), 0, st, r.sc, r.tpad,
-                       a.kv.seq_lens, a.kv.T, per_b);
+    launch_softmax<float, DT>(rows, r.sc, r.tpad, a.kv.seq_lens, a.kv.T, per_b, st);
   VKV_HIP(hipGetLastError());
   const int nrb = (nrows + kRefRows - 1) / kRefRows;
   const dim3 gp(static_cast<unsigned>(r.n_parts), static_cast<unsigned>(a.Hkv * nrb),
@@ -590,8 +617,8 @@ void launch_ref_attention(int dtype, const RefArgs& r, int64_t B, hipStream_t st
 void launch_ref_softmax_bf16(uint16_t* sc, int64_t rows, int64_t tpad, const int32_t* seq_lens,
                              int32_t T, int64_t per_b, hipStream_t st) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL((ref_softmax_kernel<uint16_t, kBF16>), dim3(static_cast<unsigned>(rows)),
-                     dim3(kSmThreads), 0, st, sc, tpad, seq_lens, T, per_b);
+  launch_softmax<uint16_t, kBF16>(dim3(static_cast<unsigned>(rows)), sc, tpad, seq_lens, T, per_b,
+                                  st);
   VKV_HIP(hipGetLastError());
 }
 
