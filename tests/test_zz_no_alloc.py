@@ -72,6 +72,34 @@ def test_noalloc_matches_allocating_entry_point(bits):
         check_against_oracle(values(got, dtype), q, keys, vals, bits, dtype, D)
 
 
+def test_noalloc_group128_matches_allocating_entry_point():
+    """A group-128 cache (the matrix-core decode's group-128 mode): the
+    partials merge in the merge launch here and inside the launch on the
+    allocating entry point, through the same merge step in the same order,
+    so the outputs are bit-identical; and within the oracle's bar."""
+    from test_gpu_decode_g128 import scene as scene_g
+    rng = np.random.default_rng(740)
+    dtype, bits, Hkv, D, Hq = O.BF16, 4, 4, 128, 16
+    lens = [1800, 40, 3300, 1]
+    print(f"noalloc group 128: lens {lens}", flush=True)
+    pool, view, keys, vals, keep = scene_g(rng, bits, 128, lens, Hkv, D, dtype)
+    q = rand_bits(rng, (len(lens), Hq, D), dtype)
+    qd = dev(q, dtype)
+    want = vkv.paged_attention(qd, view, D ** -0.5)
+    got = vkv.paged_attention(qd, view, D ** -0.5, out=torch.empty_like(want), noalloc=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(got), host(want))
+    f = lambda a: O.to_f32(a, dtype)
+    out = values(got, dtype)
+    for s, L in enumerate(lens):
+        rk = O.quantize(np.ascontiguousarray(keys[s][:L].transpose(1, 0, 2)), dtype, 128, bits)
+        rv = O.quantize(np.ascontiguousarray(vals[s][:L].transpose(1, 0, 2)), dtype, 128, bits)
+        ref, wb = (x[0, :, 0] for x in qref(f(q[s])[None, :, None], dtype, rk[0][None],
+                                            f(rk[1])[None], f(rk[2])[None], rv[0][None],
+                                            f(rv[1])[None], f(rv[2])[None], D ** -0.5, 128, bits))
+        assert_qclose(out[s], ref, wb, dtype, f"seq {s}")
+
+
 def test_noalloc_float_blocks_match():
     """bf16 blocks: the generic split-K kernel, partials in the scratch."""
     rng = np.random.default_rng(710)
